@@ -1,0 +1,415 @@
+#!/usr/bin/env python
+"""Benchmark of the VQ2 decode hot path on one MI355X.
+
+Headline: one decoder layer's projection set at
+batch 1, hidden 2048 -- RHT(2048) -> q, k, v (2 bpw); RHT(2048) -> o (2 bpw);
+RHT(2048) -> gate, up (4 bpw, two 16-bit stages); RHT(6144, 3 x 2048 blocks)
+-> down (4 bpw).  One step = one layer; the timed loop cycles through L
+distinct layer weight sets (>= 1 GiB in total) so the 256 MB Infinity Cache
+cannot hold the weights, and replays the launches as HIP graphs.
+``value`` = compressed weight bytes (index planes + row scales) per step /
+step time, in GB/s.
+
+Also reported: the config-4 MoE layer (router + 8 routed + 1 shared expert,
+T = 1) in us per layer over a 40-layer resident pool, the config-3 LM head
+(151936 x 2048, 2 bpw, fused top-1), the dominant kernel's roofline
+(4 bpw GEMV, HIP events on its stream) and the reference CPU path timed on
+the host (``cpu_baseline``).
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+                       [--only dominant|copy] (single-kernel modes for rocprofv3 --pmc runs)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+HIDDEN, Q_OUT, KV_OUT, INTER = 2048, 2048, 512, 6144
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def metric_name() -> str:
+    try:
+        return json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+    except Exception:
+        return "VQ-GEMV HBM GB/s (% of peak) + us per 35B-A3B-shape MoE layer at batch 1"
+
+
+# ----------------------------------------------------------------- workloads
+def rand_i16(shape, g, dev):
+    import torch
+
+    return torch.randint(-32768, 32768, shape, generator=g, device=dev, dtype=torch.int32).to(torch.int16)
+
+
+def rand_scale(n, g, dev):
+    import torch
+
+    return (torch.rand(n, generator=g, device=dev) + 0.5).to(torch.float16)
+
+
+class DenseLayers:
+    """L layer sets of the configs[1] projections (device-resident)."""
+
+    PROJ = [  # name, out, n, bpw
+        ("q", Q_OUT, HIDDEN, 2), ("k", KV_OUT, HIDDEN, 2), ("v", KV_OUT, HIDDEN, 2), ("o", HIDDEN, HIDDEN, 2),
+        ("gate", INTER, HIDDEN, 4), ("up", INTER, HIDDEN, 4), ("down", HIDDEN, INTER, 4),
+    ]
+
+    def __init__(self, L, dev):
+        import torch
+
+        from compressai_amd import synth
+
+        self.L, self.dev = L, dev
+        g = torch.Generator(device=dev).manual_seed(2000)
+        self.cb0 = synth.codebook(2000).to(dev)
+        self.cb1 = synth.codebook(2001).to(dev)
+        self.layers = []
+        for _ in range(L):
+            lay = {}
+            for name, out, n, bpw in self.PROJ:
+                i0 = rand_i16((out, n // 8), g, dev)
+                i1 = rand_i16((out, n // 8), g, dev) if bpw == 4 else None
+                lay[name] = (i0, i1, rand_scale(out, g, dev), out, n)
+            self.layers.append(lay)
+        self.bytes_per_step = sum(out * (n // 8) * 2 * (2 if bpw == 4 else 1) + out * 2
+                                  for _, out, n, bpw in self.PROJ)
+        self.x_attn = synth.activations(2004, HIDDEN).to(dev)
+        self.x_o = synth.activations(2014, HIDDEN).to(dev)
+        self.x_mlp = synth.activations(2024, HIDDEN).to(dev)
+        self.x_down = synth.activations(2034, INTER).to(dev)
+        self.sign_h = synth.signs(2005, HIDDEN).to(dev)
+        self.sign_i = synth.signs(2015, INTER).to(dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.xr_a, self.xr_o, self.xr_m = (torch.empty(HIDDEN, **f32) for _ in range(3))
+        self.xr_d = torch.empty(INTER, **f32)
+        self.y = {name: torch.empty(out, **f32) for name, out, _, _ in self.PROJ}
+
+    def gemv(self, lay, name, xr):
+        from compressai_amd import kernels as K
+
+        i0, i1, s, out, n = lay[name]
+        K.vq_gemv(xr, i0, i1, self.cb0, self.cb1 if i1 is not None else None, s, out, n, 1.0, y=self.y[name])
+
+    def step(self, l):
+        from compressai_amd import kernels as K
+
+        lay = self.layers[l]
+        K.vq_rht(self.x_attn, None, self.sign_h, 2048, out=self.xr_a)
+        for name in ("q", "k", "v"):
+            self.gemv(lay, name, self.xr_a)
+        K.vq_rht(self.x_o, None, self.sign_h, 2048, out=self.xr_o)
+        self.gemv(lay, "o", self.xr_o)
+        K.vq_rht(self.x_mlp, None, self.sign_h, 2048, out=self.xr_m)
+        self.gemv(lay, "gate", self.xr_m)
+        self.gemv(lay, "up", self.xr_m)
+        K.vq_rht(self.x_down, None, self.sign_i, 2048, out=self.xr_d)
+        self.gemv(lay, "down", self.xr_d)
+
+
+def capture(fn, n_items, dev):
+    """HIP graph of fn(0..n_items-1) launched back to back."""
+    import torch
+
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for i in range(n_items):  # eager warm-up of every launch shape
+            fn(i)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_items):
+            fn(i)
+    torch.cuda.synchronize(dev)
+    return g
+
+
+def time_graph(g, reps, dev):
+    """(elapsed ms on the replay stream measured by HIP events, host ms)."""
+    import torch
+
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize(dev)
+    return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
+
+def bench_dense(args, dev):
+    import torch
+
+    L = args.layers
+    dl = DenseLayers(L, dev)
+    log(f"dense: {L} layer sets, {dl.bytes_per_step * L / 2**30:.2f} GiB of compressed weights")
+    g = capture(dl.step, L, dev)
+    warm_reps = max(1, -(-args.warmup // L))
+    time_graph(g, warm_reps, dev)
+    reps = max(1, -(-args.steps // L))
+    steps = reps * L
+    ms, host_ms = time_graph(g, reps, dev)
+    ms_per_step = ms / steps
+    gbps = dl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    log(f"dense: {steps} steps in {ms:.3f} ms (host {host_ms:.3f} ms) -> {ms_per_step * 1e3:.2f} us/step, "
+        f"{gbps:.1f} GB/s")
+
+    # dominant kernel: the 4 bpw GEMV (gate shape 6144 x 2048), back to back
+    dom_bytes = INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2
+    gd = capture(lambda l: dl.gemv(dl.layers[l], "gate", dl.xr_m), L, dev)
+    time_graph(gd, 2, dev)
+    dreps = max(4, 2000 // L)
+    dms, _ = time_graph(gd, dreps, dev)
+    dom_us = dms * 1e3 / (dreps * L)
+    dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
+    log(f"dominant 4 bpw GEMV 6144x2048: {dom_us:.2f} us/launch, {dom_gbps:.1f} GB/s")
+    return dict(steps=steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
+                dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl)
+
+
+def bench_moe(args, dev, n_layers=40, T=1):
+    import torch
+
+    from compressai_amd import synth
+    from compressai_amd.moe import MoELayer
+
+    E, k = 256, 8
+    g = torch.Generator(device=dev).manual_seed(4000)
+    cb = synth.codebook(4000).to(dev)
+    layers, inputs = [], []
+    for _ in range(n_layers):
+        gu = rand_i16((E + 1, 1024, 256), g, dev)
+        gus = rand_scale((E + 1) * 1024, g, dev).view(E + 1, 1024)
+        dn = rand_i16((E + 1, 2048, 64), g, dev)
+        dns = rand_scale((E + 1) * 2048, g, dev).view(E + 1, 2048)
+        gate = (torch.randn(HIDDEN, generator=g, device=dev) * 0.02).to(torch.float16)
+        layers.append(MoELayer(gu, gus, dn, dns, cb, gate, top_k=k))
+        h = torch.randn(T, HIDDEN, generator=g, device=dev).to(torch.float16)
+        lg = torch.randn(T, E, generator=g, device=dev).to(torch.float16)
+        inputs.append((h, lg))
+    per_expert = 1024 * 256 * 2 + 1024 * 2 + 2048 * 64 * 2 + 2048 * 2
+    log(f"moe: {n_layers} layers x {E + 1} experts resident ({n_layers * (E + 1) * per_expert / 2**30:.2f} GiB)")
+    outs = [None] * n_layers
+
+    def fwd(l):
+        outs[l] = layers[l](*inputs[l])
+
+    gr = capture(fwd, n_layers, dev)
+    time_graph(gr, 3, dev)
+    reps = max(5, args.steps // n_layers)
+    ms, _ = time_graph(gr, reps, dev)
+    us = ms * 1e3 / (reps * n_layers)
+    # distinct experts actually read per layer (routed + shared)
+    distinct = []
+    for l in range(n_layers):
+        ids, _ = layers[l].route(inputs[l][0], inputs[l][1])
+        distinct.append(len(set(ids.flatten().tolist())))
+    bytes_layer = statistics.mean(distinct) * per_expert
+    gbps = bytes_layer / (us * 1e-6) / 1e9
+    log(f"moe T={T}: {us:.2f} us/layer, {gbps:.1f} GB/s ({statistics.mean(distinct):.1f} experts/layer)")
+    return dict(us=us, gbps=gbps, bytes=bytes_layer)
+
+
+def bench_lm_head(args, dev, batch=1, copies=14):
+    import torch
+
+    from compressai_amd import kernels as K, synth
+
+    out, n = 151936, 2048
+    g = torch.Generator(device=dev).manual_seed(3000)
+    cb = synth.codebook(3000).to(dev)
+    mats = [(rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)) for _ in range(copies)]
+    x = synth.activations(3004, (batch, n), dtype=torch.float32).to(dev)
+    ws = torch.empty(batch, out, dtype=torch.float32, device=dev)
+    res = [None] * copies
+
+    def fwd(l):
+        i0, s = mats[l]
+        res[l] = K.vq_gemv_argmax(x, i0, None, cb, None, s, out, n, logits_ws=ws)
+
+    gr = capture(fwd, copies, dev)
+    time_graph(gr, 2, dev)
+    reps = max(5, 200 // copies)
+    ms, _ = time_graph(gr, reps, dev)
+    us = ms * 1e3 / (reps * copies)
+    nbytes = out * (n // 8) * 2 + out * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    log(f"lm head B={batch}: {us:.2f} us/call, {gbps:.1f} GB/s")
+    return dict(us=us, gbps=gbps)
+
+
+# -------------------------------------------------------------- CPU baseline
+def cpu_baseline(dl, budget_s=20.0):
+    """The reference CPU path (PackedLinear fallback, fp32) on the host for
+    one configs[1] layer step; median of >= 3 timed runs after 1 warm-up,
+    bounded by budget_s seconds of CPU work."""
+    import platform
+
+    import torch
+
+    from oracle.ref_cpu_path import CpuRot, packed_linear_fallback
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    lay = {k: tuple(t.cpu() if hasattr(t, "cpu") else t for t in v) for k, v in dl.layers[0].items()}
+    cb0, cb1 = dl.cb0.cpu(), dl.cb1.cpu()
+    rot_h = CpuRot(None, dl.sign_h.cpu(), 2048)
+    rot_i = CpuRot(None, dl.sign_i.cpu(), 2048)
+    xa, xo, xm, xd = dl.x_attn.cpu(), dl.x_o.cpu(), dl.x_mlp.cpu(), dl.x_down.cpu()
+
+    def step():
+        for name, x, rot in (("q", xa, rot_h), ("k", xa, rot_h), ("v", xa, rot_h), ("o", xo, rot_h),
+                             ("gate", xm, rot_h), ("up", xm, rot_h), ("down", xd, rot_i)):
+            i0, i1, s, out, n = lay[name]
+            packed_linear_fallback(x, rot, i0, i1, cb0, cb1 if i1 is not None else None, s)
+
+    t0 = time.perf_counter()
+    step()
+    first = time.perf_counter() - t0
+    runs = int(max(3, min(20, budget_s / max(first, 1e-3))))
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    gbps = dl.bytes_per_step / med / 1e9
+    log(f"cpu baseline: {med * 1e3:.1f} ms/step median of {runs} on {cores} threads ({cpu}) -> {gbps:.3f} GB/s")
+    return {"value": round(gbps, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"configs[1] one layer step (q,k,v,o,gate,up,down + 4 RHTs), reference PackedLinear "
+                      f"fp32 fallback restated in torch (oracle/ref_cpu_path.py); median of {runs} runs, "
+                      f"{med * 1e3:.1f} ms/step; CPU: {cpu}"}
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (profiles/gemv4_gate_pmc.json), if present."""
+    p = ROOT / "profiles" / "gemv4_gate_pmc.json"
+    try:
+        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# ------------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--layers", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-lmhead", action="store_true")
+    ap.add_argument("--only", choices=["dominant", "copy"], default=None)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {max(args.gpus, world)}); the VQ2 decode "
+              "path is sharded by output rows / experts only by design, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from compressai_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    log(f"device: {torch.cuda.get_device_name(0)}, {torch.cuda.get_device_properties(0).multi_processor_count} CUs")
+
+    if args.only == "dominant":
+        dl = DenseLayers(args.layers, dev)
+        for l in range(args.layers):
+            dl.gemv(dl.layers[l], "gate", dl.xr_m)
+        torch.cuda.synchronize(dev)
+        log("dominant-only run done")
+        return
+    if args.only == "copy":
+        a = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize(dev)
+        log("copy calibration: 4 x 64 MiB device copies done")
+        return
+
+    d = bench_dense(args, dev)
+    moe = None if args.no_moe else bench_moe(args, dev)
+    lm1 = None if args.no_lmhead else bench_lm_head(args, dev, batch=1)
+    lm4 = None if args.no_lmhead else bench_lm_head(args, dev, batch=4)
+    cpu = None if args.no_cpu else cpu_baseline(d["dense"])
+
+    rec = {
+        "metric": metric_name(),
+        "value": round(d["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": d["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "configs[1]: dense decoder-layer projection set, batch 1, hidden 2048 (q,k,v,o 2 bpw; "
+                        "gate,up,down 4 bpw; RHT 2048 x3 + 6144); fp16 codebooks/scales/activations, fp32 out",
+            "layers_cycled": d["layers"],
+            "bytes_per_step": d["bytes_per_step"],
+            "graph_replay": True,
+        },
+        "pct_of_peak": round(100.0 * d["gbps"] / PEAK_HBM_GBPS, 3),
+        "moe_layer_us": None if moe is None else round(moe["us"], 3),
+        "moe_layer_gbps": None if moe is None else round(moe["gbps"], 2),
+        "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
+        "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
+        "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "roofline": {
+            "kernel": "vq_gemv_kernel 4 bpw (16,16), 6144 x 2048, batch 1",
+            "bound": "hbm",
+            "achieved": round(d["dom_gbps"], 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(d["dom_gbps"] / PEAK_HBM_GBPS, 5),
+            "traffic": traffic_from_profiles(),
+            "us_per_launch": round(d["dom_us"], 3),
+            "algorithmic_bytes_per_launch": d["dom_bytes"],
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,307 @@
+// vq2_capi.hip -- the extern "C" boundary of libvq2_amd.so.
+//
+// Every entry validates its arguments on the host (pointers, dtypes, sizes,
+// alignment) and returns a status code; nothing here allocates, synchronises
+// or aborts.  Reference interfaces are cited in include/vq2_amd.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <vector>
+
+#include "vq2_internal.hpp"
+
+namespace vq2 {
+
+static thread_local char g_err[512] = {0};
+
+int set_error(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int set_hip_error(hipError_t err, const char* what)
+{
+    snprintf(g_err, sizeof(g_err), "%s: %s (%d)", what, hipGetErrorString(err), (int)err);
+    return VQ2_ERR_HIP;
+}
+
+void clear_error() { g_err[0] = 0; }
+
+int device_cu_count()
+{
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+    if (cache[dev] == 0) {
+        int cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0) cu = 256;
+        cache[dev] = cu;
+    }
+    return cache[dev];
+}
+
+}  // namespace vq2
+
+using namespace vq2;
+
+#define CHECK(cond, ...)                                    \
+    do {                                                    \
+        if (!(cond)) return set_error(VQ2_ERR_ARG, __VA_ARGS__); \
+    } while (0)
+
+static int check_codebooks(int s2, const void* cb0, const void* cb1, int cb_dt)
+{
+    CHECK(dt_ok(cb_dt), "codebook dtype %d invalid", cb_dt);
+    CHECK(cb0 != nullptr, "cb0 is NULL");
+    CHECK((uintptr_t)cb0 % 16 == 0, "cb0 must be 16-byte aligned");
+    CHECK(s2 == VQ2_S2_NONE || s2 == VQ2_S2_U8 || s2 == VQ2_S2_U16, "s2_kind %d invalid", s2);
+    if (s2 != VQ2_S2_NONE) {
+        CHECK(cb1 != nullptr, "cb1 is NULL for a two-stage matrix");
+        CHECK((uintptr_t)cb1 % 16 == 0, "cb1 must be 16-byte aligned");
+    }
+    return VQ2_OK;
+}
+
+extern "C" {
+
+int vq2_version(void) { return 100; }
+
+const char* vq2_last_error(void) { return g_err; }
+
+int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0, const void* idx1,
+             int s2_kind, const void* cb0, const void* cb1, int cb_dt, const void* scale, int s_dt, void* y, int y_dt,
+             int64_t y_stride, int64_t out_rows, int64_t n, float rs, void* stream)
+{
+    clear_error();
+    CHECK(batch >= 0 && out_rows >= 0 && n > 0, "vq2_gemv: bad sizes batch=%lld out_rows=%lld n=%lld", (long long)batch,
+          (long long)out_rows, (long long)n);
+    CHECK(n % 8 == 0, "vq2_gemv: n=%lld is not a multiple of 8", (long long)n);
+    if (batch == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(x && idx0 && scale && y, "vq2_gemv: NULL pointer argument");
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_gemv: bad dtype code");
+    CHECK(x_stride >= n && y_stride >= out_rows, "vq2_gemv: strides too small");
+    int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
+    if (r) return r;
+    CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "vq2_gemv: idx1 must be given iff s2_kind != NONE");
+    GemvCall c{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.x_bstride = x_stride;
+    c.x_pstride = 0;
+    c.x_pdiv = 1;
+    c.idx0 = idx0;
+    c.idx1 = idx1;
+    c.s2 = s2_kind;
+    c.cb0 = cb0;
+    c.cb1 = cb1;
+    c.cb_dt = cb_dt;
+    c.scale = scale;
+    c.s_dt = s_dt;
+    c.ids = nullptr;
+    c.n_experts = 1;
+    c.P = 1;
+    c.n_out_groups = 1;
+    c.y = y;
+    c.y_dt = y_dt;
+    c.y_bstride = y_stride;
+    c.y_ostride = 0;
+    c.out_rows = out_rows;
+    c.ng = n / 8;
+    c.batch = batch;
+    c.rs = rs;
+    c.stream = stream;
+    return gemv_launch(c);
+}
+
+int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pairs_per_x, const void* ids,
+                    int ids_dt, int64_t n_pairs,
+                    const int16_t* pool, int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt,
+                    void* y, int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    clear_error();
+    CHECK(n_pairs >= 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_grouped: bad sizes");
+    if (n_pairs == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(x && ids && pool && pool_scale && y, "vq2_moe_grouped: NULL pointer argument");
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_moe_grouped: bad dtype code");
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_grouped: bad ids dtype");
+    CHECK(x_pair_stride == 0 || x_pair_stride >= ng * 8, "vq2_moe_grouped: x_pair_stride must be 0 or >= n");
+    CHECK(pairs_per_x >= 1 && pairs_per_x <= 0x7FFFFFFF, "vq2_moe_grouped: pairs_per_x must be >= 1");
+    CHECK(y_pair_stride >= out_rows, "vq2_moe_grouped: y_pair_stride < out_rows");
+    CHECK(n_pairs <= 65535, "vq2_moe_grouped: n_pairs=%lld > 65535", (long long)n_pairs);
+    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    if (r) return r;
+    GemvCall c{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.x_bstride = ng * 8;
+    c.x_pstride = x_pair_stride;
+    c.x_pdiv = (int)pairs_per_x;
+    c.idx0 = pool;
+    c.idx1 = nullptr;
+    c.s2 = VQ2_S2_NONE;
+    c.cb0 = cb;
+    c.cb_dt = cb_dt;
+    c.scale = pool_scale;
+    c.s_dt = s_dt;
+    c.ids = ids;
+    c.ids_i64 = ids_dt == VQ2_ID_I64;
+    c.n_experts = n_experts;
+    c.P = 1;
+    c.n_out_groups = n_pairs;
+    c.y = y;
+    c.y_dt = y_dt;
+    c.y_bstride = 0;
+    c.y_ostride = y_pair_stride;
+    c.out_rows = out_rows;
+    c.ng = ng;
+    c.batch = 1;
+    c.rs = rs;
+    c.stream = stream;
+    return gemv_launch(c);
+}
+
+int vq2_moe_down_combine(const void* x, int x_dt, const void* ids, int ids_dt, const float* w, int64_t tokens,
+                         int64_t P, const int16_t* pool, int64_t n_experts, const void* cb, int cb_dt,
+                         const void* pool_scale, int s_dt, void* out, int out_dt, int64_t out_stride,
+                         int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    clear_error();
+    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_down_combine: bad sizes");
+    if (tokens == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(x && ids && w && pool && pool_scale && out, "vq2_moe_down_combine: NULL pointer argument");
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(out_dt), "vq2_moe_down_combine: bad dtype code");
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_down_combine: bad ids dtype");
+    CHECK(out_stride >= out_rows, "vq2_moe_down_combine: out_stride < out_rows");
+    CHECK(tokens <= 65535 && P <= 4096, "vq2_moe_down_combine: too many tokens/pairs");
+    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    if (r) return r;
+    GemvCall c{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.x_bstride = ng * 8;
+    c.x_pstride = ng * 8;
+    c.x_pdiv = 1;
+    c.idx0 = pool;
+    c.s2 = VQ2_S2_NONE;
+    c.cb0 = cb;
+    c.cb_dt = cb_dt;
+    c.scale = pool_scale;
+    c.s_dt = s_dt;
+    c.ids = ids;
+    c.ids_i64 = ids_dt == VQ2_ID_I64;
+    c.n_experts = n_experts;
+    c.pair_w = w;
+    c.P = (int)P;
+    c.n_out_groups = tokens;
+    c.y = out;
+    c.y_dt = out_dt;
+    c.y_bstride = 0;
+    c.y_ostride = out_stride;
+    c.out_rows = out_rows;
+    c.ng = ng;
+    c.batch = 1;
+    c.rs = rs;
+    c.stream = stream;
+    return gemv_launch(c);
+}
+
+int vq2_rht(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride, const int32_t* perm,
+            const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale, int inverse, void* stream)
+{
+    clear_error();
+    CHECK(n > 0 && batch >= 0 && hb > 0, "vq2_rht: bad sizes");
+    if (batch == 0) return VQ2_OK;
+    CHECK(x && y, "vq2_rht: NULL pointer argument");
+    CHECK(x != y, "vq2_rht: x and y must not overlap");
+    CHECK(dt_ok(x_dt) && dt_ok(y_dt), "vq2_rht: bad dtype code");
+    CHECK(x_stride >= n && y_stride >= n, "vq2_rht: strides too small");
+    return rht_launch(x, x_dt, x_stride, y, y_dt, y_stride, perm, sign, n, hb, batch, scale, inverse, 0, 0, stream);
+}
+
+int vq2_swiglu_rht(const void* gu, int gu_dt, int64_t gu_stride, int64_t inter, void* y, int y_dt, int64_t y_stride,
+                   const int32_t* perm, const int8_t* sign, int64_t hb, int64_t batch, float scale, void* stream)
+{
+    clear_error();
+    CHECK(inter > 0 && batch >= 0 && hb > 0, "vq2_swiglu_rht: bad sizes");
+    if (batch == 0) return VQ2_OK;
+    CHECK(gu && y, "vq2_swiglu_rht: NULL pointer argument");
+    CHECK(dt_ok(gu_dt) && dt_ok(y_dt), "vq2_swiglu_rht: bad dtype code");
+    CHECK(gu_stride >= 2 * inter && y_stride >= inter, "vq2_swiglu_rht: strides too small");
+    return rht_launch(gu, gu_dt, gu_stride, y, y_dt, y_stride, perm, sign, inter, hb, batch, scale, 0, 1, inter,
+                      stream);
+}
+
+int vq2_router_topk(const void* logits, int l_dt, int64_t tokens, int64_t n_experts, int k, const void* h, int h_dt,
+                    int64_t hidden, const void* gate, int g_dt, int64_t shared_id, int32_t* ids, float* w,
+                    void* stream)
+{
+    clear_error();
+    CHECK(tokens >= 0, "vq2_router_topk: bad token count");
+    if (tokens == 0) return VQ2_OK;
+    CHECK(logits && ids && w, "vq2_router_topk: NULL pointer argument");
+    CHECK(dt_ok(l_dt), "vq2_router_topk: bad logits dtype");
+    if (shared_id >= 0) {
+        CHECK(h && gate && hidden > 0, "vq2_router_topk: shared gate needs h, gate and hidden");
+        CHECK(dt_ok(h_dt) && dt_ok(g_dt), "vq2_router_topk: bad h/gate dtype");
+    }
+    return router_launch(logits, l_dt, tokens, n_experts, k, h, h_dt, hidden, gate, g_dt, shared_id, ids, w, stream);
+}
+
+int vq2_argmax_rows(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* out_idx, float* out_val,
+                    void* stream)
+{
+    clear_error();
+    CHECK(rows >= 0 && cols > 0, "vq2_argmax_rows: bad sizes");
+    if (rows == 0) return VQ2_OK;
+    CHECK(v && out_idx, "vq2_argmax_rows: NULL pointer argument");
+    CHECK(dt_ok(v_dt), "vq2_argmax_rows: bad dtype");
+    CHECK((uintptr_t)out_idx % 8 == 0, "vq2_argmax_rows: out_idx must be 8-byte aligned");
+    return argmax_launch(v, v_dt, rows, cols, out_idx, out_val, stream);
+}
+
+int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0, const void* idx1,
+                    int s2_kind, const void* cb0, const void* cb1, int cb_dt, const void* scale, int s_dt,
+                    int64_t out_rows, int64_t n, float rs, float* logits_ws, int64_t* out_idx, float* out_val,
+                    void* stream)
+{
+    clear_error();
+    CHECK(out_rows > 0, "vq2_gemv_argmax: out_rows must be > 0");
+    CHECK(logits_ws && out_idx, "vq2_gemv_argmax: NULL workspace/output");
+    int r = vq2_gemv(x, x_dt, batch, x_stride, idx0, idx1, s2_kind, cb0, cb1, cb_dt, scale, s_dt, logits_ws,
+                     VQ2_DT_F32, out_rows, out_rows, n, rs, stream);
+    if (r) return r;
+    return vq2_argmax_rows(logits_ws, VQ2_DT_F32, batch, out_rows, out_idx, out_val, stream);
+}
+
+int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
+                     const void* scale, int s_dt, int64_t r0, int64_t r1, int64_t n, float* out, void* stream)
+{
+    clear_error();
+    CHECK(r0 >= 0 && r1 >= r0 && n > 0 && n % 8 == 0, "vq2_dequant_rows: bad row range or n");
+    if (r1 == r0) return VQ2_OK;
+    CHECK(idx0 && scale && out, "vq2_dequant_rows: NULL pointer argument");
+    CHECK(dt_ok(s_dt), "vq2_dequant_rows: bad scale dtype");
+    int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
+    if (r) return r;
+    CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "vq2_dequant_rows: idx1 must be given iff s2_kind != NONE");
+    return dequant_launch(idx0, idx1, s2_kind, cb0, cb1, cb_dt, scale, s_dt, r0, r1, n, out, stream);
+}
+
+int vq2_decode_idx(const void* in, int is_u8, int64_t count, int32_t* out, void* stream)
+{
+    clear_error();
+    CHECK(count >= 0, "vq2_decode_idx: bad count");
+    if (count == 0) return VQ2_OK;
+    CHECK(in && out, "vq2_decode_idx: NULL pointer argument");
+    return decode_launch(in, is_u8, count, out, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// vq2_common.hpp -- device helpers shared by the VQ2 decode-path kernels
+// (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq2_amd.h"
+
+namespace vq2 {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------ conversions
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// fp32 -> bf16 bits, round to nearest even, quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Load element i of a float array of runtime dtype dt as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i)
+{
+    if (dt == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    if (dt == VQ2_DT_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+// Store fp32 v into element i of an array of runtime dtype dt.
+__device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v)
+{
+    if (dt == VQ2_DT_F16)
+        ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+    else if (dt == VQ2_DT_BF16)
+        ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+    else
+        ((float*)p)[i] = v;
+}
+
+// ------------------------------------------------------- wave reductions
+// Sum over aligned groups of `width` lanes (width a power of two <= 64);
+// every lane of the group ends with the group sum.  Uses DPP row ops for the
+// in-row steps and ds_swizzle / permlane32 for the cross-row ones.
+__device__ __forceinline__ float dpp_xor1(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)); // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ float dpp_xor2(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)); // quad_perm [2,3,0,1]
+}
+// row_half_mirror: lane i <- lane (i ^ 7) within each 8-lane half row
+__device__ __forceinline__ float dpp_half_mirror(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+}
+// row_mirror: lane i <- lane (i ^ 15) within each 16-lane row
+__device__ __forceinline__ float dpp_row_mirror(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true));
+}
+// lane i <- lane i ^ 16 (ds_swizzle bit mode, and=0x1F, xor=0x10)
+__device__ __forceinline__ float swz_xor16(float v)
+{
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+// lane i <- lane i ^ 32
+__device__ __forceinline__ float xor32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ 32) & 63) << 2, __float_as_int(v)));
+}
+
+// Group sum over `width` lanes.  After the xor1/xor2 steps every lane holds
+// its quad sum, so mirrored partners (i^7, i^15) add the other half.
+__device__ __forceinline__ float group_sum(float v, int width)
+{
+    if (width >= 2) v += dpp_xor1(v);
+    if (width >= 4) v += dpp_xor2(v);
+    if (width >= 8) v += dpp_half_mirror(v);
+    if (width >= 16) v += dpp_row_mirror(v);
+    if (width >= 32) v += swz_xor16(v);
+    if (width >= 64) v += xor32(v);
+    return v;
+}
+
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
+
+}  // namespace vq2

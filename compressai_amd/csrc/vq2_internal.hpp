@@ -1,0 +1,72 @@
+// vq2_internal.hpp -- host-side internals shared by the libvq2_amd sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq2_amd.h"
+
+namespace vq2 {
+
+// Record a formatted error message for vq2_last_error(); returns code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int set_hip_error(hipError_t err, const char* what);
+void clear_error();
+
+// Compute-unit count of the current device (cached per device).
+int device_cu_count();
+
+// One launch of the shared GEMV kernel body (dense / grouped / combine).
+struct GemvCall {
+    const void* x;
+    int x_dt;
+    int64_t x_bstride;  // elements between batch columns of one x block
+    int64_t x_pstride;  // elements between x blocks
+    int x_pdiv;         // pair p reads x block p / x_pdiv
+    const int16_t* idx0;
+    const void* idx1;
+    int s2;
+    const void* cb0;
+    const void* cb1;
+    int cb_dt;
+    const void* scale;
+    int s_dt;
+    const void* ids;  // null: expert 0 for every pair
+    int ids_i64;
+    int64_t n_experts;
+    const float* pair_w;  // combine weights (P > 1)
+    int P;                // pairs per output group
+    int64_t n_out_groups; // grid.y
+    void* y;
+    int y_dt;
+    int64_t y_bstride;
+    int64_t y_ostride;
+    int64_t out_rows;
+    int64_t ng;
+    int64_t batch;
+    float rs;
+    void* stream;
+};
+
+int gemv_launch(const GemvCall& c);
+
+int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
+               const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,
+               int inverse, int swiglu, int64_t inter, void* stream);
+
+int argmax_launch(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* out_idx, float* out_val,
+                  void* stream);
+
+int router_launch(const void* logits, int l_dt, int64_t tokens, int64_t n_experts, int k, const void* h,
+                  int h_dt, int64_t hidden, const void* gate, int g_dt, int64_t shared_id, int32_t* ids, float* w,
+                  void* stream);
+
+int dequant_launch(const int16_t* idx0, const void* idx1, int s2, const void* cb0, const void* cb1, int cb_dt,
+                   const void* scale, int s_dt, int64_t r0, int64_t r1, int64_t n, float* out, void* stream);
+
+int decode_launch(const void* in, int is_u8, int64_t count, int32_t* out, void* stream);
+
+inline bool dt_ok(int dt) { return dt == VQ2_DT_F32 || dt == VQ2_DT_F16 || dt == VQ2_DT_BF16; }
+inline int64_t dt_size(int dt) { return dt == VQ2_DT_F32 ? 4 : 2; }
+
+}  // namespace vq2

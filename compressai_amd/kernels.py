@@ -1,0 +1,427 @@
+"""Drop-in VQ entry points of ``vq2.kernels`` backed by hand-written HIP
+kernels for gfx950 (libvq2_amd.so, C ABI in include/vq2_amd.h).
+
+Kept names and signatures (reference: vq2/kernels.py):
+  vq_gemv_16(xr, i0, cb0, scale, out, n, rs=1.0) -> y[out] bf16        (224-230)
+  vq_gemv_16_8(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0) -> y bf16  (215-221)
+  vq_moe_parallel_gate_up(xr, topk_ids, gate_up_idx, cb16, gate_up_scale,
+                          y_out, OUT=1024, NG=256, rs=1.0) -> None      (246-254)
+  vq_moe_parallel_down(act_r, topk_ids, down_idx, cb16, down_scale,
+                       y_out, OUT=2048, NG=64, rs=1.0) -> None           (256-264)
+  HAVE_TRITON, FUSED_KERNELS_ENABLED, set_fused_kernels_enabled           (9-20)
+  patch_transformers_kernels, optimize_deltanet_layers (no-ops here: the
+  attention / DeltaNet fusions they install are outside this library)
+
+Additive entry points: vq_gemv_16_16 (4 bpw), batched GEMV (x of shape
+[B, n]), vq_rht, vq_swiglu_rht, vq_router_topk, vq_moe_down_combine,
+vq_gemv_argmax, vq_argmax, vq_dequant_rows, vq_decode_idx.
+
+Every entry launches on the current torch stream of the input's device and
+raises ``Vq2Error`` (a RuntimeError) on any invalid argument.  There is no CPU
+or Triton fallback: CPU tensors are rejected and a missing library raises
+ImportError.  Differences from the reference kernels: any OUT (no silent
+tail drop from ``OUT // BR``), ids may be int32 or int64, an id outside the
+pool yields NaN rows instead of an out-of-bounds read, and the output dtype
+is selectable (``out_dtype``; bf16 by default, as in the reference).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import Vq2Error
+
+__all__ = [
+    "HAVE_TRITON", "FUSED_KERNELS_ENABLED", "set_fused_kernels_enabled",
+    "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
+    "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine",
+    "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
+    "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
+    "optimize_deltanet_layers", "Vq2Error",
+]
+
+
+def _library_available() -> bool:
+    try:
+        _lib.load()
+        return True
+    except (ImportError, OSError):
+        return False
+
+
+# "fused GPU kernels available" (the reference's meaning of HAVE_TRITON)
+HAVE_TRITON = _library_available() and torch.cuda.is_available()
+
+FUSED_KERNELS_ENABLED = True
+
+
+def set_fused_kernels_enabled(enabled: bool):
+    """Reference A/B switch (vq2/kernels.py:16-20).  Kept for callers; the VQ
+    entry points below always run the HIP kernels."""
+    global FUSED_KERNELS_ENABLED
+    FUSED_KERNELS_ENABLED = bool(enabled)
+
+
+def patch_transformers_kernels():
+    """Out of scope here (the reference installs attention/DeltaNet Triton
+    fusions, vq2/kernels.py:572-726).  No-op; returns False."""
+    return False
+
+
+def optimize_deltanet_layers(model):
+    """Out of scope here (vq2/kernels.py:443-565).  Returns model unchanged."""
+    return model
+
+
+# ------------------------------------------------------------------ helpers
+_DT = {torch.float32: _lib.DT_F32, torch.float16: _lib.DT_F16, torch.bfloat16: _lib.DT_BF16}
+
+
+def _dt(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise Vq2Error(f"{what}: unsupported dtype {t.dtype} (float32/float16/bfloat16)") from None
+
+
+def _dev(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise Vq2Error("libvq2_amd kernels need GPU tensors (no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise Vq2Error(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _contig(t: torch.Tensor, what: str) -> torch.Tensor:
+    if not t.is_contiguous():
+        raise Vq2Error(f"{what} must be contiguous")
+    return t
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _idx16(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype == torch.uint16:
+        t = t.view(torch.int16)
+    if t.dtype != torch.int16:
+        raise Vq2Error(f"{what}: index plane must be int16 (uint16 codes), got {t.dtype}")
+    return _contig(t, what)
+
+
+def _ids(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    if t.dtype == torch.int32:
+        return _contig(t, "topk_ids"), _lib.ID_I32
+    if t.dtype == torch.int64:
+        return _contig(t, "topk_ids"), _lib.ID_I64
+    raise Vq2Error(f"topk_ids must be int32 or int64, got {t.dtype}")
+
+
+# --------------------------------------------------------------- dense GEMV
+def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """Generic VQ GEMV: 2 bpw (i1 None), 3 bpw (i1 uint8) or 4 bpw (i1 int16).
+    xr [n] -> y [out]; xr [B, n] -> y [B, out]."""
+    dev = _dev(xr, i0, i1, cb0, cb1, scale, y)
+    n = int(n)
+    out = int(out)
+    x2 = xr.reshape(-1, n) if xr.dim() != 2 else xr
+    if x2.shape[-1] != n or x2.stride(-1) != 1:
+        raise Vq2Error(f"xr must have a unit-stride last dim of size n={n}")
+    B = x2.shape[0]
+    i0 = _idx16(i0, "i0")
+    if i0.numel() != out * (n // 8):
+        raise Vq2Error(f"i0 has {i0.numel()} codes, expected out*n/8 = {out * (n // 8)}")
+    s2 = _lib.S2_NONE
+    if i1 is not None:
+        if i1.dtype == torch.uint8:
+            s2 = _lib.S2_U8
+            if cb1.shape[0] < 256:
+                raise Vq2Error("cb1 must have 256 rows for a uint8 stage-2 plane")
+        else:
+            i1 = _idx16(i1, "i1")
+            s2 = _lib.S2_U16
+            if cb1.shape[0] < 65536:
+                raise Vq2Error("cb1 must have 65536 rows for an int16 stage-2 plane")
+        _contig(i1, "i1")
+        if i1.numel() != i0.numel():
+            raise Vq2Error("i1 and i0 must have the same number of codes")
+        _contig(cb1, "cb1")
+        if cb1.dtype != cb0.dtype:
+            raise Vq2Error("cb0 and cb1 must share a dtype")
+    _contig(cb0, "cb0")
+    if cb0.shape[-1] != 8 or cb0.shape[0] < 65536:
+        raise Vq2Error(f"cb0 must be [65536, 8], got {tuple(cb0.shape)}")
+    _contig(scale, "scale")
+    if scale.numel() != out:
+        raise Vq2Error(f"scale has {scale.numel()} entries, expected {out}")
+    if y is None:
+        y = torch.empty((B, out) if xr.dim() == 2 else (out,), dtype=out_dtype, device=dev)
+    else:
+        _contig(y, "y")
+        if y.numel() != B * out:
+            raise Vq2Error("y has the wrong size")
+    _lib.call("vq2_gemv", _p(x2), _dt(x2, "xr"), B, x2.stride(0) if B > 1 else n,
+              _p(i0), _p(i1), s2, _p(cb0), _p(cb1), _dt(cb0, "cb0"), _p(scale), _dt(scale, "scale"),
+              _p(y), _dt(y, "y"), out, out, n, float(rs), _stream(dev))
+    return y
+
+
+def vq_gemv_16(xr, i0, cb0, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """xr [n] -> y [out] for a 2.0 bpw (16,) matrix (vq2/kernels.py:224-230)."""
+    return vq_gemv(xr, i0, None, cb0, None, scale, out, n, rs, out_dtype=out_dtype, y=y)
+
+
+def vq_gemv_16_8(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """xr [n] -> y [out] for a 3.0 bpw (16,8) matrix (vq2/kernels.py:215-221)."""
+    if i1.dtype != torch.uint8:
+        raise Vq2Error("vq_gemv_16_8: i1 must be uint8")
+    return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
+
+
+def vq_gemv_16_16(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """xr [n] -> y [out] for a 4.0 bpw (16,16) matrix: both planes decoded as
+    uint16 (the PackedLinear fallback semantics, vq2/runtime.py:82-89)."""
+    if i1.dtype == torch.uint8:
+        raise Vq2Error("vq_gemv_16_16: i1 must be int16 (uint16 codes)")
+    return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
+
+
+# -------------------------------------------------------------- grouped MoE
+def _moe_checks(pool, scale, OUT, NG, what):
+    pool = _idx16(pool, what)
+    if pool.dim() != 3 or pool.shape[1] != OUT or pool.shape[2] != NG:
+        raise Vq2Error(f"{what}: pool must be [E, {OUT}, {NG}], got {tuple(pool.shape)}")
+    _contig(scale, "scale")
+    if scale.numel() != pool.shape[0] * OUT:
+        raise Vq2Error(f"{what}: scale must be [E, {OUT}]")
+    return pool
+
+
+def vq_moe_parallel_gate_up(xr, topk_ids, gate_up_idx, cb16, gate_up_scale, y_out, OUT=1024, NG=256, rs=1.0):
+    """y_out[k, :OUT] = VQ(pool[topk_ids[k]]) xr for every k (x shared).
+    Writes y_out in place, returns None (vq2/kernels.py:246-254)."""
+    dev = _dev(xr, topk_ids, gate_up_idx, cb16, gate_up_scale, y_out)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(gate_up_idx, gate_up_scale, OUT, NG, "gate_up_idx")
+    ids, ids_dt = _ids(topk_ids)
+    K = ids.numel()
+    x = _contig(xr, "xr").reshape(-1)
+    if x.numel() < NG * 8:
+        raise Vq2Error(f"xr has {x.numel()} values, need {NG * 8}")
+    if y_out.dim() != 2 or y_out.shape[0] < K or y_out.shape[1] < OUT or y_out.stride(1) != 1:
+        raise Vq2Error("y_out must be [>=K, >=OUT] with unit column stride")
+    _contig(cb16, "cb16")
+    _lib.call("vq2_moe_grouped", _p(x), _dt(x, "xr"), 0, 1, _p(ids), ids_dt, K, _p(pool), pool.shape[0],
+              _p(cb16), _dt(cb16, "cb16"), _p(gate_up_scale), _dt(gate_up_scale, "scale"),
+              _p(y_out), _dt(y_out, "y_out"), y_out.stride(0), OUT, NG, float(rs), _stream(dev))
+
+
+def vq_moe_parallel_down(act_r, topk_ids, down_idx, cb16, down_scale, y_out, OUT=2048, NG=64, rs=1.0):
+    """y_out[k, :OUT] = VQ(pool[topk_ids[k]]) act_r[k] (one activation per
+    expert).  Writes y_out in place, returns None (vq2/kernels.py:256-264)."""
+    dev = _dev(act_r, topk_ids, down_idx, cb16, down_scale, y_out)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(down_idx, down_scale, OUT, NG, "down_idx")
+    ids, ids_dt = _ids(topk_ids)
+    K = ids.numel()
+    a = _contig(act_r, "act_r").reshape(-1)
+    if a.numel() < K * NG * 8:
+        raise Vq2Error(f"act_r has {a.numel()} values, need K*NG*8 = {K * NG * 8}")
+    if y_out.dim() != 2 or y_out.shape[0] < K or y_out.shape[1] < OUT or y_out.stride(1) != 1:
+        raise Vq2Error("y_out must be [>=K, >=OUT] with unit column stride")
+    _contig(cb16, "cb16")
+    _lib.call("vq2_moe_grouped", _p(a), _dt(a, "act_r"), NG * 8, 1, _p(ids), ids_dt, K, _p(pool), pool.shape[0],
+              _p(cb16), _dt(cb16, "cb16"), _p(down_scale), _dt(down_scale, "scale"),
+              _p(y_out), _dt(y_out, "y_out"), y_out.stride(0), OUT, NG, float(rs), _stream(dev))
+
+
+def vq_moe_grouped(x, ids, pool, cb16, pool_scale, y_out, OUT, NG, rs=1.0, pairs_per_x=1, shared_x=False):
+    """General grouped launch: y_out[k] = VQ(pool[ids.flat[k]]) x_k with
+    x_k = x[k // pairs_per_x] (or x itself for every k when shared_x)."""
+    dev = _dev(x, ids, pool, cb16, pool_scale, y_out)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(pool, pool_scale, OUT, NG, "pool")
+    ids2, ids_dt = _ids(ids)
+    K = ids2.numel()
+    xx = _contig(x, "x").reshape(-1)
+    need = NG * 8 if shared_x else ((K + pairs_per_x - 1) // pairs_per_x) * NG * 8
+    if xx.numel() < need:
+        raise Vq2Error(f"x has {xx.numel()} values, need {need}")
+    y2 = y_out.reshape(-1, y_out.shape[-1]) if y_out.dim() != 2 else y_out
+    if y2.shape[0] < K or y2.shape[1] < OUT or y2.stride(1) != 1:
+        raise Vq2Error("y_out must be [>=K, >=OUT] with unit column stride")
+    _contig(cb16, "cb16")
+    _lib.call("vq2_moe_grouped", _p(xx), _dt(xx, "x"), 0 if shared_x else NG * 8, int(pairs_per_x), _p(ids2),
+              ids_dt, K, _p(pool), pool.shape[0], _p(cb16), _dt(cb16, "cb16"), _p(pool_scale),
+              _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
+    return y_out
+
+
+def vq_moe_down_combine(act_r, ids, w, down_idx, cb16, down_scale, out=None, OUT=2048, NG=64, rs=1.0,
+                        out_dtype=torch.float32):
+    """Grouped down projection fused with the weighted combine.
+    act_r [T*P, NG*8], ids [T, P], w fp32 [T, P] -> out [T, OUT] with
+    out[t] = sum_j w[t, j] * VQ(pool[ids[t, j]]) act_r[t*P + j]."""
+    dev = _dev(act_r, ids, w, down_idx, cb16, down_scale, out)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(down_idx, down_scale, OUT, NG, "down_idx")
+    ids2, ids_dt = _ids(ids)
+    if ids2.dim() != 2:
+        raise Vq2Error("ids must be [T, P]")
+    T, P = ids2.shape
+    if w.dtype != torch.float32 or w.numel() != T * P:
+        raise Vq2Error("w must be float32 [T, P]")
+    _contig(w, "w")
+    a = _contig(act_r, "act_r")
+    if a.numel() != T * P * NG * 8:
+        raise Vq2Error("act_r must be [T*P, NG*8]")
+    if out is None:
+        out = torch.empty((T, OUT), dtype=out_dtype, device=dev)
+    _contig(out, "out")
+    _lib.call("vq2_moe_down_combine", _p(a), _dt(a, "act_r"), _p(ids2), ids_dt, _p(w), T, P, _p(pool),
+              pool.shape[0], _p(cb16), _dt(cb16, "cb16"), _p(down_scale), _dt(down_scale, "scale"),
+              _p(out), _dt(out, "out"), OUT, OUT, NG, float(rs), _stream(dev))
+    return out
+
+
+# --------------------------------------------------------------------- RHT
+def vq_rht(x, perm=None, sign=None, hb=2048, scale=None, inverse=False, *, out=None, out_dtype=None):
+    """Randomised Hadamard transform over the last dim (vq2/vq.py:74-87):
+    forward y = blockdiag(H_hb)(sign * x[perm]) * scale, inverse undoes it.
+    scale defaults to hb**-0.5."""
+    dev = _dev(x, perm, sign, out)
+    n = x.shape[-1]
+    x2 = _contig(x, "x").reshape(-1, n)
+    B = x2.shape[0]
+    if perm is not None:
+        if perm.dtype != torch.int32 or perm.numel() != n:
+            raise Vq2Error("perm must be int32 [n]")
+        _contig(perm, "perm")
+    if sign is not None:
+        if sign.dtype != torch.int8 or sign.numel() != n:
+            raise Vq2Error("sign must be int8 [n] of +-1")
+        _contig(sign, "sign")
+    sc = float(hb) ** -0.5 if scale is None else float(scale)
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=dev)
+    _contig(out, "out")
+    _lib.call("vq2_rht", _p(x2), _dt(x2, "x"), n, _p(out), _dt(out, "out"), n, _p(perm), _p(sign),
+              n, int(hb), B, sc, 1 if inverse else 0, _stream(dev))
+    return out
+
+
+def vq_swiglu_rht(gu, inter, perm=None, sign=None, hb=None, scale=None, *, out=None, out_dtype=torch.float32):
+    """act = silu(gu[..., :inter]) * gu[..., inter:2*inter], then the forward
+    RHT of act (vq2/paged_runtime.py:501-504 fused)."""
+    dev = _dev(gu, perm, sign, out)
+    inter = int(inter)
+    g2 = _contig(gu, "gu").reshape(-1, gu.shape[-1])
+    if g2.shape[-1] < 2 * inter:
+        raise Vq2Error("gu last dim must be >= 2*inter")
+    hb = inter if hb is None else int(hb)
+    B = g2.shape[0]
+    for t, nm, dt in ((perm, "perm", torch.int32), (sign, "sign", torch.int8)):
+        if t is not None and (t.dtype != dt or t.numel() != inter):
+            raise Vq2Error(f"{nm} must be {dt} [{inter}]")
+    sc = float(hb) ** -0.5 if scale is None else float(scale)
+    if out is None:
+        out = torch.empty((*gu.shape[:-1], inter), dtype=out_dtype, device=dev)
+    _contig(out, "out")
+    _lib.call("vq2_swiglu_rht", _p(g2), _dt(g2, "gu"), g2.shape[-1], inter, _p(out), _dt(out, "out"), inter,
+              _p(perm), _p(sign), hb, B, sc, _stream(dev))
+    return out
+
+
+# ------------------------------------------------------------ router / top-1
+def vq_router_topk(logits, k=8, h=None, shared_gate=None, shared_id=-1, *, ids=None, w=None):
+    """Softmax (fp32) -> top-k -> renormalise per token (transformers
+    Qwen3_5MoeTopKRouter).  With shared_id >= 0 an extra slot k carries the
+    shared expert with weight sigmoid(shared_gate . h).  Returns
+    (ids int32 [T, k(+1)], w float32 [T, k(+1)])."""
+    dev = _dev(logits, h, shared_gate, ids, w)
+    lg = _contig(logits, "logits").reshape(-1, logits.shape[-1])
+    T, E = lg.shape
+    extra = 1 if shared_id >= 0 else 0
+    hid = 0
+    if extra:
+        if h is None or shared_gate is None:
+            raise Vq2Error("shared expert gate needs h and shared_gate")
+        hid = shared_gate.numel()
+        h = _contig(h, "h").reshape(T, hid)
+        _contig(shared_gate, "shared_gate")
+    if ids is None:
+        ids = torch.empty((T, k + extra), dtype=torch.int32, device=dev)
+    if w is None:
+        w = torch.empty((T, k + extra), dtype=torch.float32, device=dev)
+    _lib.call("vq2_router_topk", _p(lg), _dt(lg, "logits"), T, E, int(k), _p(h) if extra else None,
+              _dt(h, "h") if extra else 0, hid, _p(shared_gate) if extra else None,
+              _dt(shared_gate, "gate") if extra else 0, int(shared_id), _p(ids), _p(w), _stream(dev))
+    return ids, w
+
+
+def vq_argmax(v):
+    """First-maximum index per row of v [rows, cols] -> (idx int64, val fp32)."""
+    dev = _dev(v)
+    v2 = _contig(v, "v").reshape(-1, v.shape[-1])
+    idx = torch.empty(v2.shape[0], dtype=torch.int64, device=dev)
+    val = torch.empty(v2.shape[0], dtype=torch.float32, device=dev)
+    _lib.call("vq2_argmax_rows", _p(v2), _dt(v2, "v"), v2.shape[0], v2.shape[1], _p(idx), _p(val), _stream(dev))
+    return idx, val
+
+
+def vq_gemv_argmax(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, logits_ws=None):
+    """LM head + top-1: (idx int64 [B], val fp32 [B]) of the argmax of the VQ
+    GEMV logits (PackedLMHead, vq2/runtime.py:136-144, then torch.argmax)."""
+    dev = _dev(xr, i0, i1, cb0, cb1, scale)
+    n, out = int(n), int(out)
+    x2 = _contig(xr, "xr").reshape(-1, n)
+    B = x2.shape[0]
+    if logits_ws is None:
+        logits_ws = torch.empty((B, out), dtype=torch.float32, device=dev)
+    vq_gemv(x2, i0, i1, cb0, cb1, scale, out, n, rs, y=logits_ws)
+    return vq_argmax(logits_ws)
+
+
+# --------------------------------------------------------------- debugging
+def vq_dequant_rows(i0, i1, cb0, cb1, scale, r0=0, r1=None):
+    """Rotated-space fp32 rows [r1-r0, n] (QMat.dequant before rot.inv,
+    vq2/vq.py:283-292): (f32(cb0[i0]) [+ f32(cb1[i1])]) * f32(scale[r])."""
+    dev = _dev(i0, i1, cb0, cb1, scale)
+    i0 = _idx16(i0, "i0")
+    out_rows, ng = i0.shape
+    r1 = out_rows if r1 is None else int(r1)
+    s2 = _lib.S2_NONE
+    if i1 is not None:
+        s2 = _lib.S2_U8 if i1.dtype == torch.uint8 else _lib.S2_U16
+        if s2 == _lib.S2_U16:
+            i1 = _idx16(i1, "i1")
+        _contig(i1, "i1")
+    y = torch.empty((r1 - int(r0), ng * 8), dtype=torch.float32, device=dev)
+    _lib.call("vq2_dequant_rows", _p(i0), _p(i1), s2, _p(_contig(cb0, "cb0")),
+              _p(cb1.contiguous()) if cb1 is not None else None, _dt(cb0, "cb0"), _p(_contig(scale, "scale")),
+              _dt(scale, "scale"), int(r0), r1, ng * 8, _p(y), _stream(dev))
+    return y
+
+
+def vq_decode_idx(idx):
+    """int16 plane -> int32 uint16 codes (& 0xFFFF); uint8 -> int32 values
+    (vq2/runtime.py:32-35)."""
+    dev = _dev(idx)
+    is_u8 = 1 if idx.dtype == torch.uint8 else 0
+    if not is_u8:
+        idx = _idx16(idx, "idx")
+    idx = _contig(idx, "idx")
+    out = torch.empty(idx.shape, dtype=torch.int32, device=dev)
+    _lib.call("vq2_decode_idx", _p(idx), is_u8, idx.numel(), _p(out), _stream(dev))
+    return out

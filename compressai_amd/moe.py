@@ -1,0 +1,107 @@
+"""MoE expert layer of the decode path on a device-resident expert pool.
+
+``ResidentMoEExperts`` is the drop-in for the reference's resident expert
+module ``PackedMoEExpertUniversal`` (vq2/load_and_test_full_35b.py:26-95):
+``forward(hidden_states [T, H], topk_idx [T, K], topk_weights [T, K])``
+returns ``[T, H]``, computing per token t and expert e = topk_idx[t, k]
+
+    xr  = rot_H.fwd(h_t)                                   (RHT, hb = 2048)
+    gu  = VQ(gate_up[e]) xr                                 ([2I], gate | up)
+    act = rot_I.fwd(silu(gu[:I]) * gu[I:])                  (RHT, hb = I)
+    out_t = sum_k w[t, k] * VQ(down[e]) act
+
+(vq2/paged_runtime.py:495-510).  Instead of the reference's per-token Python
+loop (load_and_test_full_35b.py:75-95) every token and expert goes into one
+launch per stage: RHT -> grouped gate_up -> fused SwiGLU+RHT -> grouped down
+with the weighted combine in the epilogue.  Expert ids are read on the device:
+no ``.tolist()`` and no host synchronisation.
+
+``MoELayer`` adds the router (softmax -> top-k -> renormalise on given
+logits) and the shared expert with its sigmoid gate (transformers 5.15.0
+``Qwen3_5MoeTopKRouter`` / ``Qwen3_5MoeSparseMoeBlock``), the shared expert
+living in the same pool at id ``n_routed``.  The whole layer is five
+launches and no host synchronisation.
+
+Intermediates are fp32 by default (the parity contract); ``act_dtype`` may
+select bf16 to follow the reference's cast points instead.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import kernels as K
+from .rot import get_rot
+
+
+class ResidentMoEExperts(nn.Module):
+    def __init__(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h=None, rot_i=None,
+                 act_dtype=torch.float32, out_dtype=None):
+        super().__init__()
+        E, gu_rows, ng_h = gate_up_idx.shape
+        E2, hidden, ng_i = down_idx.shape
+        if E2 != E or gu_rows != 2 * ng_i * 8 or hidden != ng_h * 8:
+            raise K.Vq2Error("inconsistent gate_up/down pool shapes")
+        self.num_experts = E
+        self.hidden_dim = hidden
+        self.intermediate_dim = ng_i * 8
+        dev = gate_up_idx.device
+        self.gate_up_idx = gate_up_idx
+        self.gate_up_scale = gate_up_scale
+        self.down_idx = down_idx
+        self.down_scale = down_scale
+        self.cb16 = cb16
+        self.rot_h = rot_h if rot_h is not None else get_rot("moe_expert_2048", hidden, dev)
+        self.rot_i = rot_i if rot_i is not None else get_rot("moe_expert_512", self.intermediate_dim, dev)
+        self.act_dtype = act_dtype
+        self.out_dtype = out_dtype
+
+    def experts(self, xr, ids, w, out=None):
+        """xr [T, H] (rotated), ids [T, P] int32/int64, w fp32 [T, P] -> [T, H]."""
+        T, P = ids.shape
+        I = self.intermediate_dim
+        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=xr.device)
+        K.vq_moe_grouped(xr, ids, self.gate_up_idx, self.cb16, self.gate_up_scale, y_gu, OUT=2 * I,
+                         NG=self.hidden_dim // 8, pairs_per_x=P)
+        act_r = K.vq_swiglu_rht(y_gu, I, self.rot_i._perm32, self.rot_i._sign8, self.rot_i.hb,
+                                self.rot_i.scale, out_dtype=self.act_dtype)
+        return K.vq_moe_down_combine(act_r, ids, w, self.down_idx, self.cb16, self.down_scale, out=out,
+                                     OUT=self.hidden_dim, NG=I // 8,
+                                     out_dtype=self.out_dtype or torch.float32)
+
+    def forward(self, hidden_states, topk_idx, topk_weights):
+        h = hidden_states.reshape(-1, self.hidden_dim)
+        xr = self.rot_h.fwd(h.contiguous(), out_dtype=self.act_dtype)
+        ids = topk_idx.reshape(h.shape[0], -1)
+        if ids.dtype not in (torch.int32, torch.int64):
+            ids = ids.to(torch.int32)
+        w = topk_weights.reshape(ids.shape).to(torch.float32).contiguous()
+        out = self.experts(xr, ids.contiguous(), w)
+        return out.to(self.out_dtype or hidden_states.dtype)
+
+
+class MoELayer(nn.Module):
+    """Router + top-k routed experts + gated shared expert, one pool.
+
+    pools: gate_up_idx [E+1, 2I, H/8], down_idx [E+1, H, I/8] (int16), scales
+    [E+1, 2I] / [E+1, H]; id E is the shared expert.  shared_gate [H]."""
+
+    def __init__(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, shared_gate, top_k=8,
+                 n_routed=None, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=torch.float32):
+        super().__init__()
+        self.experts_mod = ResidentMoEExperts(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h,
+                                              rot_i, act_dtype, out_dtype)
+        self.n_routed = gate_up_idx.shape[0] - 1 if n_routed is None else int(n_routed)
+        self.top_k = int(top_k)
+        self.shared_gate = shared_gate
+        self.out_dtype = out_dtype
+
+    def route(self, h, router_logits):
+        return K.vq_router_topk(router_logits, self.top_k, h, self.shared_gate, shared_id=self.n_routed)
+
+    def forward(self, h, router_logits):
+        m = self.experts_mod
+        h2 = h.reshape(-1, m.hidden_dim).contiguous()
+        ids, w = self.route(h2, router_logits.reshape(h2.shape[0], -1).contiguous())
+        xr = m.rot_h.fwd(h2, out_dtype=m.act_dtype)
+        return m.experts(xr, ids, w)

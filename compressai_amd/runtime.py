@@ -1,0 +1,74 @@
+"""Dense packed-linear callers of the VQ GEMV (reference: vq2/runtime.py).
+
+``PackedLinear(shape, cfg, tag, idx, scale, cbs, device)`` keeps the
+reference constructor (vq2/runtime.py:70-80): ``idx`` is the list of index
+planes (int16 for 16-bit stages, uint8 for 8-bit stages), ``scale`` the
+per-row scales, ``cbs`` a dict of codebooks keyed by the cfg prefix
+("16", "16_8", "16_16").  ``forward(x)`` rotates x with the layer's RHT and
+runs the fused VQ GEMV for every batch size and every cfg in (16,),
+(16, 8), (16, 16) -- the reference fuses only batch 1 of (16,) and (16, 8)
+and otherwise re-materialises the dequantized matrix (runtime.py:91-110).
+``PackedLMHead`` (runtime.py:136-144) wraps it and adds ``argmax``.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import kernels as K
+from .rot import get_rot
+
+
+def cfg_key(cfg, i):
+    return "_".join(str(b) for b in cfg[: i + 1])
+
+
+class PackedLinear(nn.Module):
+    def __init__(self, shape, cfg, tag, idx, scale, cbs, device, act_dtype=torch.float32):
+        super().__init__()
+        self.out, self.n = int(shape[0]), int(shape[1])
+        self.cfg, self.tag = tuple(cfg), tag
+        if self.cfg not in ((16,), (16, 8), (16, 16)):
+            raise K.Vq2Error(f"unsupported cfg {self.cfg}")
+        self.keys = [cfg_key(self.cfg, i) for i in range(len(self.cfg))]
+        for i, a in enumerate(idx):
+            self.register_buffer(f"idx{i}", a.to(device).contiguous(), persistent=False)
+        self.register_buffer("scale", scale.to(device=device).contiguous(), persistent=False)
+        self._cbs = [cbs]
+        self.rot = get_rot(tag, self.n, device)
+        self.act_dtype = act_dtype
+
+    def _planes(self):
+        i1 = getattr(self, "idx1", None)
+        cb0 = self._cbs[0][self.keys[0]]
+        cb1 = self._cbs[0][self.keys[1]] if len(self.keys) > 1 else None
+        return self.idx0, i1, cb0, cb1
+
+    def forward(self, x, out_dtype=None):
+        xr = self.rot.fwd(x.reshape(-1, self.n).contiguous(), out_dtype=self.act_dtype)
+        i0, i1, cb0, cb1 = self._planes()
+        y = K.vq_gemv(xr, i0, i1, cb0, cb1, self.scale, self.out, self.n, 1.0,
+                      out_dtype=out_dtype or x.dtype)
+        return y.view(*x.shape[:-1], self.out)
+
+    def nbytes(self):
+        return sum(b.numel() * b.element_size() for b in self.buffers())
+
+
+class PackedLMHead(nn.Module):
+    """lm_head sharing the packed weights of a PackedLinear."""
+
+    def __init__(self, lin: PackedLinear):
+        super().__init__()
+        self.lin = lin
+
+    def forward(self, x):
+        return self.lin(x)
+
+    def argmax(self, x):
+        """Top-1 token per row of x without materialising bf16 logits:
+        (idx int64 [B], logit fp32 [B])."""
+        lin = self.lin
+        xr = lin.rot.fwd(x.reshape(-1, lin.n).contiguous(), out_dtype=lin.act_dtype)
+        i0, i1, cb0, cb1 = lin._planes()
+        return K.vq_gemv_argmax(xr, i0, i1, cb0, cb1, lin.scale, lin.out, lin.n, 1.0)

@@ -1,0 +1,177 @@
+/*
+ * vq2_amd.h -- C ABI of the MI355X-native VQ2 decode hot path
+ * (libvq2_amd.so, HIP kernels for gfx950).
+ *
+ * Conventions
+ *   - Every entry returns an int status: VQ2_OK (0) or a VQ2_ERR_* code.  On
+ *     error, vq2_last_error() returns a thread-local message.  No entry aborts.
+ *   - All pointers are device pointers unless stated otherwise; every array is
+ *     dense (C-contiguous) with the strides given in elements.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Entries only
+ *     enqueue work: no allocation, no host synchronisation, so they can be
+ *     captured in a HIP graph.
+ *   - Index planes hold uint16 codes stored as int16 bit patterns and are
+ *     decoded as (int32)v & 0xFFFF; uint8 stage-2 planes are used as is.
+ *   - Activations, codebooks, scales and outputs take a dtype code
+ *     (VQ2_DT_*); all arithmetic is fp32.
+ *
+ * Reference interfaces (paths relative to the reference repository) are
+ * cited beside each entry.
+ */
+#ifndef VQ2_AMD_H
+#define VQ2_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element dtypes */
+#define VQ2_DT_F32 0
+#define VQ2_DT_F16 1
+#define VQ2_DT_BF16 2
+
+/* stage-2 index plane kinds */
+#define VQ2_S2_NONE 0 /* cfg (16,):   2 bpw, one int16 plane                        */
+#define VQ2_S2_U8 1   /* cfg (16,8):  3 bpw, + uint8 plane into a 256 x 8 codebook   */
+#define VQ2_S2_U16 2  /* cfg (16,16): 4 bpw, + int16 plane into a 65536 x 8 codebook */
+
+/* expert-id dtypes */
+#define VQ2_ID_I32 0
+#define VQ2_ID_I64 1
+
+/* status codes */
+#define VQ2_OK 0
+#define VQ2_ERR_ARG 1         /* null pointer, bad size, dtype or alignment */
+#define VQ2_ERR_HIP 2         /* a HIP runtime call failed                  */
+#define VQ2_ERR_UNSUPPORTED 3 /* valid but unsupported shape               */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int vq2_version(void);
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* vq2_last_error(void);
+
+/* Dense VQ GEMV, batched:  y[b, r] = (sum_k W[r, k] * x[b, k]) * scale[r] * rs
+ * with W[r, 8g+j] = cb0[i0[r,g]][j] (+ cb1[i1[r,g]][j] for 3/4 bpw).
+ *   x      [batch, x_stride] (n used), dtype x_dt
+ *   idx0   [out_rows, n/8] int16;  idx1 [out_rows, n/8] uint8 (S2_U8) or int16 (S2_U16) or NULL
+ *   cb0    [65536, 8];  cb1 [256, 8] (S2_U8) or [65536, 8] (S2_U16), both dtype cb_dt, 16-byte aligned
+ *   scale  [out_rows] dtype s_dt;   y [batch, y_stride] dtype y_dt
+ * n must be a multiple of 8.
+ * Replaces vq_gemv_16 (vq2/kernels.py:224-230) and vq_gemv_16_8
+ * (vq2/kernels.py:215-221); adds the (16,16) 4 bpw variant (the reference's
+ * PackedLinear.weight_rows + F.linear fallback, vq2/runtime.py:82-110) and
+ * batch > 1 (same fallback). */
+int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+             const int16_t* idx0, const void* idx1, int s2_kind,
+             const void* cb0, const void* cb1, int cb_dt,
+             const void* scale, int s_dt,
+             void* y, int y_dt, int64_t y_stride,
+             int64_t out_rows, int64_t n, float rs, void* stream);
+
+/* Grouped per-expert 2 bpw VQ GEMV over a device-resident expert pool:
+ *   e = ids[k];  y[k, r] = (sum_g cb[pool[e, r, g]] . x_k[8g:8g+8]) * pool_scale[e, r] * rs
+ *   x_k = x + (k / pairs_per_x) * x_pair_stride
+ *         (stride 0: one activation shared by all pairs, as gate_up;
+ *          stride n, pairs_per_x 1: one per pair, as down;
+ *          stride n, pairs_per_x P: token t's activation for its P experts)
+ *   ids    [n_pairs] int32/int64 on device (expert ids or slot ids); an id
+ *          outside [0, n_experts) produces NaN rows instead of a fault
+ *   pool   [n_experts, out_rows, ng] int16;  pool_scale [n_experts, out_rows]
+ *   y      [n_pairs, y_pair_stride]
+ * Replaces vq_moe_parallel_gate_up (vq2/kernels.py:246-254) and
+ * vq_moe_parallel_down (vq2/kernels.py:256-264). */
+int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pairs_per_x,
+                    const void* ids, int ids_dt, int64_t n_pairs,
+                    const int16_t* pool, int64_t n_experts,
+                    const void* cb, int cb_dt,
+                    const void* pool_scale, int s_dt,
+                    void* y, int y_dt, int64_t y_pair_stride,
+                    int64_t out_rows, int64_t ng, float rs, void* stream);
+
+/* Grouped down projection fused with the weighted expert combine:
+ *   out[t, r] = sum_{j < P} w[t*P+j] * (VQ(pool[ids[t*P+j]]) x_{t*P+j})[r]
+ * with x_p = x + p * ng*8 and each term (acc * scale) * rs as in
+ * vq2_moe_grouped.  w is fp32 [tokens*P] on device.
+ * Replaces the vq_moe_parallel_down call plus (y_down * topk_w[:, None]).sum(0)
+ * of PagedMoEExpert.forward (vq2/paged_runtime.py:505-510). */
+int vq2_moe_down_combine(const void* x, int x_dt,
+                         const void* ids, int ids_dt, const float* w, int64_t tokens, int64_t P,
+                         const int16_t* pool, int64_t n_experts,
+                         const void* cb, int cb_dt,
+                         const void* pool_scale, int s_dt,
+                         void* out, int out_dt, int64_t out_stride,
+                         int64_t out_rows, int64_t ng, float rs, void* stream);
+
+/* Randomised Hadamard transform over the last dim, hb-point blocks:
+ *   forward: v[i] = x[perm[i]] * sign[i];  y_blk = H_hb v_blk * scale
+ *   inverse: z_blk = H_hb x_blk * scale;   y[perm[i]] = z[i] * sign[i]
+ * H_hb is the Sylvester Hadamard matrix (natural order).  perm (int32 [n])
+ * and sign (int8 +-1 [n]) may be NULL (identity / all +1).  hb is a power of
+ * two in [2, 8192] dividing n.  x and y must not overlap.
+ * Replaces Rot.fwd / Rot.inv (vq2/vq.py:74-87) and FastRot.__call__
+ * (vq2/runtime.py:57-63, which is scale = 1). */
+int vq2_rht(const void* x, int x_dt, int64_t x_stride,
+            void* y, int y_dt, int64_t y_stride,
+            const int32_t* perm, const int8_t* sign,
+            int64_t n, int64_t hb, int64_t batch, float scale, int inverse, void* stream);
+
+/* MoE expert epilogue fused with the intermediate RHT:
+ *   act = silu(gu[b, :inter]) * gu[b, inter:2*inter];  y[b] = RHT_fwd(act)
+ * Replaces act = (silu(gate.f32) * up.f32) and rot_512.fwd(act) of
+ * PagedMoEExpert.forward (vq2/paged_runtime.py:501-504). */
+int vq2_swiglu_rht(const void* gu, int gu_dt, int64_t gu_stride, int64_t inter,
+                   void* y, int y_dt, int64_t y_stride,
+                   const int32_t* perm, const int8_t* sign,
+                   int64_t hb, int64_t batch, float scale, void* stream);
+
+/* Top-k router on given logits, per token (transformers 5.15.0
+ * Qwen3_5MoeTopKRouter.forward: softmax in fp32 -> topk -> renormalise):
+ *   ids[t, j] (int32), w[t, j] (fp32), j < k, in descending-probability order
+ *   (ties toward the lower expert id).  Row stride of ids/w is k + extra.
+ * If shared_id >= 0, slot k of each row gets the shared expert:
+ *   ids[t, k] = shared_id,  w[t, k] = sigmoid(sum_i gate[i] * h[t, i])
+ * (Qwen3_5MoeSparseMoeBlock.forward shared-expert gate), with h [tokens, hidden].
+ * n_experts <= 1024, k <= 32. */
+int vq2_router_topk(const void* logits, int l_dt, int64_t tokens, int64_t n_experts, int k,
+                    const void* h, int h_dt, int64_t hidden, const void* gate, int g_dt, int64_t shared_id,
+                    int32_t* ids, float* w, void* stream);
+
+/* First-maximum index per row (torch.argmax semantics for NaN-free rows):
+ *   out_idx[r] = argmax_c v[r, c]   (int64), out_val[r] = v[r, out_idx[r]] (fp32, may be NULL)
+ * Replaces torch.argmax over logits (legion/engine.py:288, vq2/generate.py:65). */
+int vq2_argmax_rows(const void* v, int v_dt, int64_t rows, int64_t cols,
+                    int64_t* out_idx, float* out_val, void* stream);
+
+/* LM head + top-1: logits = VQ GEMV (as vq2_gemv, written in fp32 to
+ * `logits_ws` [batch, out_rows]) followed by vq2_argmax_rows.
+ * Replaces PackedLMHead.forward (vq2/runtime.py:136-144) + torch.argmax. */
+int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                    const int16_t* idx0, const void* idx1, int s2_kind,
+                    const void* cb0, const void* cb1, int cb_dt,
+                    const void* scale, int s_dt,
+                    int64_t out_rows, int64_t n, float rs,
+                    float* logits_ws, int64_t* out_idx, float* out_val, void* stream);
+
+/* Rotated-space dequantisation of rows [r0, r1) (debug / audit):
+ *   W[r, 8g+j] = (f32(cb0[i0]) [+ f32(cb1[i1])]) * f32(scale[r]), fp32 [r1-r0, n]
+ * rounded exactly in that order (no contraction).
+ * Replaces QMat.dequant before rot.inv (vq2/vq.py:283-292) and
+ * PackedLinear.weight_rows in fp32 (vq2/runtime.py:82-89). */
+int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind,
+                     const void* cb0, const void* cb1, int cb_dt,
+                     const void* scale, int s_dt,
+                     int64_t r0, int64_t r1, int64_t n, float* out, void* stream);
+
+/* Index decode: out[i] = (int32)in[i] & 0xFFFF (int16 planes) or the byte
+ * value (uint8 planes, is_u8 != 0).  Replaces _as_index (vq2/runtime.py:32-35). */
+int vq2_decode_idx(const void* in, int is_u8, int64_t count, int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VQ2_AMD_H */

@@ -1,0 +1,99 @@
+"""The C ABI library loads and exports every symbol include/vq2_amd.h
+declares; argument validation returns error codes (no GPU work is issued:
+every call here is rejected on the host before any HIP call)."""
+import ctypes
+import subprocess
+
+import pytest
+import torch
+
+from compressai_amd import _lib
+
+
+def test_header_and_binding_agree():
+    declared = _lib.header_symbols()
+    assert len(declared) >= 12
+    assert sorted(declared) == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    for name in _lib.header_symbols():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for name in _lib.header_symbols():
+        assert name in exported, name
+    assert L.vq2_version() >= 100
+
+
+def _err(code):
+    assert code != _lib.OK
+    return _lib.load().vq2_last_error().decode()
+
+
+def test_gemv_rejects_bad_arguments_on_host():
+    L = _lib.load()
+    # n not a multiple of 8
+    msg = _err(L.vq2_gemv(1, 0, 1, 12, 1, None, 0, 16, None, 1, 1, 1, 1, 0, 4, 4, 12, 1.0, None))
+    assert "multiple of 8" in msg
+    # NULL activation
+    msg = _err(L.vq2_gemv(None, 0, 1, 16, 1, None, 0, 16, None, 1, 1, 1, 1, 0, 4, 4, 16, 1.0, None))
+    assert "NULL" in msg
+    # misaligned codebook
+    msg = _err(L.vq2_gemv(8, 0, 1, 16, 8, None, 0, 24, None, 1, 8, 1, 8, 0, 4, 4, 16, 1.0, None))
+    assert "aligned" in msg
+    # idx1 given for a 2 bpw matrix
+    msg = _err(L.vq2_gemv(16, 0, 1, 16, 16, 16, 0, 32, None, 1, 16, 1, 16, 0, 4, 4, 16, 1.0, None))
+    assert "idx1" in msg
+    # bad dtype code
+    msg = _err(L.vq2_gemv(16, 7, 1, 16, 16, None, 0, 32, None, 1, 16, 1, 16, 0, 4, 4, 16, 1.0, None))
+    assert "dtype" in msg
+    # empty problems are a no-op
+    assert L.vq2_gemv(None, 0, 0, 16, None, None, 0, None, None, 1, None, 1, None, 0, 4, 4, 16, 1.0, None) == 0
+
+
+def test_moe_and_rht_reject_bad_arguments_on_host():
+    L = _lib.load()
+    msg = _err(L.vq2_moe_grouped(16, 0, 0, 1, 16, 5, 8, 16, 4, 32, 1, 16, 1, 16, 0, 1024, 1024, 256, 1.0, None))
+    assert "ids dtype" in msg
+    msg = _err(L.vq2_moe_grouped(16, 0, 0, 0, 16, 0, 8, 16, 4, 32, 1, 16, 1, 16, 0, 1024, 1024, 256, 1.0, None))
+    assert "pairs_per_x" in msg
+    msg = _err(L.vq2_rht(16, 0, 12, 32, 0, 12, None, None, 12, 3, 1, 1.0, 0, None))
+    assert "power of two" in msg
+    msg = _err(L.vq2_rht(16, 0, 2048, 32, 0, 2048, None, None, 2048, 16384, 1, 1.0, 0, None))
+    assert "power of two" in msg
+    msg = _err(L.vq2_rht(16, 0, 6144, 16, 0, 6144, None, None, 6144, 4096, 1, 1.0, 0, None))
+    assert "overlap" in msg
+    msg = _err(L.vq2_router_topk(16, 0, 1, 256, 40, None, 0, 0, None, 0, -1, 16, 16, None))
+    assert "k=40" in msg
+    msg = _err(L.vq2_argmax_rows(16, 0, 1, 0, 16, None, None))
+    assert "bad sizes" in msg
+
+
+def test_python_entry_points_refuse_cpu_tensors():
+    from compressai_amd import kernels as K
+
+    x = torch.zeros(16)
+    with pytest.raises(K.Vq2Error, match="GPU tensors"):
+        K.vq_rht(x, hb=16)
+    with pytest.raises(RuntimeError):
+        K.vq_gemv_16(x, torch.zeros(2, 2, dtype=torch.int16), torch.zeros(65536, 8), torch.ones(2), 2, 16)
+
+
+def test_error_message_is_thread_local():
+    import threading
+
+    L = _lib.load()
+    L.vq2_rht(16, 0, 12, 32, 0, 12, None, None, 12, 3, 1, 1.0, 0, None)
+    seen = {}
+
+    def other():
+        seen["msg"] = L.vq2_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "power of two" in L.vq2_last_error().decode()

@@ -1,0 +1,325 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on
+identical seeded inputs.
+
+Tolerances (the decode-path contract):
+  * index decode and dequantized weights: bit-exact;
+  * fp32 outputs: max_i |y_i - ref_i| / max_i |ref_i| <= 1e-3 against the
+    fp64-accumulation oracle (observed ~1e-6: fp32 accumulation in a
+    different order);
+  * bf16 outputs: within one bf16 ulp (2^-8 relative) of the oracle rounded
+    to bf16 (the reference kernels store bf16);
+  * RHT: <= 1e-5 (fp32 butterflies against fp64).
+"""
+import numpy as np
+import pytest
+import torch
+
+from compressai_amd import kernels as K, synth
+from oracle import vq2_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _cuda(*ts, dev):
+    return [None if t is None else t.to(dev) for t in ts]
+
+
+# --------------------------------------------------------------------- RHT
+@pytest.mark.parametrize("hb,n,batch", [(2, 2, 1), (8, 16, 3), (64, 64, 2), (128, 256, 1), (256, 256, 5),
+                                        (512, 512, 9), (1024, 1024, 1), (2048, 2048, 1), (2048, 6144, 2),
+                                        (4096, 4096, 1), (8192, 8192, 2), (2048, 8192, 4)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_rht_forward_vs_oracle(dev, hb, n, batch, dt):
+    x = synth.activations(11 + n, (batch, n), dtype=dt)
+    perm = synth.permutation(12 + n, n)
+    sign = synth.signs(13 + n, n)
+    y = K.vq_rht(x.to(dev), perm.to(dev), sign.to(dev), hb, out_dtype=torch.float32)
+    ref = O.rht(x, perm, sign, hb)
+    assert O.max_rel_err(y.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("hb,n", [(512, 512), (2048, 6144)])
+def test_rht_inverse_roundtrip(dev, hb, n):
+    x = synth.activations(21, (3, n), dtype=torch.float32).to(dev)
+    perm = synth.permutation(22, n).to(dev)
+    sign = synth.signs(23, n).to(dev)
+    y = K.vq_rht(x, perm, sign, hb)
+    z = K.vq_rht(y, perm, sign, hb, inverse=True)
+    ref = O.rht(y.cpu(), perm.cpu(), sign.cpu(), hb, inverse=True)
+    assert O.max_rel_err(z.cpu().numpy(), ref) < 1e-5
+    assert torch.allclose(z, x, atol=1e-5)
+    # orthogonality: norms preserved
+    assert torch.allclose(y.norm(dim=1), x.norm(dim=1), rtol=1e-5)
+
+
+def test_rht_no_perm_no_sign_and_bf16_in_out(dev):
+    x = synth.activations(31, (2, 2048), dtype=torch.bfloat16)
+    y = K.vq_rht(x.to(dev), None, None, 2048)  # bf16 out, like Rot.fwd on bf16
+    assert y.dtype == torch.bfloat16
+    ref = O.rht(x, None, None, 2048)
+    refb = torch.from_numpy(ref.astype(np.float32)).to(torch.bfloat16).float().numpy()
+    assert np.max(np.abs(y.float().cpu().numpy() - refb)) <= np.max(np.abs(refb)) * 2 ** -8
+
+
+def test_swiglu_rht_vs_oracle(dev):
+    I = 512
+    gu = synth.activations(41, (9, 2 * I), dtype=torch.float32)
+    perm = synth.permutation(42, I)
+    sign = synth.signs(43, I)
+    y = K.vq_swiglu_rht(gu.to(dev), I, perm.to(dev), sign.to(dev), 512)
+    g = gu.double().numpy()
+    act = g[:, :I] / (1 + np.exp(-g[:, :I])) * g[:, I:]
+    ref = O.np_rht64(act, perm, sign, 512)
+    assert O.max_rel_err(y.cpu().numpy(), ref) < 1e-5
+
+
+# ---------------------------------------------------- dequant / decode exact
+def test_decode_idx_exhaustive(dev):
+    pat = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    got = K.vq_decode_idx(pat.to(dev)).cpu().numpy()
+    assert np.array_equal(got, O.decode_idx16(pat.numpy()))
+    u8 = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    assert K.vq_decode_idx(u8.to(dev)).cpu().tolist() == list(range(256))
+
+
+@pytest.mark.parametrize("bpw", [2, 3, 4])
+@pytest.mark.parametrize("cbdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_dequant_bitexact(dev, bpw, cbdt):
+    cb0 = synth.codebook(51, dtype=cbdt)
+    cb1 = synth.codebook(52, 256 if bpw == 3 else 65536, dtype=cbdt) if bpw > 2 else None
+    m = synth.vq_matrix(5000, 96, 512, bpw=bpw)
+    got = K.vq_dequant_rows(*_cuda(m["idx0"], m["idx1"], cb0, cb1, m["scale"], dev=dev), 5, 77).cpu().numpy()
+    ref = O.dequant_rows(m["idx0"], m["idx1"], cb0, cb1, m["scale"], 5, 77)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# -------------------------------------------------------------------- GEMV
+GEMV_CASES = [
+    # (out, n, bpw, batch)
+    (2048, 2048, 2, 1),    # config 1
+    (512, 2048, 2, 1),     # config 2 k/v
+    (6144, 2048, 4, 1),    # config 2 gate/up
+    (2048, 6144, 4, 1),    # config 2 down (split-K over 3 waves)
+    (2048, 2048, 3, 1),    # (16, 8) 3 bpw
+    (1000, 2048, 2, 1),    # OUT not a multiple of any tile
+    (7, 512, 2, 3),        # tiny, batch 3
+    (333, 200, 2, 2),      # n/8 = 25: scalar (unaligned) index path
+    (64, 8, 4, 1),         # n = 8: one group per row
+    (1024, 2048, 2, 4),
+    (257, 1024, 4, 5),     # batch tile 8 with 5 columns
+    (512, 6144, 3, 8),
+    (300, 4096, 2, 16),    # two batch tiles
+    (96, 64 * 1024, 2, 1), # 32 K-chunks: waves loop over chunks
+]
+
+
+@pytest.mark.parametrize("out,n,bpw,batch", GEMV_CASES)
+def test_gemv_fp32_vs_oracle(dev, out, n, bpw, batch):
+    seed = 6000 + out + n + bpw
+    cb0 = synth.codebook(seed)
+    cb1 = synth.codebook(seed + 1, 256 if bpw == 3 else 65536) if bpw > 2 else None
+    m = synth.vq_matrix(seed, out, n, bpw=bpw)
+    x = synth.activations(seed + 4, (batch, n), dtype=torch.float32)
+    y = K.vq_gemv(*_cuda(x, m["idx0"], m["idx1"], cb0, cb1, m["scale"], dev=dev), out, n, 0.5,
+                  out_dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, m["scale"], rs=0.5)
+    assert y.shape == (batch, out)
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
+@pytest.mark.parametrize("cbdt,xdt,sdt", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.float16, torch.float32),
+                                          (torch.float16, torch.bfloat16, torch.float16)])
+@pytest.mark.parametrize("bpw", [2, 3, 4])
+def test_gemv_dtypes(dev, cbdt, xdt, sdt, bpw):
+    cb0 = synth.codebook(71, dtype=cbdt)
+    cb1 = synth.codebook(72, 256 if bpw == 3 else 65536, dtype=cbdt) if bpw > 2 else None
+    m = synth.vq_matrix(7000, 384, 1024, bpw=bpw)
+    sc = m["scale"].to(sdt)
+    x = synth.activations(74, 1024, dtype=xdt)
+    y = K.vq_gemv(*_cuda(x, m["idx0"], m["idx1"], cb0, cb1, sc, dev=dev), 384, 1024, 1.0, out_dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, sc)
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+
+
+def test_gemv_drop_in_bf16_output(dev):
+    """vq_gemv_16 / vq_gemv_16_8 keep the reference's bf16 output."""
+    cb0 = synth.codebook(81, dtype=torch.bfloat16)
+    cb1 = synth.codebook(82, 256, dtype=torch.bfloat16)
+    m = synth.vq_matrix(8000, 2048, 2048, bpw=3)
+    sc = m["scale"].to(torch.bfloat16)
+    x = synth.activations(84, 2048, dtype=torch.bfloat16)
+    xd, i0, i1, c0, c1, s = _cuda(x, m["idx0"], m["idx1"], cb0, cb1, sc, dev=dev)
+    for y, (_, y64) in ((K.vq_gemv_16(xd, i0, c0, s, 2048, 2048, 2048 ** -0.5),
+                         O.vq_gemv(x, m["idx0"], None, cb0, None, sc, rs=2048 ** -0.5)),
+                        (K.vq_gemv_16_8(xd, i0, i1, c0, c1, s, 2048, 2048, 2048 ** -0.5),
+                         O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, sc, rs=2048 ** -0.5))):
+        assert y.dtype == torch.bfloat16 and y.shape == (2048,)
+        ref = torch.from_numpy(y64[0].astype(np.float32)).to(torch.bfloat16).float().numpy()
+        diff = np.abs(y.float().cpu().numpy() - ref)
+        # at most one bf16 ulp of the value
+        assert np.all(diff <= np.abs(ref) * 2 ** -7 + 1e-30)
+
+
+def test_gemv_linearity_full_size(dev):
+    """Size-independent property at the LM-head shape: y(2a - 3b) = 2y(a) - 3y(b)."""
+    out, n = 151936, 2048
+    cb = synth.codebook(91).to(dev)
+    m = synth.vq_matrix(9000, out, n, bpw=2)
+    i0, s = m["idx0"].to(dev), m["scale"].to(dev)
+    a = synth.activations(94, n, dtype=torch.float32).to(dev)
+    b = synth.activations(95, n, dtype=torch.float32).to(dev)
+    f = lambda v: K.vq_gemv_16(v, i0, cb, s, out, n, out_dtype=torch.float32).double()
+    lhs, rhs = f(2 * a - 3 * b), 2 * f(a) - 3 * f(b)
+    assert ((lhs - rhs).abs().max() / rhs.abs().max()).item() < 1e-5
+
+
+# ------------------------------------------------------------ LM head top-1
+@pytest.mark.parametrize("batch", [1, 4])
+def test_lm_head_argmax_full_size(dev, batch):
+    """Config 3: 151936 x 2048 at 2 bpw, batch 1 and 4, fused top-1."""
+    out, n = 151936, 2048
+    cb = synth.codebook(3000)
+    m = synth.vq_matrix(3000, out, n, bpw=2)
+    x = synth.activations(3004, (batch, n), dtype=torch.float32)
+    idx, val = K.vq_gemv_argmax(*_cuda(x, m["idx0"], None, cb, None, m["scale"], dev=dev), out, n)
+    _, y64 = O.vq_gemv(x, m["idx0"], None, cb, None, m["scale"])
+    ref = O.argmax_rows(y64)
+    assert idx.cpu().tolist() == ref.tolist()
+    assert np.allclose(val.cpu().numpy(), y64[np.arange(batch), ref], rtol=1e-4)
+
+
+def test_argmax_ties_pick_first(dev):
+    v = torch.zeros(3, 50000)
+    v[0, 17] = 5.0
+    v[0, 40000] = 5.0
+    v[1, :] = -1.0
+    v[2, 49999] = 1.0
+    v[2, 8192] = 1.0  # tie across argmax chunks
+    idx, val = K.vq_argmax(v.to(dev))
+    assert idx.cpu().tolist() == [17, 0, 8192]
+    assert val.cpu().tolist() == [5.0, -1.0, 1.0]
+
+
+# -------------------------------------------------------------- grouped MoE
+def _pools(seed, E, dev=None):
+    gu = synth.indices16(seed + 2, (E, 1024, 256))
+    gus = synth.scales(seed + 3, (E, 1024))
+    dn = synth.indices16(seed + 12, (E, 2048, 64))
+    dns = synth.scales(seed + 13, (E, 2048))
+    return gu, gus, dn, dns
+
+
+@pytest.mark.parametrize("ids_dtype", [torch.int32, torch.int64])
+def test_moe_parallel_gate_up_and_down_drop_in(dev, ids_dtype):
+    """The reference call shapes: y_out written in place, bf16 pools/scales."""
+    E = 12
+    cb = synth.codebook(4000, dtype=torch.bfloat16)
+    gu, gus, dn, dns = _pools(4000, E)
+    gus, dns = gus.to(torch.bfloat16), dns.to(torch.bfloat16)
+    ids = torch.tensor([3, 11, 0, 3, 7, 5, 9, 1], dtype=ids_dtype)
+    xr = synth.activations(4004, 2048, dtype=torch.bfloat16)
+    y_gu = torch.zeros(8, 1024, dtype=torch.float32, device=dev)
+    K.vq_moe_parallel_gate_up(*_cuda(xr, ids, gu, cb, gus, dev=dev), y_gu, OUT=1024, NG=256, rs=0.7)
+    _, ref = O.moe_grouped(xr, ids.numpy(), gu.numpy(), cb, gus, 1024, 256, rs=0.7)
+    assert O.max_rel_err(y_gu.cpu().numpy(), ref) < TOL
+    assert torch.equal(y_gu[0], y_gu[3])  # same expert, same row values
+
+    act = synth.activations(4005, (8, 512), dtype=torch.bfloat16)
+    y_dn = torch.empty(8, 2048, dtype=torch.bfloat16, device=dev)
+    K.vq_moe_parallel_down(*_cuda(act, ids, dn, cb, dns, dev=dev), y_dn, OUT=2048, NG=64)
+    _, ref = O.moe_grouped(act, ids.numpy(), dn.numpy(), cb, dns, 2048, 64, per_pair_x=True)
+    refb = torch.from_numpy(ref.astype(np.float32)).to(torch.bfloat16).float().numpy()
+    diff = np.abs(y_dn.float().cpu().numpy() - refb)
+    assert np.all(diff <= np.abs(refb) * 2 ** -7 + 1e-30)
+
+
+def test_moe_bad_expert_id_gives_nan_rows(dev):
+    E = 4
+    cb = synth.codebook(4100)
+    gu, gus, _, _ = _pools(4100, E)
+    ids = torch.tensor([1, E, -1, 2], dtype=torch.int32)
+    xr = synth.activations(4104, 2048, dtype=torch.float32)
+    y = torch.zeros(4, 1024, device=dev)
+    K.vq_moe_parallel_gate_up(*_cuda(xr, ids, gu, cb, gus, dev=dev), y)
+    yc = y.cpu()
+    assert torch.isnan(yc[1]).all() and torch.isnan(yc[2]).all()
+    assert not torch.isnan(yc[0]).any() and not torch.isnan(yc[3]).any()
+
+
+def test_moe_down_combine_vs_oracle(dev):
+    E, T, P = 10, 3, 5
+    cb = synth.codebook(4200)
+    _, _, dn, dns = _pools(4200, E)
+    ids = torch.randint(0, E, (T, P), generator=synth.gen(4201), dtype=torch.int32)
+    w = torch.rand(T, P, generator=synth.gen(4202))
+    act = synth.activations(4203, (T * P, 512), dtype=torch.float32)
+    out = K.vq_moe_down_combine(*_cuda(act, ids, w, dn, cb, dns, dev=dev), OUT=2048, NG=64)
+    _, y = O.moe_grouped(act, ids.reshape(-1).numpy(), dn.numpy(), cb, dns, 2048, 64, per_pair_x=True)
+    ref = (y.reshape(T, P, 2048) * w.double().numpy()[:, :, None]).sum(1)
+    assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
+
+
+def test_router_topk_vs_oracle(dev):
+    T, E, k = 8, 256, 8
+    logits = synth.activations(4307, (T, E))
+    h = synth.activations(4304, (T, 2048))
+    gate = synth.activations(4308, 2048) * 0.02
+    ids, w = K.vq_router_topk(*_cuda(logits, dev=dev), k, h.to(dev), gate.to(dev), shared_id=E)
+    rid, rw = O.router_topk(logits, k)
+    assert ids[:, :k].cpu().numpy().tolist() == rid.tolist()
+    assert np.allclose(w[:, :k].cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    assert (ids[:, k] == E).all()
+    sg = 1 / (1 + np.exp(-(h.double().numpy() @ gate.double().numpy())))
+    assert np.allclose(w[:, k].cpu().numpy(), sg, rtol=1e-5)
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_moe_layer_config4_vs_oracle(dev, T):
+    """Config 4: 256 routed + 1 shared expert resident in one pool, top-8,
+    T = 1 and 8, router + RHTs + grouped GEMVs + combine on device."""
+    from compressai_amd.moe import MoELayer
+
+    E, k = 256, 8
+    cb = synth.codebook(4000)
+    gu, gus, dn, dns = _pools(4000, E + 1)
+    h = synth.activations(4004, (T, 2048))
+    logits = synth.activations(4007, (T, E))
+    gate = synth.activations(4008, 2048) * 0.02
+    layer = MoELayer(*_cuda(gu, gus, dn, dns, cb, gate, dev=dev), top_k=k)
+    out = layer(h.to(dev), logits.to(dev))
+    rh, ri = layer.experts_mod.rot_h, layer.experts_mod.rot_i
+    ref = O.moe_layer(h, logits, cb, gu, gus, dn, dns, gu[E], gus[E], dn[E], dns[E], gate,
+                      rh.perm.cpu().numpy(), rh.sign.float().cpu().numpy(), ri.perm.cpu().numpy(),
+                      ri.sign.float().cpu().numpy(), top_k=k)
+    assert out.shape == (T, 2048)
+    assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
+
+
+def test_resident_experts_drop_in_forward(dev):
+    """PackedMoEExpertUniversal.forward(hidden, topk_idx, topk_weights) shape."""
+    from compressai_amd.moe import ResidentMoEExperts
+
+    E = 16
+    cb = synth.codebook(4400)
+    gu, gus, dn, dns = _pools(4400, E)
+    mod = ResidentMoEExperts(*_cuda(gu, gus, dn, dns, cb, dev=dev))
+    h = synth.activations(4404, (2, 2048), dtype=torch.bfloat16)
+    ids = torch.tensor([[1, 4, 9, 15, 0, 2, 3, 8], [15, 14, 1, 0, 5, 6, 7, 4]], dtype=torch.int64)
+    w = torch.softmax(synth.activations(4405, (2, 8)).float(), -1).to(torch.bfloat16)
+    out = mod(h.to(dev), ids.to(dev), w.to(dev))
+    assert out.shape == (2, 2048) and out.dtype == torch.bfloat16
+    rh, ri = mod.rot_h, mod.rot_i
+    ref = np.zeros((2, 2048))
+    for t in range(2):
+        xr = O.np_rht64(h[t], rh.perm.cpu().numpy(), rh.sign.float().cpu().numpy(), 2048)[0]
+        for j in range(8):
+            e = int(ids[t, j])
+            Wgu = O.np_dequant64(gu[e], None, cb, None, gus[e])
+            g = Wgu @ xr
+            act = O.silu(g[:512]) * g[512:]
+            ar = O.np_rht64(act, ri.perm.cpu().numpy(), ri.sign.float().cpu().numpy(), 512)[0]
+            ref[t] += float(w[t, j]) * (O.np_dequant64(dn[e], None, cb, None, dns[e]) @ ar)
+    assert O.max_rel_err(out.float().cpu().numpy(), ref) < 8e-3  # bf16 output rounding

@@ -1,0 +1,298 @@
+"""Pins of the CPU oracle (oracle/vq2_oracle.c + the numpy cross-path).
+
+Each check is independent of the oracle's own formula: numpy/torch dtype
+conversions, exhaustive index decode against numpy's uint16 view, hand-built
+known-answer packs for unpack_fixed, scipy.linalg.hadamard, one-hot
+codebooks, linearity and fp64 dense matmul.  A plausible mistake (a dropped
+stage-2 term, a wrong index mask, a transposed Hadamard, a wrong sign or
+permutation direction) fails at least one of them.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import vq2_oracle as O
+
+
+# ------------------------------------------------------------ conversions
+def test_f16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = O.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_bf16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = O.bf16_to_f32(bits)
+    ref = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def _f32_samples():
+    rng = np.random.default_rng(7)
+    r = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    edge = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 6.1035156e-05, 5.9604645e-08,
+                     2.9802322e-08, 2.9802326e-08, 1e-45, 3.4028235e38, np.inf, -np.inf,
+                     1.0009765625, 1.00048828125, 1.000732421875, 1.0 + 2**-8, 1.0 + 3 * 2**-9],
+                    dtype=np.float32)
+    return np.concatenate([r, edge])
+
+
+def test_f32_to_bf16_matches_torch():
+    x = _f32_samples()
+    x = x[~np.isnan(x)]
+    got = O.f32_to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_f32_to_f16_matches_numpy():
+    x = _f32_samples()
+    x = x[~np.isnan(x)]
+    got = O.f32_to_f16(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ decode
+def test_decode_idx16_exhaustive():
+    pat = np.arange(-32768, 32768, dtype=np.int32).astype(np.int16)
+    got = O.decode_idx16(pat)
+    ref = pat.view(np.uint16).astype(np.int32)
+    assert np.array_equal(got, ref)
+    assert got.min() == 0 and got.max() == 65535
+
+
+def test_unpack_fixed_known_answers():
+    # 4-bit: low nibble first (vq2/export.py:62-64)
+    assert O.unpack_fixed(np.array([0x21, 0x43, 0x05], np.uint8), 4, 5).tolist() == [1, 2, 3, 4, 5]
+    # 12-bit: 3 bytes -> two symbols a | b << 12, little endian (vq2/export.py:65-69)
+    # a = 0xABC, b = 0x123 -> w = 0x123ABC -> bytes BC 3A 12
+    assert O.unpack_fixed(np.array([0xBC, 0x3A, 0x12], np.uint8), 12, 2).tolist() == [0xABC, 0x123]
+    assert O.unpack_fixed(np.array([0xBC, 0x3A, 0x12, 0xFF, 0x0F, 0x00], np.uint8), 12, 3).tolist() == [
+        0xABC, 0x123, 0xFFF]
+    # 16-bit little endian, 8-bit identity
+    assert O.unpack_fixed(np.array([0x34, 0x12, 0xFF, 0xFF], np.uint8), 16, 2).tolist() == [0x1234, 0xFFFF]
+    assert O.unpack_fixed(np.array([0, 7, 255], np.uint8), 8, 3).tolist() == [0, 7, 255]
+    with pytest.raises(ValueError):
+        O.unpack_fixed(np.zeros(4, np.uint8), 10, 2)
+
+
+# ----------------------------------------------------------------- dequant
+def _small_matrix(seed, out_rows=12, ng=6, s2=None, cb_dtype=np.float16):
+    rng = np.random.default_rng(seed)
+    cb0 = (rng.standard_normal((65536, 8)) * 0.35).astype(cb_dtype)
+    idx0 = rng.integers(-32768, 32768, size=(out_rows, ng)).astype(np.int16)
+    idx1, cb1 = None, None
+    if s2 == "u8":
+        idx1 = rng.integers(0, 256, size=(out_rows, ng)).astype(np.uint8)
+        cb1 = (rng.standard_normal((256, 8)) * 0.1).astype(cb_dtype)
+    elif s2 == "u16":
+        idx1 = rng.integers(-32768, 32768, size=(out_rows, ng)).astype(np.int16)
+        cb1 = (rng.standard_normal((65536, 8)) * 0.1).astype(cb_dtype)
+    scale = (rng.random(out_rows) + 0.5).astype(np.float16)
+    return idx0, idx1, cb0, cb1, scale
+
+
+@pytest.mark.parametrize("s2", [None, "u8", "u16"])
+def test_dequant_bitexact_vs_numpy_f32(s2):
+    idx0, idx1, cb0, cb1, scale = _small_matrix(1, s2=s2)
+    got = O.dequant_rows(idx0, idx1, cb0, cb1, scale)
+    w = cb0.astype(np.float32)[idx0.view(np.uint16).astype(np.int64)]
+    if idx1 is not None:
+        i1 = idx1.astype(np.int64) if idx1.dtype == np.uint8 else idx1.view(np.uint16).astype(np.int64)
+        w = w + cb1.astype(np.float32)[i1]
+    ref = (w.reshape(idx0.shape[0], -1) * scale.astype(np.float32)[:, None]).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_one_hot_codebook():
+    # cb0[c] = c * e_(c % 8): dequant reveals the decoded code and lane
+    cb0 = np.zeros((65536, 8), np.float32)
+    c = np.arange(65536)
+    cb0[c, c % 8] = c.astype(np.float32)
+    idx0 = np.array([[0, 1, -1, -32768], [32767, 12345, -2, 7]], np.int16)
+    scale = np.ones(2, np.float32)
+    got = O.dequant_rows(idx0, None, cb0, None, scale).reshape(2, 4, 8)
+    codes = idx0.view(np.uint16).astype(np.int64)
+    for r in range(2):
+        for g in range(4):
+            v = got[r, g]
+            assert v.sum() == codes[r, g] and (codes[r, g] == 0 or v[codes[r, g] % 8] == codes[r, g])
+
+
+def test_dequant_rows_subrange():
+    idx0, _, cb0, _, scale = _small_matrix(2)
+    full = O.dequant_rows(idx0, None, cb0, None, scale)
+    part = O.dequant_rows(idx0, None, cb0, None, scale, 3, 9)
+    assert np.array_equal(full[3:9], part)
+
+
+# -------------------------------------------------------------------- GEMV
+@pytest.mark.parametrize("s2", [None, "u8", "u16"])
+def test_gemv_vs_dense_fp64(s2):
+    idx0, idx1, cb0, cb1, scale = _small_matrix(3, out_rows=20, ng=16, s2=s2)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 128)).astype(np.float16)
+    y32, y64 = O.vq_gemv(x, idx0, idx1, cb0, cb1, scale, rs=0.125)
+    W = O.np_dequant64(idx0, idx1, cb0, cb1, scale)
+    ref = (x.astype(np.float64) @ W.T) * 0.125
+    assert np.allclose(y64, ref, rtol=1e-12, atol=1e-12)
+    assert O.max_rel_err(y32, ref) < 1e-5
+
+
+def test_gemv_one_hot_brute_force():
+    # cb0[c] = e_(c % 8): y[r] = s[r] * sum_g x[8g + (code % 8)]
+    cb0 = np.zeros((65536, 8), np.float32)
+    c = np.arange(65536)
+    cb0[c, c % 8] = 1.0
+    rng = np.random.default_rng(5)
+    idx0 = rng.integers(-32768, 32768, size=(7, 9)).astype(np.int16)
+    scale = (rng.random(7) + 0.5).astype(np.float32)
+    x = rng.standard_normal(72).astype(np.float32)
+    _, y64 = O.vq_gemv(x, idx0, None, cb0, None, scale)
+    codes = idx0.view(np.uint16).astype(np.int64)
+    for r in range(7):
+        expect = sum(float(x[8 * g + codes[r, g] % 8]) for g in range(9)) * float(scale[r])
+        assert abs(y64[0, r] - expect) < 1e-9
+
+
+def test_gemv_linearity():
+    idx0, _, cb0, _, scale = _small_matrix(6, out_rows=10, ng=8)
+    rng = np.random.default_rng(6)
+    a, b = rng.standard_normal(64), rng.standard_normal(64)
+    _, ya = O.vq_gemv(a.astype(np.float32), idx0, None, cb0, None, scale)
+    _, yb = O.vq_gemv(b.astype(np.float32), idx0, None, cb0, None, scale)
+    _, yab = O.vq_gemv((2 * a.astype(np.float32) - 3 * b.astype(np.float32)).astype(np.float32), idx0, None,
+                       cb0, None, scale)
+    assert np.allclose(yab, 2 * ya - 3 * yb, rtol=1e-6, atol=1e-6)
+
+
+def test_moe_grouped_equals_per_expert_dense():
+    rng = np.random.default_rng(8)
+    E, OUT, NG = 5, 16, 8
+    pool = rng.integers(-32768, 32768, size=(E, OUT, NG)).astype(np.int16)
+    pscale = (rng.random((E, OUT)) + 0.5).astype(np.float16)
+    cb = (rng.standard_normal((65536, 8)) * 0.35).astype(np.float16)
+    ids = np.array([3, 0, 3, 4], np.int64)
+    x_shared = rng.standard_normal(NG * 8).astype(np.float16)
+    _, y = O.moe_grouped(x_shared, ids, pool, cb, pscale, OUT, NG, rs=0.5)
+    for k, e in enumerate(ids):
+        _, ref = O.vq_gemv(x_shared, pool[e], None, cb, None, pscale[e], rs=0.5)
+        assert np.array_equal(y[k], ref[0])
+    xp = rng.standard_normal((4, NG * 8)).astype(np.float32)
+    _, y2 = O.moe_grouped(xp, ids.astype(np.int32), pool, cb, pscale, OUT, NG, per_pair_x=True)
+    for k, e in enumerate(ids):
+        _, ref = O.vq_gemv(xp[k], pool[e], None, cb, None, pscale[e])
+        assert np.array_equal(y2[k], ref[0])
+    # duplicated experts give identical rows; an out-of-range id gives NaN
+    assert np.array_equal(y[0], y[2])
+    _, ybad = O.moe_grouped(x_shared, np.array([1, E], np.int32), pool, cb, pscale, OUT, NG)
+    assert np.all(np.isnan(ybad[1])) and not np.any(np.isnan(ybad[0]))
+
+
+# --------------------------------------------------------------------- RHT
+@pytest.mark.parametrize("hb,n", [(8, 8), (64, 128), (512, 512), (2048, 2048), (2048, 6144)])
+def test_rht_vs_scipy_hadamard(hb, n):
+    from scipy.linalg import hadamard
+
+    rng = np.random.default_rng(hb + n)
+    x = rng.standard_normal((2, n))
+    perm = rng.permutation(n).astype(np.int32)
+    sign = rng.choice([-1, 1], size=n).astype(np.int8)
+    got = O.rht(x.astype(np.float32), perm, sign, hb)
+    v = x.astype(np.float32).astype(np.float64)[:, perm] * sign
+    H = hadamard(hb).astype(np.float64)
+    ref = np.concatenate([v[:, o:o + hb] @ H.T for o in range(0, n, hb)], axis=1) * hb ** -0.5
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_rht_closed_form_entries():
+    # H[i, j] = (-1)^popcount(i & j): transform of the unit vector e_j
+    hb = 256
+    for j in (0, 1, 37, 255):
+        e = np.zeros(hb, np.float32)
+        e[j] = 1.0
+        y = O.rht(e, None, None, hb, scale=1.0)
+        expect = np.array([(-1.0) ** bin(i & j).count("1") for i in range(hb)])
+        assert np.array_equal(y, expect)
+
+
+def test_rht_inverse_roundtrip_and_norm():
+    rng = np.random.default_rng(11)
+    n, hb = 6144, 2048
+    x = rng.standard_normal((3, n)).astype(np.float32)
+    perm = rng.permutation(n).astype(np.int32)
+    sign = rng.choice([-1, 1], size=n).astype(np.int8)
+    y = O.rht(x, perm, sign, hb)
+    assert np.allclose(np.linalg.norm(y, axis=1), np.linalg.norm(x.astype(np.float64), axis=1), rtol=1e-12)
+    z = O.rht(y.astype(np.float32), perm, sign, hb, inverse=True)
+    assert np.allclose(z, x, atol=1e-5)
+    # numpy cross-path agrees
+    assert np.allclose(O.np_rht64(x, perm, sign, hb), y, rtol=1e-12, atol=1e-12)
+
+
+def test_rot_tables_reference_construction():
+    # tag_seed = int(md5(tag)[:8], 16) (vq2/vq.py:40-41); digests fixed by md5
+    from compressai_amd.rot import rot_tables, tag_seed, block_size
+
+    assert hashlib.md5(b"moe_expert_2048").hexdigest()[:8] == format(tag_seed("moe_expert_2048"), "08x")
+    assert tag_seed("moe_expert_2048") == 0x24D58BA3  # md5sum CLI: 24d58ba3...
+    assert tag_seed("moe_expert_512") == 0xFD2DFEB8  # md5sum CLI: fd2dfeb8...
+    perm, sign = rot_tables(512, tag_seed("moe_expert_512"))
+    assert sorted(perm.tolist()) == list(range(512))
+    assert set(sign.tolist()) <= {-1.0, 1.0}
+    assert block_size(512) == 512 and block_size(2048) == 2048 and block_size(6144) == 2048
+    assert block_size(8192) == 2048
+
+
+# -------------------------------------------------------------------- MoE
+def test_router_identity_softmax_over_topk():
+    rng = np.random.default_rng(12)
+    logits = rng.standard_normal((4, 256)).astype(np.float16)
+    ids, w = O.router_topk(logits, 8)
+    lf = logits.astype(np.float64)
+    p = np.exp(lf - lf.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    for t in range(4):
+        top = np.argsort(-p[t], kind="stable")[:8]
+        assert ids[t].tolist() == top.tolist()
+        assert np.allclose(w[t], p[t, top] / p[t, top].sum(), rtol=1e-12)
+
+
+def test_moe_layer_oracle_vs_c_composition():
+    from compressai_amd import synth
+
+    E, k, H, I = 6, 2, 64, 32
+    cb = synth.codebook(77)
+    gu = synth.indices16(71, (E + 1, 2 * I, H // 8)).numpy()
+    gus = synth.scales(72, (E + 1, 2 * I)).numpy()
+    dn = synth.indices16(73, (E + 1, H, I // 8)).numpy()
+    dns = synth.scales(74, (E + 1, H)).numpy()
+    h = synth.activations(75, (2, H)).numpy()
+    logits = synth.activations(76, (2, E)).numpy()
+    gate = (synth.activations(78, H) * 0.05).numpy()
+    ref = O.moe_layer(h, logits, cb, gu[:E], gus[:E], dn[:E], dns[:E], gu[E], gus[E], dn[E], dns[E], gate,
+                      top_k=k)
+    # same layer composed from the C oracle's grouped GEMV and RHT
+    ids, w = O.router_topk(logits, k)
+    out = np.zeros((2, H))
+    for t in range(2):
+        xr = O.rht(h[t], None, None, H)
+        sg = 1.0 / (1.0 + np.exp(-(gate.astype(np.float64) @ h[t].astype(np.float64))))
+        pids = list(ids[t]) + [E]
+        pw = list(w[t]) + [sg]
+        _, g = O.moe_grouped(xr.astype(np.float32), np.array(pids), gu, cb, gus, 2 * I, H // 8)
+        act = g[:, :I] / (1 + np.exp(-g[:, :I])) * g[:, I:]
+        ar = O.rht(act.astype(np.float32), None, None, I)
+        _, d = O.moe_grouped(ar.astype(np.float32), np.array(pids), dn, cb, dns, H, I // 8, per_pair_x=True)
+        out[t] = sum(pw[j] * d[j] for j in range(k + 1))
+    assert O.max_rel_err(out, ref) < 1e-5
