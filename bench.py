@@ -4,7 +4,8 @@
 Headline: one decoder layer's projection set at
 batch 1, hidden 2048 -- RHT(2048) -> q, k, v (2 bpw); RHT(2048) -> o (2 bpw);
 RHT(2048) -> gate, up (4 bpw, two 16-bit stages); RHT(6144, 3 x 2048 blocks)
--> down (4 bpw).  One step = one layer; the timed loop cycles through L
+-> down (4 bpw), as four launches that each rotate their activation in LDS.
+One step = one layer; the timed loop cycles through L
 distinct layer weight sets (>= 1 GiB in total) so the 256 MB Infinity Cache
 cannot hold the weights, and replays the launches as HIP graphs.
 ``value`` = compressed weight bytes (index planes + row scales) per step /
@@ -104,20 +105,23 @@ class DenseLayers:
         i0, i1, s, out, n = lay[name]
         K.vq_gemv(xr, i0, i1, self.cb0, self.cb1 if i1 is not None else None, s, out, n, 1.0, y=self.y[name])
 
-    def step(self, l):
+    def fused(self, lay, names, x, sign):
+        """One launch: RHT of x built in LDS + the GEMVs of `names`."""
         from compressai_amd import kernels as K
 
+        mats = [(lay[nm][0], lay[nm][1], lay[nm][2], lay[nm][3]) for nm in names]
+        n = lay[names[0]][4]
+        K.vq_gemv_rht(x, mats, self.cb0, self.cb1 if mats[0][1] is not None else None, n, None, sign, 2048,
+                      ys=[self.y[nm] for nm in names])
+
+    def step(self, l):
+        """One decoder layer's projections: 4 launches (q/k/v, o, gate/up,
+        down), each rotating its activation in LDS."""
         lay = self.layers[l]
-        K.vq_rht(self.x_attn, None, self.sign_h, 2048, out=self.xr_a)
-        for name in ("q", "k", "v"):
-            self.gemv(lay, name, self.xr_a)
-        K.vq_rht(self.x_o, None, self.sign_h, 2048, out=self.xr_o)
-        self.gemv(lay, "o", self.xr_o)
-        K.vq_rht(self.x_mlp, None, self.sign_h, 2048, out=self.xr_m)
-        self.gemv(lay, "gate", self.xr_m)
-        self.gemv(lay, "up", self.xr_m)
-        K.vq_rht(self.x_down, None, self.sign_i, 2048, out=self.xr_d)
-        self.gemv(lay, "down", self.xr_d)
+        self.fused(lay, ("q", "k", "v"), self.x_attn, self.sign_h)
+        self.fused(lay, ("o",), self.x_o, self.sign_h)
+        self.fused(lay, ("gate", "up"), self.x_mlp, self.sign_h)
+        self.fused(lay, ("down",), self.x_down, self.sign_i)
 
 
 def capture(fn, n_items, dev):
@@ -172,15 +176,16 @@ def bench_dense(args, dev):
     log(f"dense: {steps} steps in {ms:.3f} ms (host {host_ms:.3f} ms) -> {ms_per_step * 1e3:.2f} us/step, "
         f"{gbps:.1f} GB/s")
 
-    # dominant kernel: the 4 bpw GEMV (gate shape 6144 x 2048), back to back
-    dom_bytes = INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2
-    gd = capture(lambda l: dl.gemv(dl.layers[l], "gate", dl.xr_m), L, dev)
+    # dominant kernel: the fused gate/up launch (RHT + two 6144 x 2048 4 bpw
+    # GEMVs), back to back over the layer sets
+    dom_bytes = 2 * (INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2)
+    gd = capture(lambda l: dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.sign_h), L, dev)
     time_graph(gd, 2, dev)
     dreps = max(4, 2000 // L)
     dms, _ = time_graph(gd, dreps, dev)
     dom_us = dms * 1e3 / (dreps * L)
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
-    log(f"dominant 4 bpw GEMV 6144x2048: {dom_us:.2f} us/launch, {dom_gbps:.1f} GB/s")
+    log(f"dominant launch gate+up (RHT + 2 x 4 bpw 6144x2048): {dom_us:.2f} us/launch, {dom_gbps:.1f} GB/s")
     return dict(steps=steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
                 dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl)
 
@@ -350,7 +355,7 @@ def main():
     if args.only == "dominant":
         dl = DenseLayers(args.layers, dev)
         for l in range(args.layers):
-            dl.gemv(dl.layers[l], "gate", dl.xr_m)
+            dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.sign_h)
         torch.cuda.synchronize(dev)
         log("dominant-only run done")
         return
@@ -396,7 +401,7 @@ def main():
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
         "roofline": {
-            "kernel": "vq_gemv_kernel 4 bpw (16,16), 6144 x 2048, batch 1",
+            "kernel": "vq_gemv_kernel (fused RHT) gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1",
             "bound": "hbm",
             "achieved": round(d["dom_gbps"], 2),
             "peak": PEAK_HBM_GBPS,

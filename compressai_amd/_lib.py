@@ -28,6 +28,12 @@ SIGNATURES = {
     "vq2_last_error": ([], ctypes.c_char_p),
     "vq2_gemv": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
                   _i64, _i64, _f32, _vp], _i32),
+    "vq2_gemv_rht": ([_vp, _i32, _i64, _i64, _vp, _vp, _i64, _f32, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _i32,
+                      _i64, _f32, _vp], _i32),
+    "vq2_moe_gate_up_rht": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _vp,
+                             _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
+    "vq2_moe_down_swiglu_combine": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _vp, _i64, _i64, _vp, _i64,
+                                     _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_grouped": ([_vp, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _i32,
                          _i64, _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_down_combine": ([_vp, _i32, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i32,
@@ -48,6 +54,12 @@ _lib = None
 
 class Vq2Error(RuntimeError):
     """A libvq2_amd entry returned a non-zero status."""
+
+
+class Seg(ctypes.Structure):
+    """struct vq2_seg of include/vq2_amd.h"""
+    _fields_ = [("idx0", ctypes.c_void_p), ("idx1", ctypes.c_void_p), ("scale", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("out_rows", ctypes.c_int64), ("y_stride", ctypes.c_int64)]
 
 
 def header_symbols() -> list[str]:

@@ -76,6 +76,38 @@ int vq2_version(void) { return 100; }
 
 const char* vq2_last_error(void) { return g_err; }
 
+// The fused-rotation entries read perm / sign with vector loads.
+static int check_rot_tables(const int32_t* perm, const int8_t* sign)
+{
+    CHECK((uintptr_t)perm % 16 == 0, "perm must be 16-byte aligned");
+    CHECK((uintptr_t)sign % 8 == 0, "sign must be 8-byte aligned");
+    return VQ2_OK;
+}
+
+static GemvCall base_call(const void* x, int x_dt, int s2, const void* cb0, const void* cb1, int cb_dt, int s_dt,
+                          int y_dt, int64_t ng, int64_t batch, float rs, void* stream)
+{
+    GemvCall c{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.x_pdiv = 1;
+    c.s2 = s2;
+    c.cb0 = cb0;
+    c.cb1 = cb1;
+    c.cb_dt = cb_dt;
+    c.s_dt = s_dt;
+    c.n_experts = 1;
+    c.P = 1;
+    c.n_out_groups = 1;
+    c.y_dt = y_dt;
+    c.ng = ng;
+    c.batch = batch;
+    c.rs = rs;
+    c.stream = stream;
+    c.xscale = 1.0f;
+    return c;
+}
+
 int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0, const void* idx1,
              int s2_kind, const void* cb0, const void* cb1, int cb_dt, const void* scale, int s_dt, void* y, int y_dt,
              int64_t y_stride, int64_t out_rows, int64_t n, float rs, void* stream)
@@ -91,40 +123,52 @@ int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int
     int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
     if (r) return r;
     CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "vq2_gemv: idx1 must be given iff s2_kind != NONE");
-    GemvCall c{};
-    c.x = x;
-    c.x_dt = x_dt;
+    GemvCall c = base_call(x, x_dt, s2_kind, cb0, cb1, cb_dt, s_dt, y_dt, n / 8, batch, rs, stream);
     c.x_bstride = x_stride;
-    c.x_pstride = 0;
-    c.x_pdiv = 1;
-    c.idx0 = idx0;
-    c.idx1 = idx1;
-    c.s2 = s2_kind;
-    c.cb0 = cb0;
-    c.cb1 = cb1;
-    c.cb_dt = cb_dt;
-    c.scale = scale;
-    c.s_dt = s_dt;
-    c.ids = nullptr;
-    c.n_experts = 1;
-    c.P = 1;
-    c.n_out_groups = 1;
-    c.y = y;
-    c.y_dt = y_dt;
-    c.y_bstride = y_stride;
-    c.y_ostride = 0;
-    c.out_rows = out_rows;
-    c.ng = n / 8;
-    c.batch = batch;
-    c.rs = rs;
-    c.stream = stream;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{idx0, idx1, scale, y, out_rows, y_stride};
+    return gemv_launch(c);
+}
+
+int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int32_t* perm, const int8_t* sign,
+                 int64_t hb, float rht_scale, int n_seg, const vq2_seg* segs, int s2_kind, const void* cb0,
+                 const void* cb1, int cb_dt, int s_dt, int y_dt, int64_t n, float rs, void* stream)
+{
+    clear_error();
+    CHECK(batch >= 0 && n > 0 && n % 8 == 0, "vq2_gemv_rht: bad sizes");
+    CHECK(n_seg >= 1 && n_seg <= 4 && segs, "vq2_gemv_rht: 1..4 segments required");
+    if (batch == 0) return VQ2_OK;
+    CHECK(x, "vq2_gemv_rht: NULL activation");
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_gemv_rht: bad dtype code");
+    CHECK(x_stride >= n, "vq2_gemv_rht: x_stride < n");
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && n % hb == 0,
+          "vq2_gemv_rht: hb=%lld must be a power of two in [2, 8192] dividing n", (long long)hb);
+    if (int rr = check_rot_tables(perm, sign)) return rr;
+    int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
+    if (r) return r;
+    GemvCall c = base_call(x, x_dt, s2_kind, cb0, cb1, cb_dt, s_dt, y_dt, n / 8, batch, rs, stream);
+    c.x_bstride = x_stride;
+    c.nseg = n_seg;
+    for (int s = 0; s < n_seg; s++) {
+        const vq2_seg& g = segs[s];
+        CHECK(g.out_rows >= 0, "vq2_gemv_rht: segment %d has negative rows", s);
+        CHECK(g.out_rows == 0 || (g.idx0 && g.scale && g.y), "vq2_gemv_rht: segment %d has a NULL pointer", s);
+        CHECK((s2_kind == VQ2_S2_NONE) == (g.idx1 == nullptr), "vq2_gemv_rht: segment %d idx1 mismatch", s);
+        CHECK(g.y_stride >= g.out_rows, "vq2_gemv_rht: segment %d y_stride < out_rows", s);
+        c.seg[s] = GemvSegCall{g.idx0, g.idx1, g.scale, g.y, g.out_rows, g.y_stride};
+    }
+    c.xm = 1;
+    c.perm = perm;
+    c.sign = sign;
+    c.hb = hb;
+    c.xscale = rht_scale;
     return gemv_launch(c);
 }
 
 int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pairs_per_x, const void* ids,
-                    int ids_dt, int64_t n_pairs,
-                    const int16_t* pool, int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt,
-                    void* y, int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+                    int ids_dt, int64_t n_pairs, const int16_t* pool, int64_t n_experts, const void* cb, int cb_dt,
+                    const void* pool_scale, int s_dt, void* y, int y_dt, int64_t y_pair_stride, int64_t out_rows,
+                    int64_t ng, float rs, void* stream)
 {
     clear_error();
     CHECK(n_pairs >= 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_grouped: bad sizes");
@@ -138,33 +182,53 @@ int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pair
     CHECK(n_pairs <= 65535, "vq2_moe_grouped: n_pairs=%lld > 65535", (long long)n_pairs);
     int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
     if (r) return r;
-    GemvCall c{};
-    c.x = x;
-    c.x_dt = x_dt;
+    GemvCall c = base_call(x, x_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, y_dt, ng, 1, rs, stream);
     c.x_bstride = ng * 8;
     c.x_pstride = x_pair_stride;
     c.x_pdiv = (int)pairs_per_x;
-    c.idx0 = pool;
-    c.idx1 = nullptr;
-    c.s2 = VQ2_S2_NONE;
-    c.cb0 = cb;
-    c.cb_dt = cb_dt;
-    c.scale = pool_scale;
-    c.s_dt = s_dt;
     c.ids = ids;
     c.ids_i64 = ids_dt == VQ2_ID_I64;
     c.n_experts = n_experts;
-    c.P = 1;
     c.n_out_groups = n_pairs;
-    c.y = y;
-    c.y_dt = y_dt;
-    c.y_bstride = 0;
     c.y_ostride = y_pair_stride;
-    c.out_rows = out_rows;
-    c.ng = ng;
-    c.batch = 1;
-    c.rs = rs;
-    c.stream = stream;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, y, out_rows, 0};
+    return gemv_launch(c);
+}
+
+int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign, int64_t hb,
+                        float rht_scale, const void* ids, int ids_dt, int64_t P, const int16_t* pool,
+                        int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* y,
+                        int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    clear_error();
+    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_gate_up_rht: bad sizes");
+    if (tokens == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(h && ids && pool && pool_scale && y, "vq2_moe_gate_up_rht: NULL pointer argument");
+    CHECK(dt_ok(h_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_moe_gate_up_rht: bad dtype code");
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_gate_up_rht: bad ids dtype");
+    CHECK(y_pair_stride >= out_rows, "vq2_moe_gate_up_rht: y_pair_stride < out_rows");
+    CHECK(tokens * P <= 65535, "vq2_moe_gate_up_rht: too many pairs");
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "vq2_moe_gate_up_rht: bad hb");
+    if (int rr = check_rot_tables(perm, sign)) return rr;
+    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    if (r) return r;
+    GemvCall c = base_call(h, h_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, y_dt, ng, 1, rs, stream);
+    c.x_bstride = ng * 8;
+    c.x_pstride = ng * 8;
+    c.x_pdiv = (int)P;
+    c.ids = ids;
+    c.ids_i64 = ids_dt == VQ2_ID_I64;
+    c.n_experts = n_experts;
+    c.n_out_groups = tokens * P;
+    c.y_ostride = y_pair_stride;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, y, out_rows, 0};
+    c.xm = 1;
+    c.perm = perm;
+    c.sign = sign;
+    c.hb = hb;
+    c.xscale = rht_scale;
     return gemv_launch(c);
 }
 
@@ -183,33 +247,57 @@ int vq2_moe_down_combine(const void* x, int x_dt, const void* ids, int ids_dt, c
     CHECK(tokens <= 65535 && P <= 4096, "vq2_moe_down_combine: too many tokens/pairs");
     int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
     if (r) return r;
-    GemvCall c{};
-    c.x = x;
-    c.x_dt = x_dt;
+    GemvCall c = base_call(x, x_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, out_dt, ng, 1, rs, stream);
     c.x_bstride = ng * 8;
     c.x_pstride = ng * 8;
-    c.x_pdiv = 1;
-    c.idx0 = pool;
-    c.s2 = VQ2_S2_NONE;
-    c.cb0 = cb;
-    c.cb_dt = cb_dt;
-    c.scale = pool_scale;
-    c.s_dt = s_dt;
     c.ids = ids;
     c.ids_i64 = ids_dt == VQ2_ID_I64;
     c.n_experts = n_experts;
     c.pair_w = w;
     c.P = (int)P;
     c.n_out_groups = tokens;
-    c.y = out;
-    c.y_dt = out_dt;
-    c.y_bstride = 0;
     c.y_ostride = out_stride;
-    c.out_rows = out_rows;
-    c.ng = ng;
-    c.batch = 1;
-    c.rs = rs;
-    c.stream = stream;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, out, out_rows, 0};
+    return gemv_launch(c);
+}
+
+int vq2_moe_down_swiglu_combine(const void* gu, int gu_dt, int64_t gu_stride, const int32_t* perm,
+                                const int8_t* sign, int64_t hb, float rht_scale, const void* ids, int ids_dt,
+                                const float* w, int64_t tokens, int64_t P, const int16_t* pool, int64_t n_experts,
+                                const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* out, int out_dt,
+                                int64_t out_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    clear_error();
+    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_down_swiglu_combine: bad sizes");
+    if (tokens == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(gu && ids && w && pool && pool_scale && out, "vq2_moe_down_swiglu_combine: NULL pointer argument");
+    CHECK(dt_ok(gu_dt) && dt_ok(s_dt) && dt_ok(out_dt), "vq2_moe_down_swiglu_combine: bad dtype code");
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_down_swiglu_combine: bad ids dtype");
+    CHECK(gu_stride >= 2 * ng * 8, "vq2_moe_down_swiglu_combine: gu_stride < 2 * n");
+    CHECK(out_stride >= out_rows, "vq2_moe_down_swiglu_combine: out_stride < out_rows");
+    CHECK(tokens <= 65535 && P <= 4096, "vq2_moe_down_swiglu_combine: too many tokens/pairs");
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "vq2_moe_down_swiglu_combine: bad hb");
+    if (int rr = check_rot_tables(perm, sign)) return rr;
+    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    if (r) return r;
+    GemvCall c = base_call(gu, gu_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, out_dt, ng, 1, rs, stream);
+    c.x_bstride = gu_stride;
+    c.x_pstride = gu_stride;
+    c.ids = ids;
+    c.ids_i64 = ids_dt == VQ2_ID_I64;
+    c.n_experts = n_experts;
+    c.pair_w = w;
+    c.P = (int)P;
+    c.n_out_groups = tokens;
+    c.y_ostride = out_stride;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, out, out_rows, 0};
+    c.xm = 2;
+    c.perm = perm;
+    c.sign = sign;
+    c.hb = hb;
+    c.xscale = rht_scale;
     return gemv_launch(c);
 }
 

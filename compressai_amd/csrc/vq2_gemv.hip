@@ -1,98 +1,192 @@
-// vq2_gemv.hip -- launch planning and dispatch of the VQ GEMV kernel
-// (kernel body and design notes: vq2_gemv_kernel.hpp).
+// vq2_gemv.hip -- launch planning and dispatch of the VQ GEMV kernels
+// (kernel bodies and design notes: vq2_gemv_kernel.hpp).
+#include <stdlib.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "vq2_gemv_kernel.hpp"
 
 namespace vq2 {
 
-static GemvPlan plan_gemv(int64_t out_rows, int64_t ng, int batch, int64_t n_out_groups, int P, int num_cu)
+// LDS the planner allows per workgroup (two workgroups per CU stay resident)
+constexpr int64_t GEMV_LDS_BUDGET = 64 * 1024;
+
+// Tuning overrides read once from the environment (VQ2_GEMV_IT: rows per
+// lane 1/2/4; VQ2_GEMV_OCC_SCALE: multiplier on the resident-workgroup grid).
+static int env_int(const char* name, int dflt)
+{
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+static double env_double(const char* name, double dflt)
+{
+    const char* v = getenv(name);
+    return v ? atof(v) : dflt;
+}
+
+int resident_blocks_per_cu(const void* fn, int threads, size_t shm)
+{
+    static std::mutex mu;
+    static std::map<std::tuple<const void*, int, size_t, int>, int> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const auto key = std::make_tuple(fn, threads, shm, dev);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, shm) != hipSuccess || nb < 1) nb = 1;
+    cache[key] = nb;
+    return nb;
+}
+
+static GemvPlan plan_gemv(const GemvCall& c, int num_cu)
 {
     GemvPlan p;
+    const int batch = (int)c.batch;
+    const int P = c.P > 0 ? c.P : 1;
+    p.xm = c.xm;
     p.bt = batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
-    p.gpl = 8 / p.bt;
-    int64_t need = (ng + p.gpl - 1) / p.gpl;
+    p.gpl = 8 / p.bt;  // activation slice per lane stays at 64 fp32 values
+    const int64_t need = (c.ng + p.gpl - 1) / p.gpl;
     int lpr = 1;
     while (lpr < need && lpr < 32) lpr <<= 1;
     p.lpr = lpr;
     const int64_t kc = (int64_t)lpr * p.gpl;
-    const int64_t nch = (ng + kc - 1) / kc;
-    p.wk = (int)(nch < 4 ? nch : 4);  // <= 4 waves: the kernel is built for 256-thread workgroups
-    p.wr = p.wk >= 4 ? 1 : 4 / p.wk;
-    p.threads = 64 * p.wk * p.wr;
+    const int64_t nch = (c.ng + kc - 1) / kc;
+    const int64_t items = (int64_t)P * nch;
+    p.wi = (int)(items < 4 ? items : 4);
+    p.wr = 4 / p.wi;
+    p.threads = 64 * p.wi * p.wr;
     const int rpw = 64 / lpr;
     const int64_t ztiles = (batch + p.bt - 1) / p.bt;
-    const bool use_lds = p.wk > 1 || P > 1;
-    // rows per lane: as many as keep >= 4 workgroups per CU busy
-    p.it = 1;
-    for (int it = 4; it >= 2; it >>= 1) {
-        const int64_t rpi = (int64_t)it * rpw * p.wr;
-        const int64_t blocks = (out_rows + rpi - 1) / rpi;
-        if (use_lds && rpi * p.bt > p.threads) continue;
-        if (blocks * n_out_groups * ztiles >= 4LL * num_cu) { p.it = it; break; }
-    }
-    p.rows_per_iter = (int64_t)p.it * rpw * p.wr;
-    p.n_rowblocks = (out_rows + p.rows_per_iter - 1) / p.rows_per_iter;
+    int64_t max_rows = 0;
+    for (int s = 0; s < c.nseg; s++) max_rows = c.seg[s].out_rows > max_rows ? c.seg[s].out_rows : max_rows;
+    // rows per lane: enough that each lane has >= 8 centroid gathers in
+    // flight per row block (GPL codes per row); the grid is persistent
+    p.it = p.gpl >= 8 ? 1 : (p.gpl == 4 ? 2 : 4);
+    static const int it_env = env_int("VQ2_GEMV_IT", 0);
+    if (it_env == 1 || it_env == 2 || it_env == 4) p.it = it_env;
+    static const double occ_env = env_double("VQ2_GEMV_OCC_SCALE", 1.0);
+    p.occ_scale = occ_env > 0 ? occ_env : 1.0;
+    p.num_cu = num_cu;
+    p.rows_per_block = (int64_t)p.it * rpw * p.wr;
+    p.n_rowblocks = 0;
+    for (int s = 0; s < c.nseg; s++) p.n_rowblocks += (c.seg[s].out_rows + p.rows_per_block - 1) / p.rows_per_block;
+    (void)ztiles;
+    (void)max_rows;
     return p;
+}
+
+hipError_t gemv_generic_dispatch(int cb_dt, int s2, int si, const GemvArgs& a, dim3 grid, hipStream_t st)
+{
+    switch (cb_dt) {
+    case VQ2_DT_F16: return launch_generic<VQ2_DT_F16>(s2, si, a, grid, st);
+    case VQ2_DT_BF16: return launch_generic<VQ2_DT_BF16>(s2, si, a, grid, st);
+    default: return launch_generic<VQ2_DT_F32>(s2, si, a, grid, st);
+    }
 }
 
 int gemv_launch(const GemvCall& c)
 {
-    if (c.out_rows == 0 || c.batch == 0 || c.n_out_groups == 0) return VQ2_OK;
+    if (c.batch == 0 || c.n_out_groups == 0 || c.nseg == 0) return VQ2_OK;
+    if (c.nseg < 0 || c.nseg > VQ2_MAX_SEG) return set_error(VQ2_ERR_ARG, "vq2 gemv: 1..%d segments", VQ2_MAX_SEG);
+    if (c.n_out_groups > 65535) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: too many output groups");
+    if (c.batch > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: batch too large");
     GemvArgs a{};
     a.x = c.x;
     a.x_dt = c.x_dt;
     a.x_bstride = c.x_bstride;
     a.x_pstride = c.x_pstride;
     a.x_pdiv = c.x_pdiv > 0 ? c.x_pdiv : 1;
-    a.idx0 = c.idx0;
-    a.idx1 = c.idx1;
     a.cb0 = c.cb0;
     a.cb1 = c.cb1;
-    a.scale = c.scale;
     a.s_dt = c.s_dt;
-    a.e_istride = c.out_rows * c.ng;
-    a.e_sstride = c.out_rows;
     a.ids = c.ids;
     a.ids_i64 = c.ids_i64;
     a.n_experts = c.n_experts;
     a.pair_w = c.pair_w;
     a.P = c.P > 0 ? c.P : 1;
-    a.y = c.y;
     a.y_dt = c.y_dt;
-    a.y_bstride = c.y_bstride;
     a.y_ostride = c.y_ostride;
-    a.out_rows = c.out_rows;
     a.ng = c.ng;
     a.batch = (int)c.batch;
     a.rs = c.rs;
+    a.nseg = c.nseg;
+    a.e_istride = c.seg[0].out_rows * c.ng;  // grouped launches have one segment
+    a.e_sstride = c.seg[0].out_rows;
+    a.perm = c.perm;
+    a.sign = c.sign;
+    a.xscale = c.xscale;
+    int L = 0;
+    if (c.xm != 0) {
+        while ((1LL << L) < c.hb) L++;
+        if (L < 1 || L > 13 || (1LL << L) != c.hb || (c.ng * 8) % c.hb)
+            return set_error(VQ2_ERR_ARG, "vq2 gemv: hb=%lld must be a power of two in [2, 8192] dividing n=%lld",
+                             (long long)c.hb, (long long)(c.ng * 8));
+    }
+    a.hb_log2 = L;
+    hipStream_t st = (hipStream_t)c.stream;
+    const int num_cu = device_cu_count();
+    const GemvPlan p = plan_gemv(c, num_cu);
 
-    const GemvPlan p = plan_gemv(c.out_rows, c.ng, (int)c.batch, c.n_out_groups, a.P, device_cu_count());
+    // the vector kernel needs GPL-wide, aligned index words and 16-byte
+    // aligned activation rows
+    uintptr_t ia = 0, i8 = 0;
+    for (int s = 0; s < c.nseg; s++) {
+        ia |= (uintptr_t)c.seg[s].idx0;
+        if (c.s2 == VQ2_S2_U16) ia |= (uintptr_t)c.seg[s].idx1;
+        if (c.s2 == VQ2_S2_U8) i8 |= (uintptr_t)c.seg[s].idx1;
+    }
+    const int64_t esz_x = dt_size(c.x_dt);
+    const bool x_vec = c.xm != 0 || (((uintptr_t)c.x % 16 == 0) && ((c.x_bstride * esz_x) % 16 == 0) &&
+                                     ((c.x_pstride * esz_x) % 16 == 0));
+    const bool vec_ok = x_vec && (c.ng % p.gpl == 0) && (ia % (2 * p.gpl) == 0) && (i8 % p.gpl == 0);
+    hipError_t err;
+    if (!vec_ok) {
+        if (c.xm != 0)
+            return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused rotation needs n %% 64 == 0 and aligned planes");
+        for (int s = 0; s < c.nseg; s++) {
+            a.seg[s] = GemvSeg{c.seg[s].idx0, c.seg[s].idx1, c.seg[s].scale, c.seg[s].y, c.seg[s].out_rows,
+                               c.seg[s].y_bstride, 0};
+            const int64_t work = c.batch * c.seg[s].out_rows;
+            int64_t blocks = (work + 255) / 256;
+            if (blocks > 4LL * num_cu) blocks = 4LL * num_cu;
+            if (blocks == 0) continue;
+            err = gemv_generic_dispatch(c.cb_dt, c.s2, s, a, dim3((unsigned)blocks, (unsigned)c.n_out_groups), st);
+            if (err != hipSuccess) return set_hip_error(err, "vq2 gemv (generic) launch");
+        }
+        return VQ2_OK;
+    }
+
+    int64_t rb = 0;
+    for (int s = 0; s < c.nseg; s++) {
+        a.seg[s] = GemvSeg{c.seg[s].idx0, c.seg[s].idx1, c.seg[s].scale, c.seg[s].y, c.seg[s].out_rows,
+                           c.seg[s].y_bstride, rb};
+        rb += (c.seg[s].out_rows + p.rows_per_block - 1) / p.rows_per_block;
+    }
     a.lpr = p.lpr;
-    a.wk = p.wk;
+    a.wi = p.wi;
     a.n_rowblocks = p.n_rowblocks;
-    const bool use_lds = p.wk > 1 || a.P > 1;
     if (p.threads > 256 || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
-    if (use_lds && p.rows_per_iter * p.bt > p.threads)
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: combine/split-K tile does not fit (rows %lld, batch tile %d)",
-                         (long long)p.rows_per_iter, p.bt);
-
-    // vector loads need 16/8/4-byte aligned index words and activation rows
-    const int64_t esz_x = c.x_dt == VQ2_DT_F32 ? 4 : 2;
-    const uintptr_t ia = (uintptr_t)c.idx0 | (uintptr_t)(c.idx1 ? c.idx1 : c.idx0);
-    const int idx_align = p.gpl * 2;
-    a.vec_ok = (c.ng % p.gpl == 0) && (ia % idx_align == 0) &&
-               (c.s2 != VQ2_S2_U8 || ((uintptr_t)c.idx1 % p.gpl == 0));
-    a.x_vec = ((uintptr_t)c.x % 16 == 0) && ((c.x_bstride * esz_x) % 16 == 0) && ((c.x_pstride * esz_x) % 16 == 0);
-
+    if (c.xm == 2 && (c.s2 != VQ2_S2_NONE || p.bt != 1))
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 bpw, batch 1");
+    if (c.xm == 1 && p.bt > 2)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused rotation supports batch <= 2 per launch");
     const int64_t ztiles = (c.batch + p.bt - 1) / p.bt;
-    if (ztiles > 65535 || c.n_out_groups > 65535)
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: too many pairs/batch tiles");
-    const int64_t cap = 8LL * device_cu_count();
-    const int64_t gx = p.n_rowblocks < cap ? p.n_rowblocks : cap;
-    dim3 grid((unsigned)gx, (unsigned)c.n_out_groups, (unsigned)ztiles);
-    const size_t shm = use_lds ? (size_t)p.wk * p.rows_per_iter * p.bt * sizeof(float) : 0;
-    hipStream_t st = (hipStream_t)c.stream;
-    hipError_t err;
+    if (ztiles > 65535) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: too many batch tiles");
+    // grid.x is set per kernel from its resident-workgroup count
+    dim3 grid(1, (unsigned)c.n_out_groups, (unsigned)ztiles);
+    const int64_t items = (int64_t)a.P * ((c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl));
+    const int64_t x_floats = c.xm == 0 ? 0 : (c.xm == 2 ? (int64_t)a.P : p.bt) * c.ng * 8;
+    const int64_t part_floats = items > 1 ? (int64_t)p.wi * p.rows_per_block * p.bt : 0;
+    const size_t shm = (size_t)(x_floats + part_floats) * sizeof(float);
+    if ((int64_t)shm > GEMV_LDS_BUDGET)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: %zu bytes of LDS needed (> %lld)", shm,
+                         (long long)GEMV_LDS_BUDGET);
     switch (c.cb_dt) {
     case VQ2_DT_F16: err = gemv_dispatch_f16(c.s2, a, p, grid, shm, st); break;
     case VQ2_DT_BF16: err = gemv_dispatch_bf16(c.s2, a, p, grid, shm, st); break;

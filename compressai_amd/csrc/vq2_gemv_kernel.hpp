@@ -1,11 +1,11 @@
 // vq2_gemv_kernel.hpp -- vector-quantized GEMV kernel body for gfx950 (CDNA4, wave64).
 //
 // One kernel body serves three call shapes of the decode path:
-//   dense    y[b, r]      = VQ(W) x_b                                   (P = 1, no ids)
-//   grouped  y[k, r]      = VQ(W_{ids[k]}) x_k                          (P = 1, ids)
-//   combine  out[t, r]    = sum_j w[t*P+j] * VQ(W_{ids[t*P+j]}) x_{t*P+j} (P > 1)
-// with VQ(W)[r, 8g+j] = (cb0[i0[r,g]] [+ cb1[i1[r,g]]])[j], the row scale and
-// rs applied after fp32 accumulation: y = (acc * s[r]) * rs.
+//   dense    y[b, r]    = VQ(W) x_b                                     (P = 1, no ids)
+//   grouped  y[k, r]    = VQ(W_{ids[k]}) x_k                            (P = 1, ids)
+//   combine  out[t, r]  = sum_j w[t*P+j] * VQ(W_{ids[t*P+j]}) x_{t*P+j}   (P > 1)
+// with VQ(W)[r, 8g+j] = (cb0[i0[r,g]] [+ cb1[i1[r,g]]])[j] and the row scale
+// and rs applied after fp32 accumulation: y = (acc * s[r]) * rs.
 //
 // Reference semantics: vq2/kernels.py:32-78 (_vq_gemv_16_8, _vq_gemv_16) and
 // vq2/kernels.py:117-176 (_parallel_moe_gate_up/_down_kernel); the weighted
@@ -16,30 +16,45 @@
 //     activation (GPL*8 values per batch column) lives in VGPRs as fp32;
 //   * LPR lanes cover one row of a K-chunk (KC = LPR*GPL groups), so a wave
 //     streams 64/LPR rows per index load: consecutive lanes read consecutive
-//     16-byte index words -> fully coalesced, non-temporal index streams;
+//     index words -> fully coalesced, non-temporal index streams;
 //   * every index triggers one 16-byte centroid gather (the 1 MiB codebook is
 //     L2-resident); the (16,8) stage-2 codebook (256 x 8) is staged in LDS;
-//   * WK waves split K (one K-chunk each) and reduce through LDS in a fixed
-//     order (deterministic split-K inside the workgroup);
+//   * a row block's work items (expert pair x K-chunk) are spread over WI
+//     waves, the other waves split the rows; item partials are scaled per
+//     pair and reduced through LDS in a fixed order (deterministic split-K
+//     and weighted combine inside the workgroup);
 //   * row partials are reduced across the LPR lanes with DPP/swizzle.
+// Shapes whose index rows or activations cannot be read with vector loads
+// (n/8 not a multiple of GPL, misaligned planes or rows) take vq_gemv_generic.
 #pragma once
 #include "vq2_common.hpp"
 #include "vq2_internal.hpp"
 
 namespace vq2 {
 
+// One matrix of a launch.  Dense launches may carry up to VQ2_MAX_SEG
+// matrices that share the activation (q/k/v, gate/up); grouped launches have
+// one segment whose pointers are the expert pool's base.
+struct GemvSeg {
+    const int16_t* idx0;
+    const void* idx1;
+    const void* scale;
+    void* y;
+    int64_t out_rows;
+    int64_t y_bstride;  // elements between batch columns of y
+    int64_t rb_start;   // first row block of this segment in the launch
+};
+
+constexpr int VQ2_MAX_SEG = 4;
+
 struct GemvArgs {
     const void* x;
     int x_dt;
-    int x_vec;          // 1: x rows are 16-byte aligned -> vector loads
     int64_t x_bstride;  // elements between batch columns
-    int64_t x_pstride;  // elements between x blocks of consecutive pair groups
-    int x_pdiv;         // pair p uses x block p / x_pdiv
-    const int16_t* idx0;
-    const void* idx1;
+    int64_t x_pstride;  // elements between x blocks
+    int x_pdiv;         // pair p reads x block p / x_pdiv
     const void* cb0;
     const void* cb1;
-    const void* scale;
     int s_dt;
     int64_t e_istride;  // elements between experts in the index planes
     int64_t e_sstride;  // elements between experts in the scale array
@@ -48,18 +63,24 @@ struct GemvArgs {
     int64_t n_experts;
     const float* pair_w;  // per-pair combine weights (P > 1), may be null
     int P;                // pairs per output group
-    void* y;
     int y_dt;
-    int64_t y_bstride;
     int64_t y_ostride;
-    int64_t out_rows;
     int64_t ng;
     int batch;
     float rs;
     int lpr;  // lanes per row (power of two <= 32)
-    int wk;   // waves along K
-    int vec_ok;  // index planes allow GPL-wide vector loads
+    int wi;   // waves along work items (pair x chunk)
     int64_t n_rowblocks;
+    int nseg;
+    GemvSeg seg[VQ2_MAX_SEG];
+    // activation prologue (XM != 0): the workgroup builds the rotated
+    // activation in LDS: XM 1: RHT(x) of each batch column; XM 2: RHT of
+    // silu(gate) * up for each pair of the output group (x holds the pairs'
+    // [gate | up] rows, stride x_pstride, width 2 * n).
+    const int32_t* perm;
+    const int8_t* sign;
+    int hb_log2;
+    float xscale;
 };
 
 template <int CBT>
@@ -69,80 +90,63 @@ struct Centroid;
 template <>
 struct Centroid<VQ2_DT_F16> {
     half8_t h;
-    __device__ __forceinline__ void load(const void* cb, uint32_t code)
-    {
-        h = *((const half8_t*)cb + code);
-    }
+    __device__ __forceinline__ void load(const void* cb, uint32_t code) { h = *((const half8_t*)cb + code); }
     __device__ __forceinline__ float get(int j) const { return (float)h[j]; }
 };
 
 template <>
 struct Centroid<VQ2_DT_BF16> {
-    uint4 u;
-    __device__ __forceinline__ void load(const void* cb, uint32_t code) { u = *((const uint4*)cb + code); }
+    u32x4 u;
+    __device__ __forceinline__ void load(const void* cb, uint32_t code) { u = *((const u32x4*)cb + code); }
     __device__ __forceinline__ float get(int j) const
     {
-        uint32_t w = (j >> 1) == 0 ? u.x : (j >> 1) == 1 ? u.y : (j >> 1) == 2 ? u.z : u.w;
+        const uint32_t w = u[j >> 1];
         return (j & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
     }
 };
 
 template <>
 struct Centroid<VQ2_DT_F32> {
-    float4 a, b;
+    u32x4 a, b;
     __device__ __forceinline__ void load(const void* cb, uint32_t code)
     {
-        const float4* p = (const float4*)cb + 2 * (size_t)code;
+        const u32x4* p = (const u32x4*)cb + 2 * (size_t)code;
         a = p[0];
         b = p[1];
     }
-    __device__ __forceinline__ float get(int j) const
-    {
-        switch (j) {
-        case 0: return a.x;
-        case 1: return a.y;
-        case 2: return a.z;
-        case 3: return a.w;
-        case 4: return b.x;
-        case 5: return b.y;
-        case 6: return b.z;
-        default: return b.w;
-        }
-    }
+    __device__ __forceinline__ float get(int j) const { return __uint_as_float(j < 4 ? a[j] : b[j - 4]); }
 };
 
 // Stage-2 centroid from the LDS copy of a 256-row codebook.
 template <int CBT>
-__device__ __forceinline__ Centroid<CBT> lds_centroid(const uint4* s_cb1, uint32_t code)
+__device__ __forceinline__ Centroid<CBT> lds_centroid(const u32x4* s_cb1, uint32_t code)
 {
     Centroid<CBT> c;
     if constexpr (CBT == VQ2_DT_F32) {
-        uint4 a = s_cb1[2 * code], b = s_cb1[2 * code + 1];
-        c.a = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w));
-        c.b = make_float4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w));
+        c.a = s_cb1[2 * code];
+        c.b = s_cb1[2 * code + 1];
     } else if constexpr (CBT == VQ2_DT_F16) {
-        uint4 a = s_cb1[code];
-        c.h = __builtin_bit_cast(half8_t, a);
+        c.h = __builtin_bit_cast(half8_t, s_cb1[code]);
     } else {
         c.u = s_cb1[code];
     }
     return c;
 }
 
-// Load GPL uint16 codes of plane 0 (int16 storage) starting at element off.
+// GPL uint16 codes (int16 storage) starting at element off; vector load.
 template <int GPL>
 __device__ __forceinline__ void load_codes16(const int16_t* p, int64_t off, uint32_t (&c)[GPL])
 {
     const int16_t* q = p + off;
     if constexpr (GPL == 8) {
-        u32x4 v = __builtin_nontemporal_load((const u32x4*)q);
-        c[0] = v.x & 0xFFFFu; c[1] = v.x >> 16; c[2] = v.y & 0xFFFFu; c[3] = v.y >> 16;
-        c[4] = v.z & 0xFFFFu; c[5] = v.z >> 16; c[6] = v.w & 0xFFFFu; c[7] = v.w >> 16;
+        const u32x4 v = __builtin_nontemporal_load((const u32x4*)q);
+#pragma unroll
+        for (int i = 0; i < 4; i++) { c[2 * i] = v[i] & 0xFFFFu; c[2 * i + 1] = v[i] >> 16; }
     } else if constexpr (GPL == 4) {
-        u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
+        const u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
         c[0] = v.x & 0xFFFFu; c[1] = v.x >> 16; c[2] = v.y & 0xFFFFu; c[3] = v.y >> 16;
     } else if constexpr (GPL == 2) {
-        uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
+        const uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
         c[0] = v & 0xFFFFu; c[1] = v >> 16;
     } else {
         c[0] = (uint32_t)(uint16_t)__builtin_nontemporal_load(q);
@@ -154,14 +158,11 @@ __device__ __forceinline__ void load_codes8(const uint8_t* p, int64_t off, uint3
 {
     const uint8_t* q = p + off;
     if constexpr (GPL == 8) {
-        u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
+        const u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            c[i] = (v.x >> (8 * i)) & 0xFFu;
-            c[4 + i] = (v.y >> (8 * i)) & 0xFFu;
-        }
+        for (int i = 0; i < 4; i++) { c[i] = (v.x >> (8 * i)) & 0xFFu; c[4 + i] = (v.y >> (8 * i)) & 0xFFu; }
     } else if constexpr (GPL == 4) {
-        uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
+        const uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
 #pragma unroll
         for (int i = 0; i < 4; i++) c[i] = (v >> (8 * i)) & 0xFFu;
     } else {
@@ -170,278 +171,588 @@ __device__ __forceinline__ void load_codes8(const uint8_t* p, int64_t off, uint3
     }
 }
 
-// Load this lane's activation slice: groups [g0, g0+GPL) for nb batch
-// columns, as fp32.  Groups at or beyond ng read as zero.
-template <int GPL, int BT>
-__device__ __forceinline__ void load_x(const GemvArgs& a, const void* xb, int64_t g0, int nb, float (&xs)[BT][GPL * 8])
+// This lane's activation slice: groups [g0, g0+GPL) for nb batch columns,
+// as fp32.  Loads are unconditional from a clamped (always valid) address;
+// idle lanes and columns >= nb are zeroed afterwards.
+template <int GPL, int BT, int XT>
+__device__ __forceinline__ void load_x_t(const GemvArgs& a, const void* xb, int64_t g0, bool lane_ok, int nb,
+                                         float (&xs)[BT][GPL * 8])
 {
 #pragma unroll
     for (int b = 0; b < BT; b++) {
-        if (b < nb) {
-            const int64_t base = (int64_t)b * a.x_bstride + g0 * 8;
-            if (a.x_vec && g0 + GPL <= a.ng) {
-                if (a.x_dt == VQ2_DT_F32) {
-                    const float4* p = (const float4*)((const float*)xb + base);
+        const bool ok = lane_ok && b < nb;
+        const int64_t base = ok ? (int64_t)b * a.x_bstride + g0 * 8 : 0;
+        const float keep = ok ? 1.0f : 0.0f;
+        if constexpr (XT == VQ2_DT_F32) {
+            const u32x4* p = (const u32x4*)((const float*)xb + base);
 #pragma unroll
-                    for (int i = 0; i < GPL * 2; i++) {
-                        float4 v = p[i];
-                        xs[b][4 * i] = v.x; xs[b][4 * i + 1] = v.y; xs[b][4 * i + 2] = v.z; xs[b][4 * i + 3] = v.w;
-                    }
-                } else {
-                    const uint4* p = (const uint4*)((const uint16_t*)xb + base);
-                    const bool bf = a.x_dt == VQ2_DT_BF16;
+            for (int i = 0; i < GPL * 2; i++) {
+                const u32x4 v = p[i];
 #pragma unroll
-                    for (int i = 0; i < GPL; i++) {
-                        uint4 v = p[i];
-                        uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            if (bf) {
-                                xs[b][8 * i + 2 * k] = __uint_as_float(w[k] << 16);
-                                xs[b][8 * i + 2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
-                            } else {
-                                xs[b][8 * i + 2 * k] = f16_bits_to_f32((uint16_t)(w[k] & 0xFFFFu));
-                                xs[b][8 * i + 2 * k + 1] = f16_bits_to_f32((uint16_t)(w[k] >> 16));
-                            }
-                        }
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < GPL * 8; i++) {
-                    const int64_t g = g0 + i / 8;
-                    xs[b][i] = g < a.ng ? load_as_f32(xb, a.x_dt, base + i) : 0.0f;
-                }
+                for (int k = 0; k < 4; k++) xs[b][4 * i + k] = __uint_as_float(v[k]) * keep;
             }
         } else {
+            const u32x4* p = (const u32x4*)((const uint16_t*)xb + base);
 #pragma unroll
-            for (int i = 0; i < GPL * 8; i++) xs[b][i] = 0.0f;
+            for (int i = 0; i < GPL; i++) {
+                const u32x4 v = p[i];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if constexpr (XT == VQ2_DT_BF16) {
+                        xs[b][8 * i + 2 * k] = __uint_as_float(v[k] << 16) * keep;
+                        xs[b][8 * i + 2 * k + 1] = __uint_as_float(v[k] & 0xFFFF0000u) * keep;
+                    } else {
+                        xs[b][8 * i + 2 * k] = f16_bits_to_f32((uint16_t)(v[k] & 0xFFFFu)) * keep;
+                        xs[b][8 * i + 2 * k + 1] = f16_bits_to_f32((uint16_t)(v[k] >> 16)) * keep;
+                    }
+                }
+            }
         }
     }
 }
 
+template <int GPL, int BT>
+__device__ __forceinline__ void load_x(const GemvArgs& a, const void* xb, int64_t g0, bool lane_ok, int nb,
+                                       float (&xs)[BT][GPL * 8])
+{
+    if (a.x_dt == VQ2_DT_F32)
+        load_x_t<GPL, BT, VQ2_DT_F32>(a, xb, g0, lane_ok, nb, xs);
+    else if (a.x_dt == VQ2_DT_F16)
+        load_x_t<GPL, BT, VQ2_DT_F16>(a, xb, g0, lane_ok, nb, xs);
+    else
+        load_x_t<GPL, BT, VQ2_DT_BF16>(a, xb, g0, lane_ok, nb, xs);
+}
+
+__device__ __forceinline__ int64_t pair_expert(const GemvArgs& a, int64_t pair, bool& bad)
+{
+    int64_t e = 0;
+    if (a.ids) e = a.ids_i64 ? ((const int64_t*)a.ids)[pair] : (int64_t)((const int32_t*)a.ids)[pair];
+    bad = a.ids && (e < 0 || e >= a.n_experts);
+    return bad ? 0 : e;
+}
+
+// In-place blockwise Walsh-Hadamard transform of v[0, total) over
+// 2^L-point blocks (natural / Sylvester order) by all threads of the block:
+// radix-8 passes, each thread butterflies whole groups in registers, one
+// barrier per pass.
+template <int W>
+__device__ __forceinline__ void fwht_pass(float* v, int64_t total, int lo)
+{
+    const int64_t groups = total >> W;
+    for (int64_t g = threadIdx.x; g < groups; g += blockDim.x) {
+        const int64_t base = ((g >> lo) << (lo + W)) | (g & ((1LL << lo) - 1));
+        float r[1 << W];
+#pragma unroll
+        for (int k = 0; k < (1 << W); k++) r[k] = v[base + ((int64_t)k << lo)];
+#pragma unroll
+        for (int h = 1; h < (1 << W); h <<= 1)
+#pragma unroll
+            for (int k = 0; k < (1 << W); k++)
+                if ((k & h) == 0) {
+                    const float x0 = r[k], x1 = r[k | h];
+                    r[k] = x0 + x1;
+                    r[k | h] = x0 - x1;
+                }
+#pragma unroll
+        for (int k = 0; k < (1 << W); k++) v[base + ((int64_t)k << lo)] = r[k];
+    }
+}
+
+__device__ __forceinline__ void block_fwht(float* v, int64_t total, int L)
+{
+    for (int lo = 0; lo < L; lo += 3) {
+        const int w = L - lo < 3 ? L - lo : 3;
+        if (w == 3) fwht_pass<3>(v, total, lo);
+        else if (w == 2) fwht_pass<2>(v, total, lo);
+        else fwht_pass<1>(v, total, lo);
+        __syncthreads();
+    }
+}
+
+template <int XT>
+__device__ __forceinline__ float ld_x(const void* p, int64_t i)
+{
+    if constexpr (XT == VQ2_DT_F32) return ((const float*)p)[i];
+    else if constexpr (XT == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// Prologue of XM 1 / 2: s_x[r * n + i] = sign[i] * f(row r)[perm[i]] for the
+// rows r of this workgroup (batch columns for XM 1, pairs for XM 2), then the
+// blockwise FWHT.  The RHT scale is applied when lanes read their slices.
+// Each thread takes 8 consecutive elements: perm and sign are read with
+// vector loads and all activation loads are issued before any is used.
+// n % 8 == 0; perm 16-byte and sign 8-byte aligned (checked on the host).
+template <int XM, int XT>
+__device__ __forceinline__ void build_x_t(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0)
+{
+    const int64_t total = (int64_t)nrows * n;
+    for (int64_t t0 = (int64_t)threadIdx.x * 8; t0 < total; t0 += (int64_t)blockDim.x * 8) {
+        const int r = (int)(t0 / n);
+        const int64_t i0 = t0 - (int64_t)r * n;
+        int64_t src[8];
+        if (a.perm) {
+            const u32x4 p0 = *(const u32x4*)(a.perm + i0);
+            const u32x4 p1 = *(const u32x4*)(a.perm + i0 + 4);
+#pragma unroll
+            for (int k = 0; k < 4; k++) { src[k] = (int32_t)p0[k]; src[4 + k] = (int32_t)p1[k]; }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) src[k] = i0 + k;
+        }
+        bool bad[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            bad[k] = (uint64_t)src[k] >= (uint64_t)n;  // not a permutation of [0, n): poison the value
+            src[k] = bad[k] ? 0 : src[k];
+        }
+        float sg[8];
+        if (a.sign) {
+            const u32x2 sv = *(const u32x2*)(a.sign + i0);
+#pragma unroll
+            for (int k = 0; k < 8; k++) sg[k] = (float)(int8_t)((sv[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) sg[k] = 1.0f;
+        }
+        float v[8];
+        if constexpr (XM == 1) {
+            const int64_t row = (int64_t)(og / a.x_pdiv) * a.x_pstride + (int64_t)(bt0 + r) * a.x_bstride;
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = ld_x<XT>(a.x, row + src[k]);
+        } else {
+            const int64_t row = ((int64_t)og * a.P + r) / a.x_pdiv * a.x_pstride;
+            float g[8], u[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) { g[k] = ld_x<XT>(a.x, row + src[k]); u[k] = ld_x<XT>(a.x, row + n + src[k]); }
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = silu_f32(g[k]) * u[k];
+        }
+        u32x4 o0, o1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o0[k] = __float_as_uint(bad[k] ? __builtin_nanf("") : v[k] * sg[k]);
+            o1[k] = __float_as_uint(bad[4 + k] ? __builtin_nanf("") : v[4 + k] * sg[4 + k]);
+        }
+        *(u32x4*)(s_x + t0) = o0;
+        *(u32x4*)(s_x + t0 + 4) = o1;
+    }
+}
+
+template <int XM>
+__device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0)
+{
+    if (a.x_dt == VQ2_DT_F32) build_x_t<XM, VQ2_DT_F32>(a, s_x, nrows, n, og, bt0);
+    else if (a.x_dt == VQ2_DT_F16) build_x_t<XM, VQ2_DT_F16>(a, s_x, nrows, n, og, bt0);
+    else build_x_t<XM, VQ2_DT_BF16>(a, s_x, nrows, n, og, bt0);
+    __syncthreads();
+    block_fwht(s_x, (int64_t)nrows * n, a.hb_log2);
+}
+
+// A lane's activation slice from the LDS activation block.
+template <int GPL, int BT>
+__device__ __forceinline__ void load_x_lds(const float* s_x, int64_t row0, int64_t rstride, int64_t g0, bool lane_ok,
+                                           int nb, float scale, float (&xs)[BT][GPL * 8])
+{
+#pragma unroll
+    for (int b = 0; b < BT; b++) {
+        const bool ok = lane_ok && b < nb;
+        const u32x4* p = (const u32x4*)(s_x + (ok ? (row0 + b) * rstride + g0 * 8 : 0));
+        const float keep = ok ? scale : 0.0f;
+#pragma unroll
+        for (int i = 0; i < GPL * 2; i++) {
+            const u32x4 v = p[i];
+#pragma unroll
+            for (int k = 0; k < 4; k++) xs[b][4 * i + k] = __uint_as_float(v[k]) * keep;
+        }
+    }
+}
+
+// Codes of row block rb for this lane (zeros and valid = false past the
+// end, for idle lanes and for rows beyond their segment).
+template <int S2, int GPL, int IT>
+__device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int rows_per_block, int wr, int wr_id,
+                                            int rpw, int sub, int64_t g0, bool lane_ok, int64_t e,
+                                            uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
+{
+    int si = 0;
+    while (si + 1 < a.nseg && rb >= a.seg[si + 1].rb_start) si++;
+    const GemvSeg& sg = a.seg[si];
+    const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+        valid[it] = rb < a.n_rowblocks && row < sg.out_rows && lane_ok;
+        const int64_t off = row * a.ng + g0;
+        if (valid[it]) {
+            load_codes16<GPL>(sg.idx0 + e * a.e_istride, off, c0[it]);
+            if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
+            if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
+        }
+    }
+}
+
+// acc[it][b] = sum over this lane's GPL groups of VQ(W)[row_it] . x_b
 template <int CBT, int S2, int GPL, int BT, int IT>
+__device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const uint32_t (&c0)[IT][GPL],
+                                          const uint32_t (&c1)[IT][GPL], const bool (&valid)[IT],
+                                          const float (&xs)[BT][GPL * 8], float (&acc)[IT][BT])
+{
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+#pragma unroll
+        for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
+        Centroid<CBT> cen[GPL];
+#pragma unroll
+        for (int q = 0; q < GPL; q++) cen[q].load(a.cb0, c0[it][q]);
+        if constexpr (S2 == VQ2_S2_U16) {
+            Centroid<CBT> cen1[GPL];
+#pragma unroll
+            for (int q = 0; q < GPL; q++) cen1[q].load(a.cb1, c1[it][q]);
+#pragma unroll
+            for (int q = 0; q < GPL; q++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float w = cen[q].get(j) + cen1[q].get(j);
+#pragma unroll
+                    for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
+                }
+        } else if constexpr (S2 == VQ2_S2_U8) {
+#pragma unroll
+            for (int q = 0; q < GPL; q++) {
+                const Centroid<CBT> c2 = lds_centroid<CBT>(s_cb1, c1[it][q]);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float w = cen[q].get(j) + c2.get(j);
+#pragma unroll
+                    for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < GPL; q++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int b = 0; b < BT; b++) acc[it][b] = fmaf(cen[q].get(j), xs[b][q * 8 + j], acc[it][b]);
+        }
+        if (!valid[it]) {
+#pragma unroll
+            for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
+        }
+    }
+
+}
+
+template <int CBT, int S2, int GPL, int BT, int IT, int XM>
 __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
 {
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
-    __shared__ uint4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
-    extern __shared__ float s_part[];
+    __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
+    extern __shared__ float s_dyn[];  // [activation block (XM != 0)] [item partials]
 
-    if constexpr (S2 == VQ2_S2_U8) {
-        const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
-        for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const uint4*)a.cb1)[i];
-        __syncthreads();
-    }
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int lpr = a.lpr, wk = a.wk;
-    const int wr = (blockDim.x >> 6) / wk;
-    const int wk_id = wave % wk, wr_id = wave / wk;
-    const int rpw = 64 / lpr;
-    const int sub = lane / lpr, col = lane % lpr;
-    const int64_t kc = (int64_t)lpr * GPL;
-    const int64_t nch = (a.ng + kc - 1) / kc;
-    const int rows_per_iter = IT * rpw * wr;
     const int og = blockIdx.y;
     const int bt0 = blockIdx.z * BT;
     const int nb = min(BT, a.batch - bt0);
-    const bool use_lds = (wk > 1) || (a.P > 1);
-    const int nfin = rows_per_iter * BT;  // finalize slots, <= blockDim.x (host-checked)
+    const int64_t n = a.ng * 8;
+    const int x_rows = XM == 2 ? a.P : (XM == 1 ? nb : 0);
+    float* s_x = s_dyn;
+    float* s_part = s_dyn + (XM == 0 ? 0 : (XM == 2 ? a.P : BT) * n);
 
-    // x stays resident across row blocks when a wave owns exactly one chunk
-    // of one pair's activation.
-    const bool x_resident = (a.P == 1) && (nch <= wk);
+    if constexpr (S2 == VQ2_S2_U8) {
+        const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
+        for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
+    }
+    if constexpr (XM != 0) build_x<XM>(a, s_x, x_rows, n, og, bt0);
+    if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lpr = a.lpr, wi = a.wi;
+    const int wr = (blockDim.x >> 6) / wi;
+    const int wi_id = wave % wi, wr_id = wave / wi;
+    const int rpw = 64 / lpr;
+    const int sub = lane / lpr, col = lane % lpr;
+    const int64_t kc = (int64_t)lpr * GPL;
+    const int nch = (int)((a.ng + kc - 1) / kc);
+    const int items = a.P * nch;
+    const int rows_per_block = IT * rpw * wr;
 
     float xs[BT][GPL * 8];
-    int64_t x_c = -1;  // chunk currently in xs
-    int x_pair = -1;
+    int cur_item = -1;
 
-    for (int64_t rb = blockIdx.x; rb < a.n_rowblocks; rb += gridDim.x) {
-        const int64_t row_base = rb * rows_per_iter;
-        float fin = 0.0f;  // combine accumulator of finalize slot threadIdx.x
-
-        for (int pj = 0; pj < a.P; pj++) {
-            const int64_t pair = (int64_t)og * a.P + pj;
-            int64_t e = 0;
-            if (a.ids) e = a.ids_i64 ? ((const int64_t*)a.ids)[pair] : (int64_t)((const int32_t*)a.ids)[pair];
-            const bool bad = a.ids && (e < 0 || e >= a.n_experts);
-            if (bad) e = 0;
-            const int16_t* I0 = a.idx0 + e * a.e_istride;
-            const void* I1 = nullptr;
-            if constexpr (S2 == VQ2_S2_U8) I1 = (const uint8_t*)a.idx1 + e * a.e_istride;
-            if constexpr (S2 == VQ2_S2_U16) I1 = (const int16_t*)a.idx1 + e * a.e_istride;
+    if (items == 1) {
+        // One work item (pair og, the whole K range) per wave: the activation
+        // slice is loaded once, and the next row block's codes are fetched
+        // before the current block's gathers so the HBM latency of the index
+        // stream overlaps the codebook gathers.
+        const int64_t pair = og;
+        bool bad;
+        const int64_t e = pair_expert(a, pair, bad);
+        const int64_t g0 = (int64_t)col * GPL;
+        const bool lane_ok = g0 < a.ng;
+        if constexpr (XM == 0) {
             const int64_t xoff = (pair / a.x_pdiv) * a.x_pstride + (int64_t)bt0 * a.x_bstride;
             const void* xb = a.x_dt == VQ2_DT_F32 ? (const void*)((const float*)a.x + xoff)
                                                   : (const void*)((const uint16_t*)a.x + xoff);
-
+            load_x<GPL, BT>(a, xb, g0, lane_ok, nb, xs);
+        } else {
+            load_x_lds<GPL, BT>(s_x, 0, n, g0, lane_ok, nb, a.xscale, xs);
+        }
+        uint32_t c0[IT][GPL], c1[IT][GPL];
+        bool valid[IT];
+        int64_t rb = blockIdx.x;
+        fetch_codes<S2, GPL, IT>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, c0, c1, valid);
+        while (rb < a.n_rowblocks) {
+            const int64_t rbn = rb + gridDim.x;
+            uint32_t n0[IT][GPL], n1[IT][GPL];
+            bool nvalid[IT];
+            fetch_codes<S2, GPL, IT>(a, rbn, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, n0, n1,
+                                     nvalid);
             float acc[IT][BT];
+            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
-                for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
-
-            for (int64_t c = wk_id; c < nch; c += wk) {
-                const int64_t g0 = c * kc + (int64_t)col * GPL;
-                if (!(x_resident && x_c == c && x_pair == (int)pair)) {
-                    load_x<GPL, BT>(a, xb, g0, nb, xs);
-                    x_c = c;
-                    x_pair = (int)pair;
-                }
-                if (bad) continue;
-                const bool full = a.vec_ok && (g0 + GPL <= a.ng);
-
-                uint32_t c0[IT][GPL], c1[IT][GPL];
-                bool valid[IT];
+                for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
+            int si = 0;
+            while (si + 1 < a.nseg && rb >= a.seg[si + 1].rb_start) si++;
+            const GemvSeg& sg = a.seg[si];
+            const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
+            if (col == 0) {
 #pragma unroll
                 for (int it = 0; it < IT; it++) {
                     const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-                    valid[it] = row < a.out_rows && g0 < a.ng;
-                    const int64_t off = row * a.ng + g0;
+                    if (row >= sg.out_rows) continue;
+                    const float sc = load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row);
 #pragma unroll
-                    for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
-                    if (valid[it]) {
-                        if (full) {
-                            load_codes16<GPL>(I0, off, c0[it]);
-                            if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)I1, off, c1[it]);
-                            if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)I1, off, c1[it]);
-                        } else {
-#pragma unroll
-                            for (int q = 0; q < GPL; q++) {
-                                if (g0 + q < a.ng) {
-                                    c0[it][q] = (uint16_t)I0[off + q];
-                                    if constexpr (S2 == VQ2_S2_U8) c1[it][q] = ((const uint8_t*)I1)[off + q];
-                                    if constexpr (S2 == VQ2_S2_U16) c1[it][q] = (uint16_t)((const int16_t*)I1)[off + q];
-                                }
-                            }
-                        }
-                    }
-                }
-
-#pragma unroll
-                for (int it = 0; it < IT; it++) {
-                    if (!valid[it]) continue;
-                    Centroid<CBT> cen[GPL];
-#pragma unroll
-                    for (int q = 0; q < GPL; q++) cen[q].load(a.cb0, c0[it][q]);
-                    if constexpr (S2 == VQ2_S2_U16) {
-                        Centroid<CBT> cen1[GPL];
-#pragma unroll
-                        for (int q = 0; q < GPL; q++) cen1[q].load(a.cb1, c1[it][q]);
-#pragma unroll
-                        for (int q = 0; q < GPL; q++) {
-                            if (!full && g0 + q >= a.ng) continue;
-#pragma unroll
-                            for (int j = 0; j < 8; j++) {
-                                const float w = cen[q].get(j) + cen1[q].get(j);
-#pragma unroll
-                                for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
-                            }
-                        }
-                    } else if constexpr (S2 == VQ2_S2_U8) {
-#pragma unroll
-                        for (int q = 0; q < GPL; q++) {
-                            if (!full && g0 + q >= a.ng) continue;
-                            const Centroid<CBT> c2 = lds_centroid<CBT>(s_cb1, c1[it][q]);
-#pragma unroll
-                            for (int j = 0; j < 8; j++) {
-                                const float w = cen[q].get(j) + c2.get(j);
-#pragma unroll
-                                for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
-                            }
-                        }
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < GPL; q++) {
-                            if (!full && g0 + q >= a.ng) continue;
-#pragma unroll
-                            for (int j = 0; j < 8; j++) {
-                                const float w = cen[q].get(j);
-#pragma unroll
-                                for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
-                            }
-                        }
+                    for (int b = 0; b < BT; b++) {
+                        float v = (acc[it][b] * sc) * a.rs;
+                        if (bad) v = __builtin_nanf("");
+                        if (b < nb)
+                            store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
+                                           v);
                     }
                 }
             }
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                valid[it] = nvalid[it];
+#pragma unroll
+                for (int q = 0; q < GPL; q++) { c0[it][q] = n0[it][q]; c1[it][q] = n1[it][q]; }
+            }
+            rb = rbn;
+        }
+        return;
+    }
 
-            // reduce row partials over the LPR lanes of each row
+    for (int64_t rbg = blockIdx.x; rbg < a.n_rowblocks; rbg += gridDim.x) {
+        int si = 0;
+        while (si + 1 < a.nseg && rbg >= a.seg[si + 1].rb_start) si++;
+        const GemvSeg& sg = a.seg[si];
+        const int64_t row_base = (rbg - sg.rb_start) * rows_per_block;
+        float fin[IT][BT];
+#pragma unroll
+        for (int it = 0; it < IT; it++)
+#pragma unroll
+            for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
+
+        for (int item = wi_id; item < items; item += wi) {
+            const int pj = item / nch, c = item - (item / nch) * nch;
+            const int64_t pair = (int64_t)og * a.P + pj;
+            bool bad;
+            const int64_t e = pair_expert(a, pair, bad);
+            const int16_t* I0 = sg.idx0 + e * a.e_istride;
+            const int64_t g0 = c * kc + (int64_t)col * GPL;
+            const bool lane_ok = g0 < a.ng;
+            if (item != cur_item) {
+                if constexpr (XM == 0) {
+                    const int64_t xoff = (pair / a.x_pdiv) * a.x_pstride + (int64_t)bt0 * a.x_bstride;
+                    const void* xb = a.x_dt == VQ2_DT_F32 ? (const void*)((const float*)a.x + xoff)
+                                                          : (const void*)((const uint16_t*)a.x + xoff);
+                    load_x<GPL, BT>(a, xb, g0, lane_ok, nb, xs);
+                } else {
+                    load_x_lds<GPL, BT>(s_x, XM == 2 ? pj : 0, n, g0, lane_ok, nb, a.xscale, xs);
+                }
+                cur_item = item;
+            }
+
+            uint32_t c0[IT][GPL], c1[IT][GPL];
+            int64_t rows[IT];
+            bool valid[IT];
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+                rows[it] = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+                valid[it] = rows[it] < sg.out_rows && lane_ok && !bad;
+                const int64_t off = rows[it] * a.ng + g0;
+                if (valid[it]) {
+                    load_codes16<GPL>(I0, off, c0[it]);
+                    if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
+                    if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
+                }
+            }
+
+            float acc[IT][BT];
+            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
+
+            // row sums over the LPR lanes; every lane of a row gets the sum
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
                 for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
 
             const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
-            if (!use_lds) {
-                if (col == 0) {
 #pragma unroll
-                    for (int it = 0; it < IT; it++) {
-                        const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-                        if (row >= a.out_rows) continue;
-                        const float s = load_as_f32(a.scale, a.s_dt, e * a.e_sstride + row);
+            for (int it = 0; it < IT; it++) {
+                const int64_t row = rows[it];
+                const float s = row < sg.out_rows ? load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row) : 0.0f;
 #pragma unroll
-                        for (int b = 0; b < BT; b++) {
-                            if (b >= nb) continue;
-                            float v = (acc[it][b] * s) * a.rs;
-                            if (bad) v = __builtin_nanf("");
-                            store_from_f32(a.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * a.y_bstride + row, v);
-                        }
-                    }
+                for (int b = 0; b < BT; b++) {
+                    float v = (acc[it][b] * s) * a.rs;
+                    if (bad) v = __builtin_nanf("");
+                    fin[it][b] = (items == 1) ? v : fmaf(pw, v, fin[it][b]);
                 }
-            } else {
-                // partials: s_part[wk_id][local_row][b]
-                if (col == 0) {
-#pragma unroll
-                    for (int it = 0; it < IT; it++) {
-                        const int lr = (it * wr + wr_id) * rpw + sub;
-#pragma unroll
-                        for (int b = 0; b < BT; b++) s_part[(wk_id * rows_per_iter + lr) * BT + b] = acc[it][b];
-                    }
-                }
-                __syncthreads();
-                if ((int)threadIdx.x < nfin) {
-                    const int lr = threadIdx.x / BT, b = threadIdx.x % BT;
-                    const int64_t row = row_base + lr;
-                    float sum = 0.0f;
-                    for (int w = 0; w < wk; w++) sum += s_part[(w * rows_per_iter + lr) * BT + b];
-                    if (row < a.out_rows) {
-                        const float s = load_as_f32(a.scale, a.s_dt, e * a.e_sstride + row);
-                        float v = (sum * s) * a.rs;
-                        if (bad) v = __builtin_nanf("");
-                        fin = (pj == 0) ? pw * v : fmaf(pw, v, fin);
-                    }
-                }
-                __syncthreads();
             }
         }
 
-        if (use_lds && (int)threadIdx.x < nfin) {
-            const int lr = threadIdx.x / BT, b = threadIdx.x % BT;
-            const int64_t row = row_base + lr;
-            if (row < a.out_rows && b < nb) {
-                // P == 1 keeps the plain (acc * s) * rs value (pw == 1)
-                store_from_f32(a.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * a.y_bstride + row, fin);
+        if (items == 1) {
+            if (col == 0) {
+#pragma unroll
+                for (int it = 0; it < IT; it++) {
+                    const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+                    if (row >= sg.out_rows) continue;
+#pragma unroll
+                    for (int b = 0; b < BT; b++)
+                        if (b < nb)
+                            store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
+                                           fin[it][b]);
+                }
             }
+        } else {
+            // fixed-order reduction of the WI item waves through LDS
+            if (col == 0) {
+#pragma unroll
+                for (int it = 0; it < IT; it++) {
+                    const int lr = (it * wr + wr_id) * rpw + sub;
+#pragma unroll
+                    for (int b = 0; b < BT; b++) s_part[(wi_id * rows_per_block + lr) * BT + b] = fin[it][b];
+                }
+            }
+            __syncthreads();
+            for (int t = threadIdx.x; t < rows_per_block * BT; t += blockDim.x) {
+                const int lr = t / BT, b = t % BT;
+                const int64_t row = row_base + lr;
+                float sum = s_part[lr * BT + b];
+                for (int w = 1; w < wi; w++) sum += s_part[(w * rows_per_block + lr) * BT + b];
+                if (row < sg.out_rows && b < nb)
+                    store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row, sum);
+            }
+            __syncthreads();
         }
+    }
+}
+
+// Generic path for shapes the vector kernel does not take (activations are
+// pre-rotated, XM 0 only): one thread per (output group, batch column, row)
+// of one segment, scalar loads, same arithmetic.
+template <int CBT>
+__global__ void __launch_bounds__(256) vq_gemv_generic(const GemvArgs a, int s2, int si)
+{
+    const GemvSeg& sg = a.seg[si];
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < a.batch * sg.out_rows;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t og = blockIdx.y;
+        const int64_t b = t / sg.out_rows, row = t - (t / sg.out_rows) * sg.out_rows;
+        float out = 0.0f;
+        for (int pj = 0; pj < a.P; pj++) {
+            const int64_t pair = og * a.P + pj;
+            bool bad;
+            const int64_t e = pair_expert(a, pair, bad);
+            const int64_t xoff = (pair / a.x_pdiv) * a.x_pstride + b * a.x_bstride;
+            float acc = 0.0f;
+            if (!bad) {
+                for (int64_t g = 0; g < a.ng; g++) {
+                    const int64_t i = e * a.e_istride + row * a.ng + g;
+                    const uint32_t c0 = (uint16_t)sg.idx0[i];
+                    uint32_t c1 = 0;
+                    if (s2 == VQ2_S2_U8) c1 = ((const uint8_t*)sg.idx1)[i];
+                    if (s2 == VQ2_S2_U16) c1 = (uint16_t)((const int16_t*)sg.idx1)[i];
+                    for (int j = 0; j < 8; j++) {
+                        float w = load_as_f32(a.cb0, CBT, (int64_t)c0 * 8 + j);
+                        if (s2 != VQ2_S2_NONE) w += load_as_f32(a.cb1, CBT, (int64_t)c1 * 8 + j);
+                        acc = fmaf(w, load_as_f32(a.x, a.x_dt, xoff + g * 8 + j), acc);
+                    }
+                }
+            }
+            const float s = load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row);
+            float v = (acc * s) * a.rs;
+            if (bad) v = __builtin_nanf("");
+            const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
+            out = (a.P == 1) ? v : fmaf(pw, v, out);
+        }
+        store_from_f32(sg.y, a.y_dt, og * a.y_ostride + b * sg.y_bstride + row, out);
     }
 }
 
 // ------------------------------------------------------------------- host
 struct GemvPlan {
-    int gpl, bt, lpr, wk, wr, it;
-    int64_t rows_per_iter, n_rowblocks;
+    int gpl, bt, lpr, wi, wr, it, xm, num_cu;
+    double occ_scale;  // multiplier on the resident-workgroup count
+    int64_t rows_per_block, n_rowblocks;
     int threads;
 };
+
+// Resident workgroups per CU of a kernel at a block size / LDS size (cached).
+int resident_blocks_per_cu(const void* fn, int threads, size_t shm);
+
+// Persistent grid: as many row-block workers as stay resident on the GPU.
+inline dim3 persistent_grid(const void* fn, const GemvPlan& p, dim3 grid, size_t shm)
+{
+    const int64_t resident = (int64_t)resident_blocks_per_cu(fn, p.threads, shm) * p.num_cu * p.occ_scale;
+    const int64_t per_x = (resident + (int64_t)grid.y * grid.z - 1) / ((int64_t)grid.y * grid.z);
+    int64_t gx = per_x < 1 ? 1 : per_x;
+    if (gx > p.n_rowblocks) gx = p.n_rowblocks;
+    grid.x = (unsigned)gx;
+    return grid;
+}
+
+template <int CBT, int S2, int GPL, int BT, int IT, int XM>
+inline hipError_t launch_one(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
+{
+    const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM>;
+    grid = persistent_grid(fn, p, grid, shm);
+    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM>), grid, dim3(p.threads), shm, st, a);
+    return hipGetLastError();
+}
+
+template <int CBT, int S2, int GPL, int BT, int IT>
+inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
+{
+    switch (p.xm) {
+    case 1:
+        if constexpr (BT <= 2) return launch_one<CBT, S2, GPL, BT, IT, 1>(a, p, grid, shm, st);
+        else return hipErrorInvalidValue;
+    case 2:
+        if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
+        else return hipErrorInvalidValue;
+    default: return launch_one<CBT, S2, GPL, BT, IT, 0>(a, p, grid, shm, st);
+    }
+}
 
 template <int CBT, int S2, int GPL, int BT>
 inline hipError_t launch_it(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
 {
     switch (p.it) {
-    case 4: hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, 4>), grid, dim3(p.threads), shm, st, a); break;
-    case 2: hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, 2>), grid, dim3(p.threads), shm, st, a); break;
-    default: hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, 1>), grid, dim3(p.threads), shm, st, a); break;
+    case 4: return launch_xm<CBT, S2, GPL, BT, 4>(a, p, grid, shm, st);
+    case 2: return launch_xm<CBT, S2, GPL, BT, 2>(a, p, grid, shm, st);
+    default: return launch_xm<CBT, S2, GPL, BT, 1>(a, p, grid, shm, st);
     }
-    return hipGetLastError();
 }
 
 template <int CBT, int S2>
@@ -465,9 +776,17 @@ inline hipError_t launch_s2(int s2, const GemvArgs& a, const GemvPlan& p, dim3 g
     }
 }
 
+template <int CBT>
+inline hipError_t launch_generic(int s2, int si, const GemvArgs& a, dim3 grid, hipStream_t st)
+{
+    hipLaunchKernelGGL((vq_gemv_generic<CBT>), grid, dim3(256), 0, st, a, s2, si);
+    return hipGetLastError();
+}
+
 // per-codebook-dtype dispatchers (one translation unit each)
 hipError_t gemv_dispatch_f16(int s2, const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st);
 hipError_t gemv_dispatch_bf16(int s2, const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st);
 hipError_t gemv_dispatch_f32(int s2, const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st);
+hipError_t gemv_generic_dispatch(int cb_dt, int s2, int si, const GemvArgs& a, dim3 grid, hipStream_t st);
 
 }  // namespace vq2

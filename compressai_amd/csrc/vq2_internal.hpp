@@ -16,6 +16,16 @@ void clear_error();
 // Compute-unit count of the current device (cached per device).
 int device_cu_count();
 
+// One matrix of a GEMV launch (segments of one launch share the activation).
+struct GemvSegCall {
+    const int16_t* idx0;
+    const void* idx1;
+    const void* scale;
+    void* y;
+    int64_t out_rows;
+    int64_t y_bstride;  // elements between batch columns of y
+};
+
 // One launch of the shared GEMV kernel body (dense / grouped / combine).
 struct GemvCall {
     const void* x;
@@ -23,13 +33,10 @@ struct GemvCall {
     int64_t x_bstride;  // elements between batch columns of one x block
     int64_t x_pstride;  // elements between x blocks
     int x_pdiv;         // pair p reads x block p / x_pdiv
-    const int16_t* idx0;
-    const void* idx1;
     int s2;
     const void* cb0;
     const void* cb1;
     int cb_dt;
-    const void* scale;
     int s_dt;
     const void* ids;  // null: expert 0 for every pair
     int ids_i64;
@@ -37,15 +44,21 @@ struct GemvCall {
     const float* pair_w;  // combine weights (P > 1)
     int P;                // pairs per output group
     int64_t n_out_groups; // grid.y
-    void* y;
     int y_dt;
-    int64_t y_bstride;
     int64_t y_ostride;
-    int64_t out_rows;
     int64_t ng;
     int64_t batch;
     float rs;
     void* stream;
+    int nseg;
+    GemvSegCall seg[4];
+    // activation prologue: 0 = x is the rotated activation; 1 = rotate x in
+    // the kernel; 2 = rotate silu(gate) * up of each pair in the kernel
+    int xm;
+    const int32_t* perm;
+    const int8_t* sign;
+    int64_t hb;
+    float xscale;
 };
 
 int gemv_launch(const GemvCall& c);

@@ -81,95 +81,138 @@ int argmax_launch(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* 
 }
 
 // ------------------------------------------------------------------ router
-// One workgroup per token: softmax over the logits in fp32, k rounds of
-// (max, lowest index) selection, renormalisation over the selected
-// probabilities, plus the sigmoid shared-expert gate.
+// One wave per token.  Logits live in registers (expert e = j*64 + lane),
+// softmax in fp32, then k rounds of a wave-wide (max probability, lowest id)
+// reduction; lane r keeps round r's probability for the renormalisation.
+// The shared-expert gate dot product is loaded alongside the logits.
 constexpr int ROUTER_MAX_E = 1024;
+constexpr int ROUTER_PER_LANE = ROUTER_MAX_E / 64;
 
-__global__ void __launch_bounds__(256) router_kernel(const void* logits, int l_dt, int64_t n_e, int k, const void* h,
-                                                     int h_dt, int64_t hidden, const void* gate, int g_dt,
-                                                     int64_t shared_id, int32_t* ids, float* w)
+__device__ __forceinline__ float wave_max(float v)
 {
-    __shared__ float s_p[ROUTER_MAX_E];
-    __shared__ float s_red[4];
-    __shared__ int s_redi[4];
-    __shared__ float s_sel_p[32];
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+template <int DT>
+__device__ __forceinline__ float ld_t(const void* p, int64_t i)
+{
+    if constexpr (DT == VQ2_DT_F32) return ((const float*)p)[i];
+    else if constexpr (DT == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+template <int LT>
+__device__ __forceinline__ void router_load_logits(const void* logits, int64_t t, int64_t n_e, int lane,
+                                                   float (&p)[ROUTER_PER_LANE])
+{
+#pragma unroll
+    for (int j = 0; j < ROUTER_PER_LANE; j++) {
+        const int e = j * 64 + lane;
+        p[j] = ld_t<LT>(logits, t * n_e + (e < n_e ? e : 0));
+    }
+#pragma unroll
+    for (int j = 0; j < ROUTER_PER_LANE; j++)
+        if (j * 64 + lane >= n_e) p[j] = -INFINITY;
+}
+
+// gate . h_t: 16 gate and 16 h loads in flight per lane per chunk
+template <int GT, int HT>
+__device__ __forceinline__ float router_gate_dot(const void* gate, const void* h, int64_t t, int64_t hidden, int lane)
+{
+    float d = 0.0f;
+    for (int64_t i0 = 0; i0 < hidden; i0 += 16 * 64) {
+        float g[16], x[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int64_t i = i0 + u * 64 + lane;
+            const int64_t ic = i < hidden ? i : 0;
+            g[u] = ld_t<GT>(gate, ic);
+            x[u] = ld_t<HT>(h, t * hidden + ic);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (i0 + u * 64 + lane < hidden) d = fmaf(g[u], x[u], d);
+    }
+    return d;
+}
+
+__device__ __forceinline__ float router_gate_dispatch(const void* gate, int g_dt, const void* h, int h_dt, int64_t t,
+                                                      int64_t hidden, int lane)
+{
+    if (g_dt == VQ2_DT_F16 && h_dt == VQ2_DT_F16) return router_gate_dot<VQ2_DT_F16, VQ2_DT_F16>(gate, h, t, hidden, lane);
+    if (g_dt == VQ2_DT_BF16 && h_dt == VQ2_DT_BF16) return router_gate_dot<VQ2_DT_BF16, VQ2_DT_BF16>(gate, h, t, hidden, lane);
+    if (g_dt == VQ2_DT_F32 && h_dt == VQ2_DT_F32) return router_gate_dot<VQ2_DT_F32, VQ2_DT_F32>(gate, h, t, hidden, lane);
+    float d = 0.0f;
+    for (int64_t i = lane; i < hidden; i += 64) d = fmaf(load_as_f32(gate, g_dt, i), load_as_f32(h, h_dt, t * hidden + i), d);
+    return d;
+}
+
+__global__ void __launch_bounds__(64) router_kernel(const void* logits, int l_dt, int64_t n_e, int k, const void* h,
+                                                    int h_dt, int64_t hidden, const void* gate, int g_dt,
+                                                    int64_t shared_id, int32_t* ids, float* w)
+{
     const int64_t t = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x;
     const int row = k + (shared_id >= 0 ? 1 : 0);
+    float p[ROUTER_PER_LANE];
+    if (l_dt == VQ2_DT_F16)
+        router_load_logits<VQ2_DT_F16>(logits, t, n_e, lane, p);
+    else if (l_dt == VQ2_DT_BF16)
+        router_load_logits<VQ2_DT_BF16>(logits, t, n_e, lane, p);
+    else
+        router_load_logits<VQ2_DT_F32>(logits, t, n_e, lane, p);
+    const float d = shared_id >= 0 ? router_gate_dispatch(gate, g_dt, h, h_dt, t, hidden, lane) : 0.0f;
 
-    // max logit
     float m = -INFINITY;
-    for (int64_t e = tid; e < n_e; e += blockDim.x) {
-        const float v = load_as_f32(logits, l_dt, t * n_e + e);
-        s_p[e] = v;
-        m = fmaxf(m, v);
-    }
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) s_red[wv] = m;
-    __syncthreads();
-    m = s_red[0];
-    for (int i = 1; i < nw; i++) m = fmaxf(m, s_red[i]);
-    __syncthreads();
-    // exp and sum
+#pragma unroll
+    for (int j = 0; j < ROUTER_PER_LANE; j++) m = fmaxf(m, p[j]);
+    m = wave_max(m);
     float sum = 0.0f;
-    for (int64_t e = tid; e < n_e; e += blockDim.x) {
-        const float p = __expf(s_p[e] - m);
-        s_p[e] = p;
-        sum += p;
+#pragma unroll
+    for (int j = 0; j < ROUTER_PER_LANE; j++) {
+        p[j] = (j * 64 + lane) < n_e ? __expf(p[j] - m) : 0.0f;
+        sum += p[j];
     }
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) s_red[wv] = sum;
-    __syncthreads();
-    sum = 0.0f;
-    for (int i = 0; i < nw; i++) sum += s_red[i];
-    __syncthreads();
-    for (int64_t e = tid; e < n_e; e += blockDim.x) s_p[e] = s_p[e] / sum;
-    __syncthreads();
+    sum = wave_sum(sum);
+#pragma unroll
+    for (int j = 0; j < ROUTER_PER_LANE; j++) p[j] = (j * 64 + lane) < n_e ? p[j] / sum : -1.0f;
 
-    // top-k selection: k rounds of (max prob, lowest id)
-    for (int j = 0; j < k; j++) {
+    float mine = 0.0f;  // lane r: probability selected in round r
+    int my_id = 0;
+    for (int r = 0; r < k; r++) {
         float bv = -1.0f;
         int bi = 0x7FFFFFFF;
-        for (int64_t e = tid; e < n_e; e += blockDim.x) {
-            const float p = s_p[e];
-            if (p > bv || (p == bv && (int)e < bi)) { bv = p; bi = (int)e; }
+#pragma unroll
+        for (int j = 0; j < ROUTER_PER_LANE; j++) {
+            const int e = j * 64 + lane;
+            if (p[j] > bv || (p[j] == bv && e < bi)) { bv = p[j]; bi = e; }
         }
         for (int off = 32; off > 0; off >>= 1) {
             const float ov = __shfl_xor(bv, off);
             const int oi = __shfl_xor(bi, off);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if (lane == 0) { s_red[wv] = bv; s_redi[wv] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            for (int i = 1; i < nw; i++)
-                if (s_red[i] > bv || (s_red[i] == bv && s_redi[i] < bi)) { bv = s_red[i]; bi = s_redi[i]; }
-            s_sel_p[j] = bv;
-            ids[t * row + j] = bi;
-            s_p[bi] = -2.0f;  // never selected again
-        }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ROUTER_PER_LANE; j++)
+            if (j * 64 + lane == bi) p[j] = -2.0f;  // never selected again
+        if (lane == r) { mine = bv; my_id = bi; }
     }
-    if (tid == 0) {
-        float tot = 0.0f;
-        for (int j = 0; j < k; j++) tot += s_sel_p[j];
-        for (int j = 0; j < k; j++) w[t * row + j] = s_sel_p[j] / tot;
+    const float tot = wave_sum(lane < k ? mine : 0.0f);
+    if (lane < k) {
+        ids[t * row + lane] = my_id;
+        w[t * row + lane] = mine / tot;
     }
-    // shared-expert gate: sigmoid(gate . h_t)
     if (shared_id >= 0) {
-        float d = 0.0f;
-        for (int64_t i = tid; i < hidden; i += blockDim.x)
-            d += load_as_f32(gate, g_dt, i) * load_as_f32(h, h_dt, t * hidden + i);
-        for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
-        __syncthreads();
-        if (lane == 0) s_red[wv] = d;
-        __syncthreads();
-        if (tid == 0) {
-            float tot = 0.0f;
-            for (int i = 0; i < nw; i++) tot += s_red[i];
+        const float dd = wave_sum(d);
+        if (lane == 0) {
             ids[t * row + k] = (int32_t)shared_id;
-            w[t * row + k] = 1.0f / (1.0f + __expf(-tot));
+            w[t * row + k] = 1.0f / (1.0f + __expf(-dd));
         }
     }
 }
@@ -182,7 +225,7 @@ int router_launch(const void* logits, int l_dt, int64_t tokens, int64_t n_expert
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 router: n_experts=%lld not in [1, %d]", (long long)n_experts, ROUTER_MAX_E);
     if (k <= 0 || k > 32 || k > n_experts) return set_error(VQ2_ERR_ARG, "vq2 router: k=%d out of range", k);
     if (tokens > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 router: too many tokens");
-    hipLaunchKernelGGL(router_kernel, dim3((unsigned)tokens), dim3(256), 0, (hipStream_t)stream, logits, l_dt,
+    hipLaunchKernelGGL(router_kernel, dim3((unsigned)tokens), dim3(64), 0, (hipStream_t)stream, logits, l_dt,
                        n_experts, k, h, h_dt, hidden, gate, g_dt, shared_id, ids, w);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_hip_error(err, "vq2 router launch");

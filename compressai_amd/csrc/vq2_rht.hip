@@ -37,9 +37,10 @@ struct RhtArgs {
 template <int L>
 struct RhtShape {
     static constexpr int HB = 1 << L;
-    static constexpr int V = HB <= 128 ? 2 : (HB / 64 < 32 ? HB / 64 : 32);
+    // threads per block: 64 for hb <= 1024, up to 256 for the largest blocks
+    static constexpr int T = HB / 16 > 256 ? 256 : (HB / 16 > (HB / 2 < 64 ? HB / 2 : 64) ? HB / 16 : (HB / 2 < 64 ? HB / 2 : 64));
+    static constexpr int V = HB / T;
     static constexpr int VB = V == 2 ? 1 : V == 4 ? 2 : V == 8 ? 3 : V == 16 ? 4 : 5;
-    static constexpr int T = HB / V;
     static constexpr int NP = (L + VB - 1) / VB;
     static constexpr int width(int p) { return L / NP + (p < L % NP ? 1 : 0); }
     static constexpr int lo(int p)
@@ -48,6 +49,7 @@ struct RhtShape {
         for (int i = 0; i < p; i++) s += width(i);
         return s;
     }
+    static_assert(T * V == HB && (1 << VB) == V, "bad RHT shape");
 };
 
 // element index of register i of thread tid in the layout whose butterfly
@@ -99,6 +101,57 @@ __device__ __forceinline__ void rht_passes(float (&v)[RhtShape<L>::V], float* ld
     }
 }
 
+template <int XT>
+__device__ __forceinline__ float ld_elem(const void* p, int64_t i)
+{
+    if constexpr (XT == VQ2_DT_F32) return ((const float*)p)[i];
+    else if constexpr (XT == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// Pass-0 load: thread tid holds elements tid*V + i.  Every address is
+// computed first and all loads are issued before any value is used.
+template <int V, int XT>
+__device__ __forceinline__ void rht_load(const RhtArgs& a, int64_t b, int64_t e0, float (&v)[V])
+{
+    const char* xrow = (const char*)a.x + (size_t)(b * a.x_stride) * (XT == VQ2_DT_F32 ? 4 : 2);
+    if (a.inverse || (!a.perm && !a.swiglu)) {
+        float raw[V];
+#pragma unroll
+        for (int i = 0; i < V; i++) raw[i] = ld_elem<XT>(xrow, e0 + i);
+        int8_t sg[V];
+#pragma unroll
+        for (int i = 0; i < V; i++) sg[i] = (!a.inverse && a.sign) ? a.sign[e0 + i] : (int8_t)1;
+#pragma unroll
+        for (int i = 0; i < V; i++) v[i] = raw[i] * (float)sg[i];
+        return;
+    }
+    int64_t src[V];
+    bool bad[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int64_t s0 = a.perm ? (int64_t)a.perm[e0 + i] : e0 + i;
+        bad[i] = (uint64_t)s0 >= (uint64_t)a.n;  // not a permutation of [0, n): poison, never read out of bounds
+        src[i] = bad[i] ? 0 : s0;
+    }
+    float g[V], u[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) g[i] = ld_elem<XT>(xrow, src[i]);
+    if (a.swiglu) {
+#pragma unroll
+        for (int i = 0; i < V; i++) u[i] = ld_elem<XT>(xrow, a.inter + src[i]);
+    }
+    int8_t sg[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) sg[i] = a.sign ? a.sign[e0 + i] : (int8_t)1;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        float val = a.swiglu ? silu_f32(g[i]) * u[i] : g[i];
+        val *= (float)sg[i];
+        v[i] = bad[i] ? __builtin_nanf("") : val;
+    }
+}
+
 template <int L>
 __global__ void __launch_bounds__(256) rht_kernel(const RhtArgs a)
 {
@@ -109,44 +162,53 @@ __global__ void __launch_bounds__(256) rht_kernel(const RhtArgs a)
     const int64_t b = blockIdx.y;
     float v[S::V];
 
-    // pass-0 layout: thread tid holds elements tid*V + i
-#pragma unroll
-    for (int i = 0; i < S::V; i++) {
-        const int64_t gi = base + tid * S::V + i;
-        float val;
-        if (a.inverse) {
-            val = load_as_f32(a.x, a.x_dt, b * a.x_stride + gi);
-        } else {
-            const int64_t src = a.perm ? (int64_t)a.perm[gi] : gi;
-            if ((uint64_t)src >= (uint64_t)a.n) {
-                val = __builtin_nanf("");  // not a permutation of [0, n): poison, never read out of bounds
-            } else if (a.swiglu) {
-                const float g = load_as_f32(a.x, a.x_dt, b * a.x_stride + src);
-                const float u = load_as_f32(a.x, a.x_dt, b * a.x_stride + a.inter + src);
-                val = silu_f32(g) * u;
-            } else {
-                val = load_as_f32(a.x, a.x_dt, b * a.x_stride + src);
-            }
-            if (a.sign) val *= (float)a.sign[gi];
-        }
-        v[i] = val;
-    }
+    const int64_t e0 = base + (int64_t)tid * S::V;
+    if (a.x_dt == VQ2_DT_F32)
+        rht_load<S::V, VQ2_DT_F32>(a, b, e0, v);
+    else if (a.x_dt == VQ2_DT_F16)
+        rht_load<S::V, VQ2_DT_F16>(a, b, e0, v);
+    else
+        rht_load<S::V, VQ2_DT_BF16>(a, b, e0, v);
 
     rht_passes<L, 0>(v, lds, tid);
 
     constexpr int WL = S::width(S::NP - 1);
     constexpr int LOL = S::lo(S::NP - 1);
+    int64_t dst[S::V];
+    float val[S::V];
 #pragma unroll
     for (int i = 0; i < S::V; i++) {
-        const int64_t gi = base + elem_of<S::VB, WL, LOL>(tid, i);
-        float val = v[i] * a.scale;
-        int64_t dst = gi;
-        if (a.inverse) {
-            if (a.sign) val *= (float)a.sign[gi];
-            if (a.perm) dst = a.perm[gi];
-            if ((uint64_t)dst >= (uint64_t)a.n) continue;  // bad permutation entry: drop the store
+        dst[i] = base + elem_of<S::VB, WL, LOL>(tid, i);
+        val[i] = v[i] * a.scale;
+    }
+    if (a.inverse) {
+        // z[i] *= sign[i]; y[perm[i]] = z[i]  (loads first, then the scatter)
+        int8_t sg[S::V];
+        int64_t pd[S::V];
+#pragma unroll
+        for (int i = 0; i < S::V; i++) {
+            sg[i] = a.sign ? a.sign[dst[i]] : (int8_t)1;
+            pd[i] = a.perm ? (int64_t)a.perm[dst[i]] : dst[i];
         }
-        store_from_f32(a.y, a.y_dt, b * a.y_stride + dst, val);
+#pragma unroll
+        for (int i = 0; i < S::V; i++) {
+            val[i] *= (float)sg[i];
+            dst[i] = (uint64_t)pd[i] < (uint64_t)a.n ? pd[i] : -1;  // bad permutation entry: drop the store
+        }
+    }
+    const int64_t yrow = b * a.y_stride;
+    if (a.y_dt == VQ2_DT_F32) {
+#pragma unroll
+        for (int i = 0; i < S::V; i++)
+            if (dst[i] >= 0) ((float*)a.y)[yrow + dst[i]] = val[i];
+    } else if (a.y_dt == VQ2_DT_F16) {
+#pragma unroll
+        for (int i = 0; i < S::V; i++)
+            if (dst[i] >= 0) ((uint16_t*)a.y)[yrow + dst[i]] = f32_to_f16_bits(val[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::V; i++)
+            if (dst[i] >= 0) ((uint16_t*)a.y)[yrow + dst[i]] = f32_to_bf16_bits(val[i]);
     }
 }
 

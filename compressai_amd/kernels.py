@@ -34,7 +34,8 @@ from ._lib import Vq2Error
 __all__ = [
     "HAVE_TRITON", "FUSED_KERNELS_ENABLED", "set_fused_kernels_enabled",
     "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
-    "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine",
+    "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine", "vq_moe_grouped",
+    "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine",
     "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
     "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
     "optimize_deltanet_layers", "Vq2Error",
@@ -197,6 +198,53 @@ def vq_gemv_16_16(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torc
     return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
 
 
+def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=None, rs=1.0, *,
+                out_dtype=torch.float32, ys=None):
+    """Rotate x with the RHT and multiply by up to 4 VQ matrices in one
+    launch (the q/k/v or gate/up fusion of a decoder layer).
+    x [n] or [B, n] (B <= 2); mats: list of (i0, i1 or None, scale, out_rows)
+    sharing one cfg.  Returns the list of outputs ([out] or [B, out])."""
+    dev = _dev(x, cb0, cb1, perm, sign)
+    n = int(n)
+    x2 = _contig(x, "x").reshape(-1, n)
+    B = x2.shape[0]
+    if not 1 <= len(mats) <= 4:
+        raise Vq2Error("vq_gemv_rht: 1..4 matrices per launch")
+    s2 = _lib.S2_NONE
+    if mats[0][1] is not None:
+        s2 = _lib.S2_U8 if mats[0][1].dtype == torch.uint8 else _lib.S2_U16
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != n):
+        raise Vq2Error("perm must be int32 [n]")
+    if sign is not None and (sign.dtype != torch.int8 or sign.numel() != n):
+        raise Vq2Error("sign must be int8 [n]")
+    segs = (_lib.Seg * len(mats))()
+    outs = []
+    for k, (i0, i1, scale, out_rows) in enumerate(mats):
+        _dev(i0, i1, scale)
+        i0 = _idx16(i0, "i0")
+        if i1 is not None and i1.dtype != torch.uint8:
+            i1 = _idx16(i1, "i1")
+        if (i1 is None) != (s2 == _lib.S2_NONE):
+            raise Vq2Error("vq_gemv_rht: all matrices of a launch share one cfg")
+        if i0.numel() != int(out_rows) * (n // 8) or scale.numel() != int(out_rows):
+            raise Vq2Error("vq_gemv_rht: matrix shape does not match out_rows x n")
+        _contig(scale, "scale")
+        if i1 is not None:
+            _contig(i1, "i1")
+        y = ys[k] if ys is not None else torch.empty((B, int(out_rows)) if x.dim() == 2 else (int(out_rows),),
+                                                      dtype=out_dtype, device=dev)
+        _contig(y, "y")
+        segs[k] = _lib.Seg(_p(i0), _p(i1), _p(scale), _p(y), int(out_rows), int(out_rows))
+        outs.append(y)
+    if scale.dtype != mats[0][2].dtype or any(o.dtype != outs[0].dtype for o in outs):
+        raise Vq2Error("vq_gemv_rht: scales and outputs of a launch share a dtype")
+    sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
+    _lib.call("vq2_gemv_rht", _p(x2), _dt(x2, "x"), B, n, _p(perm), _p(sign), int(hb), sc, len(mats), segs,
+              s2, _p(_contig(cb0, "cb0")), _p(cb1.contiguous()) if cb1 is not None else None, _dt(cb0, "cb0"),
+              _dt(mats[0][2], "scale"), _dt(outs[0], "y"), n, float(rs), _stream(dev))
+    return outs
+
+
 # -------------------------------------------------------------- grouped MoE
 def _moe_checks(pool, scale, OUT, NG, what):
     pool = _idx16(pool, what)
@@ -266,6 +314,59 @@ def vq_moe_grouped(x, ids, pool, cb16, pool_scale, y_out, OUT, NG, rs=1.0, pairs
               ids_dt, K, _p(pool), pool.shape[0], _p(cb16), _dt(cb16, "cb16"), _p(pool_scale),
               _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
     return y_out
+
+
+def vq_moe_gate_up_rht(h, ids, pool, cb16, pool_scale, y_out, OUT, NG, perm=None, sign=None, hb=2048,
+                       rht_scale=None, rs=1.0):
+    """Grouped gate_up with the activation RHT fused: token t = row of h
+    [T, NG*8], experts ids [T, P]; y_out [T*P, >=OUT]."""
+    dev = _dev(h, ids, pool, cb16, pool_scale, y_out, perm, sign)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(pool, pool_scale, OUT, NG, "pool")
+    ids2, ids_dt = _ids(ids)
+    if ids2.dim() != 2:
+        raise Vq2Error("ids must be [T, P]")
+    T, P = ids2.shape
+    hh = _contig(h, "h").reshape(-1, NG * 8)
+    if hh.shape[0] != T:
+        raise Vq2Error("h must be [T, NG*8]")
+    y2 = y_out.reshape(-1, y_out.shape[-1])
+    if y2.shape[0] < T * P or y2.shape[1] < OUT or y2.stride(1) != 1:
+        raise Vq2Error("y_out must be [>=T*P, >=OUT] with unit column stride")
+    sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
+    _lib.call("vq2_moe_gate_up_rht", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc, _p(ids2), ids_dt, P,
+              _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"), _p(pool_scale),
+              _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
+    return y_out
+
+
+def vq_moe_down_swiglu_combine(gu, ids, w, down_idx, cb16, down_scale, OUT, NG, perm=None, sign=None, hb=None,
+                               rht_scale=None, rs=1.0, out=None, out_dtype=torch.float32):
+    """silu(gate)*up -> RHT -> grouped down -> weighted combine, one launch.
+    gu [T*P, >=2*NG*8] (gate | up), ids [T, P], w fp32 [T, P] -> out [T, OUT]."""
+    dev = _dev(gu, ids, w, down_idx, cb16, down_scale, out, perm, sign)
+    OUT, NG = int(OUT), int(NG)
+    pool = _moe_checks(down_idx, down_scale, OUT, NG, "down_idx")
+    ids2, ids_dt = _ids(ids)
+    if ids2.dim() != 2:
+        raise Vq2Error("ids must be [T, P]")
+    T, P = ids2.shape
+    if w.dtype != torch.float32 or w.numel() != T * P:
+        raise Vq2Error("w must be float32 [T, P]")
+    _contig(w, "w")
+    g2 = gu.reshape(-1, gu.shape[-1])
+    if g2.shape[0] != T * P or g2.shape[1] < 2 * NG * 8 or g2.stride(1) != 1:
+        raise Vq2Error("gu must be [T*P, >=2*NG*8] with unit column stride")
+    hb = NG * 8 if hb is None else int(hb)
+    sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
+    if out is None:
+        out = torch.empty((T, OUT), dtype=out_dtype, device=dev)
+    _contig(out, "out")
+    _lib.call("vq2_moe_down_swiglu_combine", _p(g2), _dt(g2, "gu"), g2.stride(0), _p(perm), _p(sign), hb, sc,
+              _p(ids2), ids_dt, _p(w), T, P, _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"),
+              _p(down_scale), _dt(down_scale, "scale"), _p(out), _dt(out, "out"), OUT, OUT, NG, float(rs),
+              _stream(dev))
+    return out
 
 
 def vq_moe_down_combine(act_r, ids, w, down_idx, cb16, down_scale, out=None, OUT=2048, NG=64, rs=1.0,

@@ -11,16 +11,17 @@ returns ``[T, H]``, computing per token t and expert e = topk_idx[t, k]
     out_t = sum_k w[t, k] * VQ(down[e]) act
 
 (vq2/paged_runtime.py:495-510).  Instead of the reference's per-token Python
-loop (load_and_test_full_35b.py:75-95) every token and expert goes into one
-launch per stage: RHT -> grouped gate_up -> fused SwiGLU+RHT -> grouped down
-with the weighted combine in the epilogue.  Expert ids are read on the device:
-no ``.tolist()`` and no host synchronisation.
+loop (load_and_test_full_35b.py:75-95) every token and expert goes into two
+launches: grouped gate_up with the H-point RHT built in each workgroup's LDS,
+then SwiGLU + I-point RHT (again in LDS) + grouped down + weighted combine.
+Expert ids are read on the device: no ``.tolist()`` and no host
+synchronisation.
 
 ``MoELayer`` adds the router (softmax -> top-k -> renormalise on given
 logits) and the shared expert with its sigmoid gate (transformers 5.15.0
 ``Qwen3_5MoeTopKRouter`` / ``Qwen3_5MoeSparseMoeBlock``), the shared expert
-living in the same pool at id ``n_routed``.  The whole layer is five
-launches and no host synchronisation.
+living in the same pool at id ``n_routed``.  The whole layer is three
+launches (router, gate_up, down) and no host synchronisation.
 
 Intermediates are fp32 by default (the parity contract); ``act_dtype`` may
 select bf16 to follow the reference's cast points instead.
@@ -56,27 +57,28 @@ class ResidentMoEExperts(nn.Module):
         self.act_dtype = act_dtype
         self.out_dtype = out_dtype
 
-    def experts(self, xr, ids, w, out=None):
-        """xr [T, H] (rotated), ids [T, P] int32/int64, w fp32 [T, P] -> [T, H]."""
+    def experts(self, h, ids, w, out=None):
+        """h [T, H] (unrotated hidden states), ids [T, P] int32/int64,
+        w fp32 [T, P] -> [T, H].  Two launches: gate_up with the H-point RHT
+        fused, then SwiGLU + I-point RHT + down + weighted combine."""
         T, P = ids.shape
         I = self.intermediate_dim
-        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=xr.device)
-        K.vq_moe_grouped(xr, ids, self.gate_up_idx, self.cb16, self.gate_up_scale, y_gu, OUT=2 * I,
-                         NG=self.hidden_dim // 8, pairs_per_x=P)
-        act_r = K.vq_swiglu_rht(y_gu, I, self.rot_i._perm32, self.rot_i._sign8, self.rot_i.hb,
-                                self.rot_i.scale, out_dtype=self.act_dtype)
-        return K.vq_moe_down_combine(act_r, ids, w, self.down_idx, self.cb16, self.down_scale, out=out,
-                                     OUT=self.hidden_dim, NG=I // 8,
-                                     out_dtype=self.out_dtype or torch.float32)
+        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
+        K.vq_moe_gate_up_rht(h, ids, self.gate_up_idx, self.cb16, self.gate_up_scale, y_gu, OUT=2 * I,
+                             NG=self.hidden_dim // 8, perm=self.rot_h._perm32, sign=self.rot_h._sign8,
+                             hb=self.rot_h.hb, rht_scale=self.rot_h.scale)
+        return K.vq_moe_down_swiglu_combine(y_gu, ids, w, self.down_idx, self.cb16, self.down_scale,
+                                            OUT=self.hidden_dim, NG=I // 8, perm=self.rot_i._perm32,
+                                            sign=self.rot_i._sign8, hb=self.rot_i.hb, rht_scale=self.rot_i.scale,
+                                            out=out, out_dtype=self.out_dtype or torch.float32)
 
     def forward(self, hidden_states, topk_idx, topk_weights):
-        h = hidden_states.reshape(-1, self.hidden_dim)
-        xr = self.rot_h.fwd(h.contiguous(), out_dtype=self.act_dtype)
+        h = hidden_states.reshape(-1, self.hidden_dim).contiguous()
         ids = topk_idx.reshape(h.shape[0], -1)
         if ids.dtype not in (torch.int32, torch.int64):
             ids = ids.to(torch.int32)
         w = topk_weights.reshape(ids.shape).to(torch.float32).contiguous()
-        out = self.experts(xr, ids.contiguous(), w)
+        out = self.experts(h, ids.contiguous(), w)
         return out.to(self.out_dtype or hidden_states.dtype)
 
 
@@ -103,5 +105,4 @@ class MoELayer(nn.Module):
         m = self.experts_mod
         h2 = h.reshape(-1, m.hidden_dim).contiguous()
         ids, w = self.route(h2, router_logits.reshape(h2.shape[0], -1).contiguous())
-        xr = m.rot_h.fwd(h2, out_dtype=m.act_dtype)
-        return m.experts(xr, ids, w)
+        return m.experts(h2, ids, w)

@@ -45,10 +45,16 @@ class PackedLinear(nn.Module):
         return self.idx0, i1, cb0, cb1
 
     def forward(self, x, out_dtype=None):
-        xr = self.rot.fwd(x.reshape(-1, self.n).contiguous(), out_dtype=self.act_dtype)
+        x2 = x.reshape(-1, self.n).contiguous()
         i0, i1, cb0, cb1 = self._planes()
-        y = K.vq_gemv(xr, i0, i1, cb0, cb1, self.scale, self.out, self.n, 1.0,
-                      out_dtype=out_dtype or x.dtype)
+        od = out_dtype or x.dtype
+        if x2.shape[0] <= 2 and self.n % 64 == 0:
+            # one launch: every workgroup rotates x in LDS, then multiplies
+            y = K.vq_gemv_rht(x2, [(i0, i1, self.scale, self.out)], cb0, cb1, self.n, self.rot._perm32,
+                              self.rot._sign8, self.rot.hb, self.rot.scale, out_dtype=od)[0]
+        else:
+            xr = self.rot.fwd(x2, out_dtype=self.act_dtype)
+            y = K.vq_gemv(xr, i0, i1, cb0, cb1, self.scale, self.out, self.n, 1.0, out_dtype=od)
         return y.view(*x.shape[:-1], self.out)
 
     def nbytes(self):

@@ -72,6 +72,33 @@ int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride,
              void* y, int y_dt, int64_t y_stride,
              int64_t out_rows, int64_t n, float rs, void* stream);
 
+/* One matrix of a vq2_gemv_rht launch: index planes, row scales and output
+ * (y [batch, y_stride], dtype of the launch), all device pointers. */
+typedef struct vq2_seg {
+    const int16_t* idx0; /* [out_rows, n/8] int16                                   */
+    const void* idx1;    /* stage-2 plane or NULL (must match the launch's s2_kind) */
+    const void* scale;   /* [out_rows]                                              */
+    void* y;             /* [batch, y_stride]                                       */
+    int64_t out_rows;
+    int64_t y_stride;
+} vq2_seg;
+
+/* Rotate-then-multiply in one launch, for up to 4 matrices that read the same
+ * activation (q/k/v, gate/up):
+ *   xr[b] = RHT_fwd(x[b]) with perm/sign (nullable), hb-point blocks, scale
+ *   segs[s].y[b, r] = (sum_k W_s[r, k] * xr[b, k]) * segs[s].scale[r] * rs
+ * Every workgroup builds xr in LDS itself, so no rotated copy of x is written.
+ * Requires n % 64 == 0, 16-byte aligned index planes and batch <= 2 (larger
+ * batches: vq2_rht + vq2_gemv); segs is a host array.
+ * Replaces FastRot + vq_gemv_16 / vq_gemv_16_8 of PackedLinear.forward
+ * (vq2/runtime.py:91-104) and Rot.fwd + F.linear of its fallback
+ * (vq2/runtime.py:105-110). */
+int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                 const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                 int n_seg, const vq2_seg* segs,
+                 int s2_kind, const void* cb0, const void* cb1, int cb_dt, int s_dt, int y_dt,
+                 int64_t n, float rs, void* stream);
+
 /* Grouped per-expert 2 bpw VQ GEMV over a device-resident expert pool:
  *   e = ids[k];  y[k, r] = (sum_g cb[pool[e, r, g]] . x_k[8g:8g+8]) * pool_scale[e, r] * rs
  *   x_k = x + (k / pairs_per_x) * x_pair_stride
@@ -92,6 +119,20 @@ int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pair
                     void* y, int y_dt, int64_t y_pair_stride,
                     int64_t out_rows, int64_t ng, float rs, void* stream);
 
+/* Grouped gate_up with the activation rotation fused in: for token t and its
+ * P experts ids[t*P + j],
+ *   xr_t = RHT_fwd(h[t]) (perm/sign nullable, hb-point blocks, rht_scale)
+ *   y[t*P + j, r] = (sum cb[pool[e, r, g]] . xr_t[8g:8g+8]) * pool_scale[e, r] * rs
+ * h is [tokens, n] (n = ng * 8).  Replaces rot_2048.fwd + vq_moe_parallel_gate_up
+ * of PagedMoEExpert.forward (vq2/paged_runtime.py:495-500). */
+int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens,
+                        const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                        const void* ids, int ids_dt, int64_t P,
+                        const int16_t* pool, int64_t n_experts,
+                        const void* cb, int cb_dt, const void* pool_scale, int s_dt,
+                        void* y, int y_dt, int64_t y_pair_stride,
+                        int64_t out_rows, int64_t ng, float rs, void* stream);
+
 /* Grouped down projection fused with the weighted expert combine:
  *   out[t, r] = sum_{j < P} w[t*P+j] * (VQ(pool[ids[t*P+j]]) x_{t*P+j})[r]
  * with x_p = x + p * ng*8 and each term (acc * scale) * rs as in
@@ -105,6 +146,19 @@ int vq2_moe_down_combine(const void* x, int x_dt,
                          const void* pool_scale, int s_dt,
                          void* out, int out_dt, int64_t out_stride,
                          int64_t out_rows, int64_t ng, float rs, void* stream);
+
+/* The whole expert epilogue in one launch: for token t and pair p = t*P + j,
+ *   act_p = RHT_fwd(silu(gu[p, :n]) * gu[p, n:2n])   (n = ng * 8, in LDS)
+ *   out[t, r] = sum_j w[p] * (sum_k VQ(pool[ids[p]])[r, k] * act_p[k]) * scale * rs
+ * Replaces the SwiGLU, rot_512.fwd, vq_moe_parallel_down and the weighted sum
+ * of PagedMoEExpert.forward (vq2/paged_runtime.py:501-510). */
+int vq2_moe_down_swiglu_combine(const void* gu, int gu_dt, int64_t gu_stride,
+                                const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                                const void* ids, int ids_dt, const float* w, int64_t tokens, int64_t P,
+                                const int16_t* pool, int64_t n_experts,
+                                const void* cb, int cb_dt, const void* pool_scale, int s_dt,
+                                void* out, int out_dt, int64_t out_stride,
+                                int64_t out_rows, int64_t ng, float rs, void* stream);
 
 /* Randomised Hadamard transform over the last dim, hb-point blocks:
  *   forward: v[i] = x[perm[i]] * sign[i];  y_blk = H_hb v_blk * scale

@@ -323,3 +323,82 @@ def test_resident_experts_drop_in_forward(dev):
             ar = O.np_rht64(act, ri.perm.cpu().numpy(), ri.sign.float().cpu().numpy(), 512)[0]
             ref[t] += float(w[t, j]) * (O.np_dequant64(dn[e], None, cb, None, dns[e]) @ ar)
     assert O.max_rel_err(out.float().cpu().numpy(), ref) < 8e-3  # bf16 output rounding
+
+
+# ------------------------------------------------------- fused-RHT launches
+@pytest.mark.parametrize("bpw", [2, 3, 4])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_gemv_rht_fused_segments(dev, bpw, batch):
+    """RHT + q/k/v-style multi-matrix GEMV in one launch vs RHT then GEMV."""
+    n = 2048
+    cb0 = synth.codebook(9100)
+    cb1 = synth.codebook(9101, 256 if bpw == 3 else 65536) if bpw > 2 else None
+    shapes = [2048, 512, 512]
+    mats = [synth.vq_matrix(9100 + 10 * k, rows, n, bpw=bpw) for k, rows in enumerate(shapes)]
+    x = synth.activations(9104, (batch, n), dtype=torch.float16)
+    perm = synth.permutation(9106, n)
+    sign = synth.signs(9105, n)
+    ys = K.vq_gemv_rht(x.to(dev), [(m["idx0"].to(dev), None if m["idx1"] is None else m["idx1"].to(dev),
+                                    m["scale"].to(dev), rows) for m, rows in zip(mats, shapes)],
+                       cb0.to(dev), None if cb1 is None else cb1.to(dev), n, perm.to(dev), sign.to(dev), 2048)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    for y, m, rows in zip(ys, mats, shapes):
+        _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+        assert y.shape == (batch, rows)
+        assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
+def test_gemv_rht_fused_6144(dev):
+    """down projection: 2048 x 6144 at 4 bpw with its 3 x 2048-block RHT fused."""
+    n, out = 6144, 2048
+    cb0, cb1 = synth.codebook(9200), synth.codebook(9201)
+    m = synth.vq_matrix(9200, out, n, bpw=4)
+    x = synth.activations(9204, n, dtype=torch.float16)
+    sign = synth.signs(9205, n)
+    (y,) = K.vq_gemv_rht(x.to(dev), [(m["idx0"].to(dev), m["idx1"].to(dev), m["scale"].to(dev), out)],
+                         cb0.to(dev), cb1.to(dev), n, None, sign.to(dev), 2048)
+    xr = O.rht(x, None, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+
+
+def test_packed_linear_forward(dev):
+    from compressai_amd.runtime import PackedLinear, PackedLMHead
+
+    n, out = 2048, 1536
+    cbs = {"16": synth.codebook(9300).to(dev), "16_16": synth.codebook(9301).to(dev)}
+    m = synth.vq_matrix(9300, out, n, bpw=4)
+    lin = PackedLinear((out, n), (16, 16), "layers.0.mlp.gate_proj", [m["idx0"], m["idx1"]], m["scale"], cbs, dev)
+    for B in (1, 3):  # fused single launch (B <= 2) and the two-launch path
+        x = synth.activations(9304 + B, (B, n), dtype=torch.float32)
+        y = lin(x.to(dev))
+        xr = O.rht(x, lin.rot.perm.cpu(), lin.rot.sign.float().cpu().numpy().astype(np.int8), lin.rot.hb)
+        _, y64 = O.vq_gemv(xr.astype(np.float32), m["idx0"], m["idx1"], cbs["16"], cbs["16_16"], m["scale"])
+        assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+    head = PackedLMHead(lin)
+    idx, val = head.argmax(synth.activations(9310, (2, n), dtype=torch.float32).to(dev))
+    logits = head(synth.activations(9310, (2, n), dtype=torch.float32).to(dev))
+    assert idx.cpu().tolist() == logits.argmax(-1).cpu().tolist()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_fused_launches_vs_unfused(dev, T):
+    """gate_up+RHT and SwiGLU+RHT+down+combine launches vs the separate kernels."""
+    E, P = 12, 5
+    cb = synth.codebook(9400).to(dev)
+    gu, gus, dn, dns = (t.to(dev) for t in _pools(9400, E))
+    ids = torch.randint(0, E, (T, P), generator=synth.gen(9401), dtype=torch.int32).to(dev)
+    w = torch.rand(T, P, generator=synth.gen(9402)).to(dev)
+    h = synth.activations(9403, (T, 2048), dtype=torch.float16).to(dev)
+    sign_h, sign_i = synth.signs(9404, 2048).to(dev), synth.signs(9405, 512).to(dev)
+    perm_h, perm_i = synth.permutation(9406, 2048).to(dev), synth.permutation(9407, 512).to(dev)
+    y_gu = torch.empty(T * P, 1024, device=dev)
+    K.vq_moe_gate_up_rht(h, ids, gu, cb, gus, y_gu, 1024, 256, perm_h, sign_h, 2048)
+    xr = K.vq_rht(h, perm_h, sign_h, 2048, out_dtype=torch.float32)
+    ref_gu = torch.empty(T * P, 1024, device=dev)
+    K.vq_moe_grouped(xr, ids, gu, cb, gus, ref_gu, 1024, 256, pairs_per_x=P)
+    assert O.max_rel_err(y_gu.cpu().numpy(), ref_gu.double().cpu().numpy()) < 1e-5
+    out = K.vq_moe_down_swiglu_combine(y_gu, ids, w, dn, cb, dns, 2048, 64, perm_i, sign_i, 512)
+    act_r = K.vq_swiglu_rht(y_gu, 512, perm_i, sign_i, 512)
+    ref = K.vq_moe_down_combine(act_r, ids, w, dn, cb, dns, OUT=2048, NG=64)
+    assert O.max_rel_err(out.cpu().numpy(), ref.double().cpu().numpy()) < 1e-5
