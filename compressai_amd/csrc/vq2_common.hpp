@@ -95,6 +95,68 @@ __device__ __forceinline__ float group_sum(float v, int width)
     return v;
 }
 
+// Full-wave reductions that end uniform in every lane: DPP inside each row
+// of 16, ds_swizzle across the rows of a 32-lane half, then the two halves
+// combined through readlane.  Any pairing is valid for these commutative,
+// associative operators.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v)
+{
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+__device__ __forceinline__ float wave_sum_all(float v)
+{
+    v += __int_as_float(dpp_mov<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov<0x140>(__float_as_int(v)));
+    v += swz_xor16(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+__device__ __forceinline__ float wave_max_all(float v)
+{
+    v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
+    v = fmaxf(v, swz_xor16(v));
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+}
+
+// (value, index) maximum with ties to the lower index
+__device__ __forceinline__ void argmax_step(float& v, int& i, float ov, int oi)
+{
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i)
+{
+    const float ov = __int_as_float(dpp_mov<CTRL>(__float_as_int(v)));
+    const int oi = dpp_mov<CTRL>(i);
+    argmax_step(v, i, ov, oi);
+}
+
+__device__ __forceinline__ void wave_argmax_all(float& v, int& i)
+{
+    argmax_dpp<0xB1>(v, i);
+    argmax_dpp<0x4E>(v, i);
+    argmax_dpp<0x141>(v, i);
+    argmax_dpp<0x140>(v, i);
+    argmax_step(v, i, swz_xor16(v), __builtin_amdgcn_ds_swizzle(i, 0x401F));
+    const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const int i0 = __builtin_amdgcn_readlane(i, 0);
+    const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const int i1 = __builtin_amdgcn_readlane(i, 32);
+    v = v0;
+    i = i0;
+    argmax_step(v, i, v1, i1);
+}
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
 
 }  // namespace vq2

@@ -64,9 +64,9 @@ static GemvPlan plan_gemv(const GemvCall& c, int num_cu)
     const int64_t ztiles = (batch + p.bt - 1) / p.bt;
     int64_t max_rows = 0;
     for (int s = 0; s < c.nseg; s++) max_rows = c.seg[s].out_rows > max_rows ? c.seg[s].out_rows : max_rows;
-    // rows per lane: enough that each lane has >= 8 centroid gathers in
-    // flight per row block (GPL codes per row); the grid is persistent
-    p.it = p.gpl >= 8 ? 1 : (p.gpl == 4 ? 2 : 4);
+    // rows per lane (measured on MI355X over the decode shapes): 1, except
+    // 2 for the 8-column batch tile, whose lanes hold one code per row
+    p.it = p.bt == 8 ? 2 : 1;
     static const int it_env = env_int("VQ2_GEMV_IT", 0);
     if (it_env == 1 || it_env == 2 || it_env == 4) p.it = it_env;
     static const double occ_env = env_double("VQ2_GEMV_OCC_SCALE", 1.0);

@@ -395,6 +395,19 @@ __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int r
     }
 }
 
+// Codes of task (row block rb, item) for this lane: item = pair * nch + chunk.
+template <int S2, int GPL, int IT>
+__device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int item, int nch, int64_t kc, int og,
+                                           int rows_per_block, int wr, int wr_id, int rpw, int sub, int col,
+                                           uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
+{
+    const int pj = item / nch, c = item - (item / nch) * nch;
+    bool bad;
+    const int64_t e = pair_expert(a, (int64_t)og * a.P + pj, bad);
+    const int64_t g0 = c * kc + (int64_t)col * GPL;
+    fetch_codes<S2, GPL, IT>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, c0, c1, valid);
+}
+
 // acc[it][b] = sum over this lane's GPL groups of VQ(W)[row_it] . x_b
 template <int CBT, int S2, int GPL, int BT, int IT>
 __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const uint32_t (&c0)[IT][GPL],
@@ -462,13 +475,6 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
     float* s_x = s_dyn;
     float* s_part = s_dyn + (XM == 0 ? 0 : (XM == 2 ? a.P : BT) * n);
 
-    if constexpr (S2 == VQ2_S2_U8) {
-        const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
-        for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
-    }
-    if constexpr (XM != 0) build_x<XM>(a, s_x, x_rows, n, og, bt0);
-    if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int lpr = a.lpr, wi = a.wi;
@@ -480,6 +486,19 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
     const int nch = (int)((a.ng + kc - 1) / kc);
     const int items = a.P * nch;
     const int rows_per_block = IT * rpw * wr;
+
+    // the first task's index words do not depend on the activation: issue
+    // their loads before the prologue so the HBM latency overlaps it
+    uint32_t c0[IT][GPL], c1[IT][GPL];
+    bool valid[IT];
+    task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1, valid);
+
+    if constexpr (S2 == VQ2_S2_U8) {
+        const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
+        for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
+    }
+    if constexpr (XM != 0) build_x<XM>(a, s_x, x_rows, n, og, bt0);
+    if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
 
     float xs[BT][GPL * 8];
     int cur_item = -1;
@@ -502,10 +521,7 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
         } else {
             load_x_lds<GPL, BT>(s_x, 0, n, g0, lane_ok, nb, a.xscale, xs);
         }
-        uint32_t c0[IT][GPL], c1[IT][GPL];
-        bool valid[IT];
         int64_t rb = blockIdx.x;
-        fetch_codes<S2, GPL, IT>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, c0, c1, valid);
         while (rb < a.n_rowblocks) {
             const int64_t rbn = rb + gridDim.x;
             uint32_t n0[IT][GPL], n1[IT][GPL];
@@ -549,112 +565,119 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
         return;
     }
 
-    for (int64_t rbg = blockIdx.x; rbg < a.n_rowblocks; rbg += gridDim.x) {
+    // Several items (expert pairs x K-chunks) per row block: wave wi_id runs
+    // its tasks (row block, item) in order and fetches the next task's codes
+    // before the current task's gathers; the WI waves' row partials are
+    // reduced through LDS in a fixed order once per row block.
+    int64_t rbg = blockIdx.x;
+    int item = wi_id;
+    float fin[IT][BT];
+#pragma unroll
+    for (int it = 0; it < IT; it++)
+#pragma unroll
+        for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
+    while (rbg < a.n_rowblocks) {
+        int nitem = item + wi;
+        int64_t nrbg = rbg;
+        if (nitem >= items) {
+            nitem = wi_id;
+            nrbg = rbg + gridDim.x;
+        }
+        uint32_t n0[IT][GPL], n1[IT][GPL];
+        bool nvalid[IT];
+        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, n0, n1, nvalid);
+
+        const int pj = item / nch, c = item - (item / nch) * nch;
+        const int64_t pair = (int64_t)og * a.P + pj;
+        bool bad;
+        const int64_t e = pair_expert(a, pair, bad);
+        const int64_t g0 = c * kc + (int64_t)col * GPL;
+        const bool lane_ok = g0 < a.ng;
+        if (item != cur_item) {
+            if constexpr (XM == 0) {
+                const int64_t xoff = (pair / a.x_pdiv) * a.x_pstride + (int64_t)bt0 * a.x_bstride;
+                const void* xb = a.x_dt == VQ2_DT_F32 ? (const void*)((const float*)a.x + xoff)
+                                                      : (const void*)((const uint16_t*)a.x + xoff);
+                load_x<GPL, BT>(a, xb, g0, lane_ok, nb, xs);
+            } else {
+                load_x_lds<GPL, BT>(s_x, XM == 2 ? pj : 0, n, g0, lane_ok, nb, a.xscale, xs);
+            }
+            cur_item = item;
+        }
+        float acc[IT][BT];
+        block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
+#pragma unroll
+        for (int it = 0; it < IT; it++)
+#pragma unroll
+            for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
+
         int si = 0;
         while (si + 1 < a.nseg && rbg >= a.seg[si + 1].rb_start) si++;
         const GemvSeg& sg = a.seg[si];
         const int64_t row_base = (rbg - sg.rb_start) * rows_per_block;
-        float fin[IT][BT];
+        const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
 #pragma unroll
-        for (int it = 0; it < IT; it++)
+        for (int it = 0; it < IT; it++) {
+            const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+            const float sc = row < sg.out_rows ? load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row) : 0.0f;
 #pragma unroll
-            for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
-
-        for (int item = wi_id; item < items; item += wi) {
-            const int pj = item / nch, c = item - (item / nch) * nch;
-            const int64_t pair = (int64_t)og * a.P + pj;
-            bool bad;
-            const int64_t e = pair_expert(a, pair, bad);
-            const int16_t* I0 = sg.idx0 + e * a.e_istride;
-            const int64_t g0 = c * kc + (int64_t)col * GPL;
-            const bool lane_ok = g0 < a.ng;
-            if (item != cur_item) {
-                if constexpr (XM == 0) {
-                    const int64_t xoff = (pair / a.x_pdiv) * a.x_pstride + (int64_t)bt0 * a.x_bstride;
-                    const void* xb = a.x_dt == VQ2_DT_F32 ? (const void*)((const float*)a.x + xoff)
-                                                          : (const void*)((const uint16_t*)a.x + xoff);
-                    load_x<GPL, BT>(a, xb, g0, lane_ok, nb, xs);
-                } else {
-                    load_x_lds<GPL, BT>(s_x, XM == 2 ? pj : 0, n, g0, lane_ok, nb, a.xscale, xs);
-                }
-                cur_item = item;
+            for (int b = 0; b < BT; b++) {
+                float v = (acc[it][b] * sc) * a.rs;
+                if (bad) v = __builtin_nanf("");
+                fin[it][b] = fmaf(pw, v, fin[it][b]);
             }
+        }
 
-            uint32_t c0[IT][GPL], c1[IT][GPL];
-            int64_t rows[IT];
-            bool valid[IT];
+        if (nitem == wi_id) {
+            // the wave's last item of this row block: reduce and store
+            if (wi == 1) {
+                if (col == 0) {
 #pragma unroll
-            for (int it = 0; it < IT; it++) {
-                rows[it] = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-                valid[it] = rows[it] < sg.out_rows && lane_ok && !bad;
-                const int64_t off = rows[it] * a.ng + g0;
-                if (valid[it]) {
-                    load_codes16<GPL>(I0, off, c0[it]);
-                    if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
-                    if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
-                } else {
+                    for (int it = 0; it < IT; it++) {
+                        const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+                        if (row >= sg.out_rows) continue;
 #pragma unroll
-                    for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
+                        for (int b = 0; b < BT; b++)
+                            if (b < nb)
+                                store_from_f32(sg.y, a.y_dt,
+                                               (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
+                                               fin[it][b]);
+                    }
                 }
+            } else {
+                if (col == 0) {
+#pragma unroll
+                    for (int it = 0; it < IT; it++) {
+                        const int lr = (it * wr + wr_id) * rpw + sub;
+#pragma unroll
+                        for (int b = 0; b < BT; b++) s_part[(wi_id * rows_per_block + lr) * BT + b] = fin[it][b];
+                    }
+                }
+                __syncthreads();
+                for (int t = threadIdx.x; t < rows_per_block * BT; t += blockDim.x) {
+                    const int lr = t / BT, b = t % BT;
+                    const int64_t row = row_base + lr;
+                    float sum = s_part[lr * BT + b];
+                    for (int w = 1; w < wi; w++) sum += s_part[(w * rows_per_block + lr) * BT + b];
+                    if (row < sg.out_rows && b < nb)
+                        store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
+                                       sum);
+                }
+                __syncthreads();
             }
-
-            float acc[IT][BT];
-            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
-
-            // row sums over the LPR lanes; every lane of a row gets the sum
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
-                for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
-
-            const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
-#pragma unroll
-            for (int it = 0; it < IT; it++) {
-                const int64_t row = rows[it];
-                const float s = row < sg.out_rows ? load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row) : 0.0f;
-#pragma unroll
-                for (int b = 0; b < BT; b++) {
-                    float v = (acc[it][b] * s) * a.rs;
-                    if (bad) v = __builtin_nanf("");
-                    fin[it][b] = (items == 1) ? v : fmaf(pw, v, fin[it][b]);
-                }
-            }
+                for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
         }
-
-        if (items == 1) {
-            if (col == 0) {
 #pragma unroll
-                for (int it = 0; it < IT; it++) {
-                    const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-                    if (row >= sg.out_rows) continue;
+        for (int it = 0; it < IT; it++) {
+            valid[it] = nvalid[it];
 #pragma unroll
-                    for (int b = 0; b < BT; b++)
-                        if (b < nb)
-                            store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
-                                           fin[it][b]);
-                }
-            }
-        } else {
-            // fixed-order reduction of the WI item waves through LDS
-            if (col == 0) {
-#pragma unroll
-                for (int it = 0; it < IT; it++) {
-                    const int lr = (it * wr + wr_id) * rpw + sub;
-#pragma unroll
-                    for (int b = 0; b < BT; b++) s_part[(wi_id * rows_per_block + lr) * BT + b] = fin[it][b];
-                }
-            }
-            __syncthreads();
-            for (int t = threadIdx.x; t < rows_per_block * BT; t += blockDim.x) {
-                const int lr = t / BT, b = t % BT;
-                const int64_t row = row_base + lr;
-                float sum = s_part[lr * BT + b];
-                for (int w = 1; w < wi; w++) sum += s_part[(w * rows_per_block + lr) * BT + b];
-                if (row < sg.out_rows && b < nb)
-                    store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row, sum);
-            }
-            __syncthreads();
+            for (int q = 0; q < GPL; q++) { c0[it][q] = n0[it][q]; c1[it][q] = n1[it][q]; }
         }
+        item = nitem;
+        rbg = nrbg;
     }
 }
 

@@ -88,16 +88,8 @@ int argmax_launch(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* 
 constexpr int ROUTER_MAX_E = 1024;
 constexpr int ROUTER_PER_LANE = ROUTER_MAX_E / 64;
 
-__device__ __forceinline__ float wave_max(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave_max_all(v); }
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_all(v); }
 
 template <int DT>
 __device__ __forceinline__ float ld_t(const void* p, int64_t i)
@@ -193,11 +185,7 @@ __global__ void __launch_bounds__(64) router_kernel(const void* logits, int l_dt
             const int e = j * 64 + lane;
             if (p[j] > bv || (p[j] == bv && e < bi)) { bv = p[j]; bi = e; }
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        wave_argmax_all(bv, bi);
 #pragma unroll
         for (int j = 0; j < ROUTER_PER_LANE; j++)
             if (j * 64 + lane == bi) p[j] = -2.0f;  // never selected again
