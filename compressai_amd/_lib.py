@@ -34,6 +34,9 @@ SIGNATURES = {
                              _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_down_swiglu_combine": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _vp, _i64, _i64, _vp, _i64,
                                      _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
+    "vq2_gemm_small_m_workspace": ([_i64, _i64, _i64], ctypes.c_size_t),
+    "vq2_gemm_small_m": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
+                          _i64, _i64, _f32, _vp, ctypes.c_size_t, _vp], _i32),
     "vq2_moe_grouped": ([_vp, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _i32,
                          _i64, _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_down_combine": ([_vp, _i32, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i32,
@@ -65,7 +68,7 @@ class Seg(ctypes.Structure):
 def header_symbols() -> list[str]:
     """Names of the functions declared in include/vq2_amd.h."""
     text = HEADER_PATH.read_text()
-    return re.findall(r"^\s*(?:int|const char\*)\s+(vq2_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(vq2_\w+)\s*\(", text, flags=re.M)
 
 
 def load():

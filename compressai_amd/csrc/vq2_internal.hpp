@@ -63,6 +63,34 @@ struct GemvCall {
 
 int gemv_launch(const GemvCall& c);
 
+// Small-M batched GEMM on the matrix cores (vq2_gemm_mfma.hip).
+struct GemmCall {
+    const void* x;
+    int x_dt;
+    int64_t x_stride;  // elements between activation rows
+    int64_t m;         // activation rows (1..64)
+    const int16_t* idx0;
+    const void* idx1;
+    int s2;
+    const void* cb0;
+    const void* cb1;
+    int cb_dt;
+    const void* scale;
+    int s_dt;
+    void* y;
+    int y_dt;
+    int64_t y_stride;  // elements between output rows of y ([m][out_rows])
+    int64_t out_rows;
+    int64_t ng;
+    float rs;
+    void* workspace;
+    size_t ws_bytes;
+    void* stream;
+};
+
+size_t gemm_small_m_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
+int gemm_small_m_launch(const GemmCall& c);
+
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
                const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,
                int inverse, int swiglu, int64_t inter, void* stream);

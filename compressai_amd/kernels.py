@@ -26,6 +26,8 @@ is selectable (``out_dtype``; bf16 by default, as in the reference).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -35,7 +37,7 @@ __all__ = [
     "HAVE_TRITON", "FUSED_KERNELS_ENABLED", "set_fused_kernels_enabled",
     "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
     "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine", "vq_moe_grouped",
-    "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine",
+    "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine", "vq_gemm_small_m",
     "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
     "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
     "optimize_deltanet_layers", "Vq2Error",
@@ -130,16 +132,9 @@ def _ids(t: torch.Tensor) -> tuple[torch.Tensor, int]:
 
 
 # --------------------------------------------------------------- dense GEMV
-def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
-    """Generic VQ GEMV: 2 bpw (i1 None), 3 bpw (i1 uint8) or 4 bpw (i1 int16).
-    xr [n] -> y [out]; xr [B, n] -> y [B, out]."""
-    dev = _dev(xr, i0, i1, cb0, cb1, scale, y)
-    n = int(n)
-    out = int(out)
-    x2 = xr.reshape(-1, n) if xr.dim() != 2 else xr
-    if x2.shape[-1] != n or x2.stride(-1) != 1:
-        raise Vq2Error(f"xr must have a unit-stride last dim of size n={n}")
-    B = x2.shape[0]
+def _planes(i0, i1, cb0, cb1, scale, out, n):
+    """Validate one matrix's index planes, codebooks and scales; returns
+    (i0, i1, s2_kind) with the planes viewed as the kernels read them."""
     i0 = _idx16(i0, "i0")
     if i0.numel() != out * (n // 8):
         raise Vq2Error(f"i0 has {i0.numel()} codes, expected out*n/8 = {out * (n // 8)}")
@@ -166,6 +161,20 @@ def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bflo
     _contig(scale, "scale")
     if scale.numel() != out:
         raise Vq2Error(f"scale has {scale.numel()} entries, expected {out}")
+    return i0, i1, s2
+
+
+def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """Generic VQ GEMV: 2 bpw (i1 None), 3 bpw (i1 uint8) or 4 bpw (i1 int16).
+    xr [n] -> y [out]; xr [B, n] -> y [B, out]."""
+    dev = _dev(xr, i0, i1, cb0, cb1, scale, y)
+    n = int(n)
+    out = int(out)
+    x2 = xr.reshape(-1, n) if xr.dim() != 2 else xr
+    if x2.shape[-1] != n or x2.stride(-1) != 1:
+        raise Vq2Error(f"xr must have a unit-stride last dim of size n={n}")
+    B = x2.shape[0]
+    i0, i1, s2 = _planes(i0, i1, cb0, cb1, scale, out, n)
     if y is None:
         y = torch.empty((B, out) if xr.dim() == 2 else (out,), dtype=out_dtype, device=dev)
     else:
@@ -175,6 +184,51 @@ def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bflo
     _lib.call("vq2_gemv", _p(x2), _dt(x2, "xr"), B, x2.stride(0) if B > 1 else n,
               _p(i0), _p(i1), s2, _p(cb0), _p(cb1), _dt(cb0, "cb0"), _p(scale), _dt(scale, "scale"),
               _p(y), _dt(y, "y"), out, out, n, float(rs), _stream(dev))
+    return y
+
+
+# Split-K partials of vq_gemm_small_m, one buffer per (device, stream):
+# launches on one stream run in order, so they can share it.
+_WS: dict = {}
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WS[key] = buf
+    return buf
+
+
+def vq_gemm_small_m(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
+    """Small-M batched VQ GEMM on the matrix cores: xr [B, n] (B <= 64,
+    rotated) -> y [B, out], for 2 bpw (i1 None), 3 bpw (i1 uint8) or 4 bpw
+    (i1 int16).  Replaces the batch > 1 fallback of PackedLinear
+    (vq2/runtime.py:105-110): every centroid is gathered once for all B rows."""
+    dev = _dev(xr, i0, i1, cb0, cb1, scale, y)
+    n = int(n)
+    out = int(out)
+    x2 = xr.reshape(-1, n) if xr.dim() != 2 else xr
+    if x2.shape[-1] != n or x2.stride(-1) != 1:
+        raise Vq2Error(f"xr must have a unit-stride last dim of size n={n}")
+    B = x2.shape[0]
+    if not 1 <= B <= 64:
+        raise Vq2Error(f"vq_gemm_small_m: batch {B} outside 1..64")
+    i0, i1, s2 = _planes(i0, i1, cb0, cb1, scale, out, n)
+    if y is None:
+        y = torch.empty((B, out), dtype=out_dtype, device=dev)
+    else:
+        _contig(y, "y")
+        if y.numel() != B * out:
+            raise Vq2Error("y has the wrong size")
+    lib = _lib.load()
+    ws = _workspace(dev, int(lib.vq2_gemm_small_m_workspace(B, out, n)))
+    _lib.call("vq2_gemm_small_m", _p(x2), _dt(x2, "xr"), B, x2.stride(0) if B > 1 else n,
+              _p(i0), _p(i1), s2, _p(cb0), _p(cb1), _dt(cb0, "cb0"), _p(scale), _dt(scale, "scale"),
+              _p(y), _dt(y, "y"), out, out, n, float(rs), _p(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return y
 
 

@@ -72,6 +72,27 @@ int vq2_gemv(const void* x, int x_dt, int64_t batch, int64_t x_stride,
              void* y, int y_dt, int64_t y_stride,
              int64_t out_rows, int64_t n, float rs, void* stream);
 
+/* Small-M batched VQ GEMM on the matrix cores (v_mfma_f32_16x16x32_f16):
+ * y[b * y_stride + r] = (sum_k x[b * x_stride + k] * W[r, k]) * s[r] * rs for
+ * b < batch (1..64), x already rotated, n % 64 == 0, 16-byte aligned index
+ * planes and activation rows.  Every centroid is gathered once for all batch
+ * rows (vq2_gemv gathers it once per 8-row batch tile).  The activation is
+ * rounded to fp16 under a power-of-two scale per row and K split (and bf16 /
+ * fp32 centroids to fp16); accumulation is fp32.  K is split across
+ * workgroups to fill the device; the raw partials then go to `workspace`
+ * (vq2_gemm_small_m_workspace(...) bytes, 16-byte aligned, 0 = none needed;
+ * contents on entry do not matter) and a second launch sums them in a fixed
+ * order.  Replaces the PackedLinear batch > 1 fallback, dequantize + F.linear
+ * (vq2/runtime.py:82-89, 105-110). */
+size_t vq2_gemm_small_m_workspace(int64_t batch, int64_t out_rows, int64_t n);
+int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                     const int16_t* idx0, const void* idx1, int s2_kind,
+                     const void* cb0, const void* cb1, int cb_dt,
+                     const void* scale, int s_dt,
+                     void* y, int y_dt, int64_t y_stride,
+                     int64_t out_rows, int64_t n, float rs,
+                     void* workspace, size_t ws_bytes, void* stream);
+
 /* One matrix of a vq2_gemv_rht launch: index planes, row scales and output
  * (y [batch, y_stride], dtype of the launch), all device pointers. */
 typedef struct vq2_seg {
@@ -98,6 +119,7 @@ int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride,
                  int n_seg, const vq2_seg* segs,
                  int s2_kind, const void* cb0, const void* cb1, int cb_dt, int s_dt, int y_dt,
                  int64_t n, float rs, void* stream);
+
 
 /* Grouped per-expert 2 bpw VQ GEMV over a device-resident expert pool:
  *   e = ids[k];  y[k, r] = (sum_g cb[pool[e, r, g]] . x_k[8g:8g+8]) * pool_scale[e, r] * rs

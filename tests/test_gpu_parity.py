@@ -402,3 +402,77 @@ def test_moe_fused_launches_vs_unfused(dev, T):
     act_r = K.vq_swiglu_rht(y_gu, 512, perm_i, sign_i, 512)
     ref = K.vq_moe_down_combine(act_r, ids, w, dn, cb, dns, OUT=2048, NG=64)
     assert O.max_rel_err(out.cpu().numpy(), ref.double().cpu().numpy()) < 1e-5
+
+
+# ----------------------------------------------------- small-M MFMA GEMM
+def _rowwise_err(y, ref):
+    return max(O.max_rel_err(y[b], ref[b]) for b in range(ref.shape[0]))
+
+
+@pytest.mark.parametrize("out,n,bpw", [(6144, 2048, 2), (2048, 6144, 4), (1000, 512, 3), (517, 2048, 4)])
+@pytest.mark.parametrize("M", [2, 5, 16, 17, 64])
+def test_gemm_small_m_vs_oracle(dev, out, n, bpw, M):
+    """Every batch row within 1e-3 of the fp64 oracle (x and centroids go
+    through fp16 with a per-row power-of-two scale)."""
+    m = synth.vq_matrix(7000 + out + bpw, out, n, bpw=bpw)
+    cb0 = synth.codebook(7001)
+    cb1 = synth.codebook(7002, 256 if bpw == 3 else 65536) if bpw > 2 else None
+    x = synth.activations(7004 + M, (M, n), dtype=torch.float32)
+    i0, i1, sc, c0, c1, xx = _cuda(m["idx0"], m["idx1"], m["scale"], cb0, cb1, x, dev=dev)
+    y = K.vq_gemm_small_m(xx, i0, i1, c0, c1, sc, out, n, 0.5, out_dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, m["scale"], 0.5)
+    assert y.shape == (M, out)
+    assert _rowwise_err(y.cpu().numpy(), y64) < TOL
+
+
+@pytest.mark.parametrize("cbdt,xdt,ydt", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.float16, torch.float32),
+                                          (torch.float16, torch.bfloat16, torch.float16)])
+def test_gemm_small_m_dtypes(dev, cbdt, xdt, ydt):
+    out, n, M = 768, 2048, 24
+    m = synth.vq_matrix(7100, out, n, bpw=4)
+    cb0 = synth.codebook(7101, dtype=cbdt)
+    cb1 = synth.codebook(7102, dtype=cbdt)
+    x = synth.activations(7104, (M, n), dtype=xdt)
+    sc = m["scale"].to(torch.bfloat16) if cbdt == torch.bfloat16 else m["scale"]
+    i0, i1, s_, c0, c1, xx = _cuda(m["idx0"], m["idx1"], sc, cb0, cb1, x, dev=dev)
+    y = K.vq_gemm_small_m(xx, i0, i1, c0, c1, s_, out, n, out_dtype=ydt)
+    _, y64 = O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, sc)
+    tol = TOL if ydt == torch.float32 else 2.0 ** -8 + TOL
+    assert y.dtype == ydt and _rowwise_err(y.float().cpu().numpy(), y64) < tol
+
+
+def test_gemm_small_m_extreme_rows(dev):
+    """Rows scaled by 1e6 and 1e-6 (fp16 alone would overflow / lose them),
+    a zero row, and a NaN row that stays confined to its own outputs."""
+    out, n, M = 640, 1024, 6
+    m = synth.vq_matrix(7200, out, n, bpw=2)
+    cb0 = synth.codebook(7201)
+    x = synth.activations(7204, (M, n), dtype=torch.float32)
+    x[1] *= 1e6
+    x[2] *= 1e-6
+    x[3] = 0.0
+    x[4, 17] = float("nan")
+    i0, sc, c0, xx = _cuda(m["idx0"], m["scale"], cb0, x, dev=dev)
+    y = K.vq_gemm_small_m(xx, i0, None, c0, None, sc, out, n, out_dtype=torch.float32).cpu().numpy()
+    xo = x.clone()
+    xo[4] = 0.0
+    _, y64 = O.vq_gemv(xo, m["idx0"], None, cb0, None, m["scale"])
+    for b in (0, 1, 2, 5):
+        assert O.max_rel_err(y[b], y64[b]) < TOL, b
+    assert np.all(y[3] == 0.0)
+    assert np.all(np.isnan(y[4]))
+
+
+def test_gemm_small_m_matches_batched_gemv(dev):
+    """Same inputs through vq2_gemm_small_m and the batched vq2_gemv: the two
+    kernels agree to the output tolerance, on two calls in a row with the
+    second one smaller (the shared split-K workspace is reused)."""
+    for out, M in [(6144, 64), (2048, 16)]:
+        m = synth.vq_matrix(7300 + M, out, 2048, bpw=2)
+        cb0 = synth.codebook(7301)
+        x = synth.activations(7304 + M, (M, 2048), dtype=torch.float16)
+        i0, sc, c0, xx = _cuda(m["idx0"], m["scale"], cb0, x, dev=dev)
+        ya = K.vq_gemm_small_m(xx, i0, None, c0, None, sc, out, 2048, out_dtype=torch.float32)
+        yb = K.vq_gemv(xx, i0, None, c0, None, sc, out, 2048, out_dtype=torch.float32)
+        assert _rowwise_err(ya.cpu().numpy(), yb.cpu().numpy()) < TOL
