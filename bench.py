@@ -261,6 +261,59 @@ def bench_lm_head(args, dev, batch=1, copies=14):
     return dict(us=us, gbps=gbps)
 
 
+def bench_small_m(args, dev):
+    """small-M batched VQ GEMM on the matrix cores (M = 16, 64) on
+    the 6144x2048 and 2048x6144 MLP shapes at 2 and 4 bpw, >= 1 GiB of
+    distinct weights cycled; plus the RHT of the [M, 8192] activation (2048-
+    point blocks as the reference's Rot picks for n = 8192, and one 8192-point
+    block)."""
+    import torch
+
+    from compressai_amd import kernels as K, synth
+
+    g = torch.Generator(device=dev).manual_seed(5000)
+    cb0 = synth.codebook(5000).to(dev)
+    cb1 = synth.codebook(5001).to(dev)
+    res = {}
+    for out, n in ((6144, 2048), (2048, 6144)):
+        for bpw in (2, 4):
+            per = out * (n // 8) * 2 * (2 if bpw == 4 else 1) + out * 2
+            copies = int(2**30 // per) + 1
+            mats = [(rand_i16((out, n // 8), g, dev), rand_i16((out, n // 8), g, dev) if bpw == 4 else None,
+                     rand_scale(out, g, dev)) for _ in range(copies)]
+            c1 = cb1 if bpw == 4 else None
+            for M in (16, 64):
+                x = synth.activations(5004 + M, (M, n), dtype=torch.float16).to(dev)
+                y = torch.empty((M, out), dtype=torch.float32, device=dev)
+
+                def fwd(l, x=x, y=y, c1=c1):
+                    i0, i1, s = mats[l]
+                    K.vq_gemm_small_m(x, i0, i1, cb0, c1, s, out, n, y=y)
+
+                gr = capture(fwd, copies, dev)
+                time_graph(gr, 1, dev)
+                reps = max(2, 400 // copies)
+                ms, _ = time_graph(gr, reps, dev)
+                us = ms * 1e3 / (reps * copies)
+                key = f"{out}x{n}_{bpw}bpw_M{M}"
+                res[key] = {"us": round(us, 3), "gbps": round(per / (us * 1e-6) / 1e9, 2)}
+                log(f"small-M {key}: {us:.2f} us/call, {res[key]['gbps']:.1f} GB/s")
+            del mats
+            torch.cuda.empty_cache()
+    sign = synth.signs(5006, 8192).to(dev)
+    for M in (16, 64):
+        x = synth.activations(5007, (M, 8192), dtype=torch.float16).to(dev)
+        xr = torch.empty((M, 8192), dtype=torch.float32, device=dev)
+        for hb in (2048, 8192):
+            gr = capture(lambda l, x=x, hb=hb: K.vq_rht(x, None, sign, hb, out=xr), 50, dev)
+            time_graph(gr, 1, dev)
+            ms, _ = time_graph(gr, 10, dev)
+            us = ms * 1e3 / 500
+            res[f"rht8192_hb{hb}_M{M}"] = {"us": round(us, 3)}
+            log(f"RHT [M={M}, 8192] hb={hb}: {us:.2f} us/call")
+    return res
+
+
 # -------------------------------------------------------------- CPU baseline
 def cpu_baseline(dl, budget_s=20.0):
     """The reference CPU path (PackedLinear fallback, fp32) on the host for
@@ -332,6 +385,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
+    ap.add_argument("--no-small-m", action="store_true")
     ap.add_argument("--only", choices=["dominant", "copy"], default=None)
     args = ap.parse_args()
 
@@ -372,6 +426,7 @@ def main():
     moe = None if args.no_moe else bench_moe(args, dev)
     lm1 = None if args.no_lmhead else bench_lm_head(args, dev, batch=1)
     lm4 = None if args.no_lmhead else bench_lm_head(args, dev, batch=4)
+    sm = None if args.no_small_m else bench_small_m(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(d["dense"])
 
     rec = {
@@ -400,6 +455,7 @@ def main():
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "small_m": sm,
         "roofline": {
             "kernel": "vq_gemv_kernel (fused RHT) gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1",
             "bound": "hbm",

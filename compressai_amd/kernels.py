@@ -544,7 +544,13 @@ def vq_gemv_argmax(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, logits_ws=Non
     B = x2.shape[0]
     if logits_ws is None:
         logits_ws = torch.empty((B, out), dtype=torch.float32, device=dev)
-    vq_gemv(x2, i0, i1, cb0, cb1, scale, out, n, rs, y=logits_ws)
+    if B < 3 or n % 64:
+        vq_gemv(x2, i0, i1, cb0, cb1, scale, out, n, rs, y=logits_ws)
+    else:
+        # matrix cores: every centroid is gathered once per 64 rows
+        for b0 in range(0, B, 64):
+            b1 = min(B, b0 + 64)
+            vq_gemm_small_m(x2[b0:b1], i0, i1, cb0, cb1, scale, out, n, rs, y=logits_ws[b0:b1])
     return vq_argmax(logits_ws)
 
 

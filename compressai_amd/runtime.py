@@ -5,9 +5,10 @@ reference constructor (vq2/runtime.py:70-80): ``idx`` is the list of index
 planes (int16 for 16-bit stages, uint8 for 8-bit stages), ``scale`` the
 per-row scales, ``cbs`` a dict of codebooks keyed by the cfg prefix
 ("16", "16_8", "16_16").  ``forward(x)`` rotates x with the layer's RHT and
-runs the fused VQ GEMV for every batch size and every cfg in (16,),
-(16, 8), (16, 16) -- the reference fuses only batch 1 of (16,) and (16, 8)
-and otherwise re-materialises the dequantized matrix (runtime.py:91-110).
+runs the fused VQ GEMV (batch <= 2) or the matrix-core small-M GEMM
+(batch >= 3) for every cfg in (16,), (16, 8), (16, 16) -- the reference
+fuses only batch 1 of (16,) and (16, 8) and otherwise re-materialises the
+dequantized matrix (runtime.py:91-110).
 ``PackedLMHead`` (runtime.py:136-144) wraps it and adds ``argmax``.
 """
 from __future__ import annotations
@@ -21,6 +22,25 @@ from .rot import get_rot
 
 def cfg_key(cfg, i):
     return "_".join(str(b) for b in cfg[: i + 1])
+
+
+# batch rows per matrix-core launch (vq2_gemm_small_m takes up to 64)
+SMALL_M_MAX = 64
+
+
+def vq_matmul(xr, i0, i1, cb0, cb1, scale, out, n, out_dtype, y=None):
+    """y [B, out] = VQ(W) . xr for rotated xr [B, n], B >= 1: the batched
+    GEMV below 3 rows, the matrix-core GEMM (every centroid gathered once per
+    64 rows) from 3 rows on."""
+    B = xr.shape[0]
+    if B < 3 or n % 64:
+        return K.vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, 1.0, out_dtype=out_dtype, y=y)
+    if y is None:
+        y = torch.empty((B, out), dtype=out_dtype, device=xr.device)
+    for b0 in range(0, B, SMALL_M_MAX):
+        b1 = min(B, b0 + SMALL_M_MAX)
+        K.vq_gemm_small_m(xr[b0:b1], i0, i1, cb0, cb1, scale, out, n, 1.0, y=y[b0:b1])
+    return y
 
 
 class PackedLinear(nn.Module):
@@ -48,13 +68,14 @@ class PackedLinear(nn.Module):
         x2 = x.reshape(-1, self.n).contiguous()
         i0, i1, cb0, cb1 = self._planes()
         od = out_dtype or x.dtype
-        if x2.shape[0] <= 2 and self.n % 64 == 0:
+        B = x2.shape[0]
+        if B <= 2 and self.n % 64 == 0:
             # one launch: every workgroup rotates x in LDS, then multiplies
             y = K.vq_gemv_rht(x2, [(i0, i1, self.scale, self.out)], cb0, cb1, self.n, self.rot._perm32,
                               self.rot._sign8, self.rot.hb, self.rot.scale, out_dtype=od)[0]
         else:
             xr = self.rot.fwd(x2, out_dtype=self.act_dtype)
-            y = K.vq_gemv(xr, i0, i1, cb0, cb1, self.scale, self.out, self.n, 1.0, out_dtype=od)
+            y = vq_matmul(xr, i0, i1, cb0, cb1, self.scale, self.out, self.n, od)
         return y.view(*x.shape[:-1], self.out)
 
     def nbytes(self):
