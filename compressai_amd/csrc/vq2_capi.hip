@@ -280,6 +280,61 @@ int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* 
     return gemv_launch(c);
 }
 
+int vq2_moe_router_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign,
+                               int64_t hb, float rht_scale, const void* logits, int l_dt, int64_t n_routed, int k,
+                               const void* shared_gate, int g_dt, int64_t shared_id, const int16_t* pool,
+                               int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* y,
+                               int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, int32_t* ids,
+                               float* w, void* stream)
+{
+    clear_error();
+    CHECK(tokens >= 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_router_gate_up_rht: bad sizes");
+    CHECK(n_routed >= 1 && n_routed <= 1024, "vq2_moe_router_gate_up_rht: n_routed=%lld not in [1, 1024]",
+          (long long)n_routed);
+    CHECK(k >= 1 && k <= 32 && k <= n_routed, "vq2_moe_router_gate_up_rht: k=%d out of range", k);
+    CHECK(n_routed <= n_experts, "vq2_moe_router_gate_up_rht: the pool holds %lld experts < n_routed=%lld",
+          (long long)n_experts, (long long)n_routed);
+    CHECK(shared_id < n_experts, "vq2_moe_router_gate_up_rht: shared_id=%lld outside the pool", (long long)shared_id);
+    if (tokens == 0 || out_rows == 0) return VQ2_OK;
+    CHECK(h && logits && pool && pool_scale && y && ids && w, "vq2_moe_router_gate_up_rht: NULL pointer argument");
+    CHECK(dt_ok(h_dt) && dt_ok(l_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_moe_router_gate_up_rht: bad dtype code");
+    if (shared_id >= 0) CHECK(shared_gate && dt_ok(g_dt), "vq2_moe_router_gate_up_rht: the shared expert needs its gate");
+    const int64_t P = k + (shared_id >= 0 ? 1 : 0);
+    CHECK(y_pair_stride >= out_rows, "vq2_moe_router_gate_up_rht: y_pair_stride < out_rows");
+    CHECK(tokens * P <= 65535, "vq2_moe_router_gate_up_rht: too many pairs");
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "vq2_moe_router_gate_up_rht: bad hb");
+    if (int rr = check_rot_tables(perm, sign)) return rr;
+    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    if (r) return r;
+    GemvCall c = base_call(h, h_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, y_dt, ng, 1, rs, stream);
+    c.x_bstride = ng * 8;
+    c.x_pstride = ng * 8;
+    c.x_pdiv = (int)P;
+    c.ids = ids;
+    c.ids_i64 = 0;
+    c.n_experts = n_experts;
+    c.n_out_groups = tokens * P;
+    c.y_ostride = y_pair_stride;
+    c.nseg = 1;
+    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, y, out_rows, 0};
+    c.xm = 3;
+    c.perm = perm;
+    c.sign = sign;
+    c.hb = hb;
+    c.xscale = rht_scale;
+    c.r_logits = logits;
+    c.r_ldt = l_dt;
+    c.r_ne = n_routed;
+    c.r_k = k;
+    c.r_pairs = (int)P;
+    c.r_shared = shared_id;
+    c.r_gate = shared_gate;
+    c.r_gdt = g_dt;
+    c.r_ids = ids;
+    c.r_w = w;
+    return gemv_launch(c);
+}
+
 int vq2_moe_down_combine(const void* x, int x_dt, const void* ids, int ids_dt, const float* w, int64_t tokens,
                          int64_t P, const int16_t* pool, int64_t n_experts, const void* cb, int cb_dt,
                          const void* pool_scale, int s_dt, void* out, int out_dt, int64_t out_stride,

@@ -120,6 +120,16 @@ int gemv_launch(const GemvCall& c)
     a.perm = c.perm;
     a.sign = c.sign;
     a.xscale = c.xscale;
+    a.r_logits = c.r_logits;
+    a.r_ldt = c.r_ldt;
+    a.r_ne = c.r_ne;
+    a.r_k = c.r_k;
+    a.r_pairs = c.r_pairs > 0 ? c.r_pairs : 1;
+    a.r_shared = c.r_shared;
+    a.r_gate = c.r_gate;
+    a.r_gdt = c.r_gdt;
+    a.r_ids = c.r_ids;
+    a.r_w = c.r_w;
     int L = 0;
     if (c.xm != 0) {
         while ((1LL << L) < c.hb) L++;
@@ -174,6 +184,8 @@ int gemv_launch(const GemvCall& c)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
     if (c.xm == 2 && (c.s2 != VQ2_S2_NONE || p.bt != 1))
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 bpw, batch 1");
+    if (c.xm == 3 && (c.s2 != VQ2_S2_NONE || p.bt != 1 || !c.r_logits))
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused router is for 2 bpw, batch 1");
     if (c.xm == 1 && p.bt > 2)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused rotation supports batch <= 2 per launch");
     const int64_t ztiles = (c.batch + p.bt - 1) / p.bt;

@@ -29,6 +29,7 @@
 #pragma once
 #include "vq2_common.hpp"
 #include "vq2_internal.hpp"
+#include "vq2_router.hpp"
 
 namespace vq2 {
 
@@ -81,6 +82,21 @@ struct GemvArgs {
     const int8_t* sign;
     int hb_log2;
     float xscale;
+    // fused router (XM 3: the gate_up launch, one pair per output group): output group
+    // og is slot og % r_pairs of token og / r_pairs; slots < r_k take the
+    // token's top-k routed experts from its logits, slot r_k the shared
+    // expert r_shared.  Workgroup 0 of each group writes the pair's expert id
+    // and combine weight to r_ids / r_w.
+    const void* r_logits;
+    int r_ldt;
+    int64_t r_ne;
+    int r_k;
+    int r_pairs;
+    int64_t r_shared;
+    const void* r_gate;
+    int r_gdt;
+    int32_t* r_ids;
+    float* r_w;
 };
 
 template <int CBT>
@@ -223,12 +239,46 @@ __device__ __forceinline__ void load_x(const GemvArgs& a, const void* xb, int64_
         load_x_t<GPL, BT, VQ2_DT_BF16>(a, xb, g0, lane_ok, nb, xs);
 }
 
-__device__ __forceinline__ int64_t pair_expert(const GemvArgs& a, int64_t pair, bool& bad)
+__device__ __forceinline__ int64_t pair_expert(const GemvArgs& a, int64_t pair, bool& bad, int64_t e_rt = -1)
 {
+    if (e_rt >= 0) {
+        bad = false;
+        return e_rt;
+    }
     int64_t e = 0;
     if (a.ids) e = a.ids_i64 ? ((const int64_t*)a.ids)[pair] : (int64_t)((const int32_t*)a.ids)[pair];
     bad = a.ids && (e < 0 || e >= a.n_experts);
     return bad ? 0 : e;
+}
+
+// Expert of output group og under the fused router (uniform per wave; every
+// wave of the group computes it, workgroup 0 / wave 0 also publishes it).
+__device__ __forceinline__ int64_t route_pair(const GemvArgs& a, int og, int lane, int wave)
+{
+    const int64_t t = og / a.r_pairs;
+    const int p = og - (int)t * a.r_pairs;
+    const bool writer = blockIdx.x == 0 && wave == 0;
+    if (p < a.r_k) {
+        float mine, tot;
+        int my_id;
+        if (a.r_ne <= 256)
+            router_select<4>(a.r_logits, a.r_ldt, t, a.r_ne, a.r_k, lane, mine, my_id, tot);
+        else
+            router_select<ROUTER_MAX_E / 64>(a.r_logits, a.r_ldt, t, a.r_ne, a.r_k, lane, mine, my_id, tot);
+        if (writer && lane == p) {
+            a.r_ids[og] = my_id;
+            a.r_w[og] = mine / tot;
+        }
+        return __builtin_amdgcn_readlane(my_id, p);
+    }
+    if (writer) {
+        const float sw = router_shared_weight(a.r_gate, a.r_gdt, a.x, a.x_dt, t, a.ng * 8, lane);
+        if (lane == 0) {
+            a.r_ids[og] = (int32_t)a.r_shared;
+            a.r_w[og] = sw;
+        }
+    }
+    return a.r_shared;
 }
 
 // In-place blockwise Walsh-Hadamard transform of v[0, total) over
@@ -399,11 +449,12 @@ __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int r
 template <int S2, int GPL, int IT>
 __device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int item, int nch, int64_t kc, int og,
                                            int rows_per_block, int wr, int wr_id, int rpw, int sub, int col,
-                                           uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
+                                           uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT],
+                                           int64_t e_rt)
 {
     const int pj = item / nch, c = item - (item / nch) * nch;
     bool bad;
-    const int64_t e = pair_expert(a, (int64_t)og * a.P + pj, bad);
+    const int64_t e = pair_expert(a, (int64_t)og * a.P + pj, bad, e_rt);
     const int64_t g0 = c * kc + (int64_t)col * GPL;
     fetch_codes<S2, GPL, IT>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, c0, c1, valid);
 }
@@ -466,14 +517,16 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
     extern __shared__ float s_dyn[];  // [activation block (XM != 0)] [item partials]
+    // XM 3 is XM 1 (rotate x in the prologue) with the router built in
+    constexpr int XP = XM == 3 ? 1 : XM;
 
     const int og = blockIdx.y;
     const int bt0 = blockIdx.z * BT;
     const int nb = min(BT, a.batch - bt0);
     const int64_t n = a.ng * 8;
-    const int x_rows = XM == 2 ? a.P : (XM == 1 ? nb : 0);
+    const int x_rows = XP == 2 ? a.P : (XP == 1 ? nb : 0);
     float* s_x = s_dyn;
-    float* s_part = s_dyn + (XM == 0 ? 0 : (XM == 2 ? a.P : BT) * n);
+    float* s_part = s_dyn + (XP == 0 ? 0 : (XP == 2 ? a.P : BT) * n);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -489,15 +542,19 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
 
     // the first task's index words do not depend on the activation: issue
     // their loads before the prologue so the HBM latency overlaps it
+    // fused router: this group's expert, before its first index words
+    int64_t e_rt = -1;
+    if constexpr (XM == 3) e_rt = route_pair(a, og, lane, wave);
     uint32_t c0[IT][GPL], c1[IT][GPL];
     bool valid[IT];
-    task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1, valid);
+    task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1, valid,
+                            e_rt);
 
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
         for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
     }
-    if constexpr (XM != 0) build_x<XM>(a, s_x, x_rows, n, og, bt0);
+    if constexpr (XP != 0) build_x<XP>(a, s_x, x_rows, n, og, bt0);
     if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
 
     float xs[BT][GPL * 8];
@@ -510,7 +567,7 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
         // stream overlaps the codebook gathers.
         const int64_t pair = og;
         bool bad;
-        const int64_t e = pair_expert(a, pair, bad);
+        const int64_t e = pair_expert(a, pair, bad, e_rt);
         const int64_t g0 = (int64_t)col * GPL;
         const bool lane_ok = g0 < a.ng;
         if constexpr (XM == 0) {
@@ -585,12 +642,13 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
         }
         uint32_t n0[IT][GPL], n1[IT][GPL];
         bool nvalid[IT];
-        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, n0, n1, nvalid);
+        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, n0, n1, nvalid,
+                                e_rt);
 
         const int pj = item / nch, c = item - (item / nch) * nch;
         const int64_t pair = (int64_t)og * a.P + pj;
         bool bad;
-        const int64_t e = pair_expert(a, pair, bad);
+        const int64_t e = pair_expert(a, pair, bad, e_rt);
         const int64_t g0 = c * kc + (int64_t)col * GPL;
         const bool lane_ok = g0 < a.ng;
         if (item != cur_item) {
@@ -600,7 +658,7 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
                                                       : (const void*)((const uint16_t*)a.x + xoff);
                 load_x<GPL, BT>(a, xb, g0, lane_ok, nb, xs);
             } else {
-                load_x_lds<GPL, BT>(s_x, XM == 2 ? pj : 0, n, g0, lane_ok, nb, a.xscale, xs);
+                load_x_lds<GPL, BT>(s_x, XP == 2 ? pj : 0, n, g0, lane_ok, nb, a.xscale, xs);
             }
             cur_item = item;
         }
@@ -763,6 +821,9 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
         else return hipErrorInvalidValue;
     case 2:
         if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
+        else return hipErrorInvalidValue;
+    case 3:
+        if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     default: return launch_one<CBT, S2, GPL, BT, IT, 0>(a, p, grid, shm, st);
     }

@@ -59,6 +59,17 @@ struct GemvCall {
     const int8_t* sign;
     int64_t hb;
     float xscale;
+    // fused router of the gate_up launch (see GemvArgs); r_logits null = off
+    const void* r_logits;
+    int r_ldt;
+    int64_t r_ne;
+    int r_k;
+    int r_pairs;
+    int64_t r_shared;
+    const void* r_gate;
+    int r_gdt;
+    int32_t* r_ids;
+    float* r_w;
 };
 
 int gemv_launch(const GemvCall& c);

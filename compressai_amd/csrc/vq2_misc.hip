@@ -2,6 +2,7 @@
 // top-k router with the shared-expert gate, rotated-space dequant and index
 // decode (gfx950).
 #include "vq2_common.hpp"
+#include "vq2_router.hpp"
 #include "vq2_internal.hpp"
 
 namespace vq2 {
@@ -85,66 +86,6 @@ int argmax_launch(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* 
 // softmax in fp32, then k rounds of a wave-wide (max probability, lowest id)
 // reduction; lane r keeps round r's probability for the renormalisation.
 // The shared-expert gate dot product is loaded alongside the logits.
-constexpr int ROUTER_MAX_E = 1024;
-constexpr int ROUTER_PER_LANE = ROUTER_MAX_E / 64;
-
-__device__ __forceinline__ float wave_max(float v) { return wave_max_all(v); }
-__device__ __forceinline__ float wave_sum(float v) { return wave_sum_all(v); }
-
-template <int DT>
-__device__ __forceinline__ float ld_t(const void* p, int64_t i)
-{
-    if constexpr (DT == VQ2_DT_F32) return ((const float*)p)[i];
-    else if constexpr (DT == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
-    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
-}
-
-template <int LT>
-__device__ __forceinline__ void router_load_logits(const void* logits, int64_t t, int64_t n_e, int lane,
-                                                   float (&p)[ROUTER_PER_LANE])
-{
-#pragma unroll
-    for (int j = 0; j < ROUTER_PER_LANE; j++) {
-        const int e = j * 64 + lane;
-        p[j] = ld_t<LT>(logits, t * n_e + (e < n_e ? e : 0));
-    }
-#pragma unroll
-    for (int j = 0; j < ROUTER_PER_LANE; j++)
-        if (j * 64 + lane >= n_e) p[j] = -INFINITY;
-}
-
-// gate . h_t: 16 gate and 16 h loads in flight per lane per chunk
-template <int GT, int HT>
-__device__ __forceinline__ float router_gate_dot(const void* gate, const void* h, int64_t t, int64_t hidden, int lane)
-{
-    float d = 0.0f;
-    for (int64_t i0 = 0; i0 < hidden; i0 += 16 * 64) {
-        float g[16], x[16];
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int64_t i = i0 + u * 64 + lane;
-            const int64_t ic = i < hidden ? i : 0;
-            g[u] = ld_t<GT>(gate, ic);
-            x[u] = ld_t<HT>(h, t * hidden + ic);
-        }
-#pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (i0 + u * 64 + lane < hidden) d = fmaf(g[u], x[u], d);
-    }
-    return d;
-}
-
-__device__ __forceinline__ float router_gate_dispatch(const void* gate, int g_dt, const void* h, int h_dt, int64_t t,
-                                                      int64_t hidden, int lane)
-{
-    if (g_dt == VQ2_DT_F16 && h_dt == VQ2_DT_F16) return router_gate_dot<VQ2_DT_F16, VQ2_DT_F16>(gate, h, t, hidden, lane);
-    if (g_dt == VQ2_DT_BF16 && h_dt == VQ2_DT_BF16) return router_gate_dot<VQ2_DT_BF16, VQ2_DT_BF16>(gate, h, t, hidden, lane);
-    if (g_dt == VQ2_DT_F32 && h_dt == VQ2_DT_F32) return router_gate_dot<VQ2_DT_F32, VQ2_DT_F32>(gate, h, t, hidden, lane);
-    float d = 0.0f;
-    for (int64_t i = lane; i < hidden; i += 64) d = fmaf(load_as_f32(gate, g_dt, i), load_as_f32(h, h_dt, t * hidden + i), d);
-    return d;
-}
-
 __global__ void __launch_bounds__(64) router_kernel(const void* logits, int l_dt, int64_t n_e, int k, const void* h,
                                                     int h_dt, int64_t hidden, const void* gate, int g_dt,
                                                     int64_t shared_id, int32_t* ids, float* w)
@@ -152,55 +93,21 @@ __global__ void __launch_bounds__(64) router_kernel(const void* logits, int l_dt
     const int64_t t = blockIdx.x;
     const int lane = threadIdx.x;
     const int row = k + (shared_id >= 0 ? 1 : 0);
-    float p[ROUTER_PER_LANE];
-    if (l_dt == VQ2_DT_F16)
-        router_load_logits<VQ2_DT_F16>(logits, t, n_e, lane, p);
-    else if (l_dt == VQ2_DT_BF16)
-        router_load_logits<VQ2_DT_BF16>(logits, t, n_e, lane, p);
+    float mine, tot;
+    int my_id;
+    if (n_e <= 256)
+        router_select<4>(logits, l_dt, t, n_e, k, lane, mine, my_id, tot);
     else
-        router_load_logits<VQ2_DT_F32>(logits, t, n_e, lane, p);
-    const float d = shared_id >= 0 ? router_gate_dispatch(gate, g_dt, h, h_dt, t, hidden, lane) : 0.0f;
-
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < ROUTER_PER_LANE; j++) m = fmaxf(m, p[j]);
-    m = wave_max(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < ROUTER_PER_LANE; j++) {
-        p[j] = (j * 64 + lane) < n_e ? __expf(p[j] - m) : 0.0f;
-        sum += p[j];
-    }
-    sum = wave_sum(sum);
-#pragma unroll
-    for (int j = 0; j < ROUTER_PER_LANE; j++) p[j] = (j * 64 + lane) < n_e ? p[j] / sum : -1.0f;
-
-    float mine = 0.0f;  // lane r: probability selected in round r
-    int my_id = 0;
-    for (int r = 0; r < k; r++) {
-        float bv = -1.0f;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < ROUTER_PER_LANE; j++) {
-            const int e = j * 64 + lane;
-            if (p[j] > bv || (p[j] == bv && e < bi)) { bv = p[j]; bi = e; }
-        }
-        wave_argmax_all(bv, bi);
-#pragma unroll
-        for (int j = 0; j < ROUTER_PER_LANE; j++)
-            if (j * 64 + lane == bi) p[j] = -2.0f;  // never selected again
-        if (lane == r) { mine = bv; my_id = bi; }
-    }
-    const float tot = wave_sum(lane < k ? mine : 0.0f);
+        router_select<ROUTER_MAX_E / 64>(logits, l_dt, t, n_e, k, lane, mine, my_id, tot);
     if (lane < k) {
         ids[t * row + lane] = my_id;
         w[t * row + lane] = mine / tot;
     }
     if (shared_id >= 0) {
-        const float dd = wave_sum(d);
+        const float sw = router_shared_weight(gate, g_dt, h, h_dt, t, hidden, lane);
         if (lane == 0) {
             ids[t * row + k] = (int32_t)shared_id;
-            w[t * row + k] = 1.0f / (1.0f + __expf(-dd));
+            w[t * row + k] = sw;
         }
     }
 }

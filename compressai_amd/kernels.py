@@ -38,6 +38,7 @@ __all__ = [
     "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
     "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine", "vq_moe_grouped",
     "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine", "vq_gemm_small_m",
+    "vq_moe_router_gate_up_rht",
     "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
     "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
     "optimize_deltanet_layers", "Vq2Error",
@@ -392,6 +393,35 @@ def vq_moe_gate_up_rht(h, ids, pool, cb16, pool_scale, y_out, OUT, NG, perm=None
               _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"), _p(pool_scale),
               _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
     return y_out
+
+
+def vq_moe_router_gate_up_rht(h, router_logits, top_k, pool, cb16, pool_scale, y_out, OUT, NG, shared_gate=None,
+                              shared_id=-1, perm=None, sign=None, hb=2048, rht_scale=None, rs=1.0):
+    """Router + grouped gate_up + activation RHT in one launch: token t = row
+    of h [T, NG*8], logits [T, E]; P = top_k (+1 with a shared expert).
+    y_out [T*P, >=OUT].  Returns (ids int32 [T, P], w fp32 [T, P]) exactly
+    as vq_router_topk for the down/combine launch."""
+    dev = _dev(h, router_logits, pool, cb16, pool_scale, y_out, perm, sign, shared_gate)
+    OUT, NG, k = int(OUT), int(NG), int(top_k)
+    pool = _moe_checks(pool, pool_scale, OUT, NG, "pool")
+    lg = _contig(router_logits, "router_logits")
+    hh = _contig(h, "h").reshape(-1, NG * 8)
+    T = hh.shape[0]
+    lg2 = lg.reshape(T, -1)
+    P = k + (1 if shared_id >= 0 else 0)
+    y2 = y_out.reshape(-1, y_out.shape[-1])
+    if y2.shape[0] < T * P or y2.shape[1] < OUT or y2.stride(1) != 1:
+        raise Vq2Error("y_out must be [>=T*P, >=OUT] with unit column stride")
+    ids = torch.empty((T, P), dtype=torch.int32, device=dev)
+    w = torch.empty((T, P), dtype=torch.float32, device=dev)
+    sg = _contig(shared_gate, "shared_gate") if shared_gate is not None else None
+    sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
+    _lib.call("vq2_moe_router_gate_up_rht", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc,
+              _p(lg2), _dt(lg2, "router_logits"), lg2.shape[1], k, _p(sg), _dt(sg, "shared_gate") if sg is not None else 0,
+              int(shared_id), _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"), _p(pool_scale),
+              _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _p(ids), _p(w),
+              _stream(dev))
+    return ids, w
 
 
 def vq_moe_down_swiglu_combine(gu, ids, w, down_idx, cb16, down_scale, OUT, NG, perm=None, sign=None, hb=None,

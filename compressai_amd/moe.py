@@ -20,8 +20,8 @@ synchronisation.
 ``MoELayer`` adds the router (softmax -> top-k -> renormalise on given
 logits) and the shared expert with its sigmoid gate (transformers 5.15.0
 ``Qwen3_5MoeTopKRouter`` / ``Qwen3_5MoeSparseMoeBlock``), the shared expert
-living in the same pool at id ``n_routed``.  The whole layer is three
-launches (router, gate_up, down) and no host synchronisation.
+living in the same pool at id ``n_routed``.  The whole layer is two
+launches (router + gate_up, down + combine) and no host synchronisation.
 
 Intermediates are fp32 by default (the parity contract); ``act_dtype`` may
 select bf16 to follow the reference's cast points instead.
@@ -102,7 +102,19 @@ class MoELayer(nn.Module):
         return K.vq_router_topk(router_logits, self.top_k, h, self.shared_gate, shared_id=self.n_routed)
 
     def forward(self, h, router_logits):
+        """Two launches: router + gate_up (+ RHT), then SwiGLU + RHT + down +
+        combine."""
         m = self.experts_mod
         h2 = h.reshape(-1, m.hidden_dim).contiguous()
-        ids, w = self.route(h2, router_logits.reshape(h2.shape[0], -1).contiguous())
-        return m.experts(h2, ids, w)
+        T = h2.shape[0]
+        I = m.intermediate_dim
+        P = self.top_k + 1
+        y_gu = torch.empty((T * P, 2 * I), dtype=m.act_dtype, device=h2.device)
+        ids, w = K.vq_moe_router_gate_up_rht(h2, router_logits.reshape(T, -1), self.top_k, m.gate_up_idx, m.cb16,
+                                             m.gate_up_scale, y_gu, OUT=2 * I, NG=m.hidden_dim // 8,
+                                             shared_gate=self.shared_gate, shared_id=self.n_routed,
+                                             perm=m.rot_h._perm32, sign=m.rot_h._sign8, hb=m.rot_h.hb,
+                                             rht_scale=m.rot_h.scale)
+        return K.vq_moe_down_swiglu_combine(y_gu, ids, w, m.down_idx, m.cb16, m.down_scale, OUT=m.hidden_dim,
+                                            NG=I // 8, perm=m.rot_i._perm32, sign=m.rot_i._sign8, hb=m.rot_i.hb,
+                                            rht_scale=m.rot_i.scale, out_dtype=m.out_dtype or torch.float32)

@@ -155,6 +155,26 @@ int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens,
                         void* y, int y_dt, int64_t y_pair_stride,
                         int64_t out_rows, int64_t ng, float rs, void* stream);
 
+/* vq2_moe_gate_up_rht with the router built in: every workgroup selects its
+ * pair's expert from the token's router logits (softmax over n_routed, top-k,
+ * renormalised; ties to the lower id, as vq2_router_topk) before it fetches
+ * codes, so the MoE layer needs no separate router launch.  Pair p of token t
+ * (P = k + 1 with a shared expert, else k) is slot p of the top-k, slot k the
+ * shared expert shared_id (-1: none) weighted sigmoid(shared_gate . h_t).
+ * Outputs the same ids / w (int32 / fp32 [tokens, P]) as vq2_router_topk,
+ * for vq2_moe_down_swiglu_combine.  Replaces Qwen3_5MoeTopKRouter.forward
+ * (HF:760-776) + rot_2048.fwd + vq_moe_parallel_gate_up
+ * (vq2/paged_runtime.py:495-500, vq2/kernels.py:246-254). */
+int vq2_moe_router_gate_up_rht(const void* h, int h_dt, int64_t tokens,
+                               const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                               const void* logits, int l_dt, int64_t n_routed, int k,
+                               const void* shared_gate, int g_dt, int64_t shared_id,
+                               const int16_t* pool, int64_t n_experts,
+                               const void* cb, int cb_dt, const void* pool_scale, int s_dt,
+                               void* y, int y_dt, int64_t y_pair_stride,
+                               int64_t out_rows, int64_t ng, float rs,
+                               int32_t* ids, float* w, void* stream);
+
 /* Grouped down projection fused with the weighted expert combine:
  *   out[t, r] = sum_{j < P} w[t*P+j] * (VQ(pool[ids[t*P+j]]) x_{t*P+j})[r]
  * with x_p = x + p * ng*8 and each term (acc * scale) * rs as in

@@ -509,3 +509,32 @@ def test_lm_head_argmax_small_m_batch(dev):
     for b in range(B):
         if int(idx[b]) != int(ref[b]):
             assert abs(y64[b, int(idx[b])] - y64[b, int(ref[b])]) <= TOL * np.abs(y64[b]).max()
+
+
+@pytest.mark.parametrize("E,k,shared,T", [(256, 8, True, 1), (256, 8, True, 8), (300, 4, False, 3),
+                                          (64, 2, True, 5)])
+def test_fused_router_gate_up_matches_router_and_unfused(dev, E, k, shared, T):
+    """vq2_moe_router_gate_up_rht: ids and weights bit-identical to the
+    standalone router (E > 256 takes the 16-logits-per-lane path), gate_up
+    rows identical to vq2_moe_gate_up_rht fed those ids."""
+    NG, OUT = 32, 128  # n = 256 (hb 256), 2I = 128
+    g = torch.Generator().manual_seed(4500 + E + T)
+    pool = torch.randint(-32768, 32768, (E + 1, OUT, NG), generator=g, dtype=torch.int32).to(torch.int16)
+    ps = (torch.rand(E + 1, OUT, generator=g) + 0.5).to(torch.float16)
+    cb = synth.codebook(4501)
+    h = synth.activations(4504 + T, (T, NG * 8))
+    logits = synth.activations(4507 + T, (T, E))
+    gate = synth.activations(4508, NG * 8) * 0.05
+    sign = synth.signs(4509, NG * 8)
+    sid = E if shared else -1
+    P = k + (1 if shared else 0)
+    pool_d, ps_d, cb_d, h_d, lg_d, gate_d, sign_d = _cuda(pool, ps, cb, h, logits, gate, sign, dev=dev)
+    y1 = torch.empty((T * P, OUT), dtype=torch.float32, device=dev)
+    ids, w = K.vq_moe_router_gate_up_rht(h_d, lg_d, k, pool_d, cb_d, ps_d, y1, OUT, NG, shared_gate=gate_d,
+                                         shared_id=sid, sign=sign_d, hb=256)
+    rid, rw = K.vq_router_topk(lg_d, k, h_d if shared else None, gate_d if shared else None, shared_id=sid)
+    assert torch.equal(ids.cpu(), rid.cpu().to(torch.int32))
+    assert torch.equal(w.cpu(), rw.cpu())
+    y2 = torch.empty_like(y1)
+    K.vq_moe_gate_up_rht(h_d, rid, pool_d, cb_d, ps_d, y2, OUT, NG, sign=sign_d, hb=256)
+    assert torch.equal(y1.cpu(), y2.cpu())
