@@ -189,9 +189,11 @@ int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride, const
     CHECK(x, "vq2_gemv_rht: NULL activation");
     CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_gemv_rht: bad dtype code");
     CHECK(x_stride >= n, "vq2_gemv_rht: x_stride < n");
-    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && n % hb == 0,
-          "vq2_gemv_rht: hb=%lld must be a power of two in [2, 8192] dividing n", (long long)hb);
-    if (int rr = check_rot_tables(perm, sign)) return rr;
+    CHECK(hb == 0 || (hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && n % hb == 0),
+          "vq2_gemv_rht: hb=%lld must be 0 (x already rotated) or a power of two in [2, 8192] dividing n",
+          (long long)hb);
+    if (hb)
+        if (int rr = check_rot_tables(perm, sign)) return rr;
     int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
     if (r) return r;
     GemvCall c = base_call(x, x_dt, s2_kind, cb0, cb1, cb_dt, s_dt, y_dt, n / 8, batch, rs, stream);
@@ -205,11 +207,11 @@ int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride, const
         CHECK(g.y_stride >= g.out_rows, "vq2_gemv_rht: segment %d y_stride < out_rows", s);
         c.seg[s] = GemvSegCall{g.idx0, g.idx1, g.scale, g.y, g.out_rows, g.y_stride};
     }
-    c.xm = 1;
+    c.xm = hb ? 1 : 0;
     c.perm = perm;
     c.sign = sign;
     c.hb = hb;
-    c.xscale = rht_scale;
+    c.xscale = hb ? rht_scale : 1.0f;
     return gemv_launch(c);
 }
 

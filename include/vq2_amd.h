@@ -109,8 +109,10 @@ typedef struct vq2_seg {
  *   xr[b] = RHT_fwd(x[b]) with perm/sign (nullable), hb-point blocks, scale
  *   segs[s].y[b, r] = (sum_k W_s[r, k] * xr[b, k]) * segs[s].scale[r] * rs
  * Every workgroup builds xr in LDS itself, so no rotated copy of x is written.
- * Requires n % 64 == 0, 16-byte aligned index planes and batch <= 2 (larger
- * batches: vq2_rht + vq2_gemv); segs is a host array.
+ * hb == 0: x is already rotated (perm, sign and rht_scale are ignored) --
+ * for n > 2048 a separate vq2_rht launch is cheaper than rotating n values
+ * in every workgroup.  Requires n % 64 == 0, 16-byte aligned index planes
+ * and batch <= 2 (larger batches: vq2_rht + vq2_gemv); segs is a host array.
  * Replaces FastRot + vq_gemv_16 / vq_gemv_16_8 of PackedLinear.forward
  * (vq2/runtime.py:91-104) and Rot.fwd + F.linear of its fallback
  * (vq2/runtime.py:105-110). */
