@@ -97,6 +97,9 @@ class MoELayer(nn.Module):
         self.top_k = int(top_k)
         self.shared_gate = shared_gate
         self.out_dtype = out_dtype
+        # down projection: one launch (SwiGLU + RHT in every workgroup) or a
+        # separate SwiGLU + RHT launch followed by the grouped down + combine
+        self.fused_down = True
 
     def route(self, h, router_logits):
         return K.vq_router_topk(router_logits, self.top_k, h, self.shared_gate, shared_id=self.n_routed)
@@ -115,6 +118,11 @@ class MoELayer(nn.Module):
                                              shared_gate=self.shared_gate, shared_id=self.n_routed,
                                              perm=m.rot_h._perm32, sign=m.rot_h._sign8, hb=m.rot_h.hb,
                                              rht_scale=m.rot_h.scale)
-        return K.vq_moe_down_swiglu_combine(y_gu, ids, w, m.down_idx, m.cb16, m.down_scale, OUT=m.hidden_dim,
-                                            NG=I // 8, perm=m.rot_i._perm32, sign=m.rot_i._sign8, hb=m.rot_i.hb,
-                                            rht_scale=m.rot_i.scale, out_dtype=m.out_dtype or torch.float32)
+        if self.fused_down:
+            return K.vq_moe_down_swiglu_combine(y_gu, ids, w, m.down_idx, m.cb16, m.down_scale, OUT=m.hidden_dim,
+                                                NG=I // 8, perm=m.rot_i._perm32, sign=m.rot_i._sign8,
+                                                hb=m.rot_i.hb, rht_scale=m.rot_i.scale,
+                                                out_dtype=m.out_dtype or torch.float32)
+        act = K.vq_swiglu_rht(y_gu, I, m.rot_i._perm32, m.rot_i._sign8, m.rot_i.hb, m.rot_i.scale)
+        return K.vq_moe_down_combine(act, ids, w, m.down_idx, m.cb16, m.down_scale, OUT=m.hidden_dim, NG=I // 8,
+                                     out_dtype=m.out_dtype or torch.float32)
