@@ -314,6 +314,30 @@ def bench_small_m(args, dev):
     return res
 
 
+def bench_unpack(args, dev):
+    """Container load: fixed-width packed index streams -> int16 planes
+    (vq2/export.py:56-70), 2^25 symbols per call; GB/s counts bytes read +
+    written."""
+    import torch
+
+    from compressai_amd import kernels as K
+
+    n = 1 << 25
+    g = torch.Generator(device=dev).manual_seed(6000)
+    res = {}
+    for bits in (12, 16):
+        nb = (n * bits + 7) // 8
+        buf = torch.randint(0, 256, (nb,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        out = torch.empty(n, dtype=torch.int16, device=dev)
+        gr = capture(lambda l: K.vq_unpack_fixed(buf, bits, n, out=out), 10, dev)
+        time_graph(gr, 1, dev)
+        ms, _ = time_graph(gr, 10, dev)
+        us = ms * 1e3 / 100
+        res[f"{bits}bit"] = {"us": round(us, 3), "gbps": round((nb + 2 * n) / (us * 1e-6) / 1e9, 1)}
+        log(f"unpack_fixed {bits}-bit, {n} symbols: {us:.2f} us, {res[f'{bits}bit']['gbps']:.0f} GB/s")
+    return res
+
+
 # -------------------------------------------------------------- CPU baseline
 def cpu_baseline(dl, budget_s=20.0):
     """The reference CPU path (PackedLinear fallback, fp32) on the host for
@@ -427,6 +451,7 @@ def main():
     lm1 = None if args.no_lmhead else bench_lm_head(args, dev, batch=1)
     lm4 = None if args.no_lmhead else bench_lm_head(args, dev, batch=4)
     sm = None if args.no_small_m else bench_small_m(args, dev)
+    up = None if args.no_small_m else bench_unpack(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(d["dense"])
 
     rec = {
@@ -456,6 +481,7 @@ def main():
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
         "small_m": sm,
+        "unpack_fixed": up,
         "roofline": {
             "kernel": "vq_gemv_kernel (fused RHT) gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1",
             "bound": "hbm",

@@ -53,6 +53,7 @@ SIGNATURES = {
                          _f32, _vp, _vp, _vp, _vp], _i32),
     "vq2_dequant_rows": ([_vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp], _i32),
     "vq2_decode_idx": ([_vp, _i32, _i64, _vp, _vp], _i32),
+    "vq2_unpack_fixed": ([_vp, _i64, _i32, _i64, _vp, _vp], _i32),
 }
 
 _lib = None

@@ -497,4 +497,13 @@ int vq2_decode_idx(const void* in, int is_u8, int64_t count, int32_t* out, void*
     return decode_launch(in, is_u8, count, out, stream);
 }
 
+int vq2_unpack_fixed(const uint8_t* buf, int64_t nbytes, int bits, int64_t n, int16_t* out, void* stream)
+{
+    clear_error();
+    CHECK(n >= 0 && nbytes >= 0, "vq2_unpack_fixed: bad sizes");
+    if (n == 0) return VQ2_OK;
+    CHECK(buf && out, "vq2_unpack_fixed: NULL pointer argument");
+    return unpack_fixed_launch(buf, nbytes, bits, n, out, stream);
+}
+
 }  // extern "C"

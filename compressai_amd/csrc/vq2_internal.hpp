@@ -118,6 +118,8 @@ int dequant_launch(const int16_t* idx0, const void* idx1, int s2, const void* cb
 
 int decode_launch(const void* in, int is_u8, int64_t count, int32_t* out, void* stream);
 
+int unpack_fixed_launch(const uint8_t* buf, int64_t nbytes, int bits, int64_t n, int16_t* out, void* stream);
+
 inline bool dt_ok(int dt) { return dt == VQ2_DT_F32 || dt == VQ2_DT_F16 || dt == VQ2_DT_BF16; }
 inline int64_t dt_size(int dt) { return dt == VQ2_DT_F32 ? 4 : 2; }
 

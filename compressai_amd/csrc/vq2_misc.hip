@@ -188,4 +188,95 @@ int decode_launch(const void* in, int is_u8, int64_t count, int32_t* out, void* 
     return VQ2_OK;
 }
 
+// ------------------------------------------------------------ unpack_fixed
+// Fixed-width symbol streams (vq2/export.py:39-70: pack_fixed / unpack_fixed)
+// into uint16 codes in int16 storage, the planes the GEMV reads.  The
+// packings are little-endian bit streams (4-bit: low nibble first; 12-bit:
+// pairs a | b << 12 in 3 bytes), so 8 symbols always fill `bits` bytes = a
+// whole number of dwords: one thread turns such a unit into one 16-byte
+// store.  Symbols past the last whole unit, and every symbol of a buffer that
+// is not 4-byte aligned, are decoded one by one from the bytes they occupy.
+template <int BITS>
+__device__ __forceinline__ void unpack_unit(const uint32_t* w, uint32_t (&c)[8])
+{
+    if constexpr (BITS == 16) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = (w[k >> 2] >> (8 * (k & 3))) & 0xFFu;
+    } else if constexpr (BITS == 4) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = (w[0] >> (4 * k)) & 0xFu;
+    } else {
+        const uint64_t lo = (uint64_t)w[0] | ((uint64_t)w[1] << 32);
+#pragma unroll
+        for (int k = 0; k < 5; k++) c[k] = (uint32_t)(lo >> (12 * k)) & 0xFFFu;
+        c[5] = (uint32_t)(lo >> 60) | ((w[2] & 0xFFu) << 4);
+        c[6] = (w[2] >> 8) & 0xFFFu;
+        c[7] = (w[2] >> 20) & 0xFFFu;
+    }
+}
+
+__device__ __forceinline__ uint32_t unpack_one(const uint8_t* b, int bits, int64_t i)
+{
+    if (bits == 16) return (uint32_t)b[2 * i] | ((uint32_t)b[2 * i + 1] << 8);
+    if (bits == 8) return b[i];
+    if (bits == 4) return (b[i >> 1] >> (4 * (i & 1))) & 0xFu;
+    const int64_t p = 3 * (i >> 1);  // 12-bit: pair i/2 at bytes 3p .. 3p+2
+    if ((i & 1) == 0) return (uint32_t)b[p] | (((uint32_t)b[p + 1] & 0xFu) << 8);
+    return ((uint32_t)b[p + 1] >> 4) | ((uint32_t)b[p + 2] << 4);
+}
+
+template <int BITS>
+__global__ void __launch_bounds__(256) unpack_fixed_kernel(const uint8_t* buf, int64_t n, int64_t units, int16_t* out)
+{
+    constexpr int WORDS = BITS / 4;  // dwords per 8-symbol unit
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += stride) {
+        const uint32_t* src = (const uint32_t*)buf + u * WORDS;
+        uint32_t w[WORDS];
+#pragma unroll
+        for (int k = 0; k < WORDS; k++) w[k] = __builtin_nontemporal_load(src + k);
+        uint32_t c[8];
+        unpack_unit<BITS>(w, c);
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) o[k] = c[2 * k] | (c[2 * k + 1] << 16);
+        __builtin_nontemporal_store(o, (u32x4*)(out + u * 8));
+    }
+    for (int64_t i = units * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = (int16_t)(uint16_t)unpack_one(buf, BITS, i);
+}
+
+int unpack_fixed_launch(const uint8_t* buf, int64_t nbytes, int bits, int64_t n, int16_t* out, void* stream)
+{
+    if (bits != 4 && bits != 8 && bits != 12 && bits != 16)
+        return set_error(VQ2_ERR_ARG, "vq2 unpack_fixed: bits=%d not in {4, 8, 12, 16}", bits);
+    if (n < 0 || nbytes < 0) return set_error(VQ2_ERR_ARG, "vq2 unpack_fixed: negative size");
+    const int64_t need = (n * bits + 7) / 8;
+    if (nbytes < need)
+        return set_error(VQ2_ERR_ARG, "vq2 unpack_fixed: %lld symbols of %d bits need %lld bytes, got %lld", (long long)n,
+                         bits, (long long)need, (long long)nbytes);
+    if (n == 0) return VQ2_OK;
+    // whole units need a 4-byte aligned stream and a 16-byte aligned output
+    const bool vec = (uintptr_t)buf % 4 == 0 && (uintptr_t)out % 16 == 0;
+    const int64_t units = vec ? n / 8 : 0;
+    const int64_t work = units > 0 ? units : n;
+    int64_t blocks = (work + 255) / 256;
+    const int64_t cap = 8LL * device_cu_count();
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    hipStream_t st = (hipStream_t)stream;
+    switch (bits) {
+    case 4: hipLaunchKernelGGL(unpack_fixed_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, buf, n, units, out); break;
+    case 8: hipLaunchKernelGGL(unpack_fixed_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, st, buf, n, units, out); break;
+    case 12: hipLaunchKernelGGL(unpack_fixed_kernel<12>, dim3((unsigned)blocks), dim3(256), 0, st, buf, n, units, out); break;
+    default: hipLaunchKernelGGL(unpack_fixed_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, st, buf, n, units, out); break;
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_hip_error(err, "vq2 unpack_fixed launch");
+    return VQ2_OK;
+}
+
 }  // namespace vq2

@@ -38,7 +38,7 @@ __all__ = [
     "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
     "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine", "vq_moe_grouped",
     "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine", "vq_gemm_small_m",
-    "vq_moe_router_gate_up_rht",
+    "vq_moe_router_gate_up_rht", "vq_unpack_fixed",
     "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
     "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
     "optimize_deltanet_layers", "Vq2Error",
@@ -626,4 +626,21 @@ def vq_decode_idx(idx):
     idx = _contig(idx, "idx")
     out = torch.empty(idx.shape, dtype=torch.int32, device=dev)
     _lib.call("vq2_decode_idx", _p(idx), is_u8, idx.numel(), _p(out), _stream(dev))
+    return out
+
+
+def vq_unpack_fixed(buf, bits, n, *, out=None):
+    """Fixed-width packed symbols (uint8 stream, bits in {4, 8, 12, 16}) ->
+    int16 [n] holding the uint16 codes, on the device (vq2/export.py:56-70
+    unpack_fixed, at container load time)."""
+    dev = _dev(buf, out)
+    if buf.dtype != torch.uint8:
+        raise Vq2Error("buf must be a uint8 tensor")
+    b = _contig(buf, "buf").reshape(-1)
+    n = int(n)
+    if out is None:
+        out = torch.empty(n, dtype=torch.int16, device=dev)
+    elif out.dtype != torch.int16 or out.numel() < n:
+        raise Vq2Error("out must be int16 with at least n elements")
+    _lib.call("vq2_unpack_fixed", _p(b), b.numel(), int(bits), n, _p(_contig(out, "out")), _stream(dev))
     return out

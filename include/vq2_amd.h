@@ -268,6 +268,13 @@ int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind,
  * value (uint8 planes, is_u8 != 0).  Replaces _as_index (vq2/runtime.py:32-35). */
 int vq2_decode_idx(const void* in, int is_u8, int64_t count, int32_t* out, void* stream);
 
+/* Fixed-width symbol stream -> uint16 codes (int16 storage, the planes the
+ * GEMV reads): n symbols of bits in {4, 8, 12, 16} from nbytes >=
+ * ceil(n * bits / 8) bytes, in the little-endian packing of
+ * vq2/export.py:39-53 (pack_fixed).  Replaces unpack_fixed
+ * (vq2/export.py:56-70) at container load time. */
+int vq2_unpack_fixed(const uint8_t* buf, int64_t nbytes, int bits, int64_t n, int16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -538,3 +538,41 @@ def test_fused_router_gate_up_matches_router_and_unfused(dev, E, k, shared, T):
     y2 = torch.empty_like(y1)
     K.vq_moe_gate_up_rht(h_d, rid, pool_d, cb_d, ps_d, y2, OUT, NG, sign=sign_d, hb=256)
     assert torch.equal(y1.cpu(), y2.cpu())
+
+
+# ------------------------------------------------------------ unpack_fixed
+def _pack(sym, bits):
+    """Little-endian fixed-width packing, built bit by bit (independent of
+    the byte formulas of the oracle and the kernel); 4- and 12-bit streams
+    are padded to whole symbol pairs as vq2/export.py:39-53 does."""
+    if bits in (4, 12) and len(sym) % 2:
+        sym = np.append(sym, 0)
+    nbits = len(sym) * bits
+    out = np.zeros((nbits + 7) // 8, np.uint8)
+    bitpos = np.arange(len(sym))[:, None] * bits + np.arange(bits)[None, :]
+    vals = (sym[:, None] >> np.arange(bits)[None, :]) & 1
+    np.add.at(out, bitpos.reshape(-1) // 8, (vals.reshape(-1) << (bitpos.reshape(-1) % 8)).astype(np.uint8))
+    return out[: (nbits + 7) // 8]
+
+
+@pytest.mark.parametrize("bits", [4, 8, 12, 16])
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 1000, 100003])
+def test_unpack_fixed_round_trip(dev, bits, n):
+    rng = np.random.default_rng(bits * 1000 + n)
+    sym = rng.integers(0, 1 << bits, n, dtype=np.int64)
+    buf = _pack(sym, bits)
+    got = K.vq_unpack_fixed(torch.from_numpy(buf).to(dev), bits, n).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got.astype(np.int64), sym)
+    assert np.array_equal(got.astype(np.int64), O.unpack_fixed(buf, bits, n))
+
+
+def test_unpack_fixed_misaligned_and_short(dev):
+    """A stream that starts at an odd byte takes the per-symbol path; a
+    buffer shorter than ceil(n * bits / 8) is refused."""
+    sym = np.random.default_rng(5).integers(0, 4096, 333, dtype=np.int64)
+    buf = np.concatenate([np.zeros(1, np.uint8), _pack(sym, 12)])
+    t = torch.from_numpy(buf).to(dev)
+    got = K.vq_unpack_fixed(t[1:], 12, 333).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got.astype(np.int64), sym)
+    with pytest.raises(K.Vq2Error):
+        K.vq_unpack_fixed(t[1:-2], 12, 333)
