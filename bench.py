@@ -338,6 +338,58 @@ def bench_unpack(args, dev):
     return res
 
 
+def bench_paged(args, dev, E=64, steps=200):
+    """Paged expert pool (config-4 expert shape, one layer of E experts in a
+    .vq2m file): T = 1, top-8 routed ids on the device each step.  Warm: every
+    expert resident; churn: 16 slots, so most steps page experts in through
+    the pinned ring.  Host-timed (the paging decision reads the ids on the
+    host, so these steps are not graph-captured)."""
+    import shutil
+    import tempfile
+    import time
+
+    import torch
+
+    from compressai_amd import paged, synth
+
+    g = torch.Generator().manual_seed(7000)
+    gui = torch.randint(-32768, 32768, (E, 1024, 256), generator=g, dtype=torch.int32).to(torch.int16)
+    gus = (torch.rand(E, 1024, generator=g) + 0.5).to(torch.float16)
+    dni = torch.randint(-32768, 32768, (E, 2048, 64), generator=g, dtype=torch.int32).to(torch.int16)
+    dns = (torch.rand(E, 2048, generator=g) + 0.5).to(torch.float16)
+    tmp = tempfile.mkdtemp(prefix="vq2m_")
+    res = {}
+    try:
+        path = os.path.join(tmp, "layer.vq2m")
+        paged.write_vq2m(path, [gui], [gus], [dni], [dns])
+        store = paged.Vq2mStore(path)
+        cb = synth.codebook(7001).to(dev)
+        ids = torch.stack([torch.randperm(E, generator=g)[:8] for _ in range(steps)]).to(dev)
+        w = torch.full((1, 8), 1.0 / 8, device=dev)
+        h = synth.activations(7004, (1, 2048), dtype=torch.float16).to(dev)
+        for name, cap in (("warm", E), ("churn", 16)):
+            layer = paged.PagedMoEExperts(0, store, cb, capacity=cap, device=dev, out_dtype=torch.float32)
+            for s_ in range(min(steps, 2 * E)):  # fill the pool / reach the steady state
+                layer(h, ids[s_ % steps].view(1, 8), w)
+            torch.cuda.synchronize(dev)
+            m0 = layer.pager.misses
+            t0 = time.perf_counter()
+            for s_ in range(steps):
+                layer(h, ids[s_].view(1, 8), w)
+            torch.cuda.synchronize(dev)
+            dt = time.perf_counter() - t0
+            misses = layer.pager.misses - m0
+            res[name] = {"us_per_layer": round(dt * 1e6 / steps, 2), "misses_per_step": round(misses / steps, 2),
+                         "feed_gbps": round(misses * store.record_bytes / dt / 1e9, 2)}
+            log(f"paged MoE ({name}, {cap} slots of {E}): {res[name]['us_per_layer']:.1f} us/layer, "
+                f"{res[name]['misses_per_step']:.2f} misses/step, {res[name]['feed_gbps']:.2f} GB/s fed")
+            del layer
+        store.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return res
+
+
 # -------------------------------------------------------------- CPU baseline
 def cpu_baseline(dl, budget_s=20.0):
     """The reference CPU path (PackedLinear fallback, fp32) on the host for
@@ -452,6 +504,7 @@ def main():
     lm4 = None if args.no_lmhead else bench_lm_head(args, dev, batch=4)
     sm = None if args.no_small_m else bench_small_m(args, dev)
     up = None if args.no_small_m else bench_unpack(args, dev)
+    pgd = None if args.no_moe else bench_paged(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(d["dense"])
 
     rec = {
@@ -482,6 +535,7 @@ def main():
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
         "small_m": sm,
         "unpack_fixed": up,
+        "paged_moe_t1": pgd,
         "roofline": {
             "kernel": "vq_gemv_kernel (fused RHT) gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1",
             "bound": "hbm",

@@ -1,0 +1,287 @@
+"""Paged expert-pool feed for the MoE decode path (reference: vq2/paged_runtime.py).
+
+``Vq2mStore`` reads the ``.vq2m`` container the reference writes
+(vq2/pack_35b_to_vq2m.py:22-25, 225-244; reader vq2/paged_runtime.py:49-123):
+a 64-byte header ``<4sHHHH QQQQQ 12s`` (magic ``VQ2M``, version 1, layers,
+experts, table and meta offsets, payload start), one ``<QIQIQIQI`` entry per
+(layer, expert) -- offset and size of the gate_up index plane, its fp16 scales,
+the down index plane and its scales -- and a JSON meta block.  Each expert's
+four tensors are written back to back, so one read fetches the whole record
+(792,576 bytes at the config-4 shape).  ``write_vq2m`` writes the same layout
+(for tests and benchmarks).
+
+``PagedMoEExperts`` is the drop-in for ``PagedMoEExpert``
+(vq2/paged_runtime.py:316-568): ``forward(hidden_states [T, H], topk_idx
+[T, K], topk_weights [T, K])`` over a device pool of ``capacity`` expert
+slots managed LRU (``_get_slot``, vq2/paged_runtime.py:415-437).  Where the
+reference reads each missing expert synchronously through one reused pinned
+buffer and hands the kernels a slot list built element by element, here:
+
+* missing records are read (``os.preadv``) into a ring of pinned staging
+  records and copied to their slots on a dedicated copy stream; a staging
+  record is reused only after the event of its previous copy has completed;
+* the copy stream first waits for the work already queued on the compute
+  stream (a slot being evicted may still be read by the previous layer's
+  launch), and the compute stream waits for the copies through one event: no
+  host synchronisation besides the one read of the routed ids that the
+  host-side paging decision needs;
+* the slot ids of all (token, expert) pairs go to the device in one copy, and
+  the two grouped launches of ``ResidentMoEExperts`` (gate_up with the RHT,
+  SwiGLU + RHT + down + combine) run unchanged on the slot pool -- the pool
+  keeps the container's fp16 scales, the kernels read them directly.
+
+Promoted 3-bit experts (``expert_modes``, vq2/paged_runtime.py:357-389) are
+not handled by this feed: the store reports them and the layer refuses them.
+"""
+from __future__ import annotations
+
+import json
+import os
+import struct
+from collections import OrderedDict
+
+import torch
+
+from . import kernels as K
+from .rot import get_rot
+
+MAGIC = b"VQ2M"
+VERSION = 1
+HEADER_FORMAT = "<4sHHHH QQQQQ 12s"
+ENTRY_FORMAT = "<QIQIQIQI"
+HEADER_SIZE = struct.calcsize(HEADER_FORMAT)
+ENTRY_SIZE = struct.calcsize(ENTRY_FORMAT)
+
+
+class Vq2mStore:
+    """Reader of a ``.vq2m`` container (offset mode: no mapping of the file)."""
+
+    def __init__(self, path):
+        self.path = str(path)
+        self.fd = os.open(self.path, os.O_RDONLY)
+        head = os.pread(self.fd, HEADER_SIZE, 0)
+        if len(head) != HEADER_SIZE:
+            raise ValueError(f"{self.path}: truncated header")
+        (magic, version, self.num_layers, self.num_experts, _, table_off, table_len, meta_off, meta_len,
+         self.payload_start, _) = struct.unpack(HEADER_FORMAT, head)
+        if magic != MAGIC or version != VERSION:
+            raise ValueError(f"{self.path}: not a version-{VERSION} .vq2m container")
+        if table_len != self.num_layers * self.num_experts * ENTRY_SIZE:
+            raise ValueError(f"{self.path}: expert table of {table_len} bytes for "
+                             f"{self.num_layers} x {self.num_experts} entries")
+        table = os.pread(self.fd, table_len, table_off)
+        entries = list(struct.iter_unpack(ENTRY_FORMAT, table))
+        self.entries = [entries[l * self.num_experts:(l + 1) * self.num_experts] for l in range(self.num_layers)]
+        self.meta = json.loads(os.pread(self.fd, meta_len, meta_off).decode("utf-8"))
+        self.gu_rows = int(self.meta.get("gu_rows", 1024))
+        self.gu_cols = int(self.meta.get("gu_cols", 256))
+        self.dn_rows = int(self.meta.get("dn_rows", 2048))
+        self.dn_cols = int(self.meta.get("dn_cols", 64))
+        self.expert_modes = self.meta.get("expert_modes", {})
+        # byte sizes of one 2 bpw record (index planes int16, scales fp16)
+        self.sizes = (self.gu_rows * self.gu_cols * 2, self.gu_rows * 2, self.dn_rows * self.dn_cols * 2,
+                      self.dn_rows * 2)
+        self.record_bytes = sum(self.sizes)
+
+    def promoted(self, layer: int, expert: int) -> bool:
+        return self.expert_modes.get(f"{layer}:{expert}") == 3
+
+    def read_record(self, layer: int, expert: int, dst: memoryview) -> None:
+        """Read the expert's [gate_up idx | gate_up scale | down idx | down
+        scale] record into dst (record_bytes long)."""
+        e = self.entries[layer][expert]
+        offs, szs = e[0::2], e[1::2]
+        if tuple(szs) != self.sizes:
+            raise ValueError(f"layer {layer} expert {expert}: record sizes {szs} are not a 2 bpw expert {self.sizes}"
+                             + (" (promoted 3-bit expert)" if self.promoted(layer, expert) else ""))
+        contiguous = all(offs[i] + szs[i] == offs[i + 1] for i in range(3))
+        if contiguous:
+            got = os.preadv(self.fd, [dst[:self.record_bytes]], offs[0])
+            if got != self.record_bytes:
+                raise IOError(f"short read of layer {layer} expert {expert}")
+            return
+        pos = 0
+        for off, sz in zip(offs, szs):
+            if os.preadv(self.fd, [dst[pos:pos + sz]], off) != sz:
+                raise IOError(f"short read of layer {layer} expert {expert}")
+            pos += sz
+
+    def close(self):
+        if self.fd >= 0:
+            os.close(self.fd)
+            self.fd = -1
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def write_vq2m(path, gate_up_idx, gate_up_scale, down_idx, down_scale, meta=None, payload_start=4096):
+    """Write a container with the reference's layout: tensors per layer of
+    shape [E, gu_rows, gu_cols] int16, [E, gu_rows] fp16, [E, dn_rows,
+    dn_cols] int16, [E, dn_rows] fp16 (lists over layers, CPU tensors)."""
+    L = len(gate_up_idx)
+    E, gu_rows, gu_cols = gate_up_idx[0].shape
+    _, dn_rows, dn_cols = down_idx[0].shape
+    m = {"gu_rows": gu_rows, "gu_cols": gu_cols, "dn_rows": dn_rows, "dn_cols": dn_cols}
+    m.update(meta or {})
+    meta_bytes = json.dumps(m).encode("utf-8")
+    table_off = HEADER_SIZE
+    table_len = L * E * ENTRY_SIZE
+    meta_off = table_off + table_len
+    start = max(payload_start, (meta_off + len(meta_bytes) + 4095) // 4096 * 4096)
+    entries = []
+    with open(path, "wb") as f:
+        f.seek(start)
+        for l in range(L):
+            for e in range(E):
+                ent = []
+                for t in (gate_up_idx[l][e].to(torch.int16), gate_up_scale[l][e].to(torch.float16),
+                          down_idx[l][e].to(torch.int16), down_scale[l][e].to(torch.float16)):
+                    b = t.contiguous().view(torch.uint8).numpy().tobytes()
+                    ent += [f.tell(), len(b)]
+                    f.write(b)
+                entries.append(struct.pack(ENTRY_FORMAT, *ent))
+        f.seek(0)
+        f.write(struct.pack(HEADER_FORMAT, MAGIC, VERSION, L, E, 0, table_off, table_len, meta_off, len(meta_bytes),
+                            start, b"\0" * 12))
+        f.write(b"".join(entries))
+        f.write(meta_bytes)
+
+
+class ExpertPager:
+    """Device pool of `capacity` expert slots of one layer, filled from a
+    Vq2mStore, LRU replacement (vq2/paged_runtime.py:415-437)."""
+
+    def __init__(self, store: Vq2mStore, layer: int, capacity: int, device, staging: int = 16):
+        self.store, self.layer, self.capacity = store, int(layer), int(capacity)
+        self.device = torch.device(device)
+        s = store
+        self.pool_gu_idx = torch.empty((capacity, s.gu_rows, s.gu_cols), dtype=torch.int16, device=self.device)
+        self.pool_gu_scale = torch.empty((capacity, s.gu_rows), dtype=torch.float16, device=self.device)
+        self.pool_dn_idx = torch.empty((capacity, s.dn_rows, s.dn_cols), dtype=torch.int16, device=self.device)
+        self.pool_dn_scale = torch.empty((capacity, s.dn_rows), dtype=torch.float16, device=self.device)
+        self.slot_of: OrderedDict[int, int] = OrderedDict()  # expert -> slot, least recently used first
+        self.free = list(range(capacity - 1, -1, -1))
+        self.hits = self.misses = 0
+        cuda = self.device.type == "cuda"
+        self.cuda = cuda
+        self.ring = [torch.empty(s.record_bytes, dtype=torch.uint8, pin_memory=cuda) for _ in range(staging)]
+        self.ring_event = [None] * staging
+        self.ring_pos = 0
+        self.copy_stream = torch.cuda.Stream(device=self.device) if cuda else None
+
+    def _slot(self, expert: int, pending: list) -> int:
+        if expert in self.slot_of:
+            self.hits += 1
+            self.slot_of.move_to_end(expert)
+            return self.slot_of[expert]
+        self.misses += 1
+        # with at most `capacity` distinct experts per step the least recently
+        # used resident expert is never one this step needs
+        slot = self.free.pop() if self.free else self.slot_of.popitem(last=False)[1]
+        self.slot_of[expert] = slot
+        pending.append((expert, slot))
+        return slot
+
+    def ensure(self, experts) -> list:
+        """Slots of `experts` (host ints), loading the missing ones; on a GPU
+        the copies are queued and the current stream is made to wait for them.
+        A request that cannot be served changes nothing; a failed read drops
+        the experts it was loading from the pool."""
+        ex = [int(e) for e in experts]
+        for e in ex:
+            if not 0 <= e < self.store.num_experts:
+                raise K.Vq2Error(f"expert id {e} outside [0, {self.store.num_experts})")
+        if len(set(ex)) > self.capacity:
+            raise RuntimeError(f"{len(set(ex))} distinct experts in one step exceed the pool capacity {self.capacity}")
+        pending: list = []
+        slots = [self._slot(e, pending) for e in ex]
+        if pending:
+            try:
+                self._load(pending)
+            except BaseException:
+                for e, slot in pending:
+                    if self.slot_of.get(e) == slot:
+                        del self.slot_of[e]
+                        self.free.append(slot)
+                raise
+        return slots
+
+    def _load(self, pending):
+        s = self.store
+        a, b, c = s.sizes[0], s.sizes[0] + s.sizes[1], s.sizes[0] + s.sizes[1] + s.sizes[2]
+        if not self.cuda:
+            for expert, slot in pending:
+                buf = self.ring[0]
+                s.read_record(self.layer, expert, memoryview(buf.numpy()))
+                self._scatter(buf, slot, a, b, c)
+            return
+        compute = torch.cuda.current_stream(self.device)
+        # slots being overwritten may still be read by launches already queued
+        self.copy_stream.wait_stream(compute)
+        for expert, slot in pending:
+            i = self.ring_pos
+            self.ring_pos = (i + 1) % len(self.ring)
+            if self.ring_event[i] is not None:
+                self.ring_event[i].synchronize()  # the staging record's previous copy
+            buf = self.ring[i]
+            s.read_record(self.layer, expert, memoryview(buf.numpy()))
+            with torch.cuda.stream(self.copy_stream):
+                self._scatter(buf, slot, a, b, c)
+                ev = torch.cuda.Event()
+                ev.record(self.copy_stream)
+            self.ring_event[i] = ev
+        compute.wait_stream(self.copy_stream)
+
+    def _scatter(self, buf, slot, a, b, c):
+        s = self.store
+        nb = self.cuda
+        self.pool_gu_idx[slot].copy_(buf[:a].view(torch.int16).view(s.gu_rows, s.gu_cols), non_blocking=nb)
+        self.pool_gu_scale[slot].copy_(buf[a:b].view(torch.float16), non_blocking=nb)
+        self.pool_dn_idx[slot].copy_(buf[b:c].view(torch.int16).view(s.dn_rows, s.dn_cols), non_blocking=nb)
+        self.pool_dn_scale[slot].copy_(buf[c:].view(torch.float16), non_blocking=nb)
+
+
+class PagedMoEExperts(torch.nn.Module):
+    """Routed experts of one MoE layer over a paged device pool:
+    forward(hidden_states [T, H], topk_idx [T, K], topk_weights [T, K]) ->
+    [T, H] (vq2/paged_runtime.py:439-568, T == 1 fast path 491-511)."""
+
+    def __init__(self, layer: int, store: Vq2mStore, cb16, capacity: int = 96, device="cuda", staging: int = 16,
+                 act_dtype=torch.float32, out_dtype=None):
+        super().__init__()
+        self.pager = ExpertPager(store, layer, capacity, device, staging)
+        self.cb16 = cb16
+        self.hidden_dim = store.gu_cols * 8
+        self.intermediate_dim = store.dn_cols * 8
+        if store.gu_rows != 2 * self.intermediate_dim or store.dn_rows != self.hidden_dim:
+            raise K.Vq2Error("inconsistent gate_up / down shapes in the container")
+        dev = torch.device(device)
+        self.rot_h = get_rot("moe_expert_2048", self.hidden_dim, dev)
+        self.rot_i = get_rot("moe_expert_512", self.intermediate_dim, dev)
+        self.act_dtype = act_dtype
+        self.out_dtype = out_dtype
+
+    def forward(self, hidden_states, topk_idx, topk_weights):
+        p = self.pager
+        h = hidden_states.reshape(-1, self.hidden_dim).contiguous()
+        T = h.shape[0]
+        ids_host = topk_idx.reshape(T, -1).to("cpu")  # the paging decision is made on the host
+        P = ids_host.shape[1]
+        slots = p.ensure(ids_host.reshape(-1).tolist())
+        slot_t = torch.tensor(slots, dtype=torch.int32, pin_memory=p.cuda).view(T, P)
+        slot_d = slot_t.to(h.device, non_blocking=True)
+        w = topk_weights.reshape(T, P).to(device=h.device, dtype=torch.float32).contiguous()
+        I = self.intermediate_dim
+        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
+        K.vq_moe_gate_up_rht(h, slot_d, p.pool_gu_idx, self.cb16, p.pool_gu_scale, y_gu, OUT=2 * I,
+                             NG=self.hidden_dim // 8, perm=self.rot_h._perm32, sign=self.rot_h._sign8,
+                             hb=self.rot_h.hb, rht_scale=self.rot_h.scale)
+        out = K.vq_moe_down_swiglu_combine(y_gu, slot_d, w, p.pool_dn_idx, self.cb16, p.pool_dn_scale,
+                                           OUT=self.hidden_dim, NG=I // 8, perm=self.rot_i._perm32,
+                                           sign=self.rot_i._sign8, hb=self.rot_i.hb, rht_scale=self.rot_i.scale,
+                                           out_dtype=torch.float32)
+        return out.to(self.out_dtype or hidden_states.dtype)

@@ -576,3 +576,33 @@ def test_unpack_fixed_misaligned_and_short(dev):
     assert np.array_equal(got.astype(np.int64), sym)
     with pytest.raises(K.Vq2Error):
         K.vq_unpack_fixed(t[1:-2], 12, 333)
+
+
+# ------------------------------------------------------- paged expert pool
+def test_paged_experts_match_resident_pool(dev, tmp_path):
+    """PagedMoEExperts (container -> pinned ring -> slot pool, LRU with
+    evictions) gives the resident pool's outputs over a sequence of steps."""
+    from compressai_amd import paged
+    from compressai_amd.moe import ResidentMoEExperts
+    E = 16
+    g = torch.Generator().manual_seed(4600)
+    gui = torch.randint(-32768, 32768, (E, 1024, 256), generator=g, dtype=torch.int32).to(torch.int16)
+    gus = (torch.rand(E, 1024, generator=g) + 0.5).to(torch.float16)
+    dni = torch.randint(-32768, 32768, (E, 2048, 64), generator=g, dtype=torch.int32).to(torch.int16)
+    dns = (torch.rand(E, 2048, generator=g) + 0.5).to(torch.float16)
+    path = tmp_path / "moe.vq2m"
+    paged.write_vq2m(path, [gui], [gus], [dni], [dns])
+    cb = synth.codebook(4601).to(dev)
+    store = paged.Vq2mStore(path)
+    pg = paged.PagedMoEExperts(0, store, cb, capacity=6, device=dev, staging=3, out_dtype=torch.float32)
+    res = ResidentMoEExperts(gui.to(dev), gus.to(dev), dni.to(dev), dns.to(dev), cb, out_dtype=torch.float32)
+    for step in range(8):
+        T = 1 + step % 3
+        ids = torch.stack([torch.randperm(E, generator=g)[:2] for _ in range(T)]).to(torch.int64)
+        w = torch.softmax(torch.randn(T, 2, generator=g), -1)
+        h = synth.activations(4610 + step, (T, 2048), dtype=torch.float16)
+        yp = pg(h.to(dev), ids.to(dev), w.to(dev))
+        yr = res(h.to(dev), ids.to(dev), w.to(dev))
+        assert torch.equal(yp.cpu(), yr.cpu()), step
+    assert pg.pager.misses > 6 and pg.pager.hits > 0  # evictions happened and some experts stayed
+    store.close()
