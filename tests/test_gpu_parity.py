@@ -606,3 +606,49 @@ def test_paged_experts_match_resident_pool(dev, tmp_path):
         assert torch.equal(yp.cpu(), yr.cpu()), step
     assert pg.pager.misses > 6 and pg.pager.hits > 0  # evictions happened and some experts stayed
     store.close()
+
+
+# ------------------------------------------------------------ graph capture
+def test_decode_step_graph_replays_match_eager(dev):
+    """One decode step -- fused q/k/v (PackedLinear, batch 1), a 4 bpw
+    projection, the MoE layer (router inside gate_up) and the LM-head top-1 --
+    captured once; every replay, with eager work and synchronisations between
+    replays, equals the eager step on the same input."""
+    from compressai_amd.graph import DecodeStepGraph
+    from compressai_amd.moe import MoELayer
+    from compressai_amd.runtime import PackedLinear
+
+    n = 2048
+    cbs = {"16": synth.codebook(4700).to(dev), "16_16": synth.codebook(4701).to(dev)}
+    mq = synth.vq_matrix(4700, 1024, n, bpw=2)
+    mg = synth.vq_matrix(4710, 768, n, bpw=4)
+    lin_q = PackedLinear((1024, n), (16,), "layers.0.self_attn.q_proj", [mq["idx0"]], mq["scale"], cbs, dev)
+    lin_g = PackedLinear((768, n), (16, 16), "layers.0.mlp.gate_proj", [mg["idx0"], mg["idx1"]], mg["scale"], cbs,
+                         dev)
+    E, k = 32, 4
+    gu, gus, dn, dns = _pools(4720, E + 1)
+    moe = MoELayer(*_cuda(gu, gus, dn, dns, cbs["16"], synth.activations(4721, n) * 0.02, dev=dev), top_k=k)
+    head_m = synth.vq_matrix(4730, 4096, n, bpw=2)
+    head = PackedLinear((4096, n), (16,), "lm_head", [head_m["idx0"]], head_m["scale"], cbs, dev)
+
+    def step(x, logits):
+        q = lin_q(x, out_dtype=torch.float32)
+        gt = lin_g(x, out_dtype=torch.float32)
+        y = moe(x, logits)
+        xr = head.rot.fwd(x.reshape(1, n), out_dtype=torch.float32)
+        i0, _, cb0, _ = head._planes()
+        idx, val = K.vq_gemv_argmax(xr, i0, None, cb0, None, head.scale, 4096, n)
+        return q, gt, y, idx, val
+
+    x0 = synth.activations(4740, (1, n)).to(dev)
+    l0 = synth.activations(4741, (1, E)).to(dev)
+    gstep = DecodeStepGraph(step, [x0, l0])
+    for r in range(4):
+        x = synth.activations(4750 + r, (1, n)).to(dev)
+        lg = synth.activations(4760 + r, (1, E)).to(dev)
+        ref = [t.clone() for t in step(x, lg)]
+        torch.cuda.synchronize()
+        out = [t.clone() for t in gstep(x, lg)]
+        torch.cuda.synchronize()
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), r
