@@ -18,7 +18,8 @@
 //    64 contiguous bytes per row), and k-step t uses group 8q + t.
 //  * A is the activation, staged in LDS as fp16 with a power-of-two scale per
 //    (row, split): fp16 then holds any fp32 range at full fp16 precision, and
-//    the scale is divided out of the fp32 partial exactly.  fp16 codebooks
+//    the scale is divided out of the fp32 partial exactly (fp16 activations
+//    are copied as they are).  fp16 codebooks
 //    are used as they are; bf16 / fp32 centroids are rounded to fp16.  The
 //    accumulation is fp32.
 //  * A workgroup is 4 waves x 16 output rows over one K split; the split
@@ -30,6 +31,8 @@
 // F.linear (vq2/runtime.py:82-89, 105-110), for the (16,), (16,8) and (16,16)
 // index configurations.
 #include <stdlib.h>
+
+#include <mutex>
 
 #include "vq2_gemv_kernel.hpp"
 
@@ -140,6 +143,17 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
     // stage this split's activation: thread owns groups tid + j * MM_THREADS
     // of the [MP][gcount] chunk (rows >= m are zero)
     const int tot = MP * gcount;
+    if (a.x_dt == VQ2_DT_F16) {
+        // fp16 activations are exact in fp16: copied as they are, scale 1
+        const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int t = tid; t < tot; t += MM_THREADS) {
+            const int mr = t / gcount, g = t - mr * gcount;
+            s_xh[mr * xsg + g] =
+                mr < a.m ? *(const half8_t*)((const _Float16*)a.x + (int64_t)mr * a.x_stride + (g_begin + g) * 8)
+                         : zero8;
+        }
+        if (tid < MP) s_e[tid] = 0;
+    } else {
     float v[MM_STAGE][8];
 #pragma unroll
     for (int j = 0; j < MM_STAGE; j++) {
@@ -177,6 +191,7 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
             for (int k = 0; k < 8; k++) h[k] = (_Float16)ldexpf(v[j][k], e);
             s_xh[mr * xsg + g] = h;
         }
+    }
     }
     __syncthreads();
 
@@ -261,12 +276,22 @@ struct GemmPlan {
     int64_t rowtiles;
 };
 
-static GemmPlan plan_gemm(int64_t m, int64_t out_rows, int64_t ng, int num_cu)
+// LDS a workgroup may take for its activation chunk: four stay resident per
+// CU (measured: a single-split 65 KiB plan halves occupancy and slows the
+// batch-4 LM head by 4 %; larger K splits win on some shapes and lose on
+// others, so the plan keeps at least two workgroups' worth of splits per CU)
+constexpr int MM_LDS_BUDGET = 40 * 1024;
+
+// x_f16: fp16 activations are copied straight to LDS, so only LDS bounds the
+// K split; other dtypes are staged through MM_STAGE registers per thread.
+static GemmPlan plan_gemm(int64_t m, int64_t out_rows, int64_t ng, int num_cu, bool x_f16)
 {
     GemmPlan p;
     p.mt = (int)((m + 15) / 16);
     const int mp = p.mt * 16;
-    int kmax = MM_MAX_XG / mp / MM_TILE_G * MM_TILE_G;
+    const int k_lds = (MM_LDS_BUDGET / (mp * (int)sizeof(half8_t)) - 1) / MM_TILE_G * MM_TILE_G;
+    const int k_reg = MM_MAX_XG / mp / MM_TILE_G * MM_TILE_G;
+    int kmax = x_f16 ? k_lds : (k_reg < k_lds ? k_reg : k_lds);
     if (kmax < MM_TILE_G) kmax = MM_TILE_G;
     const int64_t ng_t = (ng + MM_TILE_G - 1) / MM_TILE_G * MM_TILE_G;
     int kcg = (int)(ng_t < kmax ? ng_t : kmax);
@@ -286,13 +311,22 @@ static GemmPlan plan_gemm(int64_t m, int64_t out_rows, int64_t ng, int num_cu)
 size_t gemm_small_m_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng)
 {
     if (m < 1 || out_rows < 1 || ng < 1) return 0;
-    const GemmPlan p = plan_gemm(m, out_rows, ng, device_cu_count());
+    // the register-staged plan has the most K splits: enough for any dtype
+    const GemmPlan p = plan_gemm(m, out_rows, ng, device_cu_count(), false);
     return p.splits > 1 ? (size_t)p.splits * m * out_rows * sizeof(float) : 0;
 }
 
 template <int CBT, int S2, int MT>
 static hipError_t launch_mm(const GemmArgs& a, dim3 grid, size_t shm, hipStream_t st)
 {
+    // opt in to more than 64 KiB of dynamic LDS, once per instantiation
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)vq_gemm_mfma_kernel<CBT, S2, MT>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, MM_LDS_BUDGET);
+    });
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL((vq_gemm_mfma_kernel<CBT, S2, MT>), grid, dim3(MM_THREADS), shm, st, a);
     return hipGetLastError();
 }
@@ -329,7 +363,7 @@ int gemm_small_m_launch(const GemmCall& c)
     const int64_t esz = dt_size(c.x_dt);
     if ((uintptr_t)c.x % 16 || (c.x_stride * esz) % 16)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 small-M GEMM: activation rows must be 16-byte aligned");
-    const GemmPlan p = plan_gemm(c.m, c.out_rows, c.ng, device_cu_count());
+    const GemmPlan p = plan_gemm(c.m, c.out_rows, c.ng, device_cu_count(), c.x_dt == VQ2_DT_F16);
     if (p.rowtiles > 0x7FFFFFFF || p.splits > 65535)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 small-M GEMM: shape too large");
     GemmArgs a{};
