@@ -468,6 +468,31 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride, co
     clear_error();
     CHECK(out_rows > 0, "vq2_gemv_argmax: out_rows must be > 0");
     CHECK(logits_ws && out_idx, "vq2_gemv_argmax: NULL workspace/output");
+    CHECK((uintptr_t)logits_ws % 8 == 0 && (uintptr_t)out_idx % 8 == 0,
+          "vq2_gemv_argmax: logits_ws and out_idx must be 8-byte aligned");
+    if (batch >= 1 && batch <= 2 && n > 0 && n % 8 == 0 && out_rows >= 8) {
+        // fused top-1: the GEMV keeps the best key per workgroup (in the
+        // logits workspace, 8 bytes per workgroup and column; a workgroup
+        // covers at least 8 rows, so the keys fit) and one small launch
+        // picks the winner
+        CHECK(dt_ok(x_dt) && dt_ok(s_dt) && x && idx0 && scale, "vq2_gemv_argmax: bad arguments");
+        CHECK(x_stride >= n, "vq2_gemv_argmax: x_stride < n");
+        int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
+        if (r) return r;
+        CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "vq2_gemv_argmax: idx1 must be given iff s2_kind != NONE");
+        GemvCall c = base_call(x, x_dt, s2_kind, cb0, cb1, cb_dt, s_dt, VQ2_DT_F32, n / 8, batch, rs, stream);
+        c.x_bstride = x_stride;
+        c.nseg = 1;
+        c.seg[0] = GemvSegCall{idx0, idx1, scale, logits_ws, out_rows, out_rows};
+        unsigned grid_x = 0;
+        c.ep = 1;
+        c.cand = (uint64_t*)logits_ws;
+        c.grid_x_out = &grid_x;
+        r = gemv_launch(c);
+        if (r == VQ2_OK) return argmax_final_launch((const uint64_t*)logits_ws, grid_x, batch, out_idx, out_val, stream);
+        if (r != VQ2_ERR_UNSUPPORTED) return r;
+        clear_error();  // shape outside the fused path: logits, then top-1
+    }
     int r = vq2_gemv(x, x_dt, batch, x_stride, idx0, idx1, s2_kind, cb0, cb1, cb_dt, scale, s_dt, logits_ws,
                      VQ2_DT_F32, out_rows, out_rows, n, rs, stream);
     if (r) return r;

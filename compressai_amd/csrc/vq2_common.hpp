@@ -157,6 +157,17 @@ __device__ __forceinline__ void wave_argmax_all(float& v, int& i)
     argmax_step(v, i, v1, i1);
 }
 
+// Order-preserving 64-bit key: high word = float bits mapped to an unsigned
+// order, low word = 0xFFFFFFFF - column, so an unsigned max picks the largest
+// value and, among equal values, the smallest column (torch.argmax's first
+// maximum).  NaN-free rows are assumed, as for the reference's logits.
+__device__ __forceinline__ uint64_t argmax_key(float v, int64_t col)
+{
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
+}
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
 
 }  // namespace vq2

@@ -72,6 +72,8 @@ static GemvPlan plan_gemv(const GemvCall& c, int num_cu)
     static const double occ_env = env_double("VQ2_GEMV_OCC_SCALE", 1.0);
     p.occ_scale = occ_env > 0 ? occ_env : 1.0;
     p.num_cu = num_cu;
+    p.ep = c.ep;
+    p.grid_x_out = c.grid_x_out;
     p.rows_per_block = (int64_t)p.it * rpw * p.wr;
     p.n_rowblocks = 0;
     for (int s = 0; s < c.nseg; s++) p.n_rowblocks += (c.seg[s].out_rows + p.rows_per_block - 1) / p.rows_per_block;
@@ -130,6 +132,7 @@ int gemv_launch(const GemvCall& c)
     a.r_gdt = c.r_gdt;
     a.r_ids = c.r_ids;
     a.r_w = c.r_w;
+    a.cand = c.cand;
     int L = 0;
     if (c.xm != 0) {
         while ((1LL << L) < c.hb) L++;
@@ -155,6 +158,12 @@ int gemv_launch(const GemvCall& c)
                                      ((c.x_pstride * esz_x) % 16 == 0));
     const bool vec_ok = x_vec && (c.ng % p.gpl == 0) && (ia % (2 * p.gpl) == 0) && (i8 % p.gpl == 0);
     hipError_t err;
+    if (c.ep == 1) {
+        // the fused top-1 runs in the one-item-per-wave path of the vector kernel
+        const int64_t nch = (c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl);
+        if (!vec_ok || c.xm != 0 || c.nseg != 1 || (c.P > 1) || nch != 1 || p.gpl != 8 || p.bt > 2 || !c.cand)
+            return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused top-1 does not apply to this shape");
+    }
     if (!vec_ok) {
         if (c.xm != 0)
             return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused rotation needs n %% 64 == 0 and aligned planes");

@@ -97,6 +97,7 @@ struct GemvArgs {
     int r_gdt;
     int32_t* r_ids;
     float* r_w;
+    uint64_t* cand;  // EP 1: [gridDim.x][batch] best top-1 keys
 };
 
 template <int CBT>
@@ -511,7 +512,11 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 
 }
 
-template <int CBT, int S2, int GPL, int BT, int IT, int XM>
+// EP 0: store y; EP 1 (pre-rotated x, one item per wave): no y -- every
+// workgroup keeps the best (value, row) key of each batch column over its
+// row blocks and writes it to a.cand[blockIdx.x * batch + column] (the fused
+// top-1 of the LM head).
+template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
 __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
 {
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
@@ -579,6 +584,9 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
             load_x_lds<GPL, BT>(s_x, 0, n, g0, lane_ok, nb, a.xscale, xs);
         }
         int64_t rb = blockIdx.x;
+        uint64_t bkey[BT];
+#pragma unroll
+        for (int b = 0; b < BT; b++) bkey[b] = 0;
         while (rb < a.n_rowblocks) {
             const int64_t rbn = rb + gridDim.x;
             uint32_t n0[IT][GPL], n1[IT][GPL];
@@ -605,9 +613,13 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
                     for (int b = 0; b < BT; b++) {
                         float v = (acc[it][b] * sc) * a.rs;
                         if (bad) v = __builtin_nanf("");
-                        if (b < nb)
+                        if constexpr (EP == 1) {
+                            const uint64_t k = argmax_key(v, row);
+                            bkey[b] = k > bkey[b] ? k : bkey[b];
+                        } else if (b < nb) {
                             store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
                                            v);
+                        }
                     }
                 }
             }
@@ -618,6 +630,25 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
                 for (int q = 0; q < GPL; q++) { c0[it][q] = n0[it][q]; c1[it][q] = n1[it][q]; }
             }
             rb = rbn;
+        }
+        if constexpr (EP == 1) {
+            // best key of the workgroup per batch column: wave, then waves
+            __shared__ uint64_t s_key[4][BT];
+#pragma unroll
+            for (int b = 0; b < BT; b++) {
+                uint64_t k = bkey[b];
+                for (int off = 32; off > 0; off >>= 1) {
+                    const uint64_t o = __shfl_xor(k, off);
+                    k = o > k ? o : k;
+                }
+                if (lane == 0) s_key[wave][b] = k;
+            }
+            __syncthreads();
+            if (threadIdx.x < BT && (int)threadIdx.x < nb) {
+                uint64_t k = s_key[0][threadIdx.x];
+                for (int w = 1; w < (int)(blockDim.x >> 6); w++) k = s_key[w][threadIdx.x] > k ? s_key[w][threadIdx.x] : k;
+                a.cand[(int64_t)blockIdx.x * a.batch + bt0 + threadIdx.x] = k;
+            }
         }
         return;
     }
@@ -787,6 +818,8 @@ struct GemvPlan {
     double occ_scale;  // multiplier on the resident-workgroup count
     int64_t rows_per_block, n_rowblocks;
     int threads;
+    int ep;                 // epilogue (0 store, 1 fused top-1)
+    unsigned* grid_x_out;   // receives the launched grid.x (may be null)
 };
 
 // Resident workgroups per CU of a kernel at a block size / LDS size (cached).
@@ -803,12 +836,13 @@ inline dim3 persistent_grid(const void* fn, const GemvPlan& p, dim3 grid, size_t
     return grid;
 }
 
-template <int CBT, int S2, int GPL, int BT, int IT, int XM>
+template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
 inline hipError_t launch_one(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
 {
-    const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM>;
+    const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>;
     grid = persistent_grid(fn, p, grid, shm);
-    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM>), grid, dim3(p.threads), shm, st, a);
+    if (p.grid_x_out) *p.grid_x_out = grid.x;
+    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>), grid, dim3(p.threads), shm, st, a);
     return hipGetLastError();
 }
 
@@ -825,7 +859,12 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
     case 3:
         if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
-    default: return launch_one<CBT, S2, GPL, BT, IT, 0>(a, p, grid, shm, st);
+    default:
+        if (p.ep == 1) {
+            if constexpr (GPL == 8 && BT <= 2) return launch_one<CBT, S2, GPL, BT, IT, 0, 1>(a, p, grid, shm, st);
+            else return hipErrorInvalidValue;
+        }
+        return launch_one<CBT, S2, GPL, BT, IT, 0>(a, p, grid, shm, st);
     }
 }
 

@@ -70,9 +70,18 @@ struct GemvCall {
     int r_gdt;
     int32_t* r_ids;
     float* r_w;
+    // epilogue: 0 store y; 1 fused top-1 (pre-rotated x, one item per wave):
+    // per-workgroup best keys to cand[grid.x][batch], grid.x to grid_x_out
+    int ep;
+    uint64_t* cand;
+    unsigned* grid_x_out;
 };
 
 int gemv_launch(const GemvCall& c);
+
+// Top-1 of each batch column over per-workgroup candidate keys.
+int argmax_final_launch(const uint64_t* cand, int64_t n_cand, int64_t batch, int64_t* out_idx, float* out_val,
+                        void* stream);
 
 // Small-M batched GEMM on the matrix cores (vq2_gemm_mfma.hip).
 struct GemmCall {

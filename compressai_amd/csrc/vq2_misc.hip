@@ -8,17 +8,6 @@
 namespace vq2 {
 
 // ------------------------------------------------------------------ argmax
-// Order-preserving 64-bit key: high word = float bits mapped to an unsigned
-// order, low word = 0xFFFFFFFF - column, so an unsigned max picks the largest
-// value and, among equal values, the smallest column (torch.argmax's first
-// maximum).  NaN-free rows are assumed, as for the reference's logits.
-__device__ __forceinline__ uint64_t argmax_key(float v, int64_t col)
-{
-    uint32_t u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
-}
-
 __global__ void argmax_init_kernel(uint64_t* keys, int64_t rows)
 {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -61,6 +50,46 @@ __global__ void argmax_decode_kernel(int64_t* out_idx, float* out_val, int64_t r
     u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
     if (out_val) out_val[r] = __uint_as_float(u);
     out_idx[r] = (int64_t)(0xFFFFFFFFu - lo);
+}
+
+// One workgroup per batch column: the best of the per-workgroup candidate
+// keys of the fused LM-head top-1, decoded as argmax_decode_kernel does.
+__global__ void __launch_bounds__(256) argmax_final_kernel(const uint64_t* cand, int64_t n_cand, int64_t batch,
+                                                           int64_t* out_idx, float* out_val)
+{
+    __shared__ uint64_t s_best[4];
+    const int64_t b = blockIdx.x;
+    uint64_t best = 0;
+    for (int64_t g = threadIdx.x; g < n_cand; g += blockDim.x) {
+        const uint64_t k = cand[g * batch + b];
+        best = k > best ? k : best;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = s_best[w] > best ? s_best[w] : best;
+        const uint32_t lo = (uint32_t)(best & 0xFFFFFFFFu);
+        uint32_t u = (uint32_t)(best >> 32);
+        u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+        if (out_val) out_val[b] = __uint_as_float(u);
+        out_idx[b] = (int64_t)(0xFFFFFFFFu - lo);
+    }
+}
+
+int argmax_final_launch(const uint64_t* cand, int64_t n_cand, int64_t batch, int64_t* out_idx, float* out_val,
+                        void* stream)
+{
+    if (batch <= 0) return VQ2_OK;
+    if (batch > 65535) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 argmax: batch too large");
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)batch), dim3(256), 0, (hipStream_t)stream, cand, n_cand,
+                       batch, out_idx, out_val);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_hip_error(err, "vq2 argmax final launch");
+    return VQ2_OK;
 }
 
 int argmax_launch(const void* v, int v_dt, int64_t rows, int64_t cols, int64_t* out_idx, float* out_val, void* stream)

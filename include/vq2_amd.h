@@ -244,8 +244,12 @@ int vq2_router_topk(const void* logits, int l_dt, int64_t tokens, int64_t n_expe
 int vq2_argmax_rows(const void* v, int v_dt, int64_t rows, int64_t cols,
                     int64_t* out_idx, float* out_val, void* stream);
 
-/* LM head + top-1: logits = VQ GEMV (as vq2_gemv, written in fp32 to
- * `logits_ws` [batch, out_rows]) followed by vq2_argmax_rows.
+/* LM head + top-1 of each batch column (torch.argmax's first maximum).
+ * batch 1-2, n % 64 == 0 (<= 2048 groups per wave chunk), out_rows >= 8: fused
+ * -- the GEMV keeps each workgroup's best (value, row) and one small launch
+ * picks the winner, no logits are written (`logits_ws` holds the per-
+ * workgroup keys).  Otherwise the logits go to `logits_ws` [batch, out_rows]
+ * (fp32) and vq2_argmax_rows follows.  logits_ws and out_idx 8-byte aligned.
  * Replaces PackedLMHead.forward (vq2/runtime.py:136-144) + torch.argmax. */
 int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
                     const int16_t* idx0, const void* idx1, int s2_kind,

@@ -652,3 +652,29 @@ def test_decode_step_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         for a, b in zip(out, ref):
             assert torch.equal(a, b), r
+
+
+@pytest.mark.parametrize("B,n", [(1, 2048), (2, 2048), (1, 4096)])
+def test_fused_top1_ties_and_fallback(dev, B, n):
+    """Rows 700 and 3000 are identical and hold the maximum of every batch
+    column: the fused top-1 (n = 2048) and the logits + top-1 fallback
+    (n = 4096, two K chunks) both return the lower row, as torch.argmax."""
+    out = 4096
+    m = synth.vq_matrix(4800 + n, out, n, bpw=2)
+    i0 = m["idx0"].clone()
+    i0[3000] = i0[700]
+    sc = m["scale"].clone()
+    cb = synth.codebook(4801)
+    x = synth.activations(4802 + B, (B, n), dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    sign = np.sign(y64[:, 700])  # make the tied pair the maximum of each column
+    x = x * torch.from_numpy(sign.astype(np.float32))[:, None]
+    _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    unit = y64[:, 700] / float(sc[700])
+    need = np.abs(y64).max() / unit.min()
+    sc[700] = sc[3000] = float(2.0 ** np.ceil(np.log2(need) + 1))
+    _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    assert np.all(np.argmax(y64, 1) == 700) and np.all(y64[:, 700] == y64[:, 3000])
+    idx, val = K.vq_gemv_argmax(*_cuda(x, i0, None, cb, None, sc, dev=dev), out, n)
+    assert idx.cpu().tolist() == [700] * B
+    assert np.allclose(val.cpu().numpy(), y64[:, 700], rtol=1e-4)
