@@ -470,7 +470,7 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride, co
     CHECK(logits_ws && out_idx, "vq2_gemv_argmax: NULL workspace/output");
     CHECK((uintptr_t)logits_ws % 8 == 0 && (uintptr_t)out_idx % 8 == 0,
           "vq2_gemv_argmax: logits_ws and out_idx must be 8-byte aligned");
-    if (batch >= 1 && batch <= 2 && n > 0 && n % 8 == 0 && out_rows >= 8) {
+    if (batch == 1 && n > 0 && n % 8 == 0 && n <= 2048 && out_rows >= 8) {
         // fused top-1: the GEMV keeps the best key per workgroup (in the
         // logits workspace, 8 bytes per workgroup and column; a workgroup
         // covers at least 8 rows, so the keys fit) and one small launch

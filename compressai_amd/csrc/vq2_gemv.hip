@@ -161,7 +161,7 @@ int gemv_launch(const GemvCall& c)
     if (c.ep == 1) {
         // the fused top-1 runs in the one-item-per-wave path of the vector kernel
         const int64_t nch = (c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl);
-        if (!vec_ok || c.xm != 0 || c.nseg != 1 || (c.P > 1) || nch != 1 || p.gpl != 8 || p.bt > 2 || !c.cand)
+        if (!vec_ok || c.xm != 0 || c.nseg != 1 || (c.P > 1) || nch != 1 || p.bt != 1 || p.it != 1 || !c.cand)
             return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused top-1 does not apply to this shape");
     }
     if (!vec_ok) {

@@ -861,7 +861,7 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
         else return hipErrorInvalidValue;
     default:
         if (p.ep == 1) {
-            if constexpr (GPL == 8 && BT <= 2) return launch_one<CBT, S2, GPL, BT, IT, 0, 1>(a, p, grid, shm, st);
+            if constexpr (BT == 1 && IT == 1) return launch_one<CBT, S2, GPL, BT, IT, 0, 1>(a, p, grid, shm, st);
             else return hipErrorInvalidValue;
         }
         return launch_one<CBT, S2, GPL, BT, IT, 0>(a, p, grid, shm, st);

@@ -245,7 +245,7 @@ int vq2_argmax_rows(const void* v, int v_dt, int64_t rows, int64_t cols,
                     int64_t* out_idx, float* out_val, void* stream);
 
 /* LM head + top-1 of each batch column (torch.argmax's first maximum).
- * batch 1-2, n % 64 == 0 (<= 2048 groups per wave chunk), out_rows >= 8: fused
+ * batch 1, n % 8 == 0, n <= 2048 (one K chunk per wave), out_rows >= 8: fused
  * -- the GEMV keeps each workgroup's best (value, row) and one small launch
  * picks the winner, no logits are written (`logits_ws` holds the per-
  * workgroup keys).  Otherwise the logits go to `logits_ws` [batch, out_rows]
