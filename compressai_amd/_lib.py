@@ -37,6 +37,11 @@ SIGNATURES = {
                                     _vp], _i32),
     "vq2_moe_down_swiglu_combine": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _vp, _i64, _i64, _vp, _i64,
                                      _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
+    "vq2_moe_gate_up_rht_16_8": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _i64, _vp, _vp, _i64, _vp,
+                                  _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32, _vp], _i32),
+    "vq2_moe_down_swiglu_combine_16_8": ([_vp, _i32, _i64, _vp, _vp, _i64, _f32, _vp, _i32, _vp, _i64, _i64, _vp,
+                                          _vp, _i64, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32,
+                                          _i32, _vp], _i32),
     "vq2_gemm_small_m_workspace": ([_i64, _i64, _i64], ctypes.c_size_t),
     "vq2_gemm_small_m": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
                           _i64, _i64, _f32, _vp, ctypes.c_size_t, _vp], _i32),

@@ -246,24 +246,28 @@ int vq2_moe_grouped(const void* x, int x_dt, int64_t x_pair_stride, int64_t pair
     return gemv_launch(c);
 }
 
-int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign, int64_t hb,
-                        float rht_scale, const void* ids, int ids_dt, int64_t P, const int16_t* pool,
-                        int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* y,
-                        int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+// Grouped gate_up with the RHT prologue; pool1 / cb1 give the uint8 stage-2
+// plane of (16,8) experts (s2 VQ2_S2_U8), else s2 is VQ2_S2_NONE.
+static int moe_gate_up_rht(const char* fn, const void* h, int h_dt, int64_t tokens, const int32_t* perm,
+                           const int8_t* sign, int64_t hb, float rht_scale, const void* ids, int ids_dt, int64_t P,
+                           const int16_t* pool, const uint8_t* pool1, int s2, int64_t n_experts, const void* cb,
+                           const void* cb1, int cb_dt, const void* pool_scale, int s_dt, void* y, int y_dt,
+                           int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
 {
     clear_error();
-    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_gate_up_rht: bad sizes");
+    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "%s: bad sizes", fn);
     if (tokens == 0 || out_rows == 0) return VQ2_OK;
-    CHECK(h && ids && pool && pool_scale && y, "vq2_moe_gate_up_rht: NULL pointer argument");
-    CHECK(dt_ok(h_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_moe_gate_up_rht: bad dtype code");
-    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_gate_up_rht: bad ids dtype");
-    CHECK(y_pair_stride >= out_rows, "vq2_moe_gate_up_rht: y_pair_stride < out_rows");
-    CHECK(tokens * P <= 65535, "vq2_moe_gate_up_rht: too many pairs");
-    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "vq2_moe_gate_up_rht: bad hb");
+    CHECK(h && ids && pool && pool_scale && y, "%s: NULL pointer argument", fn);
+    CHECK(s2 == VQ2_S2_NONE || pool1, "%s: NULL stage-2 plane", fn);
+    CHECK(dt_ok(h_dt) && dt_ok(s_dt) && dt_ok(y_dt), "%s: bad dtype code", fn);
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "%s: bad ids dtype", fn);
+    CHECK(y_pair_stride >= out_rows, "%s: y_pair_stride < out_rows", fn);
+    CHECK(tokens * P <= 65535, "%s: too many pairs", fn);
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "%s: bad hb", fn);
     if (int rr = check_rot_tables(perm, sign)) return rr;
-    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    int r = check_codebooks(s2, cb, cb1, cb_dt);
     if (r) return r;
-    GemvCall c = base_call(h, h_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, y_dt, ng, 1, rs, stream);
+    GemvCall c = base_call(h, h_dt, s2, cb, cb1, cb_dt, s_dt, y_dt, ng, 1, rs, stream);
     c.x_bstride = ng * 8;
     c.x_pstride = ng * 8;
     c.x_pdiv = (int)P;
@@ -273,13 +277,34 @@ int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* 
     c.n_out_groups = tokens * P;
     c.y_ostride = y_pair_stride;
     c.nseg = 1;
-    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, y, out_rows, 0};
+    c.seg[0] = GemvSegCall{pool, pool1, pool_scale, y, out_rows, 0};
     c.xm = 1;
     c.perm = perm;
     c.sign = sign;
     c.hb = hb;
     c.xscale = rht_scale;
     return gemv_launch(c);
+}
+
+int vq2_moe_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign, int64_t hb,
+                        float rht_scale, const void* ids, int ids_dt, int64_t P, const int16_t* pool,
+                        int64_t n_experts, const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* y,
+                        int y_dt, int64_t y_pair_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    return moe_gate_up_rht("vq2_moe_gate_up_rht", h, h_dt, tokens, perm, sign, hb, rht_scale, ids, ids_dt, P, pool,
+                           nullptr, VQ2_S2_NONE, n_experts, cb, nullptr, cb_dt, pool_scale, s_dt, y, y_dt,
+                           y_pair_stride, out_rows, ng, rs, stream);
+}
+
+int vq2_moe_gate_up_rht_16_8(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign,
+                             int64_t hb, float rht_scale, const void* ids, int ids_dt, int64_t P, const int16_t* pool,
+                             const uint8_t* pool1, int64_t n_experts, const void* cb, const void* cb1, int cb_dt,
+                             const void* pool_scale, int s_dt, void* y, int y_dt, int64_t y_pair_stride,
+                             int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    return moe_gate_up_rht("vq2_moe_gate_up_rht_16_8", h, h_dt, tokens, perm, sign, hb, rht_scale, ids, ids_dt, P,
+                           pool, pool1, VQ2_S2_U8, n_experts, cb, cb1, cb_dt, pool_scale, s_dt, y, y_dt,
+                           y_pair_stride, out_rows, ng, rs, stream);
 }
 
 int vq2_moe_router_gate_up_rht(const void* h, int h_dt, int64_t tokens, const int32_t* perm, const int8_t* sign,
@@ -367,43 +392,74 @@ int vq2_moe_down_combine(const void* x, int x_dt, const void* ids, int ids_dt, c
     return gemv_launch(c);
 }
 
-int vq2_moe_down_swiglu_combine(const void* gu, int gu_dt, int64_t gu_stride, const int32_t* perm,
-                                const int8_t* sign, int64_t hb, float rht_scale, const void* ids, int ids_dt,
-                                const float* w, int64_t tokens, int64_t P, const int16_t* pool, int64_t n_experts,
-                                const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* out, int out_dt,
-                                int64_t out_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+// SwiGLU + RHT + grouped down + weighted combine; s2 / pool1 / cb1 as in
+// moe_gate_up_rht; accumulate: out += the combine instead of out = it.
+static int moe_down_swiglu_combine(const char* fn, const void* gu, int gu_dt, int64_t gu_stride,
+                                   const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                                   const void* ids, int ids_dt, const float* w, int64_t tokens, int64_t P,
+                                   const int16_t* pool, const uint8_t* pool1, int s2, int64_t n_experts,
+                                   const void* cb, const void* cb1, int cb_dt, const void* pool_scale, int s_dt,
+                                   void* out, int out_dt, int64_t out_stride, int64_t out_rows, int64_t ng, float rs,
+                                   int accumulate, void* stream)
 {
     clear_error();
-    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "vq2_moe_down_swiglu_combine: bad sizes");
+    CHECK(tokens >= 0 && P > 0 && out_rows >= 0 && ng > 0 && n_experts > 0, "%s: bad sizes", fn);
     if (tokens == 0 || out_rows == 0) return VQ2_OK;
-    CHECK(gu && ids && w && pool && pool_scale && out, "vq2_moe_down_swiglu_combine: NULL pointer argument");
-    CHECK(dt_ok(gu_dt) && dt_ok(s_dt) && dt_ok(out_dt), "vq2_moe_down_swiglu_combine: bad dtype code");
-    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "vq2_moe_down_swiglu_combine: bad ids dtype");
-    CHECK(gu_stride >= 2 * ng * 8, "vq2_moe_down_swiglu_combine: gu_stride < 2 * n");
-    CHECK(out_stride >= out_rows, "vq2_moe_down_swiglu_combine: out_stride < out_rows");
-    CHECK(tokens <= 65535 && P <= 4096, "vq2_moe_down_swiglu_combine: too many tokens/pairs");
-    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "vq2_moe_down_swiglu_combine: bad hb");
+    CHECK(gu && ids && w && pool && pool_scale && out, "%s: NULL pointer argument", fn);
+    CHECK(s2 == VQ2_S2_NONE || pool1, "%s: NULL stage-2 plane", fn);
+    CHECK(dt_ok(gu_dt) && dt_ok(s_dt) && dt_ok(out_dt), "%s: bad dtype code", fn);
+    CHECK(ids_dt == VQ2_ID_I32 || ids_dt == VQ2_ID_I64, "%s: bad ids dtype", fn);
+    CHECK(gu_stride >= 2 * ng * 8, "%s: gu_stride < 2 * n", fn);
+    CHECK(out_stride >= out_rows, "%s: out_stride < out_rows", fn);
+    CHECK(tokens <= 65535 && P <= 4096, "%s: too many tokens/pairs", fn);
+    CHECK(hb >= 2 && hb <= 8192 && (hb & (hb - 1)) == 0 && (ng * 8) % hb == 0, "%s: bad hb", fn);
     if (int rr = check_rot_tables(perm, sign)) return rr;
-    int r = check_codebooks(VQ2_S2_NONE, cb, nullptr, cb_dt);
+    int r = check_codebooks(s2, cb, cb1, cb_dt);
     if (r) return r;
-    GemvCall c = base_call(gu, gu_dt, VQ2_S2_NONE, cb, nullptr, cb_dt, s_dt, out_dt, ng, 1, rs, stream);
+    GemvCall c = base_call(gu, gu_dt, s2, cb, cb1, cb_dt, s_dt, out_dt, ng, 1, rs, stream);
     c.x_bstride = gu_stride;
     c.x_pstride = gu_stride;
     c.ids = ids;
     c.ids_i64 = ids_dt == VQ2_ID_I64;
     c.n_experts = n_experts;
     c.pair_w = w;
+    c.y_acc = accumulate ? 1 : 0;
     c.P = (int)P;
     c.n_out_groups = tokens;
     c.y_ostride = out_stride;
     c.nseg = 1;
-    c.seg[0] = GemvSegCall{pool, nullptr, pool_scale, out, out_rows, 0};
+    c.seg[0] = GemvSegCall{pool, pool1, pool_scale, out, out_rows, 0};
     c.xm = 2;
     c.perm = perm;
     c.sign = sign;
     c.hb = hb;
     c.xscale = rht_scale;
     return gemv_launch(c);
+}
+
+int vq2_moe_down_swiglu_combine(const void* gu, int gu_dt, int64_t gu_stride, const int32_t* perm,
+                                const int8_t* sign, int64_t hb, float rht_scale, const void* ids, int ids_dt,
+                                const float* w, int64_t tokens, int64_t P, const int16_t* pool, int64_t n_experts,
+                                const void* cb, int cb_dt, const void* pool_scale, int s_dt, void* out, int out_dt,
+                                int64_t out_stride, int64_t out_rows, int64_t ng, float rs, void* stream)
+{
+    return moe_down_swiglu_combine("vq2_moe_down_swiglu_combine", gu, gu_dt, gu_stride, perm, sign, hb, rht_scale,
+                                   ids, ids_dt, w, tokens, P, pool, nullptr, VQ2_S2_NONE, n_experts, cb, nullptr,
+                                   cb_dt, pool_scale, s_dt, out, out_dt, out_stride, out_rows, ng, rs, 0, stream);
+}
+
+int vq2_moe_down_swiglu_combine_16_8(const void* gu, int gu_dt, int64_t gu_stride, const int32_t* perm,
+                                     const int8_t* sign, int64_t hb, float rht_scale, const void* ids, int ids_dt,
+                                     const float* w, int64_t tokens, int64_t P, const int16_t* pool,
+                                     const uint8_t* pool1, int64_t n_experts, const void* cb, const void* cb1,
+                                     int cb_dt, const void* pool_scale, int s_dt, void* out, int out_dt,
+                                     int64_t out_stride, int64_t out_rows, int64_t ng, float rs, int accumulate,
+                                     void* stream)
+{
+    return moe_down_swiglu_combine("vq2_moe_down_swiglu_combine_16_8", gu, gu_dt, gu_stride, perm, sign, hb,
+                                   rht_scale, ids, ids_dt, w, tokens, P, pool, pool1, VQ2_S2_U8, n_experts, cb, cb1,
+                                   cb_dt, pool_scale, s_dt, out, out_dt, out_stride, out_rows, ng, rs, accumulate,
+                                   stream);
 }
 
 int vq2_rht(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride, const int32_t* perm,

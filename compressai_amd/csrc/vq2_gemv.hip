@@ -110,6 +110,7 @@ int gemv_launch(const GemvCall& c)
     a.ids_i64 = c.ids_i64;
     a.n_experts = c.n_experts;
     a.pair_w = c.pair_w;
+    a.y_acc = c.y_acc;
     a.P = c.P > 0 ? c.P : 1;
     a.y_dt = c.y_dt;
     a.y_ostride = c.y_ostride;
@@ -191,8 +192,8 @@ int gemv_launch(const GemvCall& c)
     a.n_rowblocks = p.n_rowblocks;
     if (p.threads > 256 || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
-    if (c.xm == 2 && (c.s2 != VQ2_S2_NONE || p.bt != 1))
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 bpw, batch 1");
+    if (c.xm == 2 && (c.s2 == VQ2_S2_U16 || p.bt != 1))
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 and 3 bpw, batch 1");
     if (c.xm == 3 && (c.s2 != VQ2_S2_NONE || p.bt != 1 || !c.r_logits))
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused router is for 2 bpw, batch 1");
     if (c.xm == 1 && p.bt > 2)

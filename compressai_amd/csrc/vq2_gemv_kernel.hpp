@@ -62,7 +62,8 @@ struct GemvArgs {
     const void* ids;
     int ids_i64;
     int64_t n_experts;
-    const float* pair_w;  // per-pair combine weights (P > 1), may be null
+    const float* pair_w;  // per-pair combine weights, may be null
+    int y_acc;            // XM 2: add the combine to y instead of overwriting it
     int P;                // pairs per output group
     int y_dt;
     int64_t y_ostride;
@@ -565,7 +566,7 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
     float xs[BT][GPL * 8];
     int cur_item = -1;
 
-    if (items == 1) {
+    if (items == 1 && a.pair_w == nullptr) {
         // One work item (pair og, the whole K range) per wave: the activation
         // slice is loaded once, and the next row block's codes are fetched
         // before the current block's gathers so the HBM latency of the index
@@ -727,10 +728,13 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
                         if (row >= sg.out_rows) continue;
 #pragma unroll
                         for (int b = 0; b < BT; b++)
-                            if (b < nb)
-                                store_from_f32(sg.y, a.y_dt,
-                                               (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
-                                               fin[it][b]);
+                            if (b < nb) {
+                                const int64_t yi = (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row;
+                                float v = fin[it][b];
+                                if constexpr (XM == 2)
+                                    if (a.y_acc) v = load_as_f32(sg.y, a.y_dt, yi) + v;
+                                store_from_f32(sg.y, a.y_dt, yi, v);
+                            }
                     }
                 }
             } else {
@@ -748,9 +752,12 @@ __global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
                     const int64_t row = row_base + lr;
                     float sum = s_part[lr * BT + b];
                     for (int w = 1; w < wi; w++) sum += s_part[(w * rows_per_block + lr) * BT + b];
-                    if (row < sg.out_rows && b < nb)
-                        store_from_f32(sg.y, a.y_dt, (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row,
-                                       sum);
+                    if (row < sg.out_rows && b < nb) {
+                        const int64_t yi = (int64_t)og * a.y_ostride + (int64_t)(bt0 + b) * sg.y_bstride + row;
+                        if constexpr (XM == 2)
+                            if (a.y_acc) sum = load_as_f32(sg.y, a.y_dt, yi) + sum;
+                        store_from_f32(sg.y, a.y_dt, yi, sum);
+                    }
                 }
                 __syncthreads();
             }
@@ -854,7 +861,7 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
         if constexpr (BT <= 2) return launch_one<CBT, S2, GPL, BT, IT, 1>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     case 2:
-        if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
+        if constexpr (S2 != VQ2_S2_U16 && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     case 3:
         if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);

@@ -41,7 +41,8 @@ struct GemvCall {
     const void* ids;  // null: expert 0 for every pair
     int ids_i64;
     int64_t n_experts;
-    const float* pair_w;  // combine weights (P > 1)
+    const float* pair_w;  // combine weights
+    int y_acc;            // xm 2: out += combine
     int P;                // pairs per output group
     int64_t n_out_groups; // grid.y
     int y_dt;

@@ -382,11 +382,29 @@ def vq_moe_grouped(x, ids, pool, cb16, pool_scale, y_out, OUT, NG, rs=1.0, pairs
     return y_out
 
 
+def _stage2_pool(pool, pool1, cb16, cb8):
+    """uint8 stage-2 plane of a (16,8) expert pool: same [E, rows, ng] shape
+    as the int16 stage-1 pool; cb8 [256, 8] in the dtype of cb16."""
+    if pool1 is None and cb8 is None:
+        return None, None
+    if pool1 is None or cb8 is None:
+        raise Vq2Error("a (16,8) pool needs both pool1 and cb8")
+    p1 = _contig(pool1, "pool1")
+    if p1.dtype != torch.uint8 or tuple(p1.shape) != tuple(pool.shape):
+        raise Vq2Error(f"pool1 must be uint8 {tuple(pool.shape)}, got {p1.dtype} {tuple(p1.shape)}")
+    c8 = _contig(cb8, "cb8")
+    if tuple(c8.shape) != (256, 8) or c8.dtype != cb16.dtype:
+        raise Vq2Error(f"cb8 must be [256, 8] {cb16.dtype}")
+    return p1, c8
+
+
 def vq_moe_gate_up_rht(h, ids, pool, cb16, pool_scale, y_out, OUT, NG, perm=None, sign=None, hb=2048,
-                       rht_scale=None, rs=1.0):
+                       rht_scale=None, rs=1.0, pool1=None, cb8=None):
     """Grouped gate_up with the activation RHT fused: token t = row of h
-    [T, NG*8], experts ids [T, P]; y_out [T*P, >=OUT]."""
-    dev = _dev(h, ids, pool, cb16, pool_scale, y_out, perm, sign)
+    [T, NG*8], experts ids [T, P]; y_out [T*P, >=OUT].  pool1 / cb8 select a
+    (16,8) pool: uint8 stage-2 codes [E, OUT, NG] and their [256, 8]
+    codebook (promoted 3 bpw experts)."""
+    dev = _dev(h, ids, pool, cb16, pool_scale, y_out, perm, sign, pool1, cb8)
     OUT, NG = int(OUT), int(NG)
     pool = _moe_checks(pool, pool_scale, OUT, NG, "pool")
     ids2, ids_dt = _ids(ids)
@@ -400,9 +418,16 @@ def vq_moe_gate_up_rht(h, ids, pool, cb16, pool_scale, y_out, OUT, NG, perm=None
     if y2.shape[0] < T * P or y2.shape[1] < OUT or y2.stride(1) != 1:
         raise Vq2Error("y_out must be [>=T*P, >=OUT] with unit column stride")
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
-    _lib.call("vq2_moe_gate_up_rht", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc, _p(ids2), ids_dt, P,
-              _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"), _p(pool_scale),
-              _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
+    p1, c8 = _stage2_pool(pool, pool1, cb16, cb8)
+    if p1 is None:
+        _lib.call("vq2_moe_gate_up_rht", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc, _p(ids2), ids_dt,
+                  P, _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"), _p(pool_scale),
+                  _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG, float(rs), _stream(dev))
+    else:
+        _lib.call("vq2_moe_gate_up_rht_16_8", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc, _p(ids2),
+                  ids_dt, P, _p(pool), _p(p1), pool.shape[0], _p(_contig(cb16, "cb16")), _p(c8), _dt(cb16, "cb16"),
+                  _p(pool_scale), _dt(pool_scale, "scale"), _p(y2), _dt(y2, "y_out"), y2.stride(0), OUT, NG,
+                  float(rs), _stream(dev))
     return y_out
 
 
@@ -436,10 +461,13 @@ def vq_moe_router_gate_up_rht(h, router_logits, top_k, pool, cb16, pool_scale, y
 
 
 def vq_moe_down_swiglu_combine(gu, ids, w, down_idx, cb16, down_scale, OUT, NG, perm=None, sign=None, hb=None,
-                               rht_scale=None, rs=1.0, out=None, out_dtype=torch.float32):
+                               rht_scale=None, rs=1.0, out=None, out_dtype=torch.float32, pool1=None, cb8=None,
+                               accumulate=False):
     """silu(gate)*up -> RHT -> grouped down -> weighted combine, one launch.
-    gu [T*P, >=2*NG*8] (gate | up), ids [T, P], w fp32 [T, P] -> out [T, OUT]."""
-    dev = _dev(gu, ids, w, down_idx, cb16, down_scale, out, perm, sign)
+    gu [T*P, >=2*NG*8] (gate | up), ids [T, P], w fp32 [T, P] -> out [T, OUT].
+    pool1 / cb8: (16,8) pool as in vq_moe_gate_up_rht; accumulate adds the
+    combine to the given out (the (16,8) entry only)."""
+    dev = _dev(gu, ids, w, down_idx, cb16, down_scale, out, perm, sign, pool1, cb8)
     OUT, NG = int(OUT), int(NG)
     pool = _moe_checks(down_idx, down_scale, OUT, NG, "down_idx")
     ids2, ids_dt = _ids(ids)
@@ -454,13 +482,24 @@ def vq_moe_down_swiglu_combine(gu, ids, w, down_idx, cb16, down_scale, OUT, NG, 
         raise Vq2Error("gu must be [T*P, >=2*NG*8] with unit column stride")
     hb = NG * 8 if hb is None else int(hb)
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
+    p1, c8 = _stage2_pool(pool, pool1, cb16, cb8)
+    if accumulate and (out is None or p1 is None):
+        raise Vq2Error("accumulate needs an out tensor and a (16,8) pool")
     if out is None:
         out = torch.empty((T, OUT), dtype=out_dtype, device=dev)
     _contig(out, "out")
-    _lib.call("vq2_moe_down_swiglu_combine", _p(g2), _dt(g2, "gu"), g2.stride(0), _p(perm), _p(sign), hb, sc,
-              _p(ids2), ids_dt, _p(w), T, P, _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")), _dt(cb16, "cb16"),
-              _p(down_scale), _dt(down_scale, "scale"), _p(out), _dt(out, "out"), OUT, OUT, NG, float(rs),
-              _stream(dev))
+    if out.numel() < T * OUT:
+        raise Vq2Error(f"out must hold [T, OUT] = [{T}, {OUT}]")
+    if p1 is None:
+        _lib.call("vq2_moe_down_swiglu_combine", _p(g2), _dt(g2, "gu"), g2.stride(0), _p(perm), _p(sign), hb, sc,
+                  _p(ids2), ids_dt, _p(w), T, P, _p(pool), pool.shape[0], _p(_contig(cb16, "cb16")),
+                  _dt(cb16, "cb16"), _p(down_scale), _dt(down_scale, "scale"), _p(out), _dt(out, "out"), OUT, OUT, NG,
+                  float(rs), _stream(dev))
+    else:
+        _lib.call("vq2_moe_down_swiglu_combine_16_8", _p(g2), _dt(g2, "gu"), g2.stride(0), _p(perm), _p(sign), hb,
+                  sc, _p(ids2), ids_dt, _p(w), T, P, _p(pool), _p(p1), pool.shape[0], _p(_contig(cb16, "cb16")),
+                  _p(c8), _dt(cb16, "cb16"), _p(down_scale), _dt(down_scale, "scale"), _p(out), _dt(out, "out"), OUT,
+                  OUT, NG, float(rs), 1 if accumulate else 0, _stream(dev))
     return out
 
 

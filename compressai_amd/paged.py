@@ -30,8 +30,18 @@ buffer and hands the kernels a slot list built element by element, here:
   SwiGLU + RHT + down + combine) run unchanged on the slot pool -- the pool
   keeps the container's fp16 scales, the kernels read them directly.
 
-Promoted 3-bit experts (``expert_modes``, vq2/paged_runtime.py:357-389) are
-not handled by this feed: the store reports them and the layer refuses them.
+Promoted 3 bpw experts (``expert_modes["layer:expert"] == 3``, written by
+tools/build_mixed_b2_container.py:50-82, 154-165): their index entries hold
+the int16 stage-1 plane followed by the uint8 stage-2 plane of the (16,8)
+scheme (1,185,792-byte records at the config-4 shape).  The reference keeps
+them resident as dense bf16 weights and runs them through ``F.linear`` per
+token (vq2/paged_runtime.py:357-389, 446-458).  Here they stay resident in
+their compressed form, in a per-layer (16,8) pool, and run through the same
+two fused launches with the stage-2 codebook: a step whose experts mix both
+kinds splits each token's pairs into a 2 bpw set on the paged pool and a
+3 bpw set on the promoted pool (padded to a common width with weight-0 pairs
+on an expert of the same step), and the second combine adds into the first's
+output.
 """
 from __future__ import annotations
 
@@ -82,9 +92,40 @@ class Vq2mStore:
         self.sizes = (self.gu_rows * self.gu_cols * 2, self.gu_rows * 2, self.dn_rows * self.dn_cols * 2,
                       self.dn_rows * 2)
         self.record_bytes = sum(self.sizes)
+        # promoted (16,8) record: int16 stage-1 plane followed by the uint8 stage-2 plane
+        self.promoted_sizes = (self.gu_rows * self.gu_cols * 3, self.gu_rows * 2, self.dn_rows * self.dn_cols * 3,
+                               self.dn_rows * 2)
 
     def promoted(self, layer: int, expert: int) -> bool:
         return self.expert_modes.get(f"{layer}:{expert}") == 3
+
+    def promoted_experts(self, layer: int) -> list:
+        return [e for e in range(self.num_experts) if self.promoted(layer, e)]
+
+    def read_promoted(self, layer: int, expert: int) -> dict:
+        """CPU tensors of a promoted expert: gu0 int16 / gu1 uint8 [gu_rows,
+        gu_cols], gu_s fp16 [gu_rows], dn0 / dn1 [dn_rows, dn_cols], dn_s."""
+        if not self.promoted(layer, expert):
+            raise ValueError(f"layer {layer} expert {expert} is not a promoted 3-bit expert")
+        e = self.entries[layer][expert]
+        offs, szs = e[0::2], e[1::2]
+        if tuple(szs) != self.promoted_sizes:
+            raise ValueError(f"layer {layer} expert {expert}: record sizes {szs} are not a (16,8) expert "
+                             f"{self.promoted_sizes}")
+        parts = []
+        for off, sz in zip(offs, szs):
+            b = os.pread(self.fd, sz, off)
+            if len(b) != sz:
+                raise IOError(f"short read of layer {layer} expert {expert}")
+            parts.append(torch.frombuffer(bytearray(b), dtype=torch.uint8))
+        gi, gs, di, ds = parts
+        a, b = self.gu_rows * self.gu_cols * 2, self.dn_rows * self.dn_cols * 2
+        return {"gu0": gi[:a].view(torch.int16).view(self.gu_rows, self.gu_cols),
+                "gu1": gi[a:].view(self.gu_rows, self.gu_cols),
+                "gu_s": gs.view(torch.float16),
+                "dn0": di[:b].view(torch.int16).view(self.dn_rows, self.dn_cols),
+                "dn1": di[b:].view(self.dn_rows, self.dn_cols),
+                "dn_s": ds.view(torch.float16)}
 
     def read_record(self, layer: int, expert: int, dst: memoryview) -> None:
         """Read the expert's [gate_up idx | gate_up scale | down idx | down
@@ -118,15 +159,22 @@ class Vq2mStore:
             pass
 
 
-def write_vq2m(path, gate_up_idx, gate_up_scale, down_idx, down_scale, meta=None, payload_start=4096):
+def write_vq2m(path, gate_up_idx, gate_up_scale, down_idx, down_scale, meta=None, payload_start=4096,
+               promoted=None):
     """Write a container with the reference's layout: tensors per layer of
     shape [E, gu_rows, gu_cols] int16, [E, gu_rows] fp16, [E, dn_rows,
-    dn_cols] int16, [E, dn_rows] fp16 (lists over layers, CPU tensors)."""
+    dn_cols] int16, [E, dn_rows] fp16 (lists over layers, CPU tensors).
+    promoted: {(layer, expert): (gu_idx1, dn_idx1)} uint8 stage-2 planes of
+    3 bpw experts, written after their int16 planes in the index entries and
+    flagged in meta["expert_modes"] (tools/build_mixed_b2_container.py)."""
     L = len(gate_up_idx)
     E, gu_rows, gu_cols = gate_up_idx[0].shape
     _, dn_rows, dn_cols = down_idx[0].shape
+    promoted = dict(promoted or {})
     m = {"gu_rows": gu_rows, "gu_cols": gu_cols, "dn_rows": dn_rows, "dn_cols": dn_cols}
     m.update(meta or {})
+    if promoted:
+        m["expert_modes"] = {f"{l}:{e}": 3 for (l, e) in sorted(promoted)}
     meta_bytes = json.dumps(m).encode("utf-8")
     table_off = HEADER_SIZE
     table_len = L * E * ENTRY_SIZE
@@ -138,9 +186,12 @@ def write_vq2m(path, gate_up_idx, gate_up_scale, down_idx, down_scale, meta=None
         for l in range(L):
             for e in range(E):
                 ent = []
-                for t in (gate_up_idx[l][e].to(torch.int16), gate_up_scale[l][e].to(torch.float16),
-                          down_idx[l][e].to(torch.int16), down_scale[l][e].to(torch.float16)):
+                s2 = promoted.get((l, e))
+                for i, t in enumerate((gate_up_idx[l][e].to(torch.int16), gate_up_scale[l][e].to(torch.float16),
+                                       down_idx[l][e].to(torch.int16), down_scale[l][e].to(torch.float16))):
                     b = t.contiguous().view(torch.uint8).numpy().tobytes()
+                    if s2 is not None and i in (0, 2):
+                        b += s2[i // 2].to(torch.uint8).contiguous().numpy().tobytes()
                     ent += [f.tell(), len(b)]
                     f.write(b)
                 entries.append(struct.pack(ENTRY_FORMAT, *ent))
@@ -248,10 +299,12 @@ class ExpertPager:
 class PagedMoEExperts(torch.nn.Module):
     """Routed experts of one MoE layer over a paged device pool:
     forward(hidden_states [T, H], topk_idx [T, K], topk_weights [T, K]) ->
-    [T, H] (vq2/paged_runtime.py:439-568, T == 1 fast path 491-511)."""
+    [T, H] (vq2/paged_runtime.py:439-568, T == 1 fast path 491-511).
+    cb8 is the [256, 8] stage-2 codebook of the (16,8) scheme, needed when
+    the layer holds promoted 3 bpw experts."""
 
     def __init__(self, layer: int, store: Vq2mStore, cb16, capacity: int = 96, device="cuda", staging: int = 16,
-                 act_dtype=torch.float32, out_dtype=None):
+                 act_dtype=torch.float32, out_dtype=None, cb8=None):
         super().__init__()
         self.pager = ExpertPager(store, layer, capacity, device, staging)
         self.cb16 = cb16
@@ -264,6 +317,48 @@ class PagedMoEExperts(torch.nn.Module):
         self.rot_i = get_rot("moe_expert_512", self.intermediate_dim, dev)
         self.act_dtype = act_dtype
         self.out_dtype = out_dtype
+        # promoted (16,8) experts of this layer: resident, compressed
+        promoted = store.promoted_experts(layer)
+        self.promoted_index = {e: i for i, e in enumerate(promoted)}
+        self.cb8 = None
+        if promoted:
+            if cb8 is None:
+                raise K.Vq2Error(f"layer {layer} holds promoted 3-bit experts {promoted}: pass cb8, the [256, 8] "
+                                 "stage-2 codebook")
+            recs = [store.read_promoted(layer, e) for e in promoted]
+            self.pro = {k: torch.stack([r[k] for r in recs]).to(dev) for k in recs[0]}
+            self.cb8 = cb8
+
+    def _run(self, h, ids_d, w_d, pool, accumulate_into=None):
+        """Two launches over one pool: gate_up with the H-point RHT, then
+        SwiGLU + I-point RHT + down + weighted combine (out= / out+=)."""
+        T, P = ids_d.shape
+        I = self.intermediate_dim
+        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
+        gu0, gu1, gus, dn0, dn1, dns = pool
+        cb8 = self.cb8 if gu1 is not None else None
+        K.vq_moe_gate_up_rht(h, ids_d, gu0, self.cb16, gus, y_gu, OUT=2 * I, NG=self.hidden_dim // 8,
+                             perm=self.rot_h._perm32, sign=self.rot_h._sign8, hb=self.rot_h.hb,
+                             rht_scale=self.rot_h.scale, pool1=gu1, cb8=cb8)
+        return K.vq_moe_down_swiglu_combine(y_gu, ids_d, w_d, dn0, self.cb16, dns, OUT=self.hidden_dim, NG=I // 8,
+                                            perm=self.rot_i._perm32, sign=self.rot_i._sign8, hb=self.rot_i.hb,
+                                            rht_scale=self.rot_i.scale, out=accumulate_into,
+                                            out_dtype=torch.float32, pool1=dn1, cb8=cb8,
+                                            accumulate=accumulate_into is not None)
+
+    def _table(self, rows, dev):
+        """Device tensors of a padded [T, width] pair table: pool ids (int32),
+        source columns into topk_weights (int64) and a 0/1 weight mask.
+        rows[t] = [(pool id, column), ...]; a padding pair repeats the
+        table's first pool id with weight 0."""
+        width = max(len(r) for r in rows)
+        pad = next(r[0][0] for r in rows if r)
+        ids = [[r[j][0] if j < len(r) else pad for j in range(width)] for r in rows]
+        cols = [[r[j][1] if j < len(r) else 0 for j in range(width)] for r in rows]
+        mask = [[1.0 if j < len(r) else 0.0 for j in range(width)] for r in rows]
+        pin = dev.type == "cuda"
+        to = lambda v, dt: torch.tensor(v, dtype=dt, pin_memory=pin).to(dev, non_blocking=True)
+        return to(ids, torch.int32), to(cols, torch.int64), to(mask, torch.float32)
 
     def forward(self, hidden_states, topk_idx, topk_weights):
         p = self.pager
@@ -271,17 +366,26 @@ class PagedMoEExperts(torch.nn.Module):
         T = h.shape[0]
         ids_host = topk_idx.reshape(T, -1).to("cpu")  # the paging decision is made on the host
         P = ids_host.shape[1]
-        slots = p.ensure(ids_host.reshape(-1).tolist())
-        slot_t = torch.tensor(slots, dtype=torch.int32, pin_memory=p.cuda).view(T, P)
-        slot_d = slot_t.to(h.device, non_blocking=True)
         w = topk_weights.reshape(T, P).to(device=h.device, dtype=torch.float32).contiguous()
-        I = self.intermediate_dim
-        y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
-        K.vq_moe_gate_up_rht(h, slot_d, p.pool_gu_idx, self.cb16, p.pool_gu_scale, y_gu, OUT=2 * I,
-                             NG=self.hidden_dim // 8, perm=self.rot_h._perm32, sign=self.rot_h._sign8,
-                             hb=self.rot_h.hb, rht_scale=self.rot_h.scale)
-        out = K.vq_moe_down_swiglu_combine(y_gu, slot_d, w, p.pool_dn_idx, self.cb16, p.pool_dn_scale,
-                                           OUT=self.hidden_dim, NG=I // 8, perm=self.rot_i._perm32,
-                                           sign=self.rot_i._sign8, hb=self.rot_i.hb, rht_scale=self.rot_i.scale,
-                                           out_dtype=torch.float32)
+        regular = (p.pool_gu_idx, None, p.pool_gu_scale, p.pool_dn_idx, None, p.pool_dn_scale)
+        flat = ids_host.reshape(-1).tolist()
+        if not any(e in self.promoted_index for e in flat):
+            slots = p.ensure(flat)
+            slot_t = torch.tensor(slots, dtype=torch.int32, pin_memory=p.cuda).view(T, P)
+            out = self._run(h, slot_t.to(h.device, non_blocking=True), w, regular)
+            return out.to(self.out_dtype or hidden_states.dtype)
+        # mixed step: 2 bpw pairs on the paged pool, promoted pairs on the (16,8) pool
+        rows = ids_host.tolist()
+        reg = [[(e, j) for j, e in enumerate(r) if e not in self.promoted_index] for r in rows]
+        pro = [[(self.promoted_index[e], j) for j, e in enumerate(r) if e in self.promoted_index] for r in rows]
+        out = None
+        if any(reg):
+            slots = iter(p.ensure([e for r in reg for e, _ in r]))
+            reg = [[(next(slots), j) for _, j in r] for r in reg]
+            ids_d, cols_d, mask_d = self._table(reg, h.device)
+            out = self._run(h, ids_d, torch.gather(w, 1, cols_d) * mask_d, regular)
+        ids_d, cols_d, mask_d = self._table(pro, h.device)
+        pp = self.pro
+        out = self._run(h, ids_d, torch.gather(w, 1, cols_d) * mask_d,
+                        (pp["gu0"], pp["gu1"], pp["gu_s"], pp["dn0"], pp["dn1"], pp["dn_s"]), accumulate_into=out)
         return out.to(self.out_dtype or hidden_states.dtype)

@@ -204,6 +204,30 @@ int vq2_moe_down_swiglu_combine(const void* gu, int gu_dt, int64_t gu_stride,
                                 void* out, int out_dt, int64_t out_stride,
                                 int64_t out_rows, int64_t ng, float rs, void* stream);
 
+/* Promoted 3 bpw experts: vq2_moe_gate_up_rht and vq2_moe_down_swiglu_combine
+ * over (16,8) pools -- pool int16 [E, rows, ng] stage-1 codes, pool1 uint8
+ * [E, rows, ng] stage-2 codes, cb [65536, 8], cb1 [256, 8] (same dtype):
+ *   W[e, r, 8g:8g+8] = (cb[pool[e, r, g]] + cb1[pool1[e, r, g]]) * pool_scale[e, r]
+ * accumulate != 0 makes the combine add into out (out += sum_j ...), so the
+ * 2 bpw and the 3 bpw experts of one token sum into one output.
+ * Replace the dense path of promoted experts in PagedMoEExpert: stage-1 +
+ * stage-2 dequant, rot.inv and F.linear per expert (vq2/paged_runtime.py:
+ * 357-389 at load, 446-458 and 514-521 per token). */
+int vq2_moe_gate_up_rht_16_8(const void* h, int h_dt, int64_t tokens,
+                             const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                             const void* ids, int ids_dt, int64_t P,
+                             const int16_t* pool, const uint8_t* pool1, int64_t n_experts,
+                             const void* cb, const void* cb1, int cb_dt, const void* pool_scale, int s_dt,
+                             void* y, int y_dt, int64_t y_pair_stride,
+                             int64_t out_rows, int64_t ng, float rs, void* stream);
+int vq2_moe_down_swiglu_combine_16_8(const void* gu, int gu_dt, int64_t gu_stride,
+                                     const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                                     const void* ids, int ids_dt, const float* w, int64_t tokens, int64_t P,
+                                     const int16_t* pool, const uint8_t* pool1, int64_t n_experts,
+                                     const void* cb, const void* cb1, int cb_dt, const void* pool_scale, int s_dt,
+                                     void* out, int out_dt, int64_t out_stride,
+                                     int64_t out_rows, int64_t ng, float rs, int accumulate, void* stream);
+
 /* Randomised Hadamard transform over the last dim, hb-point blocks:
  *   forward: v[i] = x[perm[i]] * sign[i];  y_blk = H_hb v_blk * scale
  *   inverse: z_blk = H_hb x_blk * scale;   y[perm[i]] = z[i] * sign[i]

@@ -408,6 +408,43 @@ def moe_layer(h, logits, cb, gu_pool, gu_scale, dn_pool, dn_scale,
     return out
 
 
+def moe_experts(h, ids, w, experts, cb, cb8=None, perm_h=None, sign_h=None, perm_i=None,
+                sign_i=None) -> np.ndarray:
+    """fp64 oracle of the routed-expert sum of PagedMoEExpert.forward
+    (vq2/paged_runtime.py:439-568), per token t:
+        xr = RHT_H(h[t]);  [g | u] = VQ(gate_up_e) xr
+        out[t] = sum_k w[t, k] * VQ(down_e) RHT_I(silu(g) * u),  e = ids[t, k]
+    experts(e) -> (gu_idx0, gu_idx1, gu_scale, dn_idx0, dn_idx1, dn_scale):
+    idx1 None for a 2 bpw expert; uint8 planes over the stage-2 codebook cb8
+    for a promoted 3 bpw expert, whose dequant is cb[i0] + cb8[i1] times the
+    row scale (vq2/paged_runtime.py:376-389; the reference multiplies
+    rot.inv of that by the unrotated input, which equals the product of the
+    rotated-space weights with RHT_H(x) since the RHT is orthogonal)."""
+    H = np.atleast_2d(f64(h))
+    T, hid = H.shape
+    ids = np.asarray(ids).reshape(T, -1)
+    w = f64(w).reshape(T, -1)
+    cache = {}
+    out = None
+    for t in range(T):
+        xr = np_rht64(H[t], perm_h, sign_h, hb=min(2048, hid))[0]
+        for j in range(ids.shape[1]):
+            e = int(ids[t, j])
+            if e not in cache:
+                gu0, gu1, gus, dn0, dn1, dns = experts(e)
+                cache[e] = (np_dequant64(gu0, gu1, cb, cb8 if gu1 is not None else None, gus),
+                            np_dequant64(dn0, dn1, cb, cb8 if dn1 is not None else None, dns))
+            Wgu, Wdn = cache[e]
+            g = Wgu @ xr
+            inter = g.shape[0] // 2
+            act = silu(g[:inter]) * g[inter:]
+            y = Wdn @ np_rht64(act, perm_i, sign_i, hb=min(2048, inter))[0]
+            if out is None:
+                out = np.zeros((T, y.shape[0]), np.float64)
+            out[t] += w[t, j] * y
+    return out
+
+
 def max_rel_err(y, ref) -> float:
     """max_i |y_i - ref_i| / max_i |ref_i|, in fp64."""
     y = np.asarray(y, np.float64)

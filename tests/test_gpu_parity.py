@@ -608,6 +608,78 @@ def test_paged_experts_match_resident_pool(dev, tmp_path):
     store.close()
 
 
+def _rot_np(rot):
+    return rot.perm.cpu().numpy(), rot.sign.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_single_pair_combine_applies_weight(dev, T):
+    """One expert per token (P = 1): both combines scale by the pair weight
+    (a single-pair workgroup still runs the weighted store)."""
+    from compressai_amd.moe import ResidentMoEExperts
+
+    E = 6
+    cb = synth.codebook(4900)
+    gu, gus, dn, dns = _pools(4900, E)
+    mod = ResidentMoEExperts(*_cuda(gu, gus, dn, dns, cb, dev=dev), out_dtype=torch.float32)
+    h = synth.activations(4904, (T, 2048))
+    ids = torch.tensor([[2], [5], [0]][:T], dtype=torch.int32)
+    w = torch.tensor([[0.37], [-1.5], [2.25]][:T], dtype=torch.float32)
+    out = mod(h.to(dev), ids.to(dev), w.to(dev))
+    ph, sh = _rot_np(mod.rot_h)
+    pi, si = _rot_np(mod.rot_i)
+    ref = O.moe_experts(h, ids.numpy(), w.numpy(), lambda e: (gu[e], None, gus[e], dn[e], None, dns[e]), cb,
+                        None, ph, sh, pi, si)
+    assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
+    # the split down + combine launch as well
+    act = synth.activations(4905, (T, 512), dtype=torch.float32)
+    y = K.vq_moe_down_combine(act.to(dev), ids.to(dev), w.to(dev), *_cuda(dn, cb, dns, dev=dev), OUT=2048, NG=64)
+    ref2 = np.stack([float(w[t, 0]) * O.vq_gemv(act[t], dn[int(ids[t, 0])], None, cb, None,
+                                                  dns[int(ids[t, 0])])[1][0] for t in range(T)])
+    assert O.max_rel_err(y.cpu().numpy(), ref2) < TOL
+
+
+def test_paged_promoted_experts_vs_oracle(dev, tmp_path):
+    """A layer with promoted (16,8) experts: steps with mixed, only-promoted
+    and only-2-bpw tokens, all through the two fused launches per pool (the
+    promoted combine adding into the 2 bpw one), against the fp64 oracle."""
+    from compressai_amd import paged
+
+    E = 12
+    pro = (3, 7, 10)
+    g = torch.Generator().manual_seed(4950)
+    gui = torch.randint(-32768, 32768, (E, 1024, 256), generator=g, dtype=torch.int32).to(torch.int16)
+    gus = (torch.rand(E, 1024, generator=g) + 0.5).to(torch.float16)
+    dni = torch.randint(-32768, 32768, (E, 2048, 64), generator=g, dtype=torch.int32).to(torch.int16)
+    dns = (torch.rand(E, 2048, generator=g) + 0.5).to(torch.float16)
+    gu1 = torch.randint(0, 256, (E, 1024, 256), generator=g, dtype=torch.int32).to(torch.uint8)
+    dn1 = torch.randint(0, 256, (E, 2048, 64), generator=g, dtype=torch.int32).to(torch.uint8)
+    path = tmp_path / "mixed.vq2m"
+    paged.write_vq2m(path, [gui], [gus], [dni], [dns], promoted={(0, e): (gu1[e], dn1[e]) for e in pro})
+    cb = synth.codebook(4951)
+    cb8 = synth.codebook(4952, rows=256)
+    store = paged.Vq2mStore(path)
+    pg = paged.PagedMoEExperts(0, store, cb.to(dev), capacity=4, device=dev, staging=2, out_dtype=torch.float32,
+                               cb8=cb8.to(dev))
+    ph, sh = _rot_np(pg.rot_h)
+    pi, si = _rot_np(pg.rot_i)
+
+    def experts(e):
+        p = e in pro
+        return gui[e], gu1[e] if p else None, gus[e], dni[e], dn1[e] if p else None, dns[e]
+
+    steps = [[[3, 5]], [[3, 7], [1, 2], [10, 4]], [[7, 10], [3, 7]], [[3, 5, 6]], [[5, 6], [0, 1]], [[10, 0]]]
+    for i, rows in enumerate(steps):
+        ids = torch.tensor(rows, dtype=torch.int64)
+        T, P = ids.shape
+        w = torch.softmax(torch.randn(T, P, generator=g), -1)
+        h = synth.activations(4960 + i, (T, 2048), dtype=torch.float16)
+        y = pg(h.to(dev), ids.to(dev), w.to(dev))
+        ref = O.moe_experts(h, ids.numpy(), w.numpy(), experts, cb, cb8, ph, sh, pi, si)
+        assert O.max_rel_err(y.cpu().numpy(), ref) < TOL, (i, rows)
+    store.close()
+
+
 # ------------------------------------------------------------ graph capture
 def test_decode_step_graph_replays_match_eager(dev):
     """One decode step -- fused q/k/v (PackedLinear, batch 1), a 4 bpw

@@ -296,3 +296,46 @@ def test_moe_layer_oracle_vs_c_composition():
         _, d = O.moe_grouped(ar.astype(np.float32), np.array(pids), dn, cb, dns, H, I // 8, per_pair_x=True)
         out[t] = sum(pw[j] * d[j] for j in range(k + 1))
     assert O.max_rel_err(out, ref) < 1e-5
+
+
+def test_moe_experts_oracle_vs_c_composition():
+    """moe_experts (numpy fp64, np.take dequant) against the same sum composed
+    from the C oracle's VQ GEMV and RHT, with one promoted (16,8) expert."""
+    from compressai_amd import synth
+
+    E, H, I, T, Kp = 5, 64, 32, 3, 3
+    cb = synth.codebook(90)
+    cb8 = synth.codebook(91, rows=256)
+    gu0 = synth.indices16(92, (E, 2 * I, H // 8)).numpy()
+    gu1 = synth.indices8(93, (E, 2 * I, H // 8)).numpy()
+    gus = synth.scales(94, (E, 2 * I)).numpy()
+    dn0 = synth.indices16(95, (E, H, I // 8)).numpy()
+    dn1 = synth.indices8(96, (E, H, I // 8)).numpy()
+    dns = synth.scales(97, (E, H)).numpy()
+    ph, sh = synth.permutation(98, H).numpy(), synth.signs(99, H).numpy()
+    pi, si = synth.permutation(100, I).numpy(), synth.signs(101, I).numpy()
+    h = synth.activations(102, (T, H)).numpy()
+    ids = np.array([[0, 3, 1], [3, 3, 4], [2, 0, 3]])
+    w = synth.activations(103, (T, Kp), dtype=torch.float32).numpy()
+    promoted = {3}
+
+    def experts(e):
+        p = e in promoted
+        return gu0[e], gu1[e] if p else None, gus[e], dn0[e], dn1[e] if p else None, dns[e]
+
+    ref = O.moe_experts(h, ids, w, experts, cb, cb8, ph, sh, pi, si)
+    out = np.zeros((T, H))
+    for t in range(T):
+        xr = O.rht(h[t], ph, sh, H).astype(np.float32)
+        for j in range(Kp):
+            a, b, c, d, e1, f = experts(int(ids[t, j]))
+            _, g = O.vq_gemv(xr, a, b, cb, cb8 if b is not None else None, c)
+            g = g[0]
+            act = g[:I] / (1 + np.exp(-g[:I])) * g[I:]
+            ar = O.rht(act.astype(np.float32), pi, si, I).astype(np.float32)
+            _, y = O.vq_gemv(ar, d, e1, cb, cb8 if e1 is not None else None, f)
+            out[t] += float(w[t, j]) * y[0]
+    assert O.max_rel_err(out, ref) < 1e-5
+    # the promoted expert's stage-2 plane matters: dropping it moves the result
+    ref2 = O.moe_experts(h, ids, w, lambda e: (gu0[e], None, gus[e], dn0[e], None, dns[e]), cb, cb8, ph, sh, pi, si)
+    assert O.max_rel_err(ref2, ref) > 1e-2

@@ -100,3 +100,48 @@ def test_pager_lru_on_cpu(tmp_path):
     with pytest.raises(Exception):
         pg.ensure([8])            # outside the layer's experts
     st.close()
+
+
+def test_promoted_records_round_trip(tmp_path):
+    """Promoted (16,8) experts: the index entries hold the int16 plane then the
+    uint8 plane (1.5x the 2 bpw entry), meta flags them, read_promoted returns
+    the planes, and read_record refuses them."""
+    t = _layers(2, 4, seed=5)
+    g = torch.Generator().manual_seed(6)
+    s2 = {(1, 2): (torch.randint(0, 256, (32, 16), generator=g, dtype=torch.int32).to(torch.uint8),
+                   torch.randint(0, 256, (64, 4), generator=g, dtype=torch.int32).to(torch.uint8))}
+    path = tmp_path / "p.vq2m"
+    paged.write_vq2m(path, *t, promoted=s2)
+    st = paged.Vq2mStore(path)
+    assert st.promoted_experts(1) == [2] and st.promoted_experts(0) == []
+    assert st.promoted_sizes == (32 * 16 * 3, 32 * 2, 64 * 4 * 3, 64 * 2)
+    r = st.read_promoted(1, 2)
+    gui, gus, dni, dns = t
+    assert torch.equal(r["gu0"], gui[1][2]) and torch.equal(r["gu1"], s2[(1, 2)][0])
+    assert torch.equal(r["dn0"], dni[1][2]) and torch.equal(r["dn1"], s2[(1, 2)][1])
+    assert torch.equal(r["gu_s"], gus[1][2]) and torch.equal(r["dn_s"], dns[1][2])
+    # the gate_up index entry is the two planes back to back
+    off, sz = st.entries[1][2][0], st.entries[1][2][1]
+    raw = open(path, "rb").read()[off:off + sz]
+    assert raw == gui[1][2].numpy().tobytes() + s2[(1, 2)][0].numpy().tobytes()
+    with pytest.raises(ValueError, match="promoted"):
+        st.read_record(1, 2, memoryview(bytearray(st.record_bytes)))
+    with pytest.raises(ValueError, match="not a promoted"):
+        st.read_promoted(0, 2)
+    # a regular record of the same layer still reads through the pager path
+    buf = bytearray(st.record_bytes)
+    st.read_record(1, 1, memoryview(buf))
+    assert bytes(buf) == _record(t, 1, 1)
+    st.close()
+
+
+def test_promoted_layer_needs_stage2_codebook(tmp_path):
+    t = _layers(1, 3, gu=(64, 16), dn=(128, 4), seed=7)
+    s2 = {(0, 1): (torch.zeros(64, 16, dtype=torch.uint8), torch.zeros(128, 4, dtype=torch.uint8))}
+    path = tmp_path / "q.vq2m"
+    paged.write_vq2m(path, *t, promoted=s2)
+    st = paged.Vq2mStore(path)
+    cb = torch.zeros(65536, 8, dtype=torch.float16)
+    with pytest.raises(Exception, match="cb8"):
+        paged.PagedMoEExperts(0, st, cb, capacity=2, device="cpu")
+    st.close()
