@@ -541,18 +541,7 @@ def test_fused_router_gate_up_matches_router_and_unfused(dev, E, k, shared, T):
 
 
 # ------------------------------------------------------------ unpack_fixed
-def _pack(sym, bits):
-    """Little-endian fixed-width packing, built bit by bit (independent of
-    the byte formulas of the oracle and the kernel); 4- and 12-bit streams
-    are padded to whole symbol pairs as vq2/export.py:39-53 does."""
-    if bits in (4, 12) and len(sym) % 2:
-        sym = np.append(sym, 0)
-    nbits = len(sym) * bits
-    out = np.zeros((nbits + 7) // 8, np.uint8)
-    bitpos = np.arange(len(sym))[:, None] * bits + np.arange(bits)[None, :]
-    vals = (sym[:, None] >> np.arange(bits)[None, :]) & 1
-    np.add.at(out, bitpos.reshape(-1) // 8, (vals.reshape(-1) << (bitpos.reshape(-1) % 8)).astype(np.uint8))
-    return out[: (nbits + 7) // 8]
+from vq2_containers import pack_fixed as _pack  # noqa: E402
 
 
 @pytest.mark.parametrize("bits", [4, 8, 12, 16])
