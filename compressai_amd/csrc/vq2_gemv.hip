@@ -13,13 +13,8 @@ namespace vq2 {
 // LDS the planner allows per workgroup (two workgroups per CU stay resident)
 constexpr int64_t GEMV_LDS_BUDGET = 64 * 1024;
 
-// Tuning overrides read once from the environment (VQ2_GEMV_IT: rows per
-// lane 1/2/4; VQ2_GEMV_OCC_SCALE: multiplier on the resident-workgroup grid).
-static int env_int(const char* name, int dflt)
-{
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
+// Tuning override read once from the environment (VQ2_GEMV_OCC_SCALE:
+// multiplier on the resident-workgroup grid).
 static double env_double(const char* name, double dflt)
 {
     const char* v = getenv(name);
@@ -57,18 +52,24 @@ static GemvPlan plan_gemv(const GemvCall& c, int num_cu)
     const int64_t kc = (int64_t)lpr * p.gpl;
     const int64_t nch = (c.ng + kc - 1) / kc;
     const int64_t items = (int64_t)P * nch;
-    p.wi = (int)(items < 4 ? items : 4);
-    p.wr = 4 / p.wi;
+    if (items <= 4) {
+        p.wi = (int)items;
+        p.wr = 4 / p.wi;
+    } else {
+        // more items than 4 waves: up to the kernel's wave limit, balanced so
+        // that every wave runs the same number of item rounds (a wave's
+        // items run one after the other, each a full index + gather latency)
+        const int64_t wi_max = gemv_max_threads(c.s2, c.cb_dt, c.xm) / 64;
+        const int64_t rounds = (items + wi_max - 1) / wi_max;
+        p.wi = wi_max <= 4 ? 4 : (int)((items + rounds - 1) / rounds);
+        p.wr = 1;
+    }
     p.threads = 64 * p.wi * p.wr;
     const int rpw = 64 / lpr;
     const int64_t ztiles = (batch + p.bt - 1) / p.bt;
     int64_t max_rows = 0;
     for (int s = 0; s < c.nseg; s++) max_rows = c.seg[s].out_rows > max_rows ? c.seg[s].out_rows : max_rows;
-    // rows per lane (measured on MI355X over the decode shapes): 1, except
-    // 2 for the 8-column batch tile, whose lanes hold one code per row
-    p.it = p.bt == 8 ? 2 : 1;
-    static const int it_env = env_int("VQ2_GEMV_IT", 0);
-    if (it_env == 1 || it_env == 2 || it_env == 4) p.it = it_env;
+    p.it = p.bt == 8 ? gemv_it<8>() : gemv_it<1>();
     static const double occ_env = env_double("VQ2_GEMV_OCC_SCALE", 1.0);
     p.occ_scale = occ_env > 0 ? occ_env : 1.0;
     p.num_cu = num_cu;
@@ -190,7 +191,7 @@ int gemv_launch(const GemvCall& c)
     a.lpr = p.lpr;
     a.wi = p.wi;
     a.n_rowblocks = p.n_rowblocks;
-    if (p.threads > 256 || p.threads % 64)
+    if (p.threads > gemv_max_threads(c.s2, c.cb_dt, c.xm) || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
     if (c.xm == 2 && (c.s2 == VQ2_S2_U16 || p.bt != 1))
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 and 3 bpw, batch 1");

@@ -517,8 +517,19 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 // workgroup keeps the best (value, row) key of each batch column over its
 // row blocks and writes it to a.cand[blockIdx.x * batch + column] (the fused
 // top-1 of the LM head).
+// Workgroup size limit.  The expert epilogue (XM 2: SwiGLU + RHT + down +
+// combine over the P pairs of a token) runs one pair per wave, so it takes
+// up to 12 waves (2 bpw, fp16 codebook; <= 170 VGPRs at 3 waves per SIMD)
+// or 8 (the rest; <= 256 VGPRs), which those instantiations fit without
+// spilling.  Every other kernel keeps 4 waves: a wider bound changes their
+// register allocation, and the dense launches measured slower with it.
+constexpr int gemv_max_threads(int s2, int cbt, int xm)
+{
+    return xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512);
+}
+
 template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
-__global__ void __launch_bounds__(256) vq_gemv_kernel(const GemvArgs a)
+__global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(const GemvArgs a)
 {
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
@@ -875,14 +886,16 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
     }
 }
 
+// rows per lane: 2 for the 8-column batch tile (its lanes hold one code per
+// row), else 1 -- measured on MI355X over the decode shapes
+template <int BT>
+constexpr int gemv_it() { return BT == 8 ? 2 : 1; }
+
 template <int CBT, int S2, int GPL, int BT>
 inline hipError_t launch_it(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
 {
-    switch (p.it) {
-    case 4: return launch_xm<CBT, S2, GPL, BT, 4>(a, p, grid, shm, st);
-    case 2: return launch_xm<CBT, S2, GPL, BT, 2>(a, p, grid, shm, st);
-    default: return launch_xm<CBT, S2, GPL, BT, 1>(a, p, grid, shm, st);
-    }
+    if (p.it != gemv_it<BT>()) return hipErrorInvalidValue;
+    return launch_xm<CBT, S2, GPL, BT, gemv_it<BT>()>(a, p, grid, shm, st);
 }
 
 template <int CBT, int S2>
