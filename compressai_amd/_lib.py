@@ -43,6 +43,9 @@ SIGNATURES = {
                                           _vp, _i64, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _f32,
                                           _i32, _vp], _i32),
     "vq2_gemm_small_m_workspace": ([_i64, _i64, _i64], ctypes.c_size_t),
+    "vq2_gemm_small_m_argmax_workspace": ([_i64, _i64, _i64], ctypes.c_size_t),
+    "vq2_gemm_small_m_argmax": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _f32,
+                                 _vp, ctypes.c_size_t, _vp, _vp, _vp], _i32),
     "vq2_gemm_small_m": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
                           _i64, _i64, _f32, _vp, ctypes.c_size_t, _vp], _i32),
     "vq2_moe_grouped": ([_vp, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _i32,

@@ -178,6 +178,54 @@ int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride, c
     return gemm_small_m_launch(c);
 }
 
+size_t vq2_gemm_small_m_argmax_workspace(int64_t batch, int64_t out_rows, int64_t n)
+{
+    if (batch < 1 || batch > 64 || out_rows < 1 || n < 64 || n % 64) return 0;
+    return gemm_small_m_top1_workspace_bytes(batch, out_rows, n / 8);
+}
+
+int vq2_gemm_small_m_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0,
+                            const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
+                            const void* scale, int s_dt, int64_t out_rows, int64_t n, float rs, void* workspace,
+                            size_t ws_bytes, int64_t* out_idx, float* out_val, void* stream)
+{
+    clear_error();
+    CHECK(batch >= 0 && batch <= 64 && out_rows >= 1 && out_rows <= 0xFFFFFFFFLL && n > 0,
+          "vq2_gemm_small_m_argmax: bad sizes batch=%lld (0..64) out_rows=%lld n=%lld", (long long)batch,
+          (long long)out_rows, (long long)n);
+    CHECK(n % 64 == 0, "vq2_gemm_small_m_argmax: n=%lld is not a multiple of 64", (long long)n);
+    if (batch == 0) return VQ2_OK;
+    CHECK(x && idx0 && scale && out_idx, "vq2_gemm_small_m_argmax: NULL pointer argument");
+    CHECK((uintptr_t)out_idx % 8 == 0, "vq2_gemm_small_m_argmax: out_idx must be 8-byte aligned");
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt), "vq2_gemm_small_m_argmax: bad dtype code");
+    CHECK(x_stride >= n, "vq2_gemm_small_m_argmax: x_stride < n");
+    int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
+    if (r) return r;
+    CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr),
+          "vq2_gemm_small_m_argmax: idx1 must be given iff s2_kind != NONE");
+    GemmCall c{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.x_stride = x_stride;
+    c.m = batch;
+    c.idx0 = idx0;
+    c.idx1 = idx1;
+    c.s2 = s2_kind;
+    c.cb0 = cb0;
+    c.cb1 = cb1;
+    c.cb_dt = cb_dt;
+    c.scale = scale;
+    c.s_dt = s_dt;
+    c.y_dt = VQ2_DT_F32;
+    c.out_rows = out_rows;
+    c.ng = n / 8;
+    c.rs = rs;
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
+    c.stream = stream;
+    return gemm_small_m_top1_launch(c, out_idx, out_val);
+}
+
 int vq2_gemv_rht(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int32_t* perm, const int8_t* sign,
                  int64_t hb, float rht_scale, int n_seg, const vq2_seg* segs, int s2_kind, const void* cb0,
                  const void* cb1, int cb_dt, int s_dt, int y_dt, int64_t n, float rs, void* stream)

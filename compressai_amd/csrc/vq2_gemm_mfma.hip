@@ -67,7 +67,9 @@ struct GemmArgs {
     float rs;
     int kcg;     // groups per K split (multiple of 32)
     int splits;  // K splits (grid.y)
-    float* part; // [splits][m][out_rows] raw partials when splits > 1
+    float* part; // [splits][m][out_rows] raw partials when splits > 1 or to_part
+    int to_part;     // write raw partials even with one split (fused top-1)
+    uint64_t* cand;  // fused top-1: [gridDim.x of the reduce][m] best keys
 };
 
 // One centroid as 8 fp16 values (the MFMA B operand).
@@ -239,7 +241,8 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
 
     // D[i][j]: activation row mt * 16 + 4q + e, output row `row`
     if (!row_ok) return;
-    const float s = a.splits == 1 ? load_as_f32(a.scale, a.s_dt, row) : 0.0f;
+    const bool direct = a.splits == 1 && !a.to_part;
+    const float s = direct ? load_as_f32(a.scale, a.s_dt, row) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
@@ -247,7 +250,7 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
             const int m = mt * 16 + q * 4 + e;
             if (m >= a.m) continue;
             const float p = ldexpf(acc[mt][e], -s_e[m]);
-            if (a.splits == 1)
+            if (direct)
                 store_from_f32(a.y, a.y_dt, (int64_t)m * a.y_stride + row, (p * s) * a.rs);
             else
                 a.part[((int64_t)blockIdx.y * a.m + m) * a.out_rows + row] = p;
@@ -268,6 +271,42 @@ __global__ void __launch_bounds__(256) vq_gemm_reduce_kernel(const GemmArgs a)
         store_from_f32(a.y, a.y_dt, m * a.y_stride + row, (sum * s) * a.rs);
     }
 }
+
+// Fused top-1 of every activation row m = blockIdx.y: the same split-order
+// sum and (sum * s) * rs as vq_gemm_reduce_kernel, so the keys are those of
+// the fp32 logits; each block keeps the best (value, row) key and writes it
+// to cand[blockIdx.x * m_total + m] for argmax_final_kernel.  No logits are
+// written.
+__global__ void __launch_bounds__(256) vq_gemm_reduce_top1_kernel(const GemmArgs a)
+{
+    const int m = blockIdx.y;
+    const int64_t pstride = (int64_t)a.m * a.out_rows;
+    uint64_t best = 0;
+    for (int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; row < a.out_rows;
+         row += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = (int64_t)m * a.out_rows + row;
+        float sum = 0.0f;
+        for (int sp = 0; sp < a.splits; sp++) sum += __builtin_nontemporal_load(&a.part[sp * pstride + t]);
+        const float s = load_as_f32(a.scale, a.s_dt, row);
+        const uint64_t k = argmax_key((sum * s) * a.rs, row);
+        best = k > best ? k : best;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    __shared__ uint64_t s_best[4];
+    if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = s_best[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) b = s_best[w] > b ? s_best[w] : b;
+        a.cand[(int64_t)blockIdx.x * a.m + m] = b;
+    }
+}
+
+// reduce blocks per activation row of the fused top-1 (bounds its candidates)
+constexpr int64_t MM_TOP1_BLOCKS = 1024;
 
 struct GemmPlan {
     int mt;
@@ -306,6 +345,25 @@ static GemmPlan plan_gemm(int64_t m, int64_t out_rows, int64_t ng, int num_cu, b
     p.kcg = kcg;
     p.splits = (int)((ng + kcg - 1) / kcg);
     return p;
+}
+
+static int64_t top1_blocks(int64_t out_rows)
+{
+    const int64_t b = (out_rows + 255) / 256;
+    return b < MM_TOP1_BLOCKS ? b : MM_TOP1_BLOCKS;
+}
+
+// partials of every split (one at least), 256-byte aligned, then the keys
+static size_t top1_part_bytes(int64_t m, int64_t out_rows, int splits)
+{
+    return ((size_t)(splits > 1 ? splits : 1) * m * out_rows * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t gemm_small_m_top1_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng)
+{
+    if (m < 1 || out_rows < 1 || ng < 1) return 0;
+    const GemmPlan p = plan_gemm(m, out_rows, ng, device_cu_count(), false);
+    return top1_part_bytes(m, out_rows, p.splits) + (size_t)top1_blocks(out_rows) * m * sizeof(uint64_t);
 }
 
 size_t gemm_small_m_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng)
@@ -352,8 +410,9 @@ static hipError_t launch_mm_s2(int s2, int mt, const GemmArgs& a, dim3 grid, siz
     }
 }
 
-int gemm_small_m_launch(const GemmCall& c)
+static int gemm_launch(const GemmCall& c, int64_t* top1_idx, float* top1_val)
 {
+    const bool top1 = top1_idx != nullptr;
     if (c.m < 1 || c.m > MM_MAX_M) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 small-M GEMM: batch must be 1..%d", MM_MAX_M);
     if (c.out_rows == 0) return VQ2_OK;
     if (c.ng % 8) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 small-M GEMM: n must be a multiple of 64");
@@ -386,12 +445,16 @@ int gemm_small_m_launch(const GemmCall& c)
     a.kcg = p.kcg;
     a.splits = p.splits;
     a.part = (float*)c.workspace;
-    if (p.splits > 1) {
-        const size_t need = (size_t)p.splits * c.m * c.out_rows * sizeof(float);
+    a.to_part = top1 ? 1 : 0;
+    const int64_t t1_blocks = top1_blocks(c.out_rows);
+    if (p.splits > 1 || top1) {
+        const size_t need = top1 ? top1_part_bytes(c.m, c.out_rows, p.splits) + (size_t)t1_blocks * c.m * sizeof(uint64_t)
+                                 : (size_t)p.splits * c.m * c.out_rows * sizeof(float);
         if (!c.workspace || c.ws_bytes < need)
             return set_error(VQ2_ERR_ARG, "vq2 small-M GEMM: workspace of %zu bytes needed (got %zu)", need, c.ws_bytes);
         if ((uintptr_t)c.workspace % 16) return set_error(VQ2_ERR_ARG, "vq2 small-M GEMM: workspace must be 16-byte aligned");
     }
+    if (top1) a.cand = (uint64_t*)((char*)c.workspace + top1_part_bytes(c.m, c.out_rows, p.splits));
     const size_t shm = (size_t)p.mt * 16 * (p.kcg + 1) * sizeof(half8_t);
     hipStream_t st = (hipStream_t)c.stream;
     const dim3 grid((unsigned)p.rowtiles, (unsigned)p.splits);
@@ -402,6 +465,12 @@ int gemm_small_m_launch(const GemmCall& c)
     default: err = launch_mm_s2<VQ2_DT_F32>(c.s2, p.mt, a, grid, shm, st); break;
     }
     if (err != hipSuccess) return set_hip_error(err, "vq2 small-M GEMM launch");
+    if (top1) {
+        hipLaunchKernelGGL(vq_gemm_reduce_top1_kernel, dim3((unsigned)t1_blocks, (unsigned)c.m), dim3(256), 0, st, a);
+        err = hipGetLastError();
+        if (err != hipSuccess) return set_hip_error(err, "vq2 small-M GEMM top-1 reduce launch");
+        return argmax_final_launch(a.cand, (unsigned)t1_blocks, c.m, top1_idx, top1_val, c.stream);
+    }
     if (p.splits > 1) {
         const int64_t tot = c.m * c.out_rows;
         int64_t blocks = (tot + 255) / 256;
@@ -411,6 +480,14 @@ int gemm_small_m_launch(const GemmCall& c)
         if (err != hipSuccess) return set_hip_error(err, "vq2 small-M GEMM reduce launch");
     }
     return VQ2_OK;
+}
+
+int gemm_small_m_launch(const GemmCall& c) { return gemm_launch(c, nullptr, nullptr); }
+
+int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val)
+{
+    if (!out_idx) return set_error(VQ2_ERR_ARG, "vq2 small-M GEMM top-1: NULL out_idx");
+    return gemm_launch(c, out_idx, out_val);
 }
 
 }  // namespace vq2

@@ -111,6 +111,9 @@ struct GemmCall {
 
 size_t gemm_small_m_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
 int gemm_small_m_launch(const GemmCall& c);
+// the GEMM with the top-1 of every activation row instead of y (c.y unused)
+size_t gemm_small_m_top1_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
+int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val);
 
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
                const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,

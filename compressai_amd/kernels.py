@@ -622,26 +622,32 @@ def vq_gemv_argmax(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, logits_ws=Non
     n, out = int(n), int(out)
     x2 = _contig(xr, "xr").reshape(-1, n)
     B = x2.shape[0]
-    if logits_ws is None:
-        logits_ws = torch.empty((B, out), dtype=torch.float32, device=dev)
+    i0, i1, s2 = _planes(i0, i1, cb0, cb1, scale, out, n)
+    idx = torch.empty(B, dtype=torch.int64, device=dev)
+    val = torch.empty(B, dtype=torch.float32, device=dev)
     if B < 3 or n % 64:
         # fused top-1 (no logits written) where the shape allows, else logits + top-1
-        i0, i1, s2 = _planes(i0, i1, cb0, cb1, scale, out, n)
+        if logits_ws is None:
+            logits_ws = torch.empty((B, out), dtype=torch.float32, device=dev)
         _contig(logits_ws, "logits_ws")
         if logits_ws.dtype != torch.float32 or logits_ws.numel() < B * out:
             raise Vq2Error("logits_ws must be float32 with B * out elements")
-        idx = torch.empty(B, dtype=torch.int64, device=dev)
-        val = torch.empty(B, dtype=torch.float32, device=dev)
         _lib.call("vq2_gemv_argmax", _p(x2), _dt(x2, "xr"), B, x2.stride(0) if B > 1 else n, _p(i0), _p(i1), s2,
                   _p(cb0), _p(cb1), _dt(cb0, "cb0"), _p(scale), _dt(scale, "scale"), out, n, float(rs),
                   _p(logits_ws), _p(idx), _p(val), _stream(dev))
         return idx, val
     else:
-        # matrix cores: every centroid is gathered once per 64 rows
+        # matrix cores (every centroid gathered once per 64 rows), the top-1
+        # fused into the split-K reduce: no logits written
+        lib = _lib.load()
         for b0 in range(0, B, 64):
             b1 = min(B, b0 + 64)
-            vq_gemm_small_m(x2[b0:b1], i0, i1, cb0, cb1, scale, out, n, rs, y=logits_ws[b0:b1])
-    return vq_argmax(logits_ws)
+            xb = x2[b0:b1]
+            ws = _workspace(dev, int(lib.vq2_gemm_small_m_argmax_workspace(b1 - b0, out, n)))
+            _lib.call("vq2_gemm_small_m_argmax", _p(xb), _dt(xb, "xr"), b1 - b0, x2.stride(0), _p(i0), _p(i1), s2,
+                      _p(cb0), _p(cb1), _dt(cb0, "cb0"), _p(scale), _dt(scale, "scale"), out, n, float(rs), _p(ws),
+                      ws.numel(), _p(idx[b0:b1]), _p(val[b0:b1]), _stream(dev))
+        return idx, val
 
 
 # --------------------------------------------------------------- debugging

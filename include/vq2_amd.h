@@ -93,6 +93,24 @@ int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride,
                      int64_t out_rows, int64_t n, float rs,
                      void* workspace, size_t ws_bytes, void* stream);
 
+/* vq2_gemm_small_m followed by the top-1 of every activation row, without
+ * writing the logits: out_idx[b] = argmax_r y[b, r] (torch.argmax's first
+ * maximum; int64, 8-byte aligned), out_val[b] = y[b, out_idx[b]] (fp32, may
+ * be NULL), with y computed exactly as vq2_gemm_small_m computes it in fp32.
+ * The partials sum and the scale go into one reduce launch that keeps each
+ * block's best key, and a last launch picks the winner.  `workspace`:
+ * vq2_gemm_small_m_argmax_workspace(...) bytes, 16-byte aligned, contents on
+ * entry do not matter.  Replaces PackedLMHead.forward at batch > 1
+ * (vq2/runtime.py:136-144, 105-110) + torch.argmax (legion/engine.py:288). */
+size_t vq2_gemm_small_m_argmax_workspace(int64_t batch, int64_t out_rows, int64_t n);
+int vq2_gemm_small_m_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                            const int16_t* idx0, const void* idx1, int s2_kind,
+                            const void* cb0, const void* cb1, int cb_dt,
+                            const void* scale, int s_dt,
+                            int64_t out_rows, int64_t n, float rs,
+                            void* workspace, size_t ws_bytes,
+                            int64_t* out_idx, float* out_val, void* stream);
+
 /* One matrix of a vq2_gemv_rht launch: index planes, row scales and output
  * (y [batch, y_stride], dtype of the launch), all device pointers. */
 typedef struct vq2_seg {

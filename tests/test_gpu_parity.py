@@ -511,6 +511,38 @@ def test_lm_head_argmax_small_m_batch(dev):
             assert abs(y64[b, int(idx[b])] - y64[b, int(ref[b])]) <= TOL * np.abs(y64[b]).max()
 
 
+@pytest.mark.parametrize("B,out,bpw", [(3, 4096, 2), (4, 40000, 2), (17, 3000, 4), (64, 2048, 3), (70, 1000, 2)])
+def test_small_m_fused_top1_equals_logits_argmax(dev, B, out, bpw):
+    """The matrix-core LM-head top-1 (top-1 fused into the split-K reduce, no
+    logits written) returns exactly torch.argmax / the value of the same
+    GEMM's fp32 logits, including a tie placed across reduce blocks."""
+    n = 2048
+    m = synth.vq_matrix(7600 + B, out, n, bpw=bpw)
+    cbs = {2: (synth.codebook(7601), None), 3: (synth.codebook(7601), synth.codebook(7602, rows=256)),
+           4: (synth.codebook(7601), synth.codebook(7603))}[bpw]
+    i1 = m.get("idx1")
+    i0 = m["idx0"].clone()
+    sc = m["scale"].clone()
+    if out > 600:  # rows 300 and out-1 identical and scaled up: a tie that wins where its dot is > 0
+        i0[out - 1] = i0[300]
+        sc[300] = sc[out - 1] = 12.0
+        if i1 is not None:
+            i1 = i1.clone()
+            i1[out - 1] = i1[300]
+    x = synth.activations(7604 + B, (B, n), dtype=torch.float32)
+    args = _cuda(x, i0, i1, cbs[0], cbs[1], sc, dev=dev)
+    idx, val = K.vq_gemv_argmax(*args, out, n)
+    logits = torch.cat([K.vq_gemm_small_m(args[0][b0:b0 + 64], *args[1:], out, n, out_dtype=torch.float32)
+                        for b0 in range(0, B, 64)])
+    ref_val, ref_idx = torch.max(logits, dim=1)
+    assert torch.equal(idx, torch.argmax(logits, dim=1))
+    assert torch.equal(val, ref_val)
+    if out > 600:
+        assert torch.equal(logits[:, 300], logits[:, out - 1])
+        assert not torch.any(idx == out - 1)  # the first of the tied rows
+        assert torch.any(idx == 300)
+
+
 @pytest.mark.parametrize("E,k,shared,T", [(256, 8, True, 1), (256, 8, True, 8), (300, 4, False, 3),
                                           (64, 2, True, 5)])
 def test_fused_router_gate_up_matches_router_and_unfused(dev, E, k, shared, T):
