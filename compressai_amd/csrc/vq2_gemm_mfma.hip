@@ -126,6 +126,7 @@ __device__ __forceinline__ void load8_f32(const void* p, int dt, int64_t off, fl
 template <int CBT, int S2, int MT>
 __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs a)
 {
+    touch_kernargs(a);
     constexpr int MP = MT * 16;
     extern __shared__ half8_t s_xh[];  // [MP][kcg + 1] activation groups (fp16, scaled)
     __shared__ uint32_t s_amax[MP];

@@ -190,6 +190,7 @@ int gemv_launch(const GemvCall& c)
     }
     a.lpr = p.lpr;
     a.wi = p.wi;
+    a.nch = (int)((c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl));
     a.n_rowblocks = p.n_rowblocks;
     if (p.threads > gemv_max_threads(c.s2, c.cb_dt, c.xm) || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);

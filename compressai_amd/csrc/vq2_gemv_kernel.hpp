@@ -72,6 +72,7 @@ struct GemvArgs {
     float rs;
     int lpr;  // lanes per row (power of two <= 32)
     int wi;   // waves along work items (pair x chunk)
+    int nch;  // K chunks of lpr * GPL groups per row
     int64_t n_rowblocks;
     int nseg;
     GemvSeg seg[VQ2_MAX_SEG];
@@ -528,12 +529,30 @@ constexpr int gemv_max_threads(int s2, int cbt, int xm)
     return xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512);
 }
 
+// Touch every 64-byte line of the kernel arguments with independent scalar
+// loads at entry.  The fields the kernel reads before its first index load
+// (plan, segment, expert ids) come in a chain of dependent scalar loads with
+// a wait after each; with the lines already in the scalar cache every link
+// is a hit (measured on MI355X: first index load issued 0.4-0.5 us sooner).
+template <typename T>
+__device__ __forceinline__ void touch_kernargs(const T& a)
+{
+    const uint32_t* w = (const uint32_t*)&a;
+    uint32_t h = 0;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 4); i += 16) h ^= w[i];
+    __shared__ volatile uint32_t s_sink;  // keeps the loads; the store never happens in practice
+    if (h == 0x9E3779B9u) s_sink = h;
+}
+
 template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
 __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(const GemvArgs a)
 {
+    touch_kernargs(a);
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
-    extern __shared__ float s_dyn[];  // [activation block (XM != 0)] [item partials]
+    // 16-byte aligned: the activation block is written and read with 16-byte LDS accesses
+    extern __shared__ __align__(16) float s_dyn[];  // [activation block (XM != 0)] [item partials]
     // XM 3 is XM 1 (rotate x in the prologue) with the router built in
     constexpr int XP = XM == 3 ? 1 : XM;
 
@@ -553,7 +572,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
     const int rpw = 64 / lpr;
     const int sub = lane / lpr, col = lane % lpr;
     const int64_t kc = (int64_t)lpr * GPL;
-    const int nch = (int)((a.ng + kc - 1) / kc);
+    const int nch = a.nch;
     const int items = a.P * nch;
     const int rows_per_block = IT * rpw * wr;
 
