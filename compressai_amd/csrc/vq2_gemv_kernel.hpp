@@ -311,14 +311,51 @@ __device__ __forceinline__ void fwht_pass(float* v, int64_t total, int lo)
     }
 }
 
-__device__ __forceinline__ void block_fwht(float* v, int64_t total, int L)
+__device__ __forceinline__ void block_fwht(float* v, int64_t total, int L, int lo0 = 0)
 {
-    for (int lo = 0; lo < L; lo += 3) {
+    for (int lo = lo0; lo < L; lo += 3) {
         const int w = L - lo < 3 ? L - lo : 3;
         if (w == 3) fwht_pass<3>(v, total, lo);
         else if (w == 2) fwht_pass<2>(v, total, lo);
         else fwht_pass<1>(v, total, lo);
         __syncthreads();
+    }
+}
+
+// The stages of bits 0-5 of the 2^L-point blockwise FWHT for the 8
+// consecutive elements [8u, 8u + 8) that thread u holds: bits 0-2 inside the
+// thread, bits 3-5 with lanes u ^ 1, u ^ 2, u ^ 4 -- the stages, their order
+// and their operands as block_fwht's first two passes, so the values are the
+// same, without those passes' strided (bank-conflicting) LDS traffic and
+// barriers.  Every 2^L block whose element the thread holds lies entirely
+// inside [0, total) with total a multiple of 2^L, so partner lanes are active.
+__device__ __forceinline__ void fwht_head(float (&v)[8], int L)
+{
+#pragma unroll
+    for (int b = 0; b < 3; b++) {
+        const int h = 1 << b;
+        if (b < L) {
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if ((k & h) == 0) {
+                    const float x0 = v[k], x1 = v[k | h];
+                    v[k] = x0 + x1;
+                    v[k | h] = x0 - x1;
+                }
+        }
+    }
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 3; b < 6; b++) {
+        const int m = 1 << (b - 3);
+        if (b < L) {
+            const bool hi = (lane & m) != 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float p = __shfl_xor(v[k], m);
+                v[k] = hi ? p - v[k] : v[k] + p;
+            }
+        }
     }
 }
 
@@ -381,11 +418,14 @@ __device__ __forceinline__ void build_x_t(const GemvArgs& a, float* s_x, int nro
 #pragma unroll
             for (int k = 0; k < 8; k++) v[k] = silu_f32(g[k]) * u[k];
         }
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = bad[k] ? __builtin_nanf("") : v[k] * sg[k];
+        fwht_head(v, a.hb_log2);
         u32x4 o0, o1;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            o0[k] = __float_as_uint(bad[k] ? __builtin_nanf("") : v[k] * sg[k]);
-            o1[k] = __float_as_uint(bad[4 + k] ? __builtin_nanf("") : v[4 + k] * sg[4 + k]);
+            o0[k] = __float_as_uint(v[k]);
+            o1[k] = __float_as_uint(v[4 + k]);
         }
         *(u32x4*)(s_x + t0) = o0;
         *(u32x4*)(s_x + t0 + 4) = o1;
@@ -399,7 +439,7 @@ __device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, int nrows
     else if (a.x_dt == VQ2_DT_F16) build_x_t<XM, VQ2_DT_F16>(a, s_x, nrows, n, og, bt0);
     else build_x_t<XM, VQ2_DT_BF16>(a, s_x, nrows, n, og, bt0);
     __syncthreads();
-    block_fwht(s_x, (int64_t)nrows * n, a.hb_log2);
+    block_fwht(s_x, (int64_t)nrows * n, a.hb_log2, 6);  // bits 0-5 done by fwht_head
 }
 
 // A lane's activation slice from the LDS activation block.
