@@ -352,7 +352,16 @@ __device__ __forceinline__ void fwht_head(float (&v)[8], int L)
             const bool hi = (lane & m) != 0;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const float p = __shfl_xor(v[k], m);
+                // lane ^ 1 and lane ^ 2 stay inside a quad: a DPP quad_perm
+                // move ([1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E) instead of an
+                // LDS-pipe permute
+                float p;
+                if (m == 1)
+                    p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[k]), 0xB1, 0xF, 0xF, true));
+                else if (m == 2)
+                    p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[k]), 0x4E, 0xF, 0xF, true));
+                else
+                    p = __shfl_xor(v[k], m);
                 v[k] = hi ? p - v[k] : v[k] + p;
             }
         }
