@@ -352,16 +352,21 @@ __device__ __forceinline__ void fwht_head(float (&v)[8], int L)
             const bool hi = (lane & m) != 0;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                // lane ^ 1 and lane ^ 2 stay inside a quad: a DPP quad_perm
-                // move ([1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E) instead of an
-                // LDS-pipe permute
+                // DPP moves instead of LDS-pipe permutes: lane ^ 1 and
+                // lane ^ 2 by quad_perm ([1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E),
+                // lane ^ 4 by row_shl:4 (lane + 4, 0x104) where bit 2 is clear
+                // and row_shr:4 (lane - 4, 0x114) where it is set
                 float p;
+                const int vi = __float_as_int(v[k]);
                 if (m == 1)
-                    p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[k]), 0xB1, 0xF, 0xF, true));
+                    p = __int_as_float(__builtin_amdgcn_mov_dpp(vi, 0xB1, 0xF, 0xF, true));
                 else if (m == 2)
-                    p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[k]), 0x4E, 0xF, 0xF, true));
-                else
-                    p = __shfl_xor(v[k], m);
+                    p = __int_as_float(__builtin_amdgcn_mov_dpp(vi, 0x4E, 0xF, 0xF, true));
+                else {
+                    const int up = __builtin_amdgcn_mov_dpp(vi, 0x104, 0xF, 0xF, true);
+                    const int dn = __builtin_amdgcn_mov_dpp(vi, 0x114, 0xF, 0xF, true);
+                    p = __int_as_float(hi ? dn : up);
+                }
                 v[k] = hi ? p - v[k] : v[k] + p;
             }
         }
