@@ -170,4 +170,22 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int64_t col)
 
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
 
+// Touch every 64-byte line of the kernel arguments with independent scalar
+// loads at entry.  The fields the kernel reads before its first index load
+// (plan, segment, expert ids) come in a chain of dependent scalar loads with
+// a wait after each; with the lines already in the scalar cache every link
+// is a hit (measured on MI355X: first index load issued 0.4-0.5 us sooner).
+template <typename T>
+__device__ __forceinline__ void touch_kernargs(const T& a)
+{
+    const uint32_t* w = (const uint32_t*)&a;
+    uint32_t h = 0;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 4); i += 16) h ^= w[i];
+    // keeps the loads; the store never happens in practice.  16 aligned bytes,
+    // so LDS arrays placed after it keep their 16-byte alignment.
+    __shared__ __align__(16) volatile uint32_t s_sink[4];
+    if (h == 0x9E3779B9u) s_sink[0] = h;
+}
+
 }  // namespace vq2

@@ -583,22 +583,6 @@ constexpr int gemv_max_threads(int s2, int cbt, int xm)
     return xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512);
 }
 
-// Touch every 64-byte line of the kernel arguments with independent scalar
-// loads at entry.  The fields the kernel reads before its first index load
-// (plan, segment, expert ids) come in a chain of dependent scalar loads with
-// a wait after each; with the lines already in the scalar cache every link
-// is a hit (measured on MI355X: first index load issued 0.4-0.5 us sooner).
-template <typename T>
-__device__ __forceinline__ void touch_kernargs(const T& a)
-{
-    const uint32_t* w = (const uint32_t*)&a;
-    uint32_t h = 0;
-#pragma unroll
-    for (int i = 0; i < (int)(sizeof(T) / 4); i += 16) h ^= w[i];
-    __shared__ volatile uint32_t s_sink;  // keeps the loads; the store never happens in practice
-    if (h == 0x9E3779B9u) s_sink = h;
-}
-
 template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
 __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(const GemvArgs a)
 {

@@ -155,6 +155,7 @@ __device__ __forceinline__ void rht_load(const RhtArgs& a, int64_t b, int64_t e0
 template <int L>
 __global__ void __launch_bounds__(256) rht_kernel(const RhtArgs a)
 {
+    touch_kernargs(a);
     using S = RhtShape<L>;
     __shared__ float lds[S::NP > 1 ? S::HB : 1];
     const int tid = threadIdx.x;
