@@ -188,6 +188,8 @@ int gemv_launch(const GemvCall& c)
                            c.seg[s].y_bstride, rb};
         rb += (c.seg[s].out_rows + p.rows_per_block - 1) / p.rows_per_block;
     }
+    // unused segment slots start past every row block: seg_of() needs no nseg
+    for (int s = c.nseg; s < VQ2_MAX_SEG; s++) a.seg[s].rb_start = INT64_MAX;
     a.lpr = p.lpr;
     a.wi = p.wi;
     a.nch = (int)((c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl));

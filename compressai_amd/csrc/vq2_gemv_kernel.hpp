@@ -475,15 +475,26 @@ __device__ __forceinline__ void load_x_lds(const float* s_x, int64_t row0, int64
     }
 }
 
+// Segment of row block rb: a sum of independent comparisons (unused slots
+// start at INT64_MAX), so the segment starts load together, with no
+// dependent loop.
+__device__ __forceinline__ int seg_of(const GemvArgs& a, int64_t rb)
+{
+    int si = 0;
+#pragma unroll
+    for (int s = 1; s < VQ2_MAX_SEG; s++) si += rb >= a.seg[s].rb_start ? 1 : 0;
+    return si;
+}
+
 // Codes of row block rb for this lane (zeros and valid = false past the
-// end, for idle lanes and for rows beyond their segment).
-template <int S2, int GPL, int IT>
+// end, for idle lanes and for rows beyond their segment).  SEG0: the launch
+// has one segment, read at a fixed offset (no dependent segment lookup).
+template <int S2, int GPL, int IT, bool SEG0 = false>
 __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int rows_per_block, int wr, int wr_id,
                                             int rpw, int sub, int64_t g0, bool lane_ok, int64_t e,
                                             uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
 {
-    int si = 0;
-    while (si + 1 < a.nseg && rb >= a.seg[si + 1].rb_start) si++;
+    const int si = SEG0 ? 0 : seg_of(a, rb);
     const GemvSeg& sg = a.seg[si];
     const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
 #pragma unroll
@@ -621,8 +632,16 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
     if constexpr (XM == 3) e_rt = route_pair(a, og, lane, wave);
     uint32_t c0[IT][GPL], c1[IT][GPL];
     bool valid[IT];
-    task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1, valid,
-                            e_rt);
+    if (XM != 3 && a.nseg == 1 && a.ids == nullptr && items == 1) {
+        // the common dense case: its first index load needs no segment lookup
+        // and no expert id, so it waits only for the plan fields
+        const int64_t g0 = (int64_t)col * GPL;
+        fetch_codes<S2, GPL, IT, true>(a, blockIdx.x, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng, 0, c0, c1,
+                                       valid);
+    } else {
+        task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1,
+                                valid, e_rt);
+    }
 
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
@@ -668,8 +687,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
             for (int it = 0; it < IT; it++)
 #pragma unroll
                 for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
-            int si = 0;
-            while (si + 1 < a.nseg && rb >= a.seg[si + 1].rb_start) si++;
+            const int si = seg_of(a, rb);
             const GemvSeg& sg = a.seg[si];
             const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
             if (col == 0) {
@@ -769,8 +787,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
 #pragma unroll
             for (int b = 0; b < BT; b++) acc[it][b] = group_sum(acc[it][b], lpr);
 
-        int si = 0;
-        while (si + 1 < a.nseg && rbg >= a.seg[si + 1].rb_start) si++;
+        const int si = seg_of(a, rbg);
         const GemvSeg& sg = a.seg[si];
         const int64_t row_base = (rbg - sg.rb_start) * rows_per_block;
         const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
