@@ -3,8 +3,9 @@
 // Streams 64M uint16 codes (non-temporal 16-byte loads) and, per code,
 // gathers one entry of a 1 MiB table -- the access pattern of a VQ GEMV at
 // batch 1 with the reference layout (a 65536 x 8 fp16 codebook) -- in several
-// load flavours, plus a 128 KiB LDS-resident table for comparison.  Prints
-// codes/s for each.  Every index is masked into its table.
+// load flavours (including gfx950's direct-to-LDS global_load_lds_dwordx4),
+// plus a 128 KiB LDS-resident table for comparison.  Prints codes/s for each.
+// Every index is masked into its table.
 // Build: make -C compressai_amd/csrc bench_gather
 #include <hip/hip_runtime.h>
 #include <stdio.h>
@@ -23,6 +24,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 template <int MODE>
 __global__ void __launch_bounds__(256) kgather(const uint16_t* __restrict__ codes, int64_t n, const u32x4* __restrict__ tab, uint32_t* out) {
   extern __shared__ u32x4 lds[];
+  __shared__ u32x4 lds_dma[MODE == 8 ? 4 * 8 * 64 : 1];  // per wave: 8 gathers x 64 lanes x 16 B
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if constexpr (MODE == 5) {
     for (int i = threadIdx.x; i < 8192; i += blockDim.x) lds[i] = tab[i];
     __syncthreads();
@@ -64,6 +67,18 @@ __global__ void __launch_bounds__(256) kgather(const uint16_t* __restrict__ code
       for (int q = 0; q < 8; q++) g[q] = lds[c[q] & 8191];
 #pragma unroll
       for (int q = 0; q < 8; q++) acc ^= g[q].x + g[q].y + g[q].z + g[q].w;
+    } else if constexpr (MODE == 8) {
+      // each lane's centroid lands in LDS at the wave's slot base + lane * 16
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(tab + c[q]),
+                                         (__attribute__((address_space(3))) void*)(lds_dma + (wave * 8 + q) * 64), 16, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const u32x4 g = lds_dma[(wave * 8 + q) * 64 + lane];
+        acc ^= g.x + g.y + g.z + g.w;
+      }
     } else if constexpr (MODE == 7) {
       const uint32_t* t1 = (const uint32_t*)tab;
       uint32_t g[8];
@@ -105,8 +120,8 @@ int main() {
   for (int bpc : {4, 8, 16}) {
     const int blocks = cu * bpc;
     CK(hipMalloc(&out, (size_t)blocks * 256 * 4));
-    const char* names[] = {"stream only", "gather b128 default", "gather b128 buffer aux=1(sc0)", "gather b128 buffer aux=2(sc1)", "gather b64 default", "gather LDS b128 (128KiB)", "gather b128 buffer aux=3", "gather b32 default"};
-    float t[8];
+    const char* names[] = {"stream only", "gather b128 default", "gather b128 buffer aux=1(sc0)", "gather b128 buffer aux=2(sc1)", "gather b64 default", "gather LDS b128 (128KiB)", "gather b128 buffer aux=3", "gather b32 default", "gather b128 direct to LDS"};
+    float t[9];
     t[0] = run<0>(codes, n, tab, out, blocks, 0);
     t[1] = run<1>(codes, n, tab, out, blocks, 0);
     t[2] = run<2>(codes, n, tab, out, blocks, 0);
@@ -115,7 +130,8 @@ int main() {
     t[5] = (maxlds >= 131072 && bpc <= 4) ? run<5>(codes, n, tab, out, cu, 131072) : -1.f;
     t[6] = run<6>(codes, n, tab, out, blocks, 0);
     t[7] = run<7>(codes, n, tab, out, blocks, 0);
-    for (int m = 0; m < 8; m++) {
+    t[8] = bpc <= 4 ? run<8>(codes, n, tab, out, blocks, 0) : -1.f;
+    for (int m = 0; m < 9; m++) {
       if (t[m] < 0) continue;
       printf("blocks/CU %2d  %-32s %8.3f ms  %7.1f G codes/s  %6.1f GB/s of codes  %.3f codes/clk/CU@2.4GHz\n", bpc, names[m], t[m],
              n / (t[m] * 1e-3) / 1e9, n * 2 / (t[m] * 1e-3) / 1e9, n / (t[m] * 1e-3) / (cu * 2.4e9));
