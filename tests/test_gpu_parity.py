@@ -349,6 +349,24 @@ def test_gemv_rht_fused_segments(dev, bpw, batch):
         assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
 
 
+@pytest.mark.parametrize("hb", [2, 8, 16, 32, 64, 512])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_gemv_rht_fused_small_blocks(dev, hb, batch):
+    """Fused RHT with blocks shorter than the in-register / cross-lane FWHT
+    stages (hb < 64 stops inside them) against RHT then GEMV."""
+    n, out = 512, 700
+    cb0 = synth.codebook(9150)
+    m = synth.vq_matrix(9150 + hb, out, n, bpw=2)
+    x = synth.activations(9154 + hb, (batch, n), dtype=torch.float16)
+    perm = synth.permutation(9156, n)
+    sign = synth.signs(9155, n)
+    (y,) = K.vq_gemv_rht(x.to(dev), [(m["idx0"].to(dev), None, m["scale"].to(dev), out)], cb0.to(dev), None, n,
+                         perm.to(dev), sign.to(dev), hb)
+    xr = O.rht(x, perm, sign, hb).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], None, cb0, None, m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
 def test_gemv_rht_fused_6144(dev):
     """down projection: 2048 x 6144 at 4 bpw with its 3 x 2048-block RHT fused."""
     n, out = 6144, 2048
