@@ -194,6 +194,10 @@ int gemv_launch(const GemvCall& c)
     a.wi = p.wi;
     a.nch = (int)((c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl));
     a.n_rowblocks = p.n_rowblocks;
+    // the kernel's packed scalar arguments
+    if (c.ng > 0x7FFFFFFF || p.n_rowblocks > 0x7FFFFFFF || c.seg[0].out_rows > 0x7FFFFFFF || a.nch > 0xFFFF ||
+        a.P > 0xFFFF || p.lpr > 63 || p.wi > 15 || p.wr > 15)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: shape outside the kernel's argument ranges");
     if (p.threads > gemv_max_threads(c.s2, c.cb_dt, c.xm) || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
     if (c.xm == 2 && (c.s2 == VQ2_S2_U16 || p.bt != 1))

@@ -487,14 +487,13 @@ __device__ __forceinline__ int seg_of(const GemvArgs& a, int64_t rb)
 }
 
 // Codes of row block rb for this lane (zeros and valid = false past the
-// end, for idle lanes and for rows beyond their segment).  SEG0: the launch
-// has one segment, read at a fixed offset (no dependent segment lookup).
-template <int S2, int GPL, int IT, bool SEG0 = false>
+// end, for idle lanes and for rows beyond their segment).
+template <int S2, int GPL, int IT>
 __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int rows_per_block, int wr, int wr_id,
                                             int rpw, int sub, int64_t g0, bool lane_ok, int64_t e,
                                             uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
 {
-    const int si = SEG0 ? 0 : seg_of(a, rb);
+    const int si = seg_of(a, rb);
     const GemvSeg& sg = a.seg[si];
     const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
 #pragma unroll
@@ -595,9 +594,17 @@ constexpr int gemv_max_threads(int s2, int cbt, int xm)
 }
 
 template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
-__global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(const GemvArgs a)
+// The plan fields the first index load needs come first as 9 dwords of
+// scalar kernel arguments: with -amdgpu-kernarg-preload-count the wave
+// starts with them in SGPRs (the preload covers 14 dwords).  k_plan packs
+// lpr (bits 0-5), wi (6-9), wr (10-13; waves along rows, so blockDim, an
+// implicit-argument load, is not on that path) and "fast" (bit 14: one
+// segment and no expert ids, so the first fetch uses k_idx0 / k_idx1 /
+// k_rows0 directly); k_nchp packs nch (bits 0-15) and P (16-31).
+__global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
+    vq_gemv_kernel(const int k_ng, const int k_nrb, const uint32_t k_plan, const uint32_t k_nchp,
+                   const int16_t* const k_idx0, const void* const k_idx1, const int k_rows0, const GemvArgs a)
 {
-    touch_kernargs(a);
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
     // 16-byte aligned: the activation block is written and read with 16-byte LDS accesses
@@ -607,22 +614,21 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
 
     const int og = blockIdx.y;
     const int bt0 = blockIdx.z * BT;
-    const int nb = min(BT, a.batch - bt0);
-    const int64_t n = a.ng * 8;
-    const int x_rows = XP == 2 ? a.P : (XP == 1 ? nb : 0);
+    const int k_P = (int)(k_nchp >> 16);
+    const int64_t n = (int64_t)k_ng * 8;
     float* s_x = s_dyn;
-    float* s_part = s_dyn + (XP == 0 ? 0 : (XP == 2 ? a.P : BT) * n);
+    float* s_part = s_dyn + (XP == 0 ? 0 : (XP == 2 ? k_P : BT) * n);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int lpr = a.lpr, wi = a.wi;
-    const int wr = (blockDim.x >> 6) / wi;
+    const int lpr = (int)(k_plan & 63u), wi = (int)((k_plan >> 6) & 15u);
+    const int wr = (int)((k_plan >> 10) & 15u);
     const int wi_id = wave % wi, wr_id = wave / wi;
     const int rpw = 64 / lpr;
     const int sub = lane / lpr, col = lane % lpr;
     const int64_t kc = (int64_t)lpr * GPL;
-    const int nch = a.nch;
-    const int items = a.P * nch;
+    const int nch = (int)(k_nchp & 0xFFFFu);
+    const int items = k_P * nch;
     const int rows_per_block = IT * rpw * wr;
 
     // the first task's index words do not depend on the activation: issue
@@ -632,16 +638,34 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM)) vq_gemv_kernel(
     if constexpr (XM == 3) e_rt = route_pair(a, og, lane, wave);
     uint32_t c0[IT][GPL], c1[IT][GPL];
     bool valid[IT];
-    if (XM != 3 && a.nseg == 1 && a.ids == nullptr && items == 1) {
-        // the common dense case: its first index load needs no segment lookup
-        // and no expert id, so it waits only for the plan fields
+    if (XM != 3 && ((k_plan >> 14) & 1u) && items == 1) {
+        // the common dense case: its first index load needs only the scalar
+        // arguments (no segment lookup, no expert id, no argument load)
         const int64_t g0 = (int64_t)col * GPL;
-        fetch_codes<S2, GPL, IT, true>(a, blockIdx.x, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng, 0, c0, c1,
-                                       valid);
+        const int64_t rb = blockIdx.x;
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int64_t row = rb * rows_per_block + (int64_t)(it * wr + wr_id) * rpw + sub;
+            valid[it] = rb < k_nrb && row < k_rows0 && g0 < k_ng;
+            const int64_t off = row * k_ng + g0;
+            if (valid[it]) {
+                load_codes16<GPL>(k_idx0, off, c0[it]);
+                if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)k_idx1, off, c1[it]);
+                if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)k_idx1, off, c1[it]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
+            }
+        }
+        touch_kernargs(a);  // the argument lines the rest of the kernel reads
     } else {
+        // the lookup chain below reads several argument lines: fetch them all first
+        touch_kernargs(a);
         task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1,
                                 valid, e_rt);
     }
+    const int nb = min(BT, a.batch - bt0);
+    const int x_rows = XP == 2 ? k_P : (XP == 1 ? nb : 0);
 
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
@@ -934,7 +958,12 @@ inline hipError_t launch_one(const GemvArgs& a, const GemvPlan& p, dim3 grid, si
     const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>;
     grid = persistent_grid(fn, p, grid, shm);
     if (p.grid_x_out) *p.grid_x_out = grid.x;
-    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>), grid, dim3(p.threads), shm, st, a);
+    // packed scalar arguments (ranges checked by gemv_launch)
+    const uint32_t fast = a.nseg == 1 && a.ids == nullptr ? 1u : 0u;
+    const uint32_t plan = (uint32_t)a.lpr | ((uint32_t)a.wi << 6) | ((uint32_t)p.wr << 10) | (fast << 14);
+    const uint32_t nchp = (uint32_t)a.nch | ((uint32_t)a.P << 16);
+    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>), grid, dim3(p.threads), shm, st, (int)a.ng,
+                       (int)a.n_rowblocks, plan, nchp, a.seg[0].idx0, a.seg[0].idx1, (int)a.seg[0].out_rows, a);
     return hipGetLastError();
 }
 
