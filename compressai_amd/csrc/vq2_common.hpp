@@ -182,10 +182,10 @@ __device__ __forceinline__ void touch_kernargs(const T& a)
     uint32_t h = 0;
 #pragma unroll
     for (int i = 0; i < (int)(sizeof(T) / 4); i += 16) h ^= w[i];
-    // keeps the loads; the store never happens in practice.  16 aligned bytes,
-    // so LDS arrays placed after it keep their 16-byte alignment.
-    __shared__ __align__(16) volatile uint32_t s_sink[4];
-    if (h == 0x9E3779B9u) s_sink[0] = h;
+    // an empty asm that takes the value keeps the loads.  (A never-taken
+    // store to a sink compiled to a flat store, after which the compiler's
+    // memory-counter waits fall back to waiting for every outstanding load.)
+    asm volatile("; kernarg lines touched %0" ::"s"(h));
 }
 
 }  // namespace vq2

@@ -214,16 +214,14 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
         const bool g_ok = gl < gcount;
         const bool w_ok = g_ok && row_ok;
         const int64_t off = rowc * a.ng + g_begin + (g_ok ? gl : 0);
-        uint32_t c0[8], c1[8];
-        load_codes16<8>(a.idx0, off, c0);
-        if constexpr (S2 == VQ2_S2_U16) load_codes16<8>((const int16_t*)a.idx1, off, c1);
-        if constexpr (S2 == VQ2_S2_U8) load_codes8<8>((const uint8_t*)a.idx1, off, c1);
+        Codes<S2, 8, 1> cd;
+        load_codes<S2, 8, 1>(a.idx0, a.idx1, off, 0, cd);
         half8_t b0[8], b1[8];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            b0[t] = centroid_h8<CBT>(a.cb0, c0[t]);
-            if constexpr (S2 == VQ2_S2_U16) b1[t] = centroid_h8<CBT>(a.cb1, c1[t]);
-            if constexpr (S2 == VQ2_S2_U8) b1[t] = s_c1[c1[t]];
+            b0[t] = centroid_h8<CBT>(a.cb0, cd.c0(0, t));
+            if constexpr (S2 == VQ2_S2_U16) b1[t] = centroid_h8<CBT>(a.cb1, cd.c1(0, t));
+            if constexpr (S2 == VQ2_S2_U8) b1[t] = s_c1[cd.c1(0, t)];
         }
 #pragma unroll
         for (int t = 0; t < 8; t++) {

@@ -152,42 +152,71 @@ __device__ __forceinline__ Centroid<CBT> lds_centroid(const u32x4* s_cb1, uint32
     return c;
 }
 
-// GPL uint16 codes (int16 storage) starting at element off; vector load.
+// Raw index words of one lane for IT rows of GPL groups, as loaded: uint16
+// codes (stage 1, and stage 2 of (16,16)) two per dword, uint8 codes (stage 2
+// of (16,8)) four per dword.  Codes are unpacked where the gathers use them:
+// unpacking right after the load would make the compiler wait for the
+// (HBM-latency) load there, and the next row block's index prefetch would
+// overlap nothing.
+template <int S2, int GPL, int IT>
+struct Codes {
+    static constexpr int W0 = (GPL + 1) / 2;
+    static constexpr int W1 = S2 == VQ2_S2_U8 ? (GPL + 3) / 4 : (S2 == VQ2_S2_U16 ? W0 : 1);
+    uint32_t w0[IT][W0];
+    uint32_t w1[IT][W1];
+    __device__ __forceinline__ uint32_t c0(int it, int q) const { return (w0[it][q >> 1] >> (16 * (q & 1))) & 0xFFFFu; }
+    __device__ __forceinline__ uint32_t c1(int it, int q) const
+    {
+        if constexpr (S2 == VQ2_S2_U8) return (w1[it][q >> 2] >> (8 * (q & 3))) & 0xFFu;
+        else return (w1[it][q >> 1] >> (16 * (q & 1))) & 0xFFFFu;
+    }
+};
+
+// GPL uint16 codes (int16 storage) starting at element off; one vector load.
 template <int GPL>
-__device__ __forceinline__ void load_codes16(const int16_t* p, int64_t off, uint32_t (&c)[GPL])
+__device__ __forceinline__ void load_raw16(const int16_t* p, int64_t off, uint32_t (&w)[(GPL + 1) / 2])
 {
     const int16_t* q = p + off;
     if constexpr (GPL == 8) {
         const u32x4 v = __builtin_nontemporal_load((const u32x4*)q);
 #pragma unroll
-        for (int i = 0; i < 4; i++) { c[2 * i] = v[i] & 0xFFFFu; c[2 * i + 1] = v[i] >> 16; }
+        for (int i = 0; i < 4; i++) w[i] = v[i];
     } else if constexpr (GPL == 4) {
         const u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
-        c[0] = v.x & 0xFFFFu; c[1] = v.x >> 16; c[2] = v.y & 0xFFFFu; c[3] = v.y >> 16;
+        w[0] = v.x;
+        w[1] = v.y;
     } else if constexpr (GPL == 2) {
-        const uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
-        c[0] = v & 0xFFFFu; c[1] = v >> 16;
+        w[0] = __builtin_nontemporal_load((const uint32_t*)q);
     } else {
-        c[0] = (uint32_t)(uint16_t)__builtin_nontemporal_load(q);
+        w[0] = (uint32_t)__builtin_nontemporal_load((const uint16_t*)q);
     }
 }
 
+// GPL uint8 codes starting at element off; one load.
 template <int GPL>
-__device__ __forceinline__ void load_codes8(const uint8_t* p, int64_t off, uint32_t (&c)[GPL])
+__device__ __forceinline__ void load_raw8(const uint8_t* p, int64_t off, uint32_t (&w)[(GPL + 3) / 4])
 {
     const uint8_t* q = p + off;
     if constexpr (GPL == 8) {
         const u32x2 v = __builtin_nontemporal_load((const u32x2*)q);
-#pragma unroll
-        for (int i = 0; i < 4; i++) { c[i] = (v.x >> (8 * i)) & 0xFFu; c[4 + i] = (v.y >> (8 * i)) & 0xFFu; }
+        w[0] = v.x;
+        w[1] = v.y;
     } else if constexpr (GPL == 4) {
-        const uint32_t v = __builtin_nontemporal_load((const uint32_t*)q);
-#pragma unroll
-        for (int i = 0; i < 4; i++) c[i] = (v >> (8 * i)) & 0xFFu;
+        w[0] = __builtin_nontemporal_load((const uint32_t*)q);
+    } else if constexpr (GPL == 2) {
+        w[0] = (uint32_t)__builtin_nontemporal_load((const uint16_t*)q);
     } else {
-#pragma unroll
-        for (int i = 0; i < GPL; i++) c[i] = q[i];
+        w[0] = (uint32_t)__builtin_nontemporal_load(q);
     }
+}
+
+// The index words of one lane for every plane of a row at element offset off.
+template <int S2, int GPL, int IT>
+__device__ __forceinline__ void load_codes(const int16_t* i0, const void* i1, int64_t off, int it, Codes<S2, GPL, IT>& cd)
+{
+    load_raw16<GPL>(i0, off, cd.w0[it]);
+    if constexpr (S2 == VQ2_S2_U8) load_raw8<GPL>((const uint8_t*)i1, off, cd.w1[it]);
+    if constexpr (S2 == VQ2_S2_U16) load_raw16<GPL>((const int16_t*)i1, off, cd.w1[it]);
 }
 
 // This lane's activation slice: groups [g0, g0+GPL) for nb batch columns,
@@ -242,6 +271,17 @@ __device__ __forceinline__ void load_x(const GemvArgs& a, const void* xb, int64_
         load_x_t<GPL, BT, VQ2_DT_BF16>(a, xb, g0, lane_ok, nb, xs);
 }
 
+// Element i of a wave-uniform read-only array, read through the scalar cache
+// (the constant address space).  Scalar loads count on their own counter, so
+// waiting for one does not wait for the vector loads issued before it (the
+// prologue's activation loads).  The arrays read this way (expert ids,
+// combine weights) are inputs the kernel never writes.
+template <typename T>
+__device__ __forceinline__ T uniform_load(const void* p, int64_t i)
+{
+    return ((const __attribute__((address_space(4))) T*)p)[i];
+}
+
 __device__ __forceinline__ int64_t pair_expert(const GemvArgs& a, int64_t pair, bool& bad, int64_t e_rt = -1)
 {
     if (e_rt >= 0) {
@@ -249,7 +289,7 @@ __device__ __forceinline__ int64_t pair_expert(const GemvArgs& a, int64_t pair, 
         return e_rt;
     }
     int64_t e = 0;
-    if (a.ids) e = a.ids_i64 ? ((const int64_t*)a.ids)[pair] : (int64_t)((const int32_t*)a.ids)[pair];
+    if (a.ids) e = a.ids_i64 ? uniform_load<int64_t>(a.ids, pair) : (int64_t)uniform_load<int32_t>(a.ids, pair);
     bad = a.ids && (e < 0 || e >= a.n_experts);
     return bad ? 0 : e;
 }
@@ -373,87 +413,133 @@ __device__ __forceinline__ void fwht_head(float (&v)[8], int L)
     }
 }
 
-template <int XT>
-__device__ __forceinline__ float ld_x(const void* p, int64_t i)
-{
-    if constexpr (XT == VQ2_DT_F32) return ((const float*)p)[i];
-    else if constexpr (XT == VQ2_DT_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
-    else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
-}
-
 // Prologue of XM 1 / 2: s_x[r * n + i] = sign[i] * f(row r)[perm[i]] for the
 // rows r of this workgroup (batch columns for XM 1, pairs for XM 2), then the
 // blockwise FWHT.  The RHT scale is applied when lanes read their slices.
-// Each thread takes 8 consecutive elements: perm and sign are read with
-// vector loads and all activation loads are issued before any is used.
-// n % 8 == 0; perm 16-byte and sign 8-byte aligned (checked on the host).
-template <int XM, int XT>
-__device__ __forceinline__ void build_x_t(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0)
+// Each thread takes 8 consecutive elements per iteration: perm and sign are
+// read with vector loads.  n % 8 == 0; perm 16-byte and sign 8-byte aligned
+// (checked on the host).
+//
+// An iteration is split into its loads (xpro_load: raw element bits, sign
+// bytes, bad-index mask) and its arithmetic (xpro_finish).  The kernel issues
+// the first iteration's loads before its first index load: loads complete in
+// issue order, so the RHT arithmetic then waits only for these L2-resident
+// values, not for the index words coming from HBM.
+struct XProLoad {
+    uint32_t g[8];  // raw activation bits (gate half for XM 2)
+    uint32_t u[8];  // raw up-half bits (XM 2)
+    u32x2 sv;       // 8 sign bytes
+    bool bad[8];    // permutation entry outside [0, n): the value is poisoned
+};
+
+template <int XT>
+__device__ __forceinline__ float raw_to_f32(uint32_t r)
 {
-    const int64_t total = (int64_t)nrows * n;
-    for (int64_t t0 = (int64_t)threadIdx.x * 8; t0 < total; t0 += (int64_t)blockDim.x * 8) {
-        const int r = (int)(t0 / n);
-        const int64_t i0 = t0 - (int64_t)r * n;
-        int64_t src[8];
-        if (a.perm) {
-            const u32x4 p0 = *(const u32x4*)(a.perm + i0);
-            const u32x4 p1 = *(const u32x4*)(a.perm + i0 + 4);
+    if constexpr (XT == VQ2_DT_F32) return __uint_as_float(r);
+    else if constexpr (XT == VQ2_DT_F16) return f16_bits_to_f32((uint16_t)r);
+    else return bf16_bits_to_f32(r);
+}
+
+// +1 signs for a rotation without a sign table: the prologue then loads its
+// sign bytes from here (a select of pointers, no branch around the load).
+constexpr int VQ2_ONES = 8192;
+struct OnesTable {
+    int8_t v[VQ2_ONES];
+    constexpr OnesTable() : v() { for (int i = 0; i < VQ2_ONES; i++) v[i] = 1; }
+};
+static __device__ const OnesTable g_sign_ones = OnesTable();
+
+// Loads of the iteration starting at element t0 of the nrows x n block
+// (t0 < total; callers clamp idle threads to t0 = 0).  No loaded value is
+// used here, and no load sits inside a branch of its own (activation dtype
+// XT is a template value, a missing sign table reads g_sign_ones): a loaded
+// value merged from branches is waited for at the merge.
+template <int XM, int XT>
+__device__ __forceinline__ void xpro_load(const GemvArgs& a, int64_t t0, int64_t n, int og, int bt0, XProLoad& L)
+{
+    const int r = (int)(t0 / n);
+    const int64_t i0 = t0 - (int64_t)r * n;
+    int64_t src[8];
+    if (a.perm) {
+        const u32x4 p0 = *(const u32x4*)(a.perm + i0);
+        const u32x4 p1 = *(const u32x4*)(a.perm + i0 + 4);
 #pragma unroll
-            for (int k = 0; k < 4; k++) { src[k] = (int32_t)p0[k]; src[4 + k] = (int32_t)p1[k]; }
-        } else {
+        for (int k = 0; k < 4; k++) { src[k] = (int32_t)p0[k]; src[4 + k] = (int32_t)p1[k]; }
+    } else {
 #pragma unroll
-            for (int k = 0; k < 8; k++) src[k] = i0 + k;
-        }
-        bool bad[8];
+        for (int k = 0; k < 8; k++) src[k] = i0 + k;
+    }
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            bad[k] = (uint64_t)src[k] >= (uint64_t)n;  // not a permutation of [0, n): poison the value
-            src[k] = bad[k] ? 0 : src[k];
-        }
-        float sg[8];
-        if (a.sign) {
-            const u32x2 sv = *(const u32x2*)(a.sign + i0);
+    for (int k = 0; k < 8; k++) {
+        L.bad[k] = (uint64_t)src[k] >= (uint64_t)n;  // not a permutation of [0, n): poison the value
+        src[k] = L.bad[k] ? 0 : src[k];
+    }
+    // both tables are global memory; said explicitly, or the selected pointer
+    // is generic and the load becomes a flat load, which the compiler's
+    // memory-counter waits cannot order against the global loads
+    const int8_t* sgn = a.sign ? a.sign + i0 : g_sign_ones.v + (i0 & (VQ2_ONES - 1));
+    L.sv = *(const __attribute__((address_space(1))) u32x2*)sgn;
+    int64_t row;
+    if constexpr (XM == 1) row = (int64_t)(og / a.x_pdiv) * a.x_pstride + (int64_t)(bt0 + r) * a.x_bstride;
+    else row = ((int64_t)og * a.P + r) / a.x_pdiv * a.x_pstride;
+    if constexpr (XT == VQ2_DT_F32) {
+        const uint32_t* x = (const uint32_t*)a.x + row;
 #pragma unroll
-            for (int k = 0; k < 8; k++) sg[k] = (float)(int8_t)((sv[k >> 2] >> (8 * (k & 3))) & 0xFFu);
-        } else {
+        for (int k = 0; k < 8; k++) L.g[k] = x[src[k]];
+        if constexpr (XM == 2)
 #pragma unroll
-            for (int k = 0; k < 8; k++) sg[k] = 1.0f;
-        }
-        float v[8];
-        if constexpr (XM == 1) {
-            const int64_t row = (int64_t)(og / a.x_pdiv) * a.x_pstride + (int64_t)(bt0 + r) * a.x_bstride;
+            for (int k = 0; k < 8; k++) L.u[k] = x[n + src[k]];
+    } else {
+        const uint16_t* x = (const uint16_t*)a.x + row;
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = ld_x<XT>(a.x, row + src[k]);
-        } else {
-            const int64_t row = ((int64_t)og * a.P + r) / a.x_pdiv * a.x_pstride;
-            float g[8], u[8];
+        for (int k = 0; k < 8; k++) L.g[k] = x[src[k]];
+        if constexpr (XM == 2)
 #pragma unroll
-            for (int k = 0; k < 8; k++) { g[k] = ld_x<XT>(a.x, row + src[k]); u[k] = ld_x<XT>(a.x, row + n + src[k]); }
-#pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = silu_f32(g[k]) * u[k];
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = bad[k] ? __builtin_nanf("") : v[k] * sg[k];
-        fwht_head(v, a.hb_log2);
-        u32x4 o0, o1;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            o0[k] = __float_as_uint(v[k]);
-            o1[k] = __float_as_uint(v[4 + k]);
-        }
-        *(u32x4*)(s_x + t0) = o0;
-        *(u32x4*)(s_x + t0 + 4) = o1;
+            for (int k = 0; k < 8; k++) L.u[k] = x[n + src[k]];
     }
 }
 
-template <int XM>
-__device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0)
+// Arithmetic of one iteration: activation (silu(gate) * up for XM 2), sign,
+// FWHT bits 0-5 (fwht_head), 16-byte LDS stores.
+template <int XM, int XT>
+__device__ __forceinline__ void xpro_finish(const GemvArgs& a, float* s_x, int64_t t0, const XProLoad& L)
 {
-    if (a.x_dt == VQ2_DT_F32) build_x_t<XM, VQ2_DT_F32>(a, s_x, nrows, n, og, bt0);
-    else if (a.x_dt == VQ2_DT_F16) build_x_t<XM, VQ2_DT_F16>(a, s_x, nrows, n, og, bt0);
-    else build_x_t<XM, VQ2_DT_BF16>(a, s_x, nrows, n, og, bt0);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float g = raw_to_f32<XT>(L.g[k]);
+        if constexpr (XM == 2) v[k] = silu_f32(g) * raw_to_f32<XT>(L.u[k]);
+        else v[k] = g;
+        const float sg = (float)(int8_t)((L.sv[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+        v[k] = L.bad[k] ? __builtin_nanf("") : v[k] * sg;
+    }
+    fwht_head(v, a.hb_log2);
+    u32x4 o0, o1;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        o0[k] = __float_as_uint(v[k]);
+        o1[k] = __float_as_uint(v[4 + k]);
+    }
+    *(u32x4*)(s_x + t0) = o0;
+    *(u32x4*)(s_x + t0 + 4) = o1;
+}
+
+// The whole prologue, given the first iteration's loads (issued by the
+// caller at t0 = threadIdx.x * 8, clamped to 0 past the block).
+template <int XM, int XT>
+__device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0,
+                                        const XProLoad& first)
+{
+    const int64_t total = (int64_t)nrows * n;
+    int64_t t0 = (int64_t)threadIdx.x * 8;
+    if (t0 < total) xpro_finish<XM, XT>(a, s_x, t0, first);
+    for (t0 += (int64_t)blockDim.x * 8; t0 < total; t0 += (int64_t)blockDim.x * 8) {
+        XProLoad L;
+        xpro_load<XM, XT>(a, t0, n, og, bt0, L);
+        xpro_finish<XM, XT>(a, s_x, t0, L);
+    }
     __syncthreads();
-    block_fwht(s_x, (int64_t)nrows * n, a.hb_log2, 6);  // bits 0-5 done by fwht_head
+    block_fwht(s_x, total, a.hb_log2, 6);  // bits 0-5 done by fwht_head
 }
 
 // A lane's activation slice from the LDS activation block.
@@ -486,51 +572,61 @@ __device__ __forceinline__ int seg_of(const GemvArgs& a, int64_t rb)
     return si;
 }
 
-// Codes of row block rb for this lane (zeros and valid = false past the
-// end, for idle lanes and for rows beyond their segment).
-template <int S2, int GPL, int IT>
+// Index words of row block rb for this lane; valid = false past the end,
+// for idle lanes and for rows beyond their segment.  Past the last row block
+// (uniform over the workgroup) nothing is loaded; inside it the loads do not
+// depend on the lane: an invalid row reads its plane's first word (every
+// segment has at least one row), whose codes index the codebooks in bounds,
+// and its partial is zeroed after the dot product.  IN_RANGE: the caller
+// knows rb < n_rowblocks (a workgroup's first row block: the persistent grid
+// never exceeds the row-block count), so no branch is needed around the
+// loads -- where a path with loads and one without merge, the compiler waits
+// for every outstanding load at the next use of an earlier one.
+template <int S2, int GPL, int IT, bool IN_RANGE = false>
 __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int rows_per_block, int wr, int wr_id,
                                             int rpw, int sub, int64_t g0, bool lane_ok, int64_t e,
-                                            uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT])
+                                            Codes<S2, GPL, IT>& cd, bool (&valid)[IT])
 {
     const int si = seg_of(a, rb);
     const GemvSeg& sg = a.seg[si];
     const int64_t row_base = (rb - sg.rb_start) * rows_per_block;
+    const bool in_range = IN_RANGE || rb < a.n_rowblocks;
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-        valid[it] = rb < a.n_rowblocks && row < sg.out_rows && lane_ok;
-        const int64_t off = row * a.ng + g0;
-        if (valid[it]) {
-            load_codes16<GPL>(sg.idx0 + e * a.e_istride, off, c0[it]);
-            if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
-            if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)sg.idx1 + e * a.e_istride, off, c1[it]);
-        } else {
+        valid[it] = in_range && row < sg.out_rows && lane_ok;
+    }
+    if (!in_range) return;
 #pragma unroll
-            for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
-        }
+    for (int it = 0; it < IT; it++) {
+        const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+        const int64_t off = valid[it] ? row * a.ng + g0 : 0;
+        load_codes<S2, GPL, IT>(sg.idx0 + e * a.e_istride,
+                                S2 == VQ2_S2_U8 ? (const void*)((const uint8_t*)sg.idx1 + e * a.e_istride)
+                                                : (const void*)((const int16_t*)sg.idx1 + e * a.e_istride),
+                                off, it, cd);
     }
 }
 
 // Codes of task (row block rb, item) for this lane: item = pair * nch + chunk.
-template <int S2, int GPL, int IT>
+template <int S2, int GPL, int IT, bool IN_RANGE = false>
 __device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int item, int nch, int64_t kc, int og,
                                            int rows_per_block, int wr, int wr_id, int rpw, int sub, int col,
-                                           uint32_t (&c0)[IT][GPL], uint32_t (&c1)[IT][GPL], bool (&valid)[IT],
-                                           int64_t e_rt)
+                                           Codes<S2, GPL, IT>& cd, bool (&valid)[IT], int64_t e_rt)
 {
     const int pj = item / nch, c = item - (item / nch) * nch;
     bool bad;
     const int64_t e = pair_expert(a, (int64_t)og * a.P + pj, bad, e_rt);
     const int64_t g0 = c * kc + (int64_t)col * GPL;
-    fetch_codes<S2, GPL, IT>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, c0, c1, valid);
+    fetch_codes<S2, GPL, IT, IN_RANGE>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, cd,
+                                       valid);
 }
 
 // acc[it][b] = sum over this lane's GPL groups of VQ(W)[row_it] . x_b
 template <int CBT, int S2, int GPL, int BT, int IT>
-__device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const uint32_t (&c0)[IT][GPL],
-                                          const uint32_t (&c1)[IT][GPL], const bool (&valid)[IT],
-                                          const float (&xs)[BT][GPL * 8], float (&acc)[IT][BT])
+__device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const Codes<S2, GPL, IT>& cd,
+                                          const bool (&valid)[IT], const float (&xs)[BT][GPL * 8],
+                                          float (&acc)[IT][BT])
 {
 #pragma unroll
     for (int it = 0; it < IT; it++) {
@@ -538,11 +634,11 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
         for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
         Centroid<CBT> cen[GPL];
 #pragma unroll
-        for (int q = 0; q < GPL; q++) cen[q].load(a.cb0, c0[it][q]);
+        for (int q = 0; q < GPL; q++) cen[q].load(a.cb0, cd.c0(it, q));
         if constexpr (S2 == VQ2_S2_U16) {
             Centroid<CBT> cen1[GPL];
 #pragma unroll
-            for (int q = 0; q < GPL; q++) cen1[q].load(a.cb1, c1[it][q]);
+            for (int q = 0; q < GPL; q++) cen1[q].load(a.cb1, cd.c1(it, q));
 #pragma unroll
             for (int q = 0; q < GPL; q++)
 #pragma unroll
@@ -554,7 +650,7 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
         } else if constexpr (S2 == VQ2_S2_U8) {
 #pragma unroll
             for (int q = 0; q < GPL; q++) {
-                const Centroid<CBT> c2 = lds_centroid<CBT>(s_cb1, c1[it][q]);
+                const Centroid<CBT> c2 = lds_centroid<CBT>(s_cb1, cd.c1(it, q));
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float w = cen[q].get(j) + c2.get(j);
@@ -593,7 +689,8 @@ constexpr int gemv_max_threads(int s2, int cbt, int xm)
     return xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512);
 }
 
-template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
+// XT: activation dtype of the prologue kernels (XM != 0); unused for XM 0.
+template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0, int XT = VQ2_DT_F32>
 // The plan fields the first index load needs come first as 9 dwords of
 // scalar kernel arguments: with -amdgpu-kernarg-preload-count the wave
 // starts with them in SGPRs (the preload covers 14 dwords).  k_plan packs
@@ -620,7 +717,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     float* s_part = s_dyn + (XP == 0 ? 0 : (XP == 2 ? k_P : BT) * n);
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (an SGPR value), so per-wave work items, expert ids and
+    // their loads stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lpr = (int)(k_plan & 63u), wi = (int)((k_plan >> 6) & 15u);
     const int wr = (int)((k_plan >> 10) & 15u);
     const int wi_id = wave % wi, wr_id = wave / wi;
@@ -631,47 +730,55 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     const int items = k_P * nch;
     const int rows_per_block = IT * rpw * wr;
 
-    // the first task's index words do not depend on the activation: issue
-    // their loads before the prologue so the HBM latency overlaps it
-    // fused router: this group's expert, before its first index words
+    // Load order: the prologue's first activation loads (L2-resident), then
+    // the first task's index words (HBM).  The index latency overlaps the
+    // prologue, whose arithmetic waits only for its own loads.
+    XProLoad xpl;
+    int x_rows = 0;
+    if constexpr (XP != 0) {
+        x_rows = XP == 2 ? k_P : min(BT, a.batch - bt0);
+        const int64_t t0 = (int64_t)threadIdx.x * 8;
+        xpro_load<XP, XT>(a, t0 < (int64_t)x_rows * n ? t0 : 0, n, og, bt0, xpl);
+    }
+    // fused router: this group's expert, before its first index words.  The
+    // router reads a chain of argument fields (pairs, k, experts, logits):
+    // the argument lines are fetched first so every link hits.
     int64_t e_rt = -1;
-    if constexpr (XM == 3) e_rt = route_pair(a, og, lane, wave);
-    uint32_t c0[IT][GPL], c1[IT][GPL];
+    if constexpr (XM == 3) {
+        touch_kernargs(a);
+        e_rt = route_pair(a, og, lane, wave);
+    }
+    Codes<S2, GPL, IT> cd;
     bool valid[IT];
-    if (XM != 3 && ((k_plan >> 14) & 1u) && items == 1) {
-        // the common dense case: its first index load needs only the scalar
-        // arguments (no segment lookup, no expert id, no argument load)
+    if (XP == 0 && ((k_plan >> 14) & 1u) && items == 1) {
+        // the common pre-rotated dense case: its first index load needs only
+        // the scalar arguments (no segment lookup, no expert id, no argument
+        // load).  Prologue kernels take the general path below: their
+        // activation loads already wait for the argument lines, and a single
+        // path lets the compiler count the loads after them exactly (where two
+        // paths with different loads merge, it waits for all of them).
         const int64_t g0 = (int64_t)col * GPL;
         const int64_t rb = blockIdx.x;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int64_t row = rb * rows_per_block + (int64_t)(it * wr + wr_id) * rpw + sub;
             valid[it] = rb < k_nrb && row < k_rows0 && g0 < k_ng;
-            const int64_t off = row * k_ng + g0;
-            if (valid[it]) {
-                load_codes16<GPL>(k_idx0, off, c0[it]);
-                if constexpr (S2 == VQ2_S2_U8) load_codes8<GPL>((const uint8_t*)k_idx1, off, c1[it]);
-                if constexpr (S2 == VQ2_S2_U16) load_codes16<GPL>((const int16_t*)k_idx1, off, c1[it]);
-            } else {
-#pragma unroll
-                for (int q = 0; q < GPL; q++) { c0[it][q] = 0; c1[it][q] = 0; }
-            }
+            load_codes<S2, GPL, IT>(k_idx0, k_idx1, valid[it] ? row * k_ng + g0 : 0, it, cd);
         }
         touch_kernargs(a);  // the argument lines the rest of the kernel reads
     } else {
         // the lookup chain below reads several argument lines: fetch them all first
         touch_kernargs(a);
-        task_codes<S2, GPL, IT>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, c0, c1,
-                                valid, e_rt);
+        task_codes<S2, GPL, IT, true>(a, blockIdx.x, wi_id, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col,
+                                      cd, valid, e_rt);
     }
     const int nb = min(BT, a.batch - bt0);
-    const int x_rows = XP == 2 ? k_P : (XP == 1 ? nb : 0);
 
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
         for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
     }
-    if constexpr (XP != 0) build_x<XP>(a, s_x, x_rows, n, og, bt0);
+    if constexpr (XP != 0) build_x<XP, XT>(a, s_x, x_rows, n, og, bt0, xpl);
     if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
 
     float xs[BT][GPL * 8];
@@ -701,12 +808,11 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         for (int b = 0; b < BT; b++) bkey[b] = 0;
         while (rb < a.n_rowblocks) {
             const int64_t rbn = rb + gridDim.x;
-            uint32_t n0[IT][GPL], n1[IT][GPL];
+            Codes<S2, GPL, IT> nx;
             bool nvalid[IT];
-            fetch_codes<S2, GPL, IT>(a, rbn, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, n0, n1,
-                                     nvalid);
+            fetch_codes<S2, GPL, IT>(a, rbn, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, nx, nvalid);
             float acc[IT][BT];
-            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
+            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -735,11 +841,8 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
                 }
             }
 #pragma unroll
-            for (int it = 0; it < IT; it++) {
-                valid[it] = nvalid[it];
-#pragma unroll
-                for (int q = 0; q < GPL; q++) { c0[it][q] = n0[it][q]; c1[it][q] = n1[it][q]; }
-            }
+            for (int it = 0; it < IT; it++) valid[it] = nvalid[it];
+            cd = nx;
             rb = rbn;
         }
         if constexpr (EP == 1) {
@@ -782,9 +885,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             nitem = wi_id;
             nrbg = rbg + gridDim.x;
         }
-        uint32_t n0[IT][GPL], n1[IT][GPL];
+        Codes<S2, GPL, IT> nx;
         bool nvalid[IT];
-        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, n0, n1, nvalid,
+        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, nx, nvalid,
                                 e_rt);
 
         const int pj = item / nch, c = item - (item / nch) * nch;
@@ -805,7 +908,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             cur_item = item;
         }
         float acc[IT][BT];
-        block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, c0, c1, valid, xs, acc);
+        block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
 #pragma unroll
         for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -814,7 +917,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         const int si = seg_of(a, rbg);
         const GemvSeg& sg = a.seg[si];
         const int64_t row_base = (rbg - sg.rb_start) * rows_per_block;
-        const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
+        const float pw = a.pair_w ? uniform_load<float>(a.pair_w, pair) : 1.0f;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
@@ -876,11 +979,8 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
                 for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
         }
 #pragma unroll
-        for (int it = 0; it < IT; it++) {
-            valid[it] = nvalid[it];
-#pragma unroll
-            for (int q = 0; q < GPL; q++) { c0[it][q] = n0[it][q]; c1[it][q] = n1[it][q]; }
-        }
+        for (int it = 0; it < IT; it++) valid[it] = nvalid[it];
+        cd = nx;
         item = nitem;
         rbg = nrbg;
     }
@@ -921,7 +1021,7 @@ __global__ void __launch_bounds__(256) vq_gemv_generic(const GemvArgs a, int s2,
             const float s = load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row);
             float v = (acc * s) * a.rs;
             if (bad) v = __builtin_nanf("");
-            const float pw = a.pair_w ? a.pair_w[pair] : 1.0f;
+            const float pw = a.pair_w ? uniform_load<float>(a.pair_w, pair) : 1.0f;
             out = (a.P == 1) ? v : fmaf(pw, v, out);
         }
         store_from_f32(sg.y, a.y_dt, og * a.y_ostride + b * sg.y_bstride + row, out);
@@ -941,30 +1041,44 @@ struct GemvPlan {
 // Resident workgroups per CU of a kernel at a block size / LDS size (cached).
 int resident_blocks_per_cu(const void* fn, int threads, size_t shm);
 
-// Persistent grid: as many row-block workers as stay resident on the GPU.
+// Persistent grid: as many row-block workers as stay resident on the GPU
+// (rounded down over the grid.y * grid.z output groups: a workgroup beyond
+// the resident count would start only when another ends, a whole row block
+// late).
 inline dim3 persistent_grid(const void* fn, const GemvPlan& p, dim3 grid, size_t shm)
 {
     const int64_t resident = (int64_t)resident_blocks_per_cu(fn, p.threads, shm) * p.num_cu * p.occ_scale;
-    const int64_t per_x = (resident + (int64_t)grid.y * grid.z - 1) / ((int64_t)grid.y * grid.z);
+    const int64_t per_x = resident / ((int64_t)grid.y * grid.z);
     int64_t gx = per_x < 1 ? 1 : per_x;
     if (gx > p.n_rowblocks) gx = p.n_rowblocks;
     grid.x = (unsigned)gx;
     return grid;
 }
 
-template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0>
+template <int CBT, int S2, int GPL, int BT, int IT, int XM, int EP = 0, int XT = VQ2_DT_F32>
 inline hipError_t launch_one(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
 {
-    const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>;
+    const void* fn = (const void*)vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP, XT>;
     grid = persistent_grid(fn, p, grid, shm);
     if (p.grid_x_out) *p.grid_x_out = grid.x;
     // packed scalar arguments (ranges checked by gemv_launch)
     const uint32_t fast = a.nseg == 1 && a.ids == nullptr ? 1u : 0u;
     const uint32_t plan = (uint32_t)a.lpr | ((uint32_t)a.wi << 6) | ((uint32_t)p.wr << 10) | (fast << 14);
     const uint32_t nchp = (uint32_t)a.nch | ((uint32_t)a.P << 16);
-    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP>), grid, dim3(p.threads), shm, st, (int)a.ng,
+    hipLaunchKernelGGL((vq_gemv_kernel<CBT, S2, GPL, BT, IT, XM, EP, XT>), grid, dim3(p.threads), shm, st, (int)a.ng,
                        (int)a.n_rowblocks, plan, nchp, a.seg[0].idx0, a.seg[0].idx1, (int)a.seg[0].out_rows, a);
     return hipGetLastError();
+}
+
+// prologue kernels, one instantiation per activation dtype
+template <int CBT, int S2, int GPL, int BT, int IT, int XM>
+inline hipError_t launch_xt(const GemvArgs& a, const GemvPlan& p, dim3 grid, size_t shm, hipStream_t st)
+{
+    switch (a.x_dt) {
+    case VQ2_DT_F16: return launch_one<CBT, S2, GPL, BT, IT, XM, 0, VQ2_DT_F16>(a, p, grid, shm, st);
+    case VQ2_DT_BF16: return launch_one<CBT, S2, GPL, BT, IT, XM, 0, VQ2_DT_BF16>(a, p, grid, shm, st);
+    default: return launch_one<CBT, S2, GPL, BT, IT, XM, 0, VQ2_DT_F32>(a, p, grid, shm, st);
+    }
 }
 
 template <int CBT, int S2, int GPL, int BT, int IT>
@@ -972,13 +1086,13 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
 {
     switch (p.xm) {
     case 1:
-        if constexpr (BT <= 2) return launch_one<CBT, S2, GPL, BT, IT, 1>(a, p, grid, shm, st);
+        if constexpr (BT <= 2) return launch_xt<CBT, S2, GPL, BT, IT, 1>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     case 2:
-        if constexpr (S2 != VQ2_S2_U16 && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
+        if constexpr (S2 != VQ2_S2_U16 && BT == 1) return launch_xt<CBT, S2, GPL, BT, IT, 2>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     case 3:
-        if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_one<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);
+        if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_xt<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     default:
         if (p.ep == 1) {
