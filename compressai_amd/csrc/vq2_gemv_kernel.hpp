@@ -27,6 +27,8 @@
 // Shapes whose index rows or activations cannot be read with vector loads
 // (n/8 not a multiple of GPL, misaligned planes or rows) take vq_gemv_generic.
 #pragma once
+#include <type_traits>
+
 #include "vq2_common.hpp"
 #include "vq2_internal.hpp"
 #include "vq2_router.hpp"
@@ -622,28 +624,44 @@ __device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int it
                                        valid);
 }
 
-// acc[it][b] = sum over this lane's GPL groups of VQ(W)[row_it] . x_b
+// The centroids of one row block for this lane (global gathers; the (16,8)
+// stage-2 centroids come from LDS inside dot_block).
+template <int CBT, int S2, int GPL, int IT>
+struct Cens {
+    Centroid<CBT> c0[IT][GPL];
+    Centroid<CBT> c1[IT][S2 == VQ2_S2_U16 ? GPL : 1];
+};
+
+template <int CBT, int S2, int GPL, int IT>
+__device__ __forceinline__ void gather_block(const GemvArgs& a, const Codes<S2, GPL, IT>& cd, Cens<CBT, S2, GPL, IT>& ce)
+{
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+#pragma unroll
+        for (int q = 0; q < GPL; q++) ce.c0[it][q].load(a.cb0, cd.c0(it, q));
+        if constexpr (S2 == VQ2_S2_U16)
+#pragma unroll
+            for (int q = 0; q < GPL; q++) ce.c1[it][q].load(a.cb1, cd.c1(it, q));
+    }
+}
+
+// acc[it][b] = sum over this lane's GPL groups of VQ(W)[row_it] . x_b, from
+// gathered centroids
 template <int CBT, int S2, int GPL, int BT, int IT>
-__device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const Codes<S2, GPL, IT>& cd,
-                                          const bool (&valid)[IT], const float (&xs)[BT][GPL * 8],
-                                          float (&acc)[IT][BT])
+__device__ __forceinline__ void dot_block(const u32x4* s_cb1, const Codes<S2, GPL, IT>& cd,
+                                          const Cens<CBT, S2, GPL, IT>& ce, const bool (&valid)[IT],
+                                          const float (&xs)[BT][GPL * 8], float (&acc)[IT][BT])
 {
 #pragma unroll
     for (int it = 0; it < IT; it++) {
 #pragma unroll
         for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
-        Centroid<CBT> cen[GPL];
-#pragma unroll
-        for (int q = 0; q < GPL; q++) cen[q].load(a.cb0, cd.c0(it, q));
         if constexpr (S2 == VQ2_S2_U16) {
-            Centroid<CBT> cen1[GPL];
-#pragma unroll
-            for (int q = 0; q < GPL; q++) cen1[q].load(a.cb1, cd.c1(it, q));
 #pragma unroll
             for (int q = 0; q < GPL; q++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float w = cen[q].get(j) + cen1[q].get(j);
+                    const float w = ce.c0[it][q].get(j) + ce.c1[it][q].get(j);
 #pragma unroll
                     for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
                 }
@@ -653,7 +671,7 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
                 const Centroid<CBT> c2 = lds_centroid<CBT>(s_cb1, cd.c1(it, q));
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float w = cen[q].get(j) + c2.get(j);
+                    const float w = ce.c0[it][q].get(j) + c2.get(j);
 #pragma unroll
                     for (int b = 0; b < BT; b++) acc[it][b] = fmaf(w, xs[b][q * 8 + j], acc[it][b]);
                 }
@@ -664,14 +682,23 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 #pragma unroll
                 for (int j = 0; j < 8; j++)
 #pragma unroll
-                    for (int b = 0; b < BT; b++) acc[it][b] = fmaf(cen[q].get(j), xs[b][q * 8 + j], acc[it][b]);
+                    for (int b = 0; b < BT; b++) acc[it][b] = fmaf(ce.c0[it][q].get(j), xs[b][q * 8 + j], acc[it][b]);
         }
         if (!valid[it]) {
 #pragma unroll
             for (int b = 0; b < BT; b++) acc[it][b] = 0.0f;
         }
     }
+}
 
+template <int CBT, int S2, int GPL, int BT, int IT>
+__device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1, const Codes<S2, GPL, IT>& cd,
+                                          const bool (&valid)[IT], const float (&xs)[BT][GPL * 8],
+                                          float (&acc)[IT][BT])
+{
+    Cens<CBT, S2, GPL, IT> ce;
+    gather_block<CBT, S2, GPL, IT>(a, cd, ce);
+    dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce, valid, xs, acc);
 }
 
 // EP 0: store y; EP 1 (pre-rotated x, one item per wave): no y -- every
@@ -774,6 +801,16 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     }
     const int nb = min(BT, a.batch - bt0);
 
+    // Prologue kernels: the first task's gathers are issued as soon as its
+    // index words arrive, before the prologue's arithmetic.  The prologue's
+    // first iteration loads nothing more (its loads went out before the index
+    // words), so its barriers and LDS passes run while the gathers are in
+    // flight.  Unconditional: a branch around them would leave the compiler
+    // unsure which loads are outstanding, and it would then wait for the
+    // gathers inside the prologue.
+    Cens<CBT, S2, GPL, IT> ce0;
+    if constexpr (XP != 0) gather_block<CBT, S2, GPL, IT>(a, cd, ce0);
+
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
         for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
@@ -806,13 +843,15 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         uint64_t bkey[BT];
 #pragma unroll
         for (int b = 0; b < BT; b++) bkey[b] = 0;
-        while (rb < a.n_rowblocks) {
+        // one row block; PRE: its centroids were gathered before the prologue
+        auto step = [&](auto pre) {
             const int64_t rbn = rb + gridDim.x;
             Codes<S2, GPL, IT> nx;
             bool nvalid[IT];
             fetch_codes<S2, GPL, IT>(a, rbn, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, nx, nvalid);
             float acc[IT][BT];
-            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+            if constexpr (decltype(pre)::value) dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
+            else block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -844,7 +883,11 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             for (int it = 0; it < IT; it++) valid[it] = nvalid[it];
             cd = nx;
             rb = rbn;
-        }
+        };
+        // prologue kernels pre-gathered the first block (rb < n_rowblocks:
+        // the persistent grid never exceeds the row-block count)
+        if constexpr (XP != 0) step(std::true_type{});
+        while (rb < a.n_rowblocks) step(std::false_type{});
         if constexpr (EP == 1) {
             // best key of the workgroup per batch column: wave, then waves
             __shared__ uint64_t s_key[4][BT];
@@ -878,7 +921,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     for (int it = 0; it < IT; it++)
 #pragma unroll
         for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
-    while (rbg < a.n_rowblocks) {
+    // one task; PRE: the first task, whose centroids were gathered before the
+    // prologue (rbg < n_rowblocks and item < items hold for it)
+    auto mstep = [&](auto pre) {
         int nitem = item + wi;
         int64_t nrbg = rbg;
         if (nitem >= items) {
@@ -908,7 +953,8 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             cur_item = item;
         }
         float acc[IT][BT];
-        block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+        if constexpr (decltype(pre)::value) dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
+        else block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
 #pragma unroll
         for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -983,7 +1029,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         cd = nx;
         item = nitem;
         rbg = nrbg;
-    }
+    };
+    if constexpr (XP != 0) mstep(std::true_type{});
+    while (rbg < a.n_rowblocks) mstep(std::false_type{});
 }
 
 // Generic path for shapes the vector kernel does not take (activations are
