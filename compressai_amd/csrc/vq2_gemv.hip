@@ -64,6 +64,22 @@ static GemvPlan plan_gemv(const GemvCall& c, int num_cu)
         p.wi = wi_max <= 4 ? 4 : (int)((items + rounds - 1) / rounds);
         p.wr = 1;
     }
+    // RHT prologue wider than one pass of the 4-wave workgroup (8 values per
+    // thread): XM 4, with enough waves along rows that one pass covers the
+    // activation block (its loads are issued before the index words and its
+    // arithmetic overlaps the first gathers; later passes would wait behind
+    // them)
+    if (p.xm == 1) {
+        const int64_t x_vals = (int64_t)p.bt * c.ng * 8;
+        const int64_t waves = (x_vals / 8 + 63) / 64;
+        if (waves > (int64_t)p.wi * p.wr) {
+            const int64_t wr = (waves + p.wi - 1) / p.wi;
+            if (64 * p.wi * wr <= gemv_max_threads(c.s2, c.cb_dt, 4)) {
+                p.xm = 4;
+                p.wr = (int)wr;
+            }
+        }
+    }
     p.threads = 64 * p.wi * p.wr;
     const int rpw = 64 / lpr;
     const int64_t ztiles = (batch + p.bt - 1) / p.bt;
@@ -198,7 +214,7 @@ int gemv_launch(const GemvCall& c)
     if (c.ng > 0x7FFFFFFF || p.n_rowblocks > 0x7FFFFFFF || c.seg[0].out_rows > 0x7FFFFFFF || a.nch > 0xFFFF ||
         a.P > 0xFFFF || p.lpr > 63 || p.wi > 15 || p.wr > 15)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: shape outside the kernel's argument ranges");
-    if (p.threads > gemv_max_threads(c.s2, c.cb_dt, c.xm) || p.threads % 64)
+    if (p.threads > gemv_max_threads(c.s2, c.cb_dt, p.xm) || p.threads % 64)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: internal plan error (%d threads)", p.threads);
     if (c.xm == 2 && (c.s2 == VQ2_S2_U16 || p.bt != 1))
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: the fused SwiGLU prologue is for 2 and 3 bpw, batch 1");

@@ -632,14 +632,16 @@ struct Cens {
     Centroid<CBT> c1[IT][S2 == VQ2_S2_U16 ? GPL : 1];
 };
 
-template <int CBT, int S2, int GPL, int IT>
+// ST0 / ST1: gather the stage-1 / the (16,16) stage-2 centroids
+template <int CBT, int S2, int GPL, int IT, bool ST0 = true, bool ST1 = true>
 __device__ __forceinline__ void gather_block(const GemvArgs& a, const Codes<S2, GPL, IT>& cd, Cens<CBT, S2, GPL, IT>& ce)
 {
 #pragma unroll
     for (int it = 0; it < IT; it++) {
+        if constexpr (ST0)
 #pragma unroll
-        for (int q = 0; q < GPL; q++) ce.c0[it][q].load(a.cb0, cd.c0(it, q));
-        if constexpr (S2 == VQ2_S2_U16)
+            for (int q = 0; q < GPL; q++) ce.c0[it][q].load(a.cb0, cd.c0(it, q));
+        if constexpr (S2 == VQ2_S2_U16 && ST1)
 #pragma unroll
             for (int q = 0; q < GPL; q++) ce.c1[it][q].load(a.cb1, cd.c1(it, q));
     }
@@ -711,9 +713,12 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 // or 8 (the rest; <= 256 VGPRs), which those instantiations fit without
 // spilling.  Every other kernel keeps 4 waves: a wider bound changes their
 // register allocation, and the dense launches measured slower with it.
+// XM 4 (the RHT prologue of XM 1 for activations wider than 256 threads x 8
+// values, e.g. the 6144-input down projection) takes up to 12 waves, so its
+// single prologue pass covers n = 6144 per batch column.
 constexpr int gemv_max_threads(int s2, int cbt, int xm)
 {
-    return xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512);
+    return xm == 4 ? 768 : (xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512));
 }
 
 // XT: activation dtype of the prologue kernels (XM != 0); unused for XM 0.
@@ -733,8 +738,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
     // 16-byte aligned: the activation block is written and read with 16-byte LDS accesses
     extern __shared__ __align__(16) float s_dyn[];  // [activation block (XM != 0)] [item partials]
-    // XM 3 is XM 1 (rotate x in the prologue) with the router built in
-    constexpr int XP = XM == 3 ? 1 : XM;
+    // XM 3 is XM 1 (rotate x in the prologue) with the router built in; XM 4
+    // is XM 1 in wide workgroups
+    constexpr int XP = (XM == 3 || XM == 4) ? 1 : XM;
 
     const int og = blockIdx.y;
     const int bt0 = blockIdx.z * BT;
@@ -808,8 +814,13 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     // flight.  Unconditional: a branch around them would leave the compiler
     // unsure which loads are outstanding, and it would then wait for the
     // gathers inside the prologue.
+    // (The 12-wave XM 4 kernel has at most 168 registers: it holds only the
+    // stage-1 centroids through the prologue, and only of fp16 codebooks --
+    // more would spill, and a spill reload waits for every gather.)
+    constexpr bool PRE = XP != 0 && !(XM == 4 && CBT != VQ2_DT_F16);
+    constexpr bool PRE_ST1 = !(XM == 4 && S2 == VQ2_S2_U16);
     Cens<CBT, S2, GPL, IT> ce0;
-    if constexpr (XP != 0) gather_block<CBT, S2, GPL, IT>(a, cd, ce0);
+    if constexpr (PRE) gather_block<CBT, S2, GPL, IT, true, PRE_ST1>(a, cd, ce0);
 
     if constexpr (S2 == VQ2_S2_U8) {
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
@@ -850,8 +861,12 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             bool nvalid[IT];
             fetch_codes<S2, GPL, IT>(a, rbn, rows_per_block, wr, wr_id, rpw, sub, g0, lane_ok && !bad, e, nx, nvalid);
             float acc[IT][BT];
-            if constexpr (decltype(pre)::value) dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
-            else block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+            if constexpr (decltype(pre)::value) {
+                if constexpr (!PRE_ST1) gather_block<CBT, S2, GPL, IT, false, true>(a, cd, ce0);
+                dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
+            } else {
+                block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+            }
 #pragma unroll
             for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -886,7 +901,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         };
         // prologue kernels pre-gathered the first block (rb < n_rowblocks:
         // the persistent grid never exceeds the row-block count)
-        if constexpr (XP != 0) step(std::true_type{});
+        if constexpr (PRE) step(std::true_type{});
         while (rb < a.n_rowblocks) step(std::false_type{});
         if constexpr (EP == 1) {
             // best key of the workgroup per batch column: wave, then waves
@@ -953,8 +968,12 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             cur_item = item;
         }
         float acc[IT][BT];
-        if constexpr (decltype(pre)::value) dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
-        else block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+        if constexpr (decltype(pre)::value) {
+            if constexpr (!PRE_ST1) gather_block<CBT, S2, GPL, IT, false, true>(a, cd, ce0);
+            dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
+        } else {
+            block_dot<CBT, S2, GPL, BT, IT>(a, s_cb1, cd, valid, xs, acc);
+        }
 #pragma unroll
         for (int it = 0; it < IT; it++)
 #pragma unroll
@@ -1030,7 +1049,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         item = nitem;
         rbg = nrbg;
     };
-    if constexpr (XP != 0) mstep(std::true_type{});
+    if constexpr (PRE) mstep(std::true_type{});
     while (rbg < a.n_rowblocks) mstep(std::false_type{});
 }
 
@@ -1141,6 +1160,9 @@ inline hipError_t launch_xm(const GemvArgs& a, const GemvPlan& p, dim3 grid, siz
         else return hipErrorInvalidValue;
     case 3:
         if constexpr (S2 == VQ2_S2_NONE && BT == 1) return launch_xt<CBT, S2, GPL, BT, IT, 3>(a, p, grid, shm, st);
+        else return hipErrorInvalidValue;
+    case 4:
+        if constexpr (BT <= 2) return launch_xt<CBT, S2, GPL, BT, IT, 4>(a, p, grid, shm, st);
         else return hipErrorInvalidValue;
     default:
         if (p.ep == 1) {

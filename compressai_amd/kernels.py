@@ -253,17 +253,18 @@ def vq_gemv_16_16(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torc
     return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
 
 
-# Largest n whose RHT vq_gemv_rht builds inside the GEMV launch.
-FUSED_RHT_MAX_N = 2048
+# Largest activation block (batch x n values) whose RHT vq_gemv_rht builds
+# inside the GEMV launch: one prologue pass of a 768-thread workgroup.
+FUSED_RHT_MAX_VALS = 6144
 
 
 def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=None, rs=1.0, *,
                 out_dtype=torch.float32, ys=None):
     """Rotate x with the RHT and multiply by up to 4 VQ matrices (the q/k/v
-    or gate/up fusion of a decoder layer).  n <= 2048: one launch, every
-    workgroup rotates x in its LDS; n > 2048: a separate vq_rht launch, then
-    one launch of the matrices (measured faster on MI355X than rotating n
-    values in every workgroup).  x [n] or [B, n] (B <= 2); mats: list of
+    or gate/up fusion of a decoder layer).  B * n <= 6144: one launch, every
+    workgroup rotates x in its LDS (one pass of up to 768 threads, overlapped
+    with the first gathers); larger blocks: a separate vq_rht launch, then one
+    launch of the matrices.  x [n] or [B, n] (B <= 2); mats: list of
     (i0, i1 or None, scale, out_rows) sharing one cfg.  Returns the list of
     outputs ([out] or [B, out])."""
     dev = _dev(x, cb0, cb1, perm, sign)
@@ -301,7 +302,7 @@ def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=N
     if scale.dtype != mats[0][2].dtype or any(o.dtype != outs[0].dtype for o in outs):
         raise Vq2Error("vq_gemv_rht: scales and outputs of a launch share a dtype")
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
-    if n > FUSED_RHT_MAX_N:
+    if B * n > FUSED_RHT_MAX_VALS:
         x2 = vq_rht(x2, perm, sign, hb, sc, out_dtype=torch.float32)
         perm = sign = None
         hb = 0

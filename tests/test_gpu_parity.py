@@ -381,6 +381,30 @@ def test_gemv_rht_fused_6144(dev):
     assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
 
 
+@pytest.mark.parametrize("n,batch,bpw,xdt", [
+    (6144, 1, 4, torch.float16), (6144, 1, 2, torch.float32), (6144, 1, 3, torch.bfloat16),
+    (4096, 1, 4, torch.float32), (3072, 2, 2, torch.float16), (2048, 2, 3, torch.bfloat16)])
+def test_gemv_rht_fused_wide(dev, n, batch, bpw, xdt):
+    """Activation blocks wider than 256 threads x 8 values rotate in one pass
+    of a wider workgroup (up to 768 threads): permuted RHT + GEMV against the
+    oracle's RHT then GEMV, every codebook stage kind and activation dtype."""
+    out = 1000
+    cb0 = synth.codebook(9400)
+    cb1 = synth.codebook(9401, 256 if bpw == 3 else 65536) if bpw > 2 else None
+    m = synth.vq_matrix(9400 + n + batch, out, n, bpw=bpw)
+    x = synth.activations(9404 + n, (batch, n), dtype=xdt)
+    perm = synth.permutation(9406 + n, n)
+    sign = synth.signs(9405 + n, n)
+    hb = 2048 if n % 2048 == 0 else 1024
+    (y,) = K.vq_gemv_rht(x.to(dev), [(m["idx0"].to(dev), None if m["idx1"] is None else m["idx1"].to(dev),
+                                      m["scale"].to(dev), out)], cb0.to(dev), None if cb1 is None else cb1.to(dev),
+                         n, perm.to(dev), sign.to(dev), hb)
+    xr = O.rht(x.float(), perm, sign, hb).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert y.shape == (batch, out)
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
 def test_packed_linear_forward(dev):
     from compressai_amd.runtime import PackedLinear, PackedLMHead
 
