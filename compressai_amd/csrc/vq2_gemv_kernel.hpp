@@ -166,7 +166,15 @@ struct Codes {
     static constexpr int W1 = S2 == VQ2_S2_U8 ? (GPL + 3) / 4 : (S2 == VQ2_S2_U16 ? W0 : 1);
     uint32_t w0[IT][W0];
     uint32_t w1[IT][W1];
+    // the row scale's raw 16-bit halves (fp32: low, high; fp16 / bf16: the
+    // value twice), fetched with the index words so the epilogue has it
+    uint32_t s0[IT], s1[IT];
     __device__ __forceinline__ uint32_t c0(int it, int q) const { return (w0[it][q >> 1] >> (16 * (q & 1))) & 0xFFFFu; }
+    __device__ __forceinline__ float scale(int it, int dt) const
+    {
+        return dt == VQ2_DT_F32 ? __uint_as_float((s1[it] << 16) | s0[it])
+                                : (dt == VQ2_DT_F16 ? f16_bits_to_f32((uint16_t)s0[it]) : bf16_bits_to_f32(s0[it]));
+    }
     __device__ __forceinline__ uint32_t c1(int it, int q) const
     {
         if constexpr (S2 == VQ2_S2_U8) return (w1[it][q >> 2] >> (8 * (q & 3))) & 0xFFu;
@@ -210,6 +218,18 @@ __device__ __forceinline__ void load_raw8(const uint8_t* p, int64_t off, uint32_
     } else {
         w[0] = (uint32_t)__builtin_nontemporal_load(q);
     }
+}
+
+// Row scale element idx of a scale array of dtype dt, as two 16-bit loads at
+// addresses chosen by the dtype (no branch around a load: the compiler would
+// then wait for every outstanding load where the paths merge).
+template <int S2, int GPL, int IT>
+__device__ __forceinline__ void load_scale(const void* sp, int dt, int64_t idx, int it, Codes<S2, GPL, IT>& cd)
+{
+    const uint16_t* p = (const uint16_t*)sp;
+    const bool f32 = dt == VQ2_DT_F32;
+    cd.s0[it] = p[f32 ? 2 * idx : idx];
+    cd.s1[it] = p[f32 ? 2 * idx + 1 : idx];
 }
 
 // The index words of one lane for every plane of a row at element offset off.
@@ -608,6 +628,11 @@ __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int r
                                                 : (const void*)((const int16_t*)sg.idx1 + e * a.e_istride),
                                 off, it, cd);
     }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
+        load_scale<S2, GPL, IT>(sg.scale, a.s_dt, row < sg.out_rows ? e * a.e_sstride + row : 0, it, cd);
+    }
 }
 
 // Codes of task (row block rb, item) for this lane: item = pair * nch + chunk.
@@ -799,6 +824,11 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             load_codes<S2, GPL, IT>(k_idx0, k_idx1, valid[it] ? row * k_ng + g0 : 0, it, cd);
         }
         touch_kernargs(a);  // the argument lines the rest of the kernel reads
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int64_t row = rb * rows_per_block + (int64_t)(it * wr + wr_id) * rpw + sub;
+            load_scale<S2, GPL, IT>(a.seg[0].scale, a.s_dt, row < k_rows0 ? row : 0, it, cd);
+        }
     } else {
         // the lookup chain below reads several argument lines: fetch them all first
         touch_kernargs(a);
@@ -879,7 +909,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
                 for (int it = 0; it < IT; it++) {
                     const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
                     if (row >= sg.out_rows) continue;
-                    const float sc = load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row);
+                    const float sc = cd.scale(it, a.s_dt);
 #pragma unroll
                     for (int b = 0; b < BT; b++) {
                         float v = (acc[it][b] * sc) * a.rs;
@@ -986,7 +1016,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
-            const float sc = row < sg.out_rows ? load_as_f32(sg.scale, a.s_dt, e * a.e_sstride + row) : 0.0f;
+            const float sc = row < sg.out_rows ? cd.scale(it, a.s_dt) : 0.0f;
 #pragma unroll
             for (int b = 0; b < BT; b++) {
                 float v = (acc[it][b] * sc) * a.rs;
