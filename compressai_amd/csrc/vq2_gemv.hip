@@ -162,6 +162,7 @@ int gemv_launch(const GemvCall& c)
     hipStream_t st = (hipStream_t)c.stream;
     const int num_cu = device_cu_count();
     const GemvPlan p = plan_gemv(c, num_cu);
+    if (p.n_rowblocks == 0) return VQ2_OK;  // every segment has zero rows
 
     // the vector kernel needs GPL-wide, aligned index words and 16-byte
     // aligned activation rows

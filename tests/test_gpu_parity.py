@@ -405,6 +405,31 @@ def test_gemv_rht_fused_wide(dev, n, batch, bpw, xdt):
     assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
 
 
+def test_gemv_empty_segments(dev):
+    """Zero-row matrices: a launch with no rows is a no-op, and an empty
+    segment between non-empty ones (whose row blocks it owns none of) does not
+    shift the others' rows."""
+    n = 2048
+    cb0 = synth.codebook(9500)
+    m = synth.vq_matrix(9500, 0, n, bpw=2)
+    y = K.vq_gemv_16(synth.activations(9504, n, dtype=torch.float32).to(dev), m["idx0"].to(dev), cb0.to(dev),
+                     m["scale"].to(dev), 0, n, 1.0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert y.shape == (0,)
+    shapes = [512, 0, 300, 0]
+    mats = [synth.vq_matrix(9510 + 10 * k, rows, n, bpw=2) for k, rows in enumerate(shapes)]
+    x = synth.activations(9514, n, dtype=torch.float16)
+    sign = synth.signs(9515, n)
+    ys = K.vq_gemv_rht(x.to(dev), [(mm["idx0"].to(dev), None, mm["scale"].to(dev), rows) for mm, rows in zip(mats, shapes)],
+                       cb0.to(dev), None, n, None, sign.to(dev), 2048)
+    xr = O.rht(x, None, sign, 2048).astype(np.float32)
+    for yk, mm, rows in zip(ys, mats, shapes):
+        assert yk.shape == (rows,)
+        if rows:
+            _, y64 = O.vq_gemv(xr, mm["idx0"], None, cb0, None, mm["scale"])
+            assert O.max_rel_err(yk.cpu().numpy(), y64[0]) < TOL
+
+
 def test_packed_linear_forward(dev):
     from compressai_amd.runtime import PackedLinear, PackedLMHead
 
