@@ -257,6 +257,27 @@ __global__ void __launch_bounds__(MM_THREADS) vq_gemm_mfma_kernel(const GemmArgs
     }
 }
 
+// Sum of the splits' partials at element t in split order.  The loads go out
+// eight at a time (indices clamped to the last split, so the loads need no
+// branch) before the adds: a plain loop over a run-time split count issues
+// them a few at a time, one memory round trip apart.
+__device__ __forceinline__ float split_sum(const GemmArgs& a, int64_t t, int64_t pstride)
+{
+    float sum = 0.0f;
+    for (int sp0 = 0; sp0 < a.splits; sp0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int sp = sp0 + k < a.splits ? sp0 + k : a.splits - 1;
+            v[k] = __builtin_nontemporal_load(&a.part[sp * pstride + t]);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (sp0 + k < a.splits) sum += v[k];
+    }
+    return sum;
+}
+
 // y[b, r] = (partials summed in split order) * s[r] * rs
 __global__ void __launch_bounds__(256) vq_gemm_reduce_kernel(const GemmArgs a)
 {
@@ -264,8 +285,7 @@ __global__ void __launch_bounds__(256) vq_gemm_reduce_kernel(const GemmArgs a)
     const int64_t pstride = (int64_t)a.m * a.out_rows;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < tot; t += (int64_t)gridDim.x * blockDim.x) {
         const int64_t m = t / a.out_rows, row = t - m * a.out_rows;
-        float sum = 0.0f;
-        for (int sp = 0; sp < a.splits; sp++) sum += __builtin_nontemporal_load(&a.part[sp * pstride + t]);
+        const float sum = split_sum(a, t, pstride);
         const float s = load_as_f32(a.scale, a.s_dt, row);
         store_from_f32(a.y, a.y_dt, m * a.y_stride + row, (sum * s) * a.rs);
     }
@@ -284,8 +304,7 @@ __global__ void __launch_bounds__(256) vq_gemm_reduce_top1_kernel(const GemmArgs
     for (int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; row < a.out_rows;
          row += (int64_t)gridDim.x * blockDim.x) {
         const int64_t t = (int64_t)m * a.out_rows + row;
-        float sum = 0.0f;
-        for (int sp = 0; sp < a.splits; sp++) sum += __builtin_nontemporal_load(&a.part[sp * pstride + t]);
+        const float sum = split_sum(a, t, pstride);
         const float s = load_as_f32(a.scale, a.s_dt, row);
         const uint64_t k = argmax_key((sum * s) * a.rs, row);
         best = k > best ? k : best;
