@@ -190,7 +190,9 @@ def bench_dense(args, dev):
                 dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl)
 
 
-def bench_moe(args, dev, n_layers=40, T=1):
+def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
+    """MoE layers over a 40-layer resident pool, T tokens per step
+    for each T in `tokens` (the same pool, per-layer seeded router logits)."""
     import torch
 
     from compressai_amd import synth
@@ -199,7 +201,7 @@ def bench_moe(args, dev, n_layers=40, T=1):
     E, k = 256, 8
     g = torch.Generator(device=dev).manual_seed(4000)
     cb = synth.codebook(4000).to(dev)
-    layers, inputs = [], []
+    layers = []
     for _ in range(n_layers):
         gu = rand_i16((E + 1, 1024, 256), g, dev)
         gus = rand_scale((E + 1) * 1024, g, dev).view(E + 1, 1024)
@@ -207,30 +209,36 @@ def bench_moe(args, dev, n_layers=40, T=1):
         dns = rand_scale((E + 1) * 2048, g, dev).view(E + 1, 2048)
         gate = (torch.randn(HIDDEN, generator=g, device=dev) * 0.02).to(torch.float16)
         layers.append(MoELayer(gu, gus, dn, dns, cb, gate, top_k=k))
-        h = torch.randn(T, HIDDEN, generator=g, device=dev).to(torch.float16)
-        lg = torch.randn(T, E, generator=g, device=dev).to(torch.float16)
-        inputs.append((h, lg))
     per_expert = 1024 * 256 * 2 + 1024 * 2 + 2048 * 64 * 2 + 2048 * 2
     log(f"moe: {n_layers} layers x {E + 1} experts resident ({n_layers * (E + 1) * per_expert / 2**30:.2f} GiB)")
-    outs = [None] * n_layers
+    res = {}
+    for T in tokens:
+        inputs = []
+        for _ in range(n_layers):
+            h = torch.randn(T, HIDDEN, generator=g, device=dev).to(torch.float16)
+            lg = torch.randn(T, E, generator=g, device=dev).to(torch.float16)
+            inputs.append((h, lg))
+        outs = [None] * n_layers
 
-    def fwd(l):
-        outs[l] = layers[l](*inputs[l])
+        def fwd(l, inputs=inputs, outs=outs):
+            outs[l] = layers[l](*inputs[l])
 
-    gr = capture(fwd, n_layers, dev)
-    time_graph(gr, 3, dev)
-    reps = max(5, args.steps // n_layers)
-    ms, _ = time_graph(gr, reps, dev)
-    us = ms * 1e3 / (reps * n_layers)
-    # distinct experts actually read per layer (routed + shared)
-    distinct = []
-    for l in range(n_layers):
-        ids, _ = layers[l].route(inputs[l][0], inputs[l][1])
-        distinct.append(len(set(ids.flatten().tolist())))
-    bytes_layer = statistics.mean(distinct) * per_expert
-    gbps = bytes_layer / (us * 1e-6) / 1e9
-    log(f"moe T={T}: {us:.2f} us/layer, {gbps:.1f} GB/s ({statistics.mean(distinct):.1f} experts/layer)")
-    return dict(us=us, gbps=gbps, bytes=bytes_layer)
+        gr = capture(fwd, n_layers, dev)
+        time_graph(gr, 3, dev)
+        reps = max(5, args.steps // n_layers)
+        ms, _ = time_graph(gr, reps, dev)
+        us = ms * 1e3 / (reps * n_layers)
+        # distinct experts actually read per layer (routed + shared)
+        distinct = []
+        for l in range(n_layers):
+            ids, _ = layers[l].route(inputs[l][0], inputs[l][1])
+            distinct.append(len(set(ids.flatten().tolist())))
+        bytes_layer = statistics.mean(distinct) * per_expert
+        gbps = bytes_layer / (us * 1e-6) / 1e9
+        log(f"moe T={T}: {us:.2f} us/layer, {gbps:.1f} GB/s ({statistics.mean(distinct):.1f} experts/layer)")
+        res[T] = dict(us=us, gbps=gbps, bytes=bytes_layer)
+        del gr
+    return res
 
 
 def bench_lm_head(args, dev, batch=1, copies=14):
@@ -528,8 +536,10 @@ def main():
             "graph_replay": True,
         },
         "pct_of_peak": round(100.0 * d["gbps"] / PEAK_HBM_GBPS, 3),
-        "moe_layer_us": None if moe is None else round(moe["us"], 3),
-        "moe_layer_gbps": None if moe is None else round(moe["gbps"], 2),
+        "moe_layer_us": None if moe is None else round(moe[1]["us"], 3),
+        "moe_layer_gbps": None if moe is None else round(moe[1]["gbps"], 2),
+        "moe_layer_us_t8": None if moe is None else round(moe[8]["us"], 3),
+        "moe_layer_gbps_t8": None if moe is None else round(moe[8]["gbps"], 2),
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
