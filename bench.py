@@ -92,8 +92,11 @@ class DenseLayers:
         self.x_o = synth.activations(2014, HIDDEN).to(dev)
         self.x_mlp = synth.activations(2024, HIDDEN).to(dev)
         self.x_down = synth.activations(2034, INTER).to(dev)
+        # the reference's rotation always permutes before the sign flip
         self.sign_h = synth.signs(2005, HIDDEN).to(dev)
         self.sign_i = synth.signs(2015, INTER).to(dev)
+        self.perm_h = synth.permutation(2006, HIDDEN).to(dev)
+        self.perm_i = synth.permutation(2016, INTER).to(dev)
         f32 = dict(dtype=torch.float32, device=dev)
         self.xr_a, self.xr_o, self.xr_m = (torch.empty(HIDDEN, **f32) for _ in range(3))
         self.xr_d = torch.empty(INTER, **f32)
@@ -105,23 +108,23 @@ class DenseLayers:
         i0, i1, s, out, n = lay[name]
         K.vq_gemv(xr, i0, i1, self.cb0, self.cb1 if i1 is not None else None, s, out, n, 1.0, y=self.y[name])
 
-    def fused(self, lay, names, x, sign):
+    def fused(self, lay, names, x, perm, sign):
         """One launch: RHT of x built in LDS + the GEMVs of `names`."""
         from compressai_amd import kernels as K
 
         mats = [(lay[nm][0], lay[nm][1], lay[nm][2], lay[nm][3]) for nm in names]
         n = lay[names[0]][4]
-        K.vq_gemv_rht(x, mats, self.cb0, self.cb1 if mats[0][1] is not None else None, n, None, sign, 2048,
+        K.vq_gemv_rht(x, mats, self.cb0, self.cb1 if mats[0][1] is not None else None, n, perm, sign, 2048,
                       ys=[self.y[nm] for nm in names])
 
     def step(self, l):
         """One decoder layer's projections: 4 launches (q/k/v, o, gate/up,
         down), each rotating its activation in LDS."""
         lay = self.layers[l]
-        self.fused(lay, ("q", "k", "v"), self.x_attn, self.sign_h)
-        self.fused(lay, ("o",), self.x_o, self.sign_h)
-        self.fused(lay, ("gate", "up"), self.x_mlp, self.sign_h)
-        self.fused(lay, ("down",), self.x_down, self.sign_i)
+        self.fused(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
+        self.fused(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
+        self.fused(lay, ("gate", "up"), self.x_mlp, self.perm_h, self.sign_h)
+        self.fused(lay, ("down",), self.x_down, self.perm_i, self.sign_i)
 
 
 def capture(fn, n_items, dev):
@@ -179,7 +182,7 @@ def bench_dense(args, dev):
     # dominant kernel: the fused gate/up launch (RHT + two 6144 x 2048 4 bpw
     # GEMVs), back to back over the layer sets
     dom_bytes = 2 * (INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2)
-    gd = capture(lambda l: dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.sign_h), L, dev)
+    gd = capture(lambda l: dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h), L, dev)
     time_graph(gd, 2, dev)
     dreps = max(4, 2000 // L)
     dms, _ = time_graph(gd, dreps, dev)
@@ -309,11 +312,12 @@ def bench_small_m(args, dev):
             del mats
             torch.cuda.empty_cache()
     sign = synth.signs(5006, 8192).to(dev)
+    perm = synth.permutation(5008, 8192).to(dev)
     for M in (16, 64):
         x = synth.activations(5007, (M, 8192), dtype=torch.float16).to(dev)
         xr = torch.empty((M, 8192), dtype=torch.float32, device=dev)
         for hb in (2048, 8192):
-            gr = capture(lambda l, x=x, hb=hb: K.vq_rht(x, None, sign, hb, out=xr), 50, dev)
+            gr = capture(lambda l, x=x, hb=hb: K.vq_rht(x, perm, sign, hb, out=xr), 50, dev)
             time_graph(gr, 1, dev)
             ms, _ = time_graph(gr, 10, dev)
             us = ms * 1e3 / 500
@@ -413,8 +417,8 @@ def cpu_baseline(dl, budget_s=20.0):
     torch.set_num_threads(cores)
     lay = {k: tuple(t.cpu() if hasattr(t, "cpu") else t for t in v) for k, v in dl.layers[0].items()}
     cb0, cb1 = dl.cb0.cpu(), dl.cb1.cpu()
-    rot_h = CpuRot(None, dl.sign_h.cpu(), 2048)
-    rot_i = CpuRot(None, dl.sign_i.cpu(), 2048)
+    rot_h = CpuRot(dl.perm_h.cpu(), dl.sign_h.cpu(), 2048)
+    rot_i = CpuRot(dl.perm_i.cpu(), dl.sign_i.cpu(), 2048)
     xa, xo, xm, xd = dl.x_attn.cpu(), dl.x_o.cpu(), dl.x_mlp.cpu(), dl.x_down.cpu()
 
     def step():
@@ -493,7 +497,7 @@ def main():
     if args.only == "dominant":
         dl = DenseLayers(args.layers, dev)
         for l in range(args.layers):
-            dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.sign_h)
+            dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
         torch.cuda.synchronize(dev)
         log("dominant-only run done")
         return
