@@ -230,7 +230,10 @@ int gemv_launch(const GemvCall& c)
     const int64_t items = (int64_t)a.P * ((c.ng + (int64_t)p.lpr * p.gpl - 1) / ((int64_t)p.lpr * p.gpl));
     const int64_t x_floats = c.xm == 0 ? 0 : (c.xm == 2 ? (int64_t)a.P : p.bt) * c.ng * 8;
     const int64_t part_floats = items > 1 ? (int64_t)p.wi * p.rows_per_block * p.bt : 0;
-    const size_t shm = (size_t)(x_floats + part_floats) * sizeof(float);
+    // the prologue stages the unpermuted activation block where the partials go later: raw
+    // elements, or silu(gate) * up as fp32 for XM 2
+    const int64_t stage_floats = c.xm == 0 ? 0 : c.xm == 2 ? x_floats : (x_floats * dt_size(c.x_dt) + 3) / 4;
+    const size_t shm = (size_t)(x_floats + std::max(part_floats, stage_floats)) * sizeof(float);
     if ((int64_t)shm > GEMV_LDS_BUDGET)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 gemv: %zu bytes of LDS needed (> %lld)", shm,
                          (long long)GEMV_LDS_BUDGET);

@@ -442,14 +442,19 @@ __device__ __forceinline__ void fwht_head(float (&v)[8], int L)
 // read with vector loads.  n % 8 == 0; perm 16-byte and sign 8-byte aligned
 // (checked on the host).
 //
-// An iteration is split into its loads (xpro_load: raw element bits, sign
-// bytes, bad-index mask) and its arithmetic (xpro_finish).  The kernel issues
-// the first iteration's loads before its first index load: loads complete in
-// issue order, so the RHT arithmetic then waits only for these L2-resident
-// values, not for the index words coming from HBM.
+// The permutation is applied in LDS: a thread loads the activation elements
+// of its own 8 slots (contiguous, coalesced) together with the slots'
+// permutation and sign words, so no global load waits for another.  The
+// workgroup stages the raw block in LDS (stage_x), and after a barrier each
+// thread reads its permuted elements from there (xpro_permute) and does the
+// arithmetic (xpro_finish).  The kernel issues the first iteration's loads
+// before its first index load: loads complete in issue order, so the RHT
+// arithmetic then waits only for these L2-resident values, not for the index
+// words coming from HBM.
 struct XProLoad {
-    uint32_t g[8];  // raw activation bits (gate half for XM 2)
-    uint32_t u[8];  // raw up-half bits (XM 2)
+    uint32_t g[8];  // the slots' own activation bits (gate half for XM 2), then the permuted staged values
+    uint32_t u[8];  // the slots' up-half bits (XM 2)
+    u32x4 p0, p1;   // the slots' permutation entries (identity-table entries without a permutation)
     u32x2 sv;       // 8 sign bytes
     bool bad[8];    // permutation entry outside [0, n): the value is poisoned
 };
@@ -462,62 +467,134 @@ __device__ __forceinline__ float raw_to_f32(uint32_t r)
     else return bf16_bits_to_f32(r);
 }
 
-// +1 signs for a rotation without a sign table: the prologue then loads its
-// sign bytes from here (a select of pointers, no branch around the load).
+// +1 signs and identity entries for a rotation without a sign table or a
+// permutation: the prologue then loads its words from here (a select of
+// pointers, no branch around the load).  The tables repeat every 8192
+// elements: the identity entry of element i is i & 8191, and the prologue
+// adds i & ~8191.
 constexpr int VQ2_ONES = 8192;
 struct OnesTable {
     int8_t v[VQ2_ONES];
     constexpr OnesTable() : v() { for (int i = 0; i < VQ2_ONES; i++) v[i] = 1; }
 };
 static __device__ const OnesTable g_sign_ones = OnesTable();
+struct IotaTable {
+    int32_t v[VQ2_ONES];
+    constexpr IotaTable() : v() { for (int i = 0; i < VQ2_ONES; i++) v[i] = i; }
+};
+static __device__ const __align__(16) IotaTable g_perm_iota = IotaTable();
 
-// Loads of the iteration starting at element t0 of the nrows x n block
-// (t0 < total; callers clamp idle threads to t0 = 0).  No loaded value is
-// used here, and no load sits inside a branch of its own (activation dtype
-// XT is a template value, a missing sign table reads g_sign_ones): a loaded
-// value merged from branches is waited for at the merge.
+// Activation row of slot row r.
+template <int XM>
+__device__ __forceinline__ int64_t x_row(const GemvArgs& a, int r, int og, int bt0)
+{
+    if constexpr (XM == 1) return (int64_t)(og / a.x_pdiv) * a.x_pstride + (int64_t)(bt0 + r) * a.x_bstride;
+    else return ((int64_t)og * a.P + r) / a.x_pdiv * a.x_pstride;
+}
+
+// Activation loads of the 8 slots starting at element t0 of the nrows x n
+// block (t0 < total; callers clamp idle threads to t0 = 0): contiguous
+// elements, activation dtype XT a template value (no branch around a load).
 template <int XM, int XT>
-__device__ __forceinline__ void xpro_load(const GemvArgs& a, int64_t t0, int64_t n, int og, int bt0, XProLoad& L)
+__device__ __forceinline__ void xpro_xload(const GemvArgs& a, int64_t t0, int64_t n, int og, int bt0, XProLoad& L)
 {
     const int r = (int)(t0 / n);
     const int64_t i0 = t0 - (int64_t)r * n;
-    int64_t src[8];
-    if (a.perm) {
-        const u32x4 p0 = *(const u32x4*)(a.perm + i0);
-        const u32x4 p1 = *(const u32x4*)(a.perm + i0 + 4);
+    const int64_t row = x_row<XM>(a, r, og, bt0) + i0;
+    if constexpr (XT == VQ2_DT_F32) {
+        const uint32_t* x = (const uint32_t*)a.x + row;
 #pragma unroll
-        for (int k = 0; k < 4; k++) { src[k] = (int32_t)p0[k]; src[4 + k] = (int32_t)p1[k]; }
+        for (int k = 0; k < 8; k++) L.g[k] = x[k];
+        if constexpr (XM == 2)
+#pragma unroll
+            for (int k = 0; k < 8; k++) L.u[k] = x[n + k];
     } else {
+        const uint16_t* x = (const uint16_t*)a.x + row;
 #pragma unroll
-        for (int k = 0; k < 8; k++) src[k] = i0 + k;
+        for (int k = 0; k < 8; k++) L.g[k] = x[k];
+        if constexpr (XM == 2)
+#pragma unroll
+            for (int k = 0; k < 8; k++) L.u[k] = x[n + k];
+    }
+}
+
+// Permutation and sign words of the same slots.  Both tables are global
+// memory; said explicitly, or the selected pointer is generic and the load
+// becomes a flat load, which the compiler's memory-counter waits cannot
+// order against the global loads.
+__device__ __forceinline__ void xpro_tables(const GemvArgs& a, int64_t t0, int64_t n, XProLoad& L)
+{
+    const int r = (int)(t0 / n);
+    const int64_t i0 = t0 - (int64_t)r * n;
+    const int32_t* pp = a.perm ? a.perm + i0 : g_perm_iota.v + (i0 & (VQ2_ONES - 1));
+    const __attribute__((address_space(1))) u32x4* pg = (const __attribute__((address_space(1))) u32x4*)pp;
+    L.p0 = pg[0];
+    L.p1 = pg[1];
+    const int8_t* sgn = a.sign ? a.sign + i0 : g_sign_ones.v + (i0 & (VQ2_ONES - 1));
+    L.sv = *(const __attribute__((address_space(1))) u32x2*)sgn;
+}
+
+// All loads of an iteration; no loaded value is used here.
+template <int XM, int XT>
+__device__ __forceinline__ void xpro_load(const GemvArgs& a, int64_t t0, int64_t n, int og, int bt0, XProLoad& L)
+{
+    xpro_tables(a, t0, n, L);
+    xpro_xload<XM, XT>(a, t0, n, og, bt0, L);
+}
+
+// Staged block in LDS, [nrows x n]: XM 1 the raw elements in the
+// activation's own width; XM 2 silu(gate) * up as fp32 (the activation is
+// elementwise, so it is taken before the permutation).
+template <int XM, int XT>
+__device__ __forceinline__ void stage_store(void* s_stage, int64_t t0, const XProLoad& L)
+{
+    if constexpr (XM == 2 || XT == VQ2_DT_F32) {
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            w[k] = XM == 2 ? __float_as_uint(silu_f32(raw_to_f32<XT>(L.g[k])) * raw_to_f32<XT>(L.u[k])) : L.g[k];
+        u32x4 w0, w1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) { w0[k] = w[k]; w1[k] = w[4 + k]; }
+        uint32_t* st = (uint32_t*)s_stage;
+        *(u32x4*)(st + t0) = w0;
+        *(u32x4*)(st + t0 + 4) = w1;
+    } else {
+        u32x4 w;
+#pragma unroll
+        for (int k = 0; k < 4; k++) w[k] = (L.g[2 * k] & 0xFFFFu) | (L.g[2 * k + 1] << 16);
+        *(u32x4*)((uint16_t*)s_stage + t0) = w;
+    }
+}
+
+// The slots' permuted elements, read from the staged block (same row).
+template <int XM, int XT>
+__device__ __forceinline__ void xpro_permute(const GemvArgs& a, const void* s_stage, int64_t t0, int64_t n,
+                                             XProLoad& L)
+{
+    const int r = (int)(t0 / n);
+    const int64_t rbase = (int64_t)r * n;
+    // identity-table entries repeat every VQ2_ONES elements
+    const int64_t pbase = a.perm ? 0 : ((t0 - rbase) & ~(int64_t)(VQ2_ONES - 1));
+    int64_t src[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        src[k] = pbase + (int32_t)L.p0[k];
+        src[4 + k] = pbase + (int32_t)L.p1[k];
     }
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         L.bad[k] = (uint64_t)src[k] >= (uint64_t)n;  // not a permutation of [0, n): poison the value
-        src[k] = L.bad[k] ? 0 : src[k];
+        src[k] = rbase + (L.bad[k] ? 0 : src[k]);
     }
-    // both tables are global memory; said explicitly, or the selected pointer
-    // is generic and the load becomes a flat load, which the compiler's
-    // memory-counter waits cannot order against the global loads
-    const int8_t* sgn = a.sign ? a.sign + i0 : g_sign_ones.v + (i0 & (VQ2_ONES - 1));
-    L.sv = *(const __attribute__((address_space(1))) u32x2*)sgn;
-    int64_t row;
-    if constexpr (XM == 1) row = (int64_t)(og / a.x_pdiv) * a.x_pstride + (int64_t)(bt0 + r) * a.x_bstride;
-    else row = ((int64_t)og * a.P + r) / a.x_pdiv * a.x_pstride;
-    if constexpr (XT == VQ2_DT_F32) {
-        const uint32_t* x = (const uint32_t*)a.x + row;
+    if constexpr (XM == 2 || XT == VQ2_DT_F32) {
+        const uint32_t* st = (const uint32_t*)s_stage;
 #pragma unroll
-        for (int k = 0; k < 8; k++) L.g[k] = x[src[k]];
-        if constexpr (XM == 2)
-#pragma unroll
-            for (int k = 0; k < 8; k++) L.u[k] = x[n + src[k]];
+        for (int k = 0; k < 8; k++) L.g[k] = st[src[k]];
     } else {
-        const uint16_t* x = (const uint16_t*)a.x + row;
+        const uint16_t* st = (const uint16_t*)s_stage;
 #pragma unroll
-        for (int k = 0; k < 8; k++) L.g[k] = x[src[k]];
-        if constexpr (XM == 2)
-#pragma unroll
-            for (int k = 0; k < 8; k++) L.u[k] = x[n + src[k]];
+        for (int k = 0; k < 8; k++) L.g[k] = st[src[k]];
     }
 }
 
@@ -529,9 +606,8 @@ __device__ __forceinline__ void xpro_finish(const GemvArgs& a, float* s_x, int64
     float v[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        const float g = raw_to_f32<XT>(L.g[k]);
-        if constexpr (XM == 2) v[k] = silu_f32(g) * raw_to_f32<XT>(L.u[k]);
-        else v[k] = g;
+        if constexpr (XM == 2) v[k] = __uint_as_float(L.g[k]);  // silu(gate) * up, taken when staged
+        else v[k] = raw_to_f32<XT>(L.g[k]);
         const float sg = (float)(int8_t)((L.sv[k >> 2] >> (8 * (k & 3))) & 0xFFu);
         v[k] = L.bad[k] ? __builtin_nanf("") : v[k] * sg;
     }
@@ -546,18 +622,40 @@ __device__ __forceinline__ void xpro_finish(const GemvArgs& a, float* s_x, int64
     *(u32x4*)(s_x + t0 + 4) = o1;
 }
 
-// The whole prologue, given the first iteration's loads (issued by the
-// caller at t0 = threadIdx.x * 8, clamped to 0 past the block).
+// Prologue, part 1: every slot's raw elements into the LDS stage, given the
+// first iteration's loads (issued by the caller at t0 = threadIdx.x * 8,
+// clamped to 0 past the block); ends with the barrier after which any
+// element may be read.
 template <int XM, int XT>
-__device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, int nrows, int64_t n, int og, int bt0,
+__device__ __forceinline__ void stage_x(const GemvArgs& a, void* s_stage, int nrows, int64_t n, int og, int bt0,
                                         const XProLoad& first)
 {
     const int64_t total = (int64_t)nrows * n;
     int64_t t0 = (int64_t)threadIdx.x * 8;
-    if (t0 < total) xpro_finish<XM, XT>(a, s_x, t0, first);
+    if (t0 < total) stage_store<XM, XT>(s_stage, t0, first);
     for (t0 += (int64_t)blockDim.x * 8; t0 < total; t0 += (int64_t)blockDim.x * 8) {
         XProLoad L;
-        xpro_load<XM, XT>(a, t0, n, og, bt0, L);
+        xpro_xload<XM, XT>(a, t0, n, og, bt0, L);
+        stage_store<XM, XT>(s_stage, t0, L);
+    }
+    __syncthreads();
+}
+
+// Prologue, part 2: permuted reads, arithmetic, then the blockwise FWHT.
+template <int XM, int XT>
+__device__ __forceinline__ void build_x(const GemvArgs& a, float* s_x, const void* s_stage, int nrows, int64_t n,
+                                        XProLoad& first)
+{
+    const int64_t total = (int64_t)nrows * n;
+    int64_t t0 = (int64_t)threadIdx.x * 8;
+    if (t0 < total) {
+        xpro_permute<XM, XT>(a, s_stage, t0, n, first);
+        xpro_finish<XM, XT>(a, s_x, t0, first);
+    }
+    for (t0 += (int64_t)blockDim.x * 8; t0 < total; t0 += (int64_t)blockDim.x * 8) {
+        XProLoad L;
+        xpro_tables(a, t0, n, L);
+        xpro_permute<XM, XT>(a, s_stage, t0, n, L);
         xpro_finish<XM, XT>(a, s_x, t0, L);
     }
     __syncthreads();
@@ -740,10 +838,12 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 // register allocation, and the dense launches measured slower with it.
 // XM 4 (the RHT prologue of XM 1 for activations wider than 256 threads x 8
 // values, e.g. the 6144-input down projection) takes up to 12 waves, so its
-// single prologue pass covers n = 6144 per batch column.
+// single prologue pass covers n = 6144 per batch column -- up to 8 with fp32
+// (16,16) codebooks, whose 32 centroid words per group would spill at 12.
 constexpr int gemv_max_threads(int s2, int cbt, int xm)
 {
-    return xm == 4 ? 768 : (xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512));
+    return xm == 4 ? (cbt == VQ2_DT_F32 && s2 == VQ2_S2_U16 ? 512 : 768)
+                   : (xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512));
 }
 
 // XT: activation dtype of the prologue kernels (XM != 0); unused for XM 0.
@@ -762,7 +862,8 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     // stage-2 (uint8) codebook in LDS: 256 rows x 16 B (x2 for fp32)
     __shared__ u32x4 s_cb1[S2 == VQ2_S2_U8 ? (CBT == VQ2_DT_F32 ? 512 : 256) : 1];
     // 16-byte aligned: the activation block is written and read with 16-byte LDS accesses
-    extern __shared__ __align__(16) float s_dyn[];  // [activation block (XM != 0)] [item partials]
+    // [activation block (XM != 0)] [item partials | raw activation stage (XM != 0, prologue only)]
+    extern __shared__ __align__(16) float s_dyn[];
     // XM 3 is XM 1 (rotate x in the prologue) with the router built in; XM 4
     // is XM 1 in wide workgroups
     constexpr int XP = (XM == 3 || XM == 4) ? 1 : XM;
@@ -773,6 +874,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     const int64_t n = (int64_t)k_ng * 8;
     float* s_x = s_dyn;
     float* s_part = s_dyn + (XP == 0 ? 0 : (XP == 2 ? k_P : BT) * n);
+    void* const s_stage = s_part;  // the partials are first written after the prologue's last barrier
 
     const int lane = threadIdx.x & 63;
     // wave-uniform (an SGPR value), so per-wave work items, expert ids and
@@ -847,6 +949,9 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     // (The 12-wave XM 4 kernel has at most 168 registers: it holds only the
     // stage-1 centroids through the prologue, and only of fp16 codebooks --
     // more would spill, and a spill reload waits for every gather.)
+    // The raw activation block goes to LDS as soon as its loads arrive (the
+    // index words, issued after them, may still be in flight).
+    if constexpr (XP != 0) stage_x<XP, XT>(a, s_stage, x_rows, n, og, bt0, xpl);
     constexpr bool PRE = XP != 0 && !(XM == 4 && CBT != VQ2_DT_F16);
     constexpr bool PRE_ST1 = !(XM == 4 && S2 == VQ2_S2_U16);
     Cens<CBT, S2, GPL, IT> ce0;
@@ -856,7 +961,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         const int nent = CBT == VQ2_DT_F32 ? 512 : 256;
         for (int i = threadIdx.x; i < nent; i += blockDim.x) s_cb1[i] = ((const u32x4*)a.cb1)[i];
     }
-    if constexpr (XP != 0) build_x<XP, XT>(a, s_x, x_rows, n, og, bt0, xpl);
+    if constexpr (XP != 0) build_x<XP, XT>(a, s_x, s_stage, x_rows, n, xpl);
     if constexpr (S2 == VQ2_S2_U8 || XM != 0) __syncthreads();
 
     float xs[BT][GPL * 8];
