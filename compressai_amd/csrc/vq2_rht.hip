@@ -32,6 +32,7 @@ struct RhtArgs {
     int swiglu;     // x holds [gate | up] of width 2*inter; transform silu(gate)*up
     int64_t inter;  // n of the transform in swiglu mode
     int64_t n;      // transform length (bounds of perm entries)
+    int stage;      // forward with a permutation: the row is staged in LDS (dynamic, n elements)
 };
 
 template <int L>
@@ -152,19 +153,74 @@ __device__ __forceinline__ void rht_load(const RhtArgs& a, int64_t b, int64_t e0
     }
 }
 
+// Pass-0 load with the permutation applied in LDS (forward, no SwiGLU): the
+// thread's permutation and sign words and the whole unpermuted row (16-byte
+// chunks, contiguous) are loaded together, so no global load waits for
+// another; after a barrier the permuted elements are read from LDS.  The row
+// is 16-byte aligned and n * element size a multiple of 16 (checked on the
+// host).
+template <int T, int V, int XT>
+__device__ __forceinline__ void rht_load_staged(const RhtArgs& a, int64_t b, int64_t e0, float (&v)[V], u32x4* s_row,
+                                                int tid)
+{
+    constexpr int ESZ = XT == VQ2_DT_F32 ? 4 : 2;
+    int32_t pw[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) pw[i] = a.perm[e0 + i];
+    int8_t sg[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) sg[i] = a.sign ? a.sign[e0 + i] : (int8_t)1;
+    const u32x4* xr = (const u32x4*)((const char*)a.x + (size_t)(b * a.x_stride) * ESZ);
+    const int64_t nch = a.n * ESZ / 16;
+    // 8 chunks per thread and round, loaded before any is stored (clamped
+    // index: every load is unconditional, only the store is guarded)
+    for (int64_t c0 = tid; c0 < nch; c0 += 8 * T) {
+        u32x4 r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int64_t c = c0 + (int64_t)j * T;
+            r[j] = xr[c < nch ? c : nch - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int64_t c = c0 + (int64_t)j * T;
+            if (c < nch) s_row[c] = r[j];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const bool bad = (uint32_t)pw[i] >= (uint64_t)a.n;  // not a permutation of [0, n): poison
+        const int src = bad ? 0 : pw[i];
+        float val;
+        if constexpr (XT == VQ2_DT_F32) val = ((const float*)s_row)[src];
+        else if constexpr (XT == VQ2_DT_F16) val = f16_bits_to_f32(((const uint16_t*)s_row)[src]);
+        else val = bf16_bits_to_f32(((const uint16_t*)s_row)[src]);
+        v[i] = bad ? __builtin_nanf("") : val * (float)sg[i];
+    }
+}
+
 template <int L>
 __global__ void __launch_bounds__(256) rht_kernel(const RhtArgs a)
 {
     touch_kernargs(a);
     using S = RhtShape<L>;
     __shared__ float lds[S::NP > 1 ? S::HB : 1];
+    extern __shared__ __align__(16) u32x4 s_row[];  // the staged row (a.stage)
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)blockIdx.x * S::HB;
     const int64_t b = blockIdx.y;
     float v[S::V];
 
     const int64_t e0 = base + (int64_t)tid * S::V;
-    if (a.x_dt == VQ2_DT_F32)
+    if (a.stage) {
+        if (a.x_dt == VQ2_DT_F32)
+            rht_load_staged<S::T, S::V, VQ2_DT_F32>(a, b, e0, v, s_row, tid);
+        else if (a.x_dt == VQ2_DT_F16)
+            rht_load_staged<S::T, S::V, VQ2_DT_F16>(a, b, e0, v, s_row, tid);
+        else
+            rht_load_staged<S::T, S::V, VQ2_DT_BF16>(a, b, e0, v, s_row, tid);
+    } else if (a.x_dt == VQ2_DT_F32)
         rht_load<S::V, VQ2_DT_F32>(a, b, e0, v);
     else if (a.x_dt == VQ2_DT_F16)
         rht_load<S::V, VQ2_DT_F16>(a, b, e0, v);
@@ -214,10 +270,13 @@ __global__ void __launch_bounds__(256) rht_kernel(const RhtArgs a)
 }
 
 template <int L>
-static void launch_rht_l(const RhtArgs& a, int64_t nblk, int64_t batch, hipStream_t st)
+static void launch_rht_l(const RhtArgs& a, int64_t nblk, int64_t batch, size_t shm, hipStream_t st)
 {
-    hipLaunchKernelGGL((rht_kernel<L>), dim3((unsigned)nblk, (unsigned)batch), dim3(RhtShape<L>::T), 0, st, a);
+    hipLaunchKernelGGL((rht_kernel<L>), dim3((unsigned)nblk, (unsigned)batch), dim3(RhtShape<L>::T), shm, st, a);
 }
+
+// largest row staged in LDS by the forward permuted transform
+constexpr int64_t RHT_STAGE_BYTES = 32 * 1024;
 
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride, const int32_t* perm,
                const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale, int inverse, int swiglu,
@@ -230,23 +289,27 @@ int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int
         return set_error(VQ2_ERR_ARG, "vq2 rht: hb=%lld must be a power of two in [2, 8192]", (long long)hb);
     if (n % hb) return set_error(VQ2_ERR_ARG, "vq2 rht: n=%lld is not a multiple of hb=%lld", (long long)n, (long long)hb);
     if (batch > 65535 || n / hb > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 rht: grid too large");
-    RhtArgs a{x, x_dt, x_stride, y, y_dt, y_stride, perm, sign, scale, inverse, swiglu, inter, n};
+    const int64_t esz = dt_size(x_dt);
+    const bool stage = !inverse && !swiglu && perm && (uintptr_t)x % 16 == 0 && (x_stride * esz) % 16 == 0 &&
+                       (n * esz) % 16 == 0 && n * esz <= RHT_STAGE_BYTES;
+    RhtArgs a{x, x_dt, x_stride, y, y_dt, y_stride, perm, sign, scale, inverse, swiglu, inter, n, stage ? 1 : 0};
     hipStream_t st = (hipStream_t)stream;
     const int64_t nblk = n / hb;
+    const size_t shm = stage ? (size_t)(n * esz) : 0;
     switch (L) {
-    case 1: launch_rht_l<1>(a, nblk, batch, st); break;
-    case 2: launch_rht_l<2>(a, nblk, batch, st); break;
-    case 3: launch_rht_l<3>(a, nblk, batch, st); break;
-    case 4: launch_rht_l<4>(a, nblk, batch, st); break;
-    case 5: launch_rht_l<5>(a, nblk, batch, st); break;
-    case 6: launch_rht_l<6>(a, nblk, batch, st); break;
-    case 7: launch_rht_l<7>(a, nblk, batch, st); break;
-    case 8: launch_rht_l<8>(a, nblk, batch, st); break;
-    case 9: launch_rht_l<9>(a, nblk, batch, st); break;
-    case 10: launch_rht_l<10>(a, nblk, batch, st); break;
-    case 11: launch_rht_l<11>(a, nblk, batch, st); break;
-    case 12: launch_rht_l<12>(a, nblk, batch, st); break;
-    default: launch_rht_l<13>(a, nblk, batch, st); break;
+    case 1: launch_rht_l<1>(a, nblk, batch, shm, st); break;
+    case 2: launch_rht_l<2>(a, nblk, batch, shm, st); break;
+    case 3: launch_rht_l<3>(a, nblk, batch, shm, st); break;
+    case 4: launch_rht_l<4>(a, nblk, batch, shm, st); break;
+    case 5: launch_rht_l<5>(a, nblk, batch, shm, st); break;
+    case 6: launch_rht_l<6>(a, nblk, batch, shm, st); break;
+    case 7: launch_rht_l<7>(a, nblk, batch, shm, st); break;
+    case 8: launch_rht_l<8>(a, nblk, batch, shm, st); break;
+    case 9: launch_rht_l<9>(a, nblk, batch, shm, st); break;
+    case 10: launch_rht_l<10>(a, nblk, batch, shm, st); break;
+    case 11: launch_rht_l<11>(a, nblk, batch, shm, st); break;
+    case 12: launch_rht_l<12>(a, nblk, batch, shm, st); break;
+    default: launch_rht_l<13>(a, nblk, batch, shm, st); break;
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_hip_error(err, "vq2 rht launch");

@@ -40,6 +40,32 @@ def test_rht_forward_vs_oracle(dev, hb, n, batch, dt):
     assert O.max_rel_err(y.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_rht_forward_staged_and_unaligned_bad_perm(dev, dt, offset):
+    """The forward permuted transform stages 16-byte aligned rows in LDS
+    (offset 0) and gathers through the permutation otherwise (offset 1: rows
+    start 1 element past alignment).  An out-of-range permutation entry
+    poisons its block with NaN on both paths; the other blocks match the
+    oracle."""
+    n, hb, batch = 8192, 2048, 3
+    flat = synth.activations(51, batch * n + 8, dtype=dt)
+    xh = flat[offset:offset + batch * n].view(batch, n)
+    x = flat.to(dev)[offset:offset + batch * n].view(batch, n)  # contiguous, storage offset `offset`
+    perm = synth.permutation(52, n)
+    sign = synth.signs(53, n)
+    bad_slot = 5000  # block 2
+    pbad = perm.clone()
+    pbad[bad_slot] = n + 3
+    y = K.vq_rht(x, pbad.to(dev), sign.to(dev), hb, out_dtype=torch.float32).cpu().numpy()
+    ref = O.rht(xh.float(), perm, sign, hb)
+    blk = bad_slot // hb
+    assert np.all(np.isnan(y[:, blk * hb:(blk + 1) * hb]))
+    keep = np.ones(n, dtype=bool)
+    keep[blk * hb:(blk + 1) * hb] = False
+    assert O.max_rel_err(y[:, keep], ref[:, keep]) < 1e-5
+
+
 @pytest.mark.parametrize("hb,n", [(512, 512), (2048, 6144)])
 def test_rht_inverse_roundtrip(dev, hb, n):
     x = synth.activations(21, (3, n), dtype=torch.float32).to(dev)
