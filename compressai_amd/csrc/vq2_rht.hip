@@ -153,6 +153,14 @@ __device__ __forceinline__ void rht_load(const RhtArgs& a, int64_t b, int64_t e0
     }
 }
 
+// +1 bytes standing in for a missing sign table (repeats every RHT_ONES elements)
+constexpr int RHT_ONES = 8192;
+struct RhtOnes {
+    int8_t v[RHT_ONES];
+    constexpr RhtOnes() : v() { for (int i = 0; i < RHT_ONES; i++) v[i] = 1; }
+};
+static __device__ const __align__(16) RhtOnes g_rht_ones = RhtOnes();
+
 // Pass-0 load with the permutation applied in LDS (forward, no SwiGLU): the
 // thread's permutation and sign words and the whole unpermuted row (16-byte
 // chunks, contiguous) are loaded together, so no global load waits for
@@ -164,12 +172,34 @@ __device__ __forceinline__ void rht_load_staged(const RhtArgs& a, int64_t b, int
                                                 int tid)
 {
     constexpr int ESZ = XT == VQ2_DT_F32 ? 4 : 2;
+    // permutation and sign words with 16-byte loads where V allows (both
+    // tables 16-byte aligned, checked on the host)
     int32_t pw[V];
+    if constexpr (V % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < V; i++) pw[i] = a.perm[e0 + i];
+        for (int q = 0; q < V / 4; q++) {
+            const u32x4 w = *((const u32x4*)(a.perm + e0) + q);
+#pragma unroll
+            for (int k = 0; k < 4; k++) pw[4 * q + k] = (int32_t)w[k];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; i++) pw[i] = a.perm[e0 + i];
+    }
     int8_t sg[V];
+    if constexpr (V % 16 == 0) {
+        // a missing sign table reads +1 bytes (a pointer select, not a branch around the load)
+        const int8_t* sp = a.sign ? a.sign + e0 : g_rht_ones.v + (e0 & (RHT_ONES - 1));
 #pragma unroll
-    for (int i = 0; i < V; i++) sg[i] = a.sign ? a.sign[e0 + i] : (int8_t)1;
+        for (int q = 0; q < V / 16; q++) {
+            const u32x4 w = *((const __attribute__((address_space(1))) u32x4*)sp + q);
+#pragma unroll
+            for (int k = 0; k < 16; k++) sg[16 * q + k] = (int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; i++) sg[i] = a.sign ? a.sign[e0 + i] : (int8_t)1;
+    }
     const u32x4* xr = (const u32x4*)((const char*)a.x + (size_t)(b * a.x_stride) * ESZ);
     const int64_t nch = a.n * ESZ / 16;
     // 8 chunks per thread and round, loaded before any is stored (clamped
@@ -291,7 +321,8 @@ int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int
     if (batch > 65535 || n / hb > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 rht: grid too large");
     const int64_t esz = dt_size(x_dt);
     const bool stage = !inverse && !swiglu && perm && (uintptr_t)x % 16 == 0 && (x_stride * esz) % 16 == 0 &&
-                       (n * esz) % 16 == 0 && n * esz <= RHT_STAGE_BYTES;
+                       (n * esz) % 16 == 0 && n * esz <= RHT_STAGE_BYTES && (uintptr_t)perm % 16 == 0 &&
+                       (uintptr_t)sign % 16 == 0;
     RhtArgs a{x, x_dt, x_stride, y, y_dt, y_stride, perm, sign, scale, inverse, swiglu, inter, n, stage ? 1 : 0};
     hipStream_t st = (hipStream_t)stream;
     const int64_t nblk = n / hb;
