@@ -431,6 +431,26 @@ def test_gemv_rht_fused_wide(dev, n, batch, bpw, xdt):
     assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
 
 
+@pytest.mark.parametrize("n,batch", [(2048, 1), (2048, 2), (6144, 1)])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_gemv_rht_fused_unaligned_activation(dev, n, batch, xdt):
+    """The fused prologue's activation loads (8 contiguous elements per
+    thread) from rows that start one element past 16-byte alignment."""
+    out, bpw = 700, 2
+    cb0 = synth.codebook(9450)
+    m = synth.vq_matrix(9450 + n + batch, out, n, bpw=bpw)
+    flat = synth.activations(9454 + n, batch * n + 8, dtype=xdt)
+    xh = flat[1:1 + batch * n].view(batch, n)
+    x = flat.to(dev)[1:1 + batch * n].view(batch, n)  # contiguous, storage offset 1
+    perm = synth.permutation(9456 + n, n)
+    sign = synth.signs(9455 + n, n)
+    (y,) = K.vq_gemv_rht(x, [(m["idx0"].to(dev), None, m["scale"].to(dev), out)], cb0.to(dev), None, n,
+                         perm.to(dev), sign.to(dev), 2048)
+    xr = O.rht(xh.float(), perm, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], None, cb0, None, m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
 def test_gemv_empty_segments(dev):
     """Zero-row matrices: a launch with no rows is a no-op, and an empty
     segment between non-empty ones (whose row blocks it owns none of) does not
