@@ -702,7 +702,7 @@ __device__ __forceinline__ int seg_of(const GemvArgs& a, int64_t rb)
 // never exceeds the row-block count), so no branch is needed around the
 // loads -- where a path with loads and one without merge, the compiler waits
 // for every outstanding load at the next use of an earlier one.
-template <int S2, int GPL, int IT, bool IN_RANGE = false>
+template <int S2, int GPL, int IT, bool IN_RANGE = false, bool ZERO_PAST = false>
 __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int rows_per_block, int wr, int wr_id,
                                             int rpw, int sub, int64_t g0, bool lane_ok, int64_t e,
                                             Codes<S2, GPL, IT>& cd, bool (&valid)[IT])
@@ -716,7 +716,21 @@ __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int r
         const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
         valid[it] = in_range && row < sg.out_rows && lane_ok;
     }
-    if (!in_range) return;
+    if (!in_range) {
+        // nothing to load; ZERO_PAST: zero codes keep a gather issued ahead
+        // for this task inside the codebooks
+        if constexpr (ZERO_PAST) {
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+#pragma unroll
+                for (int q = 0; q < Codes<S2, GPL, IT>::W0; q++) cd.w0[it][q] = 0;
+#pragma unroll
+                for (int q = 0; q < Codes<S2, GPL, IT>::W1; q++) cd.w1[it][q] = 0;
+                cd.s0[it] = cd.s1[it] = 0;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const int64_t row = row_base + (int64_t)(it * wr + wr_id) * rpw + sub;
@@ -734,7 +748,7 @@ __device__ __forceinline__ void fetch_codes(const GemvArgs& a, int64_t rb, int r
 }
 
 // Codes of task (row block rb, item) for this lane: item = pair * nch + chunk.
-template <int S2, int GPL, int IT, bool IN_RANGE = false>
+template <int S2, int GPL, int IT, bool IN_RANGE = false, bool ZERO_PAST = false>
 __device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int item, int nch, int64_t kc, int og,
                                            int rows_per_block, int wr, int wr_id, int rpw, int sub, int col,
                                            Codes<S2, GPL, IT>& cd, bool (&valid)[IT], int64_t e_rt)
@@ -743,7 +757,7 @@ __device__ __forceinline__ void task_codes(const GemvArgs& a, int64_t rb, int it
     bool bad;
     const int64_t e = pair_expert(a, (int64_t)og * a.P + pj, bad, e_rt);
     const int64_t g0 = c * kc + (int64_t)col * GPL;
-    fetch_codes<S2, GPL, IT, IN_RANGE>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, cd,
+    fetch_codes<S2, GPL, IT, IN_RANGE, ZERO_PAST>(a, rb, rows_per_block, wr, wr_id, rpw, sub, g0, g0 < a.ng && !bad, e, cd,
                                        valid);
 }
 
@@ -838,11 +852,11 @@ __device__ __forceinline__ void block_dot(const GemvArgs& a, const u32x4* s_cb1,
 // register allocation, and the dense launches measured slower with it.
 // XM 4 (the RHT prologue of XM 1 for activations wider than 256 threads x 8
 // values, e.g. the 6144-input down projection) takes up to 12 waves, so its
-// single prologue pass covers n = 6144 per batch column -- up to 8 with fp32
-// (16,16) codebooks, whose 32 centroid words per group would spill at 12.
+// single prologue pass covers n = 6144 per batch column -- up to 8 with bf16
+// or fp32 (16,16) codebooks, whose centroid words would spill at 12.
 constexpr int gemv_max_threads(int s2, int cbt, int xm)
 {
-    return xm == 4 ? (cbt == VQ2_DT_F32 && s2 == VQ2_S2_U16 ? 512 : 768)
+    return xm == 4 ? (cbt != VQ2_DT_F16 && s2 == VQ2_S2_U16 ? 512 : 768)
                    : (xm != 2 ? 256 : (s2 == VQ2_S2_NONE && cbt == VQ2_DT_F16 ? 768 : 512));
 }
 
@@ -1063,7 +1077,12 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     // Several items (expert pairs x K-chunks) per row block: wave wi_id runs
     // its tasks (row block, item) in order and fetches the next task's codes
     // before the current task's gathers; the WI waves' row partials are
-    // reduced through LDS in a fixed order once per row block.
+    // reduced through LDS in a fixed order once per row block.  AHEAD: the
+    // next task's gathers are issued right after the current task's dot
+    // product, before the row block's reduction, so the barriers of that
+    // reduction do not drain the gathers in flight (not for the 12-wave XM 4
+    // kernel or batch tiles above 2, whose registers would spill).
+    constexpr bool AHEAD = XM != 4 && BT <= 2;
     int64_t rbg = blockIdx.x;
     int item = wi_id;
     float fin[IT][BT];
@@ -1071,8 +1090,13 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     for (int it = 0; it < IT; it++)
 #pragma unroll
         for (int b = 0; b < BT; b++) fin[it][b] = 0.0f;
-    // one task; PRE: the first task, whose centroids were gathered before the
-    // prologue (rbg < n_rowblocks and item < items hold for it)
+    // AHEAD: the first task's centroids (PRE: gathered before the prologue;
+    // rbg < n_rowblocks and item < items hold for it)
+    if constexpr (AHEAD && !PRE) gather_block<CBT, S2, GPL, IT, true, true>(a, cd, ce0);
+    else if constexpr (AHEAD && !PRE_ST1) gather_block<CBT, S2, GPL, IT, false, true>(a, cd, ce0);
+    // one task; AHEAD: its centroids are in ce0, and it leaves the next
+    // task's there; PRE: the first task, whose centroids were gathered before
+    // the prologue
     auto mstep = [&](auto pre) {
         int nitem = item + wi;
         int64_t nrbg = rbg;
@@ -1082,8 +1106,8 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         }
         Codes<S2, GPL, IT> nx;
         bool nvalid[IT];
-        task_codes<S2, GPL, IT>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col, nx, nvalid,
-                                e_rt);
+        task_codes<S2, GPL, IT, false, AHEAD>(a, nrbg, nitem, nch, kc, og, rows_per_block, wr, wr_id, rpw, sub, col,
+                                              nx, nvalid, e_rt);
 
         const int pj = item / nch, c = item - (item / nch) * nch;
         const int64_t pair = (int64_t)og * a.P + pj;
@@ -1103,7 +1127,11 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
             cur_item = item;
         }
         float acc[IT][BT];
-        if constexpr (decltype(pre)::value) {
+        if constexpr (AHEAD) {
+            dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
+            // the next task's gathers (zero codes past the last row block)
+            gather_block<CBT, S2, GPL, IT, true, true>(a, nx, ce0);
+        } else if constexpr (decltype(pre)::value) {
             if constexpr (!PRE_ST1) gather_block<CBT, S2, GPL, IT, false, true>(a, cd, ce0);
             dot_block<CBT, S2, GPL, BT, IT>(s_cb1, cd, ce0, valid, xs, acc);
         } else {
@@ -1184,7 +1212,7 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
         item = nitem;
         rbg = nrbg;
     };
-    if constexpr (PRE) mstep(std::true_type{});
+    if constexpr (PRE && !AHEAD) mstep(std::true_type{});
     while (rbg < a.n_rowblocks) mstep(std::false_type{});
 }
 
