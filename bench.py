@@ -534,7 +534,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "configs[1]: dense decoder-layer projection set, batch 1, hidden 2048 (q,k,v,o 2 bpw; "
-                        "gate,up,down 4 bpw; RHT 2048 x3 + 6144); fp16 codebooks/scales/activations, fp32 out",
+                        "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/scales/activations, fp32 out",
             "layers_cycled": d["layers"],
             "bytes_per_step": d["bytes_per_step"],
             "graph_replay": True,
