@@ -904,9 +904,10 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     const int items = k_P * nch;
     const int rows_per_block = IT * rpw * wr;
 
-    // Load order: the prologue's first activation loads (L2-resident), then
-    // the first task's index words (HBM).  The index latency overlaps the
-    // prologue, whose arithmetic waits only for its own loads.
+    // Load order: the prologue's first-iteration loads (permutation and sign
+    // words, the thread's own activation elements; L2-resident), then the
+    // first task's index words (HBM).  The index latency overlaps the
+    // prologue, whose LDS staging waits only for its own loads.
     XProLoad xpl;
     int x_rows = 0;
     if constexpr (XP != 0) {
@@ -953,19 +954,19 @@ __global__ void __launch_bounds__(gemv_max_threads(S2, CBT, XM))
     }
     const int nb = min(BT, a.batch - bt0);
 
-    // Prologue kernels: the first task's gathers are issued as soon as its
-    // index words arrive, before the prologue's arithmetic.  The prologue's
-    // first iteration loads nothing more (its loads went out before the index
-    // words), so its barriers and LDS passes run while the gathers are in
-    // flight.  Unconditional: a branch around them would leave the compiler
-    // unsure which loads are outstanding, and it would then wait for the
-    // gathers inside the prologue.
+    // The unpermuted activation block goes to LDS as soon as its loads
+    // arrive (the index words, issued after them, may still be in flight).
+    if constexpr (XP != 0) stage_x<XP, XT>(a, s_stage, x_rows, n, og, bt0, xpl);
+    // Prologue kernels (PRE): the first task's gathers are issued as soon as
+    // its index words arrive, before the prologue's arithmetic.  The
+    // prologue's first iteration loads nothing more (its loads went out
+    // before the index words), so its LDS reads, barriers and passes run
+    // while the gathers are in flight.  Unconditional: a branch around them
+    // would leave the compiler unsure which loads are outstanding, and it
+    // would then wait for the gathers inside the prologue.
     // (The 12-wave XM 4 kernel has at most 168 registers: it holds only the
     // stage-1 centroids through the prologue, and only of fp16 codebooks --
     // more would spill, and a spill reload waits for every gather.)
-    // The raw activation block goes to LDS as soon as its loads arrive (the
-    // index words, issued after them, may still be in flight).
-    if constexpr (XP != 0) stage_x<XP, XT>(a, s_stage, x_rows, n, og, bt0, xpl);
     constexpr bool PRE = XP != 0 && !(XM == 4 && CBT != VQ2_DT_F16);
     constexpr bool PRE_ST1 = !(XM == 4 && S2 == VQ2_S2_U16);
     Cens<CBT, S2, GPL, IT> ce0;
