@@ -451,6 +451,28 @@ def test_gemv_rht_fused_unaligned_activation(dev, n, batch, xdt):
     assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
 
 
+@pytest.mark.parametrize("n,batch", [(2048, 2), (6144, 1)])
+def test_gemv_rht_fused_bad_perm_entry_poisons(dev, n, batch):
+    """An out-of-range permutation entry in the fused prologue (staged in
+    LDS) reads in bounds and poisons its batch row: every output of that row
+    is NaN; with a valid permutation the same launch matches the oracle."""
+    out = 600
+    cb0 = synth.codebook(9470)
+    m = synth.vq_matrix(9470 + n, out, n, bpw=2)
+    x = synth.activations(9474 + n, (batch, n), dtype=torch.float16)
+    perm = synth.permutation(9476 + n, n)
+    sign = synth.signs(9475 + n, n)
+    pbad = perm.clone()
+    pbad[n // 3] = -7
+    mats = [(m["idx0"].to(dev), None, m["scale"].to(dev), out)]
+    (y,) = K.vq_gemv_rht(x.to(dev), mats, cb0.to(dev), None, n, pbad.to(dev), sign.to(dev), 2048)
+    assert torch.isnan(y).all()
+    (y2,) = K.vq_gemv_rht(x.to(dev), mats, cb0.to(dev), None, n, perm.to(dev), sign.to(dev), 2048)
+    xr = O.rht(x.float(), perm, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], None, cb0, None, m["scale"])
+    assert O.max_rel_err(y2.cpu().numpy(), y64) < TOL
+
+
 def test_gemv_empty_segments(dev):
     """Zero-row matrices: a launch with no rows is a no-op, and an empty
     segment between non-empty ones (whose row blocks it owns none of) does not
