@@ -34,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 matrix-core peak of MI355X
 HIDDEN, Q_OUT, KV_OUT, INTER = 2048, 2048, 512, 6144
 
 
@@ -162,6 +163,28 @@ def time_graph(g, reps, dev):
     return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
 
 
+def time_steps(g_full, L, g_rest, steps, dev):
+    """Replay exactly `steps` layer steps: steps // L replays of the L-layer
+    graph, then the graph of the first steps % L layers.  Returns (ms, host ms)."""
+    import torch
+
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(steps // L):
+        g_full.replay()
+    if steps % L:
+        g_rest.replay()
+    e1.record(st)
+    torch.cuda.synchronize(dev)
+    return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
+
+REPEATS = 5  # timed repetitions; the bench line reports their median
+
+
 def bench_dense(args, dev):
     import torch
 
@@ -169,28 +192,62 @@ def bench_dense(args, dev):
     dl = DenseLayers(L, dev)
     log(f"dense: {L} layer sets, {dl.bytes_per_step * L / 2**30:.2f} GiB of compressed weights")
     g = capture(dl.step, L, dev)
-    warm_reps = max(1, -(-args.warmup // L))
-    time_graph(g, warm_reps, dev)
-    reps = max(1, -(-args.steps // L))
-    steps = reps * L
-    ms, host_ms = time_graph(g, reps, dev)
-    ms_per_step = ms / steps
+    rest = args.steps % L
+    g_rest = capture(dl.step, rest, dev) if rest else None
+    time_graph(g, max(1, -(-args.warmup // L)), dev)  # warm-up: at least W steps
+    runs = [time_steps(g, L, g_rest, args.steps, dev) for _ in range(REPEATS)]
+    per_step = sorted(ms / args.steps for ms, _ in runs)
+    ms_per_step = statistics.median(per_step)
+    host_ms = statistics.median(h for _, h in runs)
     gbps = dl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
-    log(f"dense: {steps} steps in {ms:.3f} ms (host {host_ms:.3f} ms) -> {ms_per_step * 1e3:.2f} us/step, "
+    log(f"dense: {args.steps} steps x {REPEATS} repetitions, median {ms_per_step * 1e3:.2f} us/step "
+        f"(min {per_step[0] * 1e3:.2f}, max {per_step[-1] * 1e3:.2f}; host {host_ms:.3f} ms per repetition) -> "
         f"{gbps:.1f} GB/s")
 
     # dominant kernel: the fused gate/up launch (RHT + two 6144 x 2048 4 bpw
-    # GEMVs), back to back over the layer sets
+    # GEMVs), back to back over the layer sets, on the replay stream
     dom_bytes = 2 * (INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2)
     gd = capture(lambda l: dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h), L, dev)
     time_graph(gd, 2, dev)
     dreps = max(4, 2000 // L)
-    dms, _ = time_graph(gd, dreps, dev)
-    dom_us = dms * 1e3 / (dreps * L)
+    dus = sorted(time_graph(gd, dreps, dev)[0] * 1e3 / (dreps * L) for _ in range(REPEATS))
+    dom_us = statistics.median(dus)
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
     log(f"dominant launch gate+up (RHT + 2 x 4 bpw 6144x2048): {dom_us:.2f} us/launch, {dom_gbps:.1f} GB/s")
-    return dict(steps=steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
-                dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl)
+    return dict(steps=args.steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
+                dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl,
+                spread_us=[round(per_step[0] * 1e3, 3), round(per_step[-1] * 1e3, 3)])
+
+
+def bench_config0(args, dev, copies=1024):
+    """RHT(2048, permutation + signs) + 2 bpw GEMV 2048 x 2048 at
+    batch 1, one fused launch per call, over 1024 distinct matrices (1 GiB)."""
+    import torch
+
+    from compressai_amd import kernels as K, synth
+
+    n = out = 2048
+    g = torch.Generator(device=dev).manual_seed(1000)
+    cb = synth.codebook(1000).to(dev)
+    mats = [(rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)) for _ in range(copies)]
+    x = synth.activations(1004, n, dtype=torch.float16).to(dev)
+    sign = synth.signs(1005, n).to(dev)
+    perm = synth.permutation(1006, n).to(dev)
+    y = torch.empty(out, dtype=torch.float32, device=dev)
+
+    def fwd(l):
+        i0, s = mats[l]
+        K.vq_gemv_rht(x, [(i0, None, s, out)], cb, None, n, perm, sign, 2048, ys=[y])
+
+    gr = capture(fwd, copies, dev)
+    time_graph(gr, 1, dev)
+    us = statistics.median(time_graph(gr, 1, dev)[0] * 1e3 / copies for _ in range(REPEATS))
+    nbytes = out * (n // 8) * 2 + out * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    log(f"config 0 (RHT 2048 + 2 bpw 2048x2048, {copies} copies): {us:.2f} us/call, {gbps:.1f} GB/s")
+    del gr, mats
+    torch.cuda.empty_cache()
+    return {"us": round(us, 3), "gbps": round(gbps, 2), "bytes": nbytes, "copies": copies}
 
 
 def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
@@ -229,8 +286,7 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
         gr = capture(fwd, n_layers, dev)
         time_graph(gr, 3, dev)
         reps = max(5, args.steps // n_layers)
-        ms, _ = time_graph(gr, reps, dev)
-        us = ms * 1e3 / (reps * n_layers)
+        us = statistics.median(time_graph(gr, reps, dev)[0] * 1e3 / (reps * n_layers) for _ in range(REPEATS))
         # distinct experts actually read per layer (routed + shared)
         distinct = []
         for l in range(n_layers):
@@ -239,8 +295,9 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
         bytes_layer = statistics.mean(distinct) * per_expert
         gbps = bytes_layer / (us * 1e-6) / 1e9
         log(f"moe T={T}: {us:.2f} us/layer, {gbps:.1f} GB/s ({statistics.mean(distinct):.1f} experts/layer)")
-        res[T] = dict(us=us, gbps=gbps, bytes=bytes_layer)
+        res[T] = dict(us=us, gbps=gbps, bytes=bytes_layer, cpu_inputs=inputs[0])
         del gr
+    res["cpu_layer"] = layers[0]
     return res
 
 
@@ -307,8 +364,11 @@ def bench_small_m(args, dev):
                 ms, _ = time_graph(gr, reps, dev)
                 us = ms * 1e3 / (reps * copies)
                 key = f"{out}x{n}_{bpw}bpw_M{M}"
-                res[key] = {"us": round(us, 3), "gbps": round(per / (us * 1e-6) / 1e9, 2)}
-                log(f"small-M {key}: {us:.2f} us/call, {res[key]['gbps']:.1f} GB/s")
+                tflops = 2.0 * M * out * n / (us * 1e-6) / 1e12
+                res[key] = {"us": round(us, 3), "gbps": round(per / (us * 1e-6) / 1e9, 2),
+                            "tflops": round(tflops, 2), "mfma_frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 5)}
+                log(f"small-M {key}: {us:.2f} us/call, {res[key]['gbps']:.1f} GB/s, {tflops:.1f} TFLOP/s "
+                    f"({100 * tflops / PEAK_MFMA_F16_TFLOPS:.2f} % of the fp16 MFMA peak)")
             del mats
             torch.cuda.empty_cache()
     sign = synth.signs(5006, 8192).to(dev)
@@ -403,12 +463,37 @@ def bench_paged(args, dev, E=64, steps=200):
 
 
 # -------------------------------------------------------------- CPU baseline
-def cpu_baseline(dl, budget_s=20.0):
-    """The reference CPU path (PackedLinear fallback, fp32) on the host for
-    one configs[1] layer step; median of >= 3 timed runs after 1 warm-up,
-    bounded by budget_s seconds of CPU work."""
+def _cpu_info():
     import platform
 
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def _time_cpu(fn, budget_s):
+    """Median of up to 20 timed runs after one warm-up, at least 3, bounded
+    by about budget_s seconds of CPU work."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    runs = int(max(3, min(20, budget_s / max(first, 1e-3))))
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), runs
+
+
+def cpu_baseline(dl, budget_s=20.0):
+    """The reference CPU path (PackedLinear fallback, fp32) on the host for
+    one configs[1] layer step, on all host cores."""
     import torch
 
     from oracle.ref_cpu_path import CpuRot, packed_linear_fallback
@@ -427,30 +512,48 @@ def cpu_baseline(dl, budget_s=20.0):
             i0, i1, s, out, n = lay[name]
             packed_linear_fallback(x, rot, i0, i1, cb0, cb1 if i1 is not None else None, s)
 
-    t0 = time.perf_counter()
-    step()
-    first = time.perf_counter() - t0
-    runs = int(max(3, min(20, budget_s / max(first, 1e-3))))
-    ts = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
-    med = statistics.median(ts)
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    med, runs = _time_cpu(step, budget_s)
+    cpu = _cpu_info()
     gbps = dl.bytes_per_step / med / 1e9
     log(f"cpu baseline: {med * 1e3:.1f} ms/step median of {runs} on {cores} threads ({cpu}) -> {gbps:.3f} GB/s")
     return {"value": round(gbps, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"configs[1] one layer step (q,k,v,o,gate,up,down + 4 RHTs), reference PackedLinear "
                       f"fp32 fallback restated in torch (oracle/ref_cpu_path.py); median of {runs} runs, "
                       f"{med * 1e3:.1f} ms/step; CPU: {cpu}"}
+
+
+def cpu_moe_baseline(moe, budget_s=10.0):
+    """The reference CPU path of the config-4 MoE layer on the host: router,
+    then per token the vq_moe_parallel_gate_up_cpu / _down_cpu twins over the
+    8 routed + 1 shared expert with fp32 codebooks (as the reference's CPU
+    test feeds them), the two rotations, SwiGLU and the weighted combine
+    (oracle/ref_cpu_path.moe_layer_cpu), for T = 1 and T = 8 on one layer of
+    the benchmark's pool; all host cores."""
+    import torch
+
+    from oracle.ref_cpu_path import CpuRot, moe_layer_cpu
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    layer = moe["cpu_layer"]
+    m = layer.experts_mod
+    cb = m.cb16.float().cpu()
+    gu, gus, dn, dns = (t.cpu() for t in (m.gate_up_idx, m.gate_up_scale, m.down_idx, m.down_scale))
+    gate = layer.shared_gate.cpu()
+    rot_h = CpuRot(m.rot_h.perm.cpu(), m.rot_h.sign.float().cpu(), m.rot_h.hb)
+    rot_i = CpuRot(m.rot_i.perm.cpu(), m.rot_i.sign.float().cpu(), m.rot_i.hb)
+    res = {}
+    for T in (1, 8):
+        h, lg = (t.cpu() for t in moe[T]["cpu_inputs"])
+        med, runs = _time_cpu(lambda: moe_layer_cpu(h, lg, cb, gu, gus, dn, dns, gate, rot_h, rot_i,
+                                                    top_k=layer.top_k, shared_id=layer.n_routed), budget_s)
+        res[f"t{T}"] = {"us_per_layer": round(med * 1e6, 1), "runs": runs,
+                        "gpu_speedup": round(med * 1e6 / moe[T]["us"], 1)}
+        log(f"cpu moe baseline T={T}: {med * 1e3:.2f} ms/layer median of {runs} on {cores} threads")
+    return {"unit": "us per MoE layer", "cores": cores, "kind": "port", "cpu": _cpu_info(),
+            "sample": "configs[3] one MoE layer (router top-8 of 256 + shared expert, 2 bpw experts), "
+                      "reference vq_moe_parallel_*_cpu composition restated in torch (oracle/ref_cpu_path.py), "
+                      "fp32 codebook", **res}
 
 
 def traffic_from_profiles():
@@ -518,6 +621,8 @@ def main():
     up = None if args.no_small_m else bench_unpack(args, dev)
     pgd = None if args.no_moe else bench_paged(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(d["dense"])
+    cpu_moe = None if (args.no_cpu or moe is None) else cpu_moe_baseline(moe)
+    c0 = bench_config0(args, dev)
 
     rec = {
         "metric": metric_name(),
@@ -547,6 +652,9 @@ def main():
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "config0": c0,
+        "dense_spread_us": d["spread_us"],
+        "timing": f"median of {REPEATS} timed repetitions of the steps (HIP events on the replay stream)",
         "small_m": sm,
         "unpack_fixed": up,
         "paged_moe_t1": pgd,
@@ -558,10 +666,13 @@ def main():
             "unit": "GB/s",
             "frac": round(d["dom_gbps"] / PEAK_HBM_GBPS, 5),
             "traffic": traffic_from_profiles(),
+            "traffic_source": "profiles/gemv4_gate_pmc.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                              "bench.py --only dominant, scaled by a 64 MiB copy (stored profile, not this run)",
             "us_per_launch": round(d["dom_us"], 3),
             "algorithmic_bytes_per_launch": d["dom_bytes"],
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_moe": cpu_moe,
     }
     print(json.dumps(rec), flush=True)
 

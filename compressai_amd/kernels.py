@@ -135,12 +135,20 @@ def _ids(t: torch.Tensor) -> tuple[torch.Tensor, int]:
 # --------------------------------------------------------------- dense GEMV
 def _planes(i0, i1, cb0, cb1, scale, out, n):
     """Validate one matrix's index planes, codebooks and scales; returns
-    (i0, i1, s2_kind) with the planes viewed as the kernels read them."""
+    (i0, i1, s2_kind) with the planes viewed as the kernels read them.
+    Checks only shapes, dtypes and layout (no device access), so the kernels
+    never index past a plane, a codebook or the scales."""
+    if n % 8:
+        raise Vq2Error(f"n={n} must be a multiple of 8")
     i0 = _idx16(i0, "i0")
     if i0.numel() != out * (n // 8):
         raise Vq2Error(f"i0 has {i0.numel()} codes, expected out*n/8 = {out * (n // 8)}")
     s2 = _lib.S2_NONE
     if i1 is not None:
+        if cb1 is None:
+            raise Vq2Error("a stage-2 plane needs its codebook cb1")
+        if cb1.dim() != 2 or cb1.shape[-1] != 8:
+            raise Vq2Error(f"cb1 must be [K, 8], got {tuple(cb1.shape)}")
         if i1.dtype == torch.uint8:
             s2 = _lib.S2_U8
             if cb1.shape[0] < 256:
@@ -157,12 +165,38 @@ def _planes(i0, i1, cb0, cb1, scale, out, n):
         if cb1.dtype != cb0.dtype:
             raise Vq2Error("cb0 and cb1 must share a dtype")
     _contig(cb0, "cb0")
-    if cb0.shape[-1] != 8 or cb0.shape[0] < 65536:
+    if cb0.dim() != 2 or cb0.shape[-1] != 8 or cb0.shape[0] < 65536:
         raise Vq2Error(f"cb0 must be [65536, 8], got {tuple(cb0.shape)}")
+    _dt(cb0, "cb0")
     _contig(scale, "scale")
+    _dt(scale, "scale")
     if scale.numel() != out:
         raise Vq2Error(f"scale has {scale.numel()} entries, expected {out}")
     return i0, i1, s2
+
+
+def check_gemv_rht_mats(mats, cb0, cb1, n):
+    """Validate the matrices of one vq_gemv_rht launch: every matrix passes
+    the single-matrix checks (planes, codebooks, scales) and all of them
+    share the stage-2 kind and the scale dtype, which the launch passes once
+    for every segment.  Returns (s2_kind, [(i0, i1, scale, out_rows)])."""
+    if not 1 <= len(mats) <= 4:
+        raise Vq2Error("vq_gemv_rht: 1..4 matrices per launch")
+    s2 = sdt = None
+    checked = []
+    for k, (i0, i1, scale, out_rows) in enumerate(mats):
+        out_rows = int(out_rows)
+        i0v, i1v, s2k = _planes(i0, i1, cb0, cb1, scale, out_rows, n)
+        if s2 is None:
+            s2, sdt = s2k, scale.dtype
+        elif s2k != s2:
+            raise Vq2Error(f"vq_gemv_rht: matrix {k} has another stage-2 kind than matrix 0 "
+                           "(all matrices of a launch share one cfg)")
+        elif scale.dtype != sdt:
+            raise Vq2Error(f"vq_gemv_rht: matrix {k} has {scale.dtype} scales, matrix 0 {sdt} "
+                           "(the scales of a launch share a dtype)")
+        checked.append((i0v, i1v, scale, out_rows))
+    return s2, checked
 
 
 def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
@@ -189,8 +223,12 @@ def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bflo
 
 
 # Split-K partials of vq_gemm_small_m, one buffer per (device, stream):
-# launches on one stream run in order, so they can share it.
+# launches on one stream run in order, so they can share it.  The buffers
+# only grow, and a buffer that a larger one replaces is kept alive until the
+# process ends: a HIP graph captured earlier holds its raw address and writes
+# into it on every replay.
 _WS: dict = {}
+_WS_RETIRED: list = []
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -199,6 +237,8 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor | None:
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _WS_RETIRED.append(buf)
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _WS[key] = buf
     return buf
@@ -267,40 +307,28 @@ def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=N
     launch of the matrices.  x [n] or [B, n] (B <= 2); mats: list of
     (i0, i1 or None, scale, out_rows) sharing one cfg.  Returns the list of
     outputs ([out] or [B, out])."""
-    dev = _dev(x, cb0, cb1, perm, sign)
     n = int(n)
+    s2, mats = check_gemv_rht_mats(mats, cb0, cb1, n)
+    dev = _dev(x, cb0, cb1, perm, sign, *[t for m in mats for t in m[:3]])
     x2 = _contig(x, "x").reshape(-1, n)
     B = x2.shape[0]
-    if not 1 <= len(mats) <= 4:
-        raise Vq2Error("vq_gemv_rht: 1..4 matrices per launch")
-    s2 = _lib.S2_NONE
-    if mats[0][1] is not None:
-        s2 = _lib.S2_U8 if mats[0][1].dtype == torch.uint8 else _lib.S2_U16
-    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != n):
-        raise Vq2Error("perm must be int32 [n]")
-    if sign is not None and (sign.dtype != torch.int8 or sign.numel() != n):
-        raise Vq2Error("sign must be int8 [n]")
+    for t, nm, dt in ((perm, "perm", torch.int32), (sign, "sign", torch.int8)):
+        if t is not None and (t.dtype != dt or t.numel() != n or not t.is_contiguous()):
+            raise Vq2Error(f"{nm} must be a contiguous {dt} [n]")
+    if ys is not None and len(ys) != len(mats):
+        raise Vq2Error("vq_gemv_rht: one output per matrix")
     segs = (_lib.Seg * len(mats))()
     outs = []
     for k, (i0, i1, scale, out_rows) in enumerate(mats):
-        _dev(i0, i1, scale)
-        i0 = _idx16(i0, "i0")
-        if i1 is not None and i1.dtype != torch.uint8:
-            i1 = _idx16(i1, "i1")
-        if (i1 is None) != (s2 == _lib.S2_NONE):
-            raise Vq2Error("vq_gemv_rht: all matrices of a launch share one cfg")
-        if i0.numel() != int(out_rows) * (n // 8) or scale.numel() != int(out_rows):
-            raise Vq2Error("vq_gemv_rht: matrix shape does not match out_rows x n")
-        _contig(scale, "scale")
-        if i1 is not None:
-            _contig(i1, "i1")
-        y = ys[k] if ys is not None else torch.empty((B, int(out_rows)) if x.dim() == 2 else (int(out_rows),),
+        y = ys[k] if ys is not None else torch.empty((B, out_rows) if x.dim() == 2 else (out_rows,),
                                                       dtype=out_dtype, device=dev)
         _contig(y, "y")
-        segs[k] = _lib.Seg(_p(i0), _p(i1), _p(scale), _p(y), int(out_rows), int(out_rows))
+        if y.numel() != B * out_rows or y.device != dev:
+            raise Vq2Error(f"vq_gemv_rht: output {k} must hold [B, out_rows] = [{B}, {out_rows}] on {dev}")
+        segs[k] = _lib.Seg(_p(i0), _p(i1), _p(scale), _p(y), out_rows, out_rows)
         outs.append(y)
-    if scale.dtype != mats[0][2].dtype or any(o.dtype != outs[0].dtype for o in outs):
-        raise Vq2Error("vq_gemv_rht: scales and outputs of a launch share a dtype")
+    if any(o.dtype != outs[0].dtype for o in outs):
+        raise Vq2Error("vq_gemv_rht: the outputs of a launch share a dtype")
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
     if B * n > FUSED_RHT_MAX_VALS:
         x2 = vq_rht(x2, perm, sign, hb, sc, out_dtype=torch.float32)

@@ -36,9 +36,41 @@ from .rot import get_rot
 
 
 class ResidentMoEExperts(nn.Module):
-    def __init__(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h=None, rot_i=None,
-                 act_dtype=torch.float32, out_dtype=None):
+    """Resident expert pool of one MoE layer.
+
+    ``ResidentMoEExperts(q_gate_up, q_down, cb16, device)`` is the
+    reference's constructor (``PackedMoEExpertUniversal``,
+    vq2/load_and_test_full_35b.py:31-47): the quantized dicts' stage-1 index
+    planes are viewed as the pools ``[E, 2I, H/8]`` / ``[E, H, I/8]`` and their
+    row scales rounded to bf16, exactly as the reference does.  ``from_pools``
+    takes ready device pools (any scale dtype, kept as given)."""
+
+    def __init__(self, q_gate_up, q_down, cb16, device="cuda", *, num_experts=256, hidden_dim=2048,
+                 intermediate_dim=512, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=None):
         super().__init__()
+        E, H, I = int(num_experts), int(hidden_dim), int(intermediate_dim)
+        gu_idx = q_gate_up["idx"][0]
+        dn_idx = q_down["idx"][0]
+        if gu_idx.numel() != E * 2 * I * (H // 8) or dn_idx.numel() != E * H * (I // 8):
+            raise K.Vq2Error(f"quantized expert planes of {gu_idx.numel()} / {dn_idx.numel()} codes do not hold "
+                             f"{E} experts of gate_up [{2 * I}, {H}] / down [{H}, {I}]")
+        self._setup(gu_idx.view(E, 2 * I, H // 8).to(device),
+                    q_gate_up["scale"].view(E, 2 * I).to(device=device, dtype=torch.bfloat16),
+                    dn_idx.view(E, H, I // 8).to(device),
+                    q_down["scale"].view(E, H).to(device=device, dtype=torch.bfloat16),
+                    cb16, rot_h, rot_i, act_dtype, out_dtype)
+
+    @classmethod
+    def from_pools(cls, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h=None, rot_i=None,
+                   act_dtype=torch.float32, out_dtype=None):
+        """Pools already on the device: gate_up_idx [E, 2I, H/8], down_idx
+        [E, H, I/8] (int16), scales [E, 2I] / [E, H] in any float dtype."""
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self._setup(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype)
+        return self
+
+    def _setup(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype):
         E, gu_rows, ng_h = gate_up_idx.shape
         E2, hidden, ng_i = down_idx.shape
         if E2 != E or gu_rows != 2 * ng_i * 8 or hidden != ng_h * 8:
@@ -91,8 +123,8 @@ class MoELayer(nn.Module):
     def __init__(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, shared_gate, top_k=8,
                  n_routed=None, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=torch.float32):
         super().__init__()
-        self.experts_mod = ResidentMoEExperts(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h,
-                                              rot_i, act_dtype, out_dtype)
+        self.experts_mod = ResidentMoEExperts.from_pools(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16,
+                                                         rot_h, rot_i, act_dtype, out_dtype)
         self.n_routed = gate_up_idx.shape[0] - 1 if n_routed is None else int(n_routed)
         self.top_k = int(top_k)
         self.shared_gate = shared_gate
@@ -126,3 +158,8 @@ class MoELayer(nn.Module):
         act = K.vq_swiglu_rht(y_gu, I, m.rot_i._perm32, m.rot_i._sign8, m.rot_i.hb, m.rot_i.scale)
         return K.vq_moe_down_combine(act, ids, w, m.down_idx, m.cb16, m.down_scale, OUT=m.hidden_dim, NG=I // 8,
                                      out_dtype=m.out_dtype or torch.float32)
+
+
+# the reference's name for the resident expert module
+# (vq2/load_and_test_full_35b.py:26, vq2/inferencia_35b.py:22)
+PackedMoEExpertUniversal = ResidentMoEExperts

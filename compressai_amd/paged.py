@@ -27,8 +27,10 @@ buffer and hands the kernels a slot list built element by element, here:
   host-side paging decision needs;
 * the slot ids of all (token, expert) pairs go to the device in one copy, and
   the two grouped launches of ``ResidentMoEExperts`` (gate_up with the RHT,
-  SwiGLU + RHT + down + combine) run unchanged on the slot pool -- the pool
-  keeps the container's fp16 scales, the kernels read them directly.
+  SwiGLU + RHT + down + combine) run unchanged on the slot pool.  The pool
+  holds the row scales in bf16, rounded from the container's fp16 as the
+  reference's pools do (vq2/paged_runtime.py:140-173, 340-342);
+  ``scale_dtype=None`` keeps the fp16 scales.
 
 Promoted 3 bpw experts (``expert_modes["layer:expert"] == 3``, written by
 tools/build_mixed_b2_container.py:50-82, 154-165): their index entries hold
@@ -206,14 +208,16 @@ class ExpertPager:
     """Device pool of `capacity` expert slots of one layer, filled from a
     Vq2mStore, LRU replacement (vq2/paged_runtime.py:415-437)."""
 
-    def __init__(self, store: Vq2mStore, layer: int, capacity: int, device, staging: int = 16):
+    def __init__(self, store: Vq2mStore, layer: int, capacity: int, device, staging: int = 16,
+                 scale_dtype=torch.bfloat16):
         self.store, self.layer, self.capacity = store, int(layer), int(capacity)
         self.device = torch.device(device)
         s = store
+        sdt = scale_dtype or torch.float16
         self.pool_gu_idx = torch.empty((capacity, s.gu_rows, s.gu_cols), dtype=torch.int16, device=self.device)
-        self.pool_gu_scale = torch.empty((capacity, s.gu_rows), dtype=torch.float16, device=self.device)
+        self.pool_gu_scale = torch.empty((capacity, s.gu_rows), dtype=sdt, device=self.device)
         self.pool_dn_idx = torch.empty((capacity, s.dn_rows, s.dn_cols), dtype=torch.int16, device=self.device)
-        self.pool_dn_scale = torch.empty((capacity, s.dn_rows), dtype=torch.float16, device=self.device)
+        self.pool_dn_scale = torch.empty((capacity, s.dn_rows), dtype=sdt, device=self.device)
         self.slot_of: OrderedDict[int, int] = OrderedDict()  # expert -> slot, least recently used first
         self.free = list(range(capacity - 1, -1, -1))
         self.hits = self.misses = 0
@@ -304,9 +308,9 @@ class PagedMoEExperts(torch.nn.Module):
     the layer holds promoted 3 bpw experts."""
 
     def __init__(self, layer: int, store: Vq2mStore, cb16, capacity: int = 96, device="cuda", staging: int = 16,
-                 act_dtype=torch.float32, out_dtype=None, cb8=None):
+                 act_dtype=torch.float32, out_dtype=None, cb8=None, scale_dtype=torch.bfloat16):
         super().__init__()
-        self.pager = ExpertPager(store, layer, capacity, device, staging)
+        self.pager = ExpertPager(store, layer, capacity, device, staging, scale_dtype)
         self.cb16 = cb16
         self.hidden_dim = store.gu_cols * 8
         self.intermediate_dim = store.dn_cols * 8
@@ -327,6 +331,9 @@ class PagedMoEExperts(torch.nn.Module):
                                  "stage-2 codebook")
             recs = [store.read_promoted(layer, e) for e in promoted]
             self.pro = {k: torch.stack([r[k] for r in recs]).to(dev) for k in recs[0]}
+            if scale_dtype is not None:
+                for k in ("gu_s", "dn_s"):
+                    self.pro[k] = self.pro[k].to(scale_dtype)
             self.cb8 = cb8
 
     def _run(self, h, ids_d, w_d, pool, accumulate_into=None):

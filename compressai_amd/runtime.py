@@ -44,7 +44,12 @@ def vq_matmul(xr, i0, i1, cb0, cb1, scale, out, n, out_dtype, y=None):
 
 
 class PackedLinear(nn.Module):
-    def __init__(self, shape, cfg, tag, idx, scale, cbs, device, act_dtype=torch.float32):
+    """``scale_dtype``: the row scales are held in bf16 by default, as the
+    reference rounds them at construction (vq2/runtime.py:78); ``None`` keeps
+    the given dtype (e.g. the container's fp16 scales, one rounding fewer)."""
+
+    def __init__(self, shape, cfg, tag, idx, scale, cbs, device, act_dtype=torch.float32,
+                 scale_dtype=torch.bfloat16):
         super().__init__()
         self.out, self.n = int(shape[0]), int(shape[1])
         self.cfg, self.tag = tuple(cfg), tag
@@ -53,7 +58,8 @@ class PackedLinear(nn.Module):
         self.keys = [cfg_key(self.cfg, i) for i in range(len(self.cfg))]
         for i, a in enumerate(idx):
             self.register_buffer(f"idx{i}", a.to(device).contiguous(), persistent=False)
-        self.register_buffer("scale", scale.to(device=device).contiguous(), persistent=False)
+        self.register_buffer("scale", scale.to(device=device, dtype=scale_dtype or scale.dtype).contiguous(),
+                             persistent=False)
         self._cbs = [cbs]
         self.rot = get_rot(tag, self.n, device)
         self.act_dtype = act_dtype

@@ -1,0 +1,159 @@
+"""GPU checks of the drop-in modules and host plumbing: PackedLinear's bf16
+scales, the reference constructor of the resident expert module, FastRot's
+cache, the device rotation tables against the golden fixture, and split-K
+workspaces that outlive the graphs captured on them.  Every launch goes
+through libvq2_amd.so; the references are the CPU oracle (oracle/)."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from compressai_amd import kernels as K, synth
+from oracle import vq2_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+GOLDEN = Path(__file__).resolve().parent / "golden" / "rot_tables.npz"
+
+
+def _rot_np(rot):
+    return rot.perm.cpu().numpy(), rot.sign.float().cpu().numpy().astype(np.int8)
+
+
+def test_packed_linear_rounds_scales_to_bf16(dev):
+    """PackedLinear holds bf16 row scales (vq2/runtime.py:78): its output is
+    the oracle's with bf16-rounded scales, and measurably not the oracle's
+    with the container's fp16 scales."""
+    from compressai_amd.runtime import PackedLinear
+
+    n, out = 2048, 2048
+    cbs = {"16": synth.codebook(9320).to(dev)}
+    m = synth.vq_matrix(9320, out, n, bpw=2)
+    lin = PackedLinear((out, n), (16,), "layers.0.self_attn.o_proj", [m["idx0"]], m["scale"], cbs, dev)
+    assert lin.scale.dtype == torch.bfloat16
+    x = synth.activations(9321, (1, n), dtype=torch.float32)
+    y = lin(x.to(dev), out_dtype=torch.float32).cpu().numpy()
+    perm, sign = _rot_np(lin.rot)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    _, y_bf = O.vq_gemv(xr, m["idx0"], None, cbs["16"].cpu(), None, m["scale"].to(torch.bfloat16))
+    _, y_h = O.vq_gemv(xr, m["idx0"], None, cbs["16"].cpu(), None, m["scale"])
+    assert O.max_rel_err(y, y_bf) < 2e-5
+    assert O.max_rel_err(y, y_h) > 1e-4
+
+
+def test_resident_experts_reference_constructor(dev):
+    """PackedMoEExpertUniversal(q_gate_up, q_down, cb16, device) built from
+    quantized dicts shaped as the reference reads them (256 experts,
+    idx[0] viewed as [256, 1024, 256] / [256, 2048, 64], bf16 scales,
+    vq2/load_and_test_full_35b.py:31-47), T = 1 and 3, against the oracle."""
+    from compressai_amd.moe import PackedMoEExpertUniversal
+
+    E = 256
+    gu = synth.indices16(9330, (E * 1024, 256))
+    dn = synth.indices16(9331, (E * 2048, 64))
+    q_gu = {"idx": [gu], "scale": synth.scales(9332, E * 1024), "cfg": (16,), "tag": "moe_gate_up"}
+    q_dn = {"idx": [dn], "scale": synth.scales(9333, E * 2048), "cfg": (16,), "tag": "moe_down"}
+    cb = synth.codebook(9334)
+    mod = PackedMoEExpertUniversal(q_gu, q_dn, cb.to(dev), dev)
+    ph, sh = _rot_np(mod.rot_h)
+    pi, si = _rot_np(mod.rot_i)
+    gu3, dn3 = gu.view(E, 1024, 256), dn.view(E, 2048, 64)
+    gus = q_gu["scale"].view(E, 1024).to(torch.bfloat16)
+    dns = q_dn["scale"].view(E, 2048).to(torch.bfloat16)
+    for T in (1, 3):
+        h = synth.activations(9335 + T, (T, 2048), dtype=torch.bfloat16)
+        ids = torch.stack([torch.randperm(E, generator=synth.gen(9340 + t))[:8] for t in range(T)])
+        w = torch.softmax(synth.activations(9345 + T, (T, 8)).float(), -1)
+        out = mod(h.to(dev), ids.to(dev), w.to(dev))
+        assert out.shape == (T, 2048) and out.dtype == torch.bfloat16
+        ref = O.moe_experts(h, ids.numpy(), w.numpy(), lambda e: (gu3[e], None, gus[e], dn3[e], None, dns[e]),
+                            cb, None, ph, sh.astype(np.float32), pi, si.astype(np.float32))
+        # one rounding of the fp32 result to bf16: within one bf16 ulp of each element
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-5 * np.abs(ref).max()), T
+
+
+def test_fastrot_cache_and_deferred_scale(dev):
+    """FastRot (vq2/runtime.py:37-66): the unnormalised RHT (scale 1), the
+    same tensor returned while the input is unchanged, recomputed after an
+    in-place write; VQ GEMV with rs = RS on its output equals the normalised
+    RHT followed by the GEMV."""
+    from compressai_amd.rot import RS, FastRot, get_rot
+
+    n = 4096
+    rot = get_rot("layers.3.self_attn.q_proj", n, dev)
+    fr = FastRot.get("layers.3.self_attn.q_proj", n, dev, rot, out_dtype=torch.float32)
+    assert FastRot.get("layers.3.self_attn.q_proj", n, dev, rot) is fr
+    perm, sign = _rot_np(rot)
+    x = synth.activations(9350, n, dtype=torch.float32).to(dev)
+    y1 = fr(x)
+    ref1 = O.rht(x.cpu(), perm, sign, 2048, scale=1.0)
+    assert O.max_rel_err(y1.cpu().numpy(), ref1) < 1e-5
+    assert fr(x) is y1                      # cache hit: same input, same version
+    x.mul_(-0.5)                            # in-place write bumps the version
+    y2 = fr(x)
+    assert y2 is not y1
+    assert O.max_rel_err(y2.cpu().numpy(), O.rht(x.cpu(), perm, sign, 2048, scale=1.0)) < 1e-5
+    m = synth.vq_matrix(9351, 1024, n, bpw=2)
+    cb = synth.codebook(9352)
+    y = K.vq_gemv_16(y2, m["idx0"].to(dev), cb.to(dev), m["scale"].to(dev), 1024, n, RS, out_dtype=torch.float32)
+    xr = O.rht(x.cpu(), perm, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], None, cb, None, m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+
+
+def test_rot_tables_on_device_match_golden(dev):
+    """The rotations built on this machine (get_rot on the GPU) hold the
+    permutation and signs of the committed fixture."""
+    from compressai_amd.rot import get_rot
+
+    G = np.load(GOLDEN)
+    for tag, n in (("moe_expert_2048", 2048), ("moe_expert_512", 512), ("layers.0.mlp.down_proj", 6144)):
+        rot = get_rot(tag, n, dev)
+        assert np.array_equal(rot.perm.cpu().numpy(), G[f"{tag}|{n}|perm"].astype(np.int64)), tag
+        assert np.array_equal(rot._sign8.cpu().numpy(), G[f"{tag}|{n}|sign"]), tag
+
+
+def test_small_m_workspace_outlives_captured_graph(dev):
+    """A graph captured on the split-K workspace keeps working after a larger
+    launch replaces that workspace: the replaced buffer stays alive, so the
+    first graph's replays still equal its eager result."""
+    cb = synth.codebook(9360).to(dev)
+    ma = synth.vq_matrix(9361, 512, 2048, bpw=2)
+    mb = synth.vq_matrix(9362, 6144, 2048, bpw=2)
+    xa = synth.activations(9363, (8, 2048), dtype=torch.float16).to(dev)
+    xb = synth.activations(9364, (64, 2048), dtype=torch.float16).to(dev)
+    ia, sa = ma["idx0"].to(dev), ma["scale"].to(dev)
+    ib, sb = mb["idx0"].to(dev), mb["scale"].to(dev)
+    ya = torch.empty((8, 512), dtype=torch.float32, device=dev)
+    yb = torch.empty((64, 6144), dtype=torch.float32, device=dev)
+    fa = lambda: K.vq_gemm_small_m(xa, ia, None, cb, None, sa, 512, 2048, y=ya)
+    fb = lambda: K.vq_gemm_small_m(xb, ib, None, cb, None, sb, 6144, 2048, y=yb)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        fa()
+        ref_a = ya.clone()
+        ga = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ga, stream=s):
+            fa()
+        fb()                                  # needs a larger workspace on the same stream
+        ref_b = yb.clone()
+        gb = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gb, stream=s):
+            fb()
+    torch.cuda.synchronize(dev)
+    for r in range(3):
+        ya.zero_()
+        yb.zero_()
+        ga.replay()
+        gb.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(ya, ref_a), r
+        assert torch.equal(yb, ref_b), r
+        junk = torch.randn(1 << 20, device=dev)   # eager allocations between the replays
+        del junk
+    _, y64 = O.vq_gemv(xa.cpu(), ma["idx0"], None, cb.cpu(), None, ma["scale"])
+    assert max(O.max_rel_err(ref_a[b].cpu().numpy(), y64[b]) for b in range(8)) < TOL

@@ -332,7 +332,7 @@ def test_resident_experts_drop_in_forward(dev):
     E = 16
     cb = synth.codebook(4400)
     gu, gus, dn, dns = _pools(4400, E)
-    mod = ResidentMoEExperts(*_cuda(gu, gus, dn, dns, cb, dev=dev))
+    mod = ResidentMoEExperts.from_pools(*_cuda(gu, gus, dn, dns, cb, dev=dev))
     h = synth.activations(4404, (2, 2048), dtype=torch.bfloat16)
     ids = torch.tensor([[1, 4, 9, 15, 0, 2, 3, 8], [15, 14, 1, 0, 5, 6, 7, 4]], dtype=torch.int64)
     w = torch.softmax(synth.activations(4405, (2, 8)).float(), -1).to(torch.bfloat16)
@@ -509,7 +509,7 @@ def test_packed_linear_forward(dev):
         x = synth.activations(9304 + B, (B, n), dtype=torch.float32)
         y = lin(x.to(dev))
         xr = O.rht(x, lin.rot.perm.cpu(), lin.rot.sign.float().cpu().numpy().astype(np.int8), lin.rot.hb)
-        _, y64 = O.vq_gemv(xr.astype(np.float32), m["idx0"], m["idx1"], cbs["16"], cbs["16_16"], m["scale"])
+        _, y64 = O.vq_gemv(xr.astype(np.float32), m["idx0"], m["idx1"], cbs["16"], cbs["16_16"], lin.scale.cpu())
         assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
     head = PackedLMHead(lin)
     idx, val = head.argmax(synth.activations(9310, (2, n), dtype=torch.float32).to(dev))
@@ -626,7 +626,8 @@ def test_packed_linear_small_m_path(dev, B):
     x = synth.activations(7404, (B, n), dtype=torch.float32)
     y = lin(x.to(dev), out_dtype=torch.float32).cpu().numpy()
     xr = O.rht(x, lin.rot.perm.cpu(), lin.rot.sign.float().cpu().numpy().astype(np.int8), lin.rot.hb)
-    _, y64 = O.vq_gemv(xr.astype(np.float32), m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu(), m["scale"])
+    _, y64 = O.vq_gemv(xr.astype(np.float32), m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu(),
+                       lin.scale.cpu())
     assert y.shape == (B, out)
     assert _rowwise_err(y, y64) < TOL
 
@@ -751,7 +752,10 @@ def test_paged_experts_match_resident_pool(dev, tmp_path):
     cb = synth.codebook(4601).to(dev)
     store = paged.Vq2mStore(path)
     pg = paged.PagedMoEExperts(0, store, cb, capacity=6, device=dev, staging=3, out_dtype=torch.float32)
-    res = ResidentMoEExperts(gui.to(dev), gus.to(dev), dni.to(dev), dns.to(dev), cb, out_dtype=torch.float32)
+    # the paged pool holds bf16-rounded scales (as the reference's pools): same for the resident one
+    bf = torch.bfloat16
+    res = ResidentMoEExperts.from_pools(gui.to(dev), gus.to(dev, bf), dni.to(dev), dns.to(dev, bf), cb,
+                                        out_dtype=torch.float32)
     for step in range(8):
         T = 1 + step % 3
         ids = torch.stack([torch.randperm(E, generator=g)[:2] for _ in range(T)]).to(torch.int64)
@@ -777,7 +781,7 @@ def test_single_pair_combine_applies_weight(dev, T):
     E = 6
     cb = synth.codebook(4900)
     gu, gus, dn, dns = _pools(4900, E)
-    mod = ResidentMoEExperts(*_cuda(gu, gus, dn, dns, cb, dev=dev), out_dtype=torch.float32)
+    mod = ResidentMoEExperts.from_pools(*_cuda(gu, gus, dn, dns, cb, dev=dev), out_dtype=torch.float32)
     h = synth.activations(4904, (T, 2048))
     ids = torch.tensor([[2], [5], [0]][:T], dtype=torch.int32)
     w = torch.tensor([[0.37], [-1.5], [2.25]][:T], dtype=torch.float32)
@@ -820,9 +824,10 @@ def test_paged_promoted_experts_vs_oracle(dev, tmp_path):
     ph, sh = _rot_np(pg.rot_h)
     pi, si = _rot_np(pg.rot_i)
 
-    def experts(e):
+    def experts(e):  # the pools hold bf16-rounded scales, as the reference's
         p = e in pro
-        return gui[e], gu1[e] if p else None, gus[e], dni[e], dn1[e] if p else None, dns[e]
+        bf = torch.bfloat16
+        return gui[e], gu1[e] if p else None, gus[e].to(bf), dni[e], dn1[e] if p else None, dns[e].to(bf)
 
     steps = [[[3, 5]], [[3, 7], [1, 2], [10, 4]], [[7, 10], [3, 7]], [[3, 5, 6]], [[5, 6], [0, 1]], [[10, 0]]]
     for i, rows in enumerate(steps):
