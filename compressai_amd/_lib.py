@@ -19,6 +19,7 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 S2_NONE, S2_U8, S2_U16 = 0, 1, 2
 ID_I32, ID_I64 = 0, 1
 OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 16 << 20  # VQ2_NOALLOC_SCRATCH_BYTES
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
@@ -48,6 +49,8 @@ SIGNATURES = {
                                  _vp, ctypes.c_size_t, _vp, _vp, _vp], _i32),
     "vq2_gemm_small_m": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
                           _i64, _i64, _f32, _vp, ctypes.c_size_t, _vp], _i32),
+    "vq2_gemm_small_m_noalloc": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64,
+                                  _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_grouped": ([_vp, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _i32,
                          _i64, _i64, _i64, _f32, _vp], _i32),
     "vq2_moe_down_combine": ([_vp, _i32, _vp, _i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i32,

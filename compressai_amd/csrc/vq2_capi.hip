@@ -136,24 +136,24 @@ size_t vq2_gemm_small_m_workspace(int64_t batch, int64_t out_rows, int64_t n)
     return gemm_small_m_workspace_bytes(batch, out_rows, n / 8);
 }
 
-int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0, const void* idx1,
-                     int s2_kind, const void* cb0, const void* cb1, int cb_dt, const void* scale, int s_dt, void* y,
-                     int y_dt, int64_t y_stride, int64_t out_rows, int64_t n, float rs, void* workspace,
-                     size_t ws_bytes, void* stream)
+// Validates a small-M GEMM call and fills `c`; returns VQ2_OK, an error, or
+// -1 for an empty problem (nothing to launch).
+static int small_m_call(GemmCall& c, const char* who, const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                        const int16_t* idx0, const void* idx1, int s2_kind, const void* cb0, const void* cb1,
+                        int cb_dt, const void* scale, int s_dt, void* y, int y_dt, int64_t y_stride,
+                        int64_t out_rows, int64_t n, float rs, void* stream)
 {
-    clear_error();
-    CHECK(batch >= 0 && batch <= 64 && out_rows >= 0 && n > 0,
-          "vq2_gemm_small_m: bad sizes batch=%lld (0..64) out_rows=%lld n=%lld", (long long)batch,
-          (long long)out_rows, (long long)n);
-    CHECK(n % 64 == 0, "vq2_gemm_small_m: n=%lld is not a multiple of 64", (long long)n);
-    if (batch == 0 || out_rows == 0) return VQ2_OK;
-    CHECK(x && idx0 && scale && y, "vq2_gemm_small_m: NULL pointer argument");
-    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "vq2_gemm_small_m: bad dtype code");
-    CHECK(x_stride >= n && y_stride >= out_rows, "vq2_gemm_small_m: strides too small");
+    CHECK(batch >= 0 && batch <= 64 && out_rows >= 0 && n > 0, "%s: bad sizes batch=%lld (0..64) out_rows=%lld n=%lld",
+          who, (long long)batch, (long long)out_rows, (long long)n);
+    CHECK(n % 64 == 0, "%s: n=%lld is not a multiple of 64", who, (long long)n);
+    if (batch == 0 || out_rows == 0) return -1;
+    CHECK(x && idx0 && scale && y, "%s: NULL pointer argument", who);
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "%s: bad dtype code", who);
+    CHECK(x_stride >= n && y_stride >= out_rows, "%s: strides too small", who);
     int r = check_codebooks(s2_kind, cb0, cb1, cb_dt);
     if (r) return r;
-    CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "vq2_gemm_small_m: idx1 must be given iff s2_kind != NONE");
-    GemmCall c{};
+    CHECK((s2_kind == VQ2_S2_NONE) == (idx1 == nullptr), "%s: idx1 must be given iff s2_kind != NONE", who);
+    c = GemmCall{};
     c.x = x;
     c.x_dt = x_dt;
     c.x_stride = x_stride;
@@ -172,10 +172,36 @@ int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride, c
     c.out_rows = out_rows;
     c.ng = n / 8;
     c.rs = rs;
+    c.stream = stream;
+    return VQ2_OK;
+}
+
+int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0, const void* idx1,
+                     int s2_kind, const void* cb0, const void* cb1, int cb_dt, const void* scale, int s_dt, void* y,
+                     int y_dt, int64_t y_stride, int64_t out_rows, int64_t n, float rs, void* workspace,
+                     size_t ws_bytes, void* stream)
+{
+    clear_error();
+    GemmCall c;
+    const int r = small_m_call(c, "vq2_gemm_small_m", x, x_dt, batch, x_stride, idx0, idx1, s2_kind, cb0, cb1, cb_dt,
+                               scale, s_dt, y, y_dt, y_stride, out_rows, n, rs, stream);
+    if (r) return r < 0 ? VQ2_OK : r;
     c.workspace = workspace;
     c.ws_bytes = ws_bytes;
-    c.stream = stream;
     return gemm_small_m_launch(c);
+}
+
+int vq2_gemm_small_m_noalloc(const void* x, int x_dt, int64_t batch, int64_t x_stride, const int16_t* idx0,
+                             const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
+                             const void* scale, int s_dt, void* y, int y_dt, int64_t y_stride, int64_t out_rows,
+                             int64_t n, float rs, void* stream)
+{
+    clear_error();
+    GemmCall c;
+    const int r = small_m_call(c, "vq2_gemm_small_m_noalloc", x, x_dt, batch, x_stride, idx0, idx1, s2_kind, cb0,
+                               cb1, cb_dt, scale, s_dt, y, y_dt, y_stride, out_rows, n, rs, stream);
+    if (r) return r < 0 ? VQ2_OK : r;
+    return gemm_small_m_noalloc_launch(c);
 }
 
 size_t vq2_gemm_small_m_argmax_workspace(int64_t batch, int64_t out_rows, int64_t n)

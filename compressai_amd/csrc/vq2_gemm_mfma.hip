@@ -502,6 +502,69 @@ static int gemm_launch(const GemmCall& c, int64_t* top1_idx, float* top1_val)
 
 int gemm_small_m_launch(const GemmCall& c) { return gemm_launch(c, nullptr, nullptr); }
 
+// ------------------------------------------------- no-allocation variant
+// The split-K partials of vq2_gemm_small_m_noalloc live in this file-scope
+// device array instead of a caller workspace: every GPU the library runs on
+// holds its own copy, at its own address, until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and only that address reaches the kernels.  The GEMM
+// writes every partial before the reduce reads it, so nothing needs zeroing
+// between calls.
+static __device__ __align__(256) unsigned char scratch[MM_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MM_MAX_DEVICES = 64;
+
+// device address of `scratch` on the current device (nullptr + error set on failure)
+static void* scratch_on_current_device()
+{
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) {
+        set_hip_error(err, "vq2_gemm_small_m_noalloc: hipGetDevice");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= MM_MAX_DEVICES) {
+        set_error(VQ2_ERR_UNSUPPORTED, "vq2_gemm_small_m_noalloc: device %d beyond the %d the library tracks", dev,
+                  MM_MAX_DEVICES);
+        return nullptr;
+    }
+    static std::mutex mu;
+    static void* ptr[MM_MAX_DEVICES] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p) {
+            set_hip_error(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                          "vq2_gemm_small_m_noalloc: hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
+int gemm_small_m_noalloc_launch(GemmCall c)
+{
+    if (c.m >= 1 && c.m <= MM_MAX_M && c.out_rows > 0 && c.ng > 0) {
+        const GemmPlan p = plan_gemm(c.m, c.out_rows, c.ng, device_cu_count(), c.x_dt == VQ2_DT_F16);
+        const size_t need = p.splits > 1 ? (size_t)p.splits * c.m * c.out_rows * sizeof(float) : 0;
+        if (need > MM_NOALLOC_SCRATCH_BYTES)
+            return set_error(VQ2_ERR_UNSUPPORTED,
+                             "vq2_gemm_small_m_noalloc: this shape needs %zu bytes of split-K partials, more than the "
+                             "%zu-byte device scratch of the no-allocation entry (use vq2_gemm_small_m with a workspace)",
+                             need, (size_t)MM_NOALLOC_SCRATCH_BYTES);
+        if (need > 0) {
+            void* p_scratch = scratch_on_current_device();
+            if (!p_scratch) return VQ2_ERR_HIP;
+            c.workspace = p_scratch;
+            c.ws_bytes = MM_NOALLOC_SCRATCH_BYTES;
+        }
+    }
+    return gemm_launch(c, nullptr, nullptr);
+}
+
 int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val)
 {
     if (!out_idx) return set_error(VQ2_ERR_ARG, "vq2 small-M GEMM top-1: NULL out_idx");

@@ -111,6 +111,10 @@ struct GemmCall {
 
 size_t gemm_small_m_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
 int gemm_small_m_launch(const GemmCall& c);
+// the same GEMM with its split-K partials in the library's device scratch
+// (c.workspace / c.ws_bytes ignored); shapes needing more are rejected
+constexpr size_t MM_NOALLOC_SCRATCH_BYTES = VQ2_NOALLOC_SCRATCH_BYTES;
+int gemm_small_m_noalloc_launch(GemmCall c);
 // the GEMM with the top-1 of every activation row instead of y (c.y unused)
 size_t gemm_small_m_top1_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
 int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val);

@@ -93,6 +93,26 @@ int vq2_gemm_small_m(const void* x, int x_dt, int64_t batch, int64_t x_stride,
                      int64_t out_rows, int64_t n, float rs,
                      void* workspace, size_t ws_bytes, void* stream);
 
+/* vq2_gemm_small_m without the workspace arguments: allocates nothing.  No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops and harnesses that
+ * forbid hipMalloc).  The split-K partials go to a device array of the
+ * library instead, VQ2_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held until the
+ * process ends; a shape whose partials need more (vq2_gemm_small_m_workspace
+ * (batch, out_rows, n) > VQ2_NOALLOC_SCRATCH_BYTES, e.g. a 151936-row LM head
+ * at batch 64) returns VQ2_ERR_UNSUPPORTED without launching.  Every call on
+ * one GPU shares that array and leaves its partials there: calls that overlap
+ * on one GPU (several streams or host threads) race, so serialise them.  The
+ * stream's device must be the current device.  Results equal
+ * vq2_gemm_small_m's bit for bit (same kernels and plan). */
+#define VQ2_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int vq2_gemm_small_m_noalloc(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                             const int16_t* idx0, const void* idx1, int s2_kind,
+                             const void* cb0, const void* cb1, int cb_dt,
+                             const void* scale, int s_dt,
+                             void* y, int y_dt, int64_t y_stride,
+                             int64_t out_rows, int64_t n, float rs, void* stream);
+
 /* vq2_gemm_small_m followed by the top-1 of every activation row, without
  * writing the logits: out_idx[b] = argmax_r y[b, r] (torch.argmax's first
  * maximum; int64, 8-byte aligned), out_val[b] = y[b, out_idx[b]] (fp32, may
