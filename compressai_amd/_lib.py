@@ -62,6 +62,14 @@ SIGNATURES = {
     "vq2_argmax_rows": ([_vp, _i32, _i64, _i64, _vp, _vp, _vp], _i32),
     "vq2_gemv_argmax": ([_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64,
                          _f32, _vp, _vp, _vp, _vp], _i32),
+    "vq2_sorted_rows_per_chunk": ([_i64, _i64, _i64], _i64),
+    "vq2_sorted_pack": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i32], _i32),
+    "vq2_sorted_gemv_workspace": ([_vp, _i32, _i32], ctypes.c_size_t),
+    "vq2_sorted_gemv": ([_vp, _i32, _vp, _vp, _i64, _f32, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _f32, _i32,
+                         _vp, ctypes.c_size_t, _vp], _i32),
+    "vq2_sorted_gemv_argmax_workspace": ([_vp], ctypes.c_size_t),
+    "vq2_sorted_gemv_argmax": ([_vp, _i32, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _i32, _i32, _i64, _f32, _vp,
+                                ctypes.c_size_t, _vp, _vp, _vp], _i32),
     "vq2_dequant_rows": ([_vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp], _i32),
     "vq2_decode_idx": ([_vp, _i32, _i64, _vp, _vp], _i32),
     "vq2_unpack_fixed": ([_vp, _i64, _i32, _i64, _vp, _vp], _i32),
@@ -80,10 +88,18 @@ class Seg(ctypes.Structure):
                 ("y", ctypes.c_void_p), ("out_rows", ctypes.c_int64), ("y_stride", ctypes.c_int64)]
 
 
+class SortedMat(ctypes.Structure):
+    """struct vq2_sorted_mat of include/vq2_amd.h"""
+    _fields_ = [("entries", ctypes.c_void_p), ("chunk_it", ctypes.c_void_p), ("chunk_it1", ctypes.c_void_p),
+                ("n_iters", ctypes.c_int64), ("rows_per_chunk", ctypes.c_int64), ("has_stage2", ctypes.c_int),
+                ("scale", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("out_rows", ctypes.c_int64)]
+
+
 def header_symbols() -> list[str]:
     """Names of the functions declared in include/vq2_amd.h."""
     text = HEADER_PATH.read_text()
-    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(vq2_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(vq2_\w+)\s*\(", text, flags=re.M)
 
 
 def load():

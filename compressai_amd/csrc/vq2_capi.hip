@@ -629,6 +629,115 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride, co
     return vq2_argmax_rows(logits_ws, VQ2_DT_F32, batch, out_rows, out_idx, out_val, stream);
 }
 
+// ------------------------------------------------------ code-sorted layout
+int64_t vq2_sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
+{
+    return sorted_rows_per_chunk(out_rows, ng, chunk_align);
+}
+
+int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
+                    uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
+                    int n_threads)
+{
+    clear_error();
+    CHECK(idx0 && entries && chunk_it && chunk_it1 && n_iters, "vq2_sorted_pack: NULL pointer argument");
+    CHECK(out_rows >= 1 && ng >= 1, "vq2_sorted_pack: bad sizes out_rows=%lld ng=%lld", (long long)out_rows,
+          (long long)ng);
+    return sorted_pack(idx0, idx1, out_rows, ng, rows_per_chunk, entries, cap_iters, chunk_it, chunk_it1, n_iters,
+                       n_threads);
+}
+
+static int sorted_call(SortedCall& c, const char* who, const void* x, int x_dt, const int32_t* perm,
+                       const int8_t* sign, int64_t hb, float rht_scale, int n_mat, const vq2_sorted_mat* mats,
+                       const void* cb0, const void* cb1, int cb_dt, int s_dt, int y_dt, int64_t n, float rs,
+                       int slices, void* stream)
+{
+    CHECK(n > 0 && n % 8 == 0, "%s: n=%lld must be a positive multiple of 8", who, (long long)n);
+    CHECK(n_mat >= 1 && n_mat <= 4 && mats, "%s: 1..4 matrices", who);
+    CHECK(x && cb0, "%s: NULL pointer argument", who);
+    CHECK(dt_ok(x_dt) && dt_ok(s_dt) && dt_ok(y_dt), "%s: bad dtype code", who);
+    CHECK(cb_dt == VQ2_DT_F16 || cb_dt == VQ2_DT_BF16, "%s: fp16 / bf16 codebooks only", who);
+    CHECK(hb >= 0, "%s: bad hb", who);
+    c = SortedCall{};
+    c.x = x;
+    c.x_dt = x_dt;
+    c.xm = hb > 0 ? 1 : 0;
+    c.perm = perm;
+    c.sign = sign;
+    c.hb = hb;
+    c.xscale = rht_scale;
+    c.cb0 = cb0;
+    c.cb1 = cb1;
+    c.cb_dt = cb_dt;
+    c.s_dt = s_dt;
+    c.y_dt = y_dt;
+    c.ng = n / 8;
+    c.rs = rs;
+    c.slices = slices;
+    c.nseg = n_mat;
+    c.stream = stream;
+    for (int i = 0; i < n_mat; i++) {
+        const vq2_sorted_mat& m = mats[i];
+        CHECK(m.entries && m.chunk_it && m.chunk_it1 && m.scale, "%s: matrix %d has a NULL pointer", who, i);
+        CHECK(m.out_rows >= 1 && m.n_iters >= 1, "%s: matrix %d: bad sizes", who, i);
+        CHECK(!m.has_stage2 || cb1, "%s: matrix %d has stage-2 entries but no cb1", who, i);
+        CHECK((m.has_stage2 != 0) == (mats[0].has_stage2 != 0), "%s: the matrices of a launch share one cfg", who);
+        c.seg[i] = SortedSegCall{m.entries, m.chunk_it, m.chunk_it1, m.n_iters, m.rows_per_chunk,
+                                 m.has_stage2 ? 1 : 0, m.scale, m.y, m.out_rows};
+    }
+    if (!mats[0].has_stage2) c.cb1 = nullptr;
+    return VQ2_OK;
+}
+
+size_t vq2_sorted_gemv_workspace(const vq2_sorted_mat* mats, int n_mat, int slices)
+{
+    if (!mats || n_mat < 1 || n_mat > 4 || slices <= 1) return 0;
+    SortedCall c{};
+    c.slices = slices;
+    c.nseg = n_mat;
+    for (int i = 0; i < n_mat; i++) c.seg[i].out_rows = mats[i].out_rows;
+    return sorted_workspace_bytes(c);
+}
+
+int vq2_sorted_gemv(const void* x, int x_dt, const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                    int n_mat, const vq2_sorted_mat* mats, const void* cb0, const void* cb1, int cb_dt, int s_dt,
+                    int y_dt, int64_t n, float rs, int slices, void* workspace, size_t ws_bytes, void* stream)
+{
+    clear_error();
+    SortedCall c;
+    int r = sorted_call(c, "vq2_sorted_gemv", x, x_dt, perm, sign, hb, rht_scale, n_mat, mats, cb0, cb1, cb_dt, s_dt,
+                        y_dt, n, rs, slices, stream);
+    if (r) return r;
+    for (int i = 0; i < n_mat; i++) CHECK(mats[i].y, "vq2_sorted_gemv: matrix %d has no output", i);
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
+    return sorted_launch(c, nullptr, nullptr);
+}
+
+size_t vq2_sorted_gemv_argmax_workspace(const vq2_sorted_mat* mat)
+{
+    if (!mat || mat->rows_per_chunk < 1 || mat->out_rows < 1) return 0;
+    return (size_t)((mat->out_rows + mat->rows_per_chunk - 1) / mat->rows_per_chunk) * sizeof(uint64_t);
+}
+
+int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const int8_t* sign, int64_t hb,
+                           float rht_scale, const vq2_sorted_mat* mat, const void* cb0, const void* cb1, int cb_dt,
+                           int s_dt, int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
+                           float* out_val, void* stream)
+{
+    clear_error();
+    SortedCall c;
+    int r = sorted_call(c, "vq2_sorted_gemv_argmax", x, x_dt, perm, sign, hb, rht_scale, 1, mat, cb0, cb1, cb_dt, s_dt,
+                        VQ2_DT_F32, n, rs, 1, stream);
+    if (r) return r;
+    CHECK(out_idx && (uintptr_t)out_idx % 8 == 0, "vq2_sorted_gemv_argmax: out_idx must be 8-byte aligned");
+    const size_t need = vq2_sorted_gemv_argmax_workspace(mat);
+    CHECK(workspace && ws_bytes >= need && (uintptr_t)workspace % 8 == 0,
+          "vq2_sorted_gemv_argmax: workspace of %zu bytes (8-byte aligned) needed", need);
+    c.cand = (uint64_t*)workspace;
+    return sorted_launch(c, out_idx, out_val);
+}
+
 int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
                      const void* scale, int s_dt, int64_t r0, int64_t r1, int64_t n, float* out, void* stream)
 {

@@ -119,6 +119,51 @@ int gemm_small_m_noalloc_launch(GemmCall c);
 size_t gemm_small_m_top1_workspace_bytes(int64_t m, int64_t out_rows, int64_t ng);
 int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val);
 
+// VQ GEMV over the code-sorted internal layout (vq2_sorted.hip).
+struct SortedSegCall {
+    const uint32_t* entries;   // [n_iters * 256], 16-byte aligned
+    const int32_t* chunk_it;   // [n_chunks + 1] iteration offsets
+    const int32_t* chunk_it1;  // [n_chunks] stage-1 iterations per chunk
+    int64_t n_iters;
+    int64_t rows_per_chunk;
+    int s2;                    // stage-2 entries present (4 bpw)
+    const void* scale;
+    void* y;
+    int64_t out_rows;
+};
+
+struct SortedCall {
+    const void* x;
+    int x_dt;
+    int xm;  // 0: x is rotated; 1: rotate x in the kernel (perm / sign / hb / xscale)
+    const int32_t* perm;
+    const int8_t* sign;
+    int64_t hb;
+    float xscale;
+    const void* cb0;
+    const void* cb1;
+    int cb_dt;
+    int s_dt;
+    int y_dt;
+    int64_t ng;
+    float rs;
+    int slices;
+    int nseg;
+    SortedSegCall seg[4];
+    void* workspace;
+    size_t ws_bytes;
+    uint64_t* cand;  // top-1: one key per workgroup
+    void* stream;
+};
+
+int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
+int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
+                uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
+                int n_threads);
+size_t sorted_workspace_bytes(const SortedCall& c);
+// top1_idx non-null: fused top-1 (one matrix, one slice) instead of y
+int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);
+
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
                const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,
                int inverse, int swiglu, int64_t inter, void* stream);

@@ -1,0 +1,568 @@
+// vq2_sorted.hip -- VQ GEMV over a code-sorted internal layout (gfx950).
+//
+//   y[r] = (sum_g cb0[i0[r, g]] . x_g  [+ sum_g cb1[i1[r, g]] . x_g]) * s[r] * rs
+//
+// Why: at batch 1 the reference layout costs one random 16-byte codebook
+// gather per code, and random gathers from the L2-resident 1 MiB codebook are
+// capped by the L2 request rate (about 240 G codes/s on MI355X, 6 % of HBM).
+// Lanes whose codes fall in the same 128-byte codebook line share one
+// request, so the codes of a chunk of rows are reordered by value: 64
+// consecutive sorted codes of a chunk of ~65536 codes span about 8 lines
+// instead of 64 (measured up to ~860 G codes/s for 65536-code chunks).
+//
+// Layout (built once at load time on the host by vq2_sorted_pack, from the
+// reference's index planes, which stay the public format):
+//  * a matrix is cut into chunks of R rows x all ng groups; an entry is a
+//    uint32 (code << 16) | (row_in_chunk << gbits) | group, gbits =
+//    ceil(log2 ng) and R <= min(2^(16 - gbits) - 1, 255) rows (chosen at
+//    pack time: the rows split evenly over the chunks), so row R is a dummy
+//    row that padding entries (pos R << gbits, code 0) add to;
+//  * every wave keeps two accumulator arrays, one per 32-lane half; a
+//    chunk's entries are sorted by code (then position) and dealt into
+//    instructions of 64 entries, one per lane, with no row twice in a half
+//    (an entry whose row both open halves already hold waits for the next
+//    instruction), so the lanes' read-add-write of their row's accumulator
+//    never collide; padding fills the tail;
+//  * 4 instructions form an iteration: lane l holds a uint32x4 whose element
+//    q is entry l of instruction q (one 16-byte load per lane);
+//  * the chunk's stage-1 iterations come first, then its stage-2 iterations
+//    (4 bpw); chunk_it[c] / chunk_it1[c] give the iteration offset and the
+//    stage-1 count.
+//
+// Kernel: one workgroup of 16 waves per (chunk, slice).  The workgroup first
+// builds the rotated activation in LDS (the fused RHT prologue of the GEMV
+// kernel, or a copy of a pre-rotated x), fp32; every wave owns two LDS
+// accumulators per row of the chunk (2 x (R + 1) floats).  A wave takes iterations
+// of its slice round-robin: one 16-byte entry load, four centroid gathers,
+// then per entry the group's 8 activation values from LDS, the 8-term dot
+// product in fp32 and acc[half][row] += dot.  At the end the waves'
+// accumulators are summed in (wave, half) order: with one slice the rows are complete
+// (y = (acc * s) * rs, or the fused top-1 key per workgroup); with several
+// slices the raw partials go to a workspace and vq_sorted_reduce_kernel sums
+// them in slice order.  Every order is fixed, so results are deterministic.
+//
+// Semantics: vq_gemv_16 / the PackedLinear fallback (vq2/kernels.py:57-78,
+// vq2/runtime.py:82-110) for the (16,) and (16,16) configurations; the sums
+// are those of the gather kernels in another order (fp32 accumulation).
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "vq2_gemv_kernel.hpp"
+
+namespace vq2 {
+
+constexpr int SG_THREADS = 1024;
+constexpr int SG_WAVES = SG_THREADS / 64;
+constexpr int SG_ITER = 256;  // entries per iteration (64 lanes x 4)
+constexpr int SG_MAX_R = 255;
+constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
+constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
+constexpr int SG_MAX_SEG = 4;
+constexpr int SG_MAX_SHM = 96 * 1024;  // dynamic LDS: activation (+ stage) + accumulators
+
+static int sorted_gbits(int64_t ng)
+{
+    int b = 0;
+    while ((int64_t(1) << b) < ng) b++;
+    return b;
+}
+
+// Largest chunk height for ng groups: row R is the dummy row, so
+// (R << gbits) | group must fit 16 bits; at most SG_MAX_R.
+static int64_t sorted_max_rows(int64_t ng)
+{
+    const int gb = sorted_gbits(ng);
+    if (ng < 1 || gb > 15) return 0;
+    const int64_t rmax = (int64_t(1) << (16 - gb)) - 1;
+    return rmax < SG_MAX_R ? rmax : SG_MAX_R;
+}
+
+// Default chunk height: the rows split evenly over the fewest chunks; with
+// chunk_align > 1, over a multiple of chunk_align chunks (one per CU and
+// round: no CU waits for a last short round) when the chunks keep at least
+// SG_MIN_ALIGNED_R rows.
+constexpr int64_t SG_MIN_ALIGNED_R = 128;
+int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
+{
+    const int64_t rmax = sorted_max_rows(ng);
+    if (rmax == 0 || out_rows < 1) return 0;
+    const int64_t nch = (out_rows + rmax - 1) / rmax;
+    if (chunk_align > 1) {
+        const int64_t nal = (nch + chunk_align - 1) / chunk_align * chunk_align;
+        const int64_t ral = (out_rows + nal - 1) / nal;
+        if (ral >= SG_MIN_ALIGNED_R) return ral;
+    }
+    return (out_rows + nch - 1) / nch;
+}
+
+// ------------------------------------------------------------ host repack
+// Entries of one (chunk, stage) in lane layout: sorted by code, dealt into
+// 64-entry instructions with distinct rows in each lane group sharing an
+// accumulator array, padded to whole iterations.
+static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int64_t ng, int gb, int64_t R,
+                             std::vector<uint32_t>& out)
+{
+    std::vector<uint32_t> keys;
+    keys.reserve((size_t)(rows * ng));
+    for (int64_t r = 0; r < rows; r++) {
+        const int16_t* p = plane + (r0 + r) * ng;
+        for (int64_t g = 0; g < ng; g++)
+            keys.push_back(((uint32_t)(uint16_t)p[g] << 16) | (uint32_t)((r << gb) | g));
+    }
+    std::sort(keys.begin(), keys.end());
+    const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
+    std::vector<uint32_t> instr;  // instruction-major, 64 per instruction
+    instr.reserve(keys.size() + 1024);
+    std::vector<uint32_t> pending, still;
+    // lane groups of the current instruction that hold each row (valid
+    // while stamp[row] == id)
+    std::vector<int64_t> stamp((size_t)R + 1, -1);
+    std::vector<uint8_t> used((size_t)R + 1, 0);
+    static_assert(SG_PARTS <= 8, "one bit per lane group");
+    size_t next = 0;
+    int64_t id = 0;
+    while (next < keys.size() || !pending.empty()) {
+        uint32_t slot[SG_PARTS][SG_PART_LANES];
+        int fill[SG_PARTS] = {};
+        int n = 0;
+        // place k in the first open lane group that does not hold its row
+        auto place = [&](uint32_t k) {
+            const uint32_t row = (k & 0xFFFFu) >> gb;
+            const uint8_t u = stamp[row] == id ? used[row] : 0;
+            for (int qd = 0; qd < SG_PARTS; qd++)
+                if (fill[qd] < SG_PART_LANES && !(u & (1u << qd))) {
+                    slot[qd][fill[qd]++] = k;
+                    stamp[row] = id;
+                    used[row] = (uint8_t)(u | (1u << qd));
+                    n++;
+                    return true;
+                }
+            return false;
+        };
+        still.clear();
+        for (uint32_t k : pending)  // entries waiting since an earlier instruction go first
+            if (n == 64 || !place(k)) still.push_back(k);
+        pending.swap(still);
+        while (n < 64 && next < keys.size()) {
+            const uint32_t k = keys[next++];
+            if (!place(k)) pending.push_back(k);
+        }
+        for (int qd = 0; qd < SG_PARTS; qd++) {
+            while (fill[qd] < SG_PART_LANES) slot[qd][fill[qd]++] = pad;
+            instr.insert(instr.end(), slot[qd], slot[qd] + SG_PART_LANES);
+        }
+        id++;
+    }
+    while ((instr.size() / 64) % 4) instr.insert(instr.end(), 64, (uint32_t)(R << gb));
+    const size_t iters = instr.size() / SG_ITER;
+    const size_t base = out.size();
+    out.resize(base + iters * SG_ITER);
+    for (size_t it = 0; it < iters; it++)
+        for (int l = 0; l < 64; l++)
+            for (int q = 0; q < 4; q++) out[base + (it * 64 + l) * 4 + q] = instr[(it * 4 + q) * 64 + l];
+}
+
+int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t R,
+                uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
+                int n_threads)
+{
+    const int64_t rmax = sorted_max_rows(ng);
+    if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack: ng=%lld outside 1..32768", (long long)ng);
+    if (R < 1 || R > rmax)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_pack: rows_per_chunk=%lld outside 1..%lld for ng=%lld",
+                         (long long)R, (long long)rmax, (long long)ng);
+    const int gb = sorted_gbits(ng);
+    const int64_t n_chunks = (out_rows + R - 1) / R;
+    std::vector<std::vector<uint32_t>> parts((size_t)n_chunks);
+    std::vector<int64_t> it1((size_t)n_chunks);
+    int nt = n_threads > 0 ? n_threads : (int)std::thread::hardware_concurrency();
+    if (nt < 1) nt = 1;
+    if (nt > n_chunks) nt = (int)(n_chunks > 0 ? n_chunks : 1);
+    auto work = [&](int t) {
+        for (int64_t c = t; c < n_chunks; c += nt) {
+            const int64_t r0 = c * R, rows = std::min(R, out_rows - r0);
+            pack_chunk_stage(idx0, r0, rows, ng, gb, R, parts[c]);
+            it1[c] = (int64_t)parts[c].size() / SG_ITER;
+            if (idx1) pack_chunk_stage(idx1, r0, rows, ng, gb, R, parts[c]);
+        }
+    };
+    if (nt == 1) {
+        work(0);
+    } else {
+        std::vector<std::thread> th;
+        for (int t = 0; t < nt; t++) th.emplace_back(work, t);
+        for (auto& t : th) t.join();
+    }
+    int64_t total = 0;
+    for (int64_t c = 0; c < n_chunks; c++) total += (int64_t)parts[c].size() / SG_ITER;
+    *n_iters = total;
+    if (total > 0x7FFFFFFFLL) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack: matrix too large");
+    if (total > cap_iters)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_pack: %lld iterations needed, capacity %lld", (long long)total,
+                         (long long)cap_iters);
+    int64_t off = 0;
+    for (int64_t c = 0; c < n_chunks; c++) {
+        chunk_it[c] = (int32_t)off;
+        chunk_it1[c] = (int32_t)it1[c];
+        memcpy(entries + off * SG_ITER, parts[c].data(), parts[c].size() * sizeof(uint32_t));
+        off += (int64_t)parts[c].size() / SG_ITER;
+    }
+    chunk_it[n_chunks] = (int32_t)off;
+    return VQ2_OK;
+}
+
+// ------------------------------------------------------------------ kernel
+struct SortedSeg {
+    const u32x4* ent;     // [n_iters * 64] lane words
+    const int32_t* cit;   // [n_chunks + 1]
+    const int32_t* cit1;  // [n_chunks]
+    const void* scale;
+    void* y;
+    float* part;  // slices > 1: [slices][out_rows]
+    int64_t out_rows;
+    int32_t n_iters;
+    int32_t n_chunks;
+    int32_t wg_start;
+    int32_t R;  // rows per chunk
+};
+
+struct SortedArgs {
+    GemvArgs g;  // the activation fields of the prologue (x, perm, sign, hb_log2, xscale, strides)
+    const void* cb0;
+    const void* cb1;
+    int s_dt;
+    int y_dt;
+    int64_t ng;
+    int gbits;
+    int slices;
+    float rs;
+    int nseg;
+    SortedSeg seg[SG_MAX_SEG];
+    uint64_t* cand;  // EP 1: best top-1 key per workgroup
+};
+
+template <int CBT>
+__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* x)
+{
+    const u32x4 x0 = *(const u32x4*)x, x1 = *(const u32x4*)(x + 4);
+    float xv[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        xv[k] = __uint_as_float(x0[k]);
+        xv[4 + k] = __uint_as_float(x1[k]);
+    }
+    float d = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        float lo, hi;
+        if constexpr (CBT == VQ2_DT_F16) {
+            lo = f16_bits_to_f32((uint16_t)(c[w] & 0xFFFFu));
+            hi = f16_bits_to_f32((uint16_t)(c[w] >> 16));
+        } else {
+            lo = __uint_as_float(c[w] << 16);
+            hi = __uint_as_float(c[w] & 0xFFFF0000u);
+        }
+        d = fmaf(lo, xv[2 * w], d);
+        d = fmaf(hi, xv[2 * w + 1], d);
+    }
+    return d;
+}
+
+// XM 0: x holds the rotated activation (dtype XT); XM 1: rotate x in LDS.
+// EP 0: store y (or partials with several slices); EP 1: fused top-1 keys.
+template <int CBT, int XM, int XT, int EP>
+__global__ void __launch_bounds__(SG_THREADS) vq_sorted_kernel(const SortedArgs a)
+{
+    extern __shared__ __align__(16) float smem[];
+    touch_kernargs(a);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t n = a.ng * 8;
+    float* s_x = smem;                                  // n floats
+    float* s_acc = smem + n + (XM == 1 ? n : 0);        // SG_WAVES x SG_PARTS x (R + 1)
+    int si = 0;
+#pragma unroll
+    for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && (int)blockIdx.x >= a.seg[s].wg_start) ? 1 : 0;
+    const SortedSeg& sg = a.seg[si];
+    const int R = sg.R;
+    const int local = (int)blockIdx.x - sg.wg_start;
+    const int chunk = local / a.slices, slice = local - chunk * a.slices;
+    const int c_beg = min(sg.cit[chunk], sg.n_iters - 1);  // n_iters >= 1 (checked on the host)
+    const int c_end = min(max(sg.cit[chunk + 1], c_beg), sg.n_iters);
+    const int c_mid = min(c_beg + sg.cit1[chunk], c_end);
+    const int nit = c_end - c_beg;
+    const int s0 = c_beg + (int)((int64_t)nit * slice / a.slices);
+    const int s1 = c_beg + (int)((int64_t)nit * (slice + 1) / a.slices);
+
+    // prologue loads first (they return before the entries and gathers)
+    XProLoad first;
+    const int64_t t0 = (int64_t)threadIdx.x * 8;
+    if constexpr (XM == 1) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, 0, 0, first);
+
+    // the wave's first three iterations' entry words and the first two's
+    // gathers are in flight during the prologue (clamped in-bounds addresses
+    // when the wave has fewer).  A missing stage-2 codebook is never selected
+    // for a real entry; cb0 stands in so that no gather can use a null base.
+    const u32x4* cb0 = (const u32x4*)a.cb0;
+    const u32x4* cb1 = (const u32x4*)(a.cb1 ? a.cb1 : a.cb0);
+    auto clampit = [&](int i) { return i < s1 ? i : c_beg; };
+    auto load_e = [&](int i) { return __builtin_nontemporal_load(sg.ent + (int64_t)i * 64 + lane); };
+    auto gather = [&](int i, const u32x4& e, u32x4 (&c)[4]) {
+        const u32x4* cb = i < c_mid ? cb0 : cb1;
+#pragma unroll
+        for (int q = 0; q < 4; q++) c[q] = cb[e[q] >> 16];
+    };
+    int it = s0 + wave;
+    int i1 = clampit(it + SG_WAVES), i2 = clampit(it + 2 * SG_WAVES);
+    u32x4 e0 = load_e(clampit(it)), e1 = load_e(i1), e2 = load_e(i2);
+    u32x4 c0[4], c1[4];
+    gather(clampit(it), e0, c0);
+    gather(i1, e1, c1);
+
+    float* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
+    for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = 0.0f;
+    if constexpr (XM == 1) {
+        void* s_stage = smem + n;
+        stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
+        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+        for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] *= a.g.xscale;
+    } else {
+        for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] = load_as_f32(a.g.x, XT, i);
+    }
+    __syncthreads();
+    // per wave, four iterations in flight: entry words three ahead, gathers
+    // two ahead of the arithmetic (about 8K codes in flight per CU at 16
+    // waves; loads complete in issue order, and no branch separates them, so
+    // each wait covers exactly the values it needs)
+    const uint32_t gmask = (1u << a.gbits) - 1u;
+    const uint32_t gmax = (uint32_t)(a.ng - 1);
+    for (; it < s1; it += SG_WAVES) {
+        const int i3 = clampit(it + 3 * SG_WAVES);
+        const u32x4 e3 = load_e(i3);
+        u32x4 c2[4];
+        gather(i2, e2, c2);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t pos = e0[q] & 0xFFFFu;
+            const uint32_t r = min(pos >> a.gbits, (uint32_t)R);
+            const uint32_t g = min(pos & gmask, gmax);
+            const float d = centroid_dot<CBT>(c0[q], s_x + g * 8);
+            acc[r] += d;
+        }
+        e0 = e1;
+        e1 = e2;
+        e2 = e3;
+        i2 = i3;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            c0[q] = c1[q];
+            c1[q] = c2[q];
+        }
+    }
+    __syncthreads();
+
+    // row sums: thread (p, r) adds a quarter of the SG_WAVES x SG_PARTS
+    // arrays of row r, then the four partials are added in p order (fixed
+    // order: deterministic)
+    __shared__ float s_red[4][256];
+    const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
+    if (rr < R) {
+        float part = 0.0f;
+        constexpr int NA = SG_WAVES * SG_PARTS / 4;
+#pragma unroll 4
+        for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
+        s_red[pp][rr] = part;
+    }
+    __syncthreads();
+    const int64_t row0 = (int64_t)chunk * R;
+    const int64_t row = row0 + rr;
+    const bool own = pp == 0 && rr < R && row < sg.out_rows;
+    const float sum = own ? ((s_red[0][rr] + s_red[1][rr]) + s_red[2][rr]) + s_red[3][rr] : 0.0f;
+    if constexpr (EP == 1) {
+        uint64_t best = own ? argmax_key((sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs, row) : 0;
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint64_t o = __shfl_xor(best, off);
+            best = o > best ? o : best;
+        }
+        __shared__ uint64_t s_key[4];
+        if (pp == 0 && lane == 0) s_key[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < 4; w++) best = s_key[w] > best ? s_key[w] : best;
+            a.cand[blockIdx.x] = best;
+        }
+    } else if (a.slices == 1) {
+        if (own) store_from_f32(sg.y, a.y_dt, row, (sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs);
+    } else if (own) {
+        sg.part[(int64_t)slice * sg.out_rows + row] = sum;
+    }
+}
+
+// y[row] = (sum over slices of part[slice][row], in slice order) * s * rs;
+// blockIdx.y = segment.
+__global__ void __launch_bounds__(256) vq_sorted_reduce_kernel(const SortedArgs a)
+{
+    const SortedSeg& sg = a.seg[blockIdx.y];
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= sg.out_rows) return;
+    float sum = 0.0f;
+    for (int s = 0; s < a.slices; s++) sum += sg.part[(int64_t)s * sg.out_rows + row];
+    store_from_f32(sg.y, a.y_dt, row, (sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs);
+}
+
+// ------------------------------------------------------------------ launch
+template <int CBT, int XM, int XT, int EP>
+static hipError_t launch_sorted(const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
+{
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)vq_sorted_kernel<CBT, XM, XT, EP>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, SG_MAX_SHM);
+    });
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((vq_sorted_kernel<CBT, XM, XT, EP>), dim3(grid), dim3(SG_THREADS), shm, st, a);
+    return hipGetLastError();
+}
+
+template <int CBT, int EP>
+static hipError_t launch_sorted_x(int xm, int x_dt, const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
+{
+    if (xm == 1) {
+        switch (x_dt) {
+        case VQ2_DT_F16: return launch_sorted<CBT, 1, VQ2_DT_F16, EP>(a, grid, shm, st);
+        case VQ2_DT_BF16: return launch_sorted<CBT, 1, VQ2_DT_BF16, EP>(a, grid, shm, st);
+        default: return launch_sorted<CBT, 1, VQ2_DT_F32, EP>(a, grid, shm, st);
+        }
+    }
+    switch (x_dt) {
+    case VQ2_DT_F16: return launch_sorted<CBT, 0, VQ2_DT_F16, EP>(a, grid, shm, st);
+    case VQ2_DT_BF16: return launch_sorted<CBT, 0, VQ2_DT_BF16, EP>(a, grid, shm, st);
+    default: return launch_sorted<CBT, 0, VQ2_DT_F32, EP>(a, grid, shm, st);
+    }
+}
+
+size_t sorted_workspace_bytes(const SortedCall& c)
+{
+    if (c.slices <= 1) return 0;
+    size_t b = 0;
+    for (int s = 0; s < c.nseg; s++) b += (size_t)c.slices * c.seg[s].out_rows * sizeof(float);
+    return b;
+}
+
+int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
+{
+    const bool top1 = top1_idx != nullptr;
+    if (c.nseg < 1 || c.nseg > SG_MAX_SEG) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: 1..%d matrices", SG_MAX_SEG);
+    const int64_t r_lim = sorted_max_rows(c.ng);
+    if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: ng=%lld unsupported", (long long)c.ng);
+    int64_t rmax = 0;
+    for (int s = 0; s < c.nseg; s++) {
+        const int64_t R = c.seg[s].rows_per_chunk;
+        if (R < 1 || R > r_lim)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d: rows_per_chunk=%lld outside 1..%lld", s,
+                             (long long)R, (long long)r_lim);
+        rmax = std::max(rmax, R);
+    }
+    if (c.cb_dt != VQ2_DT_F16 && c.cb_dt != VQ2_DT_BF16)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: fp16 / bf16 codebooks only");
+    if (c.slices < 1 || c.slices > 64) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: slices must be 1..64");
+    if (top1 && (c.slices != 1 || c.nseg != 1))
+        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: one matrix, one slice");
+    const int64_t n = c.ng * 8;
+    const size_t shm = (size_t)(n * (c.xm == 1 ? 2 : 1) + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
+    if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large", (long long)n);
+    if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
+        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: codebooks must be 16-byte aligned");
+    if (c.xm == 1) {
+        if (n % 64) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: fused RHT needs n %% 64 == 0");
+        if (c.hb < 2 || c.hb > n || (c.hb & (c.hb - 1)) || n % c.hb)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: hb=%lld must be a power of two dividing n", (long long)c.hb);
+        if ((uintptr_t)c.perm % 16 || (uintptr_t)c.sign % 8)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: perm 16-byte, sign 8-byte aligned");
+        if ((uintptr_t)c.x % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: x must be 16-byte aligned");
+    }
+    SortedArgs a{};
+    a.g.x = c.x;
+    a.g.x_dt = c.x_dt;
+    a.g.x_bstride = n;
+    a.g.x_pstride = 0;
+    a.g.x_pdiv = 1;
+    a.g.P = 1;
+    a.g.ng = c.ng;
+    a.g.batch = 1;
+    a.g.perm = c.perm;
+    a.g.sign = c.sign;
+    int hl = 0;
+    while ((int64_t(1) << hl) < c.hb) hl++;
+    a.g.hb_log2 = hl;
+    a.g.xscale = c.xscale;
+    a.cb0 = c.cb0;
+    a.cb1 = c.cb1;
+    a.s_dt = c.s_dt;
+    a.y_dt = c.y_dt;
+    a.ng = c.ng;
+    a.gbits = sorted_gbits(c.ng);
+    a.slices = c.slices;
+    a.rs = c.rs;
+    a.nseg = c.nseg;
+    a.cand = c.cand;
+    float* part = (float*)c.workspace;
+    if (!top1 && c.slices > 1) {
+        const size_t need = sorted_workspace_bytes(c);
+        if (!c.workspace || c.ws_bytes < need)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: workspace of %zu bytes needed (got %zu)", need, c.ws_bytes);
+    }
+    int64_t wg = 0, max_rows = 0;
+    for (int s = 0; s < c.nseg; s++) {
+        const SortedSegCall& sc = c.seg[s];
+        const int64_t R = sc.rows_per_chunk;
+        const int64_t n_chunks = (sc.out_rows + R - 1) / R;
+        if (sc.n_iters < 1 || sc.n_iters > 0x7FFFFFFF)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d has %lld iterations", s, (long long)sc.n_iters);
+        if ((uintptr_t)sc.entries % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: entries must be 16-byte aligned");
+        if (sc.s2 != (c.cb1 != nullptr)) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: stage-2 entries need cb1");
+        a.seg[s].ent = (const u32x4*)sc.entries;
+        a.seg[s].cit = sc.chunk_it;
+        a.seg[s].cit1 = sc.chunk_it1;
+        a.seg[s].scale = sc.scale;
+        a.seg[s].y = sc.y;
+        a.seg[s].out_rows = sc.out_rows;
+        a.seg[s].n_iters = (int32_t)sc.n_iters;
+        a.seg[s].n_chunks = (int32_t)n_chunks;
+        a.seg[s].wg_start = (int32_t)wg;
+        a.seg[s].R = (int32_t)R;
+        a.seg[s].part = part;
+        if (!top1 && c.slices > 1) part += c.slices * sc.out_rows;
+        wg += n_chunks * c.slices;
+        max_rows = std::max(max_rows, sc.out_rows);
+    }
+    if (wg == 0) return VQ2_OK;
+    if (wg > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: grid too large");
+    hipStream_t st = (hipStream_t)c.stream;
+    hipError_t err;
+    if (top1) {
+        if (!c.cand) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: no candidate buffer");
+        err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
+                                    : launch_sorted_x<VQ2_DT_BF16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
+        if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
+        return argmax_final_launch(c.cand, wg, 1, top1_idx, top1_val, c.stream);
+    }
+    err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
+                                : launch_sorted_x<VQ2_DT_BF16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
+    if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
+    if (c.slices > 1) {
+        hipLaunchKernelGGL(vq_sorted_reduce_kernel, dim3((unsigned)((max_rows + 255) / 256), (unsigned)c.nseg), dim3(256),
+                           0, st, a);
+        err = hipGetLastError();
+        if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV reduce launch");
+    }
+    return VQ2_OK;
+}
+
+}  // namespace vq2

@@ -38,7 +38,7 @@ __all__ = [
     "vq_gemv_16", "vq_gemv_16_8", "vq_gemv_16_16", "vq_gemv",
     "vq_moe_parallel_gate_up", "vq_moe_parallel_down", "vq_moe_down_combine", "vq_moe_grouped",
     "vq_gemv_rht", "vq_moe_gate_up_rht", "vq_moe_down_swiglu_combine", "vq_gemm_small_m",
-    "vq_moe_router_gate_up_rht", "vq_unpack_fixed",
+    "vq_moe_router_gate_up_rht", "vq_unpack_fixed", "SortedPlanes", "vq_sorted_gemv", "vq_sorted_gemv_argmax",
     "vq_rht", "vq_swiglu_rht", "vq_router_topk", "vq_gemv_argmax", "vq_argmax",
     "vq_dequant_rows", "vq_decode_idx", "patch_transformers_kernels",
     "optimize_deltanet_layers", "Vq2Error",
@@ -338,6 +338,176 @@ def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=N
               s2, _p(_contig(cb0, "cb0")), _p(cb1.contiguous()) if cb1 is not None else None, _dt(cb0, "cb0"),
               _dt(mats[0][2], "scale"), _dt(outs[0], "y"), n, float(rs), _stream(dev))
     return outs
+
+
+# ------------------------------------------------------- code-sorted layout
+class SortedPlanes:
+    """Code-sorted internal layout of one VQ matrix (vq2_sorted_pack): the
+    reference's int16 index planes (2 bpw, or the two planes of (16,16)
+    4 bpw) repacked once, on the host, into chunks of rows whose codes are
+    sorted by value, so that a wave's centroid gathers share codebook lines.
+    Built at load time by the modules that own a matrix (PackedLinear,
+    PackedLMHead); the planes themselves stay the public format."""
+
+    def __init__(self, i0, i1, out_rows, n, device=None, threads=0, chunk_align=None):
+        lib = _lib.load()
+        n, out_rows = int(n), int(out_rows)
+        if n % 8:
+            raise Vq2Error(f"n={n} must be a multiple of 8")
+        ng = n // 8
+        i0 = _idx16(i0, "i0")
+        if i0.numel() != out_rows * ng:
+            raise Vq2Error(f"i0 has {i0.numel()} codes, expected {out_rows * ng}")
+        if i1 is not None:
+            if i1.dtype == torch.uint8:
+                raise Vq2Error("the sorted layout covers (16,) and (16,16) matrices, not (16,8)")
+            i1 = _idx16(i1, "i1")
+            if i1.numel() != i0.numel():
+                raise Vq2Error("i1 and i0 must have the same number of codes")
+        dev = torch.device(device) if device is not None else i0.device
+        if chunk_align is None:  # whole rounds of chunks over the device's CUs
+            chunk_align = _cu_count(dev) if dev.type == "cuda" else 1
+        R = int(lib.vq2_sorted_rows_per_chunk(out_rows, ng, int(chunk_align)))
+        if R == 0:
+            raise Vq2Error(f"sorted layout: n={n} unsupported")
+        self.out_rows, self.n, self.rows_per_chunk = out_rows, n, R
+        self.n_chunks = -(-out_rows // R)
+        self.has_stage2 = i1 is not None
+        h0 = i0.detach().to("cpu").contiguous()
+        h1 = None if i1 is None else i1.detach().to("cpu").contiguous()
+        stages = 2 if h1 is not None else 1
+        cap = self.n_chunks * stages * (-(-R * ng // 256) + 8)
+        chunk_it = torch.empty(self.n_chunks + 1, dtype=torch.int32)
+        chunk_it1 = torch.empty(self.n_chunks, dtype=torch.int32)
+        n_iters = ctypes.c_int64(0)
+        for _ in range(2):
+            entries = torch.empty(cap * 256, dtype=torch.int32)
+            st = lib.vq2_sorted_pack(h0.data_ptr(), None if h1 is None else h1.data_ptr(), out_rows, ng, R,
+                                     entries.data_ptr(), cap, chunk_it.data_ptr(), chunk_it1.data_ptr(),
+                                     ctypes.byref(n_iters), int(threads))
+            if st == _lib.ERR_ARG and n_iters.value > cap:
+                cap = n_iters.value
+                continue
+            _lib.check(st, "vq2_sorted_pack")
+            break
+        self.n_iters = int(n_iters.value)
+        # uint32 entries held in an int32 tensor (same bits)
+        self.entries = entries[: self.n_iters * 256].to(dev)
+        self.chunk_it = chunk_it.to(dev)
+        self.chunk_it1 = chunk_it1.to(dev)
+        self.device = dev
+
+    def mat(self, scale, y=None) -> "_lib.SortedMat":
+        _contig(scale, "scale")
+        if scale.numel() != self.out_rows:
+            raise Vq2Error(f"scale has {scale.numel()} entries, expected {self.out_rows}")
+        _dt(scale, "scale")
+        return _lib.SortedMat(self.entries.data_ptr(), self.chunk_it.data_ptr(), self.chunk_it1.data_ptr(),
+                              self.n_iters, self.rows_per_chunk, 1 if self.has_stage2 else 0, scale.data_ptr(), _p(y),
+                              self.out_rows)
+
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for t in (self.entries, self.chunk_it, self.chunk_it1))
+
+
+_CU_COUNT: dict = {}
+
+
+def _cu_count(dev: torch.device) -> int:
+    if dev.index not in _CU_COUNT:
+        _CU_COUNT[dev.index] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _CU_COUNT[dev.index]
+
+
+def sorted_slices(planes, dev) -> int:
+    """Workgroups per chunk: as many as keep the launch within one workgroup
+    per CU (the per-CU gather rate bounds this kernel, so a CU holding two
+    workgroups of one launch finishes last; measured on the gate/up pair:
+    50 chunks x 5 slices 20.0 us, x 6 slices 31 us)."""
+    chunks = sum(p.n_chunks for p in planes)
+    return max(1, min(32, _cu_count(dev) // chunks))
+
+
+def _sorted_cbs(planes, cb0, cb1):
+    _contig(cb0, "cb0")
+    if cb0.dim() != 2 or cb0.shape[0] < 65536 or cb0.shape[1] != 8:
+        raise Vq2Error(f"cb0 must be [65536, 8], got {tuple(cb0.shape)}")
+    if cb0.dtype not in (torch.float16, torch.bfloat16):
+        raise Vq2Error("the sorted layout takes fp16 / bf16 codebooks")
+    if planes[0].has_stage2:
+        if cb1 is None or cb1.dim() != 2 or cb1.shape[0] < 65536 or cb1.shape[1] != 8 or cb1.dtype != cb0.dtype:
+            raise Vq2Error("a (16,16) matrix needs cb1 [65536, 8] in the dtype of cb0")
+        _contig(cb1, "cb1")
+        return cb0, cb1
+    return cb0, None
+
+
+def _sorted_x(x, n, perm, sign, hb, rht_scale):
+    x2 = _contig(x, "x").reshape(-1)
+    if x2.numel() != n:
+        raise Vq2Error(f"the sorted GEMV takes one activation of n={n} values, got {x2.numel()}")
+    hb = int(hb or 0)
+    for t, nm, dt in ((perm, "perm", torch.int32), (sign, "sign", torch.int8)):
+        if t is not None and (t.dtype != dt or t.numel() != n or not t.is_contiguous()):
+            raise Vq2Error(f"{nm} must be a contiguous {dt} [n]")
+    sc = (float(hb) ** -0.5 if hb else 1.0) if rht_scale is None else float(rht_scale)
+    return x2, hb, sc
+
+
+def vq_sorted_gemv(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=None, rs=1.0, *,
+                   out_dtype=torch.float32, ys=None, slices=None):
+    """Batch-1 VQ GEMV of up to 4 matrices in the code-sorted layout that
+    share one activation: y_m = VQ(W_m) RHT(x) (hb > 0: the rotation is built
+    in the kernel's LDS; hb = 0: x is already rotated).  mats: list of
+    (SortedPlanes, scale).  With several workgroups (slices) per chunk a
+    second launch sums their partials.  Returns the list of outputs [out_rows]."""
+    n = int(n)
+    planes = [m[0] for m in mats]
+    if not 1 <= len(mats) <= 4 or any(p.n != n for p in planes):
+        raise Vq2Error("vq_sorted_gemv: 1..4 matrices of width n")
+    if any(p.has_stage2 != planes[0].has_stage2 for p in planes):
+        raise Vq2Error("vq_sorted_gemv: the matrices of a launch share one cfg")
+    dev = _dev(x, cb0, cb1, perm, sign, *[m[1] for m in mats], *[p.entries for p in planes])
+    cb0, cb1 = _sorted_cbs(planes, cb0, cb1)
+    x2, hb, sc = _sorted_x(x, n, perm, sign, hb, rht_scale)
+    if ys is None:
+        ys = [torch.empty(p.out_rows, dtype=out_dtype, device=dev) for p in planes]
+    arr = (_lib.SortedMat * len(mats))()
+    for k, ((p, s), y) in enumerate(zip(mats, ys)):
+        _contig(y, "y")
+        if y.numel() != p.out_rows or y.dtype != ys[0].dtype:
+            raise Vq2Error(f"vq_sorted_gemv: output {k} must be [{p.out_rows}] of the launch's dtype")
+        if s.dtype != mats[0][1].dtype:
+            raise Vq2Error("vq_sorted_gemv: the scales of a launch share a dtype")
+        arr[k] = p.mat(s, y)
+    slices = sorted_slices(planes, dev) if slices is None else int(slices)
+    lib = _lib.load()
+    ws = _workspace(dev, int(lib.vq2_sorted_gemv_workspace(arr, len(mats), slices)))
+    _lib.call("vq2_sorted_gemv", _p(x2), _dt(x2, "x"), _p(perm), _p(sign), hb, sc, len(mats), arr, _p(cb0), _p(cb1),
+              _dt(cb0, "cb0"), _dt(mats[0][1], "scale"), _dt(ys[0], "y"), n, float(rs), slices, _p(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
+    return ys
+
+
+def vq_sorted_gemv_argmax(x, planes, scale, cb0, cb1, n, perm=None, sign=None, hb=0, rht_scale=None, rs=1.0):
+    """LM head + top-1 at batch 1 over a code-sorted matrix: (idx int64 [1],
+    val fp32 [1]), torch.argmax's first maximum of the logits, which are
+    never written."""
+    n = int(n)
+    if planes.n != n:
+        raise Vq2Error("vq_sorted_gemv_argmax: planes of another width")
+    dev = _dev(x, cb0, cb1, perm, sign, scale, planes.entries)
+    cb0, cb1 = _sorted_cbs([planes], cb0, cb1)
+    x2, hb, sc = _sorted_x(x, n, perm, sign, hb, rht_scale)
+    lib = _lib.load()
+    m = planes.mat(scale)
+    ws = _workspace(dev, int(lib.vq2_sorted_gemv_argmax_workspace(ctypes.byref(m))))
+    idx = torch.empty(1, dtype=torch.int64, device=dev)
+    val = torch.empty(1, dtype=torch.float32, device=dev)
+    _lib.call("vq2_sorted_gemv_argmax", _p(x2), _dt(x2, "x"), _p(perm), _p(sign), hb, sc, ctypes.byref(m), _p(cb0),
+              _p(cb1), _dt(cb0, "cb0"), _dt(scale, "scale"), n, float(rs), _p(ws), ws.numel(), _p(idx), _p(val),
+              _stream(dev))
+    return idx, val
 
 
 # -------------------------------------------------------------- grouped MoE

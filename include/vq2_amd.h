@@ -320,6 +320,72 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
                     int64_t out_rows, int64_t n, float rs,
                     float* logits_ws, int64_t* out_idx, float* out_val, void* stream);
 
+/* Code-sorted internal layout of one VQ matrix (2 or 4 bpw), for the batch-1
+ * GEMV of large matrices.  The reference's int16 index planes stay the
+ * public format; this repack is built once at load time, on the host, and
+ * lets the lanes of a wave share codebook lines: random 16-byte centroid
+ * gathers are capped by the L2 request rate, sorted ones are not.
+ *   rows are cut into chunks of rows_per_chunk rows (at most min(2^(16 -
+ *   ceil(log2 ng)) - 1, 255); vq2_sorted_rows_per_chunk gives the default:
+ *   the rows split evenly, over a multiple of chunk_align chunks when the
+ *   chunks keep >= 128 rows, e.g. chunk_align = the CU count); every entry
+ *   is a uint32 (code << 16) | (row_in_chunk << ceil(log2 ng)) | group; a
+ *   chunk's entries are sorted by code and dealt into 64-entry instructions
+ *   in which no row repeats within a 32-lane half; 4 instructions form an
+ *   iteration of 256 entries (lane l holds entry l of each, as one
+ *   uint32x4).
+ * vq2_sorted_pack (host memory, no GPU work) fills `entries` (up to
+ * cap_iters * 256 uint32, 16-byte aligned), chunk_it [n_chunks + 1]
+ * (iteration offsets) and chunk_it1 [n_chunks] (stage-1 iterations, the
+ * stage-2 ones follow) with n_chunks = ceil(out_rows / rows_per_chunk),
+ * and sets *n_iters (also when the capacity is too small, which returns
+ * VQ2_ERR_ARG).  idx1 (the (16,16) stage-2 plane) may be NULL; n_threads
+ * <= 0: all host threads.  No reference counterpart (a load-time transform
+ * of the planes PackedLinear holds, vq2/runtime.py:70-80). */
+int64_t vq2_sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
+int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
+                    uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1,
+                    int64_t* n_iters, int n_threads);
+
+/* One packed matrix of a sorted launch (device pointers, except the struct). */
+typedef struct vq2_sorted_mat {
+    const uint32_t* entries;  /* from vq2_sorted_pack, copied to the device    */
+    const int32_t* chunk_it;  /* [n_chunks + 1]                                */
+    const int32_t* chunk_it1; /* [n_chunks]                                    */
+    int64_t n_iters;
+    int64_t rows_per_chunk;   /* the value the matrix was packed with          */
+    int has_stage2;           /* packed with idx1 (4 bpw): needs cb1          */
+    const void* scale;        /* [out_rows], dtype s_dt                        */
+    void* y;                  /* [out_rows], dtype y_dt (unused by the top-1) */
+    int64_t out_rows;
+} vq2_sorted_mat;
+
+/* Batch-1 VQ GEMV of up to 4 packed matrices sharing the activation, with
+ * the RHT of x built in the kernel's LDS (hb > 0: perm / sign nullable,
+ * rht_scale; n % 64 == 0, x 16-byte aligned) or x already rotated (hb == 0):
+ *   y_m[r] = (sum_k W_m[r, k] * xr[k]) * scale_m[r] * rs
+ * fp16 / bf16 codebooks.  `slices` workgroups share each chunk; with more
+ * than one the raw partials go to `workspace` (vq2_sorted_gemv_workspace
+ * bytes) and a second launch sums them in slice order.  Replaces FastRot +
+ * vq_gemv_16 of PackedLinear.forward (vq2/runtime.py:91-104) and its
+ * (16,16) fallback (vq2/runtime.py:105-110) for large matrices. */
+size_t vq2_sorted_gemv_workspace(const vq2_sorted_mat* mats, int n_mat, int slices);
+int vq2_sorted_gemv(const void* x, int x_dt, const int32_t* perm, const int8_t* sign, int64_t hb, float rht_scale,
+                    int n_mat, const vq2_sorted_mat* mats, const void* cb0, const void* cb1, int cb_dt, int s_dt,
+                    int y_dt, int64_t n, float rs, int slices, void* workspace, size_t ws_bytes, void* stream);
+
+/* LM head + top-1 over one packed matrix at batch 1: out_idx[0] = argmax_r
+ * y[r] (first maximum), out_val[0] = y[out_idx[0]] (may be NULL), with y as
+ * vq2_sorted_gemv computes it; no logits are written.  `workspace`:
+ * vq2_sorted_gemv_argmax_workspace bytes (one key per chunk).  Replaces
+ * PackedLMHead.forward (vq2/runtime.py:136-144) + torch.argmax
+ * (legion/engine.py:288). */
+size_t vq2_sorted_gemv_argmax_workspace(const vq2_sorted_mat* mat);
+int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const int8_t* sign, int64_t hb,
+                           float rht_scale, const vq2_sorted_mat* mat, const void* cb0, const void* cb1, int cb_dt,
+                           int s_dt, int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
+                           float* out_val, void* stream);
+
 /* Rotated-space dequantisation of rows [r0, r1) (debug / audit):
  *   W[r, 8g+j] = (f32(cb0[i0]) [+ f32(cb1[i1])]) * f32(scale[r]), fp32 [r1-r0, n]
  * rounded exactly in that order (no contraction).

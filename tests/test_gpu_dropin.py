@@ -157,3 +157,30 @@ def test_small_m_workspace_outlives_captured_graph(dev):
         del junk
     _, y64 = O.vq_gemv(xa.cpu(), ma["idx0"], None, cb.cpu(), None, ma["scale"])
     assert max(O.max_rel_err(ref_a[b].cpu().numpy(), y64[b]) for b in range(8)) < TOL
+
+
+@pytest.mark.parametrize("cfg,out,n", [((16, 16), 6144, 2048), ((16,), 151936, 2048), ((16, 16), 2048, 6144)])
+def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
+    """Large PackedLinear matrices keep a code-sorted copy of their planes and
+    run batch 1 on it (RHT fused in the kernel); the outputs and the LM-head
+    top-1 match the oracle, and batch 2 (gather kernel) agrees with them."""
+    from compressai_amd.runtime import PackedLinear, PackedLMHead
+
+    bpw = 4 if cfg == (16, 16) else 2
+    cbs = {"16": synth.codebook(9380).to(dev), "16_16": synth.codebook(9381).to(dev)}
+    m = synth.vq_matrix(9382 + out, out, n, bpw=bpw)
+    lin = PackedLinear((out, n), cfg, f"t_sorted_{out}_{n}", [m["idx0"], m["idx1"]][:len(cfg)], m["scale"], cbs, dev)
+    assert lin.sorted is not None and lin.sorted.has_stage2 == (bpw == 4)
+    x = synth.activations(9383, (1, n), dtype=torch.float32)
+    y = lin(x.to(dev), out_dtype=torch.float32)
+    perm, sign = _rot_np(lin.rot)
+    xr = O.rht(x, perm, sign, lin.rot.hb).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu() if bpw == 4 else None,
+                       lin.scale.cpu())
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+    y2 = lin(torch.cat([x, x]).to(dev), out_dtype=torch.float32)  # batch 2: the gather kernel
+    assert O.max_rel_err(y2[1].cpu().numpy(), y[0].cpu().numpy()) < 1e-5
+    if cfg == (16,):
+        idx, val = PackedLMHead(lin).argmax(x.to(dev))
+        assert int(idx[0]) == int(np.argmax(y64[0]))
+        assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())

@@ -1,0 +1,185 @@
+"""GPU parity of the code-sorted VQ GEMV (vq2_sorted_gemv / _argmax, through
+the C ABI) against the fp64 oracle on the same seeded inputs: the config 1-3
+shapes, ragged row counts and non-power-of-two widths, 2 and 4 bpw, fp16 and
+bf16 codebooks, the fused RHT prologue and pre-rotated activations, one or
+several workgroups per chunk, several matrices per launch, and the fused
+LM-head top-1 (ties resolve to the lower row, as torch.argmax).
+
+Tolerance: max_i |y_i - ref_i| / max_i |ref_i| <= 1e-3 (the decode-path
+contract), observed ~1e-7: fp32 accumulation in another order."""
+import numpy as np
+import pytest
+import torch
+
+from compressai_amd import kernels as K, synth
+from oracle import vq2_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _mk(seed, rows, n, bpw, dev, cb_dtype=torch.float16):
+    m = synth.vq_matrix(seed, rows, n, bpw=bpw)
+    cb0 = synth.codebook(seed + 1, dtype=cb_dtype)
+    cb1 = synth.codebook(seed + 2, dtype=cb_dtype) if bpw == 4 else None
+    sp = K.SortedPlanes(m["idx0"], m["idx1"], rows, n, device=dev)
+    return m, cb0, cb1, sp
+
+
+@pytest.mark.parametrize("rows,n,bpw,fused,slices", [
+    (2048, 2048, 2, True, None),     # configs[0] / o projection
+    (6144, 2048, 4, True, None),     # gate / up
+    (2048, 6144, 4, True, None),     # down, 3 x 2048-point RHT blocks
+    (1000, 512, 2, False, 3),
+    (97, 800, 2, False, 1),          # ng = 100: not a power of two
+    (517, 2048, 4, True, 7),
+    (300, 2048, 2, True, 64),        # more slices than iterations per chunk
+])
+def test_sorted_gemv_vs_oracle(dev, rows, n, bpw, fused, slices):
+    m, cb0, cb1, sp = _mk(9500 + rows + n, rows, n, bpw, dev)
+    x = synth.activations(9501 + rows, n, dtype=torch.float16)
+    perm, sign = synth.permutation(9502, n), synth.signs(9503, n)
+    if fused:
+        (y,) = K.vq_sorted_gemv(x.to(dev), [(sp, m["scale"].to(dev))], cb0.to(dev), None if cb1 is None else cb1.to(dev),
+                                n, perm.to(dev), sign.to(dev), 2048, slices=slices)
+        xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    else:
+        xr = (synth.activations(9504 + rows, n, dtype=torch.float32) * 0.5).numpy()
+        (y,) = K.vq_sorted_gemv(torch.from_numpy(xr).to(dev), [(sp, m["scale"].to(dev))], cb0.to(dev),
+                                None if cb1 is None else cb1.to(dev), n, hb=0, slices=slices)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert y.shape == (rows,)
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+
+
+def test_sorted_gemv_bf16_codebook_and_outputs(dev):
+    rows, n = 1536, 2048
+    m, cb0, cb1, sp = _mk(9520, rows, n, 4, dev, cb_dtype=torch.bfloat16)
+    x = synth.activations(9521, n, dtype=torch.bfloat16)
+    sc = m["scale"].to(torch.bfloat16)
+    perm, sign = synth.permutation(9522, n), synth.signs(9523, n)
+    (y,) = K.vq_sorted_gemv(x.to(dev), [(sp, sc.to(dev))], cb0.to(dev), cb1.to(dev), n, perm.to(dev), sign.to(dev),
+                            2048, out_dtype=torch.bfloat16)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, sc)
+    err = np.abs(y.float().cpu().numpy() - y64[0])
+    assert np.all(err <= 2.0 ** -8 * np.abs(y64[0]) + 1e-5 * np.abs(y64[0]).max())  # one bf16 rounding
+
+
+def test_sorted_gemv_qkv_segments_and_determinism(dev):
+    """q / k / v in one launch (shared RHT), equal to the oracle and to
+    itself bit for bit over repeated calls."""
+    n = 2048
+    cb0 = synth.codebook(9530)
+    shapes = [2048, 512, 512]
+    ms = [synth.vq_matrix(9531 + k, r, n, bpw=2) for k, r in enumerate(shapes)]
+    sps = [K.SortedPlanes(m["idx0"], None, r, n, device=dev) for m, r in zip(ms, shapes)]
+    x = synth.activations(9535, n, dtype=torch.float16)
+    perm, sign = synth.permutation(9536, n), synth.signs(9537, n)
+    mats = [(sp, m["scale"].to(dev)) for sp, m in zip(sps, ms)]
+    ys = K.vq_sorted_gemv(x.to(dev), mats, cb0.to(dev), None, n, perm.to(dev), sign.to(dev), 2048)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    for y, m in zip(ys, ms):
+        _, y64 = O.vq_gemv(xr, m["idx0"], None, cb0, None, m["scale"])
+        assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+    again = K.vq_sorted_gemv(x.to(dev), mats, cb0.to(dev), None, n, perm.to(dev), sign.to(dev), 2048)
+    for a, b in zip(ys, again):
+        assert torch.equal(a, b)
+
+
+def test_sorted_multi_slice_graph_replays(dev):
+    """A multi-slice launch (partials in the split workspace, summed by the
+    reduce launch) captured in a HIP graph: every replay, with eager launches
+    on the same matrix in between, equals the eager result bit for bit."""
+    rows, n = 6144, 2048
+    m, cb0, cb1, sp = _mk(9570, rows, n, 4, dev)
+    x = synth.activations(9571, n, dtype=torch.float16).to(dev)
+    perm, sign = synth.permutation(9572, n).to(dev), synth.signs(9573, n).to(dev)
+    sc, c0, c1 = m["scale"].to(dev), cb0.to(dev), cb1.to(dev)
+    y = torch.empty(rows, device=dev)
+    run = lambda: K.vq_sorted_gemv(x, [(sp, sc)], c0, c1, n, perm, sign, 2048, ys=[y], slices=5)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        run()
+        ref = y.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run()
+    torch.cuda.synchronize(dev)
+    for r in range(4):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, ref), r
+        run()                                   # eager call between replays
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, ref), r
+    xr = O.rht(x.cpu(), perm.cpu(), sign.cpu(), 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert O.max_rel_err(ref.cpu().numpy(), y64[0]) < TOL
+
+
+def test_sorted_matches_gather_kernel(dev):
+    """The sorted kernel and the gather kernel (vq_gemv_rht) agree to fp32
+    accumulation-order rounding on the gate/up shape."""
+    rows, n = 6144, 2048
+    m, cb0, cb1, sp = _mk(9540, rows, n, 4, dev)
+    x = synth.activations(9541, n, dtype=torch.float16).to(dev)
+    perm, sign = synth.permutation(9542, n).to(dev), synth.signs(9543, n).to(dev)
+    (ys,) = K.vq_sorted_gemv(x, [(sp, m["scale"].to(dev))], cb0.to(dev), cb1.to(dev), n, perm, sign, 2048)
+    (yg,) = K.vq_gemv_rht(x, [(m["idx0"].to(dev), m["idx1"].to(dev), m["scale"].to(dev), rows)], cb0.to(dev),
+                          cb1.to(dev), n, perm, sign, 2048)
+    assert O.max_rel_err(ys.cpu().numpy(), yg.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_sorted_lm_head_top1_full_size(dev, fused):
+    """configs[2] LM head 151936 x 2048 at 2 bpw, batch 1: the fused top-1
+    equals the argmax of the oracle's logits."""
+    rows, n = 151936, 2048
+    m, cb0, _, sp = _mk(9550, rows, n, 2, dev)
+    perm, sign = synth.permutation(9552, n), synth.signs(9553, n)
+    if fused:
+        x = synth.activations(9551, n, dtype=torch.float16)
+        idx, val = K.vq_sorted_gemv_argmax(x.to(dev), sp, m["scale"].to(dev), cb0.to(dev), None, n, perm.to(dev),
+                                           sign.to(dev), 2048)
+        xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    else:
+        xr = synth.activations(9554, n, dtype=torch.float32).numpy()
+        idx, val = K.vq_sorted_gemv_argmax(torch.from_numpy(xr).to(dev), sp, m["scale"].to(dev), cb0.to(dev), None,
+                                           n)
+    _, y64 = O.vq_gemv(xr, m["idx0"], None, cb0, None, m["scale"])
+    top = np.sort(y64[0])[-2:]
+    assert top[1] - top[0] > 1e-5 * abs(top[1])  # a unique winner at this seed
+    assert int(idx[0]) == int(np.argmax(y64[0]))
+    assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
+
+
+def test_sorted_top1_ties_pick_lower_row(dev):
+    """Two chunks with identical codes and scales (so the kernel sums their
+    rows in the same order and the values tie exactly) hold the maximum at
+    rows 100 and 100 + 5 R: the lower row wins, as torch.argmax."""
+    rows, n = 4096, 2048
+    m = synth.vq_matrix(9560, rows, n, bpw=2)
+    i0 = m["idx0"].clone()
+    R = K.SortedPlanes(i0, None, rows, n, device="cpu").rows_per_chunk
+    sc = m["scale"].clone()
+    i0[5 * R:6 * R] = i0[:R]
+    sc[5 * R:6 * R] = sc[:R]
+    cb = synth.codebook(9561)
+    x = synth.activations(9562, n, dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    if y64[0, 100] < 0:
+        x = -x
+        _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    boost = float(2.0 ** np.ceil(np.log2(np.abs(y64).max() / (y64[0, 100] / float(sc[100])) + 1)))
+    sc[100] = sc[5 * R + 100] = boost
+    _, y64 = O.vq_gemv(x, i0, None, cb, None, sc)
+    assert np.argmax(y64[0]) == 100 and y64[0, 100] == y64[0, 5 * R + 100]
+    sp = K.SortedPlanes(i0, None, rows, n, device=dev)
+    (y,) = K.vq_sorted_gemv(x.to(dev), [(sp, sc.to(dev))], cb.to(dev), None, n, hb=0, slices=1)
+    assert float(y[100]) == float(y[5 * R + 100])   # the tie is exact in the kernel too
+    idx, _ = K.vq_sorted_gemv_argmax(x.to(dev), sp, sc.to(dev), cb.to(dev), None, n)
+    assert int(idx[0]) == 100
