@@ -18,7 +18,7 @@ T = 1) in us per layer over a 40-layer resident pool, the config-3 LM head
 the host (``cpu_baseline``).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                       [--only dominant|copy] (single-kernel modes for rocprofv3 --pmc runs)
+                       [--only dominant|dominant_gather|copy] (single-launch modes for rocprofv3 --pmc runs)
 """
 from __future__ import annotations
 
@@ -63,7 +63,9 @@ def rand_scale(n, g, dev):
 
 
 class DenseLayers:
-    """L layer sets of the configs[1] projections (device-resident)."""
+    """L layer sets of the configs[1] projections (device-resident).  As
+    PackedLinear does, the large matrices (gate, up, down: >= 2M codes) also
+    get the code-sorted layout, packed once here."""
 
     PROJ = [  # name, out, n, bpw
         ("q", Q_OUT, HIDDEN, 2), ("k", KV_OUT, HIDDEN, 2), ("v", KV_OUT, HIDDEN, 2), ("o", HIDDEN, HIDDEN, 2),
@@ -73,20 +75,27 @@ class DenseLayers:
     def __init__(self, L, dev):
         import torch
 
-        from compressai_amd import synth
+        from compressai_amd import kernels as K, synth
+        from compressai_amd.runtime import SORTED_MIN_CODES
 
         self.L, self.dev = L, dev
         g = torch.Generator(device=dev).manual_seed(2000)
         self.cb0 = synth.codebook(2000).to(dev)
         self.cb1 = synth.codebook(2001).to(dev)
         self.layers = []
+        t0 = time.perf_counter()
         for _ in range(L):
             lay = {}
             for name, out, n, bpw in self.PROJ:
                 i0 = rand_i16((out, n // 8), g, dev)
                 i1 = rand_i16((out, n // 8), g, dev) if bpw == 4 else None
-                lay[name] = (i0, i1, rand_scale(out, g, dev), out, n)
+                sp = None
+                if out * (n // 8) * (2 if bpw == 4 else 1) >= SORTED_MIN_CODES:
+                    sp = K.SortedPlanes(i0, i1, out, n, device=dev)
+                lay[name] = (i0, i1, rand_scale(out, g, dev), out, n, sp)
             self.layers.append(lay)
+        log(f"dense: {L} layer sets generated, large matrices packed to the sorted layout in "
+            f"{time.perf_counter() - t0:.1f} s")
         self.bytes_per_step = sum(out * (n // 8) * 2 * (2 if bpw == 4 else 1) + out * 2
                                   for _, out, n, bpw in self.PROJ)
         self.x_attn = synth.activations(2004, HIDDEN).to(dev)
@@ -99,18 +108,10 @@ class DenseLayers:
         self.perm_h = synth.permutation(2006, HIDDEN).to(dev)
         self.perm_i = synth.permutation(2016, INTER).to(dev)
         f32 = dict(dtype=torch.float32, device=dev)
-        self.xr_a, self.xr_o, self.xr_m = (torch.empty(HIDDEN, **f32) for _ in range(3))
-        self.xr_d = torch.empty(INTER, **f32)
         self.y = {name: torch.empty(out, **f32) for name, out, _, _ in self.PROJ}
 
-    def gemv(self, lay, name, xr):
-        from compressai_amd import kernels as K
-
-        i0, i1, s, out, n = lay[name]
-        K.vq_gemv(xr, i0, i1, self.cb0, self.cb1 if i1 is not None else None, s, out, n, 1.0, y=self.y[name])
-
     def fused(self, lay, names, x, perm, sign):
-        """One launch: RHT of x built in LDS + the GEMVs of `names`."""
+        """One gather-kernel launch: RHT of x built in LDS + the GEMVs of `names`."""
         from compressai_amd import kernels as K
 
         mats = [(lay[nm][0], lay[nm][1], lay[nm][2], lay[nm][3]) for nm in names]
@@ -118,9 +119,27 @@ class DenseLayers:
         K.vq_gemv_rht(x, mats, self.cb0, self.cb1 if mats[0][1] is not None else None, n, perm, sign, 2048,
                       ys=[self.y[nm] for nm in names])
 
+    def sorted(self, lay, names, x, perm, sign):
+        """Sorted-layout launch (RHT built in LDS) + its slice reduce."""
+        from compressai_amd import kernels as K
+
+        n = lay[names[0]][4]
+        K.vq_sorted_gemv(x, [(lay[nm][5], lay[nm][2]) for nm in names], self.cb0,
+                         self.cb1 if lay[names[0]][1] is not None else None, n, perm, sign, 2048,
+                         ys=[self.y[nm] for nm in names])
+
     def step(self, l):
-        """One decoder layer's projections: 4 launches (q/k/v, o, gate/up,
-        down), each rotating its activation in LDS."""
+        """One decoder layer's projections, as PackedLinear runs them at batch
+        1: q/k/v and o on the gather kernel, gate/up and down on the sorted
+        layout; every launch rotates its activation in LDS."""
+        lay = self.layers[l]
+        self.fused(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
+        self.fused(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
+        self.sorted(lay, ("gate", "up"), self.x_mlp, self.perm_h, self.sign_h)
+        self.sorted(lay, ("down",), self.x_down, self.perm_i, self.sign_i)
+
+    def step_gather(self, l):
+        """The same step with every matrix on the gather kernel (reference layout only)."""
         lay = self.layers[l]
         self.fused(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
         self.fused(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
@@ -204,19 +223,33 @@ def bench_dense(args, dev):
         f"(min {per_step[0] * 1e3:.2f}, max {per_step[-1] * 1e3:.2f}; host {host_ms:.3f} ms per repetition) -> "
         f"{gbps:.1f} GB/s")
 
-    # dominant kernel: the fused gate/up launch (RHT + two 6144 x 2048 4 bpw
-    # GEMVs), back to back over the layer sets, on the replay stream
+    # the same step on the gather kernel only (reference layout)
+    gg = capture(dl.step_gather, L, dev)
+    time_graph(gg, 1, dev)
+    gather_us = statistics.median(time_graph(gg, max(1, args.steps // L), dev)[0] * 1e3 / (max(1, args.steps // L) * L)
+                                  for _ in range(REPEATS))
+    del gg
+    log(f"dense, gather kernel only: {gather_us:.2f} us/step, "
+        f"{dl.bytes_per_step / (gather_us * 1e-6) / 1e9:.1f} GB/s")
+
+    # dominant launch: gate + up (RHT + two 6144 x 2048 4 bpw matrices) on the
+    # sorted layout (the sorted kernel, then its slice reduce), back to back
+    # over the layer sets on the replay stream; also the gather-kernel launch
     dom_bytes = 2 * (INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2)
-    gd = capture(lambda l: dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h), L, dev)
-    time_graph(gd, 2, dev)
-    dreps = max(4, 2000 // L)
-    dus = sorted(time_graph(gd, dreps, dev)[0] * 1e3 / (dreps * L) for _ in range(REPEATS))
-    dom_us = statistics.median(dus)
+    res = {}
+    for name, fn in (("sorted", dl.sorted), ("gather", dl.fused)):
+        gd = capture(lambda l, fn=fn: fn(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h), L, dev)
+        time_graph(gd, 2, dev)
+        dreps = max(4, 2000 // L)
+        res[name] = statistics.median(time_graph(gd, dreps, dev)[0] * 1e3 / (dreps * L) for _ in range(REPEATS))
+        del gd
+        log(f"gate+up launch ({name}): {res[name]:.2f} us/call, {dom_bytes / (res[name] * 1e-6) / 1e9:.1f} GB/s")
+    dom_us = res["sorted"]
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
-    log(f"dominant launch gate+up (RHT + 2 x 4 bpw 6144x2048): {dom_us:.2f} us/launch, {dom_gbps:.1f} GB/s")
     return dict(steps=args.steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
                 dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl,
-                spread_us=[round(per_step[0] * 1e3, 3), round(per_step[-1] * 1e3, 3)])
+                spread_us=[round(per_step[0] * 1e3, 3), round(per_step[-1] * 1e3, 3)],
+                gather_step_us=gather_us, dom_gather_us=res["gather"])
 
 
 def bench_config0(args, dev, copies=1024):
@@ -302,6 +335,9 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
 
 
 def bench_lm_head(args, dev, batch=1, copies=14):
+    """LM head 151936 x 2048 at 2 bpw + top-1 over 14 copies
+    (1.1 GiB).  Batch 1: the sorted layout (as PackedLMHead.argmax runs it)
+    and the gather kernel; batch 4: the matrix-core path."""
     import torch
 
     from compressai_amd import kernels as K, synth
@@ -309,24 +345,42 @@ def bench_lm_head(args, dev, batch=1, copies=14):
     out, n = 151936, 2048
     g = torch.Generator(device=dev).manual_seed(3000)
     cb = synth.codebook(3000).to(dev)
-    mats = [(rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)) for _ in range(copies)]
+    mats = []
+    for _ in range(copies):
+        i0, s = rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)
+        mats.append((i0, s, K.SortedPlanes(i0, None, out, n, device=dev) if batch == 1 else None))
     x = synth.activations(3004, (batch, n), dtype=torch.float32).to(dev)
     ws = torch.empty(batch, out, dtype=torch.float32, device=dev)
     res = [None] * copies
+    nbytes = out * (n // 8) * 2 + out * 2
 
-    def fwd(l):
-        i0, s = mats[l]
+    def run(fwd):
+        gr = capture(fwd, copies, dev)
+        time_graph(gr, 2, dev)
+        reps = max(5, 200 // copies)
+        us = statistics.median(time_graph(gr, reps, dev)[0] * 1e3 / (reps * copies) for _ in range(REPEATS))
+        del gr
+        return us
+
+    def f_gather(l):
+        i0, s, _ = mats[l]
         res[l] = K.vq_gemv_argmax(x, i0, None, cb, None, s, out, n, logits_ws=ws)
 
-    gr = capture(fwd, copies, dev)
-    time_graph(gr, 2, dev)
-    reps = max(5, 200 // copies)
-    ms, _ = time_graph(gr, reps, dev)
-    us = ms * 1e3 / (reps * copies)
-    nbytes = out * (n // 8) * 2 + out * 2
+    def f_sorted(l):
+        _, s, sp = mats[l]
+        res[l] = K.vq_sorted_gemv_argmax(x, sp, s, cb, None, n)
+
+    out_d = {}
+    if batch == 1:
+        us = run(f_sorted)
+        out_d["gather_us"] = run(f_gather)
+        log(f"lm head B=1 (gather kernel): {out_d['gather_us']:.2f} us/call")
+    else:
+        us = run(f_gather)
     gbps = nbytes / (us * 1e-6) / 1e9
     log(f"lm head B={batch}: {us:.2f} us/call, {gbps:.1f} GB/s")
-    return dict(us=us, gbps=gbps)
+    out_d.update(us=us, gbps=gbps)
+    return out_d
 
 
 def bench_small_m(args, dev):
@@ -500,7 +554,7 @@ def cpu_baseline(dl, budget_s=20.0):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    lay = {k: tuple(t.cpu() if hasattr(t, "cpu") else t for t in v) for k, v in dl.layers[0].items()}
+    lay = {k: tuple(t.cpu() if hasattr(t, "cpu") else t for t in v[:5]) for k, v in dl.layers[0].items()}
     cb0, cb1 = dl.cb0.cpu(), dl.cb1.cpu()
     rot_h = CpuRot(dl.perm_h.cpu(), dl.sign_h.cpu(), 2048)
     rot_i = CpuRot(dl.perm_i.cpu(), dl.sign_i.cpu(), 2048)
@@ -557,9 +611,10 @@ def cpu_moe_baseline(moe, budget_s=10.0):
 
 
 def traffic_from_profiles():
-    """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 --pmc summary (profiles/gemv4_gate_pmc.json), if present."""
-    p = ROOT / "profiles" / "gemv4_gate_pmc.json"
+    """HBM bytes per call of the dominant launch pair (sorted gate+up kernel +
+    its slice reduce), from the committed rocprofv3 --pmc summary
+    (profiles/sorted_gate_up_pmc.json), if present."""
+    p = ROOT / "profiles" / "sorted_gate_up_pmc.json"
     try:
         return json.loads(p.read_text()).get("traffic_bytes_per_launch")
     except (OSError, ValueError):
@@ -577,7 +632,7 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "copy"], default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy"], default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -597,12 +652,13 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device: {torch.cuda.get_device_name(0)}, {torch.cuda.get_device_properties(0).multi_processor_count} CUs")
 
-    if args.only == "dominant":
+    if args.only in ("dominant", "dominant_gather"):
         dl = DenseLayers(args.layers, dev)
+        fn = dl.sorted if args.only == "dominant" else dl.fused
         for l in range(args.layers):
-            dl.fused(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
+            fn(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
         torch.cuda.synchronize(dev)
-        log("dominant-only run done")
+        log(f"{args.only}-only run done")
         return
     if args.only == "copy":
         a = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -639,7 +695,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "configs[1]: dense decoder-layer projection set, batch 1, hidden 2048 (q,k,v,o 2 bpw; "
-                        "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/scales/activations, fp32 out",
+                        "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/"
+                        "scales/activations, fp32 out; q/k/v, o on the gather kernel, gate/up, down on the "
+                        "code-sorted layout (as PackedLinear at batch 1)",
             "layers_cycled": d["layers"],
             "bytes_per_step": d["bytes_per_step"],
             "graph_replay": True,
@@ -652,6 +710,9 @@ def main():
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "lm_head_us_b1_gather_kernel": None if lm1 is None else round(lm1["gather_us"], 3),
+        "dense_step_us_gather_kernel": round(d["gather_step_us"], 3),
+        "gate_up_us_gather_kernel": round(d["dom_gather_us"], 3),
         "config0": c0,
         "dense_spread_us": d["spread_us"],
         "timing": f"median of {REPEATS} timed repetitions of the steps (HIP events on the replay stream)",
@@ -659,15 +720,17 @@ def main():
         "unpack_fixed": up,
         "paged_moe_t1": pgd,
         "roofline": {
-            "kernel": "vq_gemv_kernel (fused RHT) gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1",
+            "kernel": "vq_sorted_kernel (fused RHT) + vq_sorted_reduce_kernel, gate+up: 2 x 4 bpw (16,16) "
+                      "6144 x 2048, batch 1, one call = both kernels",
             "bound": "hbm",
             "achieved": round(d["dom_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(d["dom_gbps"] / PEAK_HBM_GBPS, 5),
             "traffic": traffic_from_profiles(),
-            "traffic_source": "profiles/gemv4_gate_pmc.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
-                              "bench.py --only dominant, scaled by a 64 MiB copy (stored profile, not this run)",
+            "traffic_source": "profiles/sorted_gate_up_pmc.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                              "bench.py --only dominant (both kernels), scaled by a 64 MiB copy (stored profile, "
+                              "not this run)",
             "us_per_launch": round(d["dom_us"], 3),
             "algorithmic_bytes_per_launch": d["dom_bytes"],
         },
