@@ -18,7 +18,7 @@ T = 1) in us per layer over a 40-layer resident pool, the config-3 LM head
 the host (``cpu_baseline``).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                       [--only dominant|dominant_gather|copy] (single-launch modes for rocprofv3 --pmc runs)
+                       [--only dominant|dominant_gather|copy|moe] (single-launch modes for rocprofv3 runs)
 """
 from __future__ import annotations
 
@@ -632,7 +632,7 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy"], default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy", "moe"], default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -659,6 +659,10 @@ def main():
             fn(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
         torch.cuda.synchronize(dev)
         log(f"{args.only}-only run done")
+        return
+    if args.only == "moe":
+        res = bench_moe(args, dev, n_layers=args.layers)
+        log("moe-only run done: " + ", ".join(f"T={T} {res[T]['us']:.2f} us" for T in (1, 8)))
         return
     if args.only == "copy":
         a = torch.empty(64 << 20, dtype=torch.uint8, device=dev)

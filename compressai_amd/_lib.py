@@ -70,6 +70,11 @@ SIGNATURES = {
     "vq2_sorted_gemv_argmax_workspace": ([_vp], ctypes.c_size_t),
     "vq2_sorted_gemv_argmax": ([_vp, _i32, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _i32, _i32, _i64, _f32, _vp,
                                 ctypes.c_size_t, _vp, _vp, _vp], _i32),
+    "vq2_sorted_pack_pool": ([_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32], _i32),
+    "vq2_sorted_moe_workspace": ([_i64, _i32, _i64, _i64, _i32, _i32], ctypes.c_size_t),
+    "vq2_sorted_moe": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _vp, _vp,
+                        _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
+                        ctypes.c_size_t, _vp], _i32),
     "vq2_dequant_rows": ([_vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp], _i32),
     "vq2_decode_idx": ([_vp, _i32, _i64, _vp, _vp], _i32),
     "vq2_unpack_fixed": ([_vp, _i64, _i32, _i64, _vp, _vp], _i32),
@@ -94,6 +99,19 @@ class SortedMat(ctypes.Structure):
                 ("n_iters", ctypes.c_int64), ("rows_per_chunk", ctypes.c_int64), ("has_stage2", ctypes.c_int),
                 ("scale", ctypes.c_void_p),
                 ("y", ctypes.c_void_p), ("out_rows", ctypes.c_int64)]
+
+
+class SortedPool(ctypes.Structure):
+    """struct vq2_sorted_pool of include/vq2_amd.h"""
+    _fields_ = [("entries", ctypes.c_void_p), ("iters_per_chunk", ctypes.c_int64), ("n_iters", ctypes.c_int64),
+                ("rows_per_chunk", ctypes.c_int64), ("rows", ctypes.c_int64), ("ng", ctypes.c_int64),
+                ("scale", ctypes.c_void_p), ("scale_dt", ctypes.c_int)]
+
+
+class RotTables(ctypes.Structure):
+    """struct vq2_rot_tables of include/vq2_amd.h"""
+    _fields_ = [("perm", ctypes.c_void_p), ("sign", ctypes.c_void_p), ("hb", ctypes.c_int64),
+                ("scale", ctypes.c_float)]
 
 
 def header_symbols() -> list[str]:

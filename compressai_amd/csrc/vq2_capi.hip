@@ -738,6 +738,72 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
     return sorted_launch(c, out_idx, out_val);
 }
 
+int vq2_sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
+                         uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
+                         int n_threads)
+{
+    clear_error();
+    CHECK(idx && entries && iters_per_chunk && n_iters, "vq2_sorted_pack_pool: NULL pointer argument");
+    CHECK(n_experts >= 1 && rows >= 1 && ng >= 1, "vq2_sorted_pack_pool: bad sizes n_experts=%lld rows=%lld ng=%lld",
+          (long long)n_experts, (long long)rows, (long long)ng);
+    return sorted_pack_pool(idx, n_experts, rows, ng, rows_per_chunk, entries, cap_iters, iters_per_chunk, n_iters,
+                            n_threads);
+}
+
+size_t vq2_sorted_moe_workspace(int64_t tokens, int pairs_per_token, int64_t hidden, int64_t inter, int slices_gu,
+                                int slices_dn)
+{
+    if (tokens < 1 || pairs_per_token < 1 || hidden < 1 || inter < 1 || slices_gu < 1 || slices_dn < 1) return 0;
+    return sorted_moe_workspace_bytes(tokens * pairs_per_token, hidden, inter, slices_gu, slices_dn);
+}
+
+int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token, const void* ids, int ids_i64,
+                   const float* w, const void* logits, int l_dt, int64_t n_routed, int top_k, int64_t shared_id,
+                   const void* shared_gate, int g_dt, int32_t* ids_out, float* w_out, int64_t n_experts,
+                   int64_t hidden, int64_t inter, const vq2_sorted_pool* gate_up, const vq2_sorted_pool* down,
+                   const void* cb, int cb_dt, const vq2_rot_tables* rot_h, const vq2_rot_tables* rot_i, void* out,
+                   int out_dt, int slices_gu, int slices_dn, void* workspace, size_t ws_bytes, void* stream)
+{
+    clear_error();
+    CHECK(gate_up && down && rot_h && rot_i, "vq2_sorted_moe: NULL pool or rotation");
+    SortedMoeCall c{};
+    c.h = h;
+    c.h_dt = h_dt;
+    c.tokens = tokens;
+    c.P = pairs_per_token;
+    c.ids = ids;
+    c.ids_i64 = ids_i64;
+    c.w = w;
+    c.logits = logits;
+    c.l_dt = l_dt;
+    c.n_routed = n_routed;
+    c.top_k = top_k;
+    c.shared_id = shared_id;
+    c.shared_gate = shared_gate;
+    c.g_dt = g_dt;
+    c.ids_out = ids_out;
+    c.w_out = w_out;
+    c.n_experts = n_experts;
+    c.hidden = hidden;
+    c.inter = inter;
+    c.gate_up = SortedPoolCall{gate_up->entries, gate_up->iters_per_chunk, gate_up->n_iters, gate_up->rows_per_chunk,
+                               gate_up->rows, gate_up->ng, gate_up->scale, gate_up->scale_dt};
+    c.down = SortedPoolCall{down->entries, down->iters_per_chunk, down->n_iters, down->rows_per_chunk, down->rows,
+                            down->ng, down->scale, down->scale_dt};
+    c.cb = cb;
+    c.cb_dt = cb_dt;
+    c.rot_h = SortedRot{rot_h->perm, rot_h->sign, rot_h->hb, rot_h->scale};
+    c.rot_i = SortedRot{rot_i->perm, rot_i->sign, rot_i->hb, rot_i->scale};
+    c.out = out;
+    c.out_dt = out_dt;
+    c.slices_gu = slices_gu;
+    c.slices_dn = slices_dn;
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
+    c.stream = stream;
+    return sorted_moe_launch(c);
+}
+
 int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
                      const void* scale, int s_dt, int64_t r0, int64_t r1, int64_t n, float* out, void* stream)
 {

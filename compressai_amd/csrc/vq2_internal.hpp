@@ -164,6 +164,70 @@ size_t sorted_workspace_bytes(const SortedCall& c);
 // top1_idx non-null: fused top-1 (one matrix, one slice) instead of y
 int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);
 
+// MoE experts over code-sorted expert pools (vq2_sorted_moe.hip).
+int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
+                     uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
+                     int n_threads);
+
+struct SortedPoolCall {
+    const uint32_t* entries;
+    int64_t iters_per_chunk;  // every chunk padded to this many iterations
+    int64_t n_iters;
+    int64_t rows_per_chunk;
+    int64_t rows;  // rows per expert
+    int64_t ng;    // groups per row
+    const void* scale;
+    int scale_dt;
+};
+
+struct SortedRot {
+    const int32_t* perm;
+    const int8_t* sign;
+    int64_t hb;
+    float scale;
+};
+
+struct SortedMoeCall {
+    const void* h;
+    int h_dt;
+    int64_t tokens;
+    int P;  // pairs per token
+    // routing given: ids [tokens * P] (int32 / int64), w [tokens * P]
+    const void* ids;
+    int ids_i64;
+    const float* w;
+    // or the fused router (logits non-null): P = top_k + 1, slot top_k the
+    // shared expert; writes ids_out / w_out
+    const void* logits;
+    int l_dt;
+    int64_t n_routed;
+    int top_k;
+    int64_t shared_id;
+    const void* shared_gate;
+    int g_dt;
+    int32_t* ids_out;
+    float* w_out;
+    int64_t n_experts;
+    int64_t hidden;
+    int64_t inter;
+    SortedPoolCall gate_up;
+    SortedPoolCall down;
+    const void* cb;
+    int cb_dt;
+    SortedRot rot_h;
+    SortedRot rot_i;
+    void* out;
+    int out_dt;
+    int slices_gu;
+    int slices_dn;
+    void* workspace;
+    size_t ws_bytes;
+    void* stream;
+};
+
+size_t sorted_moe_workspace_bytes(int64_t n_pairs, int64_t hidden, int64_t inter, int slices_gu, int slices_dn);
+int sorted_moe_launch(const SortedMoeCall& c);
+
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
                const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,
                int inverse, int swiglu, int64_t inter, void* stream);

@@ -72,14 +72,12 @@ __device__ __forceinline__ float router_shared_weight(const void* gate, int g_dt
     return 1.0f / (1.0f + __expf(-dd));
 }
 
-// Top-k of token t by one full wave (RPL * 64 >= n_e): lane r < k ends with
-// the round-r choice (probability `mine`, expert `my_id`); `tot` (uniform) is
-// the sum of the k chosen probabilities, so weight r = mine / tot.
+// Routing probabilities of token t by one full wave (RPL * 64 >= n_e): p[j]
+// of expert j * 64 + lane is softmax(logits)[e] in fp32, -1 past n_e.
 template <int RPL>
-__device__ __forceinline__ void router_select(const void* logits, int l_dt, int64_t t, int64_t n_e, int k, int lane,
-                                              float& mine, int& my_id, float& tot)
+__device__ __forceinline__ void router_probs(const void* logits, int l_dt, int64_t t, int64_t n_e, int lane,
+                                             float (&p)[RPL])
 {
-    float p[RPL];
     if (l_dt == VQ2_DT_F16)
         router_load_logits<VQ2_DT_F16, RPL>(logits, t, n_e, lane, p);
     else if (l_dt == VQ2_DT_BF16)
@@ -100,6 +98,17 @@ __device__ __forceinline__ void router_select(const void* logits, int l_dt, int6
     sum = wave_sum_all(sum);
 #pragma unroll
     for (int j = 0; j < RPL; j++) p[j] = (j * 64 + lane) < n_e ? p[j] / sum : -1.0f;
+}
+
+// Top-k of token t by one full wave (RPL * 64 >= n_e): lane r < k ends with
+// the round-r choice (probability `mine`, expert `my_id`); `tot` (uniform) is
+// the sum of the k chosen probabilities, so weight r = mine / tot.
+template <int RPL>
+__device__ __forceinline__ void router_select(const void* logits, int l_dt, int64_t t, int64_t n_e, int k, int lane,
+                                              float& mine, int& my_id, float& tot)
+{
+    float p[RPL];
+    router_probs<RPL>(logits, l_dt, t, n_e, lane, p);
 
     mine = 0.0f;
     my_id = 0;

@@ -52,35 +52,11 @@
 #include <thread>
 #include <vector>
 
-#include "vq2_gemv_kernel.hpp"
+#include "vq2_sorted.hpp"
 
 namespace vq2 {
 
-constexpr int SG_THREADS = 1024;
-constexpr int SG_WAVES = SG_THREADS / 64;
-constexpr int SG_ITER = 256;  // entries per iteration (64 lanes x 4)
-constexpr int SG_MAX_R = 255;
-constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
-constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
 constexpr int SG_MAX_SEG = 4;
-constexpr int SG_MAX_SHM = 96 * 1024;  // dynamic LDS: activation (+ stage) + accumulators
-
-static int sorted_gbits(int64_t ng)
-{
-    int b = 0;
-    while ((int64_t(1) << b) < ng) b++;
-    return b;
-}
-
-// Largest chunk height for ng groups: row R is the dummy row, so
-// (R << gbits) | group must fit 16 bits; at most SG_MAX_R.
-static int64_t sorted_max_rows(int64_t ng)
-{
-    const int gb = sorted_gbits(ng);
-    if (ng < 1 || gb > 15) return 0;
-    const int64_t rmax = (int64_t(1) << (16 - gb)) - 1;
-    return rmax < SG_MAX_R ? rmax : SG_MAX_R;
-}
 
 // Default chunk height: the rows split evenly over the fewest chunks; with
 // chunk_align > 1, over a multiple of chunk_align chunks (one per CU and
@@ -216,6 +192,58 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
     return VQ2_OK;
 }
 
+// Expert pool [E, rows, ng] (one stage): every expert packed as a matrix of
+// its own with the same chunk height R, experts one after another, and
+// every chunk padded (dummy-row entries) to the pool's largest iteration
+// count, so chunk c of expert e starts at iteration (e * C + c) * ipc
+// (C = ceil(rows / R)) with no table to read.
+int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t R, uint32_t* entries,
+                     int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters, int n_threads)
+{
+    const int64_t rmax = sorted_max_rows(ng);
+    if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: ng=%lld outside 1..32768", (long long)ng);
+    if (R < 1 || R > rmax)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: rows_per_chunk=%lld outside 1..%lld for ng=%lld",
+                         (long long)R, (long long)rmax, (long long)ng);
+    const int gb = sorted_gbits(ng);
+    const int64_t C = (rows + R - 1) / R;
+    const int64_t units = n_experts * C;
+    std::vector<std::vector<uint32_t>> parts((size_t)units);
+    int nt = n_threads > 0 ? n_threads : (int)std::thread::hardware_concurrency();
+    if (nt < 1) nt = 1;
+    if (nt > units) nt = (int)(units > 0 ? units : 1);
+    auto work = [&](int t) {
+        for (int64_t u = t; u < units; u += nt) {
+            const int64_t e = u / C, c = u - e * C;
+            const int64_t r0 = c * R, nr = std::min(R, rows - r0);
+            pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, parts[u]);
+        }
+    };
+    if (nt == 1) {
+        work(0);
+    } else {
+        std::vector<std::thread> th;
+        for (int t = 0; t < nt; t++) th.emplace_back(work, t);
+        for (auto& t : th) t.join();
+    }
+    int64_t ipc = 1;
+    for (int64_t u = 0; u < units; u++) ipc = std::max(ipc, (int64_t)parts[u].size() / SG_ITER);
+    const int64_t total = ipc * units;
+    *n_iters = total;
+    *iters_per_chunk = ipc;
+    if (total > 0x7FFFFFFFLL) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: pool too large");
+    if (total > cap_iters)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: %lld iterations needed, capacity %lld", (long long)total,
+                         (long long)cap_iters);
+    const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
+    for (int64_t u = 0; u < units; u++) {
+        uint32_t* dst = entries + u * ipc * SG_ITER;
+        memcpy(dst, parts[u].data(), parts[u].size() * sizeof(uint32_t));
+        std::fill(dst + parts[u].size(), dst + ipc * SG_ITER, pad);
+    }
+    return VQ2_OK;
+}
+
 // ------------------------------------------------------------------ kernel
 struct SortedSeg {
     const u32x4* ent;     // [n_iters * 64] lane words
@@ -245,33 +273,6 @@ struct SortedArgs {
     SortedSeg seg[SG_MAX_SEG];
     uint64_t* cand;  // EP 1: best top-1 key per workgroup
 };
-
-template <int CBT>
-__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* x)
-{
-    const u32x4 x0 = *(const u32x4*)x, x1 = *(const u32x4*)(x + 4);
-    float xv[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        xv[k] = __uint_as_float(x0[k]);
-        xv[4 + k] = __uint_as_float(x1[k]);
-    }
-    float d = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        float lo, hi;
-        if constexpr (CBT == VQ2_DT_F16) {
-            lo = f16_bits_to_f32((uint16_t)(c[w] & 0xFFFFu));
-            hi = f16_bits_to_f32((uint16_t)(c[w] >> 16));
-        } else {
-            lo = __uint_as_float(c[w] << 16);
-            hi = __uint_as_float(c[w] & 0xFFFF0000u);
-        }
-        d = fmaf(lo, xv[2 * w], d);
-        d = fmaf(hi, xv[2 * w + 1], d);
-    }
-    return d;
-}
 
 // XM 0: x holds the rotated activation (dtype XT); XM 1: rotate x in LDS.
 // EP 0: store y (or partials with several slices); EP 1: fused top-1 keys.
@@ -304,28 +305,16 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_kernel(const SortedArgs 
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (XM == 1) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, 0, 0, first);
 
-    // the wave's first three iterations' entry words and the first two's
-    // gathers are in flight during the prologue (clamped in-bounds addresses
-    // when the wave has fewer).  A missing stage-2 codebook is never selected
-    // for a real entry; cb0 stands in so that no gather can use a null base.
-    const u32x4* cb0 = (const u32x4*)a.cb0;
-    const u32x4* cb1 = (const u32x4*)(a.cb1 ? a.cb1 : a.cb0);
-    auto clampit = [&](int i) { return i < s1 ? i : c_beg; };
-    auto load_e = [&](int i) { return __builtin_nontemporal_load(sg.ent + (int64_t)i * 64 + lane); };
-    auto gather = [&](int i, const u32x4& e, u32x4 (&c)[4]) {
-        const u32x4* cb = i < c_mid ? cb0 : cb1;
-#pragma unroll
-        for (int q = 0; q < 4; q++) c[q] = cb[e[q] >> 16];
-    };
-    int it = s0 + wave;
-    int i1 = clampit(it + SG_WAVES), i2 = clampit(it + 2 * SG_WAVES);
-    u32x4 e0 = load_e(clampit(it)), e1 = load_e(i1), e2 = load_e(i2);
-    u32x4 c0[4], c1[4];
-    gather(clampit(it), e0, c0);
-    gather(i1, e1, c1);
+    // the wave's first entry words come from HBM while the prologue stages
+    // and rotates the activation (which waits only for its own, earlier
+    // loads); the first gathers go out after it
+    // (a pre-rotated x is only copied: there the gathers go out at once)
+    SortedPipe<CBT> pipe;
+    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
+    if constexpr (XM == 0) pipe.gathers();
 
-    float* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
-    for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = 0.0f;
+    float* acc = sorted_acc(s_acc, wave, lane, R);
+    sorted_acc_zero(acc, lane, R);
     if constexpr (XM == 1) {
         void* s_stage = smem + n;
         stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
@@ -335,54 +324,16 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_kernel(const SortedArgs 
         for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] = load_as_f32(a.g.x, XT, i);
     }
     __syncthreads();
-    // per wave, four iterations in flight: entry words three ahead, gathers
-    // two ahead of the arithmetic (about 8K codes in flight per CU at 16
-    // waves; loads complete in issue order, and no branch separates them, so
-    // each wait covers exactly the values it needs)
-    const uint32_t gmask = (1u << a.gbits) - 1u;
-    const uint32_t gmax = (uint32_t)(a.ng - 1);
-    for (; it < s1; it += SG_WAVES) {
-        const int i3 = clampit(it + 3 * SG_WAVES);
-        const u32x4 e3 = load_e(i3);
-        u32x4 c2[4];
-        gather(i2, e2, c2);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint32_t pos = e0[q] & 0xFFFFu;
-            const uint32_t r = min(pos >> a.gbits, (uint32_t)R);
-            const uint32_t g = min(pos & gmask, gmax);
-            const float d = centroid_dot<CBT>(c0[q], s_x + g * 8);
-            acc[r] += d;
-        }
-        e0 = e1;
-        e1 = e2;
-        e2 = e3;
-        i2 = i3;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            c0[q] = c1[q];
-            c1[q] = c2[q];
-        }
-    }
+    if constexpr (XM == 1) pipe.gathers();
+    pipe.run(acc, s_x, a.gbits, a.ng, R);
     __syncthreads();
 
-    // row sums: thread (p, r) adds a quarter of the SG_WAVES x SG_PARTS
-    // arrays of row r, then the four partials are added in p order (fixed
-    // order: deterministic)
     __shared__ float s_red[4][256];
+    const float sum = sorted_row_sums(s_acc, R, s_red);
     const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
-    if (rr < R) {
-        float part = 0.0f;
-        constexpr int NA = SG_WAVES * SG_PARTS / 4;
-#pragma unroll 4
-        for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
-        s_red[pp][rr] = part;
-    }
-    __syncthreads();
     const int64_t row0 = (int64_t)chunk * R;
     const int64_t row = row0 + rr;
     const bool own = pp == 0 && rr < R && row < sg.out_rows;
-    const float sum = own ? ((s_red[0][rr] + s_red[1][rr]) + s_red[2][rr]) + s_red[3][rr] : 0.0f;
     if constexpr (EP == 1) {
         uint64_t best = own ? argmax_key((sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs, row) : 0;
         for (int off = 32; off > 0; off >>= 1) {

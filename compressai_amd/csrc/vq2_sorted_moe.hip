@@ -1,0 +1,548 @@
+// vq2_sorted_moe.hip -- the MoE expert path over code-sorted expert pools
+// (gfx950).
+//
+// Per token t and pair k (expert e = ids[t, k], weight w[t, k]), as the
+// reference's expert loop computes it (vq2/paged_runtime.py:495-510,
+// vq2/load_and_test_full_35b.py:75-95):
+//
+//   gu    = VQ(gate_up[e]) . RHT_H(h_t)                       [2I]
+//   act   = RHT_I(silu(gu[:I]) * gu[I:])                      [I]
+//   out_t = sum_k w[t, k] * VQ(down[e]) . act                  [H]
+//
+// Both pools are in the code-sorted layout (vq2_sorted_pack_pool: every
+// expert a matrix of C chunks of R rows, experts one after another), so a
+// wave's 64 centroid gathers share a few codebook lines (vq2_sorted.hip
+// explains the layout).  Three launches, no host synchronisation:
+//  1. gate_up: one workgroup per (pair, chunk, slice).  The expert comes from
+//     ids (MODE 0) or from the router built in (MODE 1: softmax over the
+//     token's logits, top-k, renormalised; slot k is the shared expert with
+//     sigmoid(gate . h_t); the (pair, chunk 0, slice 0) workgroup publishes
+//     the pair's id and weight).  The workgroup builds RHT_H(h_t) in LDS and
+//     writes the raw row sums of its slice (unscaled) to a workspace.
+//  2. down (MODE 2): one workgroup per (pair, chunk, slice); its prologue adds
+//     the gate_up slices of its pair in slice order, applies the gate_up row
+//     scales, silu(gate) * up, and RHT_I in LDS, then the down slice.
+//     Each down slice writes its share w[t, k] * (row sum * s[e][row]).
+//  3. combine: out_t[row] = the sum of those shares over the token's pairs
+//     and the slices, in a fixed order (deterministic).
+// An expert id outside the pool gives NaN for its pair (never an
+// out-of-bounds read), as the gather kernels do.
+#include <mutex>
+
+#include "vq2_internal.hpp"
+#include "vq2_router.hpp"
+#include "vq2_sorted.hpp"
+
+namespace vq2 {
+
+struct SortedPoolArgs {
+    const u32x4* ent;
+    const void* scale;  // [n_experts, rows]
+    int32_t ipc;        // iterations per chunk (every chunk padded to it)
+    int s_dt;
+    int32_t n_iters;
+    int R;     // rows per chunk
+    int C;     // chunks per expert
+    int rows;  // rows per expert
+    int ng;    // groups per row
+    int gbits;
+};
+
+struct SortedMoeArgs {
+    // prologue fields: x = h [tokens, H] (token stride x_pstride, x_pdiv 1),
+    // the rotation (perm, sign, hb_log2, xscale) of this launch, and the
+    // fused router (r_*) of MODE 1
+    GemvArgs g;
+    SortedPoolArgs pool;
+    const void* cb;
+    int64_t n_experts;
+    int P;        // pairs per token
+    int n_pairs;  // tokens * P
+    int slices;
+    const void* ids;  // MODE 0 / 2 and the combine: pair experts
+    int ids_i64;
+    float* part;  // gate_up: [slices][n_pairs][pool.rows] raw row sums; down: [n_pairs][slices][pool.rows] shares
+    // MODE 2: the gate_up launch's partials and scales
+    const float* gu_part;
+    int gu_slices;
+    int gu_rows;
+    const void* gu_scale;
+    int gu_s_dt;
+    // combine
+    const float* w;
+    void* out;
+    int out_dt;
+};
+
+__device__ __forceinline__ int64_t pair_expert(const SortedMoeArgs& a, int p, bool& bad)
+{
+    const int64_t e = a.ids_i64 ? ((const int64_t*)a.ids)[p] : (int64_t)((const int32_t*)a.ids)[p];
+    bad = e < 0 || e >= a.n_experts;
+    return bad ? 0 : e;
+}
+
+// The router's top-k by wave 0 alone.  Each lane turns its 4 probabilities
+// (router_probs: the same arithmetic as router_select) into 64-bit keys
+// (bits of p) << 32 | (0xFFFFFFFF - expert) -- p >= 0, so a larger key is a
+// larger probability, or an equal one with a lower id: the order of
+// router_select's k argmax rounds -- and sorts them, descending.  Each
+// round takes the wave maximum of the lanes' first keys (DPP within rows,
+// row broadcasts across rows: no LDS), and the winning lane shifts its
+// keys.  Lane r < k ends with the rank-r key.
+template <int DPP, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v)
+{
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, DPP, ROW_MASK, 0xF, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, DPP, ROW_MASK, 0xF, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t route_topk_keys(const GemvArgs& g, int64_t t, int lane)
+{
+    float pr[4];
+    router_probs<4>(g.r_logits, g.r_ldt, t, g.r_ne, lane, pr);
+    uint64_t k0, k1, k2, k3;
+    {
+        uint64_t key[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t ex = (uint32_t)(j * 64 + lane);
+            key[j] = ex < (uint32_t)g.r_ne ? ((uint64_t)__float_as_uint(pr[j]) << 32) | (0xFFFFFFFFu - ex) : 0;
+        }
+        auto cs = [](uint64_t& x, uint64_t& y) {  // x >= y afterwards
+            const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+            x = hi;
+            y = lo;
+        };
+        cs(key[0], key[1]);
+        cs(key[2], key[3]);
+        cs(key[0], key[2]);
+        cs(key[1], key[3]);
+        cs(key[1], key[2]);
+        k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
+    }
+    uint64_t mine = 0;
+    for (int r = 0; r < g.r_k; r++) {
+        uint64_t m = k0;
+        m = dpp_max_u64<0xB1, 0xF>(m);   // quad_perm [1,0,3,2]
+        m = dpp_max_u64<0x4E, 0xF>(m);   // quad_perm [2,3,0,1]
+        m = dpp_max_u64<0x141, 0xF>(m);  // row_half_mirror
+        m = dpp_max_u64<0x140, 0xF>(m);  // row_mirror: every lane holds its row's maximum
+        m = dpp_max_u64<0x142, 0xA>(m);  // row_bcast:15 into rows 1 and 3
+        m = dpp_max_u64<0x143, 0xC>(m);  // row_bcast:31 into rows 2 and 3: lane 63 holds the maximum
+        const uint64_t best = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(m >> 32), 63) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)m, 63);
+        if (lane == r) mine = best;
+        if (k0 == best) {  // keys are distinct: one lane shifts
+            k0 = k1;
+            k1 = k2;
+            k2 = k3;
+            k3 = 0;
+        }
+    }
+    return mine;
+}
+
+constexpr int SG_MAX_TOPK = 64;
+
+// MODE 0: gate_up, ids given; MODE 1: gate_up with the router; MODE 2: down.
+// XT: dtype of h (MODE 0 / 1).
+//
+// Order of the prologue: the activation (or gate_up partial) loads, then the
+// expert's first entry words; the activation is staged and rotated in LDS
+// while the entry words come from HBM; the first centroid gathers are issued
+// after the prologue (the entry words have arrived by then).
+template <int CBT, int MODE, int XT>
+__global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedMoeArgs a)
+{
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float s_red[4][256];
+    __shared__ int s_top[SG_MAX_TOPK];
+    __shared__ float s_topv[SG_MAX_TOPK];
+    touch_kernargs(a);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const SortedPoolArgs& pl = a.pool;
+    const int64_t n = (int64_t)pl.ng * 8;
+    float* s_x = smem;              // n floats
+    float* s_stage = smem + n;      // n floats
+    float* s_acc = smem + 2 * n;    // SG_WAVES x SG_PARTS x (R + 1)
+    const int R = pl.R;
+    const int unit = (int)blockIdx.x / a.slices, slice = (int)blockIdx.x - unit * a.slices;
+    const int p = unit / pl.C, chunk = unit - p * pl.C;
+    const int t = p / a.P, kslot = p - t * a.P;
+
+    // prologue loads first: the token's activation and the rotation tables
+    // (MODE 0 / 1), or the tables alone (MODE 2)
+    XProLoad first;
+    const int64_t t0 = (int64_t)threadIdx.x * 8;
+    if constexpr (MODE != 2) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, t, 0, first);
+    else xpro_tables(a.g, t0 < n ? t0 : 0, n, first);
+
+    // chunk `chunk` of expert ex: iterations [(ex * C + chunk) * ipc, + ipc)
+    // (in the pool: ex < n_experts, chunk < C), this slice's share of them
+    SortedPipe<CBT> pipe;
+    auto entries = [&](int64_t ex) {
+        const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
+        const int s0 = c_beg + (int)((int64_t)pl.ipc * slice / a.slices);
+        const int s1 = c_beg + (int)((int64_t)pl.ipc * (slice + 1) / a.slices);
+        pipe.load_entries(pl.ent, a.cb, nullptr, c_beg, c_beg + pl.ipc, s0, s1, wave, lane);
+    };
+    float* acc = sorted_acc(s_acc, wave, lane, R);
+    bool bad = false;
+    int64_t e = 0;
+
+    if constexpr (MODE == 0) {
+        e = pair_expert(a, p, bad);
+        entries(e);
+        sorted_acc_zero(acc, lane, R);
+        stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
+        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+    } else if constexpr (MODE == 1) {
+        // the router in wave 0 (route_topk_keys); the shared expert's pairs
+        // know their expert at once
+        const bool routed = kslot < a.g.r_k;
+        const bool writer = chunk == 0 && slice == 0 && wave == 0;
+        if (!routed) {
+            e = a.g.r_shared;
+            entries(e);
+            if (writer) {
+                const float sw = router_shared_weight(a.g.r_gate, a.g.r_gdt, a.g.x, a.g.x_dt, t, n, lane);
+                if (lane == 0) {
+                    a.g.r_ids[p] = (int32_t)a.g.r_shared;
+                    a.g.r_w[p] = sw;
+                }
+            }
+        } else if (wave == 0) {
+            const uint64_t key = route_topk_keys(a.g, t, lane);
+            const uint32_t exu = 0xFFFFFFFFu - (uint32_t)key;
+            const int ex = exu < (uint32_t)a.g.r_ne ? (int)exu : 0;  // in bounds whatever the logits hold
+            if (lane < a.g.r_k) {
+                s_top[lane] = ex;
+                s_topv[lane] = __uint_as_float((uint32_t)(key >> 32));
+            }
+            if (writer) {
+                // weight = p / (sum of the k chosen p), summed as router_select
+                // sums it (lane r holds rank r)
+                const float mine = lane < a.g.r_k ? __uint_as_float((uint32_t)(key >> 32)) : 0.0f;
+                const float tot = wave_sum_all(mine);
+                if (lane == kslot) {
+                    a.g.r_ids[p] = ex;
+                    a.g.r_w[p] = mine / tot;
+                }
+            }
+        }
+        sorted_acc_zero(acc, lane, R);
+        stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);  // ends with a barrier: s_top is visible
+        if (routed) {
+            e = s_top[kslot];
+            entries(e);
+        }
+        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+    } else {
+        // the pair's gate_up rows: slices added in order, row scale, then
+        // silu(gate) * up (elementwise, so taken before the permutation).
+        // Thread i < 2n takes value i of [gate | up]; its slice loads (from
+        // other XCDs' writes: memory round trips) are issued together, before
+        // the expert id and the entry words.
+        const int64_t gstride = (int64_t)a.n_pairs * a.gu_rows;
+        const float* gp = a.gu_part + (int64_t)p * a.gu_rows;
+        auto slice_loads = [&](int64_t i, int s0, float (&pv)[8]) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) pv[s] = gp[(s0 + s < a.gu_slices ? s0 + s : 0) * gstride + i];
+        };
+        auto finish = [&](int64_t i, const float (&pv)[8], float sc) {
+            float v = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                if (s < a.gu_slices) v += pv[s];
+            for (int s0 = 8; s0 < a.gu_slices; s0 += 8) {
+                float pw[8];
+                slice_loads(i, s0, pw);
+#pragma unroll
+                for (int s = 0; s < 8; s++)
+                    if (s0 + s < a.gu_slices) v += pw[s];
+            }
+            smem[i] = v * sc;  // gate values land in s_x, up values in s_stage (= smem + n)
+        };
+        const int64_t i0 = threadIdx.x < 2 * n ? threadIdx.x : 0;
+        float pv0[8];
+        slice_loads(i0, 0, pv0);  // needs only the pair, not its expert
+        asm volatile("" ::: "memory");
+        e = pair_expert(a, p, bad);
+        const float sc0 = load_as_f32(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i0);
+        entries(e);
+        sorted_acc_zero(acc, lane, R);
+        if (threadIdx.x < 2 * n) finish(threadIdx.x, pv0, sc0);
+        for (int64_t i = threadIdx.x + SG_THREADS; i < 2 * n; i += SG_THREADS) {
+            float pv[8];
+            slice_loads(i, 0, pv);
+            finish(i, pv, load_as_f32(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i));
+        }
+        __syncthreads();
+        for (int64_t j = threadIdx.x; j < n; j += SG_THREADS) s_stage[j] = silu_f32(s_x[j]) * s_stage[j];
+        __syncthreads();
+        build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
+    }
+    for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] *= a.g.xscale;
+    __syncthreads();
+    pipe.gathers();
+    pipe.run(acc, s_x, pl.gbits, pl.ng, R);
+    __syncthreads();
+
+    const int rr = threadIdx.x;
+    const int64_t row = (int64_t)chunk * R + rr;
+    const bool own = rr < R && row < pl.rows;
+    // MODE 2: each slice's share of the combine, w[p] * (sum * s[e][row])
+    float f = 1.0f;
+    if constexpr (MODE == 2) f = own ? a.w[p] * load_as_f32(pl.scale, pl.s_dt, e * pl.rows + row) : 0.0f;
+    const float sum = sorted_row_sums(s_acc, R, s_red);
+    if (own) {
+        float v = sum;
+        if constexpr (MODE == 2) v = f * sum;
+        // gate_up: [slice][pair][row]; down: [pair][slice][row] (the combine reads a token's shares in one run)
+        const int64_t pi = MODE == 2 ? (int64_t)p * a.slices + slice : (int64_t)slice * a.n_pairs + p;
+        a.part[pi * pl.rows + row] = bad ? __builtin_nanf("") : v;
+    }
+}
+
+// out[t][row] = the sum of the token's down shares
+// part[pair][slice][row] = w[pair] * ((down row sum of the slice) * s[e][row])
+// over its pairs and slices, which are consecutive blocks of rows values.
+// Four threads per row: thread `part` adds shares part, part + 4, ... (all
+// its loads in flight together: each is a memory round trip, the shares
+// were written by other XCDs), then a fixed DPP tree adds the four partial
+// sums (deterministic).  grid (ceil(rows / 64), tokens).
+__global__ void __launch_bounds__(256) vq_sorted_moe_combine_kernel(const SortedMoeArgs a)
+{
+    const int t = blockIdx.y;
+    const int rows = a.pool.rows;
+    const int part = threadIdx.x & 3;
+    const int64_t row0 = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+    const int64_t row = row0 < rows ? row0 : rows - 1;  // every lane takes part in the DPP sums
+    const float* base = a.part + (int64_t)t * a.P * a.slices * rows + row;
+    const int terms = a.P * a.slices;
+    float fin = 0.0f;
+    for (int j0 = part; j0 < terms; j0 += 32) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = base[(int64_t)(j0 + 4 * j < terms ? j0 + 4 * j : 0) * rows];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j0 + 4 * j < terms) fin += v[j];
+    }
+    fin += __int_as_float(dpp_mov<0xB1>(__float_as_int(fin)));  // quad_perm [1,0,3,2]
+    fin += __int_as_float(dpp_mov<0x4E>(__float_as_int(fin)));  // quad_perm [2,3,0,1]
+    if (part == 0 && row0 < rows) store_from_f32(a.out, a.out_dt, (int64_t)t * rows + row0, fin);
+}
+
+// ------------------------------------------------------------------ launch
+template <int CBT, int MODE, int XT>
+static hipError_t launch_moe(const SortedMoeArgs& a, unsigned grid, size_t shm, hipStream_t st)
+{
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)vq_sorted_moe_kernel<CBT, MODE, XT>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, SG_MAX_SHM);
+    });
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((vq_sorted_moe_kernel<CBT, MODE, XT>), dim3(grid), dim3(SG_THREADS), shm, st, a);
+    return hipGetLastError();
+}
+
+template <int MODE, int XT>
+static hipError_t launch_moe_cb(int cb_dt, const SortedMoeArgs& a, unsigned grid, size_t shm, hipStream_t st)
+{
+    return cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, MODE, XT>(a, grid, shm, st)
+                               : launch_moe<VQ2_DT_BF16, MODE, XT>(a, grid, shm, st);
+}
+
+template <int MODE>
+static hipError_t launch_moe_x(int cb_dt, int x_dt, const SortedMoeArgs& a, unsigned grid, size_t shm,
+                               hipStream_t st)
+{
+    switch (x_dt) {
+    case VQ2_DT_F16: return launch_moe_cb<MODE, VQ2_DT_F16>(cb_dt, a, grid, shm, st);
+    case VQ2_DT_BF16: return launch_moe_cb<MODE, VQ2_DT_BF16>(cb_dt, a, grid, shm, st);
+    default: return launch_moe_cb<MODE, VQ2_DT_F32>(cb_dt, a, grid, shm, st);
+    }
+}
+
+static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_experts, int64_t rows, int64_t ng,
+                     SortedPoolArgs& pa)
+{
+    const int64_t r_lim = sorted_max_rows(ng);
+    if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: %s: ng=%lld unsupported", name, (long long)ng);
+    if (pc.rows != rows || pc.ng != ng)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool holds [%lld rows, %lld groups], expected [%lld, %lld]",
+                         name, (long long)pc.rows, (long long)pc.ng, (long long)rows, (long long)ng);
+    if (pc.rows_per_chunk < 1 || pc.rows_per_chunk > r_lim)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: rows_per_chunk=%lld outside 1..%lld", name,
+                         (long long)pc.rows_per_chunk, (long long)r_lim);
+    const int64_t C = (rows + pc.rows_per_chunk - 1) / pc.rows_per_chunk;
+    if (pc.iters_per_chunk < 1 || n_experts * C * pc.iters_per_chunk != pc.n_iters || pc.n_iters > 0x7FFFFFFF)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: %lld iterations are not %lld experts x %lld chunks x "
+                         "%lld", name, (long long)pc.n_iters, (long long)n_experts, (long long)C,
+                         (long long)pc.iters_per_chunk);
+    if (!pc.entries || (uintptr_t)pc.entries % 16 || !pc.scale)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: entries (16-byte aligned) and scales are required",
+                         name);
+    if (!dt_ok(pc.scale_dt)) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: bad scale dtype", name);
+    pa.ent = (const u32x4*)pc.entries;
+    pa.ipc = (int32_t)pc.iters_per_chunk;
+    pa.scale = pc.scale;
+    pa.s_dt = pc.scale_dt;
+    pa.n_iters = (int32_t)pc.n_iters;
+    pa.R = (int)pc.rows_per_chunk;
+    pa.C = (int)C;
+    pa.rows = (int)rows;
+    pa.ng = (int)ng;
+    pa.gbits = sorted_gbits(ng);
+    return VQ2_OK;
+}
+
+size_t sorted_moe_workspace_bytes(int64_t n_pairs, int64_t hidden, int64_t inter, int slices_gu, int slices_dn)
+{
+    return ((size_t)slices_gu * n_pairs * 2 * inter + (size_t)slices_dn * n_pairs * hidden) * sizeof(float);
+}
+
+static int rot_fields(GemvArgs& g, const SortedRot& r, int64_t n, const char* name)
+{
+    if (r.hb < 2 || r.hb > n || (r.hb & (r.hb - 1)) || n % r.hb)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: hb=%lld must be a power of two dividing %lld", name,
+                         (long long)r.hb, (long long)n);
+    if ((uintptr_t)r.perm % 16 || (uintptr_t)r.sign % 8)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: perm 16-byte, sign 8-byte aligned", name);
+    g.perm = r.perm;
+    g.sign = r.sign;
+    int hl = 0;
+    while ((int64_t(1) << hl) < r.hb) hl++;
+    g.hb_log2 = hl;
+    g.xscale = r.scale;
+    return VQ2_OK;
+}
+
+int sorted_moe_launch(const SortedMoeCall& c)
+{
+    const int64_t H = c.hidden, I = c.inter, T = c.tokens;
+    const bool router = c.logits != nullptr;
+    if (T < 1 || c.P < 1) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: tokens and pairs per token must be >= 1");
+    if (H % 64 || I % 64 || H < 64 || I < 64 || H > 8192 || I > 8192)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: hidden=%lld / inter=%lld must be multiples of 64 up to "
+                         "8192", (long long)H, (long long)I);
+    if (c.cb_dt != VQ2_DT_F16 && c.cb_dt != VQ2_DT_BF16)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: fp16 / bf16 codebooks only");
+    if (!c.cb || (uintptr_t)c.cb % 16) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: codebook must be 16-byte aligned");
+    if (!dt_ok(c.h_dt) || !dt_ok(c.out_dt)) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: bad h / out dtype");
+    if (!c.h || (uintptr_t)c.h % 16 || !c.out) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: h (16-byte aligned) and out required");
+    if (c.slices_gu < 1 || c.slices_gu > 64 || c.slices_dn < 1 || c.slices_dn > 64)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: slices must be 1..64");
+    if (c.n_experts < 1) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: empty pool");
+    const int64_t n_pairs = T * c.P;
+    if (n_pairs > 1 << 20) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: too many pairs");
+    if (router) {
+        if (c.top_k < 1 || c.top_k > SG_MAX_TOPK || c.P != c.top_k + 1 || c.n_routed < c.top_k || c.n_routed > 256)
+            return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: router needs 1 <= top_k <= n_routed <= 256 and pairs per "
+                             "token = top_k + 1 (the shared expert last)");
+        if (c.shared_id < 0 || c.shared_id >= c.n_experts || c.n_routed > c.n_experts)
+            return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: shared expert / routed experts outside the pool");
+        if (!c.shared_gate || !c.ids_out || !c.w_out || !dt_ok(c.l_dt) || !dt_ok(c.g_dt))
+            return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: router needs shared_gate, ids_out and w_out");
+    } else if (!c.ids || !c.w) {
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: ids and w are required without router logits");
+    }
+    SortedMoeArgs a{};
+    int r = pool_args(c.gate_up, "gate_up", c.n_experts, 2 * I, H / 8, a.pool);
+    if (r) return r;
+    SortedMoeArgs d{};
+    r = pool_args(c.down, "down", c.n_experts, H, I / 8, d.pool);
+    if (r) return r;
+    const size_t need = sorted_moe_workspace_bytes(n_pairs, H, I, c.slices_gu, c.slices_dn);
+    if (!c.workspace || c.ws_bytes < need || (uintptr_t)c.workspace % 16)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
+                         c.ws_bytes);
+    float* gu_part = (float*)c.workspace;
+    float* dn_part = gu_part + (size_t)c.slices_gu * n_pairs * 2 * I;
+    const void* ids = router ? (const void*)c.ids_out : c.ids;
+    const int ids_i64 = router ? 0 : c.ids_i64;
+    const float* w = router ? c.w_out : c.w;
+
+    // gate_up
+    a.g.x = c.h;
+    a.g.x_dt = c.h_dt;
+    a.g.x_bstride = H;
+    a.g.x_pstride = H;
+    a.g.x_pdiv = 1;
+    a.g.P = 1;
+    a.g.ng = H / 8;
+    a.g.batch = 1;
+    if ((r = rot_fields(a.g, c.rot_h, H, "rot_h"))) return r;
+    if (router) {
+        a.g.r_logits = c.logits;
+        a.g.r_ldt = c.l_dt;
+        a.g.r_ne = c.n_routed;
+        a.g.r_k = c.top_k;
+        a.g.r_pairs = c.P;
+        a.g.r_shared = c.shared_id;
+        a.g.r_gate = c.shared_gate;
+        a.g.r_gdt = c.g_dt;
+        a.g.r_ids = c.ids_out;
+        a.g.r_w = c.w_out;
+    }
+    a.cb = c.cb;
+    a.n_experts = c.n_experts;
+    a.P = c.P;
+    a.n_pairs = (int)n_pairs;
+    a.slices = c.slices_gu;
+    a.ids = ids;
+    a.ids_i64 = ids_i64;
+    a.part = gu_part;
+    hipStream_t st = (hipStream_t)c.stream;
+    const int64_t grid_gu = n_pairs * a.pool.C * c.slices_gu;
+    const int64_t grid_dn = n_pairs * d.pool.C * c.slices_dn;
+    if (grid_gu > 0x7FFFFFFF || grid_dn > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: grid too large");
+    size_t shm = (size_t)(2 * H + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
+    if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm);
+    hipError_t err = router ? launch_moe_x<1>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st)
+                            : launch_moe_x<0>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st);
+    if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe gate_up launch");
+
+    // down: SwiGLU + RHT_I prologue from the gate_up slices
+    d.g.ng = I / 8;
+    d.g.batch = 1;
+    d.g.P = 1;
+    d.g.x_pdiv = 1;
+    if ((r = rot_fields(d.g, c.rot_i, I, "rot_i"))) return r;
+    d.cb = c.cb;
+    d.n_experts = c.n_experts;
+    d.P = c.P;
+    d.n_pairs = (int)n_pairs;
+    d.slices = c.slices_dn;
+    d.ids = ids;
+    d.ids_i64 = ids_i64;
+    d.part = dn_part;
+    d.gu_part = gu_part;
+    d.gu_slices = c.slices_gu;
+    d.gu_rows = (int)(2 * I);
+    d.gu_scale = c.gate_up.scale;
+    d.gu_s_dt = c.gate_up.scale_dt;
+    d.w = w;
+    shm = (size_t)(2 * I + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
+    if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm);
+    err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st)
+                                : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st);
+    if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe down launch");
+
+    // combine
+    d.out = c.out;
+    d.out_dt = c.out_dt;
+    hipLaunchKernelGGL(vq_sorted_moe_combine_kernel, dim3((unsigned)((H + 63) / 64), (unsigned)T), dim3(256), 0, st, d);
+    err = hipGetLastError();
+    if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe combine launch");
+    return VQ2_OK;
+}
+
+}  // namespace vq2

@@ -510,6 +510,141 @@ def vq_sorted_gemv_argmax(x, planes, scale, cb0, cb1, n, perm=None, sign=None, h
     return idx, val
 
 
+# ------------------------------------------------ MoE over sorted expert pools
+class SortedPool:
+    """Code-sorted layout of an expert pool idx [E, rows, n/8] (int16, 2 bpw;
+    vq2_sorted_pack_pool): every expert packed like a SortedPlanes matrix
+    with one chunk height, experts one after another, every chunk padded to
+    the same iteration count (so the kernels compute a chunk's offset
+    instead of reading it).  Built once at load time by the expert modules;
+    the pool stays the public format."""
+
+    def __init__(self, idx, device=None, threads=0):
+        lib = _lib.load()
+        idx = _idx16(idx, "idx")
+        if idx.dim() != 3:
+            raise Vq2Error(f"expert pool must be [E, rows, ng], got {tuple(idx.shape)}")
+        E, rows, ng = (int(v) for v in idx.shape)
+        R = int(lib.vq2_sorted_rows_per_chunk(rows, ng, 1))
+        if R == 0:
+            raise Vq2Error(f"sorted layout: ng={ng} unsupported")
+        self.n_experts, self.rows, self.ng, self.rows_per_chunk = E, rows, ng, R
+        self.chunks = -(-rows // R)
+        dev = torch.device(device) if device is not None else idx.device
+        h = idx.detach().to("cpu").contiguous()
+        cap = E * self.chunks * (-(-R * ng // 256) + 8)
+        ipc = ctypes.c_int64(0)
+        n_iters = ctypes.c_int64(0)
+        for _ in range(2):
+            entries = torch.empty(cap * 256, dtype=torch.int32)
+            st = lib.vq2_sorted_pack_pool(h.data_ptr(), E, rows, ng, R, entries.data_ptr(), cap, ctypes.byref(ipc),
+                                          ctypes.byref(n_iters), int(threads))
+            if st == _lib.ERR_ARG and n_iters.value > cap:
+                cap = n_iters.value
+                continue
+            _lib.check(st, "vq2_sorted_pack_pool")
+            break
+        self.n_iters = int(n_iters.value)
+        self.iters_per_chunk = int(ipc.value)
+        self.entries = entries[: self.n_iters * 256].to(dev)
+        self.device = dev
+
+    def pool(self, scale) -> "_lib.SortedPool":
+        _contig(scale, "scale")
+        if scale.numel() != self.n_experts * self.rows:
+            raise Vq2Error(f"scale must hold [{self.n_experts}, {self.rows}] values")
+        return _lib.SortedPool(self.entries.data_ptr(), self.iters_per_chunk, self.n_iters, self.rows_per_chunk,
+                               self.rows, self.ng, scale.data_ptr(), _dt(scale, "scale"))
+
+    def nbytes(self):
+        return self.entries.numel() * self.entries.element_size()
+
+
+# per-workgroup rates that set the slice counts below (MI355X, 16-wave
+# workgroups): codes per microsecond, and the fixed cost of a workgroup
+# (prologue, epilogue) in microseconds
+_MOE_RATE = 1460.0
+_MOE_FIXED_US = (2.5, 2.0)
+
+
+def moe_slices(units, codes_per_unit, cu, fixed_us):
+    """Slices per chunk for `units` (pair, chunk) units: the count that
+    minimises rounds x (work per slice + fixed cost), with one 16-wave
+    workgroup per CU at a time."""
+    best, best_t = 1, None
+    for s in range(1, 33):
+        t = -(-units * s // cu) * (codes_per_unit / _MOE_RATE / s + fixed_us)
+        if best_t is None or t < best_t - 1e-9:
+            best, best_t = s, t
+    return best
+
+
+def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, cb, rot_h, rot_i, *, ids=None,
+                  w=None, logits=None, top_k=None, shared_id=None, shared_gate=None, out_dtype=torch.float32,
+                  out=None, slices=None):
+    """The experts of an MoE layer over code-sorted pools, three launches:
+    out [T, H] = sum_k w[t, k] * VQ(down[e]) RHT_I(silu(gu[:I]) * gu[I:]),
+    gu = VQ(gate_up[e]) RHT_H(h_t), e = ids[t, k].  With `logits` [T, E_r]
+    the router is built in (top_k routed experts plus the shared expert
+    shared_id with sigmoid(shared_gate . h_t)); it then returns
+    (out, ids int32 [T, top_k + 1], w fp32 [T, top_k + 1]).  rot_h / rot_i:
+    (perm int32, sign int8, hb, scale)."""
+    H = gate_up.ng * 8
+    I = down.ng * 8
+    if gate_up.rows != 2 * I or down.rows != H or gate_up.n_experts != down.n_experts:
+        raise Vq2Error("vq_sorted_moe: inconsistent gate_up / down pools")
+    h2 = _contig(h, "h").reshape(-1, H)
+    T = h2.shape[0]
+    dev = _dev(h2, cb, gu_scale, dn_scale, ids, w, logits, gate_up.entries, down.entries)
+    _contig(cb, "cb")
+    if cb.dim() != 2 or cb.shape[0] < 65536 or cb.shape[1] != 8 or cb.dtype not in (torch.float16, torch.bfloat16):
+        raise Vq2Error("vq_sorted_moe: cb must be an fp16 / bf16 [65536, 8] codebook")
+    router = logits is not None
+    if router:
+        lg = _contig(logits, "logits").reshape(T, -1)
+        P = int(top_k) + 1
+        ids_out = torch.empty((T, P), dtype=torch.int32, device=dev)
+        w_out = torch.empty((T, P), dtype=torch.float32, device=dev)
+        _contig(shared_gate, "shared_gate")
+        ids_p, ids64, w_p = None, 0, None
+    else:
+        if ids is None or w is None:
+            raise Vq2Error("vq_sorted_moe: ids and w, or router logits, are required")
+        ids2 = _contig(ids, "ids").reshape(T, -1)
+        if ids2.dtype not in (torch.int32, torch.int64):
+            raise Vq2Error("ids must be int32 or int64")
+        P = ids2.shape[1]
+        w2 = _contig(w, "w").reshape(T, P)
+        if w2.dtype != torch.float32:
+            raise Vq2Error("w must be fp32")
+        ids_p, ids64, w_p = _p(ids2), 1 if ids2.dtype == torch.int64 else 0, _p(w2)
+    if out is None:
+        out = torch.empty((T, H), dtype=out_dtype, device=dev)
+    elif out.numel() != T * H or not out.is_contiguous():
+        raise Vq2Error(f"out must be a contiguous [{T}, {H}]")
+    if slices is None:
+        cu = _cu_count(dev)
+        sg = moe_slices(T * P * gate_up.chunks, gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0])
+        sd = moe_slices(T * P * down.chunks, down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1])
+    else:
+        sg, sd = (int(v) for v in slices)
+    lib = _lib.load()
+    ws = _workspace(dev, int(lib.vq2_sorted_moe_workspace(T, P, H, I, sg, sd)))
+    rh = _lib.RotTables(_p(rot_h[0]), _p(rot_h[1]), int(rot_h[2]), float(rot_h[3]))
+    ri = _lib.RotTables(_p(rot_i[0]), _p(rot_i[1]), int(rot_i[2]), float(rot_i[3]))
+    gp, dp = gate_up.pool(gu_scale), down.pool(dn_scale)
+    _lib.call("vq2_sorted_moe", _p(h2), _dt(h2, "h"), T, P, ids_p, ids64, w_p,
+              _p(lg) if router else None, _dt(lg, "logits") if router else 0, lg.shape[1] if router else 0,
+              int(top_k) if router else 0, int(shared_id) if router else 0, _p(shared_gate) if router else None,
+              _dt(shared_gate, "shared_gate") if router else 0, _p(ids_out) if router else None,
+              _p(w_out) if router else None, gate_up.n_experts, H, I, ctypes.byref(gp), ctypes.byref(dp), _p(cb),
+              _dt(cb, "cb"), ctypes.byref(rh), ctypes.byref(ri), _p(out), _dt(out, "out"), sg, sd, _p(ws),
+              ws.numel(), _stream(dev))
+    if router:
+        return out, ids_out, w_out
+    return out
+
+
 # -------------------------------------------------------------- grouped MoE
 def _moe_checks(pool, scale, OUT, NG, what):
     pool = _idx16(pool, what)

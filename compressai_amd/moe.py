@@ -25,6 +25,14 @@ launches (router + gate_up, down + combine) and no host synchronisation.
 
 Intermediates are fp32 by default (the parity contract); ``act_dtype`` may
 select bf16 to follow the reference's cast points instead.
+
+On the GPU, with fp16 / bf16 codebooks and fp32 intermediates, both modules
+also keep a code-sorted copy of the expert pools (``kernels.SortedPool``,
+packed once at construction, 4 bytes per code) and run the experts over it:
+the gate_up launch (router built in for ``MoELayer``), a down launch whose
+prologue finishes the gate_up sums and builds SwiGLU + RHT, and a combine
+launch, so a wave's centroid gathers share codebook lines.  The reference
+pools stay the public format and serve ``act_dtype`` bf16 and the paged feed.
 """
 from __future__ import annotations
 
@@ -46,7 +54,8 @@ class ResidentMoEExperts(nn.Module):
     takes ready device pools (any scale dtype, kept as given)."""
 
     def __init__(self, q_gate_up, q_down, cb16, device="cuda", *, num_experts=256, hidden_dim=2048,
-                 intermediate_dim=512, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=None):
+                 intermediate_dim=512, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=None,
+                 sorted_layout=None):
         super().__init__()
         E, H, I = int(num_experts), int(hidden_dim), int(intermediate_dim)
         gu_idx = q_gate_up["idx"][0]
@@ -58,19 +67,21 @@ class ResidentMoEExperts(nn.Module):
                     q_gate_up["scale"].view(E, 2 * I).to(device=device, dtype=torch.bfloat16),
                     dn_idx.view(E, H, I // 8).to(device),
                     q_down["scale"].view(E, H).to(device=device, dtype=torch.bfloat16),
-                    cb16, rot_h, rot_i, act_dtype, out_dtype)
+                    cb16, rot_h, rot_i, act_dtype, out_dtype, sorted_layout)
 
     @classmethod
     def from_pools(cls, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h=None, rot_i=None,
-                   act_dtype=torch.float32, out_dtype=None):
+                   act_dtype=torch.float32, out_dtype=None, sorted_layout=None):
         """Pools already on the device: gate_up_idx [E, 2I, H/8], down_idx
         [E, H, I/8] (int16), scales [E, 2I] / [E, H] in any float dtype."""
         self = cls.__new__(cls)
         nn.Module.__init__(self)
-        self._setup(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype)
+        self._setup(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype,
+                    sorted_layout)
         return self
 
-    def _setup(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype):
+    def _setup(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, rot_h, rot_i, act_dtype, out_dtype,
+               sorted_layout=None):
         E, gu_rows, ng_h = gate_up_idx.shape
         E2, hidden, ng_i = down_idx.shape
         if E2 != E or gu_rows != 2 * ng_i * 8 or hidden != ng_h * 8:
@@ -88,11 +99,32 @@ class ResidentMoEExperts(nn.Module):
         self.rot_i = rot_i if rot_i is not None else get_rot("moe_expert_512", self.intermediate_dim, dev)
         self.act_dtype = act_dtype
         self.out_dtype = out_dtype
+        # code-sorted copies of the pools (the experts' batch-1 and small-T path)
+        use = sorted_layout if sorted_layout is not None else (
+            dev.type == "cuda" and act_dtype == torch.float32 and cb16.dtype in (torch.float16, torch.bfloat16)
+            and hidden % 64 == 0 and self.intermediate_dim % 64 == 0 and hidden <= 8192)
+        self.sorted_gu = K.SortedPool(gate_up_idx, device=dev) if use else None
+        self.sorted_dn = K.SortedPool(down_idx, device=dev) if use else None
+
+    def _rots(self):
+        rh, ri = self.rot_h, self.rot_i
+        return (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale)
+
+    def nbytes(self):
+        own = sum(t.numel() * t.element_size() for t in (self.gate_up_idx, self.gate_up_scale, self.down_idx,
+                                                          self.down_scale))
+        return own + sum(p.nbytes() for p in (self.sorted_gu, self.sorted_dn) if p is not None)
 
     def experts(self, h, ids, w, out=None):
         """h [T, H] (unrotated hidden states), ids [T, P] int32/int64,
-        w fp32 [T, P] -> [T, H].  Two launches: gate_up with the H-point RHT
-        fused, then SwiGLU + I-point RHT + down + weighted combine."""
+        w fp32 [T, P] -> [T, H].  Sorted pools: gate_up, down (SwiGLU + RHT
+        in its prologue) and combine launches; otherwise two launches, gate_up
+        with the H-point RHT fused, then SwiGLU + I-point RHT + down +
+        weighted combine."""
+        if self.sorted_gu is not None:
+            rh, ri = self._rots()
+            return K.vq_sorted_moe(h, self.sorted_gu, self.gate_up_scale, self.sorted_dn, self.down_scale, self.cb16,
+                                   rh, ri, ids=ids, w=w, out=out, out_dtype=self.out_dtype or torch.float32)
         T, P = ids.shape
         I = self.intermediate_dim
         y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
@@ -121,10 +153,11 @@ class MoELayer(nn.Module):
     [E+1, 2I] / [E+1, H]; id E is the shared expert.  shared_gate [H]."""
 
     def __init__(self, gate_up_idx, gate_up_scale, down_idx, down_scale, cb16, shared_gate, top_k=8,
-                 n_routed=None, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=torch.float32):
+                 n_routed=None, rot_h=None, rot_i=None, act_dtype=torch.float32, out_dtype=torch.float32,
+                 sorted_layout=None):
         super().__init__()
         self.experts_mod = ResidentMoEExperts.from_pools(gate_up_idx, gate_up_scale, down_idx, down_scale, cb16,
-                                                         rot_h, rot_i, act_dtype, out_dtype)
+                                                         rot_h, rot_i, act_dtype, out_dtype, sorted_layout)
         self.n_routed = gate_up_idx.shape[0] - 1 if n_routed is None else int(n_routed)
         self.top_k = int(top_k)
         self.shared_gate = shared_gate
@@ -137,11 +170,19 @@ class MoELayer(nn.Module):
         return K.vq_router_topk(router_logits, self.top_k, h, self.shared_gate, shared_id=self.n_routed)
 
     def forward(self, h, router_logits):
-        """Two launches: router + gate_up (+ RHT), then SwiGLU + RHT + down +
-        combine."""
+        """Sorted pools: router + gate_up, down (SwiGLU + RHT prologue),
+        combine.  Otherwise two launches: router + gate_up (+ RHT), then
+        SwiGLU + RHT + down + combine."""
         m = self.experts_mod
         h2 = h.reshape(-1, m.hidden_dim).contiguous()
         T = h2.shape[0]
+        if m.sorted_gu is not None and self.n_routed <= 256:
+            rh, ri = m._rots()
+            out, _, _ = K.vq_sorted_moe(h2, m.sorted_gu, m.gate_up_scale, m.sorted_dn, m.down_scale, m.cb16, rh, ri,
+                                        logits=router_logits.reshape(T, -1), top_k=self.top_k,
+                                        shared_id=self.n_routed, shared_gate=self.shared_gate,
+                                        out_dtype=m.out_dtype or torch.float32)
+            return out
         I = m.intermediate_dim
         P = self.top_k + 1
         y_gu = torch.empty((T * P, 2 * I), dtype=m.act_dtype, device=h2.device)

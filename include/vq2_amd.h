@@ -386,6 +386,67 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
                            int s_dt, int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
                            float* out_val, void* stream);
 
+/* ---- MoE experts over code-sorted expert pools -------------------------
+ * vq2_sorted_pack_pool (host memory, no GPU work) packs an expert pool
+ * idx [n_experts, rows, ng] (one int16 plane, 2 bpw) expert by expert, each
+ * as vq2_sorted_pack packs a matrix with the same rows_per_chunk R, and pads
+ * every chunk (dummy-row entries, code 0) to the pool's largest iteration
+ * count *iters_per_chunk, so chunk c of expert e holds iterations
+ * [(e * C + c) * ipc, (e * C + c + 1) * ipc), C = ceil(rows / R).
+ * *n_iters = n_experts * C * ipc; capacity as vq2_sorted_pack.  No
+ * reference counterpart (a load-time transform of the pools
+ * PackedMoEExpertUniversal holds, vq2/load_and_test_full_35b.py:31-47). */
+int vq2_sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
+                         uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
+                         int n_threads);
+
+/* One packed expert pool (device pointers, except the struct). */
+typedef struct vq2_sorted_pool {
+    const uint32_t* entries;  /* from vq2_sorted_pack_pool                     */
+    int64_t iters_per_chunk;
+    int64_t n_iters;
+    int64_t rows_per_chunk;
+    int64_t rows;             /* rows per expert                               */
+    int64_t ng;               /* groups per row (input width / 8)              */
+    const void* scale;        /* [n_experts, rows], dtype scale_dt             */
+    int scale_dt;
+} vq2_sorted_pool;
+
+/* The permutation, signs, block size and scale of one rotation. */
+typedef struct vq2_rot_tables {
+    const int32_t* perm;      /* [n] or NULL (16-byte aligned)                 */
+    const int8_t* sign;       /* [n] or NULL (8-byte aligned)                  */
+    int64_t hb;
+    float scale;
+} vq2_rot_tables;
+
+/* The experts of an MoE layer for `tokens` tokens of h [tokens, hidden]:
+ *   gu  = VQ(gate_up[e]) . RHT_h(h_t)           (pool [n_experts, 2 inter, hidden / 8])
+ *   act = RHT_i(silu(gu[:inter]) * gu[inter:])
+ *   out[t] = sum_k w[t, k] * VQ(down[e]) . act   (pool [n_experts, hidden, inter / 8])
+ * with e = ids[t, k] over pairs_per_token pairs, or, with router logits
+ * [tokens, n_routed] (logits != NULL), the router built in: softmax, top_k
+ * (ties to the lower id), renormalised; the last pair (pairs_per_token =
+ * top_k + 1) is the shared expert shared_id with weight
+ * sigmoid(shared_gate . h_t); the ids / weights go to ids_out / w_out.
+ * Three launches (gate_up, down, combine), fp32 arithmetic, an id outside
+ * the pool gives NaN for its token.  slices_gu / slices_dn workgroups share
+ * each chunk; workspace: vq2_sorted_moe_workspace bytes.  Replaces the
+ * per-token expert loop of PackedMoEExpertUniversal.forward
+ * (vq2/load_and_test_full_35b.py:53-95) / PagedMoEExpert.forward
+ * (vq2/paged_runtime.py:495-510), with the router, the transformers
+ * Qwen3_5MoeSparseMoeBlock routing (softmax, top-k, shared expert gate). */
+size_t vq2_sorted_moe_workspace(int64_t tokens, int pairs_per_token, int64_t hidden, int64_t inter, int slices_gu,
+                                int slices_dn);
+int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token,
+                   const void* ids, int ids_i64, const float* w,
+                   const void* logits, int l_dt, int64_t n_routed, int top_k, int64_t shared_id,
+                   const void* shared_gate, int g_dt, int32_t* ids_out, float* w_out,
+                   int64_t n_experts, int64_t hidden, int64_t inter,
+                   const vq2_sorted_pool* gate_up, const vq2_sorted_pool* down, const void* cb, int cb_dt,
+                   const vq2_rot_tables* rot_h, const vq2_rot_tables* rot_i, void* out, int out_dt,
+                   int slices_gu, int slices_dn, void* workspace, size_t ws_bytes, void* stream);
+
 /* Rotated-space dequantisation of rows [r0, r1) (debug / audit):
  *   W[r, 8g+j] = (f32(cb0[i0]) [+ f32(cb1[i1])]) * f32(scale[r]), fp32 [r1-r0, n]
  * rounded exactly in that order (no contraction).

@@ -303,10 +303,12 @@ def test_router_topk_vs_oracle(dev):
     assert np.allclose(w[:, k].cpu().numpy(), sg, rtol=1e-5)
 
 
+@pytest.mark.parametrize("sorted_layout", [True, False])
 @pytest.mark.parametrize("T", [1, 8])
-def test_moe_layer_config4_vs_oracle(dev, T):
+def test_moe_layer_config4_vs_oracle(dev, T, sorted_layout):
     """Config 4: 256 routed + 1 shared expert resident in one pool, top-8,
-    T = 1 and 8, router + RHTs + grouped GEMVs + combine on device."""
+    T = 1 and 8, router + RHTs + grouped GEMVs + combine on device, over the
+    code-sorted pools and over the reference pools (gather kernels)."""
     from compressai_amd.moe import MoELayer
 
     E, k = 256, 8
@@ -315,7 +317,8 @@ def test_moe_layer_config4_vs_oracle(dev, T):
     h = synth.activations(4004, (T, 2048))
     logits = synth.activations(4007, (T, E))
     gate = synth.activations(4008, 2048) * 0.02
-    layer = MoELayer(*_cuda(gu, gus, dn, dns, cb, gate, dev=dev), top_k=k)
+    layer = MoELayer(*_cuda(gu, gus, dn, dns, cb, gate, dev=dev), top_k=k, sorted_layout=sorted_layout)
+    assert (layer.experts_mod.sorted_gu is not None) == sorted_layout
     out = layer(h.to(dev), logits.to(dev))
     rh, ri = layer.experts_mod.rot_h, layer.experts_mod.rot_i
     ref = O.moe_layer(h, logits, cb, gu, gus, dn, dns, gu[E], gus[E], dn[E], dns[E], gate,
@@ -754,8 +757,9 @@ def test_paged_experts_match_resident_pool(dev, tmp_path):
     pg = paged.PagedMoEExperts(0, store, cb, capacity=6, device=dev, staging=3, out_dtype=torch.float32)
     # the paged pool holds bf16-rounded scales (as the reference's pools): same for the resident one
     bf = torch.bfloat16
+    # (the gather kernels on the reference pools, which the paged feed runs too)
     res = ResidentMoEExperts.from_pools(gui.to(dev), gus.to(dev, bf), dni.to(dev), dns.to(dev, bf), cb,
-                                        out_dtype=torch.float32)
+                                        out_dtype=torch.float32, sorted_layout=False)
     for step in range(8):
         T = 1 + step % 3
         ids = torch.stack([torch.randperm(E, generator=g)[:2] for _ in range(T)]).to(torch.int64)

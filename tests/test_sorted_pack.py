@@ -118,3 +118,45 @@ def test_sorted_rows_per_chunk_alignment():
     assert L.vq2_sorted_rows_per_chunk(6144, 256, 256) == 246     # 25 chunks (aligned ones would be too short)
     assert L.vq2_sorted_rows_per_chunk(2048, 768, 1) == 63        # 6144-wide: 63 rows at most (33 chunks)
     assert L.vq2_sorted_rows_per_chunk(100, 1 << 16, 1) == 0      # n beyond the 16-bit position field
+
+
+@pytest.mark.parametrize("E,rows,n", [(3, 1024, 2048), (5, 2048, 512), (2, 100, 800)])
+def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
+    """vq2_sorted_pack_pool lays the experts out one after another, each
+    chunk exactly as vq2_sorted_pack packs it alone, then padded with
+    dummy-row entries (code 0) to the pool's common iteration count."""
+    from compressai_amd.kernels import SortedPool
+
+    ng = n // 8
+    idx = synth.indices16(9950 + rows, (E, rows, ng))
+    pool = SortedPool(idx, device="cpu", threads=3)
+    C, R = pool.chunks, pool.rows_per_chunk
+    assert R == int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1)) and C == -(-rows // R)
+    ipc = pool.iters_per_chunk
+    assert pool.n_iters == E * C * ipc
+    ent = pool.entries.numpy().view(np.uint32)
+    pad = np.uint32(R << _gb(ng))
+    longest = 0
+    for e in range(E):
+        sp = SortedPlanes(idx[e], None, rows, n, device="cpu", chunk_align=1)
+        assert sp.rows_per_chunk == R
+        cit = sp.chunk_it.numpy()
+        own = sp.entries.numpy().view(np.uint32)
+        for c in range(C):
+            a, b = cit[c] * 256, cit[c + 1] * 256
+            longest = max(longest, cit[c + 1] - cit[c])
+            got = ent[(e * C + c) * ipc * 256:(e * C + c + 1) * ipc * 256]
+            assert np.array_equal(got[: b - a], own[a:b])
+            assert np.all(got[b - a:] == pad)
+    assert ipc == longest
+
+
+def test_moe_slices_cost_model():
+    """Slice counts of the sorted MoE launches on 256 CUs: T = 1 fills one
+    round (gate_up 45 units x 5, down 81 x 3); T = 8 takes 2 and 1."""
+    from compressai_amd.kernels import moe_slices
+
+    assert moe_slices(45, 205 * 256, 256, 2.5) == 5
+    assert moe_slices(81, 228 * 64, 256, 2.0) == 3
+    assert moe_slices(360, 205 * 256, 256, 2.5) == 2
+    assert moe_slices(648, 228 * 64, 256, 2.0) == 1
