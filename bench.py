@@ -18,7 +18,7 @@ T = 1) in us per layer over a 40-layer resident pool, the config-3 LM head
 the host (``cpu_baseline``).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                       [--only dominant|dominant_gather|copy|moe] (single-launch modes for rocprofv3 runs)
+                       [--only dominant|dominant_gather|copy|moe|paged] (single-part modes for rocprofv3 runs)
 """
 from __future__ import annotations
 
@@ -467,9 +467,12 @@ def bench_unpack(args, dev):
 def bench_paged(args, dev, E=64, steps=200):
     """Paged expert pool (config-4 expert shape, one layer of E experts in a
     .vq2m file): T = 1, top-8 routed ids on the device each step.  Warm: every
-    expert resident; churn: 16 slots, so most steps page experts in through
-    the pinned ring.  Host-timed (the paging decision reads the ids on the
-    host, so these steps are not graph-captured)."""
+    expert resident; churn: 16 slots, so most steps page experts in.  Host
+    pager: misses read from the file through the pinned ring, host-timed (the
+    paging decision reads the ids on the host, so the steps cannot be
+    graph-captured).  Device pager (device_tables): the slot tables on the
+    device, misses copied from the pinned host mirror of the layer; the
+    `steps` steps are one HIP graph, timed with HIP events."""
     import shutil
     import tempfile
     import time
@@ -493,18 +496,29 @@ def bench_paged(args, dev, E=64, steps=200):
         ids = torch.stack([torch.randperm(E, generator=g)[:8] for _ in range(steps)]).to(dev)
         w = torch.full((1, 8), 1.0 / 8, device=dev)
         h = synth.activations(7004, (1, 2048), dtype=torch.float16).to(dev)
-        for name, cap in (("warm", E), ("churn", 16)):
-            layer = paged.PagedMoEExperts(0, store, cb, capacity=cap, device=dev, out_dtype=torch.float32)
+        for name, cap, on_dev in (("warm", E, False), ("churn", 16, False), ("warm_device", E, True),
+                                  ("churn_device", 16, True)):
+            layer = paged.PagedMoEExperts(0, store, cb, capacity=cap, device=dev, out_dtype=torch.float32,
+                                          device_tables=on_dev)
             for s_ in range(min(steps, 2 * E)):  # fill the pool / reach the steady state
                 layer(h, ids[s_ % steps].view(1, 8), w)
             torch.cuda.synchronize(dev)
             m0 = layer.pager.misses
-            t0 = time.perf_counter()
-            for s_ in range(steps):
-                layer(h, ids[s_].view(1, 8), w)
-            torch.cuda.synchronize(dev)
-            dt = time.perf_counter() - t0
-            misses = layer.pager.misses - m0
+            if on_dev:
+                gr = capture(lambda l: layer(h, ids[l].view(1, 8), w), steps, dev)
+                m0 = layer.pager.misses
+                time_graph(gr, 1, dev)
+                dt = statistics.median(time_graph(gr, 1, dev)[0] for _ in range(REPEATS)) * 1e-3
+                reps = 1 + REPEATS
+                del gr
+            else:
+                t0 = time.perf_counter()
+                for s_ in range(steps):
+                    layer(h, ids[s_].view(1, 8), w)
+                torch.cuda.synchronize(dev)
+                dt = time.perf_counter() - t0
+                reps = 1
+            misses = (layer.pager.misses - m0) / reps
             res[name] = {"us_per_layer": round(dt * 1e6 / steps, 2), "misses_per_step": round(misses / steps, 2),
                          "feed_gbps": round(misses * store.record_bytes / dt / 1e9, 2)}
             log(f"paged MoE ({name}, {cap} slots of {E}): {res[name]['us_per_layer']:.1f} us/layer, "
@@ -632,7 +646,7 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy", "moe"], default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy", "moe", "paged"], default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -659,6 +673,9 @@ def main():
             fn(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
         torch.cuda.synchronize(dev)
         log(f"{args.only}-only run done")
+        return
+    if args.only == "paged":
+        bench_paged(args, dev)
         return
     if args.only == "moe":
         res = bench_moe(args, dev, n_layers=args.layers)

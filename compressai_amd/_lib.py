@@ -75,6 +75,9 @@ SIGNATURES = {
     "vq2_sorted_moe": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _vp, _vp,
                         _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
                         ctypes.c_size_t, _vp], _i32),
+    "vq2_pager_lds_bytes": ([_i64, _i64, _i64], ctypes.c_size_t),
+    "vq2_pager_step": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "vq2_pager_copy": ([_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp], _i32),
     "vq2_dequant_rows": ([_vp, _vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp], _i32),
     "vq2_decode_idx": ([_vp, _i32, _i64, _vp, _vp], _i32),
     "vq2_unpack_fixed": ([_vp, _i64, _i32, _i64, _vp, _vp], _i32),

@@ -804,6 +804,35 @@ int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token,
     return sorted_moe_launch(c);
 }
 
+size_t vq2_pager_lds_bytes(int64_t n_experts, int64_t capacity, int64_t n_pairs)
+{
+    return pager_lds_bytes(n_experts, capacity, n_pairs);
+}
+
+int vq2_pager_step(const void* ids, int ids_i64, int64_t n_pairs, int64_t n_experts, int64_t capacity,
+                   int32_t* slot_of, int32_t* expert_of, int32_t* stamp, int32_t* state, int32_t* copy_list,
+                   int32_t* pair_slot, void* stream)
+{
+    clear_error();
+    CHECK(n_pairs >= 1 && n_pairs <= 4096 && n_experts >= 1 && n_experts <= 65536 && capacity >= 1 &&
+              capacity <= 4096, "vq2_pager_step: bad sizes (pairs %lld, experts %lld, slots %lld)", (long long)n_pairs,
+          (long long)n_experts, (long long)capacity);
+    CHECK(ids && slot_of && expert_of && stamp && state && copy_list && pair_slot, "vq2_pager_step: NULL pointer");
+    return pager_step_launch(ids, ids_i64, n_pairs, n_experts, capacity, slot_of, expert_of, stamp, state, copy_list,
+                             pair_slot, stream);
+}
+
+int vq2_pager_copy(const void* mirror, int64_t record_bytes, const int64_t* seg_bytes, const int32_t* copy_list,
+                   const int32_t* state, int64_t max_copies, void* const* dst, const int64_t* dst_stride, int scale_dt,
+                   void* stream)
+{
+    clear_error();
+    CHECK(mirror && seg_bytes && copy_list && state && dst && dst_stride, "vq2_pager_copy: NULL pointer");
+    CHECK(dt_ok(scale_dt), "vq2_pager_copy: bad scale dtype");
+    return pager_copy_launch(mirror, record_bytes, seg_bytes, copy_list, state, max_copies, dst, dst_stride, scale_dt,
+                             stream);
+}
+
 int vq2_dequant_rows(const int16_t* idx0, const void* idx1, int s2_kind, const void* cb0, const void* cb1, int cb_dt,
                      const void* scale, int s_dt, int64_t r0, int64_t r1, int64_t n, float* out, void* stream)
 {

@@ -228,6 +228,15 @@ struct SortedMoeCall {
 size_t sorted_moe_workspace_bytes(int64_t n_pairs, int64_t hidden, int64_t inter, int slices_gu, int slices_dn);
 int sorted_moe_launch(const SortedMoeCall& c);
 
+// Device-resident expert pager (vq2_pager.hip).
+size_t pager_lds_bytes(int64_t n_experts, int64_t capacity, int64_t n_pairs);
+int pager_step_launch(const void* ids, int ids_i64, int64_t n_pairs, int64_t n_experts, int64_t capacity,
+                      int32_t* slot_of, int32_t* expert_of, int32_t* stamp, int32_t* state, int32_t* copy_list,
+                      int32_t* pair_slot, void* stream);
+int pager_copy_launch(const void* mirror_host, int64_t record_bytes, const int64_t* seg_bytes, const int32_t* copy_list,
+                      const int32_t* state, int64_t max_copies, void* const* dst, const int64_t* dst_stride,
+                      int scale_dt, void* stream);
+
 int rht_launch(const void* x, int x_dt, int64_t x_stride, void* y, int y_dt, int64_t y_stride,
                const int32_t* perm, const int8_t* sign, int64_t n, int64_t hb, int64_t batch, float scale,
                int inverse, int swiglu, int64_t inter, void* stream);

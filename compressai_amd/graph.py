@@ -7,8 +7,9 @@ vq2/generate.py:49-71: warm-up on a side stream, capture, then
 for any step built from this library: every C entry takes device pointers,
 enqueues work only (no allocation, no host synchronisation), so a step made
 of ``PackedLinear``, ``MoELayer`` / ``ResidentMoEExperts``, the RHT, the
-small-M GEMM and the LM-head argmax captures as it is.  (``PagedMoEExperts``
-does not: its paging decision reads the routed ids on the host.)
+small-M GEMM and the LM-head argmax captures as it is.  ``PagedMoEExperts``
+captures with ``device_tables=True`` (the pager then runs on the device); its
+host pager reads the routed ids on the host and does not.
 """
 from __future__ import annotations
 

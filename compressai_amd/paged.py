@@ -47,6 +47,7 @@ output.
 """
 from __future__ import annotations
 
+import ctypes
 import json
 import os
 import struct
@@ -206,10 +207,19 @@ def write_vq2m(path, gate_up_idx, gate_up_scale, down_idx, down_scale, meta=None
 
 class ExpertPager:
     """Device pool of `capacity` expert slots of one layer, filled from a
-    Vq2mStore, LRU replacement (vq2/paged_runtime.py:415-437)."""
+    Vq2mStore, LRU replacement (vq2/paged_runtime.py:415-437).
+
+    ``device_tables=True`` (GPU only): the slot tables live on the device
+    and each step is paged by two launches (vq2_pager_step, vq2_pager_copy)
+    from a pinned host mirror of the layer's records, read from the file
+    once here: no host synchronisation, so the step can be captured in a HIP
+    graph.  The least recently used slot a step does not need is replaced,
+    as on the host; an expert id outside the layer, or more distinct experts
+    in a step than slots, gives NaN rows and sets ``errors`` (bit 1 / bit 2)
+    instead of raising."""
 
     def __init__(self, store: Vq2mStore, layer: int, capacity: int, device, staging: int = 16,
-                 scale_dtype=torch.bfloat16):
+                 scale_dtype=torch.bfloat16, device_tables: bool = False):
         self.store, self.layer, self.capacity = store, int(layer), int(capacity)
         self.device = torch.device(device)
         s = store
@@ -220,20 +230,89 @@ class ExpertPager:
         self.pool_dn_scale = torch.empty((capacity, s.dn_rows), dtype=sdt, device=self.device)
         self.slot_of: OrderedDict[int, int] = OrderedDict()  # expert -> slot, least recently used first
         self.free = list(range(capacity - 1, -1, -1))
-        self.hits = self.misses = 0
+        self._hits = self._misses = 0
         cuda = self.device.type == "cuda"
         self.cuda = cuda
+        self.device_tables = bool(device_tables)
+        if self.device_tables:
+            self._init_device_tables()
+            return
         self.ring = [torch.empty(s.record_bytes, dtype=torch.uint8, pin_memory=cuda) for _ in range(staging)]
         self.ring_event = [None] * staging
         self.ring_pos = 0
         self.copy_stream = torch.cuda.Stream(device=self.device) if cuda else None
 
+    # ------------------------------------------------------ device tables
+    def _init_device_tables(self):
+        s, dev = self.store, self.device
+        if not self.cuda:
+            raise K.Vq2Error("device_tables needs a GPU device")
+        if any(sz % 16 for sz in s.sizes):
+            raise K.Vq2Error(f"device_tables needs 16-byte record segments, got {s.sizes}")
+        if s.promoted_experts(self.layer):
+            raise K.Vq2Error(f"layer {self.layer} holds promoted 3-bit experts: use the host pager")
+        E, C = s.num_experts, self.capacity
+        self.mirror = torch.empty((E, s.record_bytes), dtype=torch.uint8, pin_memory=True)
+        for e in range(E):
+            s.read_record(self.layer, e, memoryview(self.mirror[e].numpy()))
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.d_slot_of = torch.full((E,), -1, **i32)
+        self.d_expert_of = torch.full((C,), -1, **i32)
+        self.d_stamp = torch.full((C,), -1, **i32)
+        self.d_state = torch.zeros(5, **i32)
+        self._seg = (ctypes.c_int64 * 4)(*s.sizes)
+        pools = (self.pool_gu_idx, self.pool_gu_scale, self.pool_dn_idx, self.pool_dn_scale)
+        self._dst = (ctypes.c_void_p * 4)(*[t.data_ptr() for t in pools])
+        self._dst_stride = (ctypes.c_int64 * 4)(*[t[0].numel() * t.element_size() for t in pools])
+        self._scale_dt = K._dt(self.pool_gu_scale, "scale")
+        self._bufs = {}
+
+    def step(self, ids):
+        """Slots of a step's routed ids (device int32 / int64 [T, P]) ->
+        device int32 [T, P], paged on the device (device_tables mode)."""
+        if not self.device_tables:
+            raise K.Vq2Error("step() pages on the device: construct with device_tables=True")
+        ids = ids.contiguous()
+        n = ids.numel()
+        if ids.dtype not in (torch.int32, torch.int64) or ids.device != self.device:
+            raise K.Vq2Error("ids must be int32 / int64 on the pool's device")
+        if n not in self._bufs:
+            self._bufs[n] = (torch.empty((n, 2), dtype=torch.int32, device=self.device),
+                             torch.empty(n, dtype=torch.int32, device=self.device))
+        copy_list, pair_slot = self._bufs[n]
+        st = K._stream(self.device)
+        i64 = 1 if ids.dtype == torch.int64 else 0
+        E = self.store.num_experts
+        K._lib.call("vq2_pager_step", ids.data_ptr(), i64, n, E, self.capacity, self.d_slot_of.data_ptr(),
+                    self.d_expert_of.data_ptr(), self.d_stamp.data_ptr(), self.d_state.data_ptr(),
+                    copy_list.data_ptr(), pair_slot.data_ptr(), st)
+        K._lib.call("vq2_pager_copy", self.mirror.data_ptr(), self.store.record_bytes, self._seg,
+                    copy_list.data_ptr(), self.d_state.data_ptr(), n, self._dst, self._dst_stride, self._scale_dt, st)
+        return pair_slot.view(ids.shape)
+
+    def _device_state(self):
+        return self.d_state.cpu().tolist()
+
+    @property
+    def hits(self):
+        return self._device_state()[2] if self.device_tables else self._hits
+
+    @property
+    def misses(self):
+        return self._device_state()[3] if self.device_tables else self._misses
+
+    @property
+    def errors(self):
+        """Device tables: bit 1 = an expert id outside the layer, bit 2 = more
+        distinct experts in a step than slots (those pairs gave NaN)."""
+        return self._device_state()[4] if self.device_tables else 0
+
     def _slot(self, expert: int, pending: list) -> int:
         if expert in self.slot_of:
-            self.hits += 1
+            self._hits += 1
             self.slot_of.move_to_end(expert)
             return self.slot_of[expert]
-        self.misses += 1
+        self._misses += 1
         # with at most `capacity` distinct experts per step the least recently
         # used resident expert is never one this step needs
         slot = self.free.pop() if self.free else self.slot_of.popitem(last=False)[1]
@@ -246,6 +325,8 @@ class ExpertPager:
         the copies are queued and the current stream is made to wait for them.
         A request that cannot be served changes nothing; a failed read drops
         the experts it was loading from the pool."""
+        if self.device_tables:
+            raise K.Vq2Error("this pager keeps its tables on the device: use step()")
         ex = [int(e) for e in experts]
         for e in ex:
             if not 0 <= e < self.store.num_experts:
@@ -308,9 +389,10 @@ class PagedMoEExperts(torch.nn.Module):
     the layer holds promoted 3 bpw experts."""
 
     def __init__(self, layer: int, store: Vq2mStore, cb16, capacity: int = 96, device="cuda", staging: int = 16,
-                 act_dtype=torch.float32, out_dtype=None, cb8=None, scale_dtype=torch.bfloat16):
+                 act_dtype=torch.float32, out_dtype=None, cb8=None, scale_dtype=torch.bfloat16,
+                 device_tables: bool = False):
         super().__init__()
-        self.pager = ExpertPager(store, layer, capacity, device, staging, scale_dtype)
+        self.pager = ExpertPager(store, layer, capacity, device, staging, scale_dtype, device_tables)
         self.cb16 = cb16
         self.hidden_dim = store.gu_cols * 8
         self.intermediate_dim = store.dn_cols * 8
@@ -371,6 +453,16 @@ class PagedMoEExperts(torch.nn.Module):
         p = self.pager
         h = hidden_states.reshape(-1, self.hidden_dim).contiguous()
         T = h.shape[0]
+        if p.device_tables:
+            # paged on the device: no host synchronisation (graph-capturable)
+            ids_d = topk_idx.reshape(T, -1)
+            if ids_d.dtype not in (torch.int32, torch.int64):
+                ids_d = ids_d.to(torch.int32)
+            P = ids_d.shape[1]
+            w = topk_weights.reshape(T, P).to(device=h.device, dtype=torch.float32).contiguous()
+            slots = p.step(ids_d.to(h.device))
+            regular = (p.pool_gu_idx, None, p.pool_gu_scale, p.pool_dn_idx, None, p.pool_dn_scale)
+            return self._run(h, slots, w, regular).to(self.out_dtype or hidden_states.dtype)
         ids_host = topk_idx.reshape(T, -1).to("cpu")  # the paging decision is made on the host
         P = ids_host.shape[1]
         w = topk_weights.reshape(T, P).to(device=h.device, dtype=torch.float32).contiguous()

@@ -447,6 +447,34 @@ int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token,
                    const vq2_rot_tables* rot_h, const vq2_rot_tables* rot_i, void* out, int out_dt,
                    int slices_gu, int slices_dn, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---- Device-resident expert pager ---------------------------------------
+ * The slot tables of a paged expert pool on the device: slot_of
+ * [n_experts] (slot or -1), expert_of [capacity] (expert or -1), stamp
+ * [capacity] (step clock of the last use, -1 when never used; initialise
+ * all three to -1) and state int32 [5] (clock, copies of the last step,
+ * hits, misses, error bits: 1 = an expert id outside [0, n_experts),
+ * 2 = more distinct experts in a step than slots; initialise to 0).
+ * vq2_pager_step (one workgroup) pages one step's routed ids [n_pairs]
+ * (int32 / int64): resident experts keep their slots, missing ones (distinct,
+ * in pair order) take the least recently used slots the step does not use;
+ * it writes pair_slot [n_pairs] (-1 for a pair it cannot serve) and the
+ * (expert, slot) copies [n_pairs][2].  vq2_pager_copy then copies those
+ * experts' records from `mirror`, pinned host memory holding the layer's
+ * container records [n_experts][record_bytes] back to back (segments:
+ * gate_up index plane, its fp16 scales, down index plane, its fp16 scales,
+ * seg_bytes[4], each a multiple of 16), into dst[4] at slot * dst_stride[s]
+ * bytes; the scales are converted to scale_dt.  max_copies = n_pairs.  No
+ * host synchronisation: a paged step can be captured in a HIP graph.
+ * Replaces the host LRU and synchronous per-slot copies of
+ * PagedMoEExpert._get_slot / forward (vq2/paged_runtime.py:415-437, 491-500). */
+size_t vq2_pager_lds_bytes(int64_t n_experts, int64_t capacity, int64_t n_pairs);
+int vq2_pager_step(const void* ids, int ids_i64, int64_t n_pairs, int64_t n_experts, int64_t capacity,
+                   int32_t* slot_of, int32_t* expert_of, int32_t* stamp, int32_t* state, int32_t* copy_list,
+                   int32_t* pair_slot, void* stream);
+int vq2_pager_copy(const void* mirror, int64_t record_bytes, const int64_t* seg_bytes, const int32_t* copy_list,
+                   const int32_t* state, int64_t max_copies, void* const* dst, const int64_t* dst_stride, int scale_dt,
+                   void* stream);
+
 /* Rotated-space dequantisation of rows [r0, r1) (debug / audit):
  *   W[r, 8g+j] = (f32(cb0[i0]) [+ f32(cb1[i1])]) * f32(scale[r]), fp32 [r1-r0, n]
  * rounded exactly in that order (no contraction).
