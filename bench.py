@@ -18,7 +18,7 @@ T = 1) in us per layer over a 40-layer resident pool, the config-3 LM head
 the host (``cpu_baseline``).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
-                       [--only dominant|dominant_gather|copy|moe|paged] (single-part modes for rocprofv3 runs)
+                       [--only dominant|dominant_gather|dense|copy|moe|paged] (single-part modes for rocprofv3 runs)
 """
 from __future__ import annotations
 
@@ -336,8 +336,10 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
 
 def bench_lm_head(args, dev, batch=1, copies=14):
     """LM head 151936 x 2048 at 2 bpw + top-1 over 14 copies
-    (1.1 GiB).  Batch 1: the sorted layout (as PackedLMHead.argmax runs it)
-    and the gather kernel; batch 4: the matrix-core path."""
+    (1.1 GiB).  Batch 1: the sorted layout with the RHT of the fp16
+    activation built in the kernel (as PackedLMHead.argmax runs it), the
+    same on a pre-rotated activation, and the gather kernel (pre-rotated);
+    batch 4: the matrix-core path (pre-rotated)."""
     import torch
 
     from compressai_amd import kernels as K, synth
@@ -350,6 +352,8 @@ def bench_lm_head(args, dev, batch=1, copies=14):
         i0, s = rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)
         mats.append((i0, s, K.SortedPlanes(i0, None, out, n, device=dev) if batch == 1 else None))
     x = synth.activations(3004, (batch, n), dtype=torch.float32).to(dev)
+    xh = synth.activations(3005, (batch, n), dtype=torch.float16).to(dev)
+    perm, sign = synth.permutation(3006, n).to(dev), synth.signs(3007, n).to(dev)
     ws = torch.empty(batch, out, dtype=torch.float32, device=dev)
     res = [None] * copies
     nbytes = out * (n // 8) * 2 + out * 2
@@ -370,11 +374,17 @@ def bench_lm_head(args, dev, batch=1, copies=14):
         _, s, sp = mats[l]
         res[l] = K.vq_sorted_gemv_argmax(x, sp, s, cb, None, n)
 
+    def f_sorted_rht(l):
+        _, s, sp = mats[l]
+        res[l] = K.vq_sorted_gemv_argmax(xh, sp, s, cb, None, n, perm, sign, 2048)
+
     out_d = {}
     if batch == 1:
-        us = run(f_sorted)
+        us = run(f_sorted_rht)
+        out_d["prerotated_us"] = run(f_sorted)
         out_d["gather_us"] = run(f_gather)
-        log(f"lm head B=1 (gather kernel): {out_d['gather_us']:.2f} us/call")
+        log(f"lm head B=1 (sorted layout, pre-rotated x): {out_d['prerotated_us']:.2f} us/call")
+        log(f"lm head B=1 (gather kernel, pre-rotated x): {out_d['gather_us']:.2f} us/call")
     else:
         us = run(f_gather)
     gbps = nbytes / (us * 1e-6) / 1e9
@@ -646,7 +656,7 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "dominant_gather", "copy", "moe", "paged"], default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "dense", "copy", "moe", "paged"], default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -673,6 +683,13 @@ def main():
             fn(dl.layers[l], ("gate", "up"), dl.x_mlp, dl.perm_h, dl.sign_h)
         torch.cuda.synchronize(dev)
         log(f"{args.only}-only run done")
+        return
+    if args.only == "dense":
+        dl = DenseLayers(args.layers, dev)
+        for l in range(args.layers):
+            dl.step(l)
+        torch.cuda.synchronize(dev)
+        log("dense-only run done")
         return
     if args.only == "paged":
         bench_paged(args, dev)
@@ -731,6 +748,7 @@ def main():
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "lm_head_us_b1_prerotated": None if lm1 is None else round(lm1["prerotated_us"], 3),
         "lm_head_us_b1_gather_kernel": None if lm1 is None else round(lm1["gather_us"], 3),
         "dense_step_us_gather_kernel": round(d["gather_step_us"], 3),
         "gate_up_us_gather_kernel": round(d["dom_gather_us"], 3),

@@ -276,8 +276,13 @@ struct SortedArgs {
 
 // XM 0: x holds the rotated activation (dtype XT); XM 1: rotate x in LDS.
 // EP 0: store y (or partials with several slices); EP 1: fused top-1 keys.
+// The fused-RHT top-1 (the LM head: 768 workgroups, three per CU) is held
+// to 64 VGPRs so that two workgroups share a CU and one's prologue overlaps
+// the other's gathers (measured 72.5 against 77.8 us at 70 VGPRs); the
+// other instantiations run one workgroup per CU, where that bound only
+// costs spills (gate+up 19.1 -> 20.0 us).
 template <int CBT, int XM, int XT, int EP>
-__global__ void __launch_bounds__(SG_THREADS) vq_sorted_kernel(const SortedArgs a)
+__global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_sorted_kernel(const SortedArgs a)
 {
     extern __shared__ __align__(16) float smem[];
     touch_kernargs(a);
