@@ -716,8 +716,8 @@ int vq2_sorted_gemv(const void* x, int x_dt, const int32_t* perm, const int8_t* 
 
 size_t vq2_sorted_gemv_argmax_workspace(const vq2_sorted_mat* mat)
 {
-    if (!mat || mat->rows_per_chunk < 1 || mat->out_rows < 1) return 0;
-    return (size_t)((mat->out_rows + mat->rows_per_chunk - 1) / mat->rows_per_chunk) * sizeof(uint64_t);
+    if (!mat) return 0;
+    return sorted_top1_workspace_bytes(mat->out_rows, mat->rows_per_chunk);
 }
 
 int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const int8_t* sign, int64_t hb,
@@ -731,10 +731,8 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
                         VQ2_DT_F32, n, rs, 1, stream);
     if (r) return r;
     CHECK(out_idx && (uintptr_t)out_idx % 8 == 0, "vq2_sorted_gemv_argmax: out_idx must be 8-byte aligned");
-    const size_t need = vq2_sorted_gemv_argmax_workspace(mat);
-    CHECK(workspace && ws_bytes >= need && (uintptr_t)workspace % 8 == 0,
-          "vq2_sorted_gemv_argmax: workspace of %zu bytes (8-byte aligned) needed", need);
-    c.cand = (uint64_t*)workspace;
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
     return sorted_launch(c, out_idx, out_val);
 }
 

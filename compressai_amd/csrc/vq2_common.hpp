@@ -168,6 +168,16 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int64_t col)
     return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
 }
 
+// The column and value an argmax_key encodes.
+__device__ __forceinline__ void argmax_key_decode(uint64_t key, int64_t* idx, float* val)
+{
+    const uint32_t lo = (uint32_t)(key & 0xFFFFFFFFu);
+    uint32_t u = (uint32_t)(key >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    if (val) *val = __uint_as_float(u);
+    *idx = (int64_t)(0xFFFFFFFFu - lo);
+}
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
 
 // Touch every 64-byte line of the kernel arguments with independent scalar
@@ -186,6 +196,49 @@ __device__ __forceinline__ void touch_kernargs(const T& a)
     // store to a sink compiled to a flat store, after which the compiler's
     // memory-counter waits fall back to waiting for every outstanding load.)
     asm volatile("; kernarg lines touched %0" ::"s"(h));
+}
+
+// ------------------------------------------- in-kernel split reductions
+// A reduction split over workgroups is finished by the workgroup that
+// arrives last, instead of by a second launch.  Each workgroup writes its
+// share with agent-scope atomic stores (written through the XCD-private L2
+// to the device's coherence point), waits until they are complete, and
+// counts itself in; the one whose increment completes the count reads every
+// share with agent-scope atomic loads (which do not hit stale L2 lines of
+// another XCD's data) and puts the counter back to 0 for the next launch.
+// Every location involved is only ever accessed through agent-scope atomics,
+// so no agent-scope fence is needed (on gfx950 a release fence writes the
+// whole L2 back and an acquire fence invalidates it: the codebook lines the
+// other workgroups of that XCD are reading would be fetched again).
+__device__ __forceinline__ void share_store(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float share_load(const float* p)
+{
+    return __hip_atomic_load((float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of the workgroup after its share_store()s; true in
+// every thread of the workgroup whose arrival is number `expected` at cnt.
+// The counter must be 0 before the launch's first arrival; the last arrival
+// leaves it 0.
+__device__ __forceinline__ bool arrive_last(uint32_t* cnt, uint32_t expected)
+{
+    __shared__ int s_last;
+    // this wave's share stores are complete (acknowledged at the coherence
+    // point) before the barrier, so all of the workgroup's are before the
+    // increment
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old + 1u == expected;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    return s_last != 0;
 }
 
 }  // namespace vq2

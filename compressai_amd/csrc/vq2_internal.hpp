@@ -152,7 +152,6 @@ struct SortedCall {
     SortedSegCall seg[4];
     void* workspace;
     size_t ws_bytes;
-    uint64_t* cand;  // top-1: one key per workgroup
     void* stream;
 };
 
@@ -161,6 +160,7 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
                 uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
                 int n_threads);
 size_t sorted_workspace_bytes(const SortedCall& c);
+size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk);
 // top1_idx non-null: fused top-1 (one matrix, one slice) instead of y
 int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);
 

@@ -72,11 +72,7 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const uint64_t* cand,
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = s_best[w] > best ? s_best[w] : best;
-        const uint32_t lo = (uint32_t)(best & 0xFFFFFFFFu);
-        uint32_t u = (uint32_t)(best >> 32);
-        u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
-        if (out_val) out_val[b] = __uint_as_float(u);
-        out_idx[b] = (int64_t)(0xFFFFFFFFu - lo);
+        argmax_key_decode(best, out_idx + b, out_val ? out_val + b : nullptr);
     }
 }
 

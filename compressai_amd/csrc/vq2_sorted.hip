@@ -251,7 +251,8 @@ struct SortedSeg {
     const int32_t* cit1;  // [n_chunks]
     const void* scale;
     void* y;
-    float* part;  // slices > 1: [slices][out_rows]
+    float* part;    // slices > 1: [slices][out_rows] raw row sums
+    uint32_t* cnt;  // slices > 1: arrival counter per chunk
     int64_t out_rows;
     int32_t n_iters;
     int32_t n_chunks;
@@ -354,21 +355,26 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
         }
     } else if (a.slices == 1) {
         if (own) store_from_f32(sg.y, a.y_dt, row, (sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs);
-    } else if (own) {
-        sg.part[(int64_t)slice * sg.out_rows + row] = sum;
+    } else {
+        // several slices: the last of the chunk's workgroups to finish adds
+        // the slices' raw row sums in slice order
+        if (own) share_store(sg.part + (int64_t)slice * sg.out_rows + row, sum);
+        if (arrive_last(sg.cnt + chunk, (uint32_t)a.slices) && own) {
+            float tot = 0.0f;
+            for (int s0 = 0; s0 < a.slices; s0 += 8) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int s = s0 + j < a.slices ? s0 + j : slice;
+                    v[j] = s == slice ? sum : share_load(sg.part + (int64_t)s * sg.out_rows + row);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (s0 + j < a.slices) tot += v[j];
+            }
+            store_from_f32(sg.y, a.y_dt, row, (tot * load_as_f32(sg.scale, a.s_dt, row)) * a.rs);
+        }
     }
-}
-
-// y[row] = (sum over slices of part[slice][row], in slice order) * s * rs;
-// blockIdx.y = segment.
-__global__ void __launch_bounds__(256) vq_sorted_reduce_kernel(const SortedArgs a)
-{
-    const SortedSeg& sg = a.seg[blockIdx.y];
-    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (row >= sg.out_rows) return;
-    float sum = 0.0f;
-    for (int s = 0; s < a.slices; s++) sum += sg.part[(int64_t)s * sg.out_rows + row];
-    store_from_f32(sg.y, a.y_dt, row, (sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs);
 }
 
 // ------------------------------------------------------------------ launch
@@ -403,12 +409,21 @@ static hipError_t launch_sorted_x(int xm, int x_dt, const SortedArgs& a, unsigne
     }
 }
 
+// Workspace with several slices: VQ2_SORTED_WS_HEADER bytes of arrival
+// counters (zero between launches), then the slices' raw row sums (matrix
+// after matrix).  Top-1: one key per workgroup.
 size_t sorted_workspace_bytes(const SortedCall& c)
 {
     if (c.slices <= 1) return 0;
-    size_t b = 0;
+    size_t b = VQ2_SORTED_WS_HEADER;
     for (int s = 0; s < c.nseg; s++) b += (size_t)c.slices * c.seg[s].out_rows * sizeof(float);
     return b;
+}
+
+size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk)
+{
+    if (rows_per_chunk < 1 || out_rows < 1) return 0;
+    return (size_t)((out_rows + rows_per_chunk - 1) / rows_per_chunk) * sizeof(uint64_t);
 }
 
 int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
@@ -467,14 +482,21 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     a.slices = c.slices;
     a.rs = c.rs;
     a.nseg = c.nseg;
-    a.cand = c.cand;
-    float* part = (float*)c.workspace;
-    if (!top1 && c.slices > 1) {
+    uint32_t* cnt = (uint32_t*)c.workspace;
+    float* part = (float*)((char*)c.workspace + VQ2_SORTED_WS_HEADER);
+    if (top1) {
+        const size_t need = sorted_top1_workspace_bytes(c.seg[0].out_rows, c.seg[0].rows_per_chunk);
+        if (!c.workspace || c.ws_bytes < need || (uintptr_t)c.workspace % 8)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: workspace of %zu bytes (8-byte aligned) needed, got "
+                             "%zu", need, c.ws_bytes);
+        a.cand = (uint64_t*)c.workspace;
+    } else if (c.slices > 1) {
         const size_t need = sorted_workspace_bytes(c);
-        if (!c.workspace || c.ws_bytes < need)
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: workspace of %zu bytes needed (got %zu)", need, c.ws_bytes);
+        if (!c.workspace || c.ws_bytes < need || (uintptr_t)c.workspace % 16)
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: workspace of %zu bytes (16-byte aligned) needed, got %zu",
+                             need, c.ws_bytes);
     }
-    int64_t wg = 0, max_rows = 0;
+    int64_t wg = 0, n_cnt = 0;
     for (int s = 0; s < c.nseg; s++) {
         const SortedSegCall& sc = c.seg[s];
         const int64_t R = sc.rows_per_chunk;
@@ -494,30 +516,29 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         a.seg[s].wg_start = (int32_t)wg;
         a.seg[s].R = (int32_t)R;
         a.seg[s].part = part;
-        if (!top1 && c.slices > 1) part += c.slices * sc.out_rows;
+        a.seg[s].cnt = cnt + n_cnt;
+        if (!top1 && c.slices > 1) {
+            part += c.slices * sc.out_rows;
+            n_cnt += n_chunks;
+        }
         wg += n_chunks * c.slices;
-        max_rows = std::max(max_rows, sc.out_rows);
     }
+    if (n_cnt > VQ2_SORTED_MAX_COUNTERS)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: %lld chunks with several slices (at most %d)",
+                         (long long)n_cnt, VQ2_SORTED_MAX_COUNTERS);
     if (wg == 0) return VQ2_OK;
     if (wg > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: grid too large");
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {
-        if (!c.cand) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: no candidate buffer");
         err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
                                     : launch_sorted_x<VQ2_DT_BF16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
         if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
-        return argmax_final_launch(c.cand, wg, 1, top1_idx, top1_val, c.stream);
+        return argmax_final_launch(a.cand, wg, 1, top1_idx, top1_val, c.stream);
     }
     err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
                                 : launch_sorted_x<VQ2_DT_BF16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
-    if (c.slices > 1) {
-        hipLaunchKernelGGL(vq_sorted_reduce_kernel, dim3((unsigned)((max_rows + 255) / 256), (unsigned)c.nseg), dim3(256),
-                           0, st, a);
-        err = hipGetLastError();
-        if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV reduce launch");
-    }
     return VQ2_OK;
 }
 

@@ -222,8 +222,11 @@ def vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bflo
     return y
 
 
-# Split-K partials of vq_gemm_small_m, one buffer per (device, stream):
-# launches on one stream run in order, so they can share it.  The buffers
+# Split-K partials of vq_gemm_small_m and the sorted launches (in a zeroed
+# buffer of their own, the arrival counters and partials of vq_sorted_gemv),
+# one buffer per
+# (device, stream): launches on one stream run in order, so they can share
+# it.  The buffers
 # only grow, and a buffer that a larger one replaces is kept alive until the
 # process ends: a HIP graph captured earlier holds its raw address and writes
 # into it on every replay.
@@ -231,15 +234,20 @@ _WS: dict = {}
 _WS_RETIRED: list = []
 
 
-def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor | None:
+def _workspace(dev: torch.device, nbytes: int, *, sorted_kind: bool = False) -> torch.Tensor | None:
+    """The workspace of this (device, stream).  vq_sorted_gemv gets one of
+    its own, allocated zeroed: it begins with arrival counters that must be
+    zero before a launch (each launch leaves them zero), which another
+    kernel's partials must never overwrite."""
     if nbytes == 0:
         return None
-    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream, sorted_kind)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
         if buf is not None:
             _WS_RETIRED.append(buf)
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        alloc = torch.zeros if sorted_kind else torch.empty
+        buf = alloc(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _WS[key] = buf
     return buf
 
@@ -459,8 +467,9 @@ def vq_sorted_gemv(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scal
     """Batch-1 VQ GEMV of up to 4 matrices in the code-sorted layout that
     share one activation: y_m = VQ(W_m) RHT(x) (hb > 0: the rotation is built
     in the kernel's LDS; hb = 0: x is already rotated).  mats: list of
-    (SortedPlanes, scale).  With several workgroups (slices) per chunk a
-    second launch sums their partials.  Returns the list of outputs [out_rows]."""
+    (SortedPlanes, scale).  With several workgroups (slices) per chunk the
+    last of them to finish sums their partials, in slice order, in the same
+    launch.  Returns the list of outputs [out_rows]."""
     n = int(n)
     planes = [m[0] for m in mats]
     if not 1 <= len(mats) <= 4 or any(p.n != n for p in planes):
@@ -482,7 +491,7 @@ def vq_sorted_gemv(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scal
         arr[k] = p.mat(s, y)
     slices = sorted_slices(planes, dev) if slices is None else int(slices)
     lib = _lib.load()
-    ws = _workspace(dev, int(lib.vq2_sorted_gemv_workspace(arr, len(mats), slices)))
+    ws = _workspace(dev, int(lib.vq2_sorted_gemv_workspace(arr, len(mats), slices)), sorted_kind=True)
     _lib.call("vq2_sorted_gemv", _p(x2), _dt(x2, "x"), _p(perm), _p(sign), hb, sc, len(mats), arr, _p(cb0), _p(cb1),
               _dt(cb0, "cb0"), _dt(mats[0][1], "scale"), _dt(ys[0], "y"), n, float(rs), slices, _p(ws),
               0 if ws is None else ws.numel(), _stream(dev))

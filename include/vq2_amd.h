@@ -347,6 +347,17 @@ int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, 
                     uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1,
                     int64_t* n_iters, int n_threads);
 
+/* The workspace of vq2_sorted_gemv begins with VQ2_SORTED_WS_HEADER bytes
+ * of arrival counters: the slices of a chunk are summed inside the launch
+ * by the chunk's workgroup that arrives last.  The header must be zero
+ * before the first call that uses the workspace (e.g. allocate it zeroed);
+ * every call leaves it zero.  One workspace may serve all vq2_sorted_gemv
+ * calls of a stream; calls that share a workspace must not run
+ * concurrently.  A launch with several slices has at most
+ * VQ2_SORTED_MAX_COUNTERS chunks. */
+#define VQ2_SORTED_WS_HEADER 16384
+#define VQ2_SORTED_MAX_COUNTERS (VQ2_SORTED_WS_HEADER / 4)
+
 /* One packed matrix of a sorted launch (device pointers, except the struct). */
 typedef struct vq2_sorted_mat {
     const uint32_t* entries;  /* from vq2_sorted_pack, copied to the device    */
@@ -366,7 +377,8 @@ typedef struct vq2_sorted_mat {
  *   y_m[r] = (sum_k W_m[r, k] * xr[k]) * scale_m[r] * rs
  * fp16 / bf16 codebooks.  `slices` workgroups share each chunk; with more
  * than one the raw partials go to `workspace` (vq2_sorted_gemv_workspace
- * bytes) and a second launch sums them in slice order.  Replaces FastRot +
+ * bytes, zeroed header) and the chunk's last workgroup to finish sums them
+ * in slice order (one launch; deterministic).  Replaces FastRot +
  * vq_gemv_16 of PackedLinear.forward (vq2/runtime.py:91-104) and its
  * (16,16) fallback (vq2/runtime.py:105-110) for large matrices. */
 size_t vq2_sorted_gemv_workspace(const vq2_sorted_mat* mats, int n_mat, int slices);

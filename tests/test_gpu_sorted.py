@@ -88,9 +88,45 @@ def test_sorted_gemv_qkv_segments_and_determinism(dev):
         assert torch.equal(a, b)
 
 
+def _sorted_counters(dev):
+    """The arrival-counter header of this stream's sorted workspace."""
+    ws = K._WS[(dev.index, torch.cuda.current_stream(dev).cuda_stream, True)]
+    return ws[:16384].view(torch.int32)
+
+
+@pytest.mark.parametrize("rows,n,bpw,slices,n_mat", [
+    (6144, 2048, 4, 5, 2),    # the gate + up call
+    (2048, 6144, 4, 7, 1),    # down
+    (700, 1024, 2, 33, 3),    # many slices, several matrices
+])
+def test_sorted_in_kernel_reduce_fresh_inputs(dev, rows, n, bpw, slices, n_mat):
+    """The chunk's last workgroup sums the slices inside the launch.  Twelve
+    launches back to back on one stream, each with another activation and no
+    synchronisation in between: a share read before its writer's store
+    landed (or left from the previous launch) would show as an error far
+    above the tolerance.  Every output matches the gather kernel on the same
+    input to accumulation-order rounding, and the counters end at zero."""
+    cb0 = synth.codebook(9580).to(dev)
+    cb1 = synth.codebook(9581).to(dev) if bpw == 4 else None
+    ms = [synth.vq_matrix(9582 + k, rows, n, bpw=bpw) for k in range(n_mat)]
+    sps = [K.SortedPlanes(m["idx0"], m["idx1"], rows, n, device=dev) for m in ms]
+    mats = [(sp, m["scale"].to(dev)) for sp, m in zip(sps, ms)]
+    perm, sign = synth.permutation(9586, n).to(dev), synth.signs(9587, n).to(dev)
+    xs = [synth.activations(9600 + i, n, dtype=torch.float16).to(dev) for i in range(12)]
+    hb = min(2048, n)
+    outs = [K.vq_sorted_gemv(x, mats, cb0, cb1, n, perm, sign, hb, slices=slices) for x in xs]
+    torch.cuda.synchronize(dev)
+    assert int(_sorted_counters(dev).abs().sum()) == 0
+    for i, x in enumerate(xs):
+        for k, m in enumerate(ms):
+            (yg,) = K.vq_gemv_rht(x, [(m["idx0"].to(dev), None if m["idx1"] is None else m["idx1"].to(dev),
+                                       m["scale"].to(dev), rows)], cb0, cb1, n, perm, sign, hb)
+            assert O.max_rel_err(outs[i][k].cpu().numpy(), yg.cpu().numpy()) < 1e-5, (i, k)
+
+
 def test_sorted_multi_slice_graph_replays(dev):
-    """A multi-slice launch (partials in the split workspace, summed by the
-    reduce launch) captured in a HIP graph: every replay, with eager launches
+    """A multi-slice launch (partials in the workspace, summed by the chunk's
+    last workgroup) captured in a HIP graph: every replay, with eager launches
     on the same matrix in between, equals the eager result bit for bit."""
     rows, n = 6144, 2048
     m, cb0, cb1, sp = _mk(9570, rows, n, 4, dev)

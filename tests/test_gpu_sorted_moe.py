@@ -101,6 +101,31 @@ def test_sorted_moe_matches_gather_kernels(dev):
     assert O.max_rel_err(a.cpu().numpy(), b.cpu().numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("T,slices", [(1, (5, 3)), (8, (2, 1)), (4, (3, 6))])
+def test_sorted_moe_fresh_inputs_back_to_back(dev, T, slices):
+    """Ten layers back to back on one stream, each with other activations,
+    experts and weights and no synchronisation in between (the workspace of
+    partials and shares is reused by every layer): a value left from the
+    previous layer would show far above the tolerance.  Each output matches
+    the gather kernels on the reference pools."""
+    E, P = 40, 9
+    mod, cb, gu, gus, dn, dns = _module(dev, 9770, E)
+    ref_mod = _module(dev, 9770, E, sorted_layout=False)[0]
+    rh, ri = mod._rots()
+    cases = []
+    for i in range(10):
+        h = synth.activations(9771 + i, (T, 2048), dtype=torch.float16).to(dev)
+        ids = torch.stack([torch.randperm(E, generator=synth.gen(9790 + 10 * i + t))[:P] for t in range(T)]).to(dev)
+        w = torch.softmax(synth.activations(9880 + i, (T, P)).float(), -1).to(dev)
+        cases.append((h, ids, w))
+    outs = [K.vq_sorted_moe(h, mod.sorted_gu, mod.gate_up_scale, mod.sorted_dn, mod.down_scale, mod.cb16, rh, ri,
+                            ids=ids, w=w, slices=slices) for h, ids, w in cases]
+    torch.cuda.synchronize(dev)
+    for i, ((h, ids, w), out) in enumerate(zip(cases, outs)):
+        ref = ref_mod.experts(h, ids, w)
+        assert O.max_rel_err(out.cpu().numpy(), ref.cpu().numpy()) < 1e-5, i
+
+
 def test_sorted_moe_bad_expert_id_gives_nan_token(dev):
     """An id outside the pool (E, or negative) makes its token's output NaN
     and leaves the other tokens exact."""
