@@ -98,7 +98,7 @@ class Seg(ctypes.Structure):
 
 class SortedMat(ctypes.Structure):
     """struct vq2_sorted_mat of include/vq2_amd.h"""
-    _fields_ = [("entries", ctypes.c_void_p), ("chunk_it", ctypes.c_void_p), ("chunk_it1", ctypes.c_void_p),
+    _fields_ = [("entries", ctypes.c_void_p), ("iters_per_chunk", ctypes.c_int64), ("stage1_iters", ctypes.c_int64),
                 ("n_iters", ctypes.c_int64), ("rows_per_chunk", ctypes.c_int64), ("has_stage2", ctypes.c_int),
                 ("scale", ctypes.c_void_p),
                 ("y", ctypes.c_void_p), ("out_rows", ctypes.c_int64)]

@@ -636,15 +636,15 @@ int64_t vq2_sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_al
 }
 
 int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
-                    uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
-                    int n_threads)
+                    uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
+                    int64_t* n_iters, int n_threads)
 {
     clear_error();
-    CHECK(idx0 && entries && chunk_it && chunk_it1 && n_iters, "vq2_sorted_pack: NULL pointer argument");
+    CHECK(idx0 && entries && iters_per_chunk && stage1_iters && n_iters, "vq2_sorted_pack: NULL pointer argument");
     CHECK(out_rows >= 1 && ng >= 1, "vq2_sorted_pack: bad sizes out_rows=%lld ng=%lld", (long long)out_rows,
           (long long)ng);
-    return sorted_pack(idx0, idx1, out_rows, ng, rows_per_chunk, entries, cap_iters, chunk_it, chunk_it1, n_iters,
-                       n_threads);
+    return sorted_pack(idx0, idx1, out_rows, ng, rows_per_chunk, entries, cap_iters, iters_per_chunk, stage1_iters,
+                       n_iters, n_threads);
 }
 
 static int sorted_call(SortedCall& c, const char* who, const void* x, int x_dt, const int32_t* perm,
@@ -678,11 +678,11 @@ static int sorted_call(SortedCall& c, const char* who, const void* x, int x_dt, 
     c.stream = stream;
     for (int i = 0; i < n_mat; i++) {
         const vq2_sorted_mat& m = mats[i];
-        CHECK(m.entries && m.chunk_it && m.chunk_it1 && m.scale, "%s: matrix %d has a NULL pointer", who, i);
+        CHECK(m.entries && m.scale, "%s: matrix %d has a NULL pointer", who, i);
         CHECK(m.out_rows >= 1 && m.n_iters >= 1, "%s: matrix %d: bad sizes", who, i);
         CHECK(!m.has_stage2 || cb1, "%s: matrix %d has stage-2 entries but no cb1", who, i);
         CHECK((m.has_stage2 != 0) == (mats[0].has_stage2 != 0), "%s: the matrices of a launch share one cfg", who);
-        c.seg[i] = SortedSegCall{m.entries, m.chunk_it, m.chunk_it1, m.n_iters, m.rows_per_chunk,
+        c.seg[i] = SortedSegCall{m.entries, m.iters_per_chunk, m.stage1_iters, m.n_iters, m.rows_per_chunk,
                                  m.has_stage2 ? 1 : 0, m.scale, m.y, m.out_rows};
     }
     if (!mats[0].has_stage2) c.cb1 = nullptr;

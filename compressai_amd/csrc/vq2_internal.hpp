@@ -122,8 +122,8 @@ int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val
 // VQ GEMV over the code-sorted internal layout (vq2_sorted.hip).
 struct SortedSegCall {
     const uint32_t* entries;   // [n_iters * 256], 16-byte aligned
-    const int32_t* chunk_it;   // [n_chunks + 1] iteration offsets
-    const int32_t* chunk_it1;  // [n_chunks] stage-1 iterations per chunk
+    int64_t iters_per_chunk;   // every chunk padded to it
+    int64_t stage1_iters;      // of which stage 1 (the stage-2 iterations follow)
     int64_t n_iters;
     int64_t rows_per_chunk;
     int s2;                    // stage-2 entries present (4 bpw)
@@ -157,8 +157,8 @@ struct SortedCall {
 
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
 int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
-                uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
-                int n_threads);
+                uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
+                int64_t* n_iters, int n_threads);
 size_t sorted_workspace_bytes(const SortedCall& c);
 size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk);
 // top1_idx non-null: fused top-1 (one matrix, one slice) instead of y

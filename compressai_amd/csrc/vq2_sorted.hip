@@ -26,8 +26,11 @@
 //  * 4 instructions form an iteration: lane l holds a uint32x4 whose element
 //    q is entry l of instruction q (one 16-byte load per lane);
 //  * the chunk's stage-1 iterations come first, then its stage-2 iterations
-//    (4 bpw); chunk_it[c] / chunk_it1[c] give the iteration offset and the
-//    stage-1 count.
+//    (4 bpw), each stage padded to the matrix's largest count for it (ipc1,
+//    ipc2), so chunk c holds iterations [c * ipc, (c + 1) * ipc), ipc = ipc1
+//    + ipc2: a workgroup computes where its entries are from its chunk index
+//    and issues their loads at once (a table of chunk offsets cost a memory
+//    round trip in front of every other load).
 //
 // Kernel: one workgroup of 16 waves per (chunk, slice).  The workgroup first
 // builds the rotated activation in LDS (the fused RHT prologue of the GEMV
@@ -144,8 +147,8 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
 }
 
 int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t R,
-                uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1, int64_t* n_iters,
-                int n_threads)
+                uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
+                int64_t* n_iters, int n_threads)
 {
     const int64_t rmax = sorted_max_rows(ng);
     if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack: ng=%lld outside 1..32768", (long long)ng);
@@ -153,18 +156,17 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack: rows_per_chunk=%lld outside 1..%lld for ng=%lld",
                          (long long)R, (long long)rmax, (long long)ng);
     const int gb = sorted_gbits(ng);
-    const int64_t n_chunks = (out_rows + R - 1) / R;
-    std::vector<std::vector<uint32_t>> parts((size_t)n_chunks);
-    std::vector<int64_t> it1((size_t)n_chunks);
+    const ChunkSplit ks = chunk_split(out_rows, R);
+    const int64_t n_chunks = ks.n_chunks;
+    std::vector<std::vector<uint32_t>> p1((size_t)n_chunks), p2((size_t)n_chunks);
     int nt = n_threads > 0 ? n_threads : (int)std::thread::hardware_concurrency();
     if (nt < 1) nt = 1;
     if (nt > n_chunks) nt = (int)(n_chunks > 0 ? n_chunks : 1);
     auto work = [&](int t) {
         for (int64_t c = t; c < n_chunks; c += nt) {
-            const int64_t r0 = c * R, rows = std::min(R, out_rows - r0);
-            pack_chunk_stage(idx0, r0, rows, ng, gb, R, parts[c]);
-            it1[c] = (int64_t)parts[c].size() / SG_ITER;
-            if (idx1) pack_chunk_stage(idx1, r0, rows, ng, gb, R, parts[c]);
+            const int64_t r0 = c * ks.rb + std::min(c, ks.nbig), rows = ks.rb + (c < ks.nbig ? 1 : 0);
+            pack_chunk_stage(idx0, r0, rows, ng, gb, R, p1[c]);
+            if (idx1) pack_chunk_stage(idx1, r0, rows, ng, gb, R, p2[c]);
         }
     };
     if (nt == 1) {
@@ -174,21 +176,33 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
         for (int t = 0; t < nt; t++) th.emplace_back(work, t);
         for (auto& t : th) t.join();
     }
-    int64_t total = 0;
-    for (int64_t c = 0; c < n_chunks; c++) total += (int64_t)parts[c].size() / SG_ITER;
+    // every chunk's stages padded to the largest stage-1 / stage-2 iteration
+    // counts, so chunk c holds iterations [c * ipc, (c + 1) * ipc) with its
+    // stage-2 entries from c * ipc + ipc1 on: a workgroup computes where its
+    // entries are instead of reading a table
+    int64_t ipc1 = 0, ipc2 = 0;
+    for (int64_t c = 0; c < n_chunks; c++) {
+        ipc1 = std::max(ipc1, (int64_t)p1[c].size() / SG_ITER);
+        ipc2 = std::max(ipc2, (int64_t)p2[c].size() / SG_ITER);
+    }
+    const int64_t ipc = ipc1 + ipc2;
+    const int64_t total = ipc * n_chunks;
     *n_iters = total;
+    *iters_per_chunk = ipc;
+    *stage1_iters = ipc1;
     if (total > 0x7FFFFFFFLL) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack: matrix too large");
     if (total > cap_iters)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack: %lld iterations needed, capacity %lld", (long long)total,
                          (long long)cap_iters);
-    int64_t off = 0;
+    const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
     for (int64_t c = 0; c < n_chunks; c++) {
-        chunk_it[c] = (int32_t)off;
-        chunk_it1[c] = (int32_t)it1[c];
-        memcpy(entries + off * SG_ITER, parts[c].data(), parts[c].size() * sizeof(uint32_t));
-        off += (int64_t)parts[c].size() / SG_ITER;
+        uint32_t* d1 = entries + c * ipc * SG_ITER;
+        uint32_t* d2 = d1 + ipc1 * SG_ITER;
+        memcpy(d1, p1[c].data(), p1[c].size() * sizeof(uint32_t));
+        std::fill(d1 + p1[c].size(), d2, pad);
+        memcpy(d2, p2[c].data(), p2[c].size() * sizeof(uint32_t));
+        std::fill(d2 + p2[c].size(), d1 + ipc * SG_ITER, pad);
     }
-    chunk_it[n_chunks] = (int32_t)off;
     return VQ2_OK;
 }
 
@@ -206,7 +220,8 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: rows_per_chunk=%lld outside 1..%lld for ng=%lld",
                          (long long)R, (long long)rmax, (long long)ng);
     const int gb = sorted_gbits(ng);
-    const int64_t C = (rows + R - 1) / R;
+    const ChunkSplit ks = chunk_split(rows, R);
+    const int64_t C = ks.n_chunks;
     const int64_t units = n_experts * C;
     std::vector<std::vector<uint32_t>> parts((size_t)units);
     int nt = n_threads > 0 ? n_threads : (int)std::thread::hardware_concurrency();
@@ -215,7 +230,7 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
     auto work = [&](int t) {
         for (int64_t u = t; u < units; u += nt) {
             const int64_t e = u / C, c = u - e * C;
-            const int64_t r0 = c * R, nr = std::min(R, rows - r0);
+            const int64_t r0 = c * ks.rb + std::min(c, ks.nbig), nr = ks.rb + (c < ks.nbig ? 1 : 0);
             pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, parts[u]);
         }
     };
@@ -246,9 +261,9 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
 
 // ------------------------------------------------------------------ kernel
 struct SortedSeg {
-    const u32x4* ent;     // [n_iters * 64] lane words
-    const int32_t* cit;   // [n_chunks + 1]
-    const int32_t* cit1;  // [n_chunks]
+    const u32x4* ent;  // [n_iters * 64] lane words
+    int32_t ipc;       // iterations per chunk (chunk c: [c * ipc, (c + 1) * ipc))
+    int32_t ipc1;      // its stage-1 iterations (the stage-2 ones follow)
     const void* scale;
     void* y;
     float* part;    // slices > 1: [slices][out_rows] raw row sums
@@ -257,7 +272,9 @@ struct SortedSeg {
     int32_t n_iters;
     int32_t n_chunks;
     int32_t wg_start;
-    int32_t R;  // rows per chunk
+    int32_t R;     // rows per chunk at most (row R is the dummy row)
+    int32_t rb;    // chunk c: rows [c * rb + min(c, nbig), + rb + (c < nbig))
+    int32_t nbig;
 };
 
 struct SortedArgs {
@@ -290,8 +307,11 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t n = a.ng * 8;
-    float* s_x = smem;                                  // n floats
-    float* s_acc = smem + n + (XM == 1 ? n : 0);        // SG_WAVES x SG_PARTS x (R + 1)
+    // XM 1: [natural-order activation: n][stage (n), later the split
+    // activation (SG_X_SPLIT)][accumulators]; XM 0: [split][accumulators]
+    float* s_nat = smem;
+    float* s_x = smem + (XM == 1 ? n : 0);              // split activation (SG_X_SPLIT floats)
+    float* s_acc = s_x + SG_X_SPLIT;                    // SG_WAVES x SG_PARTS x (R + 1)
     int si = 0;
 #pragma unroll
     for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && (int)blockIdx.x >= a.seg[s].wg_start) ? 1 : 0;
@@ -299,10 +319,10 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
     const int R = sg.R;
     const int local = (int)blockIdx.x - sg.wg_start;
     const int chunk = local / a.slices, slice = local - chunk * a.slices;
-    const int c_beg = min(sg.cit[chunk], sg.n_iters - 1);  // n_iters >= 1 (checked on the host)
-    const int c_end = min(max(sg.cit[chunk + 1], c_beg), sg.n_iters);
-    const int c_mid = min(c_beg + sg.cit1[chunk], c_end);
-    const int nit = c_end - c_beg;
+    // chunk < n_chunks and n_iters = n_chunks * ipc (checked on the host)
+    const int c_beg = chunk * sg.ipc;
+    const int c_mid = c_beg + sg.ipc1;
+    const int nit = sg.ipc;
     const int s0 = c_beg + (int)((int64_t)nit * slice / a.slices);
     const int s1 = c_beg + (int)((int64_t)nit * (slice + 1) / a.slices);
 
@@ -315,19 +335,26 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
     // and rotates the activation (which waits only for its own, earlier
     // loads); the first gathers go out after it
     // (a pre-rotated x is only copied: there the gathers go out at once)
-    SortedPipe<CBT> pipe;
+    // the 64-VGPR instantiation (two workgroups per CU) gathers one
+    // iteration ahead: the other workgroup hides the latency
+    SortedPipe<CBT, (XM == 1 && EP == 1) ? 1 : 2> pipe;
     pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
     if constexpr (XM == 0) pipe.gathers();
 
     float* acc = sorted_acc(s_acc, wave, lane, R);
     sorted_acc_zero(acc, lane, R);
     if constexpr (XM == 1) {
-        void* s_stage = smem + n;
+        void* s_stage = smem + n;  // dead once build_x is done: the split activation takes its place
         stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
-        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
-        for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] *= a.g.xscale;
+        build_x<1, XT>(a.g, s_nat, s_stage, 1, n, first);
+        x_finalize(s_nat, s_x, n, a.g.xscale);
     } else {
-        for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] = load_as_f32(a.g.x, XT, i);
+        for (int64_t g = threadIdx.x; g < a.ng; g += SG_THREADS) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = load_as_f32(a.g.x, XT, g * 8 + k);
+            x_store_group(s_x, g, v);
+        }
     }
     __syncthreads();
     if constexpr (XM == 1) pipe.gathers();
@@ -337,9 +364,9 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
     __shared__ float s_red[4][256];
     const float sum = sorted_row_sums(s_acc, R, s_red);
     const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
-    const int64_t row0 = (int64_t)chunk * R;
+    const int64_t row0 = (int64_t)chunk * sg.rb + min(chunk, sg.nbig);
     const int64_t row = row0 + rr;
-    const bool own = pp == 0 && rr < R && row < sg.out_rows;
+    const bool own = pp == 0 && rr < sg.rb + (chunk < sg.nbig ? 1 : 0);
     if constexpr (EP == 1) {
         uint64_t best = own ? argmax_key((sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs, row) : 0;
         for (int off = 32; off > 0; off >>= 1) {
@@ -446,8 +473,9 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     if (top1 && (c.slices != 1 || c.nseg != 1))
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: one matrix, one slice");
     const int64_t n = c.ng * 8;
-    const size_t shm = (size_t)(n * (c.xm == 1 ? 2 : 1) + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
-    if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large", (long long)n);
+    const size_t shm = (size_t)((c.xm == 1 ? n : 0) + SG_X_SPLIT + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
+    if (n > 2 * SG_XB || shm > SG_MAX_SHM)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large (at most %d)", (long long)n, 2 * SG_XB);
     if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: codebooks must be 16-byte aligned");
     if (c.xm == 1) {
@@ -500,14 +528,20 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     for (int s = 0; s < c.nseg; s++) {
         const SortedSegCall& sc = c.seg[s];
         const int64_t R = sc.rows_per_chunk;
-        const int64_t n_chunks = (sc.out_rows + R - 1) / R;
+        const ChunkSplit ks = chunk_split(sc.out_rows, R);
+        const int64_t n_chunks = ks.n_chunks;
         if (sc.n_iters < 1 || sc.n_iters > 0x7FFFFFFF)
             return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d has %lld iterations", s, (long long)sc.n_iters);
         if ((uintptr_t)sc.entries % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: entries must be 16-byte aligned");
         if (sc.s2 != (c.cb1 != nullptr)) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: stage-2 entries need cb1");
+        if (sc.iters_per_chunk < 1 || sc.stage1_iters < 0 || sc.stage1_iters > sc.iters_per_chunk ||
+            sc.iters_per_chunk * n_chunks != sc.n_iters || (!sc.s2 && sc.stage1_iters != sc.iters_per_chunk))
+            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d: %lld iterations are not %lld chunks x %lld "
+                             "(%lld of stage 1)", s, (long long)sc.n_iters, (long long)n_chunks,
+                             (long long)sc.iters_per_chunk, (long long)sc.stage1_iters);
         a.seg[s].ent = (const u32x4*)sc.entries;
-        a.seg[s].cit = sc.chunk_it;
-        a.seg[s].cit1 = sc.chunk_it1;
+        a.seg[s].ipc = (int32_t)sc.iters_per_chunk;
+        a.seg[s].ipc1 = (int32_t)sc.stage1_iters;
         a.seg[s].scale = sc.scale;
         a.seg[s].y = sc.y;
         a.seg[s].out_rows = sc.out_rows;
@@ -515,6 +549,8 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         a.seg[s].n_chunks = (int32_t)n_chunks;
         a.seg[s].wg_start = (int32_t)wg;
         a.seg[s].R = (int32_t)R;
+        a.seg[s].rb = (int32_t)ks.rb;
+        a.seg[s].nbig = (int32_t)ks.nbig;
         a.seg[s].part = part;
         a.seg[s].cnt = cnt + n_cnt;
         if (!top1 && c.slices > 1) {

@@ -28,6 +28,23 @@ inline int sorted_gbits(int64_t ng)
     return b;
 }
 
+// Rows are cut into ceil(rows / R) chunks of as equal a height as possible:
+// the first rows % chunks chunks hold rows / chunks + 1 rows, the others
+// rows / chunks, so no chunk is much shorter than the rest (all chunks are
+// padded to one iteration count, and padding is not free).  Chunk c starts
+// at row c * rb + min(c, nbig) and holds rb + (c < nbig) rows.
+struct ChunkSplit {
+    int64_t n_chunks, rb, nbig;
+};
+__host__ __device__ inline ChunkSplit chunk_split(int64_t rows, int64_t R)
+{
+    ChunkSplit k;
+    k.n_chunks = (rows + R - 1) / R;
+    k.rb = k.n_chunks > 0 ? rows / k.n_chunks : 0;
+    k.nbig = k.n_chunks > 0 ? rows % k.n_chunks : 0;
+    return k;
+}
+
 // Largest chunk height for ng groups: row R is the dummy row, so
 // (R << gbits) | group must fit 16 bits; at most SG_MAX_R.
 inline int64_t sorted_max_rows(int64_t ng)
@@ -38,12 +55,51 @@ inline int64_t sorted_max_rows(int64_t ng)
     return rmax < SG_MAX_R ? rmax : SG_MAX_R;
 }
 
-// 8-term dot product of one centroid (fp16 or bf16, 16 bytes) with the
-// group's 8 activation values in LDS, fp32.
-template <int CBT>
-__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* x)
+// The activation in LDS as the loop reads it (fp32, "split" layout): the
+// first 4 values of group g at float offset 4 g, the last 4 at SG_XB + 4 g.
+// A 16-byte stride puts the reads of random groups at 16 bank positions
+// (g mod 16) instead of the 8 of a 32-byte stride (g mod 8), so the lanes
+// the LDS serves together collide less, and both halves come from one
+// address register with an immediate offset.  Needs n <= 2 SG_XB.
+constexpr int SG_XB = 4096;
+constexpr int SG_X_SPLIT = 2 * SG_XB;  // floats of the split activation
+
+__device__ __forceinline__ void x_store_group(float* s_split, int64_t g, const float (&v)[8])
 {
-    const u32x4 x0 = *(const u32x4*)x, x1 = *(const u32x4*)(x + 4);
+    u32x4 w0, w1;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w0[k] = __float_as_uint(v[k]);
+        w1[k] = __float_as_uint(v[4 + k]);
+    }
+    *(u32x4*)(s_split + 4 * g) = w0;
+    *(u32x4*)(s_split + SG_XB + 4 * g) = w1;
+}
+
+// s_split = s_nat (the rotated activation in natural order, fp32, visible
+// after a barrier) times `scale`, one thread per group.  The two regions
+// must not overlap; a barrier must follow.
+__device__ __forceinline__ void x_finalize(const float* s_nat, float* s_split, int64_t n, float scale)
+{
+    for (int64_t g = threadIdx.x; g < n / 8; g += blockDim.x) {
+        const u32x4 a = *(const u32x4*)(s_nat + g * 8), b = *(const u32x4*)(s_nat + g * 8 + 4);
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = __uint_as_float(a[k]) * scale;
+            v[4 + k] = __uint_as_float(b[k]) * scale;
+        }
+        x_store_group(s_split, g, v);
+    }
+}
+
+// 8-term dot product of one centroid (fp16 or bf16, 16 bytes) with group g
+// of the split activation in LDS, fp32.
+template <int CBT>
+__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, uint32_t g)
+{
+    const float* p = s_x + 4 * g;
+    const u32x4 x0 = *(const u32x4*)p, x1 = *(const u32x4*)(p + SG_XB);
     float xv[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -70,14 +126,17 @@ __device__ __forceinline__ float centroid_dot(const u32x4 c, const float* x)
 // One wave's pass over iterations [s0, s1) of a chunk (stride SG_WAVES,
 // starting at s0 + wave), stage-2 entries from c_mid on.  load_entries()
 // issues the first three iterations' entry words and gathers() the first
-// two's centroid gathers (clamped in-bounds addresses when the wave has
-// fewer), so a caller can put a prologue between them, or before both.
-// run() keeps entry words three iterations ahead and gathers two ahead of
-// the arithmetic (about 8K codes in flight per CU at 16 waves; loads
+// GD iterations' centroid gathers (clamped in-bounds addresses when the wave
+// has fewer), so a caller can put a prologue between them, or before both.
+// run() keeps entry words three iterations ahead and gathers GD ahead of
+// the arithmetic (GD 2: about 8K codes in flight per CU at 16 waves, 64
+// VGPRs of entry words and centroids; GD 1 saves 16 of them, for kernels
+// held to 64 VGPRs that share the CU with a second workgroup).  Loads
 // complete in issue order and no branch separates them, so each wait covers
-// exactly the values it needs).
-template <int CBT>
+// exactly the values it needs.
+template <int CBT, int GD = 2>
 struct SortedPipe {
+    static_assert(GD == 1 || GD == 2, "gather depth 1 or 2");
     const u32x4* ent;
     const u32x4* cb0;
     const u32x4* cb1;
@@ -118,7 +177,7 @@ struct SortedPipe {
     __device__ __forceinline__ void gathers()
     {
         gather(clampit(it), e0, c0);
-        gather(clampit(it + SG_WAVES), e1, c1);
+        if constexpr (GD == 2) gather(clampit(it + SG_WAVES), e1, c1);
     }
     __device__ __forceinline__ void start(const u32x4* ent_, const void* cb0_, const void* cb1_, int c_beg_,
                                           int c_mid_, int s0, int s1_, int wave, int lane_)
@@ -134,14 +193,15 @@ struct SortedPipe {
         for (; it < s1; it += SG_WAVES) {
             const int i3 = clampit(it + 3 * SG_WAVES);
             const u32x4 e3 = load_e(i3);
-            u32x4 c2[4];
-            gather(i2, e2, c2);
+            u32x4 cn[4];  // the gathers GD iterations ahead
+            if constexpr (GD == 2) gather(i2, e2, cn);
+            else gather(clampit(it + SG_WAVES), e1, cn);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const uint32_t pos = e0[q] & 0xFFFFu;
                 const uint32_t r = min(pos >> gbits, (uint32_t)R);
                 const uint32_t g = min(pos & gmask, gmax);
-                const float d = centroid_dot<CBT>(c0[q], x + g * 8);
+                const float d = centroid_dot<CBT>(c0[q], x, g);
                 acc[r] += d;
             }
             e0 = e1;
@@ -150,8 +210,12 @@ struct SortedPipe {
             i2 = i3;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                c0[q] = c1[q];
-                c1[q] = c2[q];
+                if constexpr (GD == 2) {
+                    c0[q] = c1[q];
+                    c1[q] = cn[q];
+                } else {
+                    c0[q] = cn[q];
+                }
             }
         }
     }

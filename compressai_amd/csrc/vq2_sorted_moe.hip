@@ -41,8 +41,10 @@ struct SortedPoolArgs {
     int32_t ipc;        // iterations per chunk (every chunk padded to it)
     int s_dt;
     int32_t n_iters;
-    int R;     // rows per chunk
+    int R;     // rows per chunk at most (row R is the dummy row)
     int C;     // chunks per expert
+    int rb;    // chunk c: rows [c * rb + min(c, nbig), + rb + (c < nbig))
+    int nbig;
     int rows;  // rows per expert
     int ng;    // groups per row
     int gbits;
@@ -166,9 +168,10 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const SortedPoolArgs& pl = a.pool;
     const int64_t n = (int64_t)pl.ng * 8;
-    float* s_x = smem;              // n floats
-    float* s_stage = smem + n;      // n floats
-    float* s_acc = smem + 2 * n;    // SG_WAVES x SG_PARTS x (R + 1)
+    float* s_x = smem;                     // natural-order activation, n floats
+    float* s_stage = smem + n;             // n floats; once build_x is done, the split activation
+    float* s_split = smem + n;             // (SG_X_SPLIT floats) takes its place
+    float* s_acc = s_split + SG_X_SPLIT;   // SG_WAVES x SG_PARTS x (R + 1)
     const int R = pl.R;
     const int unit = (int)blockIdx.x / a.slices, slice = (int)blockIdx.x - unit * a.slices;
     const int p = unit / pl.C, chunk = unit - p * pl.C;
@@ -286,15 +289,15 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
         __syncthreads();
         build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
     }
-    for (int64_t i = threadIdx.x; i < n; i += SG_THREADS) s_x[i] *= a.g.xscale;
+    x_finalize(s_x, s_split, n, a.g.xscale);
     __syncthreads();
     pipe.gathers();
-    pipe.run(acc, s_x, pl.gbits, pl.ng, R);
+    pipe.run(acc, s_split, pl.gbits, pl.ng, R);
     __syncthreads();
 
     const int rr = threadIdx.x;
-    const int64_t row = (int64_t)chunk * R + rr;
-    const bool own = rr < R && row < pl.rows;
+    const int64_t row = (int64_t)chunk * pl.rb + min(chunk, pl.nbig) + rr;
+    const bool own = rr < pl.rb + (chunk < pl.nbig ? 1 : 0);
     // MODE 2: each slice's share of the combine, w[p] * (sum * s[e][row])
     float f = 1.0f;
     if constexpr (MODE == 2) f = own ? a.w[p] * load_as_f32(pl.scale, pl.s_dt, e * pl.rows + row) : 0.0f;
@@ -382,7 +385,8 @@ static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_exper
     if (pc.rows_per_chunk < 1 || pc.rows_per_chunk > r_lim)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: rows_per_chunk=%lld outside 1..%lld", name,
                          (long long)pc.rows_per_chunk, (long long)r_lim);
-    const int64_t C = (rows + pc.rows_per_chunk - 1) / pc.rows_per_chunk;
+    const ChunkSplit ks = chunk_split(rows, pc.rows_per_chunk);
+    const int64_t C = ks.n_chunks;
     if (pc.iters_per_chunk < 1 || n_experts * C * pc.iters_per_chunk != pc.n_iters || pc.n_iters > 0x7FFFFFFF)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: %lld iterations are not %lld experts x %lld chunks x "
                          "%lld", name, (long long)pc.n_iters, (long long)n_experts, (long long)C,
@@ -398,6 +402,8 @@ static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_exper
     pa.n_iters = (int32_t)pc.n_iters;
     pa.R = (int)pc.rows_per_chunk;
     pa.C = (int)C;
+    pa.rb = (int)ks.rb;
+    pa.nbig = (int)ks.nbig;
     pa.rows = (int)rows;
     pa.ng = (int)ng;
     pa.gbits = sorted_gbits(ng);
@@ -504,7 +510,7 @@ int sorted_moe_launch(const SortedMoeCall& c)
     const int64_t grid_gu = n_pairs * a.pool.C * c.slices_gu;
     const int64_t grid_dn = n_pairs * d.pool.C * c.slices_dn;
     if (grid_gu > 0x7FFFFFFF || grid_dn > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: grid too large");
-    size_t shm = (size_t)(2 * H + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
+    size_t shm = (size_t)(H + SG_X_SPLIT + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm);
     hipError_t err = router ? launch_moe_x<1>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st)
                             : launch_moe_x<0>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st);
@@ -530,7 +536,7 @@ int sorted_moe_launch(const SortedMoeCall& c)
     d.gu_scale = c.gate_up.scale;
     d.gu_s_dt = c.gate_up.scale_dt;
     d.w = w;
-    shm = (size_t)(2 * I + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
+    shm = (size_t)(I + SG_X_SPLIT + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm);
     err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st)
                                 : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st);

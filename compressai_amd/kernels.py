@@ -385,13 +385,11 @@ class SortedPlanes:
         h1 = None if i1 is None else i1.detach().to("cpu").contiguous()
         stages = 2 if h1 is not None else 1
         cap = self.n_chunks * stages * (-(-R * ng // 256) + 8)
-        chunk_it = torch.empty(self.n_chunks + 1, dtype=torch.int32)
-        chunk_it1 = torch.empty(self.n_chunks, dtype=torch.int32)
-        n_iters = ctypes.c_int64(0)
+        ipc, ipc1, n_iters = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
         for _ in range(2):
             entries = torch.empty(cap * 256, dtype=torch.int32)
             st = lib.vq2_sorted_pack(h0.data_ptr(), None if h1 is None else h1.data_ptr(), out_rows, ng, R,
-                                     entries.data_ptr(), cap, chunk_it.data_ptr(), chunk_it1.data_ptr(),
+                                     entries.data_ptr(), cap, ctypes.byref(ipc), ctypes.byref(ipc1),
                                      ctypes.byref(n_iters), int(threads))
             if st == _lib.ERR_ARG and n_iters.value > cap:
                 cap = n_iters.value
@@ -399,10 +397,10 @@ class SortedPlanes:
             _lib.check(st, "vq2_sorted_pack")
             break
         self.n_iters = int(n_iters.value)
+        # every chunk holds iters_per_chunk iterations, stage1_iters of stage 1
+        self.iters_per_chunk, self.stage1_iters = int(ipc.value), int(ipc1.value)
         # uint32 entries held in an int32 tensor (same bits)
         self.entries = entries[: self.n_iters * 256].to(dev)
-        self.chunk_it = chunk_it.to(dev)
-        self.chunk_it1 = chunk_it1.to(dev)
         self.device = dev
 
     def mat(self, scale, y=None) -> "_lib.SortedMat":
@@ -410,12 +408,11 @@ class SortedPlanes:
         if scale.numel() != self.out_rows:
             raise Vq2Error(f"scale has {scale.numel()} entries, expected {self.out_rows}")
         _dt(scale, "scale")
-        return _lib.SortedMat(self.entries.data_ptr(), self.chunk_it.data_ptr(), self.chunk_it1.data_ptr(),
-                              self.n_iters, self.rows_per_chunk, 1 if self.has_stage2 else 0, scale.data_ptr(), _p(y),
-                              self.out_rows)
+        return _lib.SortedMat(self.entries.data_ptr(), self.iters_per_chunk, self.stage1_iters, self.n_iters,
+                              self.rows_per_chunk, 1 if self.has_stage2 else 0, scale.data_ptr(), _p(y), self.out_rows)
 
     def nbytes(self):
-        return sum(t.numel() * t.element_size() for t in (self.entries, self.chunk_it, self.chunk_it1))
+        return self.entries.numel() * self.entries.element_size()
 
 
 _CU_COUNT: dict = {}

@@ -325,26 +325,31 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  * public format; this repack is built once at load time, on the host, and
  * lets the lanes of a wave share codebook lines: random 16-byte centroid
  * gathers are capped by the L2 request rate, sorted ones are not.
- *   rows are cut into chunks of rows_per_chunk rows (at most min(2^(16 -
- *   ceil(log2 ng)) - 1, 255); vq2_sorted_rows_per_chunk gives the default:
- *   the rows split evenly, over a multiple of chunk_align chunks when the
- *   chunks keep >= 128 rows, e.g. chunk_align = the CU count); every entry
+ *   rows are cut into n_chunks = ceil(out_rows / rows_per_chunk) chunks
+ *   (rows_per_chunk at most min(2^(16 - ceil(log2 ng)) - 1, 255);
+ *   vq2_sorted_rows_per_chunk gives the default: over a multiple of
+ *   chunk_align chunks when the chunks keep >= 128 rows, e.g. chunk_align =
+ *   the CU count) of near-equal height: chunk c holds rows
+ *   [c * rb + min(c, nbig), + rb + (c < nbig)), rb = out_rows / n_chunks,
+ *   nbig = out_rows % n_chunks; every entry
  *   is a uint32 (code << 16) | (row_in_chunk << ceil(log2 ng)) | group; a
  *   chunk's entries are sorted by code and dealt into 64-entry instructions
  *   in which no row repeats within a 32-lane half; 4 instructions form an
  *   iteration of 256 entries (lane l holds entry l of each, as one
- *   uint32x4).
+ *   uint32x4); every chunk's stage-1 and stage-2 entries are padded (dummy
+ *   row, code 0) to the matrix's largest stage-1 / stage-2 iteration
+ *   counts, so chunk c holds iterations [c * ipc, (c + 1) * ipc), its
+ *   stage-2 ones from c * ipc + stage1_iters on.
  * vq2_sorted_pack (host memory, no GPU work) fills `entries` (up to
- * cap_iters * 256 uint32, 16-byte aligned), chunk_it [n_chunks + 1]
- * (iteration offsets) and chunk_it1 [n_chunks] (stage-1 iterations, the
- * stage-2 ones follow) with n_chunks = ceil(out_rows / rows_per_chunk),
- * and sets *n_iters (also when the capacity is too small, which returns
- * VQ2_ERR_ARG).  idx1 (the (16,16) stage-2 plane) may be NULL; n_threads
+ * cap_iters * 256 uint32, 16-byte aligned) and sets *iters_per_chunk
+ * (ipc), *stage1_iters and *n_iters = n_chunks * ipc, n_chunks =
+ * ceil(out_rows / rows_per_chunk) (also when the capacity is too small,
+ * which returns VQ2_ERR_ARG).  idx1 (the (16,16) stage-2 plane) may be NULL; n_threads
  * <= 0: all host threads.  No reference counterpart (a load-time transform
  * of the planes PackedLinear holds, vq2/runtime.py:70-80). */
 int64_t vq2_sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
 int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
-                    uint32_t* entries, int64_t cap_iters, int32_t* chunk_it, int32_t* chunk_it1,
+                    uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
                     int64_t* n_iters, int n_threads);
 
 /* The workspace of vq2_sorted_gemv begins with VQ2_SORTED_WS_HEADER bytes
@@ -361,8 +366,8 @@ int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, 
 /* One packed matrix of a sorted launch (device pointers, except the struct). */
 typedef struct vq2_sorted_mat {
     const uint32_t* entries;  /* from vq2_sorted_pack, copied to the device    */
-    const int32_t* chunk_it;  /* [n_chunks + 1]                                */
-    const int32_t* chunk_it1; /* [n_chunks]                                    */
+    int64_t iters_per_chunk;  /* the values vq2_sorted_pack set                */
+    int64_t stage1_iters;
     int64_t n_iters;
     int64_t rows_per_chunk;   /* the value the matrix was packed with          */
     int has_stage2;           /* packed with idx1 (4 bpw): needs cb1          */

@@ -4,6 +4,8 @@ and group; no row repeats inside a 32-lane half of an instruction (each
 half read-add-writes its own accumulator array, so the kernel relies on
 it); padding is the dummy row; and the instructions are sorted enough that
 a wave's 64 gathers touch few codebook lines."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -23,12 +25,11 @@ def _is_pad(v, sp):
 def _decode(sp: SortedPlanes):
     """Per chunk and stage: list of instructions, each a (64,) uint32 array."""
     ent = sp.entries.cpu().numpy().view(np.uint32).reshape(-1, 64, 4)  # [iter][lane][q]
-    cit = sp.chunk_it.cpu().numpy()
-    cit1 = sp.chunk_it1.cpu().numpy()
+    ipc, ipc1 = sp.iters_per_chunk, sp.stage1_iters
     out = []
     for c in range(sp.n_chunks):
         stages = []
-        for a, b in ((cit[c], cit[c] + cit1[c]), (cit[c] + cit1[c], cit[c + 1])):
+        for a, b in ((c * ipc, c * ipc + ipc1), (c * ipc + ipc1, (c + 1) * ipc)):
             stages.append([ent[it][:, q] for it in range(a, b) for q in range(4)])
         out.append(stages)
     return out
@@ -45,11 +46,15 @@ def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
     assert sp.rows_per_chunk == R and (R + 1) * (1 << gb) <= 1 << 16
     assert sp.n_chunks == -(-rows // R) and R <= 255
     assert R * sp.n_chunks - rows < sp.n_chunks      # the rows split evenly over the chunks
-    cit = sp.chunk_it.cpu().numpy()
-    assert cit[0] == 0 and np.all(np.diff(cit) > 0) and cit[-1] == sp.n_iters
+    assert rows // sp.n_chunks + (1 if rows % sp.n_chunks else 0) <= R
+    assert sp.n_iters == sp.n_chunks * sp.iters_per_chunk                 # chunks padded to one size
+    assert 0 < sp.stage1_iters <= sp.iters_per_chunk
+    assert (sp.stage1_iters < sp.iters_per_chunk) == (bpw == 4)
     planes = [m["idx0"].numpy().view(np.uint16)] + ([m["idx1"].numpy().view(np.uint16)] if bpw == 4 else [])
     for c, stages in enumerate(_decode(sp)):
-        r0, r1 = c * R, min(rows, (c + 1) * R)
+        rb, nbig = rows // sp.n_chunks, rows % sp.n_chunks    # near-equal chunks: heights rb + 1 then rb
+        r0 = c * rb + min(c, nbig)
+        r1 = r0 + rb + (1 if c < nbig else 0)
         for st, instrs in enumerate(stages):
             if st >= len(planes):
                 assert not instrs
@@ -99,15 +104,14 @@ def test_sorted_pack_rejects_bad_input():
     with pytest.raises(Vq2Error):
         SortedPlanes(m["idx0"], None, 17, 512, device="cpu")      # wrong row count
     L = _lib.load()
-    n_it = __import__("ctypes").c_int64(0)
+    n_it, ipc, ipc1 = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
     buf = torch.empty(256, dtype=torch.int32)
-    cit = torch.empty(2, dtype=torch.int32)
-    cit1 = torch.empty(1, dtype=torch.int32)
-    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 16, buf.data_ptr(), 1, cit.data_ptr(), cit1.data_ptr(),
-                           __import__("ctypes").byref(n_it), 1)
+    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 16, buf.data_ptr(), 1, ctypes.byref(ipc),
+                           ctypes.byref(ipc1), ctypes.byref(n_it), 1)
     assert st == _lib.ERR_ARG and n_it.value > 1   # capacity too small: the needed size is reported
-    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 256, buf.data_ptr(), 1000, cit.data_ptr(),
-                           cit1.data_ptr(), __import__("ctypes").byref(n_it), 1)
+    assert n_it.value == ipc.value and ipc1.value == ipc.value
+    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 256, buf.data_ptr(), 1000, ctypes.byref(ipc),
+                           ctypes.byref(ipc1), ctypes.byref(n_it), 1)
     assert st == _lib.ERR_ARG                     # rows_per_chunk beyond the 16-bit position field
 
 
@@ -139,15 +143,14 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
     longest = 0
     for e in range(E):
         sp = SortedPlanes(idx[e], None, rows, n, device="cpu", chunk_align=1)
-        assert sp.rows_per_chunk == R
-        cit = sp.chunk_it.numpy()
+        assert sp.rows_per_chunk == R and sp.n_chunks == C
+        ipe = sp.iters_per_chunk   # this expert's chunks, padded to its own longest
         own = sp.entries.numpy().view(np.uint32)
+        longest = max(longest, ipe)
         for c in range(C):
-            a, b = cit[c] * 256, cit[c + 1] * 256
-            longest = max(longest, cit[c + 1] - cit[c])
             got = ent[(e * C + c) * ipc * 256:(e * C + c + 1) * ipc * 256]
-            assert np.array_equal(got[: b - a], own[a:b])
-            assert np.all(got[b - a:] == pad)
+            assert np.array_equal(got[: ipe * 256], own[c * ipe * 256:(c + 1) * ipe * 256])
+            assert np.all(got[ipe * 256:] == pad)
     assert ipc == longest
 
 
