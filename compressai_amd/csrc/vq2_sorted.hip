@@ -300,17 +300,17 @@ struct SortedArgs {
 // other instantiations run one workgroup per CU, where that bound only
 // costs spills (gate+up 19.1 -> 20.0 us).
 template <int CBT, int XM, int XT, int EP>
-__global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_sorted_kernel(const SortedArgs a)
+__global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_sorted_kernel(const SortedArgs a)
 {
     extern __shared__ __align__(16) float smem[];
     touch_kernargs(a);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t n = a.ng * 8;
-    // XM 1: [natural-order activation: n][stage (n), later the split
+    // XM 1 / 3: [natural-order activation: n][stage (n), later the split
     // activation (SG_X_SPLIT)][accumulators]; XM 0: [split][accumulators]
     float* s_nat = smem;
-    float* s_x = smem + (XM == 1 ? n : 0);              // split activation (SG_X_SPLIT floats)
+    float* s_x = smem + (XM != 0 ? n : 0);              // split activation (SG_X_SPLIT floats)
     float* s_acc = s_x + SG_X_SPLIT;                    // SG_WAVES x SG_PARTS x (R + 1)
     int si = 0;
 #pragma unroll
@@ -328,8 +328,10 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
 
     // prologue loads first (they return before the entries and gathers)
     XProLoad first;
+    Rht2kLoad first2k;
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (XM == 1) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, 0, 0, first);
+    if constexpr (XM == 3) rht2k_load<XT>(a.g, (int)(n / RHT2K), 0, first2k);
 
     // the wave's first entry words come from HBM while the prologue stages
     // and rotates the activation (which waits only for its own, earlier
@@ -337,7 +339,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
     // (a pre-rotated x is only copied: there the gathers go out at once)
     // the 64-VGPR instantiation (two workgroups per CU) gathers one
     // iteration ahead: the other workgroup hides the latency
-    SortedPipe<CBT, (XM == 1 && EP == 1) ? 1 : 2> pipe;
+    SortedPipe<CBT, (XM != 0 && EP == 1) ? 1 : 2> pipe;
     pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
     if constexpr (XM == 0) pipe.gathers();
 
@@ -348,6 +350,8 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
         stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
         build_x<1, XT>(a.g, s_nat, s_stage, 1, n, first);
         x_finalize(s_nat, s_x, n, a.g.xscale);
+    } else if constexpr (XM == 3) {
+        rht2k_build<XT>((int)(n / RHT2K), n, first2k, smem + n, s_nat, s_x, a.g.xscale);
     } else {
         for (int64_t g = threadIdx.x; g < a.ng; g += SG_THREADS) {
             float v[8];
@@ -357,7 +361,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM == 1 && EP == 1) ? 8 : 1) vq_s
         }
     }
     __syncthreads();
-    if constexpr (XM == 1) pipe.gathers();
+    if constexpr (XM != 0) pipe.gathers();
     pipe.run(acc, s_x, a.gbits, a.ng, R);
     __syncthreads();
 
@@ -422,6 +426,13 @@ static hipError_t launch_sorted(const SortedArgs& a, unsigned grid, size_t shm, 
 template <int CBT, int EP>
 static hipError_t launch_sorted_x(int xm, int x_dt, const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
+    if (xm == 3) {
+        switch (x_dt) {
+        case VQ2_DT_F16: return launch_sorted<CBT, 3, VQ2_DT_F16, EP>(a, grid, shm, st);
+        case VQ2_DT_BF16: return launch_sorted<CBT, 3, VQ2_DT_BF16, EP>(a, grid, shm, st);
+        default: return launch_sorted<CBT, 3, VQ2_DT_F32, EP>(a, grid, shm, st);
+        }
+    }
     if (xm == 1) {
         switch (x_dt) {
         case VQ2_DT_F16: return launch_sorted<CBT, 1, VQ2_DT_F16, EP>(a, grid, shm, st);
@@ -473,7 +484,7 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     if (top1 && (c.slices != 1 || c.nseg != 1))
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: one matrix, one slice");
     const int64_t n = c.ng * 8;
-    const size_t shm = (size_t)((c.xm == 1 ? n : 0) + SG_X_SPLIT + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
+    const size_t shm = (size_t)((c.xm != 0 ? n : 0) + SG_X_SPLIT + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
     if (n > 2 * SG_XB || shm > SG_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large (at most %d)", (long long)n, 2 * SG_XB);
     if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
@@ -486,6 +497,8 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
             return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: perm 16-byte, sign 8-byte aligned");
         if ((uintptr_t)c.x % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: x must be 16-byte aligned");
     }
+    // 2048-point blocks: the all-threads prologue (rht2k_build)
+    const int xm = (c.xm == 1 && c.hb == RHT2K && n % RHT2K == 0 && n <= (int64_t)RHT2K * RHT2K_MAXB) ? 3 : c.xm;
     SortedArgs a{};
     a.g.x = c.x;
     a.g.x_dt = c.x_dt;
@@ -567,13 +580,13 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {
-        err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
-                                    : launch_sorted_x<VQ2_DT_BF16, 1>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
+        err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(xm, c.x_dt, a, (unsigned)wg, shm, st)
+                                    : launch_sorted_x<VQ2_DT_BF16, 1>(xm, c.x_dt, a, (unsigned)wg, shm, st);
         if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
         return argmax_final_launch(a.cand, wg, 1, top1_idx, top1_val, c.stream);
     }
-    err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st)
-                                : launch_sorted_x<VQ2_DT_BF16, 0>(c.xm, c.x_dt, a, (unsigned)wg, shm, st);
+    err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(xm, c.x_dt, a, (unsigned)wg, shm, st)
+                                : launch_sorted_x<VQ2_DT_BF16, 0>(xm, c.x_dt, a, (unsigned)wg, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
     return VQ2_OK;
 }

@@ -93,6 +93,172 @@ __device__ __forceinline__ void x_finalize(const float* s_nat, float* s_split, i
     }
 }
 
+// ---- RHT of one activation row in 2048-point blocks, by all 1024 threads
+// (n = k * 2048, 1 <= k <= 4, hb = 2048): y = FWHT_2048(sign * x[perm]) per
+// block, times `scale`, into the split layout.  The prologue of the gather
+// kernels (stage_x / build_x: 8 consecutive values per thread) keeps only
+// n / 8 threads busy, a quarter of the workgroup at n = 2048, and runs
+// latency-bound on one wave per SIMD; here every thread holds, for each
+// block b, the two values b * 2048 + 2 t + j (j = 0, 1), so value bit 0 is
+// j, bits 1-6 the lane and bits 7-10 the wave, and four waves per SIMD
+// share the work:
+//   bit 0 in registers; bits 1-6 across lanes (DPP quad permutes for lane
+//   ^ 1 and ^ 2, row shifts for ^ 4, row rotate for ^ 8, ds_swizzle for
+//   ^ 16, ds_bpermute for ^ 32); bits 7-8 and 9-10 as two radix-4 passes
+//   through LDS, the second one scaling and storing the split layout.
+// The stages and their operands are those of the blockwise Walsh-Hadamard
+// transform (stages commute; rounding differs from other stage orders only
+// at fp32 accumulation level).  A permutation entry outside [0, n) poisons
+// its value with NaN, as the gather kernels' prologue does.
+constexpr int RHT2K = 2048;
+constexpr int RHT2K_MAXB = 4;
+
+struct Rht2kLoad {
+    u32x2 p[RHT2K_MAXB];     // the two permutation entries of each block
+    uint32_t s[RHT2K_MAXB];  // the two sign bytes (low 16 bits)
+    u32x2 x[RHT2K_MAXB];     // the two raw activation values (fp32: two words; fp16 / bf16: both in x[b][0])
+};
+
+// Loads of the thread's values, issued early (nothing waits for them here).
+template <int XT>
+__device__ __forceinline__ void rht2k_load(const GemvArgs& a, int k, int64_t xrow, Rht2kLoad& L)
+{
+    typedef const __attribute__((address_space(1))) u32x2* gp2;
+    typedef const __attribute__((address_space(1))) uint16_t* gp16;
+    typedef const __attribute__((address_space(1))) uint32_t* gp32;
+#pragma unroll
+    for (int b = 0; b < RHT2K_MAXB; b++) {
+        if (b < k) {
+            const int64_t e = (int64_t)b * RHT2K + 2 * threadIdx.x;
+            L.p[b] = *(gp2)(a.perm ? a.perm + e : g_perm_iota.v + e);
+            L.s[b] = *(gp16)(a.sign ? a.sign + e : g_sign_ones.v + e);
+            if constexpr (XT == VQ2_DT_F32) L.x[b] = *(gp2)((const float*)a.x + xrow + e);
+            else L.x[b][0] = *(gp32)((const uint16_t*)a.x + xrow + e);
+        }
+    }
+}
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float v, int lane)
+{
+    const int vi = __float_as_int(v);
+    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(vi, 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(vi, 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) {
+        const int up = __builtin_amdgcn_mov_dpp(vi, 0x104, 0xF, 0xF, true);  // row_shl:4 (lane + 4)
+        const int dn = __builtin_amdgcn_mov_dpp(vi, 0x114, 0xF, 0xF, true);  // row_shr:4 (lane - 4)
+        return __int_as_float((lane & 4) ? dn : up);
+    } else if constexpr (M == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(vi, 0x128, 0xF, 0xF, true));  // row_ror:8
+    else if constexpr (M == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(vi, 0x401F));  // lane ^ 16 within 32
+    else return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, vi));
+}
+
+template <int M>
+__device__ __forceinline__ void lane_stage(float& v0, float& v1, int lane)
+{
+    const float p0 = lane_xor<M>(v0, lane), p1 = lane_xor<M>(v1, lane);
+    const bool hi = (lane & M) != 0;
+    v0 = hi ? p0 - v0 : v0 + p0;
+    v1 = hi ? p1 - v1 : v1 + p1;
+}
+
+__device__ __forceinline__ void radix4(float (&v)[4])
+{
+    const float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];
+    v[0] = a + c;
+    v[1] = b + d;
+    v[2] = a - c;
+    v[3] = b - d;
+}
+
+// Part 1: the raw values into s_stage (n values, natural order); ends with
+// a barrier.
+template <int XT>
+__device__ __forceinline__ void rht2k_stage(int k, const Rht2kLoad& L, void* s_stage)
+{
+#pragma unroll
+    for (int b = 0; b < RHT2K_MAXB; b++) {
+        if (b < k) {
+            const int64_t e = (int64_t)b * RHT2K + 2 * threadIdx.x;
+            if constexpr (XT == VQ2_DT_F32) *(u32x2*)((float*)s_stage + e) = L.x[b];
+            else *(uint32_t*)((uint16_t*)s_stage + e) = L.x[b][0];
+        }
+    }
+    __syncthreads();
+}
+
+// Part 2, the transform: s_nat: n floats; s_split: the split layout (may
+// overlap s_stage, not s_nat).  A barrier must follow.
+template <int XT>
+__device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoad& L, const void* s_stage,
+                                                float* s_nat, float* s_split, float scale)
+{
+    const int t = threadIdx.x, lane = t & 63;
+    // permuted values, signs, bit 0, bits 1-6
+#pragma unroll
+    for (int b = 0; b < RHT2K_MAXB; b++) {
+        if (b < k) {
+            float v[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t pj = L.p[b][j];
+                const bool bad = pj >= (uint32_t)n;
+                const uint32_t src = bad ? 0u : pj;
+                float xv;
+                if constexpr (XT == VQ2_DT_F32) xv = ((const float*)s_stage)[src];
+                else if constexpr (XT == VQ2_DT_F16) xv = f16_bits_to_f32(((const uint16_t*)s_stage)[src]);
+                else xv = bf16_bits_to_f32(((const uint16_t*)s_stage)[src]);
+                const float sg = (float)(int8_t)((L.s[b] >> (8 * j)) & 0xFFu);
+                v[j] = bad ? __builtin_nanf("") : xv * sg;
+            }
+            float v0 = v[0] + v[1], v1 = v[0] - v[1];
+            lane_stage<1>(v0, v1, lane);
+            lane_stage<2>(v0, v1, lane);
+            lane_stage<4>(v0, v1, lane);
+            lane_stage<8>(v0, v1, lane);
+            lane_stage<16>(v0, v1, lane);
+            lane_stage<32>(v0, v1, lane);
+            u32x2 w;
+            w[0] = __float_as_uint(v0);
+            w[1] = __float_as_uint(v1);
+            *(u32x2*)(s_nat + (int64_t)b * RHT2K + 2 * t) = w;
+        }
+    }
+    __syncthreads();
+    // bits 7-8: values base + 128 i
+    for (int u = t; u < 512 * k; u += SG_THREADS) {
+        const int64_t base = (int64_t)(u >> 9) * RHT2K + ((u & 511) >> 7 << 9) + (u & 127);
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = s_nat[base + 128 * i];
+        radix4(v);
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_nat[base + 128 * i] = v[i];
+    }
+    __syncthreads();
+    // bits 9-10: values base + 512 i, scaled, into the split layout
+    for (int u = t; u < 512 * k; u += SG_THREADS) {
+        const int64_t base = (int64_t)(u >> 9) * RHT2K + (u & 511);
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = s_nat[base + 512 * i];
+        radix4(v);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t e = base + 512 * i;
+            s_split[((e >> 2) & 1) * SG_XB + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
+        }
+    }
+}
+
+template <int XT>
+__device__ __forceinline__ void rht2k_build(int k, int64_t n, const Rht2kLoad& L, void* s_stage, float* s_nat,
+                                            float* s_split, float scale)
+{
+    rht2k_stage<XT>(k, L, s_stage);
+    rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale);
+}
+
 // 8-term dot product of one centroid (fp16 or bf16, 16 bytes) with group g
 // of the split activation in LDS, fp32.
 template <int CBT>

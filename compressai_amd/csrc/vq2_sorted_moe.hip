@@ -156,7 +156,9 @@ constexpr int SG_MAX_TOPK = 64;
 // expert's first entry words; the activation is staged and rotated in LDS
 // while the entry words come from HBM; the first centroid gathers are issued
 // after the prologue (the entry words have arrived by then).
-template <int CBT, int MODE, int XT>
+// F2K (MODE 0 / 1): hidden = k * 2048 with 2048-point rotation blocks, the
+// all-threads prologue (rht2k_stage / rht2k_transform).
+template <int CBT, int MODE, int XT, int F2K>
 __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedMoeArgs a)
 {
     extern __shared__ __align__(16) float smem[];
@@ -179,9 +181,13 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
 
     // prologue loads first: the token's activation and the rotation tables
     // (MODE 0 / 1), or the tables alone (MODE 2)
+    constexpr bool FAST = F2K != 0 && MODE != 2;
     XProLoad first;
+    Rht2kLoad first2k;
+    const int k2k = (int)(n / RHT2K);
     const int64_t t0 = (int64_t)threadIdx.x * 8;
-    if constexpr (MODE != 2) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, t, 0, first);
+    if constexpr (FAST) rht2k_load<XT>(a.g, k2k, (int64_t)t * a.g.x_pstride, first2k);
+    else if constexpr (MODE != 2) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, t, 0, first);
     else xpro_tables(a.g, t0 < n ? t0 : 0, n, first);
 
     // chunk `chunk` of expert ex: iterations [(ex * C + chunk) * ipc, + ipc)
@@ -201,8 +207,12 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
         e = pair_expert(a, p, bad);
         entries(e);
         sorted_acc_zero(acc, lane, R);
-        stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
-        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+        if constexpr (FAST) {
+            rht2k_build<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale);
+        } else {
+            stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
+            build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+        }
     } else if constexpr (MODE == 1) {
         // the router in wave 0 (route_topk_keys); the shared expert's pairs
         // know their expert at once
@@ -238,12 +248,15 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
             }
         }
         sorted_acc_zero(acc, lane, R);
-        stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);  // ends with a barrier: s_top is visible
+        // the staging ends with a barrier: s_top is visible
+        if constexpr (FAST) rht2k_stage<XT>(k2k, first2k, s_stage);
+        else stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
         if (routed) {
             e = s_top[kslot];
             entries(e);
         }
-        build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
+        if constexpr (FAST) rht2k_transform<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale);
+        else build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
     } else {
         // the pair's gate_up rows: slices added in order, row scale, then
         // silu(gate) * up (elementwise, so taken before the permutation).
@@ -289,7 +302,7 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
         __syncthreads();
         build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
     }
-    x_finalize(s_x, s_split, n, a.g.xscale);
+    if constexpr (!FAST) x_finalize(s_x, s_split, n, a.g.xscale);
     __syncthreads();
     pipe.gathers();
     pipe.run(acc, s_split, pl.gbits, pl.ng, R);
@@ -342,35 +355,42 @@ __global__ void __launch_bounds__(256) vq_sorted_moe_combine_kernel(const Sorted
 }
 
 // ------------------------------------------------------------------ launch
-template <int CBT, int MODE, int XT>
+template <int CBT, int MODE, int XT, int F2K>
 static hipError_t launch_moe(const SortedMoeArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)vq_sorted_moe_kernel<CBT, MODE, XT>,
+        attr = hipFuncSetAttribute((const void*)vq_sorted_moe_kernel<CBT, MODE, XT, F2K>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, SG_MAX_SHM);
     });
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((vq_sorted_moe_kernel<CBT, MODE, XT>), dim3(grid), dim3(SG_THREADS), shm, st, a);
+    hipLaunchKernelGGL((vq_sorted_moe_kernel<CBT, MODE, XT, F2K>), dim3(grid), dim3(SG_THREADS), shm, st, a);
     return hipGetLastError();
 }
 
-template <int MODE, int XT>
+template <int MODE, int XT, int F2K>
 static hipError_t launch_moe_cb(int cb_dt, const SortedMoeArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
-    return cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, MODE, XT>(a, grid, shm, st)
-                               : launch_moe<VQ2_DT_BF16, MODE, XT>(a, grid, shm, st);
+    return cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, MODE, XT, F2K>(a, grid, shm, st)
+                               : launch_moe<VQ2_DT_BF16, MODE, XT, F2K>(a, grid, shm, st);
 }
 
 template <int MODE>
-static hipError_t launch_moe_x(int cb_dt, int x_dt, const SortedMoeArgs& a, unsigned grid, size_t shm,
+static hipError_t launch_moe_x(int cb_dt, int x_dt, bool f2k, const SortedMoeArgs& a, unsigned grid, size_t shm,
                                hipStream_t st)
 {
+    if (f2k) {
+        switch (x_dt) {
+        case VQ2_DT_F16: return launch_moe_cb<MODE, VQ2_DT_F16, 1>(cb_dt, a, grid, shm, st);
+        case VQ2_DT_BF16: return launch_moe_cb<MODE, VQ2_DT_BF16, 1>(cb_dt, a, grid, shm, st);
+        default: return launch_moe_cb<MODE, VQ2_DT_F32, 1>(cb_dt, a, grid, shm, st);
+        }
+    }
     switch (x_dt) {
-    case VQ2_DT_F16: return launch_moe_cb<MODE, VQ2_DT_F16>(cb_dt, a, grid, shm, st);
-    case VQ2_DT_BF16: return launch_moe_cb<MODE, VQ2_DT_BF16>(cb_dt, a, grid, shm, st);
-    default: return launch_moe_cb<MODE, VQ2_DT_F32>(cb_dt, a, grid, shm, st);
+    case VQ2_DT_F16: return launch_moe_cb<MODE, VQ2_DT_F16, 0>(cb_dt, a, grid, shm, st);
+    case VQ2_DT_BF16: return launch_moe_cb<MODE, VQ2_DT_BF16, 0>(cb_dt, a, grid, shm, st);
+    default: return launch_moe_cb<MODE, VQ2_DT_F32, 0>(cb_dt, a, grid, shm, st);
     }
 }
 
@@ -512,8 +532,10 @@ int sorted_moe_launch(const SortedMoeCall& c)
     if (grid_gu > 0x7FFFFFFF || grid_dn > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: grid too large");
     size_t shm = (size_t)(H + SG_X_SPLIT + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm);
-    hipError_t err = router ? launch_moe_x<1>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st)
-                            : launch_moe_x<0>(c.cb_dt, c.h_dt, a, (unsigned)grid_gu, shm, st);
+    // 2048-point blocks: the all-threads prologue
+    const bool f2k = c.rot_h.hb == RHT2K && H % RHT2K == 0 && H <= (int64_t)RHT2K * RHT2K_MAXB;
+    hipError_t err = router ? launch_moe_x<1>(c.cb_dt, c.h_dt, f2k, a, (unsigned)grid_gu, shm, st)
+                            : launch_moe_x<0>(c.cb_dt, c.h_dt, f2k, a, (unsigned)grid_gu, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe gate_up launch");
 
     // down: SwiGLU + RHT_I prologue from the gate_up slices
@@ -538,8 +560,8 @@ int sorted_moe_launch(const SortedMoeCall& c)
     d.w = w;
     shm = (size_t)(I + SG_X_SPLIT + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm);
-    err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st)
-                                : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32>(d, (unsigned)grid_dn, shm, st);
+    err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st)
+                                : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe down launch");
 
     // combine
