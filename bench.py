@@ -120,7 +120,7 @@ class DenseLayers:
                       ys=[self.y[nm] for nm in names])
 
     def sorted(self, lay, names, x, perm, sign):
-        """Sorted-layout launch (RHT built in LDS) + its slice reduce."""
+        """Sorted-layout launch: RHT built in LDS, slices summed in the launch."""
         from compressai_amd import kernels as K
 
         n = lay[names[0]][4]
@@ -233,7 +233,7 @@ def bench_dense(args, dev):
         f"{dl.bytes_per_step / (gather_us * 1e-6) / 1e9:.1f} GB/s")
 
     # dominant launch: gate + up (RHT + two 6144 x 2048 4 bpw matrices) on the
-    # sorted layout (the sorted kernel, then its slice reduce), back to back
+    # sorted layout (one launch, slices summed by the last workgroup), back to back
     # over the layer sets on the replay stream; also the gather-kernel launch
     dom_bytes = 2 * (INTER * (HIDDEN // 8) * 2 * 2 + INTER * 2)
     res = {}
@@ -635,8 +635,8 @@ def cpu_moe_baseline(moe, budget_s=10.0):
 
 
 def traffic_from_profiles():
-    """HBM bytes per call of the dominant launch pair (sorted gate+up kernel +
-    its slice reduce), from the committed rocprofv3 --pmc summary
+    """HBM bytes per call of the dominant launch (the sorted gate+up kernel),
+    from the committed rocprofv3 --pmc summary
     (profiles/sorted_gate_up_pmc.json), if present."""
     p = ROOT / "profiles" / "sorted_gate_up_pmc.json"
     try:
@@ -759,8 +759,8 @@ def main():
         "unpack_fixed": up,
         "paged_moe_t1": pgd,
         "roofline": {
-            "kernel": "vq_sorted_kernel (fused RHT) + vq_sorted_reduce_kernel, gate+up: 2 x 4 bpw (16,16) "
-                      "6144 x 2048, batch 1, one call = both kernels",
+            "kernel": "vq_sorted_kernel<1,3,1,0> (RHT 2048 in the prologue, slice sum in the launch), "
+                      "gate+up: 2 x 4 bpw (16,16) 6144 x 2048, batch 1, one call = one launch",
             "bound": "hbm",
             "achieved": round(d["dom_gbps"], 2),
             "peak": PEAK_HBM_GBPS,
@@ -768,7 +768,7 @@ def main():
             "frac": round(d["dom_gbps"] / PEAK_HBM_GBPS, 5),
             "traffic": traffic_from_profiles(),
             "traffic_source": "profiles/sorted_gate_up_pmc.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
-                              "bench.py --only dominant (both kernels), scaled by a 64 MiB copy (stored profile, "
+                              "bench.py --only dominant --layers 8, scaled by a 64 MiB copy (stored profile, "
                               "not this run)",
             "us_per_launch": round(d["dom_us"], 3),
             "algorithmic_bytes_per_launch": d["dom_bytes"],

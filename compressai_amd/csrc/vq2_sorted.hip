@@ -41,8 +41,9 @@
 // product in fp32 and acc[half][row] += dot.  At the end the waves'
 // accumulators are summed in (wave, half) order: with one slice the rows are complete
 // (y = (acc * s) * rs, or the fused top-1 key per workgroup); with several
-// slices the raw partials go to a workspace and vq_sorted_reduce_kernel sums
-// them in slice order.  Every order is fixed, so results are deterministic.
+// slices the raw partials go to a workspace and the last workgroup of the
+// chunk to arrive sums them in slice order.  Every order is fixed, so results
+// are deterministic.
 //
 // Semantics: vq_gemv_16 / the PackedLinear fallback (vq2/kernels.py:57-78,
 // vq2/runtime.py:82-110) for the (16,) and (16,16) configurations; the sums
