@@ -272,7 +272,8 @@ struct SortedSeg {
     int64_t out_rows;
     int32_t n_iters;
     int32_t n_chunks;
-    int32_t wg_start;
+    int32_t chunk_start;  // the matrix's first chunk in the launch's chunk numbering
+    int32_t sq, sr;       // slice j of a chunk: sq + (j < sr) iterations, from j * sq + min(j, sr)
     int32_t R;     // rows per chunk at most (row R is the dummy row)
     int32_t rb;    // chunk c: rows [c * rb + min(c, nbig), + rb + (c < nbig))
     int32_t nbig;
@@ -289,6 +290,7 @@ struct SortedArgs {
     int slices;
     float rs;
     int nseg;
+    int nc;          // chunks over all matrices
     SortedSeg seg[SG_MAX_SEG];
     uint64_t* cand;  // EP 1: best top-1 key per workgroup
 };
@@ -313,26 +315,31 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     float* s_nat = smem;
     float* s_x = smem + (XM != 0 ? n : 0);              // split activation (SG_X_SPLIT floats)
     float* s_acc = s_x + SG_X_SPLIT;                    // SG_WAVES x SG_PARTS x (R + 1)
-    int si = 0;
-#pragma unroll
-    for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && (int)blockIdx.x >= a.seg[s].wg_start) ? 1 : 0;
-    const SortedSeg& sg = a.seg[si];
-    const int R = sg.R;
-    const int local = (int)blockIdx.x - sg.wg_start;
-    const int chunk = local / a.slices, slice = local - chunk * a.slices;
-    // chunk < n_chunks and n_iters = n_chunks * ipc (checked on the host)
-    const int c_beg = chunk * sg.ipc;
-    const int c_mid = c_beg + sg.ipc1;
-    const int nit = sg.ipc;
-    const int s0 = c_beg + (int)((int64_t)nit * slice / a.slices);
-    const int s1 = c_beg + (int)((int64_t)nit * (slice + 1) / a.slices);
-
-    // prologue loads first (they return before the entries and gathers)
+    // prologue loads first (they need only the activation fields, and
+    // return before the entries and gathers)
     XProLoad first;
     Rht2kLoad first2k;
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (XM == 1) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, 0, 0, first);
     if constexpr (XM == 3) rht2k_load<XT>(a.g, (int)(n / RHT2K), 0, first2k);
+
+    // workgroup b: slice b / nc of chunk b % nc (over all matrices); the
+    // slice bounds come from the host (no divisions ahead of the entry
+    // loads: with them and the prologue loads issued after the segment
+    // lookup, gate+up took 16.8 us, 15.9 us without)
+    const int pos = (int)blockIdx.x;
+    const int slice = pos / a.nc, gchunk = pos - slice * a.nc;
+    int si = 0;
+#pragma unroll
+    for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && gchunk >= a.seg[s].chunk_start) ? 1 : 0;
+    const SortedSeg& sg = a.seg[si];
+    const int R = sg.R;
+    const int chunk = gchunk - sg.chunk_start;
+    // chunk < n_chunks and n_iters = n_chunks * ipc (checked on the host)
+    const int c_beg = chunk * sg.ipc;
+    const int c_mid = c_beg + sg.ipc1;
+    const int s0 = c_beg + slice * sg.sq + min(slice, sg.sr);
+    const int s1 = s0 + sg.sq + (slice < sg.sr ? 1 : 0);
 
     // the wave's first entry words come from HBM while the prologue stages
     // and rotates the activation (which waits only for its own, earlier
@@ -538,7 +545,7 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
             return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: workspace of %zu bytes (16-byte aligned) needed, got %zu",
                              need, c.ws_bytes);
     }
-    int64_t wg = 0, n_cnt = 0;
+    int64_t wg = 0, n_cnt = 0, nc = 0;
     for (int s = 0; s < c.nseg; s++) {
         const SortedSegCall& sc = c.seg[s];
         const int64_t R = sc.rows_per_chunk;
@@ -561,7 +568,9 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         a.seg[s].out_rows = sc.out_rows;
         a.seg[s].n_iters = (int32_t)sc.n_iters;
         a.seg[s].n_chunks = (int32_t)n_chunks;
-        a.seg[s].wg_start = (int32_t)wg;
+        a.seg[s].chunk_start = (int32_t)nc;
+        a.seg[s].sq = (int32_t)(sc.iters_per_chunk / c.slices);
+        a.seg[s].sr = (int32_t)(sc.iters_per_chunk % c.slices);
         a.seg[s].R = (int32_t)R;
         a.seg[s].rb = (int32_t)ks.rb;
         a.seg[s].nbig = (int32_t)ks.nbig;
@@ -572,12 +581,14 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
             n_cnt += n_chunks;
         }
         wg += n_chunks * c.slices;
+        nc += n_chunks;
     }
     if (n_cnt > VQ2_SORTED_MAX_COUNTERS)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: %lld chunks with several slices (at most %d)",
                          (long long)n_cnt, VQ2_SORTED_MAX_COUNTERS);
     if (wg == 0) return VQ2_OK;
     if (wg > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: grid too large");
+    a.nc = (int)nc;
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {

@@ -61,6 +61,9 @@ struct SortedMoeArgs {
     int P;        // pairs per token
     int n_pairs;  // tokens * P
     int slices;
+    int sq, sr;   // slice j of a chunk: sq + (j < sr) iterations, from j * sq + min(j, sr)
+    int xmap;     // 1: XCD-ordered units (several slices, one round of workgroups)
+    int xq, xr;   // workgroups / 8, workgroups % 8
     const void* ids;  // MODE 0 / 2 and the combine: pair experts
     int ids_i64;
     float* part;  // gate_up: [slices][n_pairs][pool.rows] raw row sums; down: [n_pairs][slices][pool.rows] shares
@@ -156,8 +159,11 @@ constexpr int SG_MAX_TOPK = 64;
 // expert's first entry words; the activation is staged and rotated in LDS
 // while the entry words come from HBM; the first centroid gathers are issued
 // after the prologue (the entry words have arrived by then).
-// F2K (MODE 0 / 1): hidden = k * 2048 with 2048-point rotation blocks, the
-// all-threads prologue (rht2k_stage / rht2k_transform).
+// F2K (MODE 0 / 1): hidden = 2048 rotated as one 2048-point block, the
+// all-threads prologue (rht2k_stage / rht2k_transform).  The block count is
+// a constant there, so no load of the prologue sits behind a branch and the
+// compiler's load counts stay exact across the router's branches (with a
+// runtime block count the transform waited for the first entry words).
 template <int CBT, int MODE, int XT, int F2K>
 __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedMoeArgs a)
 {
@@ -175,7 +181,18 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     float* s_split = smem + n;             // (SG_X_SPLIT floats) takes its place
     float* s_acc = s_split + SG_X_SPLIT;   // SG_WAVES x SG_PARTS x (R + 1)
     const int R = pl.R;
-    const int unit = (int)blockIdx.x / a.slices, slice = (int)blockIdx.x - unit * a.slices;
+    // Workgroup b runs on XCD b % 8; with xmap each XCD takes a contiguous
+    // run of the (slice, pair, chunk) units in slice-major order.  A slice is
+    // a contiguous code range of every chunk (all experts share the
+    // codebook), so an XCD's L2 holds one or two slices' share of it.  The
+    // host sets xmap when there are several slices and the grid fits one
+    // round of workgroups (measured: T = 1 layer 27.8 -> 25.4-25.9 us; with
+    // two slices over 2.8 rounds, T = 8, the plain order was faster; the
+    // dense sorted GEMV gained nothing from it).
+    const int xcd = (int)blockIdx.x & 7;
+    const int pos = a.xmap ? xcd * a.xq + min(xcd, a.xr) + ((int)blockIdx.x >> 3) : (int)blockIdx.x;
+    const int units = a.n_pairs * pl.C;
+    const int slice = pos / units, unit = pos - slice * units;
     const int p = unit / pl.C, chunk = unit - p * pl.C;
     const int t = p / a.P, kslot = p - t * a.P;
 
@@ -184,7 +201,7 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     constexpr bool FAST = F2K != 0 && MODE != 2;
     XProLoad first;
     Rht2kLoad first2k;
-    const int k2k = (int)(n / RHT2K);
+    constexpr int k2k = 1;
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (FAST) rht2k_load<XT>(a.g, k2k, (int64_t)t * a.g.x_pstride, first2k);
     else if constexpr (MODE != 2) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, t, 0, first);
@@ -195,8 +212,8 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     SortedPipe<CBT> pipe;
     auto entries = [&](int64_t ex) {
         const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
-        const int s0 = c_beg + (int)((int64_t)pl.ipc * slice / a.slices);
-        const int s1 = c_beg + (int)((int64_t)pl.ipc * (slice + 1) / a.slices);
+        const int s0 = c_beg + slice * a.sq + min(slice, a.sr);
+        const int s1 = s0 + a.sq + (slice < a.sr ? 1 : 0);
         pipe.load_entries(pl.ent, a.cb, nullptr, c_beg, c_beg + pl.ipc, s0, s1, wave, lane);
     };
     float* acc = sorted_acc(s_acc, wave, lane, R);
@@ -530,10 +547,15 @@ int sorted_moe_launch(const SortedMoeCall& c)
     const int64_t grid_gu = n_pairs * a.pool.C * c.slices_gu;
     const int64_t grid_dn = n_pairs * d.pool.C * c.slices_dn;
     if (grid_gu > 0x7FFFFFFF || grid_dn > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: grid too large");
+    a.sq = a.pool.ipc / a.slices;
+    a.sr = a.pool.ipc % a.slices;
+    a.xmap = a.slices > 1 && grid_gu <= device_cu_count();
+    a.xq = (int)(grid_gu / 8);
+    a.xr = (int)(grid_gu % 8);
     size_t shm = (size_t)(H + SG_X_SPLIT + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm);
     // 2048-point blocks: the all-threads prologue
-    const bool f2k = c.rot_h.hb == RHT2K && H % RHT2K == 0 && H <= (int64_t)RHT2K * RHT2K_MAXB;
+    const bool f2k = c.rot_h.hb == RHT2K && H == RHT2K;
     hipError_t err = router ? launch_moe_x<1>(c.cb_dt, c.h_dt, f2k, a, (unsigned)grid_gu, shm, st)
                             : launch_moe_x<0>(c.cb_dt, c.h_dt, f2k, a, (unsigned)grid_gu, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe gate_up launch");
@@ -549,6 +571,11 @@ int sorted_moe_launch(const SortedMoeCall& c)
     d.P = c.P;
     d.n_pairs = (int)n_pairs;
     d.slices = c.slices_dn;
+    d.sq = d.pool.ipc / d.slices;
+    d.sr = d.pool.ipc % d.slices;
+    d.xmap = d.slices > 1 && grid_dn <= device_cu_count();
+    d.xq = (int)(grid_dn / 8);
+    d.xr = (int)(grid_dn % 8);
     d.ids = ids;
     d.ids_i64 = ids_i64;
     d.part = dn_part;
