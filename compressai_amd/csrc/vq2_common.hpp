@@ -38,6 +38,22 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i)
     return ((const float*)p)[i];
 }
 
+// Bits of element i of an array of runtime dtype dt (fp32: the word; fp16 /
+// bf16: the half in the low bits); raw_as_f32 converts them.  Kept apart so
+// that a load can be issued early and waited for at its first use (a
+// conversion inside the dtype branch makes the wait come at once).
+__device__ __forceinline__ uint32_t load_raw(const void* p, int dt, int64_t i)
+{
+    return dt == VQ2_DT_F32 ? ((const uint32_t*)p)[i] : (uint32_t)((const uint16_t*)p)[i];
+}
+
+__device__ __forceinline__ float raw_as_f32(uint32_t r, int dt)
+{
+    if (dt == VQ2_DT_F16) return f16_bits_to_f32((uint16_t)r);
+    if (dt == VQ2_DT_BF16) return bf16_bits_to_f32(r);
+    return __uint_as_float(r);
+}
+
 // Store fp32 v into element i of an array of runtime dtype dt.
 __device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v)
 {

@@ -259,6 +259,69 @@ __device__ __forceinline__ void rht2k_build(int k, int64_t n, const Rht2kLoad& L
     rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale);
 }
 
+// One 512-point block by the same all-threads scheme (the MoE down
+// projection's rotation): thread t < 256 holds the permuted, signed values
+// 2 t + j read through `val` (natural order, index < 512), bit 0 in
+// registers, bits 1-6 across lanes, bits 7-8 as one radix-4 pass through
+// LDS (s_nat: 512 floats that `val` does not read) that scales and stores
+// the split layout.  A barrier must follow.
+struct RhtPairLoad {
+    u32x2 p;     // permutation entries 2 t, 2 t + 1
+    uint32_t s;  // their two sign bytes (low 16 bits)
+};
+
+constexpr int RHT512 = 512;
+
+__device__ __forceinline__ void rht512_load(const GemvArgs& a, RhtPairLoad& L)
+{
+    typedef const __attribute__((address_space(1))) u32x2* gp2;
+    typedef const __attribute__((address_space(1))) uint16_t* gp16;
+    const int64_t e = 2 * (int64_t)(threadIdx.x < RHT512 / 2 ? threadIdx.x : 0);
+    L.p = *(gp2)(a.perm ? a.perm + e : g_perm_iota.v + e);
+    L.s = *(gp16)(a.sign ? a.sign + e : g_sign_ones.v + e);
+}
+
+template <typename F>
+__device__ __forceinline__ void rht512_transform(const RhtPairLoad& L, F val, float* s_nat, float* s_split, float scale)
+{
+    const int t = threadIdx.x, lane = t & 63;
+    if (t < RHT512 / 2) {
+        float v[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t pj = L.p[j];
+            const bool bad = pj >= (uint32_t)RHT512;
+            const float sg = (float)(int8_t)((L.s >> (8 * j)) & 0xFFu);
+            const float xv = val(bad ? 0u : pj);
+            v[j] = bad ? __builtin_nanf("") : xv * sg;
+        }
+        float v0 = v[0] + v[1], v1 = v[0] - v[1];
+        lane_stage<1>(v0, v1, lane);
+        lane_stage<2>(v0, v1, lane);
+        lane_stage<4>(v0, v1, lane);
+        lane_stage<8>(v0, v1, lane);
+        lane_stage<16>(v0, v1, lane);
+        lane_stage<32>(v0, v1, lane);
+        u32x2 w;
+        w[0] = __float_as_uint(v0);
+        w[1] = __float_as_uint(v1);
+        *(u32x2*)(s_nat + 2 * t) = w;
+    }
+    __syncthreads();
+    // bits 7-8: values t + 128 i, scaled, into the split layout
+    if (t < 128) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = s_nat[t + 128 * i];
+        radix4(v);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = t + 128 * i;
+            s_split[((e >> 2) & 1) * SG_XB + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
+        }
+    }
+}
+
 // 8-term dot product of one centroid (fp16 or bf16, 16 bytes) with group g
 // of the split activation in LDS, fp32.
 template <int CBT>

@@ -79,9 +79,13 @@ struct SortedMoeArgs {
     int out_dt;
 };
 
+// The pair's expert id by a scalar load (p is wave-uniform): waiting for it
+// does not wait for the vector loads issued before it.  In the down launch
+// the ids come from the gate_up launch before it (the scalar cache starts
+// every launch empty).
 __device__ __forceinline__ int64_t pair_expert(const SortedMoeArgs& a, int p, bool& bad)
 {
-    const int64_t e = a.ids_i64 ? ((const int64_t*)a.ids)[p] : (int64_t)((const int32_t*)a.ids)[p];
+    const int64_t e = a.ids_i64 ? uniform_load<int64_t>(a.ids, p) : (int64_t)uniform_load<int32_t>(a.ids, p);
     bad = e < 0 || e >= a.n_experts;
     return bad ? 0 : e;
 }
@@ -198,13 +202,17 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
 
     // prologue loads first: the token's activation and the rotation tables
     // (MODE 0 / 1), or the tables alone (MODE 2)
+    // F2K: the all-threads rotation (MODE 0 / 1: one 2048-point block of h;
+    // MODE 2: one 512-point block), which stores the split layout itself
     constexpr bool FAST = F2K != 0 && MODE != 2;
     XProLoad first;
     Rht2kLoad first2k;
+    RhtPairLoad first512;
     constexpr int k2k = 1;
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (FAST) rht2k_load<XT>(a.g, k2k, (int64_t)t * a.g.x_pstride, first2k);
     else if constexpr (MODE != 2) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, t, 0, first);
+    else if constexpr (F2K != 0) rht512_load(a.g, first512);
     else xpro_tables(a.g, t0 < n ? t0 : 0, n, first);
 
     // chunk `chunk` of expert ex: iterations [(ex * C + chunk) * ipc, + ipc)
@@ -219,6 +227,8 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     float* acc = sorted_acc(s_acc, wave, lane, R);
     bool bad = false;
     int64_t e = 0;
+    float wp = 1.0f;    // MODE 2: the pair's combine weight
+    uint32_t dsc = 0u;  // MODE 2: raw bits of the row's down scale
 
     if constexpr (MODE == 0) {
         e = pair_expert(a, p, bad);
@@ -305,21 +315,35 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
         slice_loads(i0, 0, pv0);  // needs only the pair, not its expert
         asm volatile("" ::: "memory");
         e = pair_expert(a, p, bad);
-        const float sc0 = load_as_f32(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i0);
+        const uint32_t sc0 = load_raw(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i0);
+        // the epilogue's combine weight and row scale, fetched now; both
+        // scale loads sit in dtype branches, ahead of the entry words so
+        // that the waits for them stay exact
+        wp = uniform_load<float>(a.w, p);
+        const bool own_e = (int)threadIdx.x < pl.rb + (chunk < pl.nbig ? 1 : 0);
+        const int64_t row_e = (int64_t)chunk * pl.rb + min(chunk, pl.nbig) + (own_e ? threadIdx.x : 0);
+        dsc = load_raw(pl.scale, pl.s_dt, e * pl.rows + row_e);
         entries(e);
         sorted_acc_zero(acc, lane, R);
-        if (threadIdx.x < 2 * n) finish(threadIdx.x, pv0, sc0);
+        if (threadIdx.x < 2 * n) finish(threadIdx.x, pv0, raw_as_f32(sc0, a.gu_s_dt));
         for (int64_t i = threadIdx.x + SG_THREADS; i < 2 * n; i += SG_THREADS) {
             float pv[8];
             slice_loads(i, 0, pv);
             finish(i, pv, load_as_f32(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i));
         }
         __syncthreads();
-        for (int64_t j = threadIdx.x; j < n; j += SG_THREADS) s_stage[j] = silu_f32(s_x[j]) * s_stage[j];
-        __syncthreads();
-        build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
+        if constexpr (F2K != 0) {
+            // silu(gate) * up taken as the transform reads it; its natural-
+            // order scratch lies in the split buffer's unused middle
+            rht512_transform(first512, [&](uint32_t i) { return silu_f32(s_x[i]) * s_stage[i]; }, s_split + 2 * RHT512,
+                             s_split, a.g.xscale);
+        } else {
+            for (int64_t j = threadIdx.x; j < n; j += SG_THREADS) s_stage[j] = silu_f32(s_x[j]) * s_stage[j];
+            __syncthreads();
+            build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
+        }
     }
-    if constexpr (!FAST) x_finalize(s_x, s_split, n, a.g.xscale);
+    if constexpr (F2K == 0) x_finalize(s_x, s_split, n, a.g.xscale);
     __syncthreads();
     pipe.gathers();
     pipe.run(acc, s_split, pl.gbits, pl.ng, R);
@@ -330,7 +354,7 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
     const bool own = rr < pl.rb + (chunk < pl.nbig ? 1 : 0);
     // MODE 2: each slice's share of the combine, w[p] * (sum * s[e][row])
     float f = 1.0f;
-    if constexpr (MODE == 2) f = own ? a.w[p] * load_as_f32(pl.scale, pl.s_dt, e * pl.rows + row) : 0.0f;
+    if constexpr (MODE == 2) f = own ? wp * raw_as_f32(dsc, pl.s_dt) : 0.0f;
     const float sum = sorted_row_sums(s_acc, R, s_red);
     if (own) {
         float v = sum;
@@ -587,8 +611,13 @@ int sorted_moe_launch(const SortedMoeCall& c)
     d.w = w;
     shm = (size_t)(I + SG_X_SPLIT + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
     if (shm > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm);
-    err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st)
-                                : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st);
+    // one 512-point rotation block: the all-threads prologue
+    if (c.rot_i.hb == RHT512 && I == RHT512)
+        err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32, 1>(d, (unsigned)grid_dn, shm, st)
+                                    : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32, 1>(d, (unsigned)grid_dn, shm, st);
+    else
+        err = c.cb_dt == VQ2_DT_F16 ? launch_moe<VQ2_DT_F16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st)
+                                    : launch_moe<VQ2_DT_BF16, 2, VQ2_DT_F32, 0>(d, (unsigned)grid_dn, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe down launch");
 
     // combine

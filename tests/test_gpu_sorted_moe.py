@@ -126,6 +126,32 @@ def test_sorted_moe_fresh_inputs_back_to_back(dev, T, slices):
         assert O.max_rel_err(out.cpu().numpy(), ref.cpu().numpy()) < 1e-5, i
 
 
+@pytest.mark.parametrize("H,I", [(1024, 256), (4096, 1024)])
+def test_sorted_moe_other_widths_vs_oracle(dev, H, I):
+    """Widths other than the 2048 / 512 of the reference model take the
+    general prologues (one 2048-point block for h and one 512-point block for
+    the intermediate have prologues of their own): hidden 1024 (one 1024-point
+    block) and 4096 (two 2048-point blocks), intermediate 256 and 1024."""
+    from compressai_amd.moe import ResidentMoEExperts
+
+    E, T, P = 6, 2, 3
+    cb = synth.codebook(9950)
+    gu = synth.indices16(9951, (E, 2 * I, H // 8))
+    gus = synth.scales(9952, (E, 2 * I))
+    dn = synth.indices16(9953, (E, H, I // 8))
+    dns = synth.scales(9954, (E, H))
+    mod = ResidentMoEExperts.from_pools(gu.to(dev), gus.to(dev), dn.to(dev), dns.to(dev), cb.to(dev),
+                                        out_dtype=torch.float32)
+    assert mod.sorted_gu is not None
+    assert mod.rot_h.hb == min(2048, H) and mod.rot_i.hb == min(2048, I)
+    h = synth.activations(9955, (T, H), dtype=torch.float16)
+    ids = torch.tensor([[0, 5, 2], [4, 1, 3]], dtype=torch.int32)
+    w = torch.softmax(synth.activations(9956, (T, P)).float(), -1)
+    out = mod.experts(h.to(dev), ids.to(dev), w.to(dev))
+    ref = _oracle(mod, h, ids.numpy(), w.numpy(), cb, gu, gus, dn, dns)
+    assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
+
+
 def test_sorted_moe_bad_expert_id_gives_nan_token(dev):
     """An id outside the pool (E, or negative) makes its token's output NaN
     and leaves the other tokens exact."""
