@@ -354,36 +354,37 @@ __device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, u
 
 // One wave's pass over iterations [s0, s1) of a chunk (stride SG_WAVES,
 // starting at s0 + wave), stage-2 entries from c_mid on.  load_entries()
-// issues the first three iterations' entry words and gathers() the first
-// GD iterations' centroid gathers (clamped in-bounds addresses when the wave
-// has fewer), so a caller can put a prologue between them, or before both.
-// run() keeps entry words three iterations ahead and gathers GD ahead of
-// the arithmetic (GD 2: about 8K codes in flight per CU at 16 waves, 64
-// VGPRs of entry words and centroids; GD 1 saves 16 of them, for kernels
-// held to 64 VGPRs that share the CU with a second workgroup).  Loads
-// complete in issue order and no branch separates them, so each wait covers
-// exactly the values it needs.
+// issues the first three (GD 3: four) iterations' entry words and gathers()
+// the first GD iterations' centroid gathers (iterations at or past s1 are
+// clamped to the chunk's first, whose lines are cached), so a caller can put
+// a prologue between them, or before both.  run() keeps entry words that far
+// ahead and gathers GD ahead of the arithmetic until the last GD iterations,
+// which it finishes from the gathers already in flight (no loads past the
+// range).  Loads complete in issue order and no branch separates them, so
+// each wait covers exactly the values it needs.
 template <int CBT, int GD = 2>
 struct SortedPipe {
-    static_assert(GD == 1 || GD == 2, "gather depth 1 or 2");
+    static_assert(GD >= 1 && GD <= 3, "gather depth 1 to 3");
+    static constexpr int NE = GD + 1 > 3 ? GD + 1 : 3;  // entry words held: iterations it .. it + (NE - 1) W
     const u32x4* ent;
     const u32x4* cb0;
     const u32x4* cb1;
     int c_beg, c_mid, s1, lane;
-    int it, i2;
-    u32x4 e0, e1, e2;
-    u32x4 c0[4], c1[4];
+    int it;
+    int ie[NE];       // the (clamped) iterations of the entry words
+    u32x4 e[NE];
+    u32x4 c[GD][4];   // centroids of iterations it .. it + (GD - 1) W
 
     __device__ __forceinline__ int clampit(int i) const { return i < s1 ? i : c_beg; }
     __device__ __forceinline__ u32x4 load_e(int i) const
     {
         return __builtin_nontemporal_load(ent + (int64_t)i * 64 + lane);
     }
-    __device__ __forceinline__ void gather(int i, const u32x4& e, u32x4 (&c)[4]) const
+    __device__ __forceinline__ void gather(int i, const u32x4& ew, u32x4 (&cw)[4]) const
     {
         const u32x4* cb = i < c_mid ? cb0 : cb1;
 #pragma unroll
-        for (int q = 0; q < 4; q++) c[q] = cb[e[q] >> 16];
+        for (int q = 0; q < 4; q++) cw[q] = cb[ew[q] >> 16];
     }
     // a missing stage-2 codebook is never selected for a real entry; cb0
     // stands in so that no gather can use a null base
@@ -398,15 +399,16 @@ struct SortedPipe {
         s1 = s1_;
         lane = lane_;
         it = s0 + wave;
-        i2 = clampit(it + 2 * SG_WAVES);
-        e0 = load_e(clampit(it));
-        e1 = load_e(clampit(it + SG_WAVES));
-        e2 = load_e(i2);
+#pragma unroll
+        for (int d = 0; d < NE; d++) {
+            ie[d] = clampit(it + d * SG_WAVES);
+            e[d] = load_e(ie[d]);
+        }
     }
     __device__ __forceinline__ void gathers()
     {
-        gather(clampit(it), e0, c0);
-        if constexpr (GD == 2) gather(clampit(it + SG_WAVES), e1, c1);
+#pragma unroll
+        for (int d = 0; d < GD; d++) gather(ie[d], e[d], c[d]);
     }
     __device__ __forceinline__ void start(const u32x4* ent_, const void* cb0_, const void* cb1_, int c_beg_,
                                           int c_mid_, int s0, int s1_, int wave, int lane_)
@@ -414,38 +416,57 @@ struct SortedPipe {
         load_entries(ent_, cb0_, cb1_, c_beg_, c_mid_, s0, s1_, wave, lane_);
         gathers();
     }
+    __device__ __forceinline__ void shift(const u32x4& enew, int inew)
+    {
+#pragma unroll
+        for (int d = 0; d + 1 < NE; d++) {
+            e[d] = e[d + 1];
+            ie[d] = ie[d + 1];
+        }
+        e[NE - 1] = enew;
+        ie[NE - 1] = inew;
+    }
+    __device__ __forceinline__ void accumulate(float* acc, const float* x, uint32_t gbits, uint32_t gmax, uint32_t R)
+    {
+        const uint32_t gmask = (1u << gbits) - 1u;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t pos = e[0][q] & 0xFFFFu;
+            const uint32_t r = min(pos >> gbits, R);
+            const uint32_t g = min(pos & gmask, gmax);
+            acc[r] += centroid_dot<CBT>(c[0][q], x, g);
+        }
+    }
     // acc: this lane's accumulator array (R + 1 floats), x: the activation
     __device__ __forceinline__ void run(float* acc, const float* x, int gbits, int64_t ng, int R)
     {
-        const uint32_t gmask = (1u << gbits) - 1u;
         const uint32_t gmax = (uint32_t)(ng - 1);
-        for (; it < s1; it += SG_WAVES) {
-            const int i3 = clampit(it + 3 * SG_WAVES);
-            const u32x4 e3 = load_e(i3);
+        // iterations whose gathers GD ahead are real
+        for (; it + GD * SG_WAVES < s1; it += SG_WAVES) {
+            const int inew = clampit(it + NE * SG_WAVES);
+            const u32x4 enew = load_e(inew);
             u32x4 cn[4];  // the gathers GD iterations ahead
-            if constexpr (GD == 2) gather(i2, e2, cn);
-            else gather(clampit(it + SG_WAVES), e1, cn);
+            gather(ie[GD], e[GD], cn);
+            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R);
+            shift(enew, inew);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t pos = e0[q] & 0xFFFFu;
-                const uint32_t r = min(pos >> gbits, (uint32_t)R);
-                const uint32_t g = min(pos & gmask, gmax);
-                const float d = centroid_dot<CBT>(c0[q], x, g);
-                acc[r] += d;
-            }
-            e0 = e1;
-            e1 = e2;
-            e2 = e3;
-            i2 = i3;
+            for (int d = 0; d + 1 < GD; d++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                if constexpr (GD == 2) {
-                    c0[q] = c1[q];
-                    c1[q] = cn[q];
-                } else {
-                    c0[q] = cn[q];
-                }
-            }
+                for (int q = 0; q < 4; q++) c[d][q] = c[d + 1][q];
+#pragma unroll
+            for (int q = 0; q < 4; q++) c[GD - 1][q] = cn[q];
+        }
+        // the last (at most GD) iterations: their gathers are in flight
+#pragma unroll
+        for (int k = 0; k < GD; k++) {
+            if (it >= s1) break;
+            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R);
+            shift(e[NE - 1], ie[NE - 1]);
+#pragma unroll
+            for (int d = 0; d + 1 < GD; d++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) c[d][q] = c[d + 1][q];
+            it += SG_WAVES;
         }
     }
 };

@@ -217,7 +217,9 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
 
     // chunk `chunk` of expert ex: iterations [(ex * C + chunk) * ipc, + ipc)
     // (in the pool: ex < n_experts, chunk < C), this slice's share of them
-    SortedPipe<CBT> pipe;
+    // gathers two iterations ahead in gate_up, one in down (measured: T = 1
+    // layer 22.7 / 21.4 / 23.2 / 21.0 us for 1-1, 2-2, 1-2, 2-1)
+    SortedPipe<CBT, MODE == 2 ? 1 : 2> pipe;
     auto entries = [&](int64_t ex) {
         const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
         const int s0 = c_beg + slice * a.sq + min(slice, a.sr);
