@@ -345,10 +345,11 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     // and rotates the activation (which waits only for its own, earlier
     // loads); the first gathers go out after it
     // (a pre-rotated x is only copied: there the gathers go out at once)
-    // gathers one iteration ahead (measured, gate+up: 15.7 us against 15.7
-    // at two and 16.7 at three, dense step 49.1 / 49.3 / 51.3 us; the
-    // 64-VGPR fused-RHT top-1, two workgroups per CU, needs one); the
-    // pre-rotated top-1 gathers two ahead (69.6 against 72.5 us at one)
+    // gathers one iteration ahead (measured on the dense step: 49.1 us
+    // against 49.3 at two; three, before the pipeline's tail stopped loading
+    // past the range, 51.3 against 50.2 at two); the 64-VGPR fused-RHT
+    // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
+    // two
     SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2> pipe;
     pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
     if constexpr (XM == 0) pipe.gathers();
