@@ -65,7 +65,8 @@ def rand_scale(n, g, dev):
 class DenseLayers:
     """L layer sets of the configs[1] projections (device-resident).  As
     PackedLinear does, the large matrices (gate, up, down: >= 2M codes) also
-    get the code-sorted layout, packed once here."""
+    get the code-sorted layout, packed once here, and so do q, k and v, which
+    PackedProjections runs in one launch (0.79 M codes together)."""
 
     PROJ = [  # name, out, n, bpw
         ("q", Q_OUT, HIDDEN, 2), ("k", KV_OUT, HIDDEN, 2), ("v", KV_OUT, HIDDEN, 2), ("o", HIDDEN, HIDDEN, 2),
@@ -76,7 +77,7 @@ class DenseLayers:
         import torch
 
         from compressai_amd import kernels as K, synth
-        from compressai_amd.runtime import SORTED_MIN_CODES
+        from compressai_amd.runtime import SORTED_MIN_CODES, SORTED_MIN_LAUNCH_CODES
 
         self.L, self.dev = L, dev
         g = torch.Generator(device=dev).manual_seed(2000)
@@ -84,13 +85,15 @@ class DenseLayers:
         self.cb1 = synth.codebook(2001).to(dev)
         self.layers = []
         t0 = time.perf_counter()
+        qkv_codes = sum(out * (n // 8) * (2 if bpw == 4 else 1) for name, out, n, bpw in self.PROJ[:3])
         for _ in range(L):
             lay = {}
             for name, out, n, bpw in self.PROJ:
                 i0 = rand_i16((out, n // 8), g, dev)
                 i1 = rand_i16((out, n // 8), g, dev) if bpw == 4 else None
                 sp = None
-                if out * (n // 8) * (2 if bpw == 4 else 1) >= SORTED_MIN_CODES:
+                codes = out * (n // 8) * (2 if bpw == 4 else 1)
+                if codes >= SORTED_MIN_CODES or (name in ("q", "k", "v") and qkv_codes >= SORTED_MIN_LAUNCH_CODES):
                     sp = K.SortedPlanes(i0, i1, out, n, device=dev)
                 lay[name] = (i0, i1, rand_scale(out, g, dev), out, n, sp)
             self.layers.append(lay)
@@ -129,11 +132,12 @@ class DenseLayers:
                          ys=[self.y[nm] for nm in names])
 
     def step(self, l):
-        """One decoder layer's projections, as PackedLinear runs them at batch
-        1: q/k/v and o on the gather kernel, gate/up and down on the sorted
-        layout; every launch rotates its activation in LDS."""
+        """One decoder layer's projections, as the runtime runs them at batch
+        1: q/k/v in one sorted-layout launch (PackedProjections), o on the
+        gather kernel, gate/up and down on the sorted layout (PackedLinear);
+        every launch rotates its activation in LDS."""
         lay = self.layers[l]
-        self.fused(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
+        self.sorted(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
         self.fused(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
         self.sorted(lay, ("gate", "up"), self.x_mlp, self.perm_h, self.sign_h)
         self.sorted(lay, ("down",), self.x_down, self.perm_i, self.sign_i)
@@ -734,8 +738,8 @@ def main():
         "config": {
             "workload": "configs[1]: dense decoder-layer projection set, batch 1, hidden 2048 (q,k,v,o 2 bpw; "
                         "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/"
-                        "scales/activations, fp32 out; q/k/v, o on the gather kernel, gate/up, down on the "
-                        "code-sorted layout (as PackedLinear at batch 1)",
+                        "scales/activations, fp32 out; q/k/v in one code-sorted launch (PackedProjections), o "
+                        "on the gather kernel, gate/up, down on the code-sorted layout (PackedLinear), batch 1",
             "layers_cycled": d["layers"],
             "bytes_per_step": d["bytes_per_step"],
             "graph_replay": True,

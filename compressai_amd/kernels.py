@@ -428,9 +428,13 @@ def sorted_slices(planes, dev) -> int:
     """Workgroups per chunk: as many as keep the launch within one workgroup
     per CU (the per-CU gather rate bounds this kernel, so a CU holding two
     workgroups of one launch finishes last; measured on the gate/up pair:
-    50 chunks x 5 slices 20.0 us, x 6 slices 31 us)."""
+    50 chunks x 5 slices 20.0 us, x 6 slices 31 us), and few enough that
+    each of a workgroup's 16 waves has at least one iteration (measured on
+    q, k, v of 2048-wide attention, 15 chunks of 171-228 iterations: 17
+    slices 10.6 us, 6-12 slices 9.3 us)."""
     chunks = sum(p.n_chunks for p in planes)
-    return max(1, min(32, _cu_count(dev) // chunks))
+    per_wave = min(p.iters_per_chunk for p in planes) // 20
+    return max(1, min(32, _cu_count(dev) // chunks, per_wave))
 
 
 def _sorted_cbs(planes, cb0, cb1):

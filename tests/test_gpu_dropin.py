@@ -184,3 +184,50 @@ def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
         idx, val = PackedLMHead(lin).argmax(x.to(dev))
         assert int(idx[0]) == int(np.argmax(y64[0]))
         assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.float16])
+def test_packed_projections_qkv(dev, act):
+    """q, k and v of a 2048-wide attention (tag "attn", one activation) in one
+    launch: the sorted layout at batch 1 (0.79 M codes together), the fused
+    gather kernel at batch 2, each projection at batch 3; every output matches
+    the projection's own PackedLinear forward and the oracle."""
+    from compressai_amd.runtime import PackedLinear, PackedProjections
+
+    n = 2048
+    cbs = {"16": synth.codebook(9390).to(dev)}
+    lins = []
+    mats = []
+    for k, out in enumerate((2048, 512, 512)):
+        m = synth.vq_matrix(9391 + k, out, n, bpw=2)
+        mats.append(m)
+        lins.append(PackedLinear((out, n), (16,), "attn", [m["idx0"]], m["scale"], cbs, dev))
+    assert all(lin.sorted is None for lin in lins)
+    proj = PackedProjections(lins)
+    assert proj.sorted is not None and len(proj.sorted) == 3
+    perm, sign = _rot_np(lins[0].rot)
+    for B in (1, 2, 3):
+        x = synth.activations(9395 + B, (B, n), dtype=act)
+        ys = proj(x.to(dev), out_dtype=torch.float32)
+        xr = O.rht(x.float(), perm, sign, 2048).astype(np.float32)
+        for lin, m, y in zip(lins, mats, ys):
+            assert y.shape == (B, lin.out) and y.dtype == torch.float32
+            own = lin(x.to(dev), out_dtype=torch.float32)
+            assert O.max_rel_err(y.cpu().numpy(), own.cpu().numpy()) < 1e-5
+            _, y64 = O.vq_gemv(xr, m["idx0"], None, cbs["16"].cpu(), None, lin.scale.cpu())
+            assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+
+
+def test_packed_projections_rejects_mixed(dev):
+    """Projections of other widths, tags or codebooks cannot share a launch."""
+    from compressai_amd.runtime import PackedLinear, PackedProjections
+
+    cbs = {"16": synth.codebook(9397).to(dev)}
+    other = {"16": synth.codebook(9398).to(dev)}
+    m = synth.vq_matrix(9399, 512, 2048, bpw=2)
+    a = PackedLinear((512, 2048), (16,), "attn", [m["idx0"]], m["scale"], cbs, dev)
+    b = PackedLinear((512, 2048), (16,), "mlp", [m["idx0"]], m["scale"], cbs, dev)
+    c = PackedLinear((512, 2048), (16,), "attn", [m["idx0"]], m["scale"], other, dev)
+    for bad in ([a, b], [a, c], [a] * 5):
+        with pytest.raises(K.Vq2Error):
+            PackedProjections(bad)
