@@ -153,13 +153,31 @@ __device__ __forceinline__ float lane_xor(float v, int lane)
     else return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, vi));
 }
 
+// One butterfly stage across lanes: v' = p + v on the lane whose bit M is
+// clear, p - v on its partner (p: the partner's value), written as
+// p + (v with its sign flipped on the upper lane) -- the same sums, and the
+// single-row DPP moves then fold into the adds (v_add_f32 with a DPP source).
 template <int M>
 __device__ __forceinline__ void lane_stage(float& v0, float& v1, int lane)
 {
-    const float p0 = lane_xor<M>(v0, lane), p1 = lane_xor<M>(v1, lane);
-    const bool hi = (lane & M) != 0;
-    v0 = hi ? p0 - v0 : v0 + p0;
-    v1 = hi ? p1 - v1 : v1 + p1;
+    const uint32_t flip = (uint32_t)(lane & M) << (31 - __builtin_ctz(M));
+    const float t0 = __uint_as_float(__float_as_uint(v0) ^ flip);
+    const float t1 = __uint_as_float(__float_as_uint(v1) ^ flip);
+    if constexpr (M == 4) {
+        // lane ^ 4 as two row shifts into one register: lane + 4 written
+        // into banks 0 and 2 of each row (lanes with bit 2 clear), lane - 4
+        // into banks 1 and 3
+        auto x4 = [](float v) {
+            const int vi = __float_as_int(v);
+            const int lo = __builtin_amdgcn_update_dpp(vi, vi, 0x104, 0xF, 0x5, false);  // row_shl:4
+            return __int_as_float(__builtin_amdgcn_update_dpp(lo, vi, 0x114, 0xF, 0xA, false));  // row_shr:4
+        };
+        v0 = x4(v0) + t0;
+        v1 = x4(v1) + t1;
+    } else {
+        v0 = lane_xor<M>(v0, lane) + t0;
+        v1 = lane_xor<M>(v1, lane) + t1;
+    }
 }
 
 __device__ __forceinline__ void radix4(float (&v)[4])
