@@ -666,7 +666,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for {max(args.gpus, world)}); the VQ2 decode "
-              "path is sharded by output rows / experts only by design, see DESIGN.md", file=sys.stderr)
+              "path would shard by output rows (dense) and by experts (MoE), which is designed, not built",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
