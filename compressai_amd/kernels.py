@@ -235,10 +235,10 @@ _WS_RETIRED: list = []
 
 
 def _workspace(dev: torch.device, nbytes: int, *, sorted_kind: bool = False) -> torch.Tensor | None:
-    """The workspace of this (device, stream).  vq_sorted_gemv gets one of
-    its own, allocated zeroed: it begins with arrival counters that must be
-    zero before a launch (each launch leaves them zero), which another
-    kernel's partials must never overwrite."""
+    """The workspace of this (device, stream).  vq_sorted_gemv and
+    vq_sorted_moe share one of their own, allocated zeroed: it begins with
+    arrival counters that must be zero before a launch (each call leaves them
+    zero), which another kernel's partials must never overwrite."""
     if nbytes == 0:
         return None
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream, sorted_kind)
@@ -639,7 +639,7 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
     else:
         sg, sd = (int(v) for v in slices)
     lib = _lib.load()
-    ws = _workspace(dev, int(lib.vq2_sorted_moe_workspace(T, P, H, I, sg, sd)))
+    ws = _workspace(dev, int(lib.vq2_sorted_moe_workspace(T, P, H, I, sg, sd)), sorted_kind=True)
     rh = _lib.RotTables(_p(rot_h[0]), _p(rot_h[1]), int(rot_h[2]), float(rot_h[3]))
     ri = _lib.RotTables(_p(rot_i[0]), _p(rot_i[1]), int(rot_i[2]), float(rot_i[3]))
     gp, dp = gate_up.pool(gu_scale), down.pool(dn_scale)

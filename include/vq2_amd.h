@@ -446,9 +446,15 @@ typedef struct vq2_rot_tables {
  * (ties to the lower id), renormalised; the last pair (pairs_per_token =
  * top_k + 1) is the shared expert shared_id with weight
  * sigmoid(shared_gate . h_t); the ids / weights go to ids_out / w_out.
- * Three launches (gate_up, down, combine), fp32 arithmetic, an id outside
+ * At most three launches (gate_up, down, combine), fp32 arithmetic, an id outside
  * the pool gives NaN for its token.  slices_gu / slices_dn workgroups share
- * each chunk; workspace: vq2_sorted_moe_workspace bytes.  Replaces the
+ * each chunk; workspace: vq2_sorted_moe_workspace bytes, whose first
+ * VQ2_SORTED_WS_HEADER bytes (per-pair counters) are zero before the first
+ * call; every call leaves them zero.  For hidden 2048 / inter 512 and at
+ * most 128 pairs (a 128-byte count each) the
+ * gate_up and down launches are one launch whose down workgroups wait
+ * (bounded) on the per-pair counts of finished gate_up workgroups; calls
+ * that share a workspace must not overlap.  Replaces the
  * per-token expert loop of PackedMoEExpertUniversal.forward
  * (vq2/load_and_test_full_35b.py:53-95) / PagedMoEExpert.forward
  * (vq2/paged_runtime.py:495-510), with the router, the transformers

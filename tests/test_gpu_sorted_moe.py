@@ -1,8 +1,8 @@
 """GPU parity of the MoE experts over code-sorted expert pools
 (vq2_sorted_moe through the C ABI: gate_up with the RHT built in, down with
 SwiGLU + RHT in its prologue, combine) against the fp64 oracle on the same
-seeded inputs: ids given (int32 / int64) and the router built in, T = 1..8,
-fp16 / bf16 codebooks and activations, 1 to 9 slices per chunk, NaN for an
+seeded inputs: ids given (int32 / int64) and the router built in, T = 1..8
+(gate_up and down in one launch) and T = 15 (135 pairs: two launches), fp16 / bf16 codebooks and activations, 1 to 9 slices per chunk, NaN for an
 expert id outside the pool, bit-identical repeats, and agreement with the
 gather kernels on the reference pools.
 
@@ -53,6 +53,7 @@ def _oracle(mod, h, ids, w, cb, gu, gus, dn, dns):
     (2, 8, torch.int64, torch.bfloat16),
     (3, 3, torch.int32, torch.float32),
     (8, 9, torch.int64, torch.float16),
+    (15, 9, torch.int32, torch.float32),
 ])
 def test_sorted_moe_experts_vs_oracle(dev, T, P, ids_dtype, h_dtype):
     E = 24
