@@ -343,7 +343,8 @@ def bench_lm_head(args, dev, batch=1, copies=14):
     (1.1 GiB).  Batch 1: the sorted layout with the RHT of the fp16
     activation built in the kernel (as PackedLMHead.argmax runs it), the
     same on a pre-rotated activation, and the gather kernel (pre-rotated);
-    batch 4: the matrix-core path (pre-rotated)."""
+    batch 4: the sorted batch kernel (pre-rotated, as PackedLMHead.argmax runs
+    it after the RHT) and the matrix-core path."""
     import torch
 
     from compressai_amd import kernels as K, synth
@@ -354,7 +355,7 @@ def bench_lm_head(args, dev, batch=1, copies=14):
     mats = []
     for _ in range(copies):
         i0, s = rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)
-        mats.append((i0, s, K.SortedPlanes(i0, None, out, n, device=dev) if batch == 1 else None))
+        mats.append((i0, s, K.SortedPlanes(i0, None, out, n, device=dev)))
     x = synth.activations(3004, (batch, n), dtype=torch.float32).to(dev)
     xh = synth.activations(3005, (batch, n), dtype=torch.float16).to(dev)
     perm, sign = synth.permutation(3006, n).to(dev), synth.signs(3007, n).to(dev)
@@ -382,6 +383,10 @@ def bench_lm_head(args, dev, batch=1, copies=14):
         _, s, sp = mats[l]
         res[l] = K.vq_sorted_gemv_argmax(xh, sp, s, cb, None, n, perm, sign, 2048)
 
+    def f_sorted_batch(l):
+        _, s, sp = mats[l]
+        res[l] = K.vq_sorted_gemm_batch_argmax(x, sp, s, cb, None, n)
+
     out_d = {}
     if batch == 1:
         us = run(f_sorted_rht)
@@ -390,7 +395,9 @@ def bench_lm_head(args, dev, batch=1, copies=14):
         log(f"lm head B=1 (sorted layout, pre-rotated x): {out_d['prerotated_us']:.2f} us/call")
         log(f"lm head B=1 (gather kernel, pre-rotated x): {out_d['gather_us']:.2f} us/call")
     else:
-        us = run(f_gather)
+        us = run(f_sorted_batch)
+        out_d["matrix_cores_us"] = run(f_gather)
+        log(f"lm head B={batch} (matrix cores, pre-rotated x): {out_d['matrix_cores_us']:.2f} us/call")
     gbps = nbytes / (us * 1e-6) / 1e9
     log(f"lm head B={batch}: {us:.2f} us/call, {gbps:.1f} GB/s")
     out_d.update(us=us, gbps=gbps)
@@ -753,6 +760,8 @@ def main():
         "lm_head_us_b1": None if lm1 is None else round(lm1["us"], 3),
         "lm_head_gbps_b1": None if lm1 is None else round(lm1["gbps"], 2),
         "lm_head_us_b4": None if lm4 is None else round(lm4["us"], 3),
+        "lm_head_gbps_b4": None if lm4 is None else round(lm4["gbps"], 2),
+        "lm_head_us_b4_matrix_cores": None if lm4 is None else round(lm4["matrix_cores_us"], 3),
         "lm_head_us_b1_prerotated": None if lm1 is None else round(lm1["prerotated_us"], 3),
         "lm_head_us_b1_gather_kernel": None if lm1 is None else round(lm1["gather_us"], 3),
         "dense_step_us_gather_kernel": round(d["gather_step_us"], 3),

@@ -70,6 +70,12 @@ SIGNATURES = {
     "vq2_sorted_gemv_argmax_workspace": ([_vp], ctypes.c_size_t),
     "vq2_sorted_gemv_argmax": ([_vp, _i32, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _i32, _i32, _i64, _f32, _vp,
                                 ctypes.c_size_t, _vp, _vp, _vp], _i32),
+    "vq2_sorted_gemm_batch_workspace": ([_vp, _i32, _i64, _i32], ctypes.c_size_t),
+    "vq2_sorted_gemm_batch": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _f32, _i32, _vp,
+                               ctypes.c_size_t, _vp], _i32),
+    "vq2_sorted_gemm_batch_argmax_workspace": ([_vp, _i64], ctypes.c_size_t),
+    "vq2_sorted_gemm_batch_argmax": ([_vp, _i32, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i64, _f32, _vp,
+                                      ctypes.c_size_t, _vp, _vp, _vp], _i32),
     "vq2_sorted_pack_pool": ([_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32], _i32),
     "vq2_sorted_moe_workspace": ([_i64, _i32, _i64, _i64, _i32, _i32], ctypes.c_size_t),
     "vq2_sorted_moe": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _vp, _vp,

@@ -736,6 +736,58 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
     return sorted_launch(c, out_idx, out_val);
 }
 
+size_t vq2_sorted_gemm_batch_workspace(const vq2_sorted_mat* mats, int n_mat, int64_t batch, int slices)
+{
+    if (!mats || n_mat < 1 || n_mat > 4 || slices <= 1 || batch < 1 || batch > 4) return 0;
+    SortedCall c{};
+    c.slices = slices;
+    c.nseg = n_mat;
+    c.batch = batch;
+    for (int i = 0; i < n_mat; i++) c.seg[i].out_rows = mats[i].out_rows;
+    return sorted_batch_workspace_bytes(c);
+}
+
+int vq2_sorted_gemm_batch(const void* x, int x_dt, int64_t batch, int64_t x_stride, int n_mat,
+                          const vq2_sorted_mat* mats, const void* cb0, const void* cb1, int cb_dt, int s_dt, int y_dt,
+                          int64_t n, float rs, int slices, void* workspace, size_t ws_bytes, void* stream)
+{
+    clear_error();
+    SortedCall c;
+    int r = sorted_call(c, "vq2_sorted_gemm_batch", x, x_dt, nullptr, nullptr, 0, 1.0f, n_mat, mats, cb0, cb1, cb_dt,
+                        s_dt, y_dt, n, rs, slices, stream);
+    if (r) return r;
+    for (int i = 0; i < n_mat; i++) CHECK(mats[i].y, "vq2_sorted_gemm_batch: matrix %d has no output", i);
+    c.batch = batch;
+    c.x_stride = x_stride;
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
+    return sorted_batch_launch(c, nullptr, nullptr);
+}
+
+size_t vq2_sorted_gemm_batch_argmax_workspace(const vq2_sorted_mat* mat, int64_t batch)
+{
+    if (!mat) return 0;
+    return sorted_batch_top1_workspace_bytes(mat->out_rows, mat->rows_per_chunk, batch);
+}
+
+int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                                 const vq2_sorted_mat* mat, const void* cb0, const void* cb1, int cb_dt, int s_dt,
+                                 int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
+                                 float* out_val, void* stream)
+{
+    clear_error();
+    SortedCall c;
+    int r = sorted_call(c, "vq2_sorted_gemm_batch_argmax", x, x_dt, nullptr, nullptr, 0, 1.0f, 1, mat, cb0, cb1,
+                        cb_dt, s_dt, VQ2_DT_F32, n, rs, 1, stream);
+    if (r) return r;
+    CHECK(out_idx && (uintptr_t)out_idx % 8 == 0, "vq2_sorted_gemm_batch_argmax: out_idx must be 8-byte aligned");
+    c.batch = batch;
+    c.x_stride = x_stride;
+    c.workspace = workspace;
+    c.ws_bytes = ws_bytes;
+    return sorted_batch_launch(c, out_idx, out_val);
+}
+
 int vq2_sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
                          uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
                          int n_threads)

@@ -153,9 +153,14 @@ struct SortedCall {
     void* workspace;
     size_t ws_bytes;
     void* stream;
+    int64_t batch = 1;     // activation rows (sorted_batch_launch: 1..4)
+    int64_t x_stride = 0;  // sorted_batch_launch: elements between activation rows
 };
 
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
+size_t sorted_batch_workspace_bytes(const SortedCall& c);
+size_t sorted_batch_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk, int64_t batch);
+int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);
 int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t rows_per_chunk,
                 uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
                 int64_t* n_iters, int n_threads);

@@ -370,7 +370,7 @@ __device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, u
     return d;
 }
 
-// One wave's pass over iterations [s0, s1) of a chunk (stride SG_WAVES,
+// One wave's pass over iterations [s0, s1) of a chunk (stride W, the waves of the workgroup,
 // starting at s0 + wave), stage-2 entries from c_mid on.  load_entries()
 // issues the first three (GD 3: four) iterations' entry words and gathers()
 // the first GD iterations' centroid gathers (iterations at or past s1 are
@@ -380,7 +380,7 @@ __device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, u
 // which it finishes from the gathers already in flight (no loads past the
 // range).  Loads complete in issue order and no branch separates them, so
 // each wait covers exactly the values it needs.
-template <int CBT, int GD = 2>
+template <int CBT, int GD = 2, int W = SG_WAVES>
 struct SortedPipe {
     static_assert(GD >= 1 && GD <= 3, "gather depth 1 to 3");
     static constexpr int NE = GD + 1 > 3 ? GD + 1 : 3;  // entry words held: iterations it .. it + (NE - 1) W
@@ -419,7 +419,7 @@ struct SortedPipe {
         it = s0 + wave;
 #pragma unroll
         for (int d = 0; d < NE; d++) {
-            ie[d] = clampit(it + d * SG_WAVES);
+            ie[d] = clampit(it + d * W);
             e[d] = load_e(ie[d]);
         }
     }
@@ -460,8 +460,8 @@ struct SortedPipe {
     {
         const uint32_t gmax = (uint32_t)(ng - 1);
         // iterations whose gathers GD ahead are real
-        for (; it + GD * SG_WAVES < s1; it += SG_WAVES) {
-            const int inew = clampit(it + NE * SG_WAVES);
+        for (; it + GD * W < s1; it += W) {
+            const int inew = clampit(it + NE * W);
             const u32x4 enew = load_e(inew);
             u32x4 cn[4];  // the gathers GD iterations ahead
             gather(ie[GD], e[GD], cn);
@@ -484,7 +484,38 @@ struct SortedPipe {
             for (int d = 0; d + 1 < GD; d++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) c[d][q] = c[d + 1][q];
-            it += SG_WAVES;
+            it += W;
+        }
+    }
+    // run() with the arithmetic of an iteration given by the caller:
+    // f(entry words, their four centroids)
+    template <class F>
+    __device__ __forceinline__ void run_each(F&& f)
+    {
+        for (; it + GD * W < s1; it += W) {
+            const int inew = clampit(it + NE * W);
+            const u32x4 enew = load_e(inew);
+            u32x4 cn[4];
+            gather(ie[GD], e[GD], cn);
+            f(e[0], c[0]);
+            shift(enew, inew);
+#pragma unroll
+            for (int d = 0; d + 1 < GD; d++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) c[d][q] = c[d + 1][q];
+#pragma unroll
+            for (int q = 0; q < 4; q++) c[GD - 1][q] = cn[q];
+        }
+#pragma unroll
+        for (int k = 0; k < GD; k++) {
+            if (it >= s1) break;
+            f(e[0], c[0]);
+            shift(e[NE - 1], ie[NE - 1]);
+#pragma unroll
+            for (int d = 0; d + 1 < GD; d++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) c[d][q] = c[d + 1][q];
+            it += W;
         }
     }
 };

@@ -520,6 +520,93 @@ def vq_sorted_gemv_argmax(x, planes, scale, cb0, cb1, n, perm=None, sign=None, h
     return idx, val
 
 
+SORTED_BATCH_MAX = 4
+
+
+def sorted_batch_slices(planes, dev) -> int:
+    """Workgroups per chunk of the batch 2-4 launch (8-wave workgroups, two
+    per CU): as many as keep the launch within one round, and few enough
+    that each wave has at least one iteration."""
+    chunks = sum(p.n_chunks for p in planes)
+    per_wave = min(p.iters_per_chunk for p in planes) // 10
+    return max(1, min(32, 2 * _cu_count(dev) // chunks, per_wave))
+
+
+def sorted_batch_fits(planes, batch) -> bool:
+    """Whether the batch kernel's LDS (fp16 activation of 2 or 4 rows, and
+    the accumulators of the tallest chunk) fits its 80 KiB: n = 2048 with
+    any chunk height, n = 6144 with the default 62-row chunks."""
+    nb = 2 if batch <= 2 else 4
+    n = planes[0].n
+    R = max(p.rows_per_chunk for p in planes)
+    return (max(n * nb // 2, 512 * nb) + 16 * (R + 1) * nb) * 4 <= 80 * 1024
+
+
+def _batch_x(x, n):
+    x2 = _contig(x, "x").reshape(-1, n)
+    if not 1 <= x2.shape[0] <= SORTED_BATCH_MAX:
+        raise Vq2Error(f"the sorted batch kernels take 1..{SORTED_BATCH_MAX} activation rows, got {x2.shape[0]}")
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    return x2
+
+
+def vq_sorted_gemm_batch(x, mats, cb0, cb1, n, rs=1.0, *, out_dtype=torch.float32, ys=None, slices=None):
+    """VQ GEMM of B = 1..4 rotated activation rows x [B, n] with up to 4
+    code-sorted matrices: one centroid gather serves every row (the
+    activation is held in fp16 with a power-of-two scale per row).  mats:
+    list of (SortedPlanes, scale).  Returns the list of outputs [B, out_rows]."""
+    n = int(n)
+    planes = [m[0] for m in mats]
+    if not 1 <= len(mats) <= 4 or any(p.n != n for p in planes):
+        raise Vq2Error("vq_sorted_gemm_batch: 1..4 matrices of width n")
+    if any(p.has_stage2 != planes[0].has_stage2 for p in planes):
+        raise Vq2Error("vq_sorted_gemm_batch: the matrices of a launch share one cfg")
+    dev = _dev(x, cb0, cb1, *[m[1] for m in mats], *[p.entries for p in planes])
+    cb0, cb1 = _sorted_cbs(planes, cb0, cb1)
+    x2 = _batch_x(x, n)
+    B = x2.shape[0]
+    if ys is None:
+        ys = [torch.empty((B, p.out_rows), dtype=out_dtype, device=dev) for p in planes]
+    arr = (_lib.SortedMat * len(mats))()
+    for k, ((p, s), y) in enumerate(zip(mats, ys)):
+        _contig(y, "y")
+        if y.numel() != B * p.out_rows or y.dtype != ys[0].dtype or y.device != dev:
+            raise Vq2Error(f"vq_sorted_gemm_batch: output {k} must be [{B}, {p.out_rows}] of the launch's dtype")
+        if s.dtype != mats[0][1].dtype:
+            raise Vq2Error("vq_sorted_gemm_batch: the scales of a launch share a dtype")
+        arr[k] = p.mat(s, y)
+    slices = sorted_batch_slices(planes, dev) if slices is None else int(slices)
+    lib = _lib.load()
+    ws = _workspace(dev, int(lib.vq2_sorted_gemm_batch_workspace(arr, len(mats), B, slices)), sorted_kind=True)
+    _lib.call("vq2_sorted_gemm_batch", _p(x2), _dt(x2, "x"), B, n, len(mats), arr, _p(cb0), _p(cb1),
+              _dt(cb0, "cb0"), _dt(mats[0][1], "scale"), _dt(ys[0], "y"), n, float(rs), slices, _p(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
+    return ys
+
+
+def vq_sorted_gemm_batch_argmax(x, planes, scale, cb0, cb1, n, rs=1.0):
+    """LM head + top-1 of B = 1..4 rotated activation rows x [B, n] over a
+    code-sorted matrix: (idx int64 [B], val fp32 [B]), torch.argmax's first
+    maximum per row of the logits, which are never written."""
+    n = int(n)
+    if planes.n != n:
+        raise Vq2Error("vq_sorted_gemm_batch_argmax: planes of another width")
+    dev = _dev(x, cb0, cb1, scale, planes.entries)
+    cb0, cb1 = _sorted_cbs([planes], cb0, cb1)
+    x2 = _batch_x(x, n)
+    B = x2.shape[0]
+    lib = _lib.load()
+    m = planes.mat(scale)
+    ws = _workspace(dev, int(lib.vq2_sorted_gemm_batch_argmax_workspace(ctypes.byref(m), B)))
+    idx = torch.empty(B, dtype=torch.int64, device=dev)
+    val = torch.empty(B, dtype=torch.float32, device=dev)
+    _lib.call("vq2_sorted_gemm_batch_argmax", _p(x2), _dt(x2, "x"), B, n, ctypes.byref(m), _p(cb0), _p(cb1),
+              _dt(cb0, "cb0"), _dt(scale, "scale"), n, float(rs), _p(ws), ws.numel(), _p(idx), _p(val),
+              _stream(dev))
+    return idx, val
+
+
 # ------------------------------------------------ MoE over sorted expert pools
 class SortedPool:
     """Code-sorted layout of an expert pool idx [E, rows, n/8] (int16, 2 bpw;

@@ -45,6 +45,22 @@ SORTED_MIN_CODES = 1 << 21
 # MI355X: q, k and v of the 2048-wide attention (0.79 M codes) 9.3 us
 # against 11.4 us on the gather kernel; o alone (0.52 M codes) 8.9 against 7.9.
 SORTED_MIN_LAUNCH_CODES = 640 * 1024
+# Batch 2-4 on the sorted layout (vq_sorted_gemm_batch: one centroid gather
+# for every activation row, the activation rotated by its own launch first)
+# where it was measured faster (HIP graphs, MI355X, us per call):
+#  * matrices of SORTED_BATCH_MIN_CODES codes or more -- the LM head
+#    151936 x 2048: 68.5 against 195.6 (gather kernel) at batch 2, 144
+#    against 181 (matrix cores) at batch 4, top-1 or logits;
+#  * batch 2 of inputs wider than 2048 (down 2048 x 6144, 4 bpw: 22.4 against
+#    28.9 on the gather kernel with the 6144-point RHT in its prologue);
+#  * PackedProjections at batch 3-4 (q, k, v in one launch: 22.0-24.4 against
+#    35.9-36.1 for the three projections on the matrix cores).
+# Not used where it was slower: one 6144 x 2048 4 bpw matrix at batch 2
+# (23.2 against 20.9) and 3-4 (32-35 against 24 on the matrix cores), the
+# down matrix at batch 3-4 (35-39 against 25), q / k / v at batch 2 (17.6
+# against 12.9).
+SORTED_BATCH = True
+SORTED_BATCH_MIN_CODES = 8 << 20
 # the sorted kernel builds the RHT in LDS up to this width, else x is rotated first
 SORTED_FUSED_RHT_MAX_N = 8192
 
@@ -102,6 +118,15 @@ class PackedLinear(nn.Module):
     def _sorted_ok(self, B, cb0):
         return self.sorted is not None and B == 1 and cb0.dtype in (torch.float16, torch.bfloat16)
 
+    def _sorted_batch_ok(self, B, cb0):
+        """Batch 2-4 on the sorted layout, where it was measured faster (see
+        SORTED_BATCH)."""
+        if not (SORTED_BATCH and self.sorted is not None and 2 <= B <= K.SORTED_BATCH_MAX
+                and cb0.dtype in (torch.float16, torch.bfloat16) and K.sorted_batch_fits([self.sorted], B)):
+            return False
+        codes = self.out * (self.n // 8) * len(self.cfg)
+        return codes >= SORTED_BATCH_MIN_CODES or (B == 2 and self.n > 2048)
+
     def _sorted_args(self, x1):
         """(x, perm, sign, hb, rht scale) for a sorted launch: the RHT built in
         the kernel up to SORTED_FUSED_RHT_MAX_N, else x rotated first."""
@@ -119,6 +144,9 @@ class PackedLinear(nn.Module):
             xs, perm, sign, hb, sc = self._sorted_args(x2.reshape(-1))
             y = K.vq_sorted_gemv(xs, [(self.sorted, self.scale)], cb0, cb1, self.n, perm, sign, hb, sc,
                                  out_dtype=od)[0]
+        elif self._sorted_batch_ok(B, cb0):
+            xr = self.rot.fwd(x2, out_dtype=torch.float32)
+            y = K.vq_sorted_gemm_batch(xr, [(self.sorted, self.scale)], cb0, cb1, self.n, out_dtype=od)[0]
         elif B <= 2 and self.n % 64 == 0:
             # one launch: every workgroup rotates x in LDS, then multiplies
             y = K.vq_gemv_rht(x2, [(i0, i1, self.scale, self.out)], cb0, cb1, self.n, self.rot._perm32,
@@ -140,10 +168,11 @@ class PackedProjections(nn.Module):
     "attn", vq2/quantize_35b.py:146-161, so they share the RHT of the input).
     ``forward(x)`` returns the list of the projections' outputs, each what the
     projection's own forward gives (vq2/runtime.py:91-110, once per matrix
-    there): at batch 1 one sorted-layout launch when the matrices hold
-    ``SORTED_MIN_LAUNCH_CODES`` codes or more together, else one gather-kernel
-    launch with the RHT built in for batch <= 2; larger batches run each
-    projection.  Up to 4 projections."""
+    there): with the sorted layout (the matrices hold
+    ``SORTED_MIN_LAUNCH_CODES`` codes or more together) one sorted launch at
+    batch 1 and one sorted batch launch after the RHT at batch 3-4; else one
+    gather-kernel launch with the RHT built in for batch <= 2; other batches
+    run each projection.  Up to 4 projections."""
 
     def __init__(self, linears, sorted_layout=None):
         super().__init__()
@@ -177,6 +206,11 @@ class PackedProjections(nn.Module):
             xs, perm, sign, hb, sc = a._sorted_args(x2.reshape(-1))
             ys = K.vq_sorted_gemv(xs, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n, perm,
                                   sign, hb, sc, out_dtype=od)
+        elif (SORTED_BATCH and self.sorted is not None and 3 <= B <= K.SORTED_BATCH_MAX
+              and cb0.dtype in (torch.float16, torch.bfloat16) and K.sorted_batch_fits(self.sorted, B)):
+            xr = a.rot.fwd(x2, out_dtype=torch.float32)
+            ys = K.vq_sorted_gemm_batch(xr, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n,
+                                        out_dtype=od)
         elif B <= 2 and a.n % 64 == 0:
             mats = []
             for m in lins:
@@ -208,5 +242,8 @@ class PackedLMHead(nn.Module):
         if lin._sorted_ok(x2.shape[0], cb0):
             xs, perm, sign, hb, sc = lin._sorted_args(x2.reshape(-1))
             return K.vq_sorted_gemv_argmax(xs, lin.sorted, lin.scale, cb0, cb1, lin.n, perm, sign, hb, sc)
+        if lin._sorted_batch_ok(x2.shape[0], cb0):
+            xr = lin.rot.fwd(x2, out_dtype=torch.float32)
+            return K.vq_sorted_gemm_batch_argmax(xr, lin.sorted, lin.scale, cb0, cb1, lin.n)
         xr = lin.rot.fwd(x2, out_dtype=lin.act_dtype)
         return K.vq_gemv_argmax(xr, i0, i1, cb0, cb1, lin.scale, lin.out, lin.n, 1.0)

@@ -403,6 +403,38 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
                            int s_dt, int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
                            float* out_val, void* stream);
 
+/* VQ GEMM of batch = 1..4 activation rows over up to 4 packed matrices:
+ *   y_m[b * out_rows + r] = (sum_k W_m[r, k] * xr[b * x_stride + k]) * scale_m[r] * rs
+ * with xr already rotated (16-byte aligned, x_stride >= n, a multiple of 8)
+ * and every output y_m [batch, out_rows].  One centroid gather serves every
+ * activation row.  The activation is held in fp16 with a power-of-two
+ * scale per row (fp16 activations as they are; ~1e-4 of max |y|), all sums
+ * in fp32.  `slices` workgroups share each chunk; with more than one,
+ * `workspace` (vq2_sorted_gemm_batch_workspace bytes, header zero as for
+ * vq2_sorted_gemv, which it may share) holds the partials and the chunk's
+ * last workgroup sums them in slice order (deterministic).  Needs
+ * n * (2 or 4) * 2 + 64 * (rows_per_chunk + 1) * (2 or 4) bytes of LDS at
+ * most 80 KiB (e.g. n = 2048 with 255-row chunks, n = 6144 with 62-row
+ * chunks), else VQ2_ERR_UNSUPPORTED.  Replaces the PackedLinear batch > 1
+ * fallback, dequant + F.linear (vq2/runtime.py:82-89, 105-110). */
+size_t vq2_sorted_gemm_batch_workspace(const vq2_sorted_mat* mats, int n_mat, int64_t batch, int slices);
+int vq2_sorted_gemm_batch(const void* x, int x_dt, int64_t batch, int64_t x_stride, int n_mat,
+                          const vq2_sorted_mat* mats, const void* cb0, const void* cb1, int cb_dt, int s_dt, int y_dt,
+                          int64_t n, float rs, int slices, void* workspace, size_t ws_bytes, void* stream);
+
+/* vq2_sorted_gemm_batch of one matrix followed by the top-1 of every
+ * activation row, without writing logits: out_idx[b] = argmax_r y[b, r]
+ * (first maximum; int64, 8-byte aligned), out_val[b] = y[b, out_idx[b]]
+ * (may be NULL).  `workspace`: vq2_sorted_gemm_batch_argmax_workspace bytes
+ * (one key per chunk and row, 8-byte aligned).  Replaces PackedLMHead.forward
+ * at batch > 1 (vq2/runtime.py:136-144, 105-110) + torch.argmax
+ * (legion/engine.py:288). */
+size_t vq2_sorted_gemm_batch_argmax_workspace(const vq2_sorted_mat* mat, int64_t batch);
+int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
+                                 const vq2_sorted_mat* mat, const void* cb0, const void* cb1, int cb_dt, int s_dt,
+                                 int64_t n, float rs, void* workspace, size_t ws_bytes, int64_t* out_idx,
+                                 float* out_val, void* stream);
+
 /* ---- MoE experts over code-sorted expert pools -------------------------
  * vq2_sorted_pack_pool (host memory, no GPU work) packs an expert pool
  * idx [n_experts, rows, ng] (one int16 plane, 2 bpw) expert by expert, each

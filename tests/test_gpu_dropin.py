@@ -11,6 +11,7 @@ import torch
 
 from compressai_amd import kernels as K, synth
 from oracle import vq2_oracle as O
+from act_rounding import fp16_row_scaled
 
 pytestmark = pytest.mark.gpu
 
@@ -162,8 +163,9 @@ def test_small_m_workspace_outlives_captured_graph(dev):
 @pytest.mark.parametrize("cfg,out,n", [((16, 16), 6144, 2048), ((16,), 151936, 2048), ((16, 16), 2048, 6144)])
 def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
     """Large PackedLinear matrices keep a code-sorted copy of their planes and
-    run batch 1 on it (RHT fused in the kernel); the outputs and the LM-head
-    top-1 match the oracle, and batch 2 (gather kernel) agrees with them."""
+    run batch 1 on it (RHT fused in the kernel); batch 2 runs the sorted batch
+    kernel (LM head, 6144-wide input) or the gather kernel; the outputs and
+    the LM-head top-1 match the oracle."""
     from compressai_amd.runtime import PackedLinear, PackedLMHead
 
     bpw = 4 if cfg == (16, 16) else 2
@@ -178,20 +180,57 @@ def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
     _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu() if bpw == 4 else None,
                        lin.scale.cpu())
     assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
-    y2 = lin(torch.cat([x, x]).to(dev), out_dtype=torch.float32)  # batch 2: the gather kernel
-    assert O.max_rel_err(y2[1].cpu().numpy(), y[0].cpu().numpy()) < 1e-5
+    # batch 2: the sorted batch kernel for the LM head and the 6144-wide
+    # input (x rotated first, held in fp16 under a power-of-two scale per
+    # row), the gather kernel with the RHT built in for the gate shape
+    y2 = lin(torch.cat([x, x]).to(dev), out_dtype=torch.float32)
+    batch_kernel = out == 151936 or n > 2048
+    xk = fp16_row_scaled(lin.rot.fwd(x.to(dev), out_dtype=torch.float32).cpu().numpy()) if batch_kernel else xr
+    _, y64k = O.vq_gemv(xk, m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu() if bpw == 4 else None,
+                        lin.scale.cpu())
+    for b in range(2):
+        assert O.max_rel_err(y2[b].cpu().numpy(), y64[0]) < TOL
+        assert O.max_rel_err(y2[b].cpu().numpy(), y64k[0]) < 1e-5
     if cfg == (16,):
         idx, val = PackedLMHead(lin).argmax(x.to(dev))
         assert int(idx[0]) == int(np.argmax(y64[0]))
         assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
 
 
+@pytest.mark.parametrize("B", [2, 3, 4])
+def test_lm_head_batch_top1_on_sorted_batch_kernel(dev, B):
+    """An LM head of 32768 x 2048 (8.4 M codes) at batch 2-4: PackedLMHead.argmax
+    and the logits of PackedLinear run the sorted batch kernel after the RHT;
+    the top-1 of every row is the argmax of the oracle's logits of the
+    activation as the kernel holds it, and the logits match them."""
+    from compressai_amd.runtime import PackedLinear, PackedLMHead
+
+    out, n = 32768, 2048
+    cbs = {"16": synth.codebook(9386).to(dev)}
+    m = synth.vq_matrix(9387, out, n, bpw=2)
+    lin = PackedLinear((out, n), (16,), "lm_head", [m["idx0"]], m["scale"], cbs, dev)
+    assert lin._sorted_batch_ok(B, cbs["16"])
+    x = synth.activations(9388 + B, (B, n), dtype=torch.float16)
+    # the activation as the kernel holds it: the rotation the runtime ran
+    # (pinned against the oracle by the RHT tests), rounded as the kernel rounds
+    xk = fp16_row_scaled(lin.rot.fwd(x.to(dev), out_dtype=torch.float32).cpu().numpy())
+    _, y64k = O.vq_gemv(xk, m["idx0"], None, cbs["16"].cpu(), None, lin.scale.cpu())
+    idx, val = PackedLMHead(lin).argmax(x.to(dev))
+    y = lin(x.to(dev), out_dtype=torch.float32)
+    for b in range(B):
+        assert int(idx[b]) == int(np.argmax(y64k[b])), b
+        assert abs(float(val[b]) - y64k[b].max()) <= 1e-5 * abs(y64k[b].max()), b
+        assert O.max_rel_err(y[b].cpu().numpy(), y64k[b]) < 1e-5, b
+
+
 @pytest.mark.parametrize("act", [torch.float32, torch.float16])
 def test_packed_projections_qkv(dev, act):
     """q, k and v of a 2048-wide attention (tag "attn", one activation) in one
     launch: the sorted layout at batch 1 (0.79 M codes together), the fused
-    gather kernel at batch 2, each projection at batch 3; every output matches
-    the projection's own PackedLinear forward and the oracle."""
+    gather kernel at batch 2, the sorted batch kernel at batch 3 (activation
+    held in fp16 under a power-of-two scale per row); every output matches
+    the oracle (to 1e-5 on the activation as the kernel holds it) and the
+    projection's own PackedLinear forward."""
     from compressai_amd.runtime import PackedLinear, PackedProjections
 
     n = 2048
@@ -210,12 +249,15 @@ def test_packed_projections_qkv(dev, act):
         x = synth.activations(9395 + B, (B, n), dtype=act)
         ys = proj(x.to(dev), out_dtype=torch.float32)
         xr = O.rht(x.float(), perm, sign, 2048).astype(np.float32)
+        xk = fp16_row_scaled(lins[0].rot.fwd(x.to(dev), out_dtype=torch.float32).cpu().numpy()) if B >= 3 else xr
         for lin, m, y in zip(lins, mats, ys):
             assert y.shape == (B, lin.out) and y.dtype == torch.float32
             own = lin(x.to(dev), out_dtype=torch.float32)
-            assert O.max_rel_err(y.cpu().numpy(), own.cpu().numpy()) < 1e-5
+            assert O.max_rel_err(y.cpu().numpy(), own.cpu().numpy()) < (1e-5 if B <= 2 else TOL)
             _, y64 = O.vq_gemv(xr, m["idx0"], None, cbs["16"].cpu(), None, lin.scale.cpu())
             assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+            _, y64k = O.vq_gemv(xk, m["idx0"], None, cbs["16"].cpu(), None, lin.scale.cpu())
+            assert O.max_rel_err(y.cpu().numpy(), y64k) < 1e-5
 
 
 def test_packed_projections_rejects_mixed(dev):
