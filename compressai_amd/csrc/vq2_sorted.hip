@@ -343,7 +343,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
 
     // the wave's first entry words come from HBM while the prologue stages
     // and rotates the activation (which waits only for its own, earlier
-    // loads); the first gathers go out after it
+    // loads); the first gathers go out inside it (XM 3) or after it (XM 1)
     // (a pre-rotated x is only copied: there the gathers go out at once)
     // gathers one iteration ahead (measured on the dense step: 49.1 us
     // against 49.3 at two; three, before the pipeline's tail stopped loading
@@ -362,7 +362,11 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
         build_x<1, XT>(a.g, s_nat, s_stage, 1, n, first);
         x_finalize(s_nat, s_x, n, a.g.xscale);
     } else if constexpr (XM == 3) {
-        rht2k_build<XT>((int)(n / RHT2K), n, first2k, smem + n, s_nat, s_x, a.g.xscale);
+        // the first gathers go out between the lane stages and the LDS
+        // passes (measured: dense step 46.96 -> 46.65 us, LM head 65.2 ->
+        // 64.9; before the transform, waiting there for the entry words:
+        // 48.1)
+        rht2k_build<XT>((int)(n / RHT2K), n, first2k, smem + n, s_nat, s_x, a.g.xscale, [&]() { pipe.gathers(); });
     } else {
         for (int64_t g = threadIdx.x; g < a.ng; g += SG_THREADS) {
             float v[8];
@@ -372,7 +376,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
         }
     }
     __syncthreads();
-    if constexpr (XM != 0) pipe.gathers();
+    if constexpr (XM == 1) pipe.gathers();
     pipe.run(acc, s_x, a.gbits, a.ng, R);
     __syncthreads();
 

@@ -206,10 +206,16 @@ __device__ __forceinline__ void rht2k_stage(int k, const Rht2kLoad& L, void* s_s
 }
 
 // Part 2, the transform: s_nat: n floats; s_split: the split layout (may
-// overlap s_stage, not s_nat).  A barrier must follow.
-template <int XT>
+// overlap s_stage, not s_nat).  mid() runs after the register and lane
+// stages, before the two LDS passes (a caller issues its first centroid
+// gathers there: their latency then overlaps the LDS passes).  A barrier
+// must follow.
+struct NoMid {
+    __device__ void operator()() const {}
+};
+template <int XT, class M = NoMid>
 __device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoad& L, const void* s_stage,
-                                                float* s_nat, float* s_split, float scale)
+                                                float* s_nat, float* s_split, float scale, M mid = M())
 {
     const int t = threadIdx.x, lane = t & 63;
     // permuted values, signs, bit 0, bits 1-6
@@ -243,6 +249,7 @@ __device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoa
         }
     }
     __syncthreads();
+    mid();
     // bits 7-8: values base + 128 i
     for (int u = t; u < 512 * k; u += SG_THREADS) {
         const int64_t base = (int64_t)(u >> 9) * RHT2K + ((u & 511) >> 7 << 9) + (u & 127);
@@ -269,12 +276,12 @@ __device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoa
     }
 }
 
-template <int XT>
+template <int XT, class M = NoMid>
 __device__ __forceinline__ void rht2k_build(int k, int64_t n, const Rht2kLoad& L, void* s_stage, float* s_nat,
-                                            float* s_split, float scale)
+                                            float* s_split, float scale, M mid = M())
 {
     rht2k_stage<XT>(k, L, s_stage);
-    rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale);
+    rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale, mid);
 }
 
 // One 512-point block by the same all-threads scheme (the MoE down
