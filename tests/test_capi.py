@@ -72,6 +72,34 @@ def test_moe_and_rht_reject_bad_arguments_on_host():
     assert "bad sizes" in msg
 
 
+def test_sorted_batch_rejects_bad_arguments_on_host():
+    """vq2_sorted_gemm_batch / _argmax: batch outside 1..4, a short or
+    unaligned activation row, LDS beyond 80 KiB and a bad chunk height are
+    refused before any HIP call (the pointers are never dereferenced)."""
+    L = _lib.load()
+
+    def mat(rows=512, ng=256, R=205, ipc=10):
+        chunks = -(-rows // R)
+        return _lib.SortedMat(4096, ipc, ipc, ipc * chunks, R, 0, 4096, 4096, rows)
+
+    m = mat()
+    args = lambda batch, stride, mm, n: (4096, 0, batch, stride, 1, ctypes.byref(mm), 4096, None, 1, 1, 0, n, 1.0,
+                                         1, None, 0, None)
+    assert "batch=5" in _err(L.vq2_sorted_gemm_batch(*args(5, 2048, m, 2048)))
+    assert "batch=0" in _err(L.vq2_sorted_gemm_batch(*args(0, 2048, m, 2048)))
+    assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2040, m, 2048)))
+    assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2052, m, 2048)))
+    # n = 16384 (ng 2048, chunks of at most 31 rows): 4 fp16 rows are 128 KiB of LDS
+    big = mat(rows=64, ng=2048, R=31)
+    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(4, 16384, big, 16384)))
+    # rows_per_chunk beyond what 16-bit positions hold for ng = 256
+    assert "rows_per_chunk" in _err(L.vq2_sorted_gemm_batch(*args(2, 2048, mat(R=300), 2048)))
+    msg = _err(L.vq2_sorted_gemm_batch_argmax(4096, 0, 3, 2048, ctypes.byref(m), 4096, None, 1, 1, 2048, 1.0,
+                                              4096, 1 << 20, None, None, None))
+    assert "out_idx" in msg
+    assert L.vq2_sorted_gemm_batch_workspace(ctypes.byref(m), 1, 2, 1) == 0
+
+
 def test_python_entry_points_refuse_cpu_tensors():
     from compressai_amd import kernels as K
 
