@@ -664,10 +664,15 @@ _MOE_RATE = 1460.0
 _MOE_FIXED_US = (2.5, 2.0)
 
 
-def moe_slices(units, codes_per_unit, cu, fixed_us):
+def moe_slices(units, codes_per_unit, cu, fixed_us, one_launch=False):
     """Slices per chunk for `units` (pair, chunk) units: the count that
     minimises rounds x (work per slice + fixed cost), with one 16-wave
-    workgroup per CU at a time."""
+    workgroup per CU at a time.  one_launch (gate_up and down in one launch):
+    units that fill the device on their own take one slice, since the down
+    workgroups fill a last partial round (measured, T = 8: one gate_up slice
+    72.97 us per layer, two 80.2)."""
+    if one_launch and units >= cu:
+        return 1
     best, best_t = 1, None
     for s in range(1, 33):
         t = -(-units * s // cu) * (codes_per_unit / _MOE_RATE / s + fixed_us)
@@ -679,7 +684,8 @@ def moe_slices(units, codes_per_unit, cu, fixed_us):
 def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, cb, rot_h, rot_i, *, ids=None,
                   w=None, logits=None, top_k=None, shared_id=None, shared_gate=None, out_dtype=torch.float32,
                   out=None, slices=None):
-    """The experts of an MoE layer over code-sorted pools, three launches:
+    """The experts of an MoE layer over code-sorted pools, two launches
+    (gate_up and down in one, then the combine; three at other widths):
     out [T, H] = sum_k w[t, k] * VQ(down[e]) RHT_I(silu(gu[:I]) * gu[I:]),
     gu = VQ(gate_up[e]) RHT_H(h_t), e = ids[t, k].  With `logits` [T, E_r]
     the router is built in (top_k routed experts plus the shared expert
@@ -721,8 +727,11 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         raise Vq2Error(f"out must be a contiguous [{T}, {H}]")
     if slices is None:
         cu = _cu_count(dev)
-        sg = moe_slices(T * P * gate_up.chunks, gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0])
-        sd = moe_slices(T * P * down.chunks, down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1])
+        # the library runs gate_up and down as one launch for these shapes
+        # (2048-point and 512-point rotations, at most 128 pairs)
+        one = H == 2048 and I == 512 and int(rot_h[2]) == 2048 and int(rot_i[2]) == 512 and T * P <= 128
+        sg = moe_slices(T * P * gate_up.chunks, gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0], one)
+        sd = moe_slices(T * P * down.chunks, down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1], one)
     else:
         sg, sd = (int(v) for v in slices)
     lib = _lib.load()
