@@ -54,11 +54,13 @@ SORTED_MIN_LAUNCH_CODES = 640 * 1024
 #  * batch 2 of inputs wider than 2048 (down 2048 x 6144, 4 bpw: 22.4 against
 #    28.9 on the gather kernel with the 6144-point RHT in its prologue);
 #  * PackedProjections at batch 3-4 (q, k, v in one launch: 22.0-24.4 against
-#    35.9-36.1 for the three projections on the matrix cores).
+#    35.9-36.1 for the three projections on the matrix cores; gate + up:
+#    40.1-42.0 against 47.0-47.4), and at batch 2 with SORTED_MIN_CODES codes
+#    or more (gate + up: 24.6 against 37.6 in one gather-kernel launch).
 # Not used where it was slower: one 6144 x 2048 4 bpw matrix at batch 2
 # (23.2 against 20.9) and 3-4 (32-35 against 24 on the matrix cores), the
 # down matrix at batch 3-4 (35-39 against 25), q / k / v at batch 2 (17.6
-# against 12.9).
+# against 12.9; 0.79 M codes).
 SORTED_BATCH = True
 SORTED_BATCH_MIN_CODES = 8 << 20
 # the sorted kernel builds the RHT in LDS up to this width, else x is rotated first
@@ -170,7 +172,8 @@ class PackedProjections(nn.Module):
     projection's own forward gives (vq2/runtime.py:91-110, once per matrix
     there): with the sorted layout (the matrices hold
     ``SORTED_MIN_LAUNCH_CODES`` codes or more together) one sorted launch at
-    batch 1 and one sorted batch launch after the RHT at batch 3-4; else one
+    batch 1 and one sorted batch launch after the RHT at batch 3-4, and at
+    batch 2 with ``SORTED_MIN_CODES`` codes or more (gate + up); else one
     gather-kernel launch with the RHT built in for batch <= 2; other batches
     run each projection.  Up to 4 projections."""
 
@@ -187,6 +190,7 @@ class PackedProjections(nn.Module):
                 raise K.Vq2Error("PackedProjections: the projections must share the scale dtype")
         self.lins = nn.ModuleList(lins)
         codes = sum(m.out * (m.n // 8) * len(m.cfg) for m in lins)
+        self.codes = codes
         dev = a.idx0.device
         use = sorted_layout if sorted_layout is not None else (
             codes >= SORTED_MIN_LAUNCH_CODES and dev.type == "cuda" and a.cfg in ((16,), (16, 16)))
@@ -206,7 +210,8 @@ class PackedProjections(nn.Module):
             xs, perm, sign, hb, sc = a._sorted_args(x2.reshape(-1))
             ys = K.vq_sorted_gemv(xs, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n, perm,
                                   sign, hb, sc, out_dtype=od)
-        elif (SORTED_BATCH and self.sorted is not None and 3 <= B <= K.SORTED_BATCH_MAX
+        elif (SORTED_BATCH and self.sorted is not None and 2 <= B <= K.SORTED_BATCH_MAX
+              and (B >= 3 or self.codes >= SORTED_MIN_CODES)
               and cb0.dtype in (torch.float16, torch.bfloat16) and K.sorted_batch_fits(self.sorted, B)):
             xr = a.rot.fwd(x2, out_dtype=torch.float32)
             ys = K.vq_sorted_gemm_batch(xr, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n,

@@ -260,6 +260,34 @@ def test_packed_projections_qkv(dev, act):
             assert O.max_rel_err(y.cpu().numpy(), y64k) < 1e-5
 
 
+@pytest.mark.parametrize("B", [2, 4])
+def test_packed_projections_gate_up_batch(dev, B):
+    """gate and up (tag "mlp", 2 x 6144 x 2048 at 4 bpw, 6.3 M codes) as one
+    PackedProjections at batch 2 and 4: one sorted batch launch after the
+    RHT; each output matches the oracle, to 1e-5 on the activation as the
+    kernel holds it."""
+    from compressai_amd.runtime import PackedLinear, PackedProjections
+
+    n = 2048
+    cbs = {"16": synth.codebook(9400).to(dev), "16_16": synth.codebook(9401).to(dev)}
+    ms = [synth.vq_matrix(9402 + k, 6144, n, bpw=4) for k in range(2)]
+    lins = [PackedLinear((6144, n), (16, 16), "mlp", [m["idx0"], m["idx1"]], m["scale"], cbs, dev) for m in ms]
+    proj = PackedProjections(lins)
+    assert proj.sorted is not None and proj.codes >= 2 << 20
+    x = synth.activations(9405 + B, (B, n), dtype=torch.float16)
+    ys = proj(x.to(dev), out_dtype=torch.float32)
+    perm, sign = _rot_np(lins[0].rot)
+    xr = O.rht(x.float(), perm, sign, 2048).astype(np.float32)
+    xk = fp16_row_scaled(lins[0].rot.fwd(x.to(dev), out_dtype=torch.float32).cpu().numpy())
+    for lin, m, y in zip(lins, ms, ys):
+        assert y.shape == (B, 6144)
+        args = (m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_16"].cpu(), lin.scale.cpu())
+        _, y64 = O.vq_gemv(xr, *args)
+        _, y64k = O.vq_gemv(xk, *args)
+        assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+        assert O.max_rel_err(y.cpu().numpy(), y64k) < 1e-5
+
+
 def test_packed_projections_rejects_mixed(dev):
     """Projections of other widths, tags or codebooks cannot share a launch."""
     from compressai_amd.runtime import PackedLinear, PackedProjections
