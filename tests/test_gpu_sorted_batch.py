@@ -3,7 +3,8 @@
 on the same seeded inputs: 2 and 4 bpw, fp16 / bf16 codebooks, fp32 / fp16 /
 bf16 activations, the config 2 / 3 shapes and ragged ones, one or several
 workgroups per chunk, two matrices per launch, the fused top-1 at the
-config 3 LM-head size (ties resolve to the lower row), and the error paths.
+config 3 LM-head size (ties resolve to the lower row), graph replays and the
+error paths.
 
 Tolerance: max_i |y_i - ref_i| / max_i |ref_i| <= 1e-3 against the fp32
 activation (the decode-path contract; the kernel holds the activation in
@@ -165,3 +166,36 @@ def test_batch_gemm_errors(dev):
     with pytest.raises(Vq2Error, match="LDS"):
         K.vq_sorted_gemm_batch(torch.zeros(4, 16384, device=dev), [(spb, big["scale"].to(dev))], cb0.to(dev), None,
                                16384)
+
+
+def test_batch_paths_graph_replays_match_eager(dev):
+    """gate + up at batch 2 (one sorted batch launch, several slices per
+    chunk summed in the launch) and the LM-head top-1 at batch 2, captured
+    once; every replay, with eager work and synchronisations between the
+    replays, equals the eager step bit for bit."""
+    from compressai_amd.graph import DecodeStepGraph
+    from compressai_amd.runtime import PackedLinear, PackedLMHead, PackedProjections
+
+    n = 2048
+    cbs = {"16": synth.codebook(9780).to(dev), "16_16": synth.codebook(9781).to(dev)}
+    ms = [synth.vq_matrix(9782 + k, 6144, n, bpw=4) for k in range(2)]
+    gu = PackedProjections([PackedLinear((6144, n), (16, 16), "mlp", [m["idx0"], m["idx1"]], m["scale"], cbs, dev)
+                            for m in ms])
+    mh = synth.vq_matrix(9784, 32768, n, bpw=2)
+    head = PackedLMHead(PackedLinear((32768, n), (16,), "lm_head", [mh["idx0"]], mh["scale"], cbs, dev))
+    assert K.sorted_batch_slices(gu.sorted, dev) > 1
+
+    def step(x):
+        g, u = gu(x, out_dtype=torch.float32)
+        idx, val = head.argmax(x)
+        return g, u, idx, val
+
+    gstep = DecodeStepGraph(step, [synth.activations(9785, (2, n), dtype=torch.float16).to(dev)])
+    for r in range(4):
+        x = synth.activations(9786 + r, (2, n), dtype=torch.float16).to(dev)
+        ref = [t.clone() for t in step(x)]
+        torch.cuda.synchronize()
+        out = [t.clone() for t in gstep(x)]
+        torch.cuda.synchronize()
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), r
