@@ -158,6 +158,14 @@ struct SortedCall {
 };
 
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
+// Checks shared by the sorted launches (`who` prefixes the messages): the
+// matrix count, chunk heights (*rmax: the tallest), codebook dtype and
+// alignment, slices, and the top-1's single matrix and slice; then, per
+// matrix, its iteration count, entry alignment, stage-2 codebook and
+// iterations = chunks x iterations per chunk (*ks: its chunks).
+struct ChunkSplit;
+int sorted_check_call(const SortedCall& c, bool top1, const char* who, int64_t* rmax);
+int sorted_check_seg(const SortedCall& c, int s, const char* who, ChunkSplit* ks);
 size_t sorted_batch_workspace_bytes(const SortedCall& c);
 size_t sorted_batch_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk, int64_t batch);
 int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);

@@ -60,7 +60,6 @@
 
 namespace vq2 {
 
-constexpr int SG_MAX_SEG = 4;
 
 // Default chunk height: the rows split evenly over the fewest chunks; with
 // chunk_align > 1, over a multiple of chunk_align chunks (one per CU and
@@ -479,31 +478,53 @@ size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk)
     return (size_t)((out_rows + rows_per_chunk - 1) / rows_per_chunk) * sizeof(uint64_t);
 }
 
-int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
+int sorted_check_call(const SortedCall& c, bool top1, const char* who, int64_t* rmax)
 {
-    const bool top1 = top1_idx != nullptr;
-    if (c.nseg < 1 || c.nseg > SG_MAX_SEG) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: 1..%d matrices", SG_MAX_SEG);
+    if (c.nseg < 1 || c.nseg > SG_MAX_SEG) return set_error(VQ2_ERR_ARG, "%s: 1..%d matrices", who, SG_MAX_SEG);
     const int64_t r_lim = sorted_max_rows(c.ng);
-    if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: ng=%lld unsupported", (long long)c.ng);
-    int64_t rmax = 0;
+    if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "%s: ng=%lld unsupported", who, (long long)c.ng);
+    *rmax = 0;
     for (int s = 0; s < c.nseg; s++) {
         const int64_t R = c.seg[s].rows_per_chunk;
         if (R < 1 || R > r_lim)
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d: rows_per_chunk=%lld outside 1..%lld", s,
-                             (long long)R, (long long)r_lim);
-        rmax = std::max(rmax, R);
+            return set_error(VQ2_ERR_ARG, "%s: matrix %d: rows_per_chunk=%lld outside 1..%lld", who, s, (long long)R,
+                             (long long)r_lim);
+        *rmax = std::max(*rmax, R);
     }
     if (c.cb_dt != VQ2_DT_F16 && c.cb_dt != VQ2_DT_BF16)
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: fp16 / bf16 codebooks only");
-    if (c.slices < 1 || c.slices > 64) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: slices must be 1..64");
-    if (top1 && (c.slices != 1 || c.nseg != 1))
-        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV top-1: one matrix, one slice");
+        return set_error(VQ2_ERR_UNSUPPORTED, "%s: fp16 / bf16 codebooks only", who);
+    if (c.slices < 1 || c.slices > 64) return set_error(VQ2_ERR_ARG, "%s: slices must be 1..64", who);
+    if (top1 && (c.slices != 1 || c.nseg != 1)) return set_error(VQ2_ERR_ARG, "%s top-1: one matrix, one slice", who);
+    if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
+        return set_error(VQ2_ERR_ARG, "%s: codebooks must be 16-byte aligned", who);
+    return VQ2_OK;
+}
+
+int sorted_check_seg(const SortedCall& c, int s, const char* who, ChunkSplit* ks)
+{
+    const SortedSegCall& sc = c.seg[s];
+    *ks = chunk_split(sc.out_rows, sc.rows_per_chunk);
+    if (sc.n_iters < 1 || sc.n_iters > 0x7FFFFFFF)
+        return set_error(VQ2_ERR_ARG, "%s: matrix %d has %lld iterations", who, s, (long long)sc.n_iters);
+    if ((uintptr_t)sc.entries % 16) return set_error(VQ2_ERR_ARG, "%s: entries must be 16-byte aligned", who);
+    if (sc.s2 != (c.cb1 != nullptr)) return set_error(VQ2_ERR_ARG, "%s: stage-2 entries need cb1", who);
+    if (sc.iters_per_chunk < 1 || sc.stage1_iters < 0 || sc.stage1_iters > sc.iters_per_chunk ||
+        sc.iters_per_chunk * ks->n_chunks != sc.n_iters || (!sc.s2 && sc.stage1_iters != sc.iters_per_chunk))
+        return set_error(VQ2_ERR_ARG, "%s: matrix %d: %lld iterations are not %lld chunks x %lld (%lld of stage 1)",
+                         who, s, (long long)sc.n_iters, (long long)ks->n_chunks, (long long)sc.iters_per_chunk,
+                         (long long)sc.stage1_iters);
+    return VQ2_OK;
+}
+
+int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
+{
+    const bool top1 = top1_idx != nullptr;
+    int64_t rmax = 0;
+    if (int r = sorted_check_call(c, top1, "vq2 sorted GEMV", &rmax)) return r;
     const int64_t n = c.ng * 8;
     const size_t shm = (size_t)((c.xm != 0 ? n : 0) + SG_X_SPLIT + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
     if (n > 2 * SG_XB || shm > SG_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large (at most %d)", (long long)n, 2 * SG_XB);
-    if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
-        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: codebooks must be 16-byte aligned");
     if (c.xm == 1) {
         if (n % 64) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: fused RHT needs n %% 64 == 0");
         if (c.hb < 2 || c.hb > n || (c.hb & (c.hb - 1)) || n % c.hb)
@@ -556,17 +577,9 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     for (int s = 0; s < c.nseg; s++) {
         const SortedSegCall& sc = c.seg[s];
         const int64_t R = sc.rows_per_chunk;
-        const ChunkSplit ks = chunk_split(sc.out_rows, R);
+        ChunkSplit ks;
+        if (int r = sorted_check_seg(c, s, "vq2 sorted GEMV", &ks)) return r;
         const int64_t n_chunks = ks.n_chunks;
-        if (sc.n_iters < 1 || sc.n_iters > 0x7FFFFFFF)
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d has %lld iterations", s, (long long)sc.n_iters);
-        if ((uintptr_t)sc.entries % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: entries must be 16-byte aligned");
-        if (sc.s2 != (c.cb1 != nullptr)) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: stage-2 entries need cb1");
-        if (sc.iters_per_chunk < 1 || sc.stage1_iters < 0 || sc.stage1_iters > sc.iters_per_chunk ||
-            sc.iters_per_chunk * n_chunks != sc.n_iters || (!sc.s2 && sc.stage1_iters != sc.iters_per_chunk))
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMV: matrix %d: %lld iterations are not %lld chunks x %lld "
-                             "(%lld of stage 1)", s, (long long)sc.n_iters, (long long)n_chunks,
-                             (long long)sc.iters_per_chunk, (long long)sc.stage1_iters);
         a.seg[s].ent = (const u32x4*)sc.entries;
         a.seg[s].ipc = (int32_t)sc.iters_per_chunk;
         a.seg[s].ipc1 = (int32_t)sc.stage1_iters;

@@ -20,6 +20,7 @@ constexpr int SG_MAX_R = 255;
 constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
 constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
 constexpr int SG_MAX_SHM = 96 * 1024;         // dynamic LDS: activation (+ stage) + accumulators
+constexpr int SG_MAX_SEG = 4;                 // matrices per launch
 
 inline int sorted_gbits(int64_t ng)
 {

@@ -42,7 +42,6 @@ constexpr int SB_THREADS = 512;
 constexpr int SB_WAVES = SB_THREADS / 64;
 constexpr int SB_ARRAYS = SB_WAVES * SG_PARTS;  // accumulator arrays per workgroup
 constexpr int SB_MAX_SHM = 80 * 1024;           // two workgroups per CU
-constexpr int SB_MAX_SEG = 4;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -86,7 +85,7 @@ struct SortedBatchArgs {
     int nseg;
     int nc;
     int x_floats;  // floats of LDS before the accumulators (activation, later the row-sum stage)
-    SortedBatchSeg seg[SB_MAX_SEG];
+    SortedBatchSeg seg[SG_MAX_SEG];
     uint64_t* cand;  // EP 1: [workgroup][batch] best top-1 keys
 };
 
@@ -178,7 +177,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     const int slice = pos / a.nc, gchunk = pos - slice * a.nc;
     int si = 0;
 #pragma unroll
-    for (int s = 1; s < SB_MAX_SEG; s++) si += (s < a.nseg && gchunk >= a.seg[s].chunk_start) ? 1 : 0;
+    for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && gchunk >= a.seg[s].chunk_start) ? 1 : 0;
     const SortedBatchSeg& sg = a.seg[si];
     const int R = sg.R;
     const int chunk = gchunk - sg.chunk_start;
@@ -400,28 +399,12 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
 {
     const bool top1 = top1_idx != nullptr;
     if (c.batch < 1 || c.batch > 4) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: batch=%lld outside 1..4", (long long)c.batch);
-    if (c.nseg < 1 || c.nseg > SB_MAX_SEG) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: 1..%d matrices", SB_MAX_SEG);
-    const int64_t r_lim = sorted_max_rows(c.ng);
-    if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: ng=%lld unsupported", (long long)c.ng);
     int64_t rmax = 0;
-    for (int s = 0; s < c.nseg; s++) {
-        const int64_t R = c.seg[s].rows_per_chunk;
-        if (R < 1 || R > r_lim)
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: matrix %d: rows_per_chunk=%lld outside 1..%lld", s,
-                             (long long)R, (long long)r_lim);
-        rmax = std::max(rmax, R);
-    }
-    if (c.cb_dt != VQ2_DT_F16 && c.cb_dt != VQ2_DT_BF16)
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: fp16 / bf16 codebooks only");
-    if (c.slices < 1 || c.slices > 64) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: slices must be 1..64");
-    if (top1 && (c.slices != 1 || c.nseg != 1))
-        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM top-1: one matrix, one slice");
+    if (int r = sorted_check_call(c, top1, "vq2 sorted GEMM", &rmax)) return r;
     const int64_t n = c.ng * 8;
     if (c.x_stride < n || c.x_stride % 8 || (uintptr_t)c.x % 16)
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: x must be 16-byte aligned with a row stride >= n, a multiple "
                          "of 8 (got %lld)", (long long)c.x_stride);
-    if ((uintptr_t)c.cb0 % 16 || (c.cb1 && (uintptr_t)c.cb1 % 16))
-        return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: codebooks must be 16-byte aligned");
     const int nb = batch_slots(c.batch);
     // activation (fp16, nb rows) or the row-sum stage, whichever is larger, then the accumulators
     const int64_t x_floats = std::max<int64_t>(n * nb / 2, 2 * 256 * nb);
@@ -460,17 +443,9 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     int64_t wg = 0, n_cnt = 0, nc = 0;
     for (int s = 0; s < c.nseg; s++) {
         const SortedSegCall& sc = c.seg[s];
-        const ChunkSplit ks = chunk_split(sc.out_rows, sc.rows_per_chunk);
+        ChunkSplit ks;
+        if (int r = sorted_check_seg(c, s, "vq2 sorted GEMM", &ks)) return r;
         const int64_t n_chunks = ks.n_chunks;
-        if (sc.n_iters < 1 || sc.n_iters > 0x7FFFFFFF)
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: matrix %d has %lld iterations", s, (long long)sc.n_iters);
-        if ((uintptr_t)sc.entries % 16) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: entries must be 16-byte aligned");
-        if (sc.s2 != (c.cb1 != nullptr)) return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: stage-2 entries need cb1");
-        if (sc.iters_per_chunk < 1 || sc.stage1_iters < 0 || sc.stage1_iters > sc.iters_per_chunk ||
-            sc.iters_per_chunk * n_chunks != sc.n_iters || (!sc.s2 && sc.stage1_iters != sc.iters_per_chunk))
-            return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: matrix %d: %lld iterations are not %lld chunks x %lld "
-                             "(%lld of stage 1)", s, (long long)sc.n_iters, (long long)n_chunks,
-                             (long long)sc.iters_per_chunk, (long long)sc.stage1_iters);
         SortedBatchSeg& d = a.seg[s];
         d.ent = (const u32x4*)sc.entries;
         d.ipc = (int32_t)sc.iters_per_chunk;
