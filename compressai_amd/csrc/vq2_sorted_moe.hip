@@ -70,6 +70,7 @@ struct SortedMoeArgs {
     // its finished workgroups per pair; down waits for gu_arrivals of them
     uint32_t* pair_cnt;
     int gu_arrivals;
+    int id_poll;  // down part of one launch with the router: the pair's (id, weight) is published in the launch
     const void* ids;  // MODE 0 / 2 and the combine: pair experts
     int ids_i64;
     float* part;  // gate_up: [slices][n_pairs][pool.rows] raw row sums; down: [n_pairs][slices][pool.rows] shares
@@ -188,6 +189,19 @@ constexpr int SG_MAX_TOPK = 64;
 constexpr int MOE_CNT_STRIDE = 32;        // uint32 per pair count
 constexpr int MOE_WAIT_POLLS = 1 << 20;   // ~1 s of polls, then the pair's shares turn NaN
 
+// The router's pair (expert id + 1, combine weight) as one 64-bit word in
+// the pair's count line (words 2-3), so a down workgroup can load its entry
+// words while the pair's gate_up workgroups still run; 0 = not yet.
+__device__ __forceinline__ uint64_t* pair_word(const SortedMoeArgs& a, int p)
+{
+    return (uint64_t*)(a.pair_cnt + p * MOE_CNT_STRIDE + 2);
+}
+__device__ __forceinline__ void publish_pair(const SortedMoeArgs& a, int p, uint32_t ex, float w)
+{
+    __hip_atomic_store(pair_word(a, p), ((uint64_t)__float_as_uint(w) << 32) | (uint64_t)(ex + 1u), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int CBT, int MODE, int XT, int F2K, int FUSED>
 __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float* smem)
 {
@@ -196,6 +210,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
     __shared__ float s_topv[SG_MAX_TOPK];
     __shared__ int32_t s_e;
     __shared__ float s_w;
+    __shared__ int s_ok;
     if (bid >= a.wgs) return;  // padding of a fused launch (whole workgroup, before any barrier)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -276,6 +291,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
                 if (lane == 0) {
                     __hip_atomic_store(a.g.r_ids + p, (int32_t)a.g.r_shared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     share_store(a.g.r_w + p, sw);
+                    if constexpr (FUSED) publish_pair(a, p, (uint32_t)a.g.r_shared, sw);
                 }
             }
         } else if (wave == 0) {
@@ -294,6 +310,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
                 if (lane == kslot) {
                     __hip_atomic_store(a.g.r_ids + p, (int32_t)ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     share_store(a.g.r_w + p, mine / tot);
+                    if constexpr (FUSED) publish_pair(a, p, (uint32_t)ex, mine / tot);
                 }
             }
         }
@@ -316,25 +333,24 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         const int64_t gstride = (int64_t)a.n_pairs * a.gu_rows;
         const float* gp = a.gu_part + (int64_t)p * a.gu_rows;
         if constexpr (FUSED) {
-            // wait for the pair's gate_up workgroups; take its expert id and
-            // combine weight (written by the router in the same launch)
+            // the pair's expert id and combine weight: given, or published
+            // by the router's writer in this launch (a bounded poll)
             if (threadIdx.x == 0) {
-                bool ok = false;
-                for (int it = 0; it < MOE_WAIT_POLLS; it++) {
-                    if (__hip_atomic_load(a.pair_cnt + p * MOE_CNT_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
-                        (uint32_t)a.gu_arrivals) {
-                        ok = true;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(10);
-                }
                 int64_t ev = -1;
                 float wv = 0.0f;
-                if (ok) {
-                    ev = a.ids_i64 ? __hip_atomic_load((int64_t*)a.ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                   : (int64_t)__hip_atomic_load((int32_t*)a.ids + p, __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT);
-                    wv = share_load(a.w + p);
+                if (a.id_poll) {
+                    for (int it = 0; it < MOE_WAIT_POLLS; it++) {
+                        const uint64_t v = __hip_atomic_load(pair_word(a, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if ((uint32_t)v != 0u) {
+                            ev = (int64_t)((uint32_t)v - 1u);
+                            wv = __uint_as_float((uint32_t)(v >> 32));
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(10);
+                    }
+                } else {
+                    ev = a.ids_i64 ? ((const int64_t*)a.ids)[p] : (int64_t)((const int32_t*)a.ids)[p];
+                    wv = a.w[p];
                 }
                 s_e = (ev >= 0 && ev < a.n_experts) ? (int32_t)ev : -1;
                 s_w = wv;
@@ -364,13 +380,13 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         };
         const int64_t i0 = threadIdx.x < 2 * n ? threadIdx.x : 0;
         float pv0[8];
-        slice_loads(i0, 0, pv0);  // needs only the pair, not its expert
-        asm volatile("" ::: "memory");
-        if constexpr (FUSED) {
+        if constexpr (!FUSED) {
+            slice_loads(i0, 0, pv0);  // needs only the pair, not its expert
+            asm volatile("" ::: "memory");
+            e = pair_expert(a, p, bad);
+        } else {
             bad = s_e < 0;
             e = bad ? 0 : s_e;
-        } else {
-            e = pair_expert(a, p, bad);
         }
         const uint32_t sc0 = load_raw(a.gu_scale, a.gu_s_dt, e * a.gu_rows + i0);
         // the epilogue's combine weight and row scale, fetched now; both
@@ -381,6 +397,25 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         const int64_t row_e = (int64_t)chunk * pl.rb + min(chunk, pl.nbig) + (own_e ? threadIdx.x : 0);
         dsc = load_raw(pl.scale, pl.s_dt, e * pl.rows + row_e);
         entries(e);
+        if constexpr (FUSED) {
+            // the entry words come while the pair's gate_up workgroups
+            // finish; then their row sums (a bounded poll of the count)
+            if (threadIdx.x == 0) {
+                bool ok = false;
+                for (int it = 0; it < MOE_WAIT_POLLS; it++) {
+                    if (__hip_atomic_load(a.pair_cnt + p * MOE_CNT_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                        (uint32_t)a.gu_arrivals) {
+                        ok = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(10);
+                }
+                s_ok = ok ? 1 : 0;
+            }
+            __syncthreads();
+            bad = bad || s_ok == 0;
+            slice_loads(i0, 0, pv0);
+        }
         sorted_acc_zero(acc, lane, R);
         if (threadIdx.x < 2 * n) finish(threadIdx.x, pv0, raw_as_f32(sc0, a.gu_s_dt));
         for (int64_t i = threadIdx.x + SG_THREADS; i < 2 * n; i += SG_THREADS) {
@@ -469,7 +504,10 @@ __global__ void __launch_bounds__(256) vq_sorted_moe_combine_kernel(const Sorted
 {
     // the fused launch's per-pair counts go back to 0 for the next layer
     if (a.pair_cnt && blockIdx.x == 0 && blockIdx.y == 0)
-        for (int i = threadIdx.x; i < a.n_pairs; i += 256) a.pair_cnt[i * MOE_CNT_STRIDE] = 0u;
+        for (int i = threadIdx.x; i < a.n_pairs; i += 256) {
+            a.pair_cnt[i * MOE_CNT_STRIDE] = 0u;
+            *pair_word(a, i) = 0ull;
+        }
     const int t = blockIdx.y;
     const int rows = a.pool.rows;
     const int part = threadIdx.x & 3;
@@ -754,6 +792,7 @@ int sorted_moe_launch(const SortedMoeCall& c)
         // their pair's gate_up workgroups (counts in the workspace header)
         a.pair_cnt = d.pair_cnt = pair_cnt;
         d.gu_arrivals = (int)(a.pool.C * c.slices_gu);
+        d.id_poll = router ? 1 : 0;
         const unsigned grid = (unsigned)((grid_gu + 7) / 8 * 8 + grid_dn);
         err = router ? launch_fused<1>(c.cb_dt, c.h_dt, a, d, grid, std::max(shm_gu, shm_dn), st)
                      : launch_fused<0>(c.cb_dt, c.h_dt, a, d, grid, std::max(shm_gu, shm_dn), st);
