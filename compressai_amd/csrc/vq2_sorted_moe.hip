@@ -12,7 +12,9 @@
 // Both pools are in the code-sorted layout (vq2_sorted_pack_pool: every
 // expert a matrix of C chunks of R rows, experts one after another), so a
 // wave's 64 centroid gathers share a few codebook lines (vq2_sorted.hip
-// explains the layout).  Three launches, no host synchronisation:
+// explains the layout).  Three launches, no host synchronisation (for
+// hidden 2048 / intermediate 512, parts 1 and 2 are one launch whose down
+// workgroups wait, bounded, on per-pair counts: vq_sorted_moe_fused_kernel):
 //  1. gate_up: one workgroup per (pair, chunk, slice).  The expert comes from
 //     ids (MODE 0) or from the router built in (MODE 1: softmax over the
 //     token's logits, top-k, renormalised; slot k is the shared expert with
