@@ -121,7 +121,7 @@ int gemm_small_m_top1_launch(const GemmCall& c, int64_t* out_idx, float* out_val
 
 // VQ GEMV over the code-sorted internal layout (vq2_sorted.hip).
 struct SortedSegCall {
-    const uint32_t* entries;   // [n_iters * 256], 16-byte aligned
+    const uint32_t* entries;   // [n_iters * 192] (768 bytes per iteration), 16-byte aligned
     int64_t iters_per_chunk;   // every chunk padded to it
     int64_t stage1_iters;      // of which stage 1 (the stage-2 iterations follow)
     int64_t n_iters;

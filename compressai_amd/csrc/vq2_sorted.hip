@@ -12,19 +12,23 @@
 //
 // Layout (built once at load time on the host by vq2_sorted_pack, from the
 // reference's index planes, which stay the public format):
-//  * a matrix is cut into chunks of R rows x all ng groups; an entry is a
-//    uint32 (code << 16) | (row_in_chunk << gbits) | group, gbits =
+//  * a matrix is cut into chunks of R rows x all ng groups, gbits =
 //    ceil(log2 ng) and R <= min(2^(16 - gbits) - 1, 255) rows (chosen at
 //    pack time: the rows split evenly over the chunks), so row R is a dummy
-//    row that padding entries (pos R << gbits, code 0) add to;
+//    row that padding entries add to;
 //  * every wave keeps two accumulator arrays, one per 32-lane half; a
-//    chunk's entries are sorted by code (then position) and dealt into
-//    instructions of 64 entries, one per lane, with no row twice in a half
-//    (an entry whose row both open halves already hold waits for the next
-//    instruction), so the lanes' read-add-write of their row's accumulator
-//    never collide; padding fills the tail;
-//  * 4 instructions form an iteration: lane l holds a uint32x4 whose element
-//    q is entry l of instruction q (one 16-byte load per lane);
+//    chunk's codes are sorted by value (then position) and dealt into
+//    instructions of 64 lanes with no row twice in a half (an entry whose row
+//    both open halves already hold waits for the next instruction), so the
+//    lanes' read-add-write of their row's accumulator never collide;
+//  * lane 63 of an instruction carries its base code (the smallest), the
+//    other 63 lanes one code each as a 24-bit field (code - base) << P | row
+//    << gbits | group (P = gbits + bitlen(R) <= 16); an instruction whose next
+//    code would be 2^(24 - P) or more above its base is closed early;
+//    padding fills the tail;
+//  * 4 instructions form an iteration of 768 bytes: lane l reads 12 bytes
+//    (its four fields' low 16 bits in two words, their high bytes in a
+//    third), so the entry stream is fully coalesced at 3 bytes per code;
 //  * the chunk's stage-1 iterations come first, then its stage-2 iterations
 //    (4 bpw), each stage padded to the matrix's largest count for it (ipc1,
 //    ipc2), so chunk c holds iterations [c * ipc, (c + 1) * ipc), ipc = ipc1
@@ -36,7 +40,7 @@
 // builds the rotated activation in LDS (the fused RHT prologue of the GEMV
 // kernel, or a copy of a pre-rotated x), fp32; every wave owns two LDS
 // accumulators per row of the chunk (2 x (R + 1) floats).  A wave takes iterations
-// of its slice round-robin: one 16-byte entry load, four centroid gathers,
+// of its slice round-robin: one 12-byte entry load, four centroid gathers,
 // then per entry the group's 8 activation values from LDS, the 8-term dot
 // product in fp32 and acc[half][row] += dot.  At the end the waves'
 // accumulators are summed in (wave, half) order: with one slice the rows are complete
@@ -80,12 +84,29 @@ int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
 }
 
 // ------------------------------------------------------------ host repack
+// Whole iterations of padding: every field adds code 0 into the dummy row
+// (position `pad`), the base lane's words hold base code 0.
+static void fill_pad_iters(uint32_t* dst, int64_t iters, uint32_t pad)
+{
+    for (int64_t it = 0; it < iters; it++)
+        for (int l = 0; l < 64; l++) {
+            uint32_t* w = dst + (it * 64 + l) * SG_LANE_WORDS;
+            const uint32_t pp = l == SG_BASE_LANE ? 0u : pad | pad << 16;
+            w[0] = pp;
+            w[1] = pp;
+            w[2] = 0u;
+        }
+}
+
 // Entries of one (chunk, stage) in lane layout: sorted by code, dealt into
-// 64-entry instructions with distinct rows in each lane group sharing an
-// accumulator array, padded to whole iterations.
+// 64-lane instructions (lanes 0-31 and 32-62 in two halves with distinct rows
+// each, lane 63 the instruction's base code) whose codes lie within 2^(24 - P)
+// of the base, padded to whole iterations.
 static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int64_t ng, int gb, int64_t R,
                              std::vector<uint32_t>& out)
 {
+    const int pb = sorted_pbits(gb, (int)R);
+    const uint32_t span = 1u << (24 - pb);  // code offsets below this
     std::vector<uint32_t> keys;
     keys.reserve((size_t)(rows * ng));
     for (int64_t r = 0; r < rows; r++) {
@@ -94,56 +115,89 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
             keys.push_back(((uint32_t)(uint16_t)p[g] << 16) | (uint32_t)((r << gb) | g));
     }
     std::sort(keys.begin(), keys.end());
-    const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
-    std::vector<uint32_t> instr;  // instruction-major, 64 per instruction
-    instr.reserve(keys.size() + 1024);
+    const uint32_t pad = (uint32_t)(R << gb);  // offset 0, dummy row R
+    std::vector<uint32_t> instr;  // instruction-major 24-bit fields, 64 per instruction
+    instr.reserve(keys.size() + keys.size() / 32 + 1024);
     std::vector<uint32_t> pending, still;
     // lane groups of the current instruction that hold each row (valid
     // while stamp[row] == id)
     std::vector<int64_t> stamp((size_t)R + 1, -1);
     std::vector<uint8_t> used((size_t)R + 1, 0);
-    static_assert(SG_PARTS <= 8, "one bit per lane group");
+    static_assert(SG_PARTS == 2 && SG_BASE_LANE == 63, "two halves, the base in the last lane");
+    const int cap[SG_PARTS] = {SG_PART_LANES, SG_PART_LANES - 1};
     size_t next = 0;
     int64_t id = 0;
     while (next < keys.size() || !pending.empty()) {
         uint32_t slot[SG_PARTS][SG_PART_LANES];
         int fill[SG_PARTS] = {};
         int n = 0;
-        // place k in the first open lane group that does not hold its row
-        auto place = [&](uint32_t k) {
+        bool have_base = false;
+        uint32_t base = 0;
+        // place k in the first open lane group that does not hold its row:
+        // 0 placed, 1 its row is in both groups, 2 its code is too far from
+        // the base (every later key's is too: codes ascend)
+        auto place = [&](uint32_t k) -> int {
+            const uint32_t code = k >> 16;
+            if (have_base && code - base >= span) return 2;
             const uint32_t row = (k & 0xFFFFu) >> gb;
             const uint8_t u = stamp[row] == id ? used[row] : 0;
             for (int qd = 0; qd < SG_PARTS; qd++)
-                if (fill[qd] < SG_PART_LANES && !(u & (1u << qd))) {
-                    slot[qd][fill[qd]++] = k;
+                if (fill[qd] < cap[qd] && !(u & (1u << qd))) {
+                    if (!have_base) {
+                        have_base = true;
+                        base = code;
+                    }
+                    slot[qd][fill[qd]++] = ((code - base) << pb) | (k & 0xFFFFu);
                     stamp[row] = id;
                     used[row] = (uint8_t)(u | (1u << qd));
                     n++;
-                    return true;
+                    return 0;
                 }
-            return false;
+            return 1;
         };
+        const int full = cap[0] + cap[1];
+        // entries waiting since an earlier instruction go first (their codes
+        // are the smallest left, in ascending order, so the first one placed
+        // is the instruction's smallest code)
         still.clear();
-        for (uint32_t k : pending)  // entries waiting since an earlier instruction go first
-            if (n == 64 || !place(k)) still.push_back(k);
+        size_t i = 0;
+        for (; i < pending.size() && n < full; i++) {
+            const int r = place(pending[i]);
+            if (r == 2) break;
+            if (r == 1) still.push_back(pending[i]);
+        }
+        const bool closed = i < pending.size() && n < full;
+        for (; i < pending.size(); i++) still.push_back(pending[i]);
         pending.swap(still);
-        while (n < 64 && next < keys.size()) {
-            const uint32_t k = keys[next++];
-            if (!place(k)) pending.push_back(k);
+        while (!closed && n < full && next < keys.size()) {
+            const int r = place(keys[next]);
+            if (r == 2) break;
+            if (r == 1) pending.push_back(keys[next]);
+            next++;
         }
         for (int qd = 0; qd < SG_PARTS; qd++) {
             while (fill[qd] < SG_PART_LANES) slot[qd][fill[qd]++] = pad;
             instr.insert(instr.end(), slot[qd], slot[qd] + SG_PART_LANES);
         }
+        instr.back() = base;  // lane 63: the base code
         id++;
     }
-    while ((instr.size() / 64) % 4) instr.insert(instr.end(), 64, (uint32_t)(R << gb));
+    while ((instr.size() / 64) % 4) {
+        instr.insert(instr.end(), 64, pad);
+        instr.back() = 0u;
+    }
     const size_t iters = instr.size() / SG_ITER;
-    const size_t base = out.size();
-    out.resize(base + iters * SG_ITER);
+    const size_t at = out.size();
+    out.resize(at + iters * SG_ITER_WORDS);
     for (size_t it = 0; it < iters; it++)
-        for (int l = 0; l < 64; l++)
-            for (int q = 0; q < 4; q++) out[base + (it * 64 + l) * 4 + q] = instr[(it * 4 + q) * 64 + l];
+        for (int l = 0; l < 64; l++) {
+            uint32_t f[4];
+            for (int q = 0; q < 4; q++) f[q] = instr[(it * 4 + q) * 64 + l];
+            uint32_t* w = &out[at + (it * 64 + l) * SG_LANE_WORDS];
+            w[0] = (f[0] & 0xFFFFu) | (f[1] & 0xFFFFu) << 16;
+            w[1] = (f[2] & 0xFFFFu) | (f[3] & 0xFFFFu) << 16;
+            w[2] = (f[0] >> 16) | (f[1] >> 16) << 8 | (f[2] >> 16) << 16 | (f[3] >> 16) << 24;
+        }
 }
 
 int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int64_t ng, int64_t R,
@@ -182,8 +236,8 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
     // entries are instead of reading a table
     int64_t ipc1 = 0, ipc2 = 0;
     for (int64_t c = 0; c < n_chunks; c++) {
-        ipc1 = std::max(ipc1, (int64_t)p1[c].size() / SG_ITER);
-        ipc2 = std::max(ipc2, (int64_t)p2[c].size() / SG_ITER);
+        ipc1 = std::max(ipc1, (int64_t)p1[c].size() / SG_ITER_WORDS);
+        ipc2 = std::max(ipc2, (int64_t)p2[c].size() / SG_ITER_WORDS);
     }
     const int64_t ipc = ipc1 + ipc2;
     const int64_t total = ipc * n_chunks;
@@ -196,12 +250,13 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
                          (long long)cap_iters);
     const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
     for (int64_t c = 0; c < n_chunks; c++) {
-        uint32_t* d1 = entries + c * ipc * SG_ITER;
-        uint32_t* d2 = d1 + ipc1 * SG_ITER;
+        uint32_t* d1 = entries + c * ipc * SG_ITER_WORDS;
+        uint32_t* d2 = d1 + ipc1 * SG_ITER_WORDS;
+        const int64_t n1 = (int64_t)p1[c].size() / SG_ITER_WORDS, n2 = (int64_t)p2[c].size() / SG_ITER_WORDS;
         memcpy(d1, p1[c].data(), p1[c].size() * sizeof(uint32_t));
-        std::fill(d1 + p1[c].size(), d2, pad);
+        fill_pad_iters(d1 + n1 * SG_ITER_WORDS, ipc1 - n1, pad);
         memcpy(d2, p2[c].data(), p2[c].size() * sizeof(uint32_t));
-        std::fill(d2 + p2[c].size(), d1 + ipc * SG_ITER, pad);
+        fill_pad_iters(d2 + n2 * SG_ITER_WORDS, ipc2 - n2, pad);
     }
     return VQ2_OK;
 }
@@ -242,7 +297,7 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
         for (auto& t : th) t.join();
     }
     int64_t ipc = 1;
-    for (int64_t u = 0; u < units; u++) ipc = std::max(ipc, (int64_t)parts[u].size() / SG_ITER);
+    for (int64_t u = 0; u < units; u++) ipc = std::max(ipc, (int64_t)parts[u].size() / SG_ITER_WORDS);
     const int64_t total = ipc * units;
     *n_iters = total;
     *iters_per_chunk = ipc;
@@ -252,16 +307,17 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
                          (long long)cap_iters);
     const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
     for (int64_t u = 0; u < units; u++) {
-        uint32_t* dst = entries + u * ipc * SG_ITER;
+        uint32_t* dst = entries + u * ipc * SG_ITER_WORDS;
+        const int64_t nu = (int64_t)parts[u].size() / SG_ITER_WORDS;
         memcpy(dst, parts[u].data(), parts[u].size() * sizeof(uint32_t));
-        std::fill(dst + parts[u].size(), dst + ipc * SG_ITER, pad);
+        fill_pad_iters(dst + nu * SG_ITER_WORDS, ipc - nu, pad);
     }
     return VQ2_OK;
 }
 
 // ------------------------------------------------------------------ kernel
 struct SortedSeg {
-    const u32x4* ent;  // [n_iters * 64] lane words
+    const uint32_t* ent;  // [n_iters * SG_ITER_WORDS] lane words
     int32_t ipc;       // iterations per chunk (chunk c: [c * ipc, (c + 1) * ipc))
     int32_t ipc1;      // its stage-1 iterations (the stage-2 ones follow)
     const void* scale;
@@ -350,7 +406,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
     // two
     SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2> pipe;
-    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
+    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R);
     if constexpr (XM == 0) pipe.gathers();
 
     float* acc = sorted_acc(s_acc, wave, lane, R);
@@ -580,7 +636,7 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         ChunkSplit ks;
         if (int r = sorted_check_seg(c, s, "vq2 sorted GEMV", &ks)) return r;
         const int64_t n_chunks = ks.n_chunks;
-        a.seg[s].ent = (const u32x4*)sc.entries;
+        a.seg[s].ent = sc.entries;
         a.seg[s].ipc = (int32_t)sc.iters_per_chunk;
         a.seg[s].ipc1 = (int32_t)sc.stage1_iters;
         a.seg[s].scale = sc.scale;

@@ -1,12 +1,22 @@
 // vq2_sorted.hpp -- device pieces shared by the kernels over the code-sorted
-// layout (vq2_sorted.hip: dense matrices; vq2_sorted_moe.hip: expert pools).
+// layout (vq2_sorted.hip: dense matrices; vq2_sorted_batch.hip: batch 2-4;
+// vq2_sorted_moe.hip: expert pools).
 //
 // Layout recap (built by vq2_sorted_pack / vq2_sorted_pack_pool): a matrix
-// is cut into chunks of R rows; every code of a chunk is one uint32 entry
-// (code << 16) | (row << gbits) | group, sorted by code and dealt into
-// 64-entry instructions with no row twice in a 32-lane half; 4 instructions
-// form a 1 KiB iteration, lane l reading the 16-byte word l of it; padding
-// entries add code 0 into the dummy row R.
+// is cut into chunks of R rows; the codes of a chunk are sorted by value and
+// dealt into 64-lane instructions with no row twice in a 32-lane half.
+// Lane 63 of an instruction holds no code: it carries the instruction's base
+// code (its smallest).  Every other lane holds a 24-bit field
+//     F = (code - base) << P | row << gbits | group,   P = gbits + bitlen(R),
+// so P <= 16 and the code offset has 24 - P >= 8 bits (the packer closes an
+// instruction early rather than exceed it).  Four instructions form an
+// iteration of 768 bytes: lane l reads the 12 bytes at 12 l, three words
+//     w0 = lo16(F0) | lo16(F1) << 16,  w1 = lo16(F2) | lo16(F3) << 16,
+//     w2 = hi8(F0) | hi8(F1) << 8 | hi8(F2) << 16 | hi8(F3) << 24,
+// and lane 63's w0 / w1 are the four base codes in the same places (w2 = 0).
+// Padding fields add code `base` into the dummy row R (group 0).  3 bytes
+// per code against 2 in the reference planes (4 in the first version of
+// this format, which stored every code in full).
 #pragma once
 
 #include "vq2_gemv_kernel.hpp"
@@ -15,7 +25,10 @@ namespace vq2 {
 
 constexpr int SG_THREADS = 1024;
 constexpr int SG_WAVES = SG_THREADS / 64;
-constexpr int SG_ITER = 256;  // entries per iteration (64 lanes x 4)
+constexpr int SG_ITER = 256;        // entry slots per iteration (64 lanes x 4 instructions)
+constexpr int SG_LANE_WORDS = 3;    // uint32 words per lane and iteration
+constexpr int SG_ITER_WORDS = 64 * SG_LANE_WORDS;  // 768 bytes per iteration
+constexpr int SG_BASE_LANE = 63;    // the lane that carries the instructions' base codes
 constexpr int SG_MAX_R = 255;
 constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
 constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
@@ -44,6 +57,13 @@ __host__ __device__ inline ChunkSplit chunk_split(int64_t rows, int64_t R)
     k.rb = k.n_chunks > 0 ? rows / k.n_chunks : 0;
     k.nbig = k.n_chunks > 0 ? rows % k.n_chunks : 0;
     return k;
+}
+
+// Bits of a field's position part: gbits + bitlen(R) (rows 0..R, R the
+// dummy row); at most 16 when R <= sorted_max_rows(ng).
+__host__ __device__ inline int sorted_pbits(int gbits, int R)
+{
+    return gbits + (32 - __builtin_clz((unsigned)R));
 }
 
 // Largest chunk height for ng groups: row R is the dummy row, so
@@ -378,44 +398,88 @@ __device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, u
     return d;
 }
 
-// One wave's pass over iterations [s0, s1) of a chunk (stride W, the waves of the workgroup,
-// starting at s0 + wave), stage-2 entries from c_mid on.  load_entries()
-// issues the first three (GD 3: four) iterations' entry words and gathers()
-// the first GD iterations' centroid gathers (iterations at or past s1 are
-// clamped to the chunk's first, whose lines are cached), so a caller can put
-// a prologue between them, or before both.  run() keeps entry words that far
-// ahead and gathers GD ahead of the arithmetic until the last GD iterations,
-// which it finishes from the gathers already in flight (no loads past the
-// range).  Loads complete in issue order and no branch separates them, so
-// each wait covers exactly the values it needs.
+// One lane's entry words of an iteration (SG_LANE_WORDS = 3; a 3-element
+// vector type would be read as 16 bytes).
+struct Ent3 {
+    uint32_t w[SG_LANE_WORDS];
+};
+
+// One wave's pass over iterations [s0, s1) of a chunk (stride W, the waves of
+// the workgroup, starting at s0 + wave), stage-2 entries from c_mid on.
+// load_entries() issues the first three (GD 3: four) iterations' entry words
+// and gathers() the first GD iterations' centroid gathers (iterations at or
+// past s1 are clamped to the chunk's first, whose lines are cached), so a
+// caller can put a prologue between them, or before both.  run() keeps entry
+// words that far ahead and gathers GD ahead of the arithmetic until the last
+// GD iterations, which it finishes from the gathers already in flight (no
+// loads past the range).  Loads complete in issue order and no branch
+// separates them, so each wait covers exactly the values it needs.
+// A gather reads the iteration's four base codes from lane SG_BASE_LANE
+// (v_readlane: scalar registers, no memory access) and adds each lane's
+// offset; a code is taken mod 65536, so no entry word can address outside
+// the codebook.
 template <int CBT, int GD = 2, int W = SG_WAVES>
 struct SortedPipe {
     static_assert(GD >= 1 && GD <= 3, "gather depth 1 to 3");
     static constexpr int NE = GD + 1 > 3 ? GD + 1 : 3;  // entry words held: iterations it .. it + (NE - 1) W
-    const u32x4* ent;
+    const uint32_t* ent;
     const u32x4* cb0;
     const u32x4* cb1;
     int c_beg, c_mid, s1, lane;
     int it;
-    int ie[NE];       // the (clamped) iterations of the entry words
-    u32x4 e[NE];
-    u32x4 c[GD][4];   // centroids of iterations it .. it + (GD - 1) W
+    uint32_t pb;     // position bits P of a field
+    uint32_t dummy;  // the dummy row's position, R << gbits
+    int ie[NE];      // the (clamped) iterations of the entry words
+    Ent3 e[NE];
+    u32x4 c[GD][4];  // centroids of iterations it .. it + (GD - 1) W
 
     __device__ __forceinline__ int clampit(int i) const { return i < s1 ? i : c_beg; }
-    __device__ __forceinline__ u32x4 load_e(int i) const
+    __device__ __forceinline__ Ent3 load_e(int i) const
     {
-        return __builtin_nontemporal_load(ent + (int64_t)i * 64 + lane);
+        typedef const __attribute__((address_space(1))) uint32_t* gp;
+        const gp p = (gp)(ent + ((int64_t)i * 64 + lane) * SG_LANE_WORDS);
+        Ent3 v;
+#pragma unroll
+        for (int k = 0; k < SG_LANE_WORDS; k++) v.w[k] = __builtin_nontemporal_load(p + k);
+        return v;
     }
-    __device__ __forceinline__ void gather(int i, const u32x4& ew, u32x4 (&cw)[4]) const
+    // the low 16 bits of field q (its position, and for P < 16 the low bits
+    // of its code offset) and the whole 24-bit field
+    static __device__ __forceinline__ uint32_t lo16(const Ent3& ew, int q)
+    {
+        const uint32_t d = ew.w[q >> 1];
+        return (q & 1) ? d >> 16 : d & 0xFFFFu;
+    }
+    static __device__ __forceinline__ uint32_t field(const Ent3& ew, int q)
+    {
+        return lo16(ew, q) | (((ew.w[2] >> (8 * q)) & 0xFFu) << 16);
+    }
+    __device__ __forceinline__ void gather(int i, const Ent3& ew, u32x4 (&cw)[4]) const
     {
         const u32x4* cb = i < c_mid ? cb0 : cb1;
+        const uint32_t b01 = (uint32_t)__builtin_amdgcn_readlane((int)ew.w[0], SG_BASE_LANE);
+        const uint32_t b23 = (uint32_t)__builtin_amdgcn_readlane((int)ew.w[1], SG_BASE_LANE);
 #pragma unroll
-        for (int q = 0; q < 4; q++) cw[q] = cb[ew[q] >> 16];
+        for (int q = 0; q < 4; q++) {
+            const uint32_t bw = q < 2 ? b01 : b23;
+            const uint32_t base = (q & 1) ? bw >> 16 : bw & 0xFFFFu;
+            cw[q] = cb[(base + (field(ew, q) >> pb)) & 0xFFFFu];
+        }
+    }
+    // the four positions (row << gbits | group) of this lane's entries;
+    // the base lane's are the dummy row's
+    __device__ __forceinline__ u32x4 positions(const Ent3& ew) const
+    {
+        const uint32_t pmask = (1u << pb) - 1u;
+        u32x4 p;
+#pragma unroll
+        for (int q = 0; q < 4; q++) p[q] = lane == SG_BASE_LANE ? dummy : lo16(ew, q) & pmask;
+        return p;
     }
     // a missing stage-2 codebook is never selected for a real entry; cb0
     // stands in so that no gather can use a null base
-    __device__ __forceinline__ void load_entries(const u32x4* ent_, const void* cb0_, const void* cb1_, int c_beg_,
-                                                 int c_mid_, int s0, int s1_, int wave, int lane_)
+    __device__ __forceinline__ void load_entries(const uint32_t* ent_, const void* cb0_, const void* cb1_, int c_beg_,
+                                                 int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R)
     {
         ent = ent_;
         cb0 = (const u32x4*)cb0_;
@@ -424,6 +488,8 @@ struct SortedPipe {
         c_mid = c_mid_;
         s1 = s1_;
         lane = lane_;
+        pb = (uint32_t)sorted_pbits(gbits, R);
+        dummy = (uint32_t)R << gbits;
         it = s0 + wave;
 #pragma unroll
         for (int d = 0; d < NE; d++) {
@@ -436,13 +502,13 @@ struct SortedPipe {
 #pragma unroll
         for (int d = 0; d < GD; d++) gather(ie[d], e[d], c[d]);
     }
-    __device__ __forceinline__ void start(const u32x4* ent_, const void* cb0_, const void* cb1_, int c_beg_,
-                                          int c_mid_, int s0, int s1_, int wave, int lane_)
+    __device__ __forceinline__ void start(const uint32_t* ent_, const void* cb0_, const void* cb1_, int c_beg_,
+                                          int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R)
     {
-        load_entries(ent_, cb0_, cb1_, c_beg_, c_mid_, s0, s1_, wave, lane_);
+        load_entries(ent_, cb0_, cb1_, c_beg_, c_mid_, s0, s1_, wave, lane_, gbits, R);
         gathers();
     }
-    __device__ __forceinline__ void shift(const u32x4& enew, int inew)
+    __device__ __forceinline__ void shift(const Ent3& enew, int inew)
     {
 #pragma unroll
         for (int d = 0; d + 1 < NE; d++) {
@@ -455,11 +521,11 @@ struct SortedPipe {
     __device__ __forceinline__ void accumulate(float* acc, const float* x, uint32_t gbits, uint32_t gmax, uint32_t R)
     {
         const uint32_t gmask = (1u << gbits) - 1u;
+        const u32x4 pos = positions(e[0]);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const uint32_t pos = e[0][q] & 0xFFFFu;
-            const uint32_t r = min(pos >> gbits, R);
-            const uint32_t g = min(pos & gmask, gmax);
+            const uint32_t r = min(pos[q] >> gbits, R);
+            const uint32_t g = min(pos[q] & gmask, gmax);
             acc[r] += centroid_dot<CBT>(c[0][q], x, g);
         }
     }
@@ -470,7 +536,7 @@ struct SortedPipe {
         // iterations whose gathers GD ahead are real
         for (; it + GD * W < s1; it += W) {
             const int inew = clampit(it + NE * W);
-            const u32x4 enew = load_e(inew);
+            const Ent3 enew = load_e(inew);
             u32x4 cn[4];  // the gathers GD iterations ahead
             gather(ie[GD], e[GD], cn);
             accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R);
@@ -496,16 +562,16 @@ struct SortedPipe {
         }
     }
     // run() with the arithmetic of an iteration given by the caller:
-    // f(entry words, their four centroids)
+    // f(the four positions of this lane's entries, their four centroids)
     template <class F>
     __device__ __forceinline__ void run_each(F&& f)
     {
         for (; it + GD * W < s1; it += W) {
             const int inew = clampit(it + NE * W);
-            const u32x4 enew = load_e(inew);
+            const Ent3 enew = load_e(inew);
             u32x4 cn[4];
             gather(ie[GD], e[GD], cn);
-            f(e[0], c[0]);
+            f(positions(e[0]), c[0]);
             shift(enew, inew);
 #pragma unroll
             for (int d = 0; d + 1 < GD; d++)
@@ -517,7 +583,7 @@ struct SortedPipe {
 #pragma unroll
         for (int k = 0; k < GD; k++) {
             if (it >= s1) break;
-            f(e[0], c[0]);
+            f(positions(e[0]), c[0]);
             shift(e[NE - 1], ie[NE - 1]);
 #pragma unroll
             for (int d = 0; d + 1 < GD; d++)

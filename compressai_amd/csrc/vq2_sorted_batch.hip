@@ -58,7 +58,7 @@ struct AccVec<4> {
 };
 
 struct SortedBatchSeg {
-    const u32x4* ent;
+    const uint32_t* ent;
     int32_t ipc, ipc1;
     const void* scale;
     void* y;        // [batch][out_rows]
@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     // from L2 meanwhile.  Gathers one iteration ahead (measured, LM head at
     // batch 2 / 4: 67.9 / 144.6 us; two ahead 68.8 / 144.9, three 70.9 / 154.8)
     SortedPipe<CBT, 1, SB_WAVES> pipe;
-    pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane);
+    pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R);
 
     accv* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
     for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = (accv)0.0f;
@@ -247,10 +247,10 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     __syncthreads();
 
     const uint32_t gmask = (1u << a.gbits) - 1u, gmax = (uint32_t)(a.ng - 1);
-    pipe.run_each([&](const u32x4& ew, const u32x4 (&cw)[4]) {
+    pipe.run_each([&](const u32x4& pos, const u32x4 (&cw)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const uint32_t p = ew[q] & 0xFFFFu;
+            const uint32_t p = pos[q];
             const uint32_t r = min(p >> a.gbits, (uint32_t)R);
             const uint32_t g = min(p & gmask, gmax);
             float d[NB];
@@ -447,7 +447,7 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         if (int r = sorted_check_seg(c, s, "vq2 sorted GEMM", &ks)) return r;
         const int64_t n_chunks = ks.n_chunks;
         SortedBatchSeg& d = a.seg[s];
-        d.ent = (const u32x4*)sc.entries;
+        d.ent = sc.entries;
         d.ipc = (int32_t)sc.iters_per_chunk;
         d.ipc1 = (int32_t)sc.stage1_iters;
         d.scale = sc.scale;

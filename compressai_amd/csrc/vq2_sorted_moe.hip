@@ -39,7 +39,7 @@
 namespace vq2 {
 
 struct SortedPoolArgs {
-    const u32x4* ent;
+    const uint32_t* ent;
     const void* scale;  // [n_experts, rows]
     int32_t ipc;        // iterations per chunk (every chunk padded to it)
     int s_dt;
@@ -262,7 +262,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
         const int s0 = c_beg + slice * a.sq + min(slice, a.sr);
         const int s1 = s0 + a.sq + (slice < a.sr ? 1 : 0);
-        pipe.load_entries(pl.ent, a.cb, nullptr, c_beg, c_beg + pl.ipc, s0, s1, wave, lane);
+        pipe.load_entries(pl.ent, a.cb, nullptr, c_beg, c_beg + pl.ipc, s0, s1, wave, lane, pl.gbits, R);
     };
     float* acc = sorted_acc(s_acc, wave, lane, R);
     bool bad = false;
@@ -624,7 +624,7 @@ static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_exper
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: entries (16-byte aligned) and scales are required",
                          name);
     if (!dt_ok(pc.scale_dt)) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: bad scale dtype", name);
-    pa.ent = (const u32x4*)pc.entries;
+    pa.ent = pc.entries;
     pa.ipc = (int32_t)pc.iters_per_chunk;
     pa.scale = pc.scale;
     pa.s_dt = pc.scale_dt;

@@ -349,6 +349,11 @@ def vq_gemv_rht(x, mats, cb0, cb1, n, perm=None, sign=None, hb=2048, rht_scale=N
 
 
 # ------------------------------------------------------- code-sorted layout
+# uint32 words per iteration of the sorted layout: 64 lanes x 12 bytes, the
+# four 64-lane instructions of 63 codes and one base code each
+ITER_WORDS = 192
+
+
 class SortedPlanes:
     """Code-sorted internal layout of one VQ matrix (vq2_sorted_pack): the
     reference's int16 index planes (2 bpw, or the two planes of (16,16)
@@ -384,10 +389,12 @@ class SortedPlanes:
         h0 = i0.detach().to("cpu").contiguous()
         h1 = None if i1 is None else i1.detach().to("cpu").contiguous()
         stages = 2 if h1 is not None else 1
-        cap = self.n_chunks * stages * (-(-R * ng // 256) + 8)
+        # 252 codes per iteration (lane 63 of an instruction holds its base
+        # code), a few instructions more where the packer closes one early
+        cap = self.n_chunks * stages * (-(-R * ng // 240) + 8)
         ipc, ipc1, n_iters = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
         for _ in range(2):
-            entries = torch.empty(cap * 256, dtype=torch.int32)
+            entries = torch.empty(cap * ITER_WORDS, dtype=torch.int32)
             st = lib.vq2_sorted_pack(h0.data_ptr(), None if h1 is None else h1.data_ptr(), out_rows, ng, R,
                                      entries.data_ptr(), cap, ctypes.byref(ipc), ctypes.byref(ipc1),
                                      ctypes.byref(n_iters), int(threads))
@@ -399,8 +406,8 @@ class SortedPlanes:
         self.n_iters = int(n_iters.value)
         # every chunk holds iters_per_chunk iterations, stage1_iters of stage 1
         self.iters_per_chunk, self.stage1_iters = int(ipc.value), int(ipc1.value)
-        # uint32 entries held in an int32 tensor (same bits)
-        self.entries = entries[: self.n_iters * 256].to(dev)
+        # uint32 entry words held in an int32 tensor (same bits)
+        self.entries = entries[: self.n_iters * ITER_WORDS].to(dev)
         self.device = dev
 
     def mat(self, scale, y=None) -> "_lib.SortedMat":
@@ -629,11 +636,11 @@ class SortedPool:
         self.chunks = -(-rows // R)
         dev = torch.device(device) if device is not None else idx.device
         h = idx.detach().to("cpu").contiguous()
-        cap = E * self.chunks * (-(-R * ng // 256) + 8)
+        cap = E * self.chunks * (-(-R * ng // 240) + 8)
         ipc = ctypes.c_int64(0)
         n_iters = ctypes.c_int64(0)
         for _ in range(2):
-            entries = torch.empty(cap * 256, dtype=torch.int32)
+            entries = torch.empty(cap * ITER_WORDS, dtype=torch.int32)
             st = lib.vq2_sorted_pack_pool(h.data_ptr(), E, rows, ng, R, entries.data_ptr(), cap, ctypes.byref(ipc),
                                           ctypes.byref(n_iters), int(threads))
             if st == _lib.ERR_ARG and n_iters.value > cap:
@@ -643,7 +650,7 @@ class SortedPool:
             break
         self.n_iters = int(n_iters.value)
         self.iters_per_chunk = int(ipc.value)
-        self.entries = entries[: self.n_iters * 256].to(dev)
+        self.entries = entries[: self.n_iters * ITER_WORDS].to(dev)
         self.device = dev
 
     def pool(self, scale) -> "_lib.SortedPool":

@@ -331,17 +331,22 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  *   chunk_align chunks when the chunks keep >= 128 rows, e.g. chunk_align =
  *   the CU count) of near-equal height: chunk c holds rows
  *   [c * rb + min(c, nbig), + rb + (c < nbig)), rb = out_rows / n_chunks,
- *   nbig = out_rows % n_chunks; every entry
- *   is a uint32 (code << 16) | (row_in_chunk << ceil(log2 ng)) | group; a
- *   chunk's entries are sorted by code and dealt into 64-entry instructions
- *   in which no row repeats within a 32-lane half; 4 instructions form an
- *   iteration of 256 entries (lane l holds entry l of each, as one
- *   uint32x4); every chunk's stage-1 and stage-2 entries are padded (dummy
- *   row, code 0) to the matrix's largest stage-1 / stage-2 iteration
- *   counts, so chunk c holds iterations [c * ipc, (c + 1) * ipc), its
- *   stage-2 ones from c * ipc + stage1_iters on.
+ *   nbig = out_rows % n_chunks; a chunk's codes are sorted by value and
+ *   dealt into 64-lane instructions in which no row repeats within a
+ *   32-lane half (lanes 0-31, 32-62); lane 63 carries the instruction's
+ *   base code (its smallest), every other lane one code as the 24-bit field
+ *   (code - base) << P | row_in_chunk << ceil(log2 ng) | group, P =
+ *   ceil(log2 ng) + bitlen(rows_per_chunk) <= 16 (an instruction is closed
+ *   before an offset would reach 2^(24 - P)); 4 instructions form an
+ *   iteration of 192 uint32 (768 bytes): lane l's three words at 3 l are
+ *   lo16(F0) | lo16(F1) << 16, lo16(F2) | lo16(F3) << 16 and the four
+ *   fields' high bytes (lane 63: the four base codes, then 0); every
+ *   chunk's stage-1 and stage-2 entries are padded (dummy row, offset 0) to
+ *   the matrix's largest stage-1 / stage-2 iteration counts, so chunk c
+ *   holds iterations [c * ipc, (c + 1) * ipc), its stage-2 ones from
+ *   c * ipc + stage1_iters on.  3 bytes per code.
  * vq2_sorted_pack (host memory, no GPU work) fills `entries` (up to
- * cap_iters * 256 uint32, 16-byte aligned) and sets *iters_per_chunk
+ * cap_iters * 192 uint32, 16-byte aligned) and sets *iters_per_chunk
  * (ipc), *stage1_iters and *n_iters = n_chunks * ipc, n_chunks =
  * ceil(out_rows / rows_per_chunk) (also when the capacity is too small,
  * which returns VQ2_ERR_ARG).  idx1 (the (16,16) stage-2 plane) may be NULL; n_threads
@@ -439,7 +444,7 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
  * vq2_sorted_pack_pool (host memory, no GPU work) packs an expert pool
  * idx [n_experts, rows, ng] (one int16 plane, 2 bpw) expert by expert, each
  * as vq2_sorted_pack packs a matrix with the same rows_per_chunk R, and pads
- * every chunk (dummy-row entries, code 0) to the pool's largest iteration
+ * every chunk (dummy-row entries) to the pool's largest iteration
  * count *iters_per_chunk, so chunk c of expert e holds iterations
  * [(e * C + c) * ipc, (e * C + c + 1) * ipc), C = ceil(rows / R).
  * *n_iters = n_experts * C * ipc; capacity as vq2_sorted_pack.  No

@@ -2,8 +2,16 @@
 CPU: every code of the planes appears exactly once in its chunk, with its row
 and group; no row repeats inside a 32-lane half of an instruction (each
 half read-add-writes its own accumulator array, so the kernel relies on
-it); padding is the dummy row; and the instructions are sorted enough that
-a wave's 64 gathers touch few codebook lines."""
+it); lane 63 carries the instruction's smallest code and every offset fits
+its field; padding is the dummy row at offset 0; and the instructions are
+sorted enough that a wave's 64 gathers touch few codebook lines.
+
+Format (3 bytes per code): an iteration is 64 lanes x 3 uint32; lane l
+holds four 24-bit fields F_q = lo16_q | hi8_q << 16 (q = the iteration's
+instruction), words lo16_0 | lo16_1 << 16, lo16_2 | lo16_3 << 16 and
+hi8_0 | hi8_1 << 8 | hi8_2 << 16 | hi8_3 << 24.  Lane 63's lo16_q is the
+base code of instruction q; every other field is
+(code - base) << P | row << gbits | group, P = gbits + bitlen(R)."""
 import ctypes
 
 import numpy as np
@@ -11,46 +19,74 @@ import pytest
 import torch
 
 from compressai_amd import _lib, synth
-from compressai_amd.kernels import SortedPlanes, Vq2Error
+from compressai_amd.kernels import ITER_WORDS, SortedPlanes, Vq2Error
+
 
 def _gb(ng):
     return int(np.ceil(np.log2(ng))) if ng > 1 else 0
 
 
-def _is_pad(v, sp):
-    gb = _gb(sp.n // 8)
-    return (v & 0xFFFF) == (sp.rows_per_chunk << gb)
+def _pb(ng, R):
+    return _gb(ng) + int(R).bit_length()
+
+
+def _fields(words):
+    """uint32 [iters * 192] -> (F [iters, 64, 4] 24-bit fields, lo16, hi8)."""
+    w = words.reshape(-1, 64, 3).astype(np.uint32)
+    lo = np.stack([w[..., 0] & 0xFFFF, w[..., 0] >> 16, w[..., 1] & 0xFFFF, w[..., 1] >> 16], axis=-1)
+    hi = np.stack([(w[..., 2] >> (8 * q)) & 0xFF for q in range(4)], axis=-1)
+    return lo | (hi << 16), lo, hi
+
+
+def _decode_words(words, ng, R):
+    """Per instruction (iteration-major, then q): (codes [63], positions [63],
+    base, offsets [63])."""
+    F, lo, hi = _fields(words)
+    pb = _pb(ng, R)
+    assert np.all(hi[:, 63, :] == 0)  # the base lane's high bytes are zero
+    out = []
+    for it in range(F.shape[0]):
+        for q in range(4):
+            f = F[it, :63, q]
+            base = int(lo[it, 63, q])
+            off = f >> pb
+            assert np.all(off < (1 << (24 - pb)))
+            out.append(((base + off) & 0xFFFF, f & ((1 << pb) - 1), base, off))
+    return out
 
 
 def _decode(sp: SortedPlanes):
-    """Per chunk and stage: list of instructions, each a (64,) uint32 array."""
-    ent = sp.entries.cpu().numpy().view(np.uint32).reshape(-1, 64, 4)  # [iter][lane][q]
+    """Per chunk and stage: list of instructions as _decode_words gives them."""
+    words = sp.entries.cpu().numpy().view(np.uint32)
     ipc, ipc1 = sp.iters_per_chunk, sp.stage1_iters
+    ng, R = sp.n // 8, sp.rows_per_chunk
     out = []
     for c in range(sp.n_chunks):
         stages = []
         for a, b in ((c * ipc, c * ipc + ipc1), (c * ipc + ipc1, (c + 1) * ipc)):
-            stages.append([ent[it][:, q] for it in range(a, b) for q in range(4)])
+            stages.append(_decode_words(words[a * ITER_WORDS:b * ITER_WORDS], ng, R))
         out.append(stages)
     return out
 
 
 @pytest.mark.parametrize("rows,n,bpw", [(300, 2048, 2), (256, 2048, 4), (100, 6144, 4), (1000, 512, 2),
-                                        (97, 800, 2), (5, 64, 4)])
+                                        (97, 800, 2), (5, 64, 4), (1, 2048, 2), (3, 16, 2)])
 def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
     ng = n // 8
     m = synth.vq_matrix(9800 + rows + bpw, rows, n, bpw=bpw)
     sp = SortedPlanes(m["idx0"], m["idx1"], rows, n, device="cpu", threads=3)
     R = int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1))
     gb = _gb(ng)
-    assert sp.rows_per_chunk == R and (R + 1) * (1 << gb) <= 1 << 16
+    assert sp.rows_per_chunk == R and (R + 1) * (1 << gb) <= 1 << 16 and _pb(ng, R) <= 16
     assert sp.n_chunks == -(-rows // R) and R <= 255
     assert R * sp.n_chunks - rows < sp.n_chunks      # the rows split evenly over the chunks
     assert rows // sp.n_chunks + (1 if rows % sp.n_chunks else 0) <= R
     assert sp.n_iters == sp.n_chunks * sp.iters_per_chunk                 # chunks padded to one size
+    assert sp.entries.numel() == sp.n_iters * ITER_WORDS
     assert 0 < sp.stage1_iters <= sp.iters_per_chunk
     assert (sp.stage1_iters < sp.iters_per_chunk) == (bpw == 4)
     planes = [m["idx0"].numpy().view(np.uint16)] + ([m["idx1"].numpy().view(np.uint16)] if bpw == 4 else [])
+    dummy = R << gb
     for c, stages in enumerate(_decode(sp)):
         rb, nbig = rows // sp.n_chunks, rows % sp.n_chunks    # near-equal chunks: heights rb + 1 then rb
         r0 = c * rb + min(c, nbig)
@@ -59,42 +95,46 @@ def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
             if st >= len(planes):
                 assert not instrs
                 continue
-            allv = np.concatenate(instrs) if instrs else np.zeros(0, np.uint32)
-            real = allv[~_is_pad(allv, sp)]
-            pad = allv[_is_pad(allv, sp)]
-            assert np.all(pad >> 16 == 0)  # padding gathers code 0
-            code, pos = real >> 16, real & 0xFFFF
-            r, g = pos >> gb, pos & ((1 << gb) - 1)
+            assert len(instrs) % 4 == 0
+            codes = np.concatenate([i[0] for i in instrs])
+            pos = np.concatenate([i[1] for i in instrs])
+            real = pos != dummy
+            assert np.all(np.concatenate([i[3] for i in instrs])[~real] == 0)  # padding: offset 0
+            code, p = codes[real], pos[real]
+            r, g = p >> gb, p & ((1 << gb) - 1)
             assert np.all(r < r1 - r0) and np.all(g < ng)
             got = np.zeros((r1 - r0, ng), np.int64) - 1
-            assert len(real) == (r1 - r0) * ng          # every code exactly once ...
+            assert len(code) == (r1 - r0) * ng          # every code exactly once ...
             got[r, g] = code
             assert np.array_equal(got, planes[st][r0:r1].astype(np.int64))  # ... at its row and group
-            for ins in instrs:
-                for qd in range(2):                      # no row twice in a 32-lane half
-                    qv = ins[32 * qd:32 * qd + 32]
-                    rr = (qv[~_is_pad(qv, sp)] & 0xFFFF) >> gb
+            for cd, ps, base, off in instrs:
+                rl = ps != dummy
+                if rl.any():
+                    assert base == cd[rl].min()           # the base is the instruction's smallest code
+                for lo, hi in ((0, 32), (32, 63)):        # no row twice in a 32-lane half (lane 63: the base)
+                    rr = ps[lo:hi][ps[lo:hi] != dummy] >> gb
                     assert len(np.unique(rr)) == len(rr)
-            assert len(instrs) % 4 == 0
 
 
 def test_sorted_pack_keeps_instructions_within_few_lines():
-    """At the gate/up shape (6144 x 2048, 4 bpw) a 64-entry instruction of a
-    255-row chunk (65280 codes) spans ~8-10 128-byte codebook lines (8 fp16
-    centroids per line) instead of the ~64 of unsorted codes."""
+    """At the gate/up shape (6144 x 2048, 4 bpw) a 63-code instruction of a
+    246-row chunk (~63000 codes) spans ~8-10 128-byte codebook lines (8 fp16
+    centroids per line) instead of the ~64 of unsorted codes; lane 63 gathers
+    the base code's line, which lane 0 reads too."""
     rows, n = 6144, 2048
     m = synth.vq_matrix(9900, rows, n, bpw=4)
     sp = SortedPlanes(m["idx0"], m["idx1"], rows, n, device="cpu")
+    dummy = sp.rows_per_chunk << _gb(n // 8)
     lines = []
     for stages in _decode(sp)[:8]:
         for instrs in stages:
-            for ins in instrs:
-                real = ins[~_is_pad(ins, sp)]
-                if len(real) == 64:
-                    lines.append(len(np.unique((real >> 16) >> 3)))
+            for cd, ps, base, off in instrs:
+                if np.all(ps != dummy):
+                    lines.append(len(np.unique(np.append(cd, base) >> 3)))
     assert 6 <= np.mean(lines) <= 12, np.mean(lines)
     print("mean codebook lines per instruction:", np.mean(lines))
-    assert sp.n_iters <= 1.02 * (rows * n // 8 * 2) / 256  # little padding
+    assert sp.n_iters <= 1.02 * (rows * n // 8 * 2) / 252  # little padding
+    assert sp.entries.numel() * 4 <= 3.1 * rows * n // 8 * 2  # ~3 bytes per code
 
 
 def test_sorted_pack_rejects_bad_input():
@@ -105,7 +145,7 @@ def test_sorted_pack_rejects_bad_input():
         SortedPlanes(m["idx0"], None, 17, 512, device="cpu")      # wrong row count
     L = _lib.load()
     n_it, ipc, ipc1 = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
-    buf = torch.empty(256, dtype=torch.int32)
+    buf = torch.empty(ITER_WORDS, dtype=torch.int32)
     st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 16, buf.data_ptr(), 1, ctypes.byref(ipc),
                            ctypes.byref(ipc1), ctypes.byref(n_it), 1)
     assert st == _lib.ERR_ARG and n_it.value > 1   # capacity too small: the needed size is reported
@@ -128,7 +168,8 @@ def test_sorted_rows_per_chunk_alignment():
 def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
     """vq2_sorted_pack_pool lays the experts out one after another, each
     chunk exactly as vq2_sorted_pack packs it alone, then padded with
-    dummy-row entries (code 0) to the pool's common iteration count."""
+    dummy-row iterations (offset 0, base code 0) to the pool's common
+    iteration count."""
     from compressai_amd.kernels import SortedPool
 
     ng = n // 8
@@ -140,7 +181,9 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
     assert pool.n_iters == E * C * ipc
     ent = pool.entries.numpy().view(np.uint32)
     pad = np.uint32(R << _gb(ng))
+    pad_lane = np.array([pad | (pad << 16), pad | (pad << 16), 0], np.uint32)
     longest = 0
+    W = ITER_WORDS
     for e in range(E):
         sp = SortedPlanes(idx[e], None, rows, n, device="cpu", chunk_align=1)
         assert sp.rows_per_chunk == R and sp.n_chunks == C
@@ -148,9 +191,10 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
         own = sp.entries.numpy().view(np.uint32)
         longest = max(longest, ipe)
         for c in range(C):
-            got = ent[(e * C + c) * ipc * 256:(e * C + c + 1) * ipc * 256]
-            assert np.array_equal(got[: ipe * 256], own[c * ipe * 256:(c + 1) * ipe * 256])
-            assert np.all(got[ipe * 256:] == pad)
+            got = ent[(e * C + c) * ipc * W:(e * C + c + 1) * ipc * W]
+            assert np.array_equal(got[: ipe * W], own[c * ipe * W:(c + 1) * ipe * W])
+            tail = got[ipe * W:].reshape(-1, 64, 3)
+            assert np.all(tail[:, :63] == pad_lane) and np.all(tail[:, 63] == 0)
     assert ipc == longest
 
 
