@@ -124,6 +124,23 @@ def _idx16(t: torch.Tensor, what: str) -> torch.Tensor:
     return _contig(t, what)
 
 
+def _perm_sign(perm, sign, n, what="") -> None:
+    """The kernels read n entries of each rotation table: perm int32 [n],
+    sign int8 [n], contiguous (either may be None)."""
+    for t, nm, dt in ((perm, "perm", torch.int32), (sign, "sign", torch.int8)):
+        if t is not None and (t.dtype != dt or t.numel() != n or not t.is_contiguous()):
+            raise Vq2Error(f"{what}{nm} must be a contiguous {dt} [{n}]")
+
+
+def _gate_vec(gate, n, what="shared_gate") -> torch.Tensor:
+    """A shared-expert gate vector: n contiguous fp32 / fp16 / bf16 values."""
+    _contig(gate, what)
+    if gate.numel() != n:
+        raise Vq2Error(f"{what} must hold {n} values, got {gate.numel()}")
+    _dt(gate, what)
+    return gate
+
+
 def _ids(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     if t.dtype == torch.int32:
         return _contig(t, "topk_ids"), _lib.ID_I32
@@ -688,6 +705,16 @@ def moe_slices(units, codes_per_unit, cu, fixed_us, one_launch=False):
     return best
 
 
+def _rot_tables(rot, n, what):
+    """A rotation (perm int32 [n] or None, sign int8 [n] or None, hb, scale)
+    checked for the kernels, which read n entries of each table."""
+    if len(rot) != 4:
+        raise Vq2Error(f"{what} must be (perm, sign, hb, scale)")
+    perm, sign, hb, sc = rot
+    _perm_sign(perm, sign, n, what + " ")
+    return _lib.RotTables(_p(perm), _p(sign), int(hb), float(sc))
+
+
 def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, cb, rot_h, rot_i, *, ids=None,
                   w=None, logits=None, top_k=None, shared_id=None, shared_gate=None, out_dtype=torch.float32,
                   out=None, slices=None):
@@ -705,7 +732,14 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         raise Vq2Error("vq_sorted_moe: inconsistent gate_up / down pools")
     h2 = _contig(h, "h").reshape(-1, H)
     T = h2.shape[0]
-    dev = _dev(h2, cb, gu_scale, dn_scale, ids, w, logits, gate_up.entries, down.entries)
+    rh = _rot_tables(rot_h, H, "rot_h")
+    ri = _rot_tables(rot_i, I, "rot_i")
+    if logits is not None:
+        if shared_gate is None or shared_id is None or top_k is None:
+            raise Vq2Error("vq_sorted_moe: the built-in router needs top_k, shared_id and shared_gate")
+        _gate_vec(shared_gate, H)
+    dev = _dev(h2, cb, gu_scale, dn_scale, ids, w, logits, gate_up.entries, down.entries, rot_h[0], rot_h[1],
+               rot_i[0], rot_i[1], shared_gate if logits is not None else None)
     _contig(cb, "cb")
     if cb.dim() != 2 or cb.shape[0] < 65536 or cb.shape[1] != 8 or cb.dtype not in (torch.float16, torch.bfloat16):
         raise Vq2Error("vq_sorted_moe: cb must be an fp16 / bf16 [65536, 8] codebook")
@@ -715,7 +749,6 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         P = int(top_k) + 1
         ids_out = torch.empty((T, P), dtype=torch.int32, device=dev)
         w_out = torch.empty((T, P), dtype=torch.float32, device=dev)
-        _contig(shared_gate, "shared_gate")
         ids_p, ids64, w_p = None, 0, None
     else:
         if ids is None or w is None:
@@ -743,8 +776,6 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         sg, sd = (int(v) for v in slices)
     lib = _lib.load()
     ws = _workspace(dev, int(lib.vq2_sorted_moe_workspace(T, P, H, I, sg, sd)), sorted_kind=True)
-    rh = _lib.RotTables(_p(rot_h[0]), _p(rot_h[1]), int(rot_h[2]), float(rot_h[3]))
-    ri = _lib.RotTables(_p(rot_i[0]), _p(rot_i[1]), int(rot_i[2]), float(rot_i[3]))
     gp, dp = gate_up.pool(gu_scale), down.pool(dn_scale)
     _lib.call("vq2_sorted_moe", _p(h2), _dt(h2, "h"), T, P, ids_p, ids64, w_p,
               _p(lg) if router else None, _dt(lg, "logits") if router else 0, lg.shape[1] if router else 0,
@@ -861,6 +892,7 @@ def vq_moe_gate_up_rht(h, ids, pool, cb16, pool_scale, y_out, OUT, NG, perm=None
     hh = _contig(h, "h").reshape(-1, NG * 8)
     if hh.shape[0] != T:
         raise Vq2Error("h must be [T, NG*8]")
+    _perm_sign(perm, sign, NG * 8)
     y2 = y_out.reshape(-1, y_out.shape[-1])
     if y2.shape[0] < T * P or y2.shape[1] < OUT or y2.stride(1) != 1:
         raise Vq2Error("y_out must be [>=T*P, >=OUT] with unit column stride")
@@ -897,7 +929,10 @@ def vq_moe_router_gate_up_rht(h, router_logits, top_k, pool, cb16, pool_scale, y
         raise Vq2Error("y_out must be [>=T*P, >=OUT] with unit column stride")
     ids = torch.empty((T, P), dtype=torch.int32, device=dev)
     w = torch.empty((T, P), dtype=torch.float32, device=dev)
-    sg = _contig(shared_gate, "shared_gate") if shared_gate is not None else None
+    _perm_sign(perm, sign, NG * 8)
+    if shared_id >= 0 and shared_gate is None:
+        raise Vq2Error("a shared expert needs shared_gate")
+    sg = _gate_vec(shared_gate, NG * 8) if shared_gate is not None else None
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
     _lib.call("vq2_moe_router_gate_up_rht", _p(hh), _dt(hh, "h"), T, _p(perm), _p(sign), int(hb), sc,
               _p(lg2), _dt(lg2, "router_logits"), lg2.shape[1], k, _p(sg), _dt(sg, "shared_gate") if sg is not None else 0,
@@ -927,6 +962,7 @@ def vq_moe_down_swiglu_combine(gu, ids, w, down_idx, cb16, down_scale, OUT, NG, 
     g2 = gu.reshape(-1, gu.shape[-1])
     if g2.shape[0] != T * P or g2.shape[1] < 2 * NG * 8 or g2.stride(1) != 1:
         raise Vq2Error("gu must be [T*P, >=2*NG*8] with unit column stride")
+    _perm_sign(perm, sign, NG * 8)
     hb = NG * 8 if hb is None else int(hb)
     sc = float(hb) ** -0.5 if rht_scale is None else float(rht_scale)
     p1, c8 = _stage2_pool(pool, pool1, cb16, cb8)
@@ -986,14 +1022,7 @@ def vq_rht(x, perm=None, sign=None, hb=2048, scale=None, inverse=False, *, out=N
     n = x.shape[-1]
     x2 = _contig(x, "x").reshape(-1, n)
     B = x2.shape[0]
-    if perm is not None:
-        if perm.dtype != torch.int32 or perm.numel() != n:
-            raise Vq2Error("perm must be int32 [n]")
-        _contig(perm, "perm")
-    if sign is not None:
-        if sign.dtype != torch.int8 or sign.numel() != n:
-            raise Vq2Error("sign must be int8 [n] of +-1")
-        _contig(sign, "sign")
+    _perm_sign(perm, sign, n)
     sc = float(hb) ** -0.5 if scale is None else float(scale)
     if out is None:
         out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=dev)
@@ -1013,9 +1042,7 @@ def vq_swiglu_rht(gu, inter, perm=None, sign=None, hb=None, scale=None, *, out=N
         raise Vq2Error("gu last dim must be >= 2*inter")
     hb = inter if hb is None else int(hb)
     B = g2.shape[0]
-    for t, nm, dt in ((perm, "perm", torch.int32), (sign, "sign", torch.int8)):
-        if t is not None and (t.dtype != dt or t.numel() != inter):
-            raise Vq2Error(f"{nm} must be {dt} [{inter}]")
+    _perm_sign(perm, sign, inter)
     sc = float(hb) ** -0.5 if scale is None else float(scale)
     if out is None:
         out = torch.empty((*gu.shape[:-1], inter), dtype=out_dtype, device=dev)
@@ -1039,9 +1066,8 @@ def vq_router_topk(logits, k=8, h=None, shared_gate=None, shared_id=-1, *, ids=N
     if extra:
         if h is None or shared_gate is None:
             raise Vq2Error("shared expert gate needs h and shared_gate")
-        hid = shared_gate.numel()
+        hid = _gate_vec(shared_gate, shared_gate.numel()).numel()
         h = _contig(h, "h").reshape(T, hid)
-        _contig(shared_gate, "shared_gate")
     if ids is None:
         ids = torch.empty((T, k + extra), dtype=torch.int32, device=dev)
     if w is None:

@@ -194,3 +194,55 @@ def test_resident_experts_reference_constructor_on_cpu():
     assert torch.equal(mod.down_scale, q_dn["scale"].view(E, H).to(torch.bfloat16))
     with pytest.raises(Vq2Error):
         ResidentMoEExperts(q_gu, q_dn, cb, "cpu", num_experts=E + 1, hidden_dim=H, intermediate_dim=I)
+
+
+# ---------------------------------- vq_sorted_moe argument checks (CPU)
+def _small_sorted_pools():
+    from compressai_amd.kernels import SortedPool
+
+    E, H, I = 2, 64, 32
+    gu = SortedPool(synth.indices16(7100, (E, 2 * I, H // 8)), device="cpu", threads=1)
+    dn = SortedPool(synth.indices16(7101, (E, H, I // 8)), device="cpu", threads=1)
+    return E, H, I, gu, dn
+
+
+def _rot(n, perm_dt=torch.int32, sign_dt=torch.int8, n_perm=None, n_sign=None):
+    perm = torch.arange(n if n_perm is None else n_perm, dtype=perm_dt)
+    sign = torch.ones(n if n_sign is None else n_sign, dtype=sign_dt)
+    return (perm, sign, n, n ** -0.5)
+
+
+@pytest.mark.parametrize("which,bad", [
+    ("rot_h", dict(n_perm=63)), ("rot_h", dict(perm_dt=torch.int64)), ("rot_h", dict(n_sign=65)),
+    ("rot_h", dict(sign_dt=torch.int32)), ("rot_i", dict(n_perm=31)), ("rot_i", dict(sign_dt=torch.float32)),
+    ("rot_i", dict(n_sign=64)),
+])
+def test_sorted_moe_rejects_bad_rotation_tables(which, bad):
+    """Each rotation table is read over H (rot_h) or I (rot_i) entries by the
+    kernels: a short, long or wrong-dtype table is refused on the host."""
+    from compressai_amd.kernels import vq_sorted_moe
+
+    E, H, I, gu, dn = _small_sorted_pools()
+    rh = _rot(H, **bad) if which == "rot_h" else _rot(H)
+    ri = _rot(I, **bad) if which == "rot_i" else _rot(I)
+    with pytest.raises(Vq2Error, match=which):
+        vq_sorted_moe(torch.zeros(1, H), gu, torch.ones(E, 2 * I), dn, torch.ones(E, H),
+                      torch.zeros(65536, 8, dtype=torch.float16), rh, ri,
+                      ids=torch.zeros(1, 1, dtype=torch.int32), w=torch.ones(1, 1))
+
+
+def test_sorted_moe_rejects_noncontiguous_table_and_bad_gate():
+    from compressai_amd.kernels import vq_sorted_moe
+
+    E, H, I, gu, dn = _small_sorted_pools()
+    args = (torch.zeros(1, H), gu, torch.ones(E, 2 * I), dn, torch.ones(E, H),
+            torch.zeros(65536, 8, dtype=torch.float16))
+    perm = torch.arange(2 * H, dtype=torch.int32)[::2]  # H entries, strided
+    with pytest.raises(Vq2Error, match="rot_h perm"):
+        vq_sorted_moe(*args, (perm, None, H, 1.0), _rot(I), ids=torch.zeros(1, 1, dtype=torch.int32),
+                      w=torch.ones(1, 1))
+    router = dict(logits=torch.zeros(1, E - 1), top_k=1, shared_id=E - 1)
+    for gate, msg in ((torch.zeros(H - 1), "shared_gate"), (torch.zeros(H, dtype=torch.int32), "shared_gate"),
+                      (torch.zeros(2 * H)[::2], "shared_gate"), (None, "router needs")):
+        with pytest.raises(Vq2Error, match=msg):
+            vq_sorted_moe(*args, _rot(H), _rot(I), shared_gate=gate, **router)
