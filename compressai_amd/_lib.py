@@ -81,6 +81,8 @@ SIGNATURES = {
     "vq2_sorted_moe": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _vp, _vp,
                         _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
                         ctypes.c_size_t, _vp], _i32),
+    "vq2_sorted_moe_status": ([_vp, _i32, _vp], _i32),
+    "vq2_sorted_moe_set_wait": ([_i64, _i32], _i32),
     "vq2_pager_lds_bytes": ([_i64, _i64, _i64], ctypes.c_size_t),
     "vq2_pager_step": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "vq2_pager_copy": ([_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp], _i32),

@@ -807,6 +807,30 @@ size_t vq2_sorted_moe_workspace(int64_t tokens, int pairs_per_token, int64_t hid
     return sorted_moe_workspace_bytes(tokens * pairs_per_token, hidden, inter, slices_gu, slices_dn);
 }
 
+int vq2_sorted_moe_status(void* workspace, int clear, void* stream)
+{
+    clear_error();
+    CHECK(workspace, "vq2_sorted_moe_status: NULL workspace");
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* word = (uint32_t*)((char*)workspace + VQ2_SORTED_WS_STATUS);
+    uint32_t v = 0;
+    hipError_t err = hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, st);
+    if (err == hipSuccess) err = hipStreamSynchronize(st);
+    if (err == hipSuccess && clear) {
+        static const uint32_t zero = 0;
+        err = hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, st);
+        if (err == hipSuccess) err = hipStreamSynchronize(st);
+    }
+    if (err != hipSuccess) return set_hip_error(err, "vq2_sorted_moe_status");
+    return (int)(v & 0x7FFFFFFFu);
+}
+
+int vq2_sorted_moe_set_wait(int64_t max_polls, int32_t extra_arrivals)
+{
+    clear_error();
+    return sorted_moe_set_wait(max_polls, extra_arrivals);
+}
+
 int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token, const void* ids, int ids_i64,
                    const float* w, const void* logits, int l_dt, int64_t n_routed, int top_k, int64_t shared_id,
                    const void* shared_gate, int g_dt, int32_t* ids_out, float* w_out, int64_t n_experts,

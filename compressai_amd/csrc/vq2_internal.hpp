@@ -182,6 +182,14 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
                      uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
                      int n_threads);
 
+// The one-launch MoE's wait bound (polls) and arrival target offset.
+struct MoeWait {
+    int max_polls;
+    int extra_arrivals;
+};
+MoeWait sorted_moe_wait();
+int sorted_moe_set_wait(int64_t max_polls, int32_t extra_arrivals);
+
 struct SortedPoolCall {
     const uint32_t* entries;
     int64_t iters_per_chunk;  // every chunk padded to this many iterations

@@ -30,6 +30,7 @@
 // An expert id outside the pool gives NaN for its pair (never an
 // out-of-bounds read), as the gather kernels do.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "vq2_internal.hpp"
@@ -72,7 +73,9 @@ struct SortedMoeArgs {
     // its finished workgroups per pair; down waits for gu_arrivals of them
     uint32_t* pair_cnt;
     int gu_arrivals;
-    int id_poll;  // down part of one launch with the router: the pair's (id, weight) is published in the launch
+    int id_poll;     // down part of one launch with the router: the pair's (id, weight) is published in the launch
+    int max_polls;   // bound of each wait (polls of ~640 clocks each)
+    uint32_t* status;  // sticky wait-timeout bits (VQ2_MOE_WAIT_*), never cleared by the kernels
     const void* ids;  // MODE 0 / 2 and the combine: pair experts
     int ids_i64;
     float* part;  // gate_up: [slices][n_pairs][pool.rows] raw row sums; down: [n_pairs][slices][pool.rows] shares
@@ -189,7 +192,16 @@ constexpr int SG_MAX_TOPK = 64;
 // (measured, T = 1 layer: 25.8 us fused against 20.9 us in two launches;
 // padded, 20.15 us; with no wait at all, wrong results, 19.45 us).
 constexpr int MOE_CNT_STRIDE = 32;        // uint32 per pair count
-constexpr int MOE_WAIT_POLLS = 1 << 20;   // ~1 s of polls, then the pair's shares turn NaN
+// Each wait is bounded: after max_polls polls (each a sleep of 640 clocks,
+// ~0.27 us at 2.4 GHz, plus the agent-scope load's round trip; the default
+// 2^20 is at least ~0.3 s) the waiting workgroup gives up, ORs its bit
+// (VQ2_MOE_WAIT_ID: the pair's published id; VQ2_MOE_WAIT_COUNT: the
+// pair's gate_up count) into the status word of the workspace header, and
+// its pair's shares turn NaN.  Forward progress relies on the dispatcher
+// starting workgroups in index order on each XCD (every gate_up workgroup
+// precedes every down workgroup of its XCD, and gate_up workgroups wait for
+// nothing), so a give-up means the order was broken or the launch was fed
+// an unreachable count; the host reads the bits (vq2_sorted_moe_status).
 
 // The router's pair (expert id + 1, combine weight) as one 64-bit word in
 // the pair's count line (words 2-3), so a down workgroup can load its entry
@@ -341,7 +353,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
                 int64_t ev = -1;
                 float wv = 0.0f;
                 if (a.id_poll) {
-                    for (int it = 0; it < MOE_WAIT_POLLS; it++) {
+                    for (int it = 0; it < a.max_polls; it++) {
                         const uint64_t v = __hip_atomic_load(pair_word(a, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         if ((uint32_t)v != 0u) {
                             ev = (int64_t)((uint32_t)v - 1u);
@@ -350,6 +362,9 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
                         }
                         __builtin_amdgcn_s_sleep(10);
                     }
+                    if (ev < 0)
+                        __hip_atomic_fetch_or(a.status, (uint32_t)VQ2_MOE_WAIT_ID, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
                 } else {
                     ev = a.ids_i64 ? ((const int64_t*)a.ids)[p] : (int64_t)((const int32_t*)a.ids)[p];
                     wv = a.w[p];
@@ -404,7 +419,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
             // finish; then their row sums (a bounded poll of the count)
             if (threadIdx.x == 0) {
                 bool ok = false;
-                for (int it = 0; it < MOE_WAIT_POLLS; it++) {
+                for (int it = 0; it < a.max_polls; it++) {
                     if (__hip_atomic_load(a.pair_cnt + p * MOE_CNT_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
                         (uint32_t)a.gu_arrivals) {
                         ok = true;
@@ -412,6 +427,9 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
                     }
                     __builtin_amdgcn_s_sleep(10);
                 }
+                if (!ok)
+                    __hip_atomic_fetch_or(a.status, (uint32_t)VQ2_MOE_WAIT_COUNT, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
                 s_ok = ok ? 1 : 0;
             }
             __syncthreads();
@@ -639,6 +657,23 @@ static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_exper
     return VQ2_OK;
 }
 
+// Bound of the one-launch waits and an arrival target offset (a test of the
+// give-up path passes a target the gate_up part cannot reach); process-wide.
+static std::atomic<int64_t> g_wait_polls{int64_t(1) << 20};
+static std::atomic<int32_t> g_wait_extra{0};
+MoeWait sorted_moe_wait()
+{
+    return MoeWait{(int)g_wait_polls.load(), (int)g_wait_extra.load()};
+}
+int sorted_moe_set_wait(int64_t max_polls, int32_t extra_arrivals)
+{
+    if (max_polls < 0 || max_polls > 0x7FFFFFFF || extra_arrivals < 0 || extra_arrivals > 1024)
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe_set_wait: max_polls 0..2^31-1, extra_arrivals 0..1024");
+    g_wait_polls.store(max_polls);
+    g_wait_extra.store(extra_arrivals);
+    return VQ2_OK;
+}
+
 // Workspace: VQ2_SORTED_WS_HEADER bytes of per-pair counters (the fused
 // launch; zero between calls), then the gate_up row sums and the down
 // shares.
@@ -790,11 +825,15 @@ int sorted_moe_launch(const SortedMoeCall& c)
 
     hipError_t err;
     if (f2k && f512 && n_pairs <= VQ2_SORTED_MAX_COUNTERS / MOE_CNT_STRIDE) {
+        static_assert(VQ2_SORTED_MAX_COUNTERS * 4 <= VQ2_SORTED_WS_STATUS, "counts below the status word");
         // gate_up and down in one launch, the down workgroups waiting for
         // their pair's gate_up workgroups (counts in the workspace header)
         a.pair_cnt = d.pair_cnt = pair_cnt;
-        d.gu_arrivals = (int)(a.pool.C * c.slices_gu);
+        const MoeWait wt = sorted_moe_wait();
+        d.gu_arrivals = (int)(a.pool.C * c.slices_gu) + wt.extra_arrivals;
         d.id_poll = router ? 1 : 0;
+        d.max_polls = wt.max_polls;
+        d.status = (uint32_t*)((char*)c.workspace + VQ2_SORTED_WS_STATUS);
         const unsigned grid = (unsigned)((grid_gu + 7) / 8 * 8 + grid_dn);
         err = router ? launch_fused<1>(c.cb_dt, c.h_dt, a, d, grid, std::max(shm_gu, shm_dn), st)
                      : launch_fused<0>(c.cb_dt, c.h_dt, a, d, grid, std::max(shm_gu, shm_dn), st);

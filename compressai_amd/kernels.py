@@ -261,12 +261,50 @@ def _workspace(dev: torch.device, nbytes: int, *, sorted_kind: bool = False) -> 
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream, sorted_kind)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
-        if buf is not None:
-            _WS_RETIRED.append(buf)
         alloc = torch.zeros if sorted_kind else torch.empty
-        buf = alloc(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        new = alloc(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        if buf is not None:
+            if sorted_kind:  # the MoE status word carries over
+                new[WS_STATUS:WS_STATUS + 4].copy_(buf[WS_STATUS:WS_STATUS + 4])
+            _WS_RETIRED.append(buf)
+        buf = new
         _WS[key] = buf
     return buf
+
+
+# The sorted workspace's header (include/vq2_amd.h): arrival counters, and in
+# its last 128-byte line the one-launch MoE's status word.
+WS_HEADER = 16384
+WS_STATUS = WS_HEADER - 128
+MOE_WAIT_ID = 1      # a down workgroup gave up waiting for its pair's routed id
+MOE_WAIT_COUNT = 2   # a down workgroup gave up waiting for its pair's gate_up sums
+
+
+def vq_sorted_moe_status(device=None, *, clear=False) -> int:
+    """Wait-timeout bits (MOE_WAIT_ID | MOE_WAIT_COUNT) that the one-launch
+    MoE kernels left in this (device, stream)'s sorted workspace, read after
+    the stream's queued work (a host synchronisation, so never inside graph
+    capture).  0: no wait gave up.  A set bit means some pair's output was
+    NaN because its wait gave up; clear=True resets the word."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    buf = _WS.get((dev.index, torch.cuda.current_stream(dev).cuda_stream, True))
+    if buf is None:
+        return 0
+    st = int(_lib.load().vq2_sorted_moe_status(buf.data_ptr(), 1 if clear else 0, _stream(dev)))
+    if st < 0:
+        _lib.check(st, "vq2_sorted_moe_status")
+    return st
+
+
+def vq_sorted_moe_set_wait(max_polls=1 << 20, extra_arrivals=0) -> None:
+    """Bound of each wait of the one-launch MoE (polls of >= 640 clocks) and
+    an offset added to the gate_up count its down workgroups wait for, for
+    all later launches of the process.  The defaults (2^20, 0) are the
+    production values; tests of the give-up path pass a short bound and an
+    unreachable count."""
+    _lib.call("vq2_sorted_moe_set_wait", int(max_polls), int(extra_arrivals))
 
 
 def vq_gemm_small_m(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
@@ -719,7 +757,9 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
                   w=None, logits=None, top_k=None, shared_id=None, shared_gate=None, out_dtype=torch.float32,
                   out=None, slices=None):
     """The experts of an MoE layer over code-sorted pools, two launches
-    (gate_up and down in one, then the combine; three at other widths):
+    (gate_up and down in one, then the combine; three at other widths or
+    above 127 pairs); a one-launch wait that gives up leaves its pair NaN
+    and a bit in vq_sorted_moe_status():
     out [T, H] = sum_k w[t, k] * VQ(down[e]) RHT_I(silu(gu[:I]) * gu[I:]),
     gu = VQ(gate_up[e]) RHT_H(h_t), e = ids[t, k].  With `logits` [T, E_r]
     the router is built in (top_k routed experts plus the shared expert
@@ -769,7 +809,7 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         cu = _cu_count(dev)
         # the library runs gate_up and down as one launch for these shapes
         # (2048-point and 512-point rotations, at most 128 pairs)
-        one = H == 2048 and I == 512 and int(rot_h[2]) == 2048 and int(rot_i[2]) == 512 and T * P <= 128
+        one = H == 2048 and I == 512 and int(rot_h[2]) == 2048 and int(rot_i[2]) == 512 and T * P <= 127
         sg = moe_slices(T * P * gate_up.chunks, gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0], one)
         sd = moe_slices(T * P * down.chunks, down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1], one)
     else:

@@ -21,18 +21,23 @@ synchronisation.
 logits) and the shared expert with its sigmoid gate (transformers 5.15.0
 ``Qwen3_5MoeTopKRouter`` / ``Qwen3_5MoeSparseMoeBlock``), the shared expert
 living in the same pool at id ``n_routed``.  The whole layer is two
-launches (router + gate_up, down + combine) and no host synchronisation.
+launches and no host synchronisation.
 
 Intermediates are fp32 by default (the parity contract); ``act_dtype`` may
 select bf16 to follow the reference's cast points instead.
 
 On the GPU, with fp16 / bf16 codebooks and fp32 intermediates, both modules
 also keep a code-sorted copy of the expert pools (``kernels.SortedPool``,
-packed once at construction, 4 bytes per code) and run the experts over it:
-the gate_up launch (router built in for ``MoELayer``), a down launch whose
-prologue finishes the gate_up sums and builds SwiGLU + RHT, and a combine
-launch, so a wave's centroid gathers share codebook lines.  The reference
-pools stay the public format and serve ``act_dtype`` bf16 and the paged feed.
+packed once at construction, ~3.06 bytes per code against the pools' 2) and
+run the experts over it, so a wave's centroid gathers share codebook lines:
+at hidden 2048 / intermediate 512 (the 35B-A3B shape) gate_up (router built
+in for ``MoELayer``) and down (SwiGLU + RHT in its prologue) are one launch,
+followed by the combine launch; other widths take a separate down launch.
+The reference pools stay the public format and serve ``act_dtype`` bf16,
+more than 256 routed experts and the paged feed; a caller that needs none
+of these frees them with ``release_reference_pools()`` (resident index
+memory then ~3.06 instead of ~5.06 bytes per code; ``sorted_layout=False``
+keeps only the 2-byte pools, on the gather kernels).
 """
 from __future__ import annotations
 
@@ -106,25 +111,46 @@ class ResidentMoEExperts(nn.Module):
         self.sorted_gu = K.SortedPool(gate_up_idx, device=dev) if use else None
         self.sorted_dn = K.SortedPool(down_idx, device=dev) if use else None
 
+    def release_reference_pools(self):
+        """Drop the reference index pools once the sorted copies exist (the
+        row scales stay: both layouts read them).  Afterwards only the
+        sorted path runs; act_dtype bf16 and n_routed > 256 raise."""
+        if self.sorted_gu is None:
+            raise K.Vq2Error("release_reference_pools: no sorted copy to run on")
+        self.gate_up_idx = None
+        self.down_idx = None
+
+    def _reference_pools(self):
+        if self.gate_up_idx is None:
+            raise K.Vq2Error("the reference pools were released (release_reference_pools); only the sorted "
+                             "path runs")
+
+    def wait_errors(self, clear=False) -> int:
+        """Wait-timeout bits of the one-launch sorted MoE on the current
+        stream (kernels.vq_sorted_moe_status; a host synchronisation)."""
+        return K.vq_sorted_moe_status(self.cb16.device, clear=clear)
+
     def _rots(self):
         rh, ri = self.rot_h, self.rot_i
         return (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale)
 
     def nbytes(self):
+        """Resident bytes: index pools, scales and the sorted copies."""
         own = sum(t.numel() * t.element_size() for t in (self.gate_up_idx, self.gate_up_scale, self.down_idx,
-                                                          self.down_scale))
+                                                          self.down_scale) if t is not None)
         return own + sum(p.nbytes() for p in (self.sorted_gu, self.sorted_dn) if p is not None)
 
     def experts(self, h, ids, w, out=None):
         """h [T, H] (unrotated hidden states), ids [T, P] int32/int64,
-        w fp32 [T, P] -> [T, H].  Sorted pools: gate_up, down (SwiGLU + RHT
-        in its prologue) and combine launches; otherwise two launches, gate_up
-        with the H-point RHT fused, then SwiGLU + I-point RHT + down +
-        weighted combine."""
+        w fp32 [T, P] -> [T, H].  Sorted pools: gate_up and down (SwiGLU +
+        RHT in its prologue) in one launch at the 35B shape, then the combine;
+        otherwise two launches, gate_up with the H-point RHT fused, then
+        SwiGLU + I-point RHT + down + weighted combine."""
         if self.sorted_gu is not None:
             rh, ri = self._rots()
             return K.vq_sorted_moe(h, self.sorted_gu, self.gate_up_scale, self.sorted_dn, self.down_scale, self.cb16,
                                    rh, ri, ids=ids, w=w, out=out, out_dtype=self.out_dtype or torch.float32)
+        self._reference_pools()
         T, P = ids.shape
         I = self.intermediate_dim
         y_gu = torch.empty((T * P, 2 * I), dtype=self.act_dtype, device=h.device)
@@ -169,10 +195,14 @@ class MoELayer(nn.Module):
     def route(self, h, router_logits):
         return K.vq_router_topk(router_logits, self.top_k, h, self.shared_gate, shared_id=self.n_routed)
 
+    def wait_errors(self, clear=False) -> int:
+        return self.experts_mod.wait_errors(clear)
+
     def forward(self, h, router_logits):
-        """Sorted pools: router + gate_up, down (SwiGLU + RHT prologue),
-        combine.  Otherwise two launches: router + gate_up (+ RHT), then
-        SwiGLU + RHT + down + combine."""
+        """Sorted pools: router + gate_up and down (SwiGLU + RHT prologue) in
+        one launch at the 35B shape, then the combine.  Otherwise two
+        launches: router + gate_up (+ RHT), then SwiGLU + RHT + down +
+        combine."""
         m = self.experts_mod
         h2 = h.reshape(-1, m.hidden_dim).contiguous()
         T = h2.shape[0]
@@ -183,6 +213,7 @@ class MoELayer(nn.Module):
                                         shared_id=self.n_routed, shared_gate=self.shared_gate,
                                         out_dtype=m.out_dtype or torch.float32)
             return out
+        m._reference_pools()
         I = m.intermediate_dim
         P = self.top_k + 1
         y_gu = torch.empty((T * P, 2 * I), dtype=m.act_dtype, device=h2.device)

@@ -366,7 +366,10 @@ int vq2_sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, 
  * concurrently.  A launch with several slices has at most
  * VQ2_SORTED_MAX_COUNTERS chunks. */
 #define VQ2_SORTED_WS_HEADER 16384
-#define VQ2_SORTED_MAX_COUNTERS (VQ2_SORTED_WS_HEADER / 4)
+/* The header's last 128-byte line holds vq2_sorted_moe's status word
+ * (below); counters use the words before it. */
+#define VQ2_SORTED_WS_STATUS (VQ2_SORTED_WS_HEADER - 128)
+#define VQ2_SORTED_MAX_COUNTERS (VQ2_SORTED_WS_STATUS / 4)
 
 /* One packed matrix of a sorted launch (device pointers, except the struct). */
 typedef struct vq2_sorted_mat {
@@ -487,17 +490,36 @@ typedef struct vq2_rot_tables {
  * the pool gives NaN for its token.  slices_gu / slices_dn workgroups share
  * each chunk; workspace: vq2_sorted_moe_workspace bytes, whose first
  * VQ2_SORTED_WS_HEADER bytes (per-pair counters) are zero before the first
- * call; every call leaves them zero.  For hidden 2048 / inter 512 and at
- * most 128 pairs (a 128-byte count each) the
+ * call; every call leaves the counters zero.  For hidden 2048 / inter 512
+ * and at most 127 pairs (a 128-byte count each) the
  * gate_up and down launches are one launch whose down workgroups wait
  * (bounded) on the per-pair counts of finished gate_up workgroups; calls
- * that share a workspace must not overlap.  Replaces the
+ * that share a workspace must not overlap.  A wait that gives up (the
+ * dispatcher did not start the gate_up workgroups ahead of the down ones
+ * that wait for them, or the count was unreachable) turns its pair's
+ * output NaN and ORs VQ2_MOE_WAIT_ID (the router's published id) or
+ * VQ2_MOE_WAIT_COUNT (the pair's gate_up count) into the uint32 status
+ * word at byte VQ2_SORTED_WS_STATUS of the workspace; no kernel clears it
+ * (vq2_sorted_moe_status reads it, and may clear it, synchronously).  Replaces the
  * per-token expert loop of PackedMoEExpertUniversal.forward
  * (vq2/load_and_test_full_35b.py:53-95) / PagedMoEExpert.forward
  * (vq2/paged_runtime.py:495-510), with the router, the transformers
  * Qwen3_5MoeSparseMoeBlock routing (softmax, top-k, shared expert gate). */
 size_t vq2_sorted_moe_workspace(int64_t tokens, int pairs_per_token, int64_t hidden, int64_t inter, int slices_gu,
                                 int slices_dn);
+#define VQ2_MOE_WAIT_ID 1
+#define VQ2_MOE_WAIT_COUNT 2
+/* The status word of a vq2_sorted_moe workspace (device pointer), read after
+ * the work queued on `stream` so far has finished; clear != 0 sets it back
+ * to 0.  Returns the bits (>= 0) or a negative VQ2_ERR_*.  No reference
+ * counterpart (the reference's expert loop has no cross-workgroup wait). */
+int vq2_sorted_moe_status(void* workspace, int clear, void* stream);
+/* Process-wide bound of each wait of the one-launch MoE (max_polls polls of
+ * >= 640 clocks; default 2^20) and an offset added to the gate_up count the
+ * down workgroups wait for (default 0).  For tests of the give-up path: a
+ * short bound with an unreachable count makes every wait give up while
+ * every kernel still exits normally.  No reference counterpart. */
+int vq2_sorted_moe_set_wait(int64_t max_polls, int32_t extra_arrivals);
 int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token,
                    const void* ids, int ids_i64, const float* w,
                    const void* logits, int l_dt, int64_t n_routed, int top_k, int64_t shared_id,

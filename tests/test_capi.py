@@ -125,3 +125,11 @@ def test_error_message_is_thread_local():
     t.join()
     assert seen["msg"] == ""
     assert "power of two" in L.vq2_last_error().decode()
+
+
+def test_moe_wait_knob_and_status_refuse_bad_arguments_on_host():
+    L = _lib.load()
+    assert "max_polls" in _err(L.vq2_sorted_moe_set_wait(-1, 0))
+    assert "extra_arrivals" in _err(L.vq2_sorted_moe_set_wait(10, 5000))
+    assert L.vq2_sorted_moe_set_wait(1 << 20, 0) == _lib.OK     # the production values
+    assert "NULL workspace" in _err(L.vq2_sorted_moe_status(None, 0, None))
