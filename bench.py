@@ -101,6 +101,11 @@ class DenseLayers:
             f"{time.perf_counter() - t0:.1f} s")
         self.bytes_per_step = sum(out * (n // 8) * 2 * (2 if bpw == 4 else 1) + out * 2
                                   for _, out, n, bpw in self.PROJ)
+        # resident index bytes of one layer set: the reference planes, and the
+        # code-sorted copies kept beside them
+        lay0 = self.layers[0]
+        self.plane_bytes = sum(t.numel() * t.element_size() for v in lay0.values() for t in v[:2] if t is not None)
+        self.sorted_bytes = sum(v[5].nbytes() for v in lay0.values() if v[5] is not None)
         self.x_attn = synth.activations(2004, HIDDEN).to(dev)
         self.x_o = synth.activations(2014, HIDDEN).to(dev)
         self.x_mlp = synth.activations(2024, HIDDEN).to(dev)
@@ -251,6 +256,7 @@ def bench_dense(args, dev):
     dom_us = res["sorted"]
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
     return dict(steps=args.steps, ms_per_step=ms_per_step, gbps=gbps, bytes_per_step=dl.bytes_per_step, layers=L,
+                plane_bytes=dl.plane_bytes, sorted_bytes=dl.sorted_bytes,
                 dom_us=dom_us, dom_gbps=dom_gbps, dom_bytes=dom_bytes, host_ms=host_ms, dense=dl,
                 spread_us=[round(per_step[0] * 1e3, 3), round(per_step[-1] * 1e3, 3)],
                 gather_step_us=gather_us, dom_gather_us=res["gather"])
@@ -335,10 +341,14 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
         res[T] = dict(us=us, gbps=gbps, bytes=bytes_layer, cpu_inputs=inputs[0])
         del gr
     res["cpu_layer"] = layers[0]
+    m0 = layers[0].experts_mod
+    res["resident"] = dict(
+        planes=sum(t.numel() * t.element_size() for t in (m0.gate_up_idx, m0.down_idx)),
+        sorted=sum(p.nbytes() for p in (m0.sorted_gu, m0.sorted_dn) if p is not None))
     return res
 
 
-def bench_lm_head(args, dev, batch=1, copies=14):
+def bench_lm_head(args, dev, batch=1, copies=14, only=False):
     """LM head 151936 x 2048 at 2 bpw + top-1 over 14 copies
     (1.1 GiB).  Batch 1: the sorted layout with the RHT of the fp16
     activation built in the kernel (as PackedLMHead.argmax runs it), the
@@ -362,6 +372,13 @@ def bench_lm_head(args, dev, batch=1, copies=14):
     ws = torch.empty(batch, out, dtype=torch.float32, device=dev)
     res = [None] * copies
     nbytes = out * (n // 8) * 2 + out * 2
+
+    if only:  # one call per copy, as the B = 1 runtime path runs it (for counter runs)
+        for l in range(copies):
+            _, s, sp = mats[l]
+            K.vq_sorted_gemv_argmax(xh, sp, s, cb, None, n, perm, sign, 2048)
+        torch.cuda.synchronize(dev)
+        return None
 
     def run(fwd):
         gr = capture(fwd, copies, dev)
@@ -400,7 +417,7 @@ def bench_lm_head(args, dev, batch=1, copies=14):
         log(f"lm head B={batch} (matrix cores, pre-rotated x): {out_d['matrix_cores_us']:.2f} us/call")
     gbps = nbytes / (us * 1e-6) / 1e9
     log(f"lm head B={batch}: {us:.2f} us/call, {gbps:.1f} GB/s")
-    out_d.update(us=us, gbps=gbps)
+    out_d.update(us=us, gbps=gbps, plane_bytes=mats[0][0].numel() * 2, sorted_bytes=mats[0][2].nbytes())
     return out_d
 
 
@@ -667,7 +684,8 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "dominant_gather", "dense", "copy", "moe", "paged"], default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "dense", "copy", "moe", "paged", "lmhead"],
+                    default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -702,6 +720,10 @@ def main():
             dl.step(l)
         torch.cuda.synchronize(dev)
         log("dense-only run done")
+        return
+    if args.only == "lmhead":
+        bench_lm_head(args, dev, batch=1, copies=args.layers, only=True)
+        log("lmhead-only run done")
         return
     if args.only == "paged":
         bench_paged(args, dev)
@@ -748,11 +770,20 @@ def main():
                         "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/"
                         "scales/activations, fp32 out; q/k/v in one code-sorted launch (PackedProjections), o "
                         "on the gather kernel, gate/up, down on the code-sorted layout (PackedLinear), batch 1",
-            "layers_cycled": d["layers"],
+            "layers_cycled": min(d["layers"], d["steps"]),
+            "layer_sets_resident": d["layers"],
             "bytes_per_step": d["bytes_per_step"],
             "graph_replay": True,
         },
         "pct_of_peak": round(100.0 * d["gbps"] / PEAK_HBM_GBPS, 3),
+        "resident_index_bytes": {
+            "note": "index bytes held on the device per unit: the reference planes (2 bytes per code, the public "
+                    "format) and the code-sorted copies the batch-1 kernels read (~3.06 bytes per code); both "
+                    "are resident unless the owner releases the planes",
+            "dense_layer": {"planes": d["plane_bytes"], "sorted": d["sorted_bytes"]},
+            "moe_layer_257_experts": None if moe is None else moe["resident"],
+            "lm_head": None if lm1 is None else {"planes": lm1["plane_bytes"], "sorted": lm1["sorted_bytes"]},
+        },
         "moe_layer_us": None if moe is None else round(moe[1]["us"], 3),
         "moe_layer_gbps": None if moe is None else round(moe[1]["gbps"], 2),
         "moe_layer_us_t8": None if moe is None else round(moe[8]["us"], 3),
