@@ -684,8 +684,8 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-lmhead", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "dominant_gather", "dense", "copy", "moe", "paged", "lmhead"],
-                    default=None)
+    ap.add_argument("--only", choices=["dominant", "dominant_gather", "dense", "copy", "moe", "paged", "lmhead",
+                                       "small_m"], default=None)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -720,6 +720,10 @@ def main():
             dl.step(l)
         torch.cuda.synchronize(dev)
         log("dense-only run done")
+        return
+    if args.only == "small_m":
+        bench_small_m(args, dev)
+        log("small_m-only run done")
         return
     if args.only == "lmhead":
         bench_lm_head(args, dev, batch=1, copies=args.layers, only=True)

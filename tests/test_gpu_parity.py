@@ -617,6 +617,44 @@ def test_gemm_small_m_matches_batched_gemv(dev):
         assert _rowwise_err(ya.cpu().numpy(), yb.cpu().numpy()) < TOL
 
 
+def test_gemm_small_m_split_sum_in_launch_is_deterministic(dev):
+    """The K splits are summed inside the launch by the last workgroup of
+    each row tile to arrive (arrival counters in the workspace header): the
+    same result on every call, interleaved with sorted launches that share
+    the workspace, and on every replay of a captured graph (with eager work
+    between the replays), bit for bit; and the counters are left at zero."""
+    out, n, M = 6144, 2048, 64
+    m = synth.vq_matrix(7350, out, n, bpw=4)
+    cb0, cb1 = synth.codebook(7351), synth.codebook(7352)
+    x = synth.activations(7354, (M, n), dtype=torch.float16)
+    i0, i1, sc, c0, c1, xx = _cuda(m["idx0"], m["idx1"], m["scale"], cb0, cb1, x, dev=dev)
+    y0 = K.vq_gemm_small_m(xx, i0, i1, c0, c1, sc, out, n, out_dtype=torch.float32)
+    _, y64 = O.vq_gemv(x, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert _rowwise_err(y0.cpu().numpy(), y64) < TOL
+    sp = K.SortedPlanes(m["idx0"], m["idx1"], out, n, device=dev)
+    ys = K.vq_sorted_gemv(xx[0], [(sp, sc)], c0, c1, n, hb=0)
+    y1 = K.vq_gemm_small_m(xx, i0, i1, c0, c1, sc, out, n, out_dtype=torch.float32)
+    assert torch.equal(y0, y1)
+    y = torch.empty_like(y0)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        K.vq_gemm_small_m(xx, i0, i1, c0, c1, sc, out, n, out_dtype=torch.float32, y=y)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        K.vq_gemm_small_m(xx, i0, i1, c0, c1, sc, out, n, out_dtype=torch.float32, y=y)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, y0)
+        K.vq_sorted_gemv(xx[1], [(sp, sc)], c0, c1, n, hb=0, ys=ys)
+    torch.cuda.synchronize(dev)
+    for ws in [t for k, t in K._WS.items() if k[0] == dev.index and k[2]]:
+        assert int(ws[:K.WS_STATUS].view(torch.int32).abs().sum()) == 0
+
+
 @pytest.mark.parametrize("B", [3, 70])
 def test_packed_linear_small_m_path(dev, B):
     """PackedLinear at batch >= 3 (matrix-core GEMM, chunked at 64 rows)
