@@ -680,12 +680,14 @@ static int sorted_call(SortedCall& c, const char* who, const void* x, int x_dt, 
         const vq2_sorted_mat& m = mats[i];
         CHECK(m.entries && m.scale, "%s: matrix %d has a NULL pointer", who, i);
         CHECK(m.out_rows >= 1 && m.n_iters >= 1, "%s: matrix %d: bad sizes", who, i);
+        CHECK(m.has_stage2 >= 0 && m.has_stage2 <= 2, "%s: matrix %d: has_stage2 must be 0, 1 or 2", who, i);
         CHECK(!m.has_stage2 || cb1, "%s: matrix %d has stage-2 entries but no cb1", who, i);
-        CHECK((m.has_stage2 != 0) == (mats[0].has_stage2 != 0), "%s: the matrices of a launch share one cfg", who);
+        CHECK(m.has_stage2 == mats[0].has_stage2, "%s: the matrices of a launch share one cfg", who);
         c.seg[i] = SortedSegCall{m.entries, m.iters_per_chunk, m.stage1_iters, m.n_iters, m.rows_per_chunk,
                                  m.has_stage2 ? 1 : 0, m.scale, m.y, m.out_rows};
     }
     if (!mats[0].has_stage2) c.cb1 = nullptr;
+    c.cb1_rows = mats[0].has_stage2 == 2 ? 256 : 65536;
     return VQ2_OK;
 }
 

@@ -142,6 +142,7 @@ struct SortedCall {
     float xscale;
     const void* cb0;
     const void* cb1;
+    int64_t cb1_rows = 65536;  // 256: the uint8 stage 2 of (16,8) (codes masked to 8 bits)
     int cb_dt;
     int s_dt;
     int y_dt;

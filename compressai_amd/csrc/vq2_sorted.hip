@@ -338,6 +338,7 @@ struct SortedArgs {
     GemvArgs g;  // the activation fields of the prologue (x, perm, sign, hb_log2, xscale, strides)
     const void* cb0;
     const void* cb1;
+    uint32_t c1mask;  // stage-2 code mask (0xFF: the 256-row codebook of (16,8))
     int s_dt;
     int y_dt;
     int64_t ng;
@@ -406,7 +407,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
     // two
     SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2> pipe;
-    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R);
+    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R, a.c1mask);
     if constexpr (XM == 0) pipe.gathers();
 
     float* acc = sorted_acc(s_acc, wave, lane, R);
@@ -608,6 +609,7 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     a.g.xscale = c.xscale;
     a.cb0 = c.cb0;
     a.cb1 = c.cb1;
+    a.c1mask = c.cb1_rows == 256 ? 0xFFu : 0xFFFFu;
     a.s_dt = c.s_dt;
     a.y_dt = c.y_dt;
     a.ng = c.ng;

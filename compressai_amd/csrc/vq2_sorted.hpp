@@ -416,8 +416,8 @@ struct Ent3 {
 // separates them, so each wait covers exactly the values it needs.
 // A gather reads the iteration's four base codes from lane SG_BASE_LANE
 // (v_readlane: scalar registers, no memory access) and adds each lane's
-// offset; a code is taken mod 65536, so no entry word can address outside
-// the codebook.
+// offset; a code is masked to its codebook's size (65536 rows, or 256 for
+// the uint8 stage 2 of (16,8)), so no entry word can address outside it.
 template <int CBT, int GD = 2, int W = SG_WAVES>
 struct SortedPipe {
     static_assert(GD >= 1 && GD <= 3, "gather depth 1 to 3");
@@ -429,6 +429,7 @@ struct SortedPipe {
     int it;
     uint32_t pb;     // position bits P of a field
     uint32_t dummy;  // the dummy row's position, R << gbits
+    uint32_t mask1;  // stage-2 code mask: 0xFFFF, or 0xFF for a 256-row codebook
     int ie[NE];      // the (clamped) iterations of the entry words
     Ent3 e[NE];
     u32x4 c[GD][4];  // centroids of iterations it .. it + (GD - 1) W
@@ -457,13 +458,14 @@ struct SortedPipe {
     __device__ __forceinline__ void gather(int i, const Ent3& ew, u32x4 (&cw)[4]) const
     {
         const u32x4* cb = i < c_mid ? cb0 : cb1;
+        const uint32_t cmask = i < c_mid ? 0xFFFFu : mask1;
         const uint32_t b01 = (uint32_t)__builtin_amdgcn_readlane((int)ew.w[0], SG_BASE_LANE);
         const uint32_t b23 = (uint32_t)__builtin_amdgcn_readlane((int)ew.w[1], SG_BASE_LANE);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const uint32_t bw = q < 2 ? b01 : b23;
             const uint32_t base = (q & 1) ? bw >> 16 : bw & 0xFFFFu;
-            cw[q] = cb[(base + (field(ew, q) >> pb)) & 0xFFFFu];
+            cw[q] = cb[(base + (field(ew, q) >> pb)) & cmask];
         }
     }
     // the four positions (row << gbits | group) of this lane's entries;
@@ -479,8 +481,10 @@ struct SortedPipe {
     // a missing stage-2 codebook is never selected for a real entry; cb0
     // stands in so that no gather can use a null base
     __device__ __forceinline__ void load_entries(const uint32_t* ent_, const void* cb0_, const void* cb1_, int c_beg_,
-                                                 int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R)
+                                                 int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R,
+                                                 uint32_t mask1_ = 0xFFFFu)
     {
+        mask1 = mask1_;
         ent = ent_;
         cb0 = (const u32x4*)cb0_;
         cb1 = (const u32x4*)(cb1_ ? cb1_ : cb0_);
@@ -503,9 +507,10 @@ struct SortedPipe {
         for (int d = 0; d < GD; d++) gather(ie[d], e[d], c[d]);
     }
     __device__ __forceinline__ void start(const uint32_t* ent_, const void* cb0_, const void* cb1_, int c_beg_,
-                                          int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R)
+                                          int c_mid_, int s0, int s1_, int wave, int lane_, int gbits, int R,
+                                          uint32_t mask1_ = 0xFFFFu)
     {
-        load_entries(ent_, cb0_, cb1_, c_beg_, c_mid_, s0, s1_, wave, lane_, gbits, R);
+        load_entries(ent_, cb0_, cb1_, c_beg_, c_mid_, s0, s1_, wave, lane_, gbits, R, mask1_);
         gathers();
     }
     __device__ __forceinline__ void shift(const Ent3& enew, int inew)

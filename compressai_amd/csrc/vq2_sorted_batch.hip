@@ -76,6 +76,7 @@ struct SortedBatchArgs {
     int batch;
     const void* cb0;
     const void* cb1;
+    uint32_t c1mask;  // stage-2 code mask (0xFF: the 256-row codebook of (16,8))
     int s_dt;
     int y_dt;
     int64_t ng;
@@ -190,7 +191,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     // from L2 meanwhile.  Gathers one iteration ahead (measured, LM head at
     // batch 2 / 4: 67.9 / 144.6 us; two ahead 68.8 / 144.9, three 70.9 / 154.8)
     SortedPipe<CBT, 1, SB_WAVES> pipe;
-    pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R);
+    pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R, a.c1mask);
 
     accv* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
     for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = (accv)0.0f;
@@ -418,6 +419,7 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     a.batch = (int)c.batch;
     a.cb0 = c.cb0;
     a.cb1 = c.cb1;
+    a.c1mask = c.cb1_rows == 256 ? 0xFFu : 0xFFFFu;
     a.s_dt = c.s_dt;
     a.y_dt = c.y_dt;
     a.ng = c.ng;

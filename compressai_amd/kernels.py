@@ -426,10 +426,17 @@ class SortedPlanes:
         i0 = _idx16(i0, "i0")
         if i0.numel() != out_rows * ng:
             raise Vq2Error(f"i0 has {i0.numel()} codes, expected {out_rows * ng}")
+        # stage-2 kind: 0 none, 1 int16 plane ((16,16), 65536-row cb1), 2 uint8
+        # plane ((16,8), 256-row cb1: its codes are packed as 16-bit codes
+        # below 256, and the kernels mask them to 8 bits)
+        self.s2_kind = 0
         if i1 is not None:
             if i1.dtype == torch.uint8:
-                raise Vq2Error("the sorted layout covers (16,) and (16,16) matrices, not (16,8)")
-            i1 = _idx16(i1, "i1")
+                _contig(i1, "i1")
+                self.s2_kind = 2
+            else:
+                i1 = _idx16(i1, "i1")
+                self.s2_kind = 1
             if i1.numel() != i0.numel():
                 raise Vq2Error("i1 and i0 must have the same number of codes")
         dev = torch.device(device) if device is not None else i0.device
@@ -442,7 +449,7 @@ class SortedPlanes:
         self.n_chunks = -(-out_rows // R)
         self.has_stage2 = i1 is not None
         h0 = i0.detach().to("cpu").contiguous()
-        h1 = None if i1 is None else i1.detach().to("cpu").contiguous()
+        h1 = None if i1 is None else i1.detach().to("cpu").to(torch.int16).contiguous()
         stages = 2 if h1 is not None else 1
         # 252 codes per iteration (lane 63 of an instruction holds its base
         # code), a few instructions more where the packer closes one early
@@ -471,7 +478,7 @@ class SortedPlanes:
             raise Vq2Error(f"scale has {scale.numel()} entries, expected {self.out_rows}")
         _dt(scale, "scale")
         return _lib.SortedMat(self.entries.data_ptr(), self.iters_per_chunk, self.stage1_iters, self.n_iters,
-                              self.rows_per_chunk, 1 if self.has_stage2 else 0, scale.data_ptr(), _p(y), self.out_rows)
+                              self.rows_per_chunk, self.s2_kind, scale.data_ptr(), _p(y), self.out_rows)
 
     def nbytes(self):
         return self.entries.numel() * self.entries.element_size()
@@ -505,9 +512,12 @@ def _sorted_cbs(planes, cb0, cb1):
         raise Vq2Error(f"cb0 must be [65536, 8], got {tuple(cb0.shape)}")
     if cb0.dtype not in (torch.float16, torch.bfloat16):
         raise Vq2Error("the sorted layout takes fp16 / bf16 codebooks")
+    if any(p.s2_kind != planes[0].s2_kind for p in planes):
+        raise Vq2Error("the matrices of a sorted launch share one cfg")
     if planes[0].has_stage2:
-        if cb1 is None or cb1.dim() != 2 or cb1.shape[0] < 65536 or cb1.shape[1] != 8 or cb1.dtype != cb0.dtype:
-            raise Vq2Error("a (16,16) matrix needs cb1 [65536, 8] in the dtype of cb0")
+        rows = 256 if planes[0].s2_kind == 2 else 65536
+        if cb1 is None or cb1.dim() != 2 or cb1.shape[0] < rows or cb1.shape[1] != 8 or cb1.dtype != cb0.dtype:
+            raise Vq2Error(f"this matrix needs cb1 [{rows}, 8] in the dtype of cb0")
         _contig(cb1, "cb1")
         return cb0, cb1
     return cb0, None

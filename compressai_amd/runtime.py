@@ -106,7 +106,7 @@ class PackedLinear(nn.Module):
         codes = self.out * (self.n // 8) * len(self.cfg)
         dev = torch.device(device)
         use = sorted_layout if sorted_layout is not None else (
-            codes >= SORTED_MIN_CODES and dev.type == "cuda" and self.cfg in ((16,), (16, 16)))
+            codes >= SORTED_MIN_CODES and dev.type == "cuda" and self.cfg in ((16,), (16, 8), (16, 16)))
         self.sorted = None
         if use:
             self.sorted = K.SortedPlanes(self.idx0, getattr(self, "idx1", None), self.out, self.n, device=dev)
@@ -193,7 +193,7 @@ class PackedProjections(nn.Module):
         self.codes = codes
         dev = a.idx0.device
         use = sorted_layout if sorted_layout is not None else (
-            codes >= SORTED_MIN_LAUNCH_CODES and dev.type == "cuda" and a.cfg in ((16,), (16, 16)))
+            codes >= SORTED_MIN_LAUNCH_CODES and dev.type == "cuda" and a.cfg in ((16,), (16, 8), (16, 16)))
         self.sorted = None
         if use:
             self.sorted = [m.sorted if m.sorted is not None else

@@ -349,7 +349,8 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  * cap_iters * 192 uint32, 16-byte aligned) and sets *iters_per_chunk
  * (ipc), *stage1_iters and *n_iters = n_chunks * ipc, n_chunks =
  * ceil(out_rows / rows_per_chunk) (also when the capacity is too small,
- * which returns VQ2_ERR_ARG).  idx1 (the (16,16) stage-2 plane) may be NULL; n_threads
+ * which returns VQ2_ERR_ARG).  idx1 (the stage-2 plane as int16: (16,16), or
+ * a (16,8) uint8 plane widened to int16 values 0..255) may be NULL; n_threads
  * <= 0: all host threads.  No reference counterpart (a load-time transform
  * of the planes PackedLinear holds, vq2/runtime.py:70-80). */
 int64_t vq2_sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align);
@@ -378,7 +379,10 @@ typedef struct vq2_sorted_mat {
     int64_t stage1_iters;
     int64_t n_iters;
     int64_t rows_per_chunk;   /* the value the matrix was packed with          */
-    int has_stage2;           /* packed with idx1 (4 bpw): needs cb1          */
+    int has_stage2;           /* 0: none; 1: packed with an int16 idx1 ((16,16),
+                                 cb1 [65536, 8]); 2: packed with a uint8 idx1
+                                 widened to int16 ((16,8), cb1 [256, 8], codes
+                                 masked to 8 bits)                             */
     const void* scale;        /* [out_rows], dtype s_dt                        */
     void* y;                  /* [out_rows], dtype y_dt (unused by the top-1) */
     int64_t out_rows;

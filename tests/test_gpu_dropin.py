@@ -197,6 +197,30 @@ def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
         assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
 
 
+def test_packed_linear_16_8_on_the_sorted_layout(dev):
+    """A (16,8) 3 bpw PackedLinear of 2.1 M codes keeps a sorted copy whose
+    stage 2 is the uint8 plane (packed as codes below 256 into the [256, 8]
+    stage-2 codebook) and runs batch 1 on it with the RHT fused; the output
+    matches the oracle and the gather kernel on the reference planes."""
+    from compressai_amd import kernels as K
+    from compressai_amd.runtime import PackedLinear
+
+    out, n = 4096, 2048
+    cbs = {"16": synth.codebook(9390).to(dev), "16_8": synth.codebook(9391, 256).to(dev)}
+    m = synth.vq_matrix(9392, out, n, bpw=3)
+    lin = PackedLinear((out, n), (16, 8), "t_sorted_16_8", [m["idx0"], m["idx1"]], m["scale"], cbs, dev)
+    assert lin.sorted is not None and lin.sorted.s2_kind == 2
+    x = synth.activations(9393, (1, n), dtype=torch.float32)
+    y = lin(x.to(dev), out_dtype=torch.float32)
+    perm, sign = _rot_np(lin.rot)
+    xr = O.rht(x, perm, sign, lin.rot.hb).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cbs["16"].cpu(), cbs["16_8"].cpu(), lin.scale.cpu())
+    assert O.max_rel_err(y.cpu().numpy(), y64) < TOL
+    yg = K.vq_gemv(torch.from_numpy(xr).to(dev), lin.idx0, lin.idx1, cbs["16"], cbs["16_8"], lin.scale, out, n,
+                   out_dtype=torch.float32)
+    assert O.max_rel_err(y.cpu().numpy(), yg.cpu().numpy()) < 1e-5
+
+
 @pytest.mark.parametrize("B", [2, 3, 4])
 def test_lm_head_batch_top1_on_sorted_batch_kernel(dev, B):
     """An LM head of 32768 x 2048 (8.4 M codes) at batch 2-4: PackedLMHead.argmax

@@ -1,6 +1,6 @@
 """GPU parity of the code-sorted VQ GEMV (vq2_sorted_gemv / _argmax, through
 the C ABI) against the fp64 oracle on the same seeded inputs: the config 1-3
-shapes, ragged row counts and non-power-of-two widths, 2 and 4 bpw, fp16 and
+shapes, ragged row counts and non-power-of-two widths, 2, 3 (16,8) and 4 bpw, fp16 and
 bf16 codebooks, the fused RHT prologue and pre-rotated activations, one or
 several workgroups per chunk, several matrices per launch, and the fused
 LM-head top-1 (ties resolve to the lower row, as torch.argmax).
@@ -22,7 +22,7 @@ TOL = 1e-3
 def _mk(seed, rows, n, bpw, dev, cb_dtype=torch.float16):
     m = synth.vq_matrix(seed, rows, n, bpw=bpw)
     cb0 = synth.codebook(seed + 1, dtype=cb_dtype)
-    cb1 = synth.codebook(seed + 2, dtype=cb_dtype) if bpw == 4 else None
+    cb1 = synth.codebook(seed + 2, 256 if bpw == 3 else 65536, dtype=cb_dtype) if bpw > 2 else None
     sp = K.SortedPlanes(m["idx0"], m["idx1"], rows, n, device=dev)
     return m, cb0, cb1, sp
 
@@ -35,6 +35,9 @@ def _mk(seed, rows, n, bpw, dev, cb_dtype=torch.float16):
     (97, 800, 2, False, 1),          # ng = 100: not a power of two
     (517, 2048, 4, True, 7),
     (300, 2048, 2, True, 64),        # more slices than iterations per chunk
+    (2048, 2048, 3, True, None),     # (16,8): stage-2 uint8 codes into the 256-row codebook
+    (512, 6144, 3, True, None),
+    (97, 800, 3, False, 2),
 ])
 def test_sorted_gemv_vs_oracle(dev, rows, n, bpw, fused, slices):
     m, cb0, cb1, sp = _mk(9500 + rows + n, rows, n, bpw, dev)
@@ -219,3 +222,37 @@ def test_sorted_top1_ties_pick_lower_row(dev):
     assert float(y[100]) == float(y[5 * R + 100])   # the tie is exact in the kernel too
     idx, _ = K.vq_sorted_gemv_argmax(x.to(dev), sp, sc.to(dev), cb.to(dev), None, n)
     assert int(idx[0]) == 100
+
+
+def test_sorted_gemv_16_8_bf16_and_batch_kernel(dev):
+    """(16,8) on the sorted layout with bf16 codebooks and scales, through
+    the batch-1 kernel and the batch 2 / 4 kernel, against the oracle (the
+    batch kernel rounds the activation to fp16 under a power-of-two row
+    scale: tested against the oracle fed that rounded activation)."""
+    from act_rounding import fp16_row_scaled
+
+    rows, n = 1024, 2048
+    m, cb0, cb1, sp = _mk(9560, rows, n, 3, dev, cb_dtype=torch.bfloat16)
+    assert sp.s2_kind == 2
+    sc = m["scale"].to(torch.bfloat16)
+    xr = synth.activations(9561, (4, n), dtype=torch.float32)
+    (y,) = K.vq_sorted_gemv(xr[0].to(dev), [(sp, sc.to(dev))], cb0.to(dev), cb1.to(dev), n, hb=0)
+    _, y64 = O.vq_gemv(xr[:1].numpy(), m["idx0"], m["idx1"], cb0, cb1, sc)
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+    for B in (2, 4):
+        (yb,) = K.vq_sorted_gemm_batch(xr[:B].to(dev), [(sp, sc.to(dev))], cb0.to(dev), cb1.to(dev), n)
+        _, yr = O.vq_gemv(fp16_row_scaled(xr[:B].numpy()), m["idx0"], m["idx1"], cb0, cb1, sc)
+        assert max(O.max_rel_err(yb[b].cpu().numpy(), yr[b]) for b in range(B)) < 1e-5
+
+
+def test_sorted_16_8_refuses_a_65536_row_stage2_mismatch(dev):
+    """A (16,8) sorted matrix needs the [256, 8] stage-2 codebook of cb0's
+    dtype; a (16,16) one a [65536, 8]; one launch takes one kind."""
+    m, cb0, cb1, sp = _mk(9570, 64, 512, 3, dev)
+    x = synth.activations(9571, 512, dtype=torch.float32).to(dev)
+    with pytest.raises(K.Vq2Error):
+        K.vq_sorted_gemv(x, [(sp, m["scale"].to(dev))], cb0.to(dev), None, 512, hb=0)
+    m4, _, c4, sp4 = _mk(9572, 64, 512, 4, dev)
+    with pytest.raises(K.Vq2Error):
+        K.vq_sorted_gemv(x, [(sp, m["scale"].to(dev)), (sp4, m4["scale"].to(dev))], cb0.to(dev), c4.to(dev), 512,
+                         hb=0)

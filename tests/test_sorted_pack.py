@@ -70,7 +70,8 @@ def _decode(sp: SortedPlanes):
 
 
 @pytest.mark.parametrize("rows,n,bpw", [(300, 2048, 2), (256, 2048, 4), (100, 6144, 4), (1000, 512, 2),
-                                        (97, 800, 2), (5, 64, 4), (1, 2048, 2), (3, 16, 2)])
+                                        (97, 800, 2), (5, 64, 4), (1, 2048, 2), (3, 16, 2), (200, 2048, 3),
+                                        (7, 16, 3)])
 def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
     ng = n // 8
     m = synth.vq_matrix(9800 + rows + bpw, rows, n, bpw=bpw)
@@ -84,8 +85,13 @@ def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
     assert sp.n_iters == sp.n_chunks * sp.iters_per_chunk                 # chunks padded to one size
     assert sp.entries.numel() == sp.n_iters * ITER_WORDS
     assert 0 < sp.stage1_iters <= sp.iters_per_chunk
-    assert (sp.stage1_iters < sp.iters_per_chunk) == (bpw == 4)
-    planes = [m["idx0"].numpy().view(np.uint16)] + ([m["idx1"].numpy().view(np.uint16)] if bpw == 4 else [])
+    assert (sp.stage1_iters < sp.iters_per_chunk) == (bpw > 2)
+    assert sp.s2_kind == {2: 0, 3: 2, 4: 1}[bpw]
+    planes = [m["idx0"].numpy().view(np.uint16)]
+    if bpw == 4:
+        planes.append(m["idx1"].numpy().view(np.uint16))
+    if bpw == 3:  # the (16,8) uint8 plane: packed as codes 0..255
+        planes.append(m["idx1"].numpy().astype(np.uint16))
     dummy = R << gb
     for c, stages in enumerate(_decode(sp)):
         rb, nbig = rows // sp.n_chunks, rows % sp.n_chunks    # near-equal chunks: heights rb + 1 then rb
@@ -140,7 +146,7 @@ def test_sorted_pack_keeps_instructions_within_few_lines():
 def test_sorted_pack_rejects_bad_input():
     m = synth.vq_matrix(9910, 16, 512, bpw=3)
     with pytest.raises(Vq2Error):
-        SortedPlanes(m["idx0"], m["idx1"], 16, 512, device="cpu")  # (16,8) is not covered
+        SortedPlanes(m["idx0"], m["idx1"][:8], 16, 512, device="cpu")  # stage-2 plane of another size
     with pytest.raises(Vq2Error):
         SortedPlanes(m["idx0"], None, 17, 512, device="cpu")      # wrong row count
     L = _lib.load()
