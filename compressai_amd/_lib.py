@@ -76,7 +76,7 @@ SIGNATURES = {
     "vq2_sorted_gemm_batch_argmax_workspace": ([_vp, _i64], ctypes.c_size_t),
     "vq2_sorted_gemm_batch_argmax": ([_vp, _i32, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _i64, _f32, _vp,
                                       ctypes.c_size_t, _vp, _vp, _vp], _i32),
-    "vq2_sorted_pack_pool": ([_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32], _i32),
+    "vq2_sorted_pack_pool": ([_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i32], _i32),
     "vq2_sorted_moe_workspace": ([_i64, _i32, _i64, _i64, _i32, _i32], ctypes.c_size_t),
     "vq2_sorted_moe": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _vp, _vp,
                         _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
@@ -116,7 +116,8 @@ class SortedPool(ctypes.Structure):
     """struct vq2_sorted_pool of include/vq2_amd.h"""
     _fields_ = [("entries", ctypes.c_void_p), ("iters_per_chunk", ctypes.c_int64), ("n_iters", ctypes.c_int64),
                 ("rows_per_chunk", ctypes.c_int64), ("rows", ctypes.c_int64), ("ng", ctypes.c_int64),
-                ("scale", ctypes.c_void_p), ("scale_dt", ctypes.c_int)]
+                ("scale", ctypes.c_void_p), ("scale_dt", ctypes.c_int), ("stage1_iters", ctypes.c_int64),
+                ("has_stage2", ctypes.c_int), ("cb1", ctypes.c_void_p)]
 
 
 class RotTables(ctypes.Structure):

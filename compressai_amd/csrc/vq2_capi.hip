@@ -790,16 +790,16 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
     return sorted_batch_launch(c, out_idx, out_val);
 }
 
-int vq2_sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
-                         uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
-                         int n_threads)
+int vq2_sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts, int64_t rows, int64_t ng,
+                         int64_t rows_per_chunk, uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk,
+                         int64_t* stage1_iters, int64_t* n_iters, int n_threads)
 {
     clear_error();
-    CHECK(idx && entries && iters_per_chunk && n_iters, "vq2_sorted_pack_pool: NULL pointer argument");
+    CHECK(idx && entries && iters_per_chunk && stage1_iters && n_iters, "vq2_sorted_pack_pool: NULL pointer argument");
     CHECK(n_experts >= 1 && rows >= 1 && ng >= 1, "vq2_sorted_pack_pool: bad sizes n_experts=%lld rows=%lld ng=%lld",
           (long long)n_experts, (long long)rows, (long long)ng);
-    return sorted_pack_pool(idx, n_experts, rows, ng, rows_per_chunk, entries, cap_iters, iters_per_chunk, n_iters,
-                            n_threads);
+    return sorted_pack_pool(idx, idx1, n_experts, rows, ng, rows_per_chunk, entries, cap_iters, iters_per_chunk,
+                            stage1_iters, n_iters, n_threads);
 }
 
 size_t vq2_sorted_moe_workspace(int64_t tokens, int pairs_per_token, int64_t hidden, int64_t inter, int slices_gu,
@@ -862,10 +862,11 @@ int vq2_sorted_moe(const void* h, int h_dt, int64_t tokens, int pairs_per_token,
     c.n_experts = n_experts;
     c.hidden = hidden;
     c.inter = inter;
-    c.gate_up = SortedPoolCall{gate_up->entries, gate_up->iters_per_chunk, gate_up->n_iters, gate_up->rows_per_chunk,
-                               gate_up->rows, gate_up->ng, gate_up->scale, gate_up->scale_dt};
-    c.down = SortedPoolCall{down->entries, down->iters_per_chunk, down->n_iters, down->rows_per_chunk, down->rows,
-                            down->ng, down->scale, down->scale_dt};
+    c.gate_up = SortedPoolCall{gate_up->entries, gate_up->iters_per_chunk, gate_up->stage1_iters, gate_up->has_stage2,
+                               gate_up->cb1, gate_up->n_iters, gate_up->rows_per_chunk, gate_up->rows, gate_up->ng,
+                               gate_up->scale, gate_up->scale_dt};
+    c.down = SortedPoolCall{down->entries, down->iters_per_chunk, down->stage1_iters, down->has_stage2, down->cb1,
+                            down->n_iters, down->rows_per_chunk, down->rows, down->ng, down->scale, down->scale_dt};
     c.cb = cb;
     c.cb_dt = cb_dt;
     c.rot_h = SortedRot{rot_h->perm, rot_h->sign, rot_h->hb, rot_h->scale};

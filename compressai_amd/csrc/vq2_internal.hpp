@@ -179,9 +179,9 @@ size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk);
 int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val);
 
 // MoE experts over code-sorted expert pools (vq2_sorted_moe.hip).
-int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
-                     uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
-                     int n_threads);
+int sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts, int64_t rows, int64_t ng,
+                     int64_t rows_per_chunk, uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk,
+                     int64_t* stage1_iters, int64_t* n_iters, int n_threads);
 
 // The one-launch MoE's wait bound (polls) and arrival target offset.
 struct MoeWait {
@@ -194,6 +194,9 @@ int sorted_moe_set_wait(int64_t max_polls, int32_t extra_arrivals);
 struct SortedPoolCall {
     const uint32_t* entries;
     int64_t iters_per_chunk;  // every chunk padded to this many iterations
+    int64_t stage1_iters;     // of which stage 1 (the stage-2 ones follow)
+    int s2;                   // 0 none, 1 int16 stage 2 (cb1 [65536, 8]), 2 uint8 stage 2 (cb1 [256, 8])
+    const void* cb1;
     int64_t n_iters;
     int64_t rows_per_chunk;
     int64_t rows;  // rows per expert

@@ -261,13 +261,15 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
     return VQ2_OK;
 }
 
-// Expert pool [E, rows, ng] (one stage): every expert packed as a matrix of
-// its own with the same chunk height R, experts one after another, and
-// every chunk padded (dummy-row entries) to the pool's largest iteration
-// count, so chunk c of expert e starts at iteration (e * C + c) * ipc
-// (C = ceil(rows / R)) with no table to read.
-int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t R, uint32_t* entries,
-                     int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters, int n_threads)
+// Expert pool [E, rows, ng] (one or two stages): every expert packed as a
+// matrix of its own with the same chunk height R, experts one after another,
+// and every chunk's stage-1 and stage-2 entries padded (dummy-row entries)
+// to the pool's largest stage-1 / stage-2 iteration counts, so chunk c of
+// expert e starts at iteration (e * C + c) * ipc (C = ceil(rows / R)), its
+// stage-2 entries ipc1 later, with no table to read.
+int sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts, int64_t rows, int64_t ng, int64_t R,
+                     uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
+                     int64_t* n_iters, int n_threads)
 {
     const int64_t rmax = sorted_max_rows(ng);
     if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: ng=%lld outside 1..32768", (long long)ng);
@@ -278,7 +280,7 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
     const ChunkSplit ks = chunk_split(rows, R);
     const int64_t C = ks.n_chunks;
     const int64_t units = n_experts * C;
-    std::vector<std::vector<uint32_t>> parts((size_t)units);
+    std::vector<std::vector<uint32_t>> p1((size_t)units), p2((size_t)units);
     int nt = n_threads > 0 ? n_threads : (int)std::thread::hardware_concurrency();
     if (nt < 1) nt = 1;
     if (nt > units) nt = (int)(units > 0 ? units : 1);
@@ -286,7 +288,8 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
         for (int64_t u = t; u < units; u += nt) {
             const int64_t e = u / C, c = u - e * C;
             const int64_t r0 = c * ks.rb + std::min(c, ks.nbig), nr = ks.rb + (c < ks.nbig ? 1 : 0);
-            pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, parts[u]);
+            pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, p1[u]);
+            if (idx1) pack_chunk_stage(idx1 + e * rows * ng, r0, nr, ng, gb, R, p2[u]);
         }
     };
     if (nt == 1) {
@@ -296,21 +299,29 @@ int sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_
         for (int t = 0; t < nt; t++) th.emplace_back(work, t);
         for (auto& t : th) t.join();
     }
-    int64_t ipc = 1;
-    for (int64_t u = 0; u < units; u++) ipc = std::max(ipc, (int64_t)parts[u].size() / SG_ITER_WORDS);
+    int64_t ipc1 = 1, ipc2 = 0;
+    for (int64_t u = 0; u < units; u++) {
+        ipc1 = std::max(ipc1, (int64_t)p1[u].size() / SG_ITER_WORDS);
+        ipc2 = std::max(ipc2, (int64_t)p2[u].size() / SG_ITER_WORDS);
+    }
+    const int64_t ipc = ipc1 + ipc2;
     const int64_t total = ipc * units;
     *n_iters = total;
     *iters_per_chunk = ipc;
+    *stage1_iters = ipc1;
     if (total > 0x7FFFFFFFLL) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: pool too large");
     if (total > cap_iters)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: %lld iterations needed, capacity %lld", (long long)total,
                          (long long)cap_iters);
     const uint32_t pad = (uint32_t)(R << gb);  // code 0, dummy row R
     for (int64_t u = 0; u < units; u++) {
-        uint32_t* dst = entries + u * ipc * SG_ITER_WORDS;
-        const int64_t nu = (int64_t)parts[u].size() / SG_ITER_WORDS;
-        memcpy(dst, parts[u].data(), parts[u].size() * sizeof(uint32_t));
-        fill_pad_iters(dst + nu * SG_ITER_WORDS, ipc - nu, pad);
+        uint32_t* d1 = entries + u * ipc * SG_ITER_WORDS;
+        uint32_t* d2 = d1 + ipc1 * SG_ITER_WORDS;
+        const int64_t n1 = (int64_t)p1[u].size() / SG_ITER_WORDS, n2 = (int64_t)p2[u].size() / SG_ITER_WORDS;
+        memcpy(d1, p1[u].data(), p1[u].size() * sizeof(uint32_t));
+        fill_pad_iters(d1 + n1 * SG_ITER_WORDS, ipc1 - n1, pad);
+        memcpy(d2, p2[u].data(), p2[u].size() * sizeof(uint32_t));
+        fill_pad_iters(d2 + n2 * SG_ITER_WORDS, ipc2 - n2, pad);
     }
     return VQ2_OK;
 }

@@ -42,6 +42,9 @@ namespace vq2 {
 struct SortedPoolArgs {
     const uint32_t* ent;
     const void* scale;  // [n_experts, rows]
+    const void* cb1;    // stage-2 codebook (two-stage pools), else nullptr
+    uint32_t c1mask;    // stage-2 code mask: 0xFFFF, or 0xFF for the 256-row codebook of (16,8)
+    int32_t ipc1;       // stage-1 iterations of a chunk (the stage-2 ones follow)
     int32_t ipc;        // iterations per chunk (every chunk padded to it)
     int s_dt;
     int32_t n_iters;
@@ -274,7 +277,8 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
         const int s0 = c_beg + slice * a.sq + min(slice, a.sr);
         const int s1 = s0 + a.sq + (slice < a.sr ? 1 : 0);
-        pipe.load_entries(pl.ent, a.cb, nullptr, c_beg, c_beg + pl.ipc, s0, s1, wave, lane, pl.gbits, R);
+        pipe.load_entries(pl.ent, a.cb, pl.cb1, c_beg, c_beg + pl.ipc1, s0, s1, wave, lane, pl.gbits, R,
+                          pl.c1mask);
     };
     float* acc = sorted_acc(s_acc, wave, lane, R);
     bool bad = false;
@@ -642,7 +646,17 @@ static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_exper
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: entries (16-byte aligned) and scales are required",
                          name);
     if (!dt_ok(pc.scale_dt)) return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s: bad scale dtype", name);
+    if (pc.s2 < 0 || pc.s2 > 2 || pc.stage1_iters < 1 || pc.stage1_iters > pc.iters_per_chunk ||
+        (pc.s2 == 0 && pc.stage1_iters != pc.iters_per_chunk))
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: %lld stage-1 iterations of %lld (stage-2 kind %d)",
+                         name, (long long)pc.stage1_iters, (long long)pc.iters_per_chunk, pc.s2);
+    if (pc.s2 && (!pc.cb1 || (uintptr_t)pc.cb1 % 16))
+        return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool: a stage-2 pool needs its codebook (16-byte aligned)",
+                         name);
     pa.ent = pc.entries;
+    pa.cb1 = pc.s2 ? pc.cb1 : nullptr;
+    pa.c1mask = pc.s2 == 2 ? 0xFFu : 0xFFFFu;
+    pa.ipc1 = (int32_t)pc.stage1_iters;
     pa.ipc = (int32_t)pc.iters_per_chunk;
     pa.scale = pc.scale;
     pa.s_dt = pc.scale_dt;

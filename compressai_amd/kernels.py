@@ -681,19 +681,31 @@ def vq_sorted_gemm_batch_argmax(x, planes, scale, cb0, cb1, n, rs=1.0):
 
 # ------------------------------------------------ MoE over sorted expert pools
 class SortedPool:
-    """Code-sorted layout of an expert pool idx [E, rows, n/8] (int16, 2 bpw;
-    vq2_sorted_pack_pool): every expert packed like a SortedPlanes matrix
-    with one chunk height, experts one after another, every chunk padded to
-    the same iteration count (so the kernels compute a chunk's offset
-    instead of reading it).  Built once at load time by the expert modules;
-    the pool stays the public format."""
+    """Code-sorted layout of an expert pool idx [E, rows, n/8] (int16 stage-1
+    plane) with an optional stage-2 plane idx1 of the same shape (int16 for
+    (16,16), uint8 for the (16,8) 3 bpw experts; vq2_sorted_pack_pool): every
+    expert packed like a SortedPlanes matrix with one chunk height, experts
+    one after another, every chunk padded to the same iteration counts (so
+    the kernels compute a chunk's offset instead of reading it).  Built once
+    at load time by the expert modules; the pool stays the public format.
+    ``SortedPool.slots`` makes an empty (zeroed) pool of the same layout for
+    a paged slot pool whose records are copied in later."""
 
-    def __init__(self, idx, device=None, threads=0):
+    def __init__(self, idx, device=None, threads=0, idx1=None):
         lib = _lib.load()
         idx = _idx16(idx, "idx")
         if idx.dim() != 3:
             raise Vq2Error(f"expert pool must be [E, rows, ng], got {tuple(idx.shape)}")
         E, rows, ng = (int(v) for v in idx.shape)
+        self.s2_kind = 0
+        h1 = None
+        if idx1 is not None:
+            if tuple(idx1.shape) != tuple(idx.shape):
+                raise Vq2Error(f"idx1 must be {tuple(idx.shape)}, got {tuple(idx1.shape)}")
+            self.s2_kind = 2 if idx1.dtype == torch.uint8 else 1
+            if self.s2_kind == 1:
+                idx1 = _idx16(idx1, "idx1")
+            h1 = idx1.detach().to("cpu").to(torch.int16).contiguous()
         R = int(lib.vq2_sorted_rows_per_chunk(rows, ng, 1))
         if R == 0:
             raise Vq2Error(f"sorted layout: ng={ng} unsupported")
@@ -701,12 +713,13 @@ class SortedPool:
         self.chunks = -(-rows // R)
         dev = torch.device(device) if device is not None else idx.device
         h = idx.detach().to("cpu").contiguous()
-        cap = E * self.chunks * (-(-R * ng // 240) + 8)
-        ipc = ctypes.c_int64(0)
-        n_iters = ctypes.c_int64(0)
+        stages = 2 if h1 is not None else 1
+        cap = E * self.chunks * stages * (-(-R * ng // 240) + 8)
+        ipc, ipc1, n_iters = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
         for _ in range(2):
             entries = torch.empty(cap * ITER_WORDS, dtype=torch.int32)
-            st = lib.vq2_sorted_pack_pool(h.data_ptr(), E, rows, ng, R, entries.data_ptr(), cap, ctypes.byref(ipc),
+            st = lib.vq2_sorted_pack_pool(h.data_ptr(), None if h1 is None else h1.data_ptr(), E, rows, ng, R,
+                                          entries.data_ptr(), cap, ctypes.byref(ipc), ctypes.byref(ipc1),
                                           ctypes.byref(n_iters), int(threads))
             if st == _lib.ERR_ARG and n_iters.value > cap:
                 cap = n_iters.value
@@ -714,16 +727,46 @@ class SortedPool:
             _lib.check(st, "vq2_sorted_pack_pool")
             break
         self.n_iters = int(n_iters.value)
-        self.iters_per_chunk = int(ipc.value)
+        self.iters_per_chunk, self.stage1_iters = int(ipc.value), int(ipc1.value)
         self.entries = entries[: self.n_iters * ITER_WORDS].to(dev)
         self.device = dev
 
-    def pool(self, scale) -> "_lib.SortedPool":
+    @classmethod
+    def slots(cls, like: "SortedPool", capacity: int, device=None):
+        """An empty pool of `capacity` experts in the layout of `like` (the
+        same chunking and iteration counts), zeroed: entry words that decode
+        to code 0 at row 0, group 0 of every chunk, so a slot read before its
+        record arrives gives finite values, never an out-of-range access."""
+        self = cls.__new__(cls)
+        for k in ("rows", "ng", "rows_per_chunk", "chunks", "iters_per_chunk", "stage1_iters", "s2_kind"):
+            setattr(self, k, getattr(like, k))
+        self.n_experts = int(capacity)
+        self.n_iters = self.n_experts * self.chunks * self.iters_per_chunk
+        dev = torch.device(device) if device is not None else like.device
+        self.entries = torch.zeros(self.n_iters * ITER_WORDS, dtype=torch.int32, device=dev)
+        self.device = dev
+        return self
+
+    def expert_words(self):
+        """uint32 words of one expert's chunks (the unit a slot copy moves)."""
+        return self.chunks * self.iters_per_chunk * ITER_WORDS
+
+    @property
+    def has_stage2(self):
+        return self.s2_kind != 0
+
+    def pool(self, scale, cb1=None) -> "_lib.SortedPool":
         _contig(scale, "scale")
         if scale.numel() != self.n_experts * self.rows:
             raise Vq2Error(f"scale must hold [{self.n_experts}, {self.rows}] values")
+        if self.s2_kind:
+            rows = 256 if self.s2_kind == 2 else 65536
+            if cb1 is None or cb1.dim() != 2 or cb1.shape[0] < rows or cb1.shape[1] != 8:
+                raise Vq2Error(f"a two-stage pool needs its stage-2 codebook [{rows}, 8]")
+            _contig(cb1, "cb1")
         return _lib.SortedPool(self.entries.data_ptr(), self.iters_per_chunk, self.n_iters, self.rows_per_chunk,
-                               self.rows, self.ng, scale.data_ptr(), _dt(scale, "scale"))
+                               self.rows, self.ng, scale.data_ptr(), _dt(scale, "scale"), self.stage1_iters,
+                               self.s2_kind, _p(cb1) if self.s2_kind else None)
 
     def nbytes(self):
         return self.entries.numel() * self.entries.element_size()
@@ -765,7 +808,7 @@ def _rot_tables(rot, n, what):
 
 def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, cb, rot_h, rot_i, *, ids=None,
                   w=None, logits=None, top_k=None, shared_id=None, shared_gate=None, out_dtype=torch.float32,
-                  out=None, slices=None):
+                  out=None, slices=None, cb1=None):
     """The experts of an MoE layer over code-sorted pools, two launches
     (gate_up and down in one, then the combine; three at other widths or
     above 127 pairs); a one-launch wait that gives up leaves its pair NaN
@@ -775,7 +818,8 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
     the router is built in (top_k routed experts plus the shared expert
     shared_id with sigmoid(shared_gate . h_t)); it then returns
     (out, ids int32 [T, top_k + 1], w fp32 [T, top_k + 1]).  rot_h / rot_i:
-    (perm int32, sign int8, hb, scale)."""
+    (perm int32, sign int8, hb, scale).  Two-stage pools (the (16,8) 3 bpw
+    experts) take their stage-2 codebook cb1 ([256, 8] in cb's dtype)."""
     H = gate_up.ng * 8
     I = down.ng * 8
     if gate_up.rows != 2 * I or down.rows != H or gate_up.n_experts != down.n_experts:
@@ -789,7 +833,7 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
             raise Vq2Error("vq_sorted_moe: the built-in router needs top_k, shared_id and shared_gate")
         _gate_vec(shared_gate, H)
     dev = _dev(h2, cb, gu_scale, dn_scale, ids, w, logits, gate_up.entries, down.entries, rot_h[0], rot_h[1],
-               rot_i[0], rot_i[1], shared_gate if logits is not None else None)
+               rot_i[0], rot_i[1], shared_gate if logits is not None else None, cb1)
     _contig(cb, "cb")
     if cb.dim() != 2 or cb.shape[0] < 65536 or cb.shape[1] != 8 or cb.dtype not in (torch.float16, torch.bfloat16):
         raise Vq2Error("vq_sorted_moe: cb must be an fp16 / bf16 [65536, 8] codebook")
@@ -820,13 +864,16 @@ def vq_sorted_moe(h, gate_up: SortedPool, gu_scale, down: SortedPool, dn_scale, 
         # the library runs gate_up and down as one launch for these shapes
         # (2048-point and 512-point rotations, at most 128 pairs)
         one = H == 2048 and I == 512 and int(rot_h[2]) == 2048 and int(rot_i[2]) == 512 and T * P <= 127
-        sg = moe_slices(T * P * gate_up.chunks, gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0], one)
-        sd = moe_slices(T * P * down.chunks, down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1], one)
+        st = 2 if gate_up.has_stage2 else 1
+        sg = moe_slices(T * P * gate_up.chunks, st * gate_up.rows_per_chunk * gate_up.ng, cu, _MOE_FIXED_US[0], one)
+        sd = moe_slices(T * P * down.chunks, st * down.rows_per_chunk * down.ng, cu, _MOE_FIXED_US[1], one)
     else:
         sg, sd = (int(v) for v in slices)
     lib = _lib.load()
     ws = _workspace(dev, int(lib.vq2_sorted_moe_workspace(T, P, H, I, sg, sd)), sorted_kind=True)
-    gp, dp = gate_up.pool(gu_scale), down.pool(dn_scale)
+    if cb1 is not None and cb1.dtype != cb.dtype:
+        raise Vq2Error("vq_sorted_moe: cb1 must have cb's dtype")
+    gp, dp = gate_up.pool(gu_scale, cb1), down.pool(dn_scale, cb1)
     _lib.call("vq2_sorted_moe", _p(h2), _dt(h2, "h"), T, P, ids_p, ids64, w_p,
               _p(lg) if router else None, _dt(lg, "logits") if router else 0, lg.shape[1] if router else 0,
               int(top_k) if router else 0, int(shared_id) if router else 0, _p(shared_gate) if router else None,

@@ -449,17 +449,20 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
 
 /* ---- MoE experts over code-sorted expert pools -------------------------
  * vq2_sorted_pack_pool (host memory, no GPU work) packs an expert pool
- * idx [n_experts, rows, ng] (one int16 plane, 2 bpw) expert by expert, each
- * as vq2_sorted_pack packs a matrix with the same rows_per_chunk R, and pads
- * every chunk (dummy-row entries) to the pool's largest iteration
- * count *iters_per_chunk, so chunk c of expert e holds iterations
- * [(e * C + c) * ipc, (e * C + c + 1) * ipc), C = ceil(rows / R).
- * *n_iters = n_experts * C * ipc; capacity as vq2_sorted_pack.  No
- * reference counterpart (a load-time transform of the pools
- * PackedMoEExpertUniversal holds, vq2/load_and_test_full_35b.py:31-47). */
-int vq2_sorted_pack_pool(const int16_t* idx, int64_t n_experts, int64_t rows, int64_t ng, int64_t rows_per_chunk,
-                         uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* n_iters,
-                         int n_threads);
+ * idx [n_experts, rows, ng] (the int16 stage-1 plane; idx1, the stage-2
+ * plane as int16 -- a (16,8) uint8 plane widened to values 0..255 -- or
+ * NULL) expert by expert, each as vq2_sorted_pack packs a matrix with the
+ * same rows_per_chunk R, and pads every chunk's stage-1 and stage-2 entries
+ * (dummy-row entries) to the pool's largest counts, so chunk c of expert e
+ * holds iterations [(e * C + c) * ipc, (e * C + c + 1) * ipc), C =
+ * ceil(rows / R), its stage-2 ones from *stage1_iters on.  *n_iters =
+ * n_experts * C * ipc; capacity as vq2_sorted_pack.  No reference
+ * counterpart (a load-time transform of the pools PackedMoEExpertUniversal
+ * holds, vq2/load_and_test_full_35b.py:31-47, and of the promoted 3 bpw
+ * experts of vq2/paged_runtime.py:357-389). */
+int vq2_sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts, int64_t rows, int64_t ng,
+                         int64_t rows_per_chunk, uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk,
+                         int64_t* stage1_iters, int64_t* n_iters, int n_threads);
 
 /* One packed expert pool (device pointers, except the struct). */
 typedef struct vq2_sorted_pool {
@@ -471,6 +474,10 @@ typedef struct vq2_sorted_pool {
     int64_t ng;               /* groups per row (input width / 8)              */
     const void* scale;        /* [n_experts, rows], dtype scale_dt             */
     int scale_dt;
+    int64_t stage1_iters;     /* = iters_per_chunk without a stage 2           */
+    int has_stage2;           /* 0; 1: int16 stage 2, cb1 [65536, 8]; 2: the
+                                 uint8 stage 2 of (16,8), cb1 [256, 8]         */
+    const void* cb1;          /* stage-2 codebook in the dtype of cb, or NULL  */
 } vq2_sorted_pool;
 
 /* The permutation, signs, block size and scale of one rotation. */

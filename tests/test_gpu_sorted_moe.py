@@ -191,3 +191,37 @@ def test_sorted_moe_router_ids_and_weights(dev, T):
     again = m.experts(h, rid, rw)
     assert torch.equal(out, again)
     assert torch.equal(layer(h, logits), out)
+
+
+@pytest.mark.parametrize("T,P", [(1, 4), (3, 5)])
+def test_sorted_moe_16_8_pools_vs_oracle(dev, T, P):
+    """Promoted 3 bpw (16,8) experts on two-stage sorted pools: stage-1
+    entries gather from the 65536-row codebook, stage-2 entries from the
+    [256, 8] stage-2 codebook; gate_up and down in one launch, then the
+    combine, against the fp64 oracle."""
+    from compressai_amd.rot import get_rot
+
+    E = 6
+    cb = synth.codebook(9980)
+    cb8 = synth.codebook(9981, 256)
+    gu, gus, dn, dns = _pools(9980, E)
+    g8 = synth.gen(9982)
+    gu1 = torch.randint(0, 256, (E, 1024, 256), generator=g8, dtype=torch.int32).to(torch.uint8)
+    dn1 = torch.randint(0, 256, (E, 2048, 64), generator=g8, dtype=torch.int32).to(torch.uint8)
+    gup = K.SortedPool(gu, device=dev, idx1=gu1)
+    dnp = K.SortedPool(dn, device=dev, idx1=dn1)
+    assert gup.s2_kind == 2 and dnp.s2_kind == 2
+    rh, ri = get_rot("moe_expert_2048", 2048, dev), get_rot("moe_expert_512", 512, dev)
+    h = synth.activations(9983 + T, (T, 2048), dtype=torch.float16)
+    ids = torch.stack([torch.randperm(E, generator=synth.gen(9984 + t))[:P] for t in range(T)]).to(torch.int32)
+    w = torch.softmax(synth.activations(9990 + T, (T, P)).float(), -1)
+    out = K.vq_sorted_moe(h.to(dev), gup, gus.to(dev), dnp, dns.to(dev), cb.to(dev),
+                          (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale),
+                          ids=ids.to(dev), w=w.to(dev), cb1=cb8.to(dev))
+    ref = O.moe_experts(h, ids.numpy(), w.numpy(), lambda e: (gu[e], gu1[e], gus[e], dn[e], dn1[e], dns[e]), cb, cb8,
+                        *_rot_np(rh), *_rot_np(ri))
+    assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
+    with pytest.raises(K.Vq2Error):  # a two-stage pool without its codebook
+        K.vq_sorted_moe(h.to(dev), gup, gus.to(dev), dnp, dns.to(dev), cb.to(dev),
+                        (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale),
+                        ids=ids.to(dev), w=w.to(dev))

@@ -213,3 +213,46 @@ def test_moe_slices_cost_model():
     assert moe_slices(81, 228 * 64, 256, 2.0) == 3
     assert moe_slices(360, 205 * 256, 256, 2.5) == 2
     assert moe_slices(648, 228 * 64, 256, 2.0) == 1
+
+
+@pytest.mark.parametrize("s2", ["u8", "i16"])
+def test_sorted_two_stage_pool_equals_per_expert_pack(s2):
+    """A two-stage pool ((16,8) uint8 or (16,16) int16 stage 2): every chunk
+    holds the expert's stage-1 iterations as vq2_sorted_pack packs them,
+    padded to the pool's stage-1 count, then its stage-2 iterations, padded
+    to the pool's stage-2 count."""
+    from compressai_amd.kernels import SortedPool
+
+    E, rows, n = 3, 300, 512
+    ng = n // 8
+    idx = synth.indices16(9960, (E, rows, ng))
+    if s2 == "u8":
+        idx1 = torch.randint(0, 256, (E, rows, ng), generator=synth.gen(9961), dtype=torch.int32).to(torch.uint8)
+    else:
+        idx1 = synth.indices16(9961, (E, rows, ng))
+    pool = SortedPool(idx, device="cpu", threads=2, idx1=idx1)
+    assert pool.s2_kind == (2 if s2 == "u8" else 1)
+    C, R, ipc, ipc1 = pool.chunks, pool.rows_per_chunk, pool.iters_per_chunk, pool.stage1_iters
+    assert 0 < ipc1 < ipc and pool.n_iters == E * C * ipc
+    W = ITER_WORDS
+    ent = pool.entries.numpy().view(np.uint32)
+    pad = np.uint32(R << _gb(ng))
+    pad_lane = np.array([pad | (pad << 16), pad | (pad << 16), 0], np.uint32)
+
+    def is_pad(words):
+        t = words.reshape(-1, 64, 3)
+        return np.all(t[:, :63] == pad_lane) and np.all(t[:, 63] == 0)
+
+    for e in range(E):
+        sp = SortedPlanes(idx[e], idx1[e], rows, n, device="cpu", chunk_align=1)
+        own = sp.entries.numpy().view(np.uint32)
+        ie, ie1 = sp.iters_per_chunk, sp.stage1_iters
+        for c in range(C):
+            got = ent[(e * C + c) * ipc * W:(e * C + c + 1) * ipc * W]
+            o1 = own[c * ie * W:(c * ie + ie1) * W]
+            o2 = own[(c * ie + ie1) * W:(c + 1) * ie * W]
+            g1, g2 = got[:ipc1 * W], got[ipc1 * W:]
+            assert np.array_equal(g1[:len(o1)], o1) and is_pad(g1[len(o1):])
+            assert np.array_equal(g2[:len(o2)], o2) and is_pad(g2[len(o2):])
+    empty = SortedPool.slots(pool, 5)
+    assert empty.n_iters == 5 * C * ipc and empty.stage1_iters == ipc1 and int(empty.entries.abs().sum()) == 0
