@@ -534,10 +534,14 @@ def bench_paged(args, dev, E=64, steps=200):
         ids = torch.stack([torch.randperm(E, generator=g)[:8] for _ in range(steps)]).to(dev)
         w = torch.full((1, 8), 1.0 / 8, device=dev)
         h = synth.activations(7004, (1, 2048), dtype=torch.float16).to(dev)
-        for name, cap, on_dev in (("warm", E, False), ("churn", 16, False), ("warm_device", E, True),
-                                  ("churn_device", 16, True)):
+        # device pager: sorted slot pool and one-launch sorted MoE (the
+        # default), and the reference-layout slots on the gather kernels
+        for name, cap, on_dev, srt in (("warm", E, False, None), ("churn", 16, False, None),
+                                       ("warm_device", E, True, None), ("churn_device", 16, True, None),
+                                       ("warm_device_gather_kernels", E, True, False)):
             layer = paged.PagedMoEExperts(0, store, cb, capacity=cap, device=dev, out_dtype=torch.float32,
-                                          device_tables=on_dev)
+                                          device_tables=on_dev, sorted_layout=srt)
+            rec = layer.pager.mirror_record_bytes if layer.pager.sorted_layout else store.record_bytes
             for s_ in range(min(steps, 2 * E)):  # fill the pool / reach the steady state
                 layer(h, ids[s_ % steps].view(1, 8), w)
             torch.cuda.synchronize(dev)
@@ -558,7 +562,7 @@ def bench_paged(args, dev, E=64, steps=200):
                 reps = 1
             misses = (layer.pager.misses - m0) / reps
             res[name] = {"us_per_layer": round(dt * 1e6 / steps, 2), "misses_per_step": round(misses / steps, 2),
-                         "feed_gbps": round(misses * store.record_bytes / dt / 1e9, 2)}
+                         "feed_gbps": round(misses * rec / dt / 1e9, 2), "record_bytes": rec}
             log(f"paged MoE ({name}, {cap} slots of {E}): {res[name]['us_per_layer']:.1f} us/layer, "
                 f"{res[name]['misses_per_step']:.2f} misses/step, {res[name]['feed_gbps']:.2f} GB/s fed")
             del layer

@@ -216,17 +216,29 @@ class ExpertPager:
     graph.  The least recently used slot a step does not need is replaced,
     as on the host; an expert id outside the layer, or more distinct experts
     in a step than slots, gives NaN rows and sets ``errors`` (bit 1 / bit 2)
-    instead of raising."""
+    instead of raising.
+
+    ``sorted_layout=True`` (with device tables): the mirror holds every
+    expert of the layer in the code-sorted layout (packed here once, all
+    experts with the layer's common iteration counts) and the slots are a
+    sorted pool (``sorted_gu`` / ``sorted_dn``) that the one-launch sorted
+    MoE reads; the copy kernel moves a sorted record (~1.5x the bytes of a
+    container record) per miss.  The reference-layout slot pools are not
+    allocated then."""
 
     def __init__(self, store: Vq2mStore, layer: int, capacity: int, device, staging: int = 16,
-                 scale_dtype=torch.bfloat16, device_tables: bool = False):
+                 scale_dtype=torch.bfloat16, device_tables: bool = False, sorted_layout: bool = False):
         self.store, self.layer, self.capacity = store, int(layer), int(capacity)
         self.device = torch.device(device)
         s = store
         sdt = scale_dtype or torch.float16
-        self.pool_gu_idx = torch.empty((capacity, s.gu_rows, s.gu_cols), dtype=torch.int16, device=self.device)
+        self.sorted_layout = bool(sorted_layout)
+        if self.sorted_layout and not device_tables:
+            raise K.Vq2Error("the sorted slot pool is paged on the device: pass device_tables=True")
+        if not self.sorted_layout:
+            self.pool_gu_idx = torch.empty((capacity, s.gu_rows, s.gu_cols), dtype=torch.int16, device=self.device)
+            self.pool_dn_idx = torch.empty((capacity, s.dn_rows, s.dn_cols), dtype=torch.int16, device=self.device)
         self.pool_gu_scale = torch.empty((capacity, s.gu_rows), dtype=sdt, device=self.device)
-        self.pool_dn_idx = torch.empty((capacity, s.dn_rows, s.dn_cols), dtype=torch.int16, device=self.device)
         self.pool_dn_scale = torch.empty((capacity, s.dn_rows), dtype=sdt, device=self.device)
         self.slot_of: OrderedDict[int, int] = OrderedDict()  # expert -> slot, least recently used first
         self.free = list(range(capacity - 1, -1, -1))
@@ -252,20 +264,56 @@ class ExpertPager:
         if s.promoted_experts(self.layer):
             raise K.Vq2Error(f"layer {self.layer} holds promoted 3-bit experts: use the host pager")
         E, C = s.num_experts, self.capacity
-        self.mirror = torch.empty((E, s.record_bytes), dtype=torch.uint8, pin_memory=True)
-        for e in range(E):
-            s.read_record(self.layer, e, memoryview(self.mirror[e].numpy()))
+        if self.sorted_layout:
+            self._init_sorted_mirror()
+        else:
+            self.mirror = torch.empty((E, s.record_bytes), dtype=torch.uint8, pin_memory=True)
+            for e in range(E):
+                s.read_record(self.layer, e, memoryview(self.mirror[e].numpy()))
+            self._seg = (ctypes.c_int64 * 4)(*s.sizes)
+            pools = (self.pool_gu_idx, self.pool_gu_scale, self.pool_dn_idx, self.pool_dn_scale)
         i32 = dict(dtype=torch.int32, device=dev)
         self.d_slot_of = torch.full((E,), -1, **i32)
         self.d_expert_of = torch.full((C,), -1, **i32)
         self.d_stamp = torch.full((C,), -1, **i32)
         self.d_state = torch.zeros(5, **i32)
-        self._seg = (ctypes.c_int64 * 4)(*s.sizes)
-        pools = (self.pool_gu_idx, self.pool_gu_scale, self.pool_dn_idx, self.pool_dn_scale)
-        self._dst = (ctypes.c_void_p * 4)(*[t.data_ptr() for t in pools])
-        self._dst_stride = (ctypes.c_int64 * 4)(*[t[0].numel() * t.element_size() for t in pools])
+        if self.sorted_layout:
+            gw, dw = self.sorted_gu.expert_words() * 4, self.sorted_dn.expert_words() * 4
+            self._dst = (ctypes.c_void_p * 4)(self.sorted_gu.entries.data_ptr(), self.pool_gu_scale.data_ptr(),
+                                              self.sorted_dn.entries.data_ptr(), self.pool_dn_scale.data_ptr())
+            self._dst_stride = (ctypes.c_int64 * 4)(gw, self.pool_gu_scale[0].numel() * self.pool_gu_scale.element_size(),
+                                                    dw, self.pool_dn_scale[0].numel() * self.pool_dn_scale.element_size())
+        else:
+            self._dst = (ctypes.c_void_p * 4)(*[t.data_ptr() for t in pools])
+            self._dst_stride = (ctypes.c_int64 * 4)(*[t[0].numel() * t.element_size() for t in pools])
         self._scale_dt = K._dt(self.pool_gu_scale, "scale")
         self._bufs = {}
+
+    def _init_sorted_mirror(self):
+        """Every expert of the layer in the code-sorted layout, in a pinned
+        mirror of records [gate_up entries | gate_up fp16 scales | down
+        entries | down fp16 scales], and the empty sorted slot pools."""
+        s, E = self.store, self.store.num_experts
+        raw = torch.empty((E, s.record_bytes), dtype=torch.uint8)
+        for e in range(E):
+            s.read_record(self.layer, e, memoryview(raw[e].numpy()))
+        a, b, c = s.sizes[0], s.sizes[0] + s.sizes[1], s.sizes[0] + s.sizes[1] + s.sizes[2]
+        gu = raw[:, :a].contiguous().view(torch.int16).view(E, s.gu_rows, s.gu_cols)
+        dn = raw[:, b:c].contiguous().view(torch.int16).view(E, s.dn_rows, s.dn_cols)
+        pgu = K.SortedPool(gu, device="cpu")
+        pdn = K.SortedPool(dn, device="cpu")
+        gw, dw = pgu.expert_words(), pdn.expert_words()
+        sizes = (gw * 4, s.sizes[1], dw * 4, s.sizes[3])
+        self._seg = (ctypes.c_int64 * 4)(*sizes)
+        self.mirror_record_bytes = sum(sizes)
+        self.mirror = torch.empty((E, self.mirror_record_bytes), dtype=torch.uint8, pin_memory=True)
+        o1, o2, o3 = sizes[0], sizes[0] + sizes[1], sizes[0] + sizes[1] + sizes[2]
+        self.mirror[:, :o1].copy_(pgu.entries.view(E, gw).view(torch.uint8).view(E, -1))
+        self.mirror[:, o1:o2].copy_(raw[:, a:b])
+        self.mirror[:, o2:o3].copy_(pdn.entries.view(E, dw).view(torch.uint8).view(E, -1))
+        self.mirror[:, o3:].copy_(raw[:, c:])
+        self.sorted_gu = K.SortedPool.slots(pgu, self.capacity, self.device)
+        self.sorted_dn = K.SortedPool.slots(pdn, self.capacity, self.device)
 
     def step(self, ids):
         """Slots of a step's routed ids (device int32 / int64 [T, P]) ->
@@ -286,7 +334,8 @@ class ExpertPager:
         K._lib.call("vq2_pager_step", ids.data_ptr(), i64, n, E, self.capacity, self.d_slot_of.data_ptr(),
                     self.d_expert_of.data_ptr(), self.d_stamp.data_ptr(), self.d_state.data_ptr(),
                     copy_list.data_ptr(), pair_slot.data_ptr(), st)
-        K._lib.call("vq2_pager_copy", self.mirror.data_ptr(), self.store.record_bytes, self._seg,
+        rec = self.mirror_record_bytes if self.sorted_layout else self.store.record_bytes
+        K._lib.call("vq2_pager_copy", self.mirror.data_ptr(), rec, self._seg,
                     copy_list.data_ptr(), self.d_state.data_ptr(), n, self._dst, self._dst_stride, self._scale_dt, st)
         return pair_slot.view(ids.shape)
 
@@ -390,15 +439,21 @@ class PagedMoEExperts(torch.nn.Module):
 
     def __init__(self, layer: int, store: Vq2mStore, cb16, capacity: int = 96, device="cuda", staging: int = 16,
                  act_dtype=torch.float32, out_dtype=None, cb8=None, scale_dtype=torch.bfloat16,
-                 device_tables: bool = False):
+                 device_tables: bool = False, sorted_layout=None):
         super().__init__()
-        self.pager = ExpertPager(store, layer, capacity, device, staging, scale_dtype, device_tables)
+        dev = torch.device(device)
+        H, I = store.gu_cols * 8, store.dn_cols * 8
+        if sorted_layout is None:  # the device pager over a sorted slot pool where the sorted MoE runs
+            sorted_layout = (device_tables and dev.type == "cuda" and act_dtype == torch.float32
+                             and cb16.dtype in (torch.float16, torch.bfloat16) and H % 64 == 0 and I % 64 == 0
+                             and H <= 8192 and I <= 8192 and not store.promoted_experts(layer))
+        self.pager = ExpertPager(store, layer, capacity, device, staging, scale_dtype, device_tables,
+                                 sorted_layout=bool(sorted_layout))
         self.cb16 = cb16
-        self.hidden_dim = store.gu_cols * 8
-        self.intermediate_dim = store.dn_cols * 8
+        self.hidden_dim = H
+        self.intermediate_dim = I
         if store.gu_rows != 2 * self.intermediate_dim or store.dn_rows != self.hidden_dim:
             raise K.Vq2Error("inconsistent gate_up / down shapes in the container")
-        dev = torch.device(device)
         self.rot_h = get_rot("moe_expert_2048", self.hidden_dim, dev)
         self.rot_i = get_rot("moe_expert_512", self.intermediate_dim, dev)
         self.act_dtype = act_dtype
@@ -417,6 +472,13 @@ class PagedMoEExperts(torch.nn.Module):
                 for k in ("gu_s", "dn_s"):
                     self.pro[k] = self.pro[k].to(scale_dtype)
             self.cb8 = cb8
+            # the promoted pool also in the two-stage sorted layout, where the
+            # one-launch sorted MoE runs (stage-2 codes into cb8)
+            self.pro_sorted = None
+            if (dev.type == "cuda" and act_dtype == torch.float32 and cb16.dtype in (torch.float16, torch.bfloat16)
+                    and cb8.dtype == cb16.dtype and self.hidden_dim % 64 == 0 and self.intermediate_dim % 64 == 0):
+                self.pro_sorted = (K.SortedPool(self.pro["gu0"], device=dev, idx1=self.pro["gu1"]),
+                                   K.SortedPool(self.pro["dn0"], device=dev, idx1=self.pro["dn1"]))
 
     def _run(self, h, ids_d, w_d, pool, accumulate_into=None):
         """Two launches over one pool: gate_up with the H-point RHT, then
@@ -461,6 +523,12 @@ class PagedMoEExperts(torch.nn.Module):
             P = ids_d.shape[1]
             w = topk_weights.reshape(T, P).to(device=h.device, dtype=torch.float32).contiguous()
             slots = p.step(ids_d.to(h.device))
+            if p.sorted_layout:
+                rh, ri = self.rot_h, self.rot_i
+                out = K.vq_sorted_moe(h, p.sorted_gu, p.pool_gu_scale, p.sorted_dn, p.pool_dn_scale, self.cb16,
+                                      (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale),
+                                      ids=slots, w=w)
+                return out.to(self.out_dtype or hidden_states.dtype)
             regular = (p.pool_gu_idx, None, p.pool_gu_scale, p.pool_dn_idx, None, p.pool_dn_scale)
             return self._run(h, slots, w, regular).to(self.out_dtype or hidden_states.dtype)
         ids_host = topk_idx.reshape(T, -1).to("cpu")  # the paging decision is made on the host
@@ -485,6 +553,16 @@ class PagedMoEExperts(torch.nn.Module):
             out = self._run(h, ids_d, torch.gather(w, 1, cols_d) * mask_d, regular)
         ids_d, cols_d, mask_d = self._table(pro, h.device)
         pp = self.pro
-        out = self._run(h, ids_d, torch.gather(w, 1, cols_d) * mask_d,
-                        (pp["gu0"], pp["gu1"], pp["gu_s"], pp["dn0"], pp["dn1"], pp["dn_s"]), accumulate_into=out)
+        wp = torch.gather(w, 1, cols_d) * mask_d
+        if self.pro_sorted is not None:
+            # promoted pairs on the sorted two-stage pool, added to the 2 bpw
+            # pairs' sum (per token: 2 bpw pairs, then promoted pairs)
+            rh, ri = self.rot_h, self.rot_i
+            out_p = K.vq_sorted_moe(h, self.pro_sorted[0], pp["gu_s"], self.pro_sorted[1], pp["dn_s"], self.cb16,
+                                    (rh._perm32, rh._sign8, rh.hb, rh.scale), (ri._perm32, ri._sign8, ri.hb, ri.scale),
+                                    ids=ids_d, w=wp, cb1=self.cb8)
+            out = out_p if out is None else out + out_p
+        else:
+            out = self._run(h, ids_d, wp, (pp["gu0"], pp["gu1"], pp["gu_s"], pp["dn0"], pp["dn1"], pp["dn_s"]),
+                            accumulate_into=out)
         return out.to(self.out_dtype or hidden_states.dtype)

@@ -67,10 +67,11 @@ class LruModel:
         return [self.slot_of[e] if e >= 0 else -1 for e in pe], [(miss[r], elig[r]) for r in range(served)]
 
 
-def test_device_pager_tables_follow_the_model(dev, tmp_path):
+@pytest.mark.parametrize("sorted_layout", [False, True])
+def test_device_pager_tables_follow_the_model(dev, tmp_path, sorted_layout):
     E, C, T, P = 40, 12, 2, 5
     store, (gui, gus, dni, dns) = _container(tmp_path, E)
-    pager = paged.ExpertPager(store, 0, C, dev, device_tables=True)
+    pager = paged.ExpertPager(store, 0, C, dev, device_tables=True, sorted_layout=sorted_layout)
     model = LruModel(E, C)
     g = torch.Generator().manual_seed(5)
     for step in range(60):
@@ -86,12 +87,22 @@ def test_device_pager_tables_follow_the_model(dev, tmp_path):
         assert pager.d_stamp.cpu().tolist() == model.stamp, step
         st = pager.d_state.cpu().tolist()
         assert st[0] == model.clock and st[1] == len(copies) and st[2:] == [model.hits, model.misses, 0], step
-    # every resident slot holds its expert's record
+    # every resident slot holds its expert's record (sorted: the expert's
+    # chunks as the layer's sorted pool packs them)
+    if sorted_layout:
+        from compressai_amd.kernels import SortedPool
+
+        ref_gu, ref_dn = SortedPool(gui, device="cpu"), SortedPool(dni, device="cpu")
+        gw, dw = ref_gu.expert_words(), ref_dn.expert_words()
     for v, e in enumerate(model.expert_of):
         if e < 0:
             continue
-        assert torch.equal(pager.pool_gu_idx[v].cpu(), gui[e])
-        assert torch.equal(pager.pool_dn_idx[v].cpu(), dni[e])
+        if sorted_layout:
+            assert torch.equal(pager.sorted_gu.entries[v * gw:(v + 1) * gw].cpu(), ref_gu.entries[e * gw:(e + 1) * gw])
+            assert torch.equal(pager.sorted_dn.entries[v * dw:(v + 1) * dw].cpu(), ref_dn.entries[e * dw:(e + 1) * dw])
+        else:
+            assert torch.equal(pager.pool_gu_idx[v].cpu(), gui[e])
+            assert torch.equal(pager.pool_dn_idx[v].cpu(), dni[e])
         assert torch.equal(pager.pool_gu_scale[v].cpu(), gus[e].to(torch.bfloat16))
         assert torch.equal(pager.pool_dn_scale[v].cpu(), dns[e].to(torch.bfloat16))
     store.close()
@@ -119,20 +130,25 @@ def test_device_pager_fp16_scales_and_errors(dev, tmp_path):
     store.close()
 
 
-def test_paged_device_tables_match_resident_pool_and_replay(dev, tmp_path):
+@pytest.mark.parametrize("sorted_layout", [False, True])
+def test_paged_device_tables_match_resident_pool_and_replay(dev, tmp_path, sorted_layout):
     """PagedMoEExperts(device_tables=True) at the config-4 expert shape,
-    6 slots over 16 experts: every step equals the resident pool (gather
-    kernels) bit for bit; a captured graph of 4 steps replays them exactly."""
+    6 slots over 16 experts: every step equals the resident pool bit for bit
+    (gather kernels on reference-layout slots, or the one-launch sorted MoE
+    on a sorted slot pool against the resident sorted pool); a captured graph
+    of 4 steps replays them exactly."""
     from compressai_amd.graph import DecodeStepGraph
     from compressai_amd.moe import ResidentMoEExperts
 
     E = 16
     store, (gui, gus, dni, dns) = _container(tmp_path, E, gu=(1024, 256), dn=(2048, 64), seed=11)
     cb = synth.codebook(4601).to(dev)
-    pg = paged.PagedMoEExperts(0, store, cb, capacity=6, device=dev, out_dtype=torch.float32, device_tables=True)
+    pg = paged.PagedMoEExperts(0, store, cb, capacity=6, device=dev, out_dtype=torch.float32, device_tables=True,
+                               sorted_layout=sorted_layout)
+    assert pg.pager.sorted_layout == sorted_layout
     bf = torch.bfloat16
     res = ResidentMoEExperts.from_pools(gui.to(dev), gus.to(dev, bf), dni.to(dev), dns.to(dev, bf), cb,
-                                        out_dtype=torch.float32, sorted_layout=False)
+                                        out_dtype=torch.float32, sorted_layout=sorted_layout)
     g = torch.Generator().manual_seed(4602)
     steps = []
     for step in range(8):

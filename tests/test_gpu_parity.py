@@ -843,8 +843,10 @@ def test_single_pair_combine_applies_weight(dev, T):
 
 def test_paged_promoted_experts_vs_oracle(dev, tmp_path):
     """A layer with promoted (16,8) experts: steps with mixed, only-promoted
-    and only-2-bpw tokens, all through the two fused launches per pool (the
-    promoted combine adding into the 2 bpw one), against the fp64 oracle."""
+    and only-2-bpw tokens, the 2 bpw pairs through the two fused launches on
+    the paged pool and the promoted pairs through the one-launch sorted MoE
+    on the two-stage sorted pool (added to the 2 bpw sum), against the fp64
+    oracle."""
     from compressai_amd import paged
 
     E = 12
@@ -863,6 +865,7 @@ def test_paged_promoted_experts_vs_oracle(dev, tmp_path):
     store = paged.Vq2mStore(path)
     pg = paged.PagedMoEExperts(0, store, cb.to(dev), capacity=4, device=dev, staging=2, out_dtype=torch.float32,
                                cb8=cb8.to(dev))
+    assert pg.pro_sorted is not None and pg.pro_sorted[0].s2_kind == 2  # promoted pairs on the sorted path
     ph, sh = _rot_np(pg.rot_h)
     pi, si = _rot_np(pg.rot_i)
 
