@@ -27,6 +27,7 @@ is selectable (``out_dtype``; bf16 by default, as in the reference).
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -336,16 +337,87 @@ def vq_gemm_small_m(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=to
     return y
 
 
+# ------------------------------------------ sorted copies behind the function entries
+# The function-level drop-in (vq_gemv_16 / _16_8 / _16_16, the names a caller
+# swaps in for vq2.kernels) has no module to hold a code-sorted copy, so at
+# batch 1 it keeps one per index plane of at least SORTED_CACHE_MIN_CODES
+# codes, built on the first call (a host repack, ~20 ms for 3 M codes).  An
+# entry is used only for the same tensor object (a weak reference: a freed
+# plane drops its entry) with an unchanged version counter (an in-place write
+# makes a new copy), so a view made anew on every call, or any other plane,
+# takes the gather kernel.  The reference's PackedLinear passes its own
+# buffers (vq2/runtime.py:93-104), which hit.
+SORTED_CACHE_MIN_CODES = 2 << 20
+_SORTED_CACHE: dict = {}
+_sorted_cache_on = [True]
+
+
+def sorted_cache_enabled(flag=None) -> bool:
+    """Turn the function entries' sorted copies on / off (None: query);
+    turning them off drops the copies."""
+    if flag is not None:
+        _sorted_cache_on[0] = bool(flag)
+        if not flag:
+            _SORTED_CACHE.clear()
+    return _sorted_cache_on[0]
+
+
+def sorted_cache_bytes() -> int:
+    return sum(e[4].nbytes() for e in _SORTED_CACHE.values())
+
+
+def _cached_sorted(xr, i0, i1, cb0, out, n):
+    """The sorted copy of (i0, i1) for a batch-1 call, or None."""
+    if not _sorted_cache_on[0] or not i0.is_cuda or cb0.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    if xr.numel() != n or int(out) * (int(n) // 8) * (1 if i1 is None else 2) < SORTED_CACHE_MIN_CODES:
+        return None
+    key = id(i0)
+    e = _SORTED_CACHE.get(key)
+    if (e is not None and e[0]() is i0 and e[1] == i0._version and
+            (e[2]() if e[2] is not None else None) is i1 and (i1 is None or e[3] == i1._version)):
+        return e[4]
+    sp = SortedPlanes(i0, i1, int(out), int(n), device=i0.device)
+
+    def drop(ref, key=key):
+        cur = _SORTED_CACHE.get(key)
+        if cur is not None and (cur[0] is ref or cur[2] is ref):
+            del _SORTED_CACHE[key]
+
+    _SORTED_CACHE[key] = (weakref.ref(i0, drop), i0._version, None if i1 is None else weakref.ref(i1, drop),
+                          None if i1 is None else i1._version, sp)
+    return sp
+
+
+def _gemv_entry(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype, y):
+    """The reference-named GEMV entries: batch 1 of a large plane on its
+    sorted copy (pre-rotated x), otherwise the gather kernel."""
+    sp = _cached_sorted(xr, i0, i1, cb0, out, n) if torch.is_tensor(xr) and xr.is_cuda else None
+    if sp is not None:
+        _dev(xr, i0, i1, cb0, cb1, scale, y)
+        if y is not None:
+            _contig(y, "y")
+            if y.numel() != int(out):
+                raise Vq2Error("y has the wrong size")
+        yv = None if y is None else y.reshape(-1)
+        (r,) = vq_sorted_gemv(_contig(xr, "xr").reshape(-1), [(sp, scale)], cb0, cb1, int(n), hb=0, rs=rs,
+                              out_dtype=out_dtype if y is None else y.dtype, ys=None if y is None else [yv])
+        return y if y is not None else r.view(*xr.shape[:-1], int(out))
+    return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
+
+
 def vq_gemv_16(xr, i0, cb0, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
-    """xr [n] -> y [out] for a 2.0 bpw (16,) matrix (vq2/kernels.py:224-230)."""
-    return vq_gemv(xr, i0, None, cb0, None, scale, out, n, rs, out_dtype=out_dtype, y=y)
+    """xr [n] -> y [out] for a 2.0 bpw (16,) matrix (vq2/kernels.py:224-230).
+    Batch 1 of a plane of >= 2 M codes runs on a code-sorted copy of it (see
+    SORTED_CACHE_MIN_CODES)."""
+    return _gemv_entry(xr, i0, None, cb0, None, scale, out, n, rs, out_dtype, y)
 
 
 def vq_gemv_16_8(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
     """xr [n] -> y [out] for a 3.0 bpw (16,8) matrix (vq2/kernels.py:215-221)."""
     if i1.dtype != torch.uint8:
         raise Vq2Error("vq_gemv_16_8: i1 must be uint8")
-    return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
+    return _gemv_entry(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype, y)
 
 
 def vq_gemv_16_16(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torch.bfloat16, y=None):
@@ -353,7 +425,7 @@ def vq_gemv_16_16(xr, i0, i1, cb0, cb1, scale, out, n, rs=1.0, *, out_dtype=torc
     uint16 (the PackedLinear fallback semantics, vq2/runtime.py:82-89)."""
     if i1.dtype == torch.uint8:
         raise Vq2Error("vq_gemv_16_16: i1 must be int16 (uint16 codes)")
-    return vq_gemv(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype=out_dtype, y=y)
+    return _gemv_entry(xr, i0, i1, cb0, cb1, scale, out, n, rs, out_dtype, y)
 
 
 # Largest activation block (batch x n values) whose RHT vq_gemv_rht builds

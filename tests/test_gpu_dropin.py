@@ -325,3 +325,51 @@ def test_packed_projections_rejects_mixed(dev):
     for bad in ([a, b], [a, c], [a] * 5):
         with pytest.raises(K.Vq2Error):
             PackedProjections(bad)
+
+
+def test_function_entries_use_a_sorted_copy_of_large_planes(dev):
+    """vq_gemv_16 / vq_gemv_16_16 (the function-level drop-in) at batch 1 on a
+    plane of >= 2 M codes keep a code-sorted copy of it: the first call packs
+    it, later calls on the same tensor reuse it, an in-place write to the
+    plane makes a fresh copy, a freed plane drops its copy, and the results
+    match the oracle and the gather kernel."""
+    import gc
+
+    out, n = 8192, 2048
+    cb = synth.codebook(9395).to(dev)
+    cb1 = synth.codebook(9396).to(dev)
+    m = synth.vq_matrix(9397, out, n, bpw=4)
+    i0, i1, sc = m["idx0"].to(dev), m["idx1"].to(dev), m["scale"].to(dev)
+    xr = synth.activations(9398, n, dtype=torch.bfloat16).to(dev)
+    K.sorted_cache_enabled(True)
+    before = len(K._SORTED_CACHE)
+    y = K.vq_gemv_16_16(xr, i0, i1, cb, cb1, sc, out, n, out_dtype=torch.float32)
+    assert len(K._SORTED_CACHE) == before + 1
+    sp = K._SORTED_CACHE[id(i0)][4]
+    y2 = K.vq_gemv_16_16(xr, i0, i1, cb, cb1, sc, out, n, out_dtype=torch.float32)
+    assert K._SORTED_CACHE[id(i0)][4] is sp and torch.equal(y, y2)
+    _, y64 = O.vq_gemv(xr.float().cpu()[None], m["idx0"], m["idx1"], cb.cpu(), cb1.cpu(), m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+    yg = K.vq_gemv(xr, i0, i1, cb, cb1, sc, out, n, out_dtype=torch.float32)   # the gather kernel
+    assert O.max_rel_err(y.cpu().numpy(), yg.cpu().numpy()) < 1e-5
+    # an in-place write: a new copy, and the new codes are used
+    i0[0, :8] = 0
+    y3 = K.vq_gemv_16_16(xr, i0, i1, cb, cb1, sc, out, n, out_dtype=torch.float32)
+    assert K._SORTED_CACHE[id(i0)][4] is not sp
+    yg3 = K.vq_gemv(xr, i0, i1, cb, cb1, sc, out, n, out_dtype=torch.float32)
+    assert O.max_rel_err(y3.cpu().numpy(), yg3.cpu().numpy()) < 1e-5
+    # a 2 bpw plane through vq_gemv_16, bf16 out as the reference returns it
+    m2 = synth.vq_matrix(9399, 16384, n, bpw=2)
+    j0, s2 = m2["idx0"].to(dev), m2["scale"].to(dev)
+    yb = K.vq_gemv_16(xr, j0, cb, s2, 16384, n)
+    assert yb.dtype == torch.bfloat16 and id(j0) in K._SORTED_CACHE
+    _, yb64 = O.vq_gemv(xr.float().cpu()[None], m2["idx0"], None, cb.cpu(), None, m2["scale"])
+    assert O.max_rel_err(yb.float().cpu().numpy(), yb64[0]) < 2.0 ** -8 + TOL
+    # freed planes drop their copies; small planes never get one
+    k0 = id(i0)
+    del i0, j0
+    gc.collect()
+    assert k0 not in K._SORTED_CACHE
+    small = synth.vq_matrix(9400, 256, n, bpw=2)
+    K.vq_gemv_16(xr, small["idx0"].to(dev), cb, small["scale"].to(dev), 256, n)
+    assert K.sorted_cache_bytes() >= 0 and len(K._SORTED_CACHE) == before
