@@ -369,14 +369,31 @@ struct SortedArgs {
 // the other's gathers (measured 72.5 against 77.8 us at 70 VGPRs); the
 // other instantiations run one workgroup per CU, where that bound only
 // costs spills (gate+up 19.1 -> 20.0 us).
+//
+// What the first loads need comes first as 14 dwords of scalar kernel
+// arguments: with -amdgpu-kernarg-preload-count the wave starts with them in
+// SGPRs, so the activation, permutation and sign loads and the first entry
+// words of a workgroup of the first two matrices issue at once, not after a
+// load of the argument lines (dense step 45.94 -> 45.64 us with the
+// activation fields alone).  k_ent0 / k_ent1: the entries of matrices 0 and
+// 1 (matrix 0 twice in a one-matrix launch); k_geo0 / k_geo1: their
+// iterations per chunk | iterations per slice << 16; k_cs: chunks over all
+// matrices | matrix 1's first chunk << 16 (the chunk count itself in a
+// one-matrix launch); k_srn: the two matrices' longer-slice counts (8 bits
+// each) | matrix count << 16 | 2048-point blocks of the activation << 24.
 template <int CBT, int XM, int XT, int EP>
-__global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_sorted_kernel(const SortedArgs a)
+__global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
+    vq_sorted_kernel(const void* const k_x, const int32_t* const k_perm, const int8_t* const k_sign,
+                     const uint32_t* const k_ent0, const uint32_t* const k_ent1, const uint32_t k_geo0,
+                     const uint32_t k_geo1, const uint32_t k_cs, const uint32_t k_srn, const SortedArgs a)
 {
     extern __shared__ __align__(16) float smem[];
-    touch_kernargs(a);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t n = a.ng * 8;
+    // the 2048-point block count (XM 3) from the leading arguments: a.ng
+    // would be a load of the argument struct ahead of the first loads
+    const int k2k = (int)(k_srn >> 24);
+    const int64_t n = XM == 3 ? (int64_t)k2k * RHT2K : a.ng * 8;
     // XM 1 / 3: [natural-order activation: n][stage (n), later the split
     // activation (SG_X_SPLIT)][accumulators]; XM 0: [split][accumulators]
     float* s_nat = smem;
@@ -388,25 +405,41 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     Rht2kLoad first2k;
     const int64_t t0 = (int64_t)threadIdx.x * 8;
     if constexpr (XM == 1) xpro_load<1, XT>(a.g, t0 < n ? t0 : 0, n, 0, 0, first);
-    if constexpr (XM == 3) rht2k_load<XT>(a.g, (int)(n / RHT2K), 0, first2k);
+    if constexpr (XM == 3) rht2k_load<XT>(k_x, k_perm, k_sign, k2k, 0, first2k);
 
     // workgroup b: slice b / nc of chunk b % nc (over all matrices); the
     // slice bounds come from the host (no divisions ahead of the entry
     // loads: with them and the prologue loads issued after the segment
-    // lookup, gate+up took 16.8 us, 15.9 us without)
+    // lookup, gate+up took 16.8 us, 15.9 us without).  Matrices 0 and 1
+    // from the leading arguments, 2 and 3 from the argument struct.
+    const int nc = (int)(k_cs & 0xFFFFu), cs1 = (int)(k_cs >> 16);
+    const int nseg = (int)((k_srn >> 16) & 0xFFu);
     const int pos = (int)blockIdx.x;
-    const int slice = pos / a.nc, gchunk = pos - slice * a.nc;
-    int si = 0;
+    const int slice = pos / nc, gchunk = pos - slice * nc;
+    int si = gchunk < cs1 ? 0 : 1;
+    const uint32_t geo = si == 0 ? k_geo0 : k_geo1;
+    const uint32_t* ent = si == 0 ? k_ent0 : k_ent1;
+    int ipc = (int)(geo & 0xFFFFu), sq = (int)(geo >> 16), sr = (int)((k_srn >> (8 * si)) & 0xFFu);
+    int chunk = gchunk - (si == 0 ? 0 : cs1);
+    if (si == 1 && nseg > 2) {
 #pragma unroll
-    for (int s = 1; s < SG_MAX_SEG; s++) si += (s < a.nseg && gchunk >= a.seg[s].chunk_start) ? 1 : 0;
-    const SortedSeg& sg = a.seg[si];
-    const int R = sg.R;
-    const int chunk = gchunk - sg.chunk_start;
+        for (int s = 2; s < SG_MAX_SEG; s++) si += (s < nseg && gchunk >= a.seg[s].chunk_start) ? 1 : 0;
+        if (si > 1) {
+            ent = a.seg[si].ent;
+            ipc = a.seg[si].ipc;
+            sq = a.seg[si].sq;
+            sr = a.seg[si].sr;
+            chunk = gchunk - a.seg[si].chunk_start;
+        }
+        // the wait for these scalar loads stays on this path (merged after
+        // the branch, it held every workgroup's entry loads behind the
+        // argument struct's other loads)
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    }
     // chunk < n_chunks and n_iters = n_chunks * ipc (checked on the host)
-    const int c_beg = chunk * sg.ipc;
-    const int c_mid = c_beg + sg.ipc1;
-    const int s0 = c_beg + slice * sg.sq + min(slice, sg.sr);
-    const int s1 = s0 + sg.sq + (slice < sg.sr ? 1 : 0);
+    const int c_beg = chunk * ipc;
+    const int s0 = c_beg + slice * sq + min(slice, sr);
+    const int s1 = s0 + sq + (slice < sr ? 1 : 0);
 
     // the wave's first entry words come from HBM while the prologue stages
     // and rotates the activation (which waits only for its own, earlier
@@ -418,7 +451,13 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
     // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
     // two
     SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2> pipe;
-    pipe.load_entries(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R, a.c1mask);
+    pipe.load_entries(ent, a.cb0, a.cb1, c_beg, c_beg, s0, s1, wave, lane, 0, 1, a.c1mask);
+    // the fields the loop needs, from the argument struct (its lines were
+    // not needed before this point)
+    touch_kernargs(a);
+    const SortedSeg& sg = a.seg[si];
+    const int R = sg.R;
+    pipe.set_fields(c_beg + sg.ipc1, a.gbits, R);
     if constexpr (XM == 0) pipe.gathers();
 
     float* acc = sorted_acc(s_acc, wave, lane, R);
@@ -433,7 +472,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1) vq_s
         // passes (measured: dense step 46.96 -> 46.65 us, LM head 65.2 ->
         // 64.9; before the transform, waiting there for the entry words:
         // 48.1)
-        rht2k_build<XT>((int)(n / RHT2K), n, first2k, smem + n, s_nat, s_x, a.g.xscale, [&]() { pipe.gathers(); });
+        rht2k_build<XT>(k2k, n, first2k, smem + n, s_nat, s_x, a.g.xscale, [&]() { pipe.gathers(); });
     } else {
         for (int64_t g = threadIdx.x; g < a.ng; g += SG_THREADS) {
             float v[8];
@@ -501,7 +540,16 @@ static hipError_t launch_sorted(const SortedArgs& a, unsigned grid, size_t shm, 
                                    hipFuncAttributeMaxDynamicSharedMemorySize, SG_MAX_SHM);
     });
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((vq_sorted_kernel<CBT, XM, XT, EP>), dim3(grid), dim3(SG_THREADS), shm, st, a);
+    // the leading arguments (SortedLead): matrices 0 and 1 (matrix 0 again
+    // for a one-matrix launch, whose chunks all lie below cs1 = nc)
+    const SortedSeg& s0 = a.seg[0];
+    const SortedSeg& s1 = a.seg[a.nseg > 1 ? 1 : 0];
+    const uint32_t geo0 = (uint32_t)s0.ipc | (uint32_t)s0.sq << 16, geo1 = (uint32_t)s1.ipc | (uint32_t)s1.sq << 16;
+    const uint32_t cs = (uint32_t)a.nc | (uint32_t)(a.nseg > 1 ? s1.chunk_start : a.nc) << 16;
+    const uint32_t srn = (uint32_t)s0.sr | (uint32_t)s1.sr << 8 | (uint32_t)a.nseg << 16 |
+                         (uint32_t)(a.ng * 8 / RHT2K) << 24;
+    hipLaunchKernelGGL((vq_sorted_kernel<CBT, XM, XT, EP>), dim3(grid), dim3(SG_THREADS), shm, st, a.g.x, a.g.perm,
+                       a.g.sign, s0.ent, s1.ent, geo0, geo1, cs, srn, a);
     return hipGetLastError();
 }
 
@@ -677,6 +725,13 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
                          (long long)n_cnt, VQ2_SORTED_MAX_COUNTERS);
     if (wg == 0) return VQ2_OK;
     if (wg > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: grid too large");
+    // the leading kernel arguments carry chunk counts, iterations per chunk
+    // and slice lengths in 16 bits
+    if (nc > 0xFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: %lld chunks (at most 65535)", (long long)nc);
+    for (int s = 0; s < c.nseg; s++)
+        if (c.seg[s].iters_per_chunk > 0xFFFF)
+            return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: matrix %d: %lld iterations per chunk (at most "
+                             "65535)", s, (long long)c.seg[s].iters_per_chunk);
     a.nc = (int)nc;
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;

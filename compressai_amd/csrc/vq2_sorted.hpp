@@ -142,7 +142,8 @@ struct Rht2kLoad {
 
 // Loads of the thread's values, issued early (nothing waits for them here).
 template <int XT>
-__device__ __forceinline__ void rht2k_load(const GemvArgs& a, int k, int64_t xrow, Rht2kLoad& L)
+__device__ __forceinline__ void rht2k_load(const void* x, const int32_t* perm, const int8_t* sign, int k, int64_t xrow,
+                                           Rht2kLoad& L)
 {
     typedef const __attribute__((address_space(1))) u32x2* gp2;
     typedef const __attribute__((address_space(1))) uint16_t* gp16;
@@ -151,12 +152,17 @@ __device__ __forceinline__ void rht2k_load(const GemvArgs& a, int k, int64_t xro
     for (int b = 0; b < RHT2K_MAXB; b++) {
         if (b < k) {
             const int64_t e = (int64_t)b * RHT2K + 2 * threadIdx.x;
-            L.p[b] = *(gp2)(a.perm ? a.perm + e : g_perm_iota.v + e);
-            L.s[b] = *(gp16)(a.sign ? a.sign + e : g_sign_ones.v + e);
-            if constexpr (XT == VQ2_DT_F32) L.x[b] = *(gp2)((const float*)a.x + xrow + e);
-            else L.x[b][0] = *(gp32)((const uint16_t*)a.x + xrow + e);
+            L.p[b] = *(gp2)(perm ? perm + e : g_perm_iota.v + e);
+            L.s[b] = *(gp16)(sign ? sign + e : g_sign_ones.v + e);
+            if constexpr (XT == VQ2_DT_F32) L.x[b] = *(gp2)((const float*)x + xrow + e);
+            else L.x[b][0] = *(gp32)((const uint16_t*)x + xrow + e);
         }
     }
+}
+template <int XT>
+__device__ __forceinline__ void rht2k_load(const GemvArgs& a, int k, int64_t xrow, Rht2kLoad& L)
+{
+    rht2k_load<XT>(a.x, a.perm, a.sign, k, xrow, L);
 }
 
 template <int M>
@@ -500,6 +506,14 @@ struct SortedPipe {
             ie[d] = clampit(it + d * W);
             e[d] = load_e(ie[d]);
         }
+    }
+    // the stage-2 start and the position fields, set after load_entries
+    // (whose loads need neither)
+    __device__ __forceinline__ void set_fields(int c_mid_, int gbits, int R)
+    {
+        c_mid = c_mid_;
+        pb = (uint32_t)sorted_pbits(gbits, R);
+        dummy = (uint32_t)R << gbits;
     }
     __device__ __forceinline__ void gathers()
     {
