@@ -13,9 +13,10 @@
 // Layout (built once at load time on the host by vq2_sorted_pack, from the
 // reference's index planes, which stay the public format):
 //  * a matrix is cut into chunks of R rows x all ng groups, gbits =
-//    ceil(log2 ng) and R <= min(2^(16 - gbits) - 1, 255) rows (chosen at
-//    pack time: the rows split evenly over the chunks), so row R is a dummy
-//    row that padding entries add to;
+//    ceil(log2 ng) and R <= min(2^(17 - gbits) - 1, 511) rows (chosen at
+//    pack time: the rows split evenly over the chunks; by default at most
+//    min(2^(16 - gbits) - 1, 255), more for very tall matrices), so row R is
+//    a dummy row that padding entries add to;
 //  * every wave keeps two accumulator arrays, one per 32-lane half; a
 //    chunk's codes are sorted by value (then position) and dealt into
 //    instructions of 64 lanes with no row twice in a half (an entry whose row
@@ -23,7 +24,7 @@
 //    lanes' read-add-write of their row's accumulator never collide;
 //  * lane 63 of an instruction carries its base code (the smallest), the
 //    other 63 lanes one code each as a 24-bit field (code - base) << P | row
-//    << gbits | group (P = gbits + bitlen(R) <= 16); an instruction whose next
+//    << gbits | group (P = gbits + bitlen(R) <= 17); an instruction whose next
 //    code would be 2^(24 - P) or more above its base is closed early;
 //    padding fills the tail;
 //  * 4 instructions form an iteration of 768 bytes: lane l reads 12 bytes
@@ -65,15 +66,28 @@
 namespace vq2 {
 
 
-// Default chunk height: the rows split evenly over the fewest chunks; with
-// chunk_align > 1, over a multiple of chunk_align chunks (one per CU and
-// round: no CU waits for a last short round) when the chunks keep at least
-// SG_MIN_ALIGNED_R rows.
+// Default chunk height: the rows split evenly over the fewest chunks of at
+// most 255 rows with 16-bit positions; with chunk_align > 1, over a
+// multiple of chunk_align chunks (one per CU and round: no CU waits for a
+// last short round) when the chunks keep at least SG_MIN_ALIGNED_R rows.
+// A matrix so tall that taller chunks (17-bit positions) fill a multiple of
+// 2 x chunk_align chunks takes those: the LM head (151,936 rows) as 512
+// chunks of 297 rows, one round of two workgroups per CU, instead of 768
+// of 198 (measured 63.4 against 68.8 us per call).  More codes per chunk
+// put more codes on each code value, so a wave's 63 sorted codes span
+// fewer codebook lines.  (Taller chunks for the other shapes measured
+// slower: gate+up 16.3 -> 17.5 us at 473 rows, down 13.8 -> 16.8 at 228.)
 constexpr int64_t SG_MIN_ALIGNED_R = 128;
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
 {
-    const int64_t rmax = sorted_max_rows(ng);
+    const int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
     if (rmax == 0 || out_rows < 1) return 0;
+    if (chunk_align > 1) {
+        const int64_t rmax17 = sorted_max_rows(ng, 17), two = 2 * chunk_align;
+        const int64_t n17 = ((out_rows + rmax17 - 1) / rmax17 + two - 1) / two * two;
+        const int64_t r17 = (out_rows + n17 - 1) / n17;
+        if (r17 > rmax) return r17;
+    }
     const int64_t nch = (out_rows + rmax - 1) / rmax;
     if (chunk_align > 1) {
         const int64_t nal = (nch + chunk_align - 1) / chunk_align * chunk_align;
@@ -91,10 +105,11 @@ static void fill_pad_iters(uint32_t* dst, int64_t iters, uint32_t pad)
     for (int64_t it = 0; it < iters; it++)
         for (int l = 0; l < 64; l++) {
             uint32_t* w = dst + (it * 64 + l) * SG_LANE_WORDS;
-            const uint32_t pp = l == SG_BASE_LANE ? 0u : pad | pad << 16;
+            // pad: up to 17 bits (its bit 16 in each field's high byte)
+            const uint32_t pp = l == SG_BASE_LANE ? 0u : (pad & 0xFFFFu) | (pad & 0xFFFFu) << 16;
             w[0] = pp;
             w[1] = pp;
-            w[2] = 0u;
+            w[2] = l == SG_BASE_LANE ? 0u : (pad >> 16) * 0x01010101u;
         }
 }
 
@@ -107,18 +122,19 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
 {
     const int pb = sorted_pbits(gb, (int)R);
     const uint32_t span = 1u << (24 - pb);  // code offsets below this
-    std::vector<uint32_t> keys;
+    // code << 32 | position (row << gb | group: up to 17 bits)
+    std::vector<uint64_t> keys;
     keys.reserve((size_t)(rows * ng));
     for (int64_t r = 0; r < rows; r++) {
         const int16_t* p = plane + (r0 + r) * ng;
         for (int64_t g = 0; g < ng; g++)
-            keys.push_back(((uint32_t)(uint16_t)p[g] << 16) | (uint32_t)((r << gb) | g));
+            keys.push_back(((uint64_t)(uint16_t)p[g] << 32) | (uint64_t)((r << gb) | g));
     }
     std::sort(keys.begin(), keys.end());
     const uint32_t pad = (uint32_t)(R << gb);  // offset 0, dummy row R
     std::vector<uint32_t> instr;  // instruction-major 24-bit fields, 64 per instruction
     instr.reserve(keys.size() + keys.size() / 32 + 1024);
-    std::vector<uint32_t> pending, still;
+    std::vector<uint64_t> pending, still;
     // lane groups of the current instruction that hold each row (valid
     // while stamp[row] == id)
     std::vector<int64_t> stamp((size_t)R + 1, -1);
@@ -136,10 +152,10 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
         // place k in the first open lane group that does not hold its row:
         // 0 placed, 1 its row is in both groups, 2 its code is too far from
         // the base (every later key's is too: codes ascend)
-        auto place = [&](uint32_t k) -> int {
-            const uint32_t code = k >> 16;
+        auto place = [&](uint64_t k) -> int {
+            const uint32_t code = (uint32_t)(k >> 32), kp = (uint32_t)k;
             if (have_base && code - base >= span) return 2;
-            const uint32_t row = (k & 0xFFFFu) >> gb;
+            const uint32_t row = kp >> gb;
             const uint8_t u = stamp[row] == id ? used[row] : 0;
             for (int qd = 0; qd < SG_PARTS; qd++)
                 if (fill[qd] < cap[qd] && !(u & (1u << qd))) {
@@ -147,7 +163,7 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
                         have_base = true;
                         base = code;
                     }
-                    slot[qd][fill[qd]++] = ((code - base) << pb) | (k & 0xFFFFu);
+                    slot[qd][fill[qd]++] = ((code - base) << pb) | kp;
                     stamp[row] = id;
                     used[row] = (uint8_t)(u | (1u << qd));
                     n++;
@@ -271,7 +287,7 @@ int sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts,
                      uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
                      int64_t* n_iters, int n_threads)
 {
-    const int64_t rmax = sorted_max_rows(ng);
+    const int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);  // pools: 16-bit positions
     if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: ng=%lld outside 1..32768", (long long)ng);
     if (R < 1 || R > rmax)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: rows_per_chunk=%lld outside 1..%lld for ng=%lld",
@@ -381,7 +397,11 @@ struct SortedArgs {
 // matrices | matrix 1's first chunk << 16 (the chunk count itself in a
 // one-matrix launch); k_srn: the two matrices' longer-slice counts (8 bits
 // each) | matrix count << 16 | 2048-point blocks of the activation << 24.
-template <int CBT, int XM, int XT, int EP>
+// TALL: a launch whose chunks hold 256 or more rows or 17-bit positions
+// (very tall matrices: the LM head); it also keeps the split activation in
+// n floats (halves n / 2 apart) so that the LM head's workgroups stay
+// small enough for two per CU; the other instantiations keep SG_XB.
+template <int CBT, int XM, int XT, int EP, bool TALL>
 __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     vq_sorted_kernel(const void* const k_x, const int32_t* const k_perm, const int8_t* const k_sign,
                      const uint32_t* const k_ent0, const uint32_t* const k_ent1, const uint32_t k_geo0,
@@ -395,10 +415,12 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     const int k2k = (int)(k_srn >> 24);
     const int64_t n = XM == 3 ? (int64_t)k2k * RHT2K : a.ng * 8;
     // XM 1 / 3: [natural-order activation: n][stage (n), later the split
-    // activation (SG_X_SPLIT)][accumulators]; XM 0: [split][accumulators]
+    // activation (SG_X_SPLIT floats, or TALL: n floats)][accumulators]; XM 0:
+    // [split][accumulators]
     float* s_nat = smem;
-    float* s_x = smem + (XM != 0 ? n : 0);              // split activation (SG_X_SPLIT floats)
-    float* s_acc = s_x + SG_X_SPLIT;                    // SG_WAVES x SG_PARTS x (R + 1)
+    const int xb = TALL ? (int)(n / 2) : SG_XB;
+    float* s_x = smem + (XM != 0 ? n : 0);              // split activation
+    float* s_acc = s_x + (TALL ? n : SG_X_SPLIT);       // SG_WAVES x SG_PARTS x (R + 1)
     // prologue loads first (they need only the activation fields, and
     // return before the entries and gathers)
     XProLoad first;
@@ -450,7 +472,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     // past the range, 51.3 against 50.2 at two); the 64-VGPR fused-RHT
     // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
     // two
-    SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2> pipe;
+    SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2, SG_WAVES, TALL> pipe;
     pipe.load_entries(ent, a.cb0, a.cb1, c_beg, c_beg, s0, s1, wave, lane, 0, 1, a.c1mask);
     // the fields the loop needs, from the argument struct (its lines were
     // not needed before this point)
@@ -466,43 +488,47 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
         void* s_stage = smem + n;  // dead once build_x is done: the split activation takes its place
         stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
         build_x<1, XT>(a.g, s_nat, s_stage, 1, n, first);
-        x_finalize(s_nat, s_x, n, a.g.xscale);
+        x_finalize(s_nat, s_x, n, a.g.xscale, xb);
     } else if constexpr (XM == 3) {
         // the first gathers go out between the lane stages and the LDS
         // passes (measured: dense step 46.96 -> 46.65 us, LM head 65.2 ->
         // 64.9; before the transform, waiting there for the entry words:
         // 48.1)
-        rht2k_build<XT>(k2k, n, first2k, smem + n, s_nat, s_x, a.g.xscale, [&]() { pipe.gathers(); });
+        rht2k_build<XT>(k2k, n, first2k, smem + n, s_nat, s_x, a.g.xscale, xb, [&]() { pipe.gathers(); });
     } else {
         for (int64_t g = threadIdx.x; g < a.ng; g += SG_THREADS) {
             float v[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) v[k] = load_as_f32(a.g.x, XT, g * 8 + k);
-            x_store_group(s_x, g, v);
+            x_store_group(s_x, g, v, xb);
         }
     }
     __syncthreads();
     if constexpr (XM == 1) pipe.gathers();
-    pipe.run(acc, s_x, a.gbits, a.ng, R);
+    pipe.run(acc, s_x, a.gbits, a.ng, R, xb);
     __syncthreads();
 
     __shared__ float s_red[4][256];
-    const float sum = sorted_row_sums(s_acc, R, s_red);
-    const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
+    const float sum = sorted_row_sums<TALL>(s_acc, R, s_red);
+    // thread rr < R holds row rr's sum
+    const int rr = TALL ? (int)threadIdx.x : (int)(threadIdx.x & 255);
+    const bool lead = TALL || threadIdx.x < 256;
     const int64_t row0 = (int64_t)chunk * sg.rb + min(chunk, sg.nbig);
     const int64_t row = row0 + rr;
-    const bool own = pp == 0 && rr < sg.rb + (chunk < sg.nbig ? 1 : 0);
+    const bool own = lead && rr < sg.rb + (chunk < sg.nbig ? 1 : 0);
     if constexpr (EP == 1) {
         uint64_t best = own ? argmax_key((sum * load_as_f32(sg.scale, a.s_dt, row)) * a.rs, row) : 0;
         for (int off = 32; off > 0; off >>= 1) {
             const uint64_t o = __shfl_xor(best, off);
             best = o > best ? o : best;
         }
-        __shared__ uint64_t s_key[4];
-        if (pp == 0 && lane == 0) s_key[wave] = best;
+        // the rows are the first 4 waves' threads (TALL: 8, at most 511 rows)
+        constexpr int KW = TALL ? 8 : 4;
+        __shared__ uint64_t s_key[KW];
+        if (wave < KW && lane == 0) s_key[wave] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
-            for (int w = 1; w < 4; w++) best = s_key[w] > best ? s_key[w] : best;
+            for (int w = 1; w < KW; w++) best = s_key[w] > best ? s_key[w] : best;
             a.cand[blockIdx.x] = best;
         }
     } else if (a.slices == 1) {
@@ -530,51 +556,65 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
 }
 
 // ------------------------------------------------------------------ launch
-template <int CBT, int XM, int XT, int EP>
+template <int CBT, int XM, int XT, int EP, bool TALL>
 static hipError_t launch_sorted(const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)vq_sorted_kernel<CBT, XM, XT, EP>,
+        attr = hipFuncSetAttribute((const void*)vq_sorted_kernel<CBT, XM, XT, EP, TALL>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, SG_MAX_SHM);
     });
     if (attr != hipSuccess) return attr;
-    // the leading arguments (SortedLead): matrices 0 and 1 (matrix 0 again
-    // for a one-matrix launch, whose chunks all lie below cs1 = nc)
+    // the leading arguments: matrices 0 and 1 (matrix 0 again for a
+    // one-matrix launch, whose chunks all lie below cs1 = nc)
     const SortedSeg& s0 = a.seg[0];
     const SortedSeg& s1 = a.seg[a.nseg > 1 ? 1 : 0];
     const uint32_t geo0 = (uint32_t)s0.ipc | (uint32_t)s0.sq << 16, geo1 = (uint32_t)s1.ipc | (uint32_t)s1.sq << 16;
     const uint32_t cs = (uint32_t)a.nc | (uint32_t)(a.nseg > 1 ? s1.chunk_start : a.nc) << 16;
     const uint32_t srn = (uint32_t)s0.sr | (uint32_t)s1.sr << 8 | (uint32_t)a.nseg << 16 |
                          (uint32_t)(a.ng * 8 / RHT2K) << 24;
-    hipLaunchKernelGGL((vq_sorted_kernel<CBT, XM, XT, EP>), dim3(grid), dim3(SG_THREADS), shm, st, a.g.x, a.g.perm,
-                       a.g.sign, s0.ent, s1.ent, geo0, geo1, cs, srn, a);
+    hipLaunchKernelGGL((vq_sorted_kernel<CBT, XM, XT, EP, TALL>), dim3(grid), dim3(SG_THREADS), shm, st, a.g.x,
+                       a.g.perm, a.g.sign, s0.ent, s1.ent, geo0, geo1, cs, srn, a);
     return hipGetLastError();
 }
 
-template <int CBT, int EP>
-static hipError_t launch_sorted_x(int xm, int x_dt, const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
+// TALL launches: the 2048-point prologue (XM 3) or a rotated activation
+// (XM 0) only (the host refuses the others)
+template <int CBT, int EP, bool TALL>
+static hipError_t launch_sorted_t(int xm, int x_dt, const SortedArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
     if (xm == 3) {
         switch (x_dt) {
-        case VQ2_DT_F16: return launch_sorted<CBT, 3, VQ2_DT_F16, EP>(a, grid, shm, st);
-        case VQ2_DT_BF16: return launch_sorted<CBT, 3, VQ2_DT_BF16, EP>(a, grid, shm, st);
-        default: return launch_sorted<CBT, 3, VQ2_DT_F32, EP>(a, grid, shm, st);
+        case VQ2_DT_F16: return launch_sorted<CBT, 3, VQ2_DT_F16, EP, TALL>(a, grid, shm, st);
+        case VQ2_DT_BF16: return launch_sorted<CBT, 3, VQ2_DT_BF16, EP, TALL>(a, grid, shm, st);
+        default: return launch_sorted<CBT, 3, VQ2_DT_F32, EP, TALL>(a, grid, shm, st);
         }
     }
-    if (xm == 1) {
-        switch (x_dt) {
-        case VQ2_DT_F16: return launch_sorted<CBT, 1, VQ2_DT_F16, EP>(a, grid, shm, st);
-        case VQ2_DT_BF16: return launch_sorted<CBT, 1, VQ2_DT_BF16, EP>(a, grid, shm, st);
-        default: return launch_sorted<CBT, 1, VQ2_DT_F32, EP>(a, grid, shm, st);
+    if constexpr (!TALL) {
+        if (xm == 1) {
+            switch (x_dt) {
+            case VQ2_DT_F16: return launch_sorted<CBT, 1, VQ2_DT_F16, EP, false>(a, grid, shm, st);
+            case VQ2_DT_BF16: return launch_sorted<CBT, 1, VQ2_DT_BF16, EP, false>(a, grid, shm, st);
+            default: return launch_sorted<CBT, 1, VQ2_DT_F32, EP, false>(a, grid, shm, st);
+            }
         }
+    } else if (xm == 1) {
+        return hipErrorInvalidValue;
     }
     switch (x_dt) {
-    case VQ2_DT_F16: return launch_sorted<CBT, 0, VQ2_DT_F16, EP>(a, grid, shm, st);
-    case VQ2_DT_BF16: return launch_sorted<CBT, 0, VQ2_DT_BF16, EP>(a, grid, shm, st);
-    default: return launch_sorted<CBT, 0, VQ2_DT_F32, EP>(a, grid, shm, st);
+    case VQ2_DT_F16: return launch_sorted<CBT, 0, VQ2_DT_F16, EP, TALL>(a, grid, shm, st);
+    case VQ2_DT_BF16: return launch_sorted<CBT, 0, VQ2_DT_BF16, EP, TALL>(a, grid, shm, st);
+    default: return launch_sorted<CBT, 0, VQ2_DT_F32, EP, TALL>(a, grid, shm, st);
     }
+}
+
+template <int CBT, int EP>
+static hipError_t launch_sorted_x(int xm, int x_dt, bool tall, const SortedArgs& a, unsigned grid, size_t shm,
+                                  hipStream_t st)
+{
+    return tall ? launch_sorted_t<CBT, EP, true>(xm, x_dt, a, grid, shm, st)
+                : launch_sorted_t<CBT, EP, false>(xm, x_dt, a, grid, shm, st);
 }
 
 // Workspace with several slices: VQ2_SORTED_WS_HEADER bytes of arrival
@@ -638,7 +678,10 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     int64_t rmax = 0;
     if (int r = sorted_check_call(c, top1, "vq2 sorted GEMV", &rmax)) return r;
     const int64_t n = c.ng * 8;
-    const size_t shm = (size_t)((c.xm != 0 ? n : 0) + SG_X_SPLIT + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
+    // chunks of 256 rows or more, or 17-bit positions: the TALL kernels
+    const bool tall = rmax >= 256 || sorted_pbits(sorted_gbits(c.ng), (int)rmax) > 16;
+    const size_t shm =
+        (size_t)((c.xm != 0 ? n : 0) + (tall ? n : SG_X_SPLIT) + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
     if (n > 2 * SG_XB || shm > SG_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large (at most %d)", (long long)n, 2 * SG_XB);
     if (c.xm == 1) {
@@ -651,6 +694,9 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     }
     // 2048-point blocks: the all-threads prologue (rht2k_build)
     const int xm = (c.xm == 1 && c.hb == RHT2K && n % RHT2K == 0 && n <= (int64_t)RHT2K * RHT2K_MAXB) ? 3 : c.xm;
+    if (tall && xm == 1)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: chunks of %lld rows (256 or more, or 17-bit positions) "
+                         "need a 2048-point rotation or a rotated activation", (long long)rmax);
     SortedArgs a{};
     a.g.x = c.x;
     a.g.x_dt = c.x_dt;
@@ -736,13 +782,13 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {
-        err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(xm, c.x_dt, a, (unsigned)wg, shm, st)
-                                    : launch_sorted_x<VQ2_DT_BF16, 1>(xm, c.x_dt, a, (unsigned)wg, shm, st);
+        err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 1>(xm, c.x_dt, tall, a, (unsigned)wg, shm, st)
+                                    : launch_sorted_x<VQ2_DT_BF16, 1>(xm, c.x_dt, tall, a, (unsigned)wg, shm, st);
         if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
         return argmax_final_launch(a.cand, wg, 1, top1_idx, top1_val, c.stream);
     }
-    err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(xm, c.x_dt, a, (unsigned)wg, shm, st)
-                                : launch_sorted_x<VQ2_DT_BF16, 0>(xm, c.x_dt, a, (unsigned)wg, shm, st);
+    err = c.cb_dt == VQ2_DT_F16 ? launch_sorted_x<VQ2_DT_F16, 0>(xm, c.x_dt, tall, a, (unsigned)wg, shm, st)
+                                : launch_sorted_x<VQ2_DT_BF16, 0>(xm, c.x_dt, tall, a, (unsigned)wg, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMV launch");
     return VQ2_OK;
 }

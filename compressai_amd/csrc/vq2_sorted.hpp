@@ -8,8 +8,9 @@
 // Lane 63 of an instruction holds no code: it carries the instruction's base
 // code (its smallest).  Every other lane holds a 24-bit field
 //     F = (code - base) << P | row << gbits | group,   P = gbits + bitlen(R),
-// so P <= 16 and the code offset has 24 - P >= 8 bits (the packer closes an
-// instruction early rather than exceed it).  Four instructions form an
+// so P <= 17 and the code offset has 24 - P >= 7 bits (the packer closes an
+// instruction early rather than exceed it; P = 17 only for the taller
+// chunks of very tall matrices, sorted_rows_per_chunk).  Four instructions form an
 // iteration of 768 bytes: lane l reads the 12 bytes at 12 l, three words
 //     w0 = lo16(F0) | lo16(F1) << 16,  w1 = lo16(F2) | lo16(F3) << 16,
 //     w2 = hi8(F0) | hi8(F1) << 8 | hi8(F2) << 16 | hi8(F3) << 24,
@@ -29,10 +30,10 @@ constexpr int SG_ITER = 256;        // entry slots per iteration (64 lanes x 4 i
 constexpr int SG_LANE_WORDS = 3;    // uint32 words per lane and iteration
 constexpr int SG_ITER_WORDS = 64 * SG_LANE_WORDS;  // 768 bytes per iteration
 constexpr int SG_BASE_LANE = 63;    // the lane that carries the instructions' base codes
-constexpr int SG_MAX_R = 255;
+constexpr int SG_MAX_R = 511;
 constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
 constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
-constexpr int SG_MAX_SHM = 96 * 1024;         // dynamic LDS: activation (+ stage) + accumulators
+constexpr int SG_MAX_SHM = 150 * 1024;        // dynamic LDS: activation (+ stage) + accumulators
 constexpr int SG_MAX_SEG = 4;                 // matrices per launch
 
 inline int sorted_gbits(int64_t ng)
@@ -60,32 +61,34 @@ __host__ __device__ inline ChunkSplit chunk_split(int64_t rows, int64_t R)
 }
 
 // Bits of a field's position part: gbits + bitlen(R) (rows 0..R, R the
-// dummy row); at most 16 when R <= sorted_max_rows(ng).
+// dummy row); at most 17 when R <= sorted_max_rows(ng).
 __host__ __device__ inline int sorted_pbits(int gbits, int R)
 {
     return gbits + (32 - __builtin_clz((unsigned)R));
 }
 
 // Largest chunk height for ng groups: row R is the dummy row, so
-// (R << gbits) | group must fit 16 bits; at most SG_MAX_R.
-inline int64_t sorted_max_rows(int64_t ng)
+// (R << gbits) | group must fit `pbits` bits (17: what a field holds with a
+// 7-bit code offset; 16: the default chunking's limit); at most SG_MAX_R.
+inline int64_t sorted_max_rows(int64_t ng, int pbits = 17)
 {
     const int gb = sorted_gbits(ng);
     if (ng < 1 || gb > 15) return 0;
-    const int64_t rmax = (int64_t(1) << (16 - gb)) - 1;
+    const int64_t rmax = (int64_t(1) << (pbits - gb)) - 1;
     return rmax < SG_MAX_R ? rmax : SG_MAX_R;
 }
 
 // The activation in LDS as the loop reads it (fp32, "split" layout): the
-// first 4 values of group g at float offset 4 g, the last 4 at SG_XB + 4 g.
+// first 4 values of group g at float offset 4 g, the last 4 at xb + 4 g.
 // A 16-byte stride puts the reads of random groups at 16 bank positions
 // (g mod 16) instead of the 8 of a 32-byte stride (g mod 8), so the lanes
-// the LDS serves together collide less, and both halves come from one
-// address register with an immediate offset.  Needs n <= 2 SG_XB.
+// the LDS serves together collide less.  The dense kernels take xb = n / 2
+// (the layout fills n floats: the LM head's workgroups stay small enough for
+// two per CU); the MoE kernels the fixed SG_XB (n <= 2 SG_XB).
 constexpr int SG_XB = 4096;
-constexpr int SG_X_SPLIT = 2 * SG_XB;  // floats of the split activation
+constexpr int SG_X_SPLIT = 2 * SG_XB;  // floats of the split activation at xb = SG_XB
 
-__device__ __forceinline__ void x_store_group(float* s_split, int64_t g, const float (&v)[8])
+__device__ __forceinline__ void x_store_group(float* s_split, int64_t g, const float (&v)[8], int xb)
 {
     u32x4 w0, w1;
 #pragma unroll
@@ -94,13 +97,13 @@ __device__ __forceinline__ void x_store_group(float* s_split, int64_t g, const f
         w1[k] = __float_as_uint(v[4 + k]);
     }
     *(u32x4*)(s_split + 4 * g) = w0;
-    *(u32x4*)(s_split + SG_XB + 4 * g) = w1;
+    *(u32x4*)(s_split + xb + 4 * g) = w1;
 }
 
 // s_split = s_nat (the rotated activation in natural order, fp32, visible
 // after a barrier) times `scale`, one thread per group.  The two regions
 // must not overlap; a barrier must follow.
-__device__ __forceinline__ void x_finalize(const float* s_nat, float* s_split, int64_t n, float scale)
+__device__ __forceinline__ void x_finalize(const float* s_nat, float* s_split, int64_t n, float scale, int xb)
 {
     for (int64_t g = threadIdx.x; g < n / 8; g += blockDim.x) {
         const u32x4 a = *(const u32x4*)(s_nat + g * 8), b = *(const u32x4*)(s_nat + g * 8 + 4);
@@ -110,7 +113,7 @@ __device__ __forceinline__ void x_finalize(const float* s_nat, float* s_split, i
             v[k] = __uint_as_float(a[k]) * scale;
             v[4 + k] = __uint_as_float(b[k]) * scale;
         }
-        x_store_group(s_split, g, v);
+        x_store_group(s_split, g, v, xb);
     }
 }
 
@@ -242,7 +245,7 @@ struct NoMid {
 };
 template <int XT, class M = NoMid>
 __device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoad& L, const void* s_stage,
-                                                float* s_nat, float* s_split, float scale, M mid = M())
+                                                float* s_nat, float* s_split, float scale, int xb, M mid = M())
 {
     const int t = threadIdx.x, lane = t & 63;
     // permuted values, signs, bit 0, bits 1-6
@@ -298,17 +301,17 @@ __device__ __forceinline__ void rht2k_transform(int k, int64_t n, const Rht2kLoa
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int64_t e = base + 512 * i;
-            s_split[((e >> 2) & 1) * SG_XB + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
+            s_split[((e >> 2) & 1) * xb + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
         }
     }
 }
 
 template <int XT, class M = NoMid>
 __device__ __forceinline__ void rht2k_build(int k, int64_t n, const Rht2kLoad& L, void* s_stage, float* s_nat,
-                                            float* s_split, float scale, M mid = M())
+                                            float* s_split, float scale, int xb, M mid = M())
 {
     rht2k_stage<XT>(k, L, s_stage);
-    rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale, mid);
+    rht2k_transform<XT>(k, n, L, s_stage, s_nat, s_split, scale, xb, mid);
 }
 
 // One 512-point block by the same all-threads scheme (the MoE down
@@ -377,10 +380,10 @@ __device__ __forceinline__ void rht512_transform(const RhtPairLoad& L, F val, fl
 // 8-term dot product of one centroid (fp16 or bf16, 16 bytes) with group g
 // of the split activation in LDS, fp32.
 template <int CBT>
-__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, uint32_t g)
+__device__ __forceinline__ float centroid_dot(const u32x4 c, const float* s_x, uint32_t g, int xb)
 {
     const float* p = s_x + 4 * g;
-    const u32x4 x0 = *(const u32x4*)p, x1 = *(const u32x4*)(p + SG_XB);
+    const u32x4 x0 = *(const u32x4*)p, x1 = *(const u32x4*)(p + xb);
     float xv[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -424,7 +427,10 @@ struct Ent3 {
 // (v_readlane: scalar registers, no memory access) and adds each lane's
 // offset; a code is masked to its codebook's size (65536 rows, or 256 for
 // the uint8 stage 2 of (16,8)), so no entry word can address outside it.
-template <int CBT, int GD = 2, int W = SG_WAVES>
+// TALL: chunks whose positions may take 17 bits (bit 16 in the field's high
+// byte); the others read a position from its field's low 16 bits alone
+// (the full decode measured 0.24 us slower per dense step).
+template <int CBT, int GD = 2, int W = SG_WAVES, bool TALL = false>
 struct SortedPipe {
     static_assert(GD >= 1 && GD <= 3, "gather depth 1 to 3");
     static constexpr int NE = GD + 1 > 3 ? GD + 1 : 3;  // entry words held: iterations it .. it + (NE - 1) W
@@ -481,7 +487,7 @@ struct SortedPipe {
         const uint32_t pmask = (1u << pb) - 1u;
         u32x4 p;
 #pragma unroll
-        for (int q = 0; q < 4; q++) p[q] = lane == SG_BASE_LANE ? dummy : lo16(ew, q) & pmask;
+        for (int q = 0; q < 4; q++) p[q] = lane == SG_BASE_LANE ? dummy : (TALL ? field(ew, q) : lo16(ew, q)) & pmask;
         return p;
     }
     // a missing stage-2 codebook is never selected for a real entry; cb0
@@ -537,7 +543,8 @@ struct SortedPipe {
         e[NE - 1] = enew;
         ie[NE - 1] = inew;
     }
-    __device__ __forceinline__ void accumulate(float* acc, const float* x, uint32_t gbits, uint32_t gmax, uint32_t R)
+    __device__ __forceinline__ void accumulate(float* acc, const float* x, uint32_t gbits, uint32_t gmax, uint32_t R,
+                                               int xb)
     {
         const uint32_t gmask = (1u << gbits) - 1u;
         const u32x4 pos = positions(e[0]);
@@ -545,11 +552,12 @@ struct SortedPipe {
         for (int q = 0; q < 4; q++) {
             const uint32_t r = min(pos[q] >> gbits, R);
             const uint32_t g = min(pos[q] & gmask, gmax);
-            acc[r] += centroid_dot<CBT>(c[0][q], x, g);
+            acc[r] += centroid_dot<CBT>(c[0][q], x, g, xb);
         }
     }
     // acc: this lane's accumulator array (R + 1 floats), x: the activation
-    __device__ __forceinline__ void run(float* acc, const float* x, int gbits, int64_t ng, int R)
+    // (split layout, halves xb floats apart)
+    __device__ __forceinline__ void run(float* acc, const float* x, int gbits, int64_t ng, int R, int xb)
     {
         const uint32_t gmax = (uint32_t)(ng - 1);
         // iterations whose gathers GD ahead are real
@@ -558,7 +566,7 @@ struct SortedPipe {
             const Ent3 enew = load_e(inew);
             u32x4 cn[4];  // the gathers GD iterations ahead
             gather(ie[GD], e[GD], cn);
-            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R);
+            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R, xb);
             shift(enew, inew);
 #pragma unroll
             for (int d = 0; d + 1 < GD; d++)
@@ -571,7 +579,7 @@ struct SortedPipe {
 #pragma unroll
         for (int k = 0; k < GD; k++) {
             if (it >= s1) break;
-            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R);
+            accumulate(acc, x, (uint32_t)gbits, gmax, (uint32_t)R, xb);
             shift(e[NE - 1], ie[NE - 1]);
 #pragma unroll
             for (int d = 0; d + 1 < GD; d++)
@@ -626,11 +634,27 @@ __device__ __forceinline__ void sorted_acc_zero(float* acc, int lane, int R)
 
 // Row sums of the SG_WAVES x SG_PARTS accumulator arrays (after a barrier):
 // thread (p, r) adds a quarter of the arrays of row r, then the four
-// partials are added in p order (a fixed order: deterministic).  The result
-// is meaningful for threads with threadIdx.x < R (row threadIdx.x); ends with
-// a barrier-free read, after the barrier between the two halves.
+// partials are added in p order (a fixed order: deterministic); chunks of
+// 256 rows or more (TALL instantiations), half of them and then the two
+// halves.  The result is meaningful for threads with threadIdx.x < R (row
+// threadIdx.x); ends with a barrier-free read, after the barrier between
+// the two halves.
+template <bool TALL = false>
 __device__ __forceinline__ float sorted_row_sums(const float* s_acc, int R, float (*s_red)[256])
 {
+    if (TALL && R >= 256) {
+        float* sr = &s_red[0][0];  // [2][512]
+        const int rr = threadIdx.x & 511, pp = threadIdx.x >> 9;
+        if (rr < R) {
+            float part = 0.0f;
+            constexpr int NA = SG_WAVES * SG_PARTS / 2;
+#pragma unroll 4
+            for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
+            sr[pp * 512 + rr] = part;
+        }
+        __syncthreads();
+        return (pp == 0 && rr < R) ? sr[rr] + sr[512 + rr] : 0.0f;
+    }
     const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
     if (rr < R) {
         float part = 0.0f;

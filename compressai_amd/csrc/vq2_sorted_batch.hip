@@ -41,7 +41,7 @@ namespace vq2 {
 constexpr int SB_THREADS = 512;
 constexpr int SB_WAVES = SB_THREADS / 64;
 constexpr int SB_ARRAYS = SB_WAVES * SG_PARTS;  // accumulator arrays per workgroup
-constexpr int SB_MAX_SHM = 80 * 1024;           // two workgroups per CU
+constexpr int SB_MAX_SHM = 150 * 1024;          // two workgroups per CU up to 80 KiB (chunks of <= 255 rows)
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -161,7 +161,10 @@ __device__ __forceinline__ void sb_dots(const u32x4 c, const _Float16* s_xh, uin
 }
 
 // XT: activation dtype; EP 0: y (or slice partials), EP 1: fused top-1 keys.
-template <int CBT, int NB, int XT, int EP>
+// TALL: chunks of 256 rows or more or 17-bit positions (the row sums and
+// the position decode for them; the other instantiations keep the short
+// ones).
+template <int CBT, int NB, int XT, int EP, bool TALL>
 __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const SortedBatchArgs a)
 {
     typedef typename AccVec<NB>::type accv;
@@ -190,7 +193,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     // entry words and the first gathers go out first; the activation comes
     // from L2 meanwhile.  Gathers one iteration ahead (measured, LM head at
     // batch 2 / 4: 67.9 / 144.6 us; two ahead 68.8 / 144.9, three 70.9 / 154.8)
-    SortedPipe<CBT, 1, SB_WAVES> pipe;
+    SortedPipe<CBT, 1, SB_WAVES, TALL> pipe;
     pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R, a.c1mask);
 
     accv* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
@@ -265,22 +268,37 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     __syncthreads();
 
     // row sums: thread (pp, rr) adds half the arrays of row rr, then the two
-    // halves in order (the activation's LDS is free by now)
-    accv* s_red = (accv*)smem;  // [2][256]
-    const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
-    if (rr <= R) {
-        accv part = (accv)0.0f;
-        constexpr int NA = SB_ARRAYS / 2;
+    // halves in order (the activation's LDS is free by now); chunks of 256
+    // rows or more: thread rr adds both halves itself (the same order)
+    constexpr int NA = SB_ARRAYS / 2;
+    const bool tall = TALL && R >= 256;
+    const int rr = tall ? (int)threadIdx.x : (int)(threadIdx.x & 255), pp = tall ? 0 : (int)(threadIdx.x >> 8);
+    accv tsum = (accv)0.0f;
+    if (tall) {
+        if (rr <= R) {
+            accv p0 = (accv)0.0f, p1 = (accv)0.0f;
 #pragma unroll 4
-        for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
-        s_red[pp * 256 + rr] = part;
+            for (int w = 0; w < NA; w++) p0 += s_acc[w * (R + 1) + rr];
+#pragma unroll 4
+            for (int w = NA; w < 2 * NA; w++) p1 += s_acc[w * (R + 1) + rr];
+            tsum = p0 + p1;
+        }
+    } else {
+        accv* s_red = (accv*)smem;  // [2][256]
+        if (rr <= R) {
+            accv part = (accv)0.0f;
+#pragma unroll 4
+            for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
+            s_red[pp * 256 + rr] = part;
+        }
+        __syncthreads();
+        if (pp == 0 && rr <= R) tsum = s_red[rr] + s_red[256 + rr];
     }
-    __syncthreads();
     const bool own = pp == 0 && rr < sg.rb + (chunk < sg.nbig ? 1 : 0);
     const int64_t row = (int64_t)chunk * sg.rb + min(chunk, sg.nbig) + rr;
     float sum[NB];
     if (pp == 0 && rr <= R) {
-        const accv t = s_red[rr] + s_red[256 + rr];
+        const accv t = tsum;
 #pragma unroll
         for (int b = 0; b < NB; b++) sum[b] = ldexpf(t[b], -s_e[b]);
     } else {
@@ -289,7 +307,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     }
     if constexpr (EP == 1) {
         const float sc = own ? load_as_f32(sg.scale, a.s_dt, row) : 0.0f;
-        __shared__ uint64_t s_key[4][NB];
+        __shared__ uint64_t s_key[SB_WAVES][NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             uint64_t best = own ? argmax_key((sum[b] * sc) * a.rs, row) : 0;
@@ -297,13 +315,13 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
                 const uint64_t o = __shfl_xor(best, off);
                 best = o > best ? o : best;
             }
-            if (pp == 0 && lane == 0) s_key[wave][b] = best;
+            if (lane == 0) s_key[wave][b] = best;  // 0 from waves with no row of their own
         }
         __syncthreads();
         if (threadIdx.x < NB && (int)threadIdx.x < a.batch) {
             const int b = threadIdx.x;
             uint64_t best = s_key[0][b];
-            for (int w = 1; w < 4; w++) best = s_key[w][b] > best ? s_key[w][b] : best;
+            for (int w = 1; w < SB_WAVES; w++) best = s_key[w][b] > best ? s_key[w][b] : best;
             a.cand[(int64_t)blockIdx.x * a.batch + b] = best;
         }
     } else if (a.slices == 1) {
@@ -344,36 +362,44 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
 }
 
 // ------------------------------------------------------------------ launch
-template <int CBT, int NB, int XT, int EP>
+template <int CBT, int NB, int XT, int EP, bool TALL>
 static hipError_t launch_batch(const SortedBatchArgs& a, unsigned grid, size_t shm, hipStream_t st)
 {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)vq_sorted_batch_kernel<CBT, NB, XT, EP>,
+        attr = hipFuncSetAttribute((const void*)vq_sorted_batch_kernel<CBT, NB, XT, EP, TALL>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, SB_MAX_SHM);
     });
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((vq_sorted_batch_kernel<CBT, NB, XT, EP>), dim3(grid), dim3(SB_THREADS), shm, st, a);
+    hipLaunchKernelGGL((vq_sorted_batch_kernel<CBT, NB, XT, EP, TALL>), dim3(grid), dim3(SB_THREADS), shm, st, a);
     return hipGetLastError();
 }
 
-template <int NB, int EP>
-static hipError_t launch_batch_nb(int cb_dt, int x_dt, const SortedBatchArgs& a, unsigned grid, size_t shm,
-                                  hipStream_t st)
+template <int NB, int EP, bool TALL>
+static hipError_t launch_batch_t(int cb_dt, int x_dt, const SortedBatchArgs& a, unsigned grid, size_t shm,
+                                 hipStream_t st)
 {
     if (cb_dt == VQ2_DT_F16) {
         switch (x_dt) {
-        case VQ2_DT_F16: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_F16, EP>(a, grid, shm, st);
-        case VQ2_DT_BF16: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_BF16, EP>(a, grid, shm, st);
-        default: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_F32, EP>(a, grid, shm, st);
+        case VQ2_DT_F16: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_F16, EP, TALL>(a, grid, shm, st);
+        case VQ2_DT_BF16: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_BF16, EP, TALL>(a, grid, shm, st);
+        default: return launch_batch<VQ2_DT_F16, NB, VQ2_DT_F32, EP, TALL>(a, grid, shm, st);
         }
     }
     switch (x_dt) {
-    case VQ2_DT_F16: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_F16, EP>(a, grid, shm, st);
-    case VQ2_DT_BF16: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_BF16, EP>(a, grid, shm, st);
-    default: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_F32, EP>(a, grid, shm, st);
+    case VQ2_DT_F16: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_F16, EP, TALL>(a, grid, shm, st);
+    case VQ2_DT_BF16: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_BF16, EP, TALL>(a, grid, shm, st);
+    default: return launch_batch<VQ2_DT_BF16, NB, VQ2_DT_F32, EP, TALL>(a, grid, shm, st);
     }
+}
+
+template <int NB, int EP>
+static hipError_t launch_batch_nb(int cb_dt, int x_dt, bool tall, const SortedBatchArgs& a, unsigned grid,
+                                  size_t shm, hipStream_t st)
+{
+    return tall ? launch_batch_t<NB, EP, true>(cb_dt, x_dt, a, grid, shm, st)
+                : launch_batch_t<NB, EP, false>(cb_dt, x_dt, a, grid, shm, st);
 }
 
 static int batch_slots(int64_t batch) { return batch <= 2 ? 2 : 4; }
@@ -407,6 +433,8 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: x must be 16-byte aligned with a row stride >= n, a multiple "
                          "of 8 (got %lld)", (long long)c.x_stride);
     const int nb = batch_slots(c.batch);
+    // chunks of 256 rows or more, or 17-bit positions: the TALL kernels
+    const bool tall = rmax >= 256 || sorted_pbits(sorted_gbits(c.ng), (int)rmax) > 16;
     // activation (fp16, nb rows) or the row-sum stage, whichever is larger, then the accumulators
     const int64_t x_floats = std::max<int64_t>(n * nb / 2, 2 * 256 * nb);
     const size_t shm = (size_t)(x_floats + (int64_t)SB_ARRAYS * (rmax + 1) * nb) * sizeof(float);
@@ -479,13 +507,13 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {
-        err = nb == 2 ? launch_batch_nb<2, 1>(c.cb_dt, c.x_dt, a, (unsigned)wg, shm, st)
-                      : launch_batch_nb<4, 1>(c.cb_dt, c.x_dt, a, (unsigned)wg, shm, st);
+        err = nb == 2 ? launch_batch_nb<2, 1>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st)
+                      : launch_batch_nb<4, 1>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st);
         if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMM launch");
         return argmax_final_launch(a.cand, wg, c.batch, top1_idx, top1_val, c.stream);
     }
-    err = nb == 2 ? launch_batch_nb<2, 0>(c.cb_dt, c.x_dt, a, (unsigned)wg, shm, st)
-                  : launch_batch_nb<4, 0>(c.cb_dt, c.x_dt, a, (unsigned)wg, shm, st);
+    err = nb == 2 ? launch_batch_nb<2, 0>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st)
+                  : launch_batch_nb<4, 0>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMM launch");
     return VQ2_OK;
 }

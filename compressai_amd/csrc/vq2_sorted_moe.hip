@@ -291,7 +291,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         entries(e);
         sorted_acc_zero(acc, lane, R);
         if constexpr (FAST) {
-            rht2k_build<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale);
+            rht2k_build<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, SG_XB);
         } else {
             stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
             build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
@@ -340,7 +340,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
             e = s_top[kslot];
             entries(e);
         }
-        if constexpr (FAST) rht2k_transform<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale);
+        if constexpr (FAST) rht2k_transform<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, SG_XB);
         else build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
     } else {
         // the pair's gate_up rows: slices added in order, row scale, then
@@ -459,10 +459,10 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
             build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
         }
     }
-    if constexpr (F2K == 0) x_finalize(s_x, s_split, n, a.g.xscale);
+    if constexpr (F2K == 0) x_finalize(s_x, s_split, n, a.g.xscale, SG_XB);
     __syncthreads();
     pipe.gathers();
-    pipe.run(acc, s_split, pl.gbits, pl.ng, R);
+    pipe.run(acc, s_split, pl.gbits, pl.ng, R, SG_XB);
     __syncthreads();
 
     const int rr = threadIdx.x;
@@ -628,7 +628,8 @@ static hipError_t launch_fused(int cb_dt, int x_dt, const SortedMoeArgs& a, cons
 static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_experts, int64_t rows, int64_t ng,
                      SortedPoolArgs& pa)
 {
-    const int64_t r_lim = sorted_max_rows(ng);
+    // pools: chunks of at most 255 rows with 16-bit positions
+    const int64_t r_lim = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
     if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: %s: ng=%lld unsupported", name, (long long)ng);
     if (pc.rows != rows || pc.ng != ng)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool holds [%lld rows, %lld groups], expected [%lld, %lld]",

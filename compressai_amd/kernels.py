@@ -489,7 +489,7 @@ class SortedPlanes:
     Built at load time by the modules that own a matrix (PackedLinear,
     PackedLMHead); the planes themselves stay the public format."""
 
-    def __init__(self, i0, i1, out_rows, n, device=None, threads=0, chunk_align=None):
+    def __init__(self, i0, i1, out_rows, n, device=None, threads=0, chunk_align=None, rows_per_chunk=None):
         lib = _lib.load()
         n, out_rows = int(n), int(out_rows)
         if n % 8:
@@ -514,7 +514,10 @@ class SortedPlanes:
         dev = torch.device(device) if device is not None else i0.device
         if chunk_align is None:  # whole rounds of chunks over the device's CUs
             chunk_align = _cu_count(dev) if dev.type == "cuda" else 1
-        R = int(lib.vq2_sorted_rows_per_chunk(out_rows, ng, int(chunk_align)))
+        # rows_per_chunk: the library's default (vq2_sorted_rows_per_chunk)
+        # unless given; vq2_sorted_pack refuses a height its positions cannot hold
+        R = int(lib.vq2_sorted_rows_per_chunk(out_rows, ng, int(chunk_align))) if rows_per_chunk is None \
+            else int(rows_per_chunk)
         if R == 0:
             raise Vq2Error(f"sorted layout: n={n} unsupported")
         self.out_rows, self.n, self.rows_per_chunk = out_rows, n, R
@@ -678,12 +681,13 @@ def sorted_batch_slices(planes, dev) -> int:
 
 def sorted_batch_fits(planes, batch) -> bool:
     """Whether the batch kernel's LDS (fp16 activation of 2 or 4 rows, and
-    the accumulators of the tallest chunk) fits its 80 KiB: n = 2048 with
-    any chunk height, n = 6144 with the default 62-row chunks."""
+    the accumulators of the tallest chunk) fits its 150 KiB (two workgroups
+    per CU up to 80 KiB): n = 2048 with any chunk height, n = 6144 with the
+    default 62-row chunks."""
     nb = 2 if batch <= 2 else 4
     n = planes[0].n
     R = max(p.rows_per_chunk for p in planes)
-    return (max(n * nb // 2, 512 * nb) + 16 * (R + 1) * nb) * 4 <= 80 * 1024
+    return (max(n * nb // 2, 512 * nb) + 16 * (R + 1) * nb) * 4 <= 150 * 1024
 
 
 def _batch_x(x, n):

@@ -326,17 +326,21 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  * lets the lanes of a wave share codebook lines: random 16-byte centroid
  * gathers are capped by the L2 request rate, sorted ones are not.
  *   rows are cut into n_chunks = ceil(out_rows / rows_per_chunk) chunks
- *   (rows_per_chunk at most min(2^(16 - ceil(log2 ng)) - 1, 255);
- *   vq2_sorted_rows_per_chunk gives the default: over a multiple of
+ *   (rows_per_chunk at most min(2^(17 - ceil(log2 ng)) - 1, 511);
+ *   vq2_sorted_rows_per_chunk gives the default: at most
+ *   min(2^(16 - ceil(log2 ng)) - 1, 255) rows, over a multiple of
  *   chunk_align chunks when the chunks keep >= 128 rows, e.g. chunk_align =
- *   the CU count) of near-equal height: chunk c holds rows
+ *   the CU count; a matrix tall enough that a multiple of 2 x chunk_align
+ *   chunks of more rows (up to the first limit) covers it takes those, e.g.
+ *   a 151,936-row LM head: 512 chunks of 297 rows) of near-equal height:
+ *   chunk c holds rows
  *   [c * rb + min(c, nbig), + rb + (c < nbig)), rb = out_rows / n_chunks,
  *   nbig = out_rows % n_chunks; a chunk's codes are sorted by value and
  *   dealt into 64-lane instructions in which no row repeats within a
  *   32-lane half (lanes 0-31, 32-62); lane 63 carries the instruction's
  *   base code (its smallest), every other lane one code as the 24-bit field
  *   (code - base) << P | row_in_chunk << ceil(log2 ng) | group, P =
- *   ceil(log2 ng) + bitlen(rows_per_chunk) <= 16 (an instruction is closed
+ *   ceil(log2 ng) + bitlen(rows_per_chunk) <= 17 (an instruction is closed
  *   before an offset would reach 2^(24 - P)); 4 instructions form an
  *   iteration of 192 uint32 (768 bytes): lane l's three words at 3 l are
  *   lo16(F0) | lo16(F1) << 16, lo16(F2) | lo16(F3) << 16 and the four
@@ -426,8 +430,9 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
  * vq2_sorted_gemv, which it may share) holds the partials and the chunk's
  * last workgroup sums them in slice order (deterministic).  Needs
  * n * (2 or 4) * 2 + 64 * (rows_per_chunk + 1) * (2 or 4) bytes of LDS at
- * most 80 KiB (e.g. n = 2048 with 255-row chunks, n = 6144 with 62-row
- * chunks), else VQ2_ERR_UNSUPPORTED.  Replaces the PackedLinear batch > 1
+ * most 150 KiB (two workgroups per CU up to 80 KiB, e.g. n = 2048 with
+ * 255-row chunks, n = 6144 with 62-row chunks; one above), else
+ * VQ2_ERR_UNSUPPORTED.  Replaces the PackedLinear batch > 1
  * fallback, dequant + F.linear (vq2/runtime.py:82-89, 105-110). */
 size_t vq2_sorted_gemm_batch_workspace(const vq2_sorted_mat* mats, int n_mat, int64_t batch, int slices);
 int vq2_sorted_gemm_batch(const void* x, int x_dt, int64_t batch, int64_t x_stride, int n_mat,
@@ -452,7 +457,8 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
  * idx [n_experts, rows, ng] (the int16 stage-1 plane; idx1, the stage-2
  * plane as int16 -- a (16,8) uint8 plane widened to values 0..255 -- or
  * NULL) expert by expert, each as vq2_sorted_pack packs a matrix with the
- * same rows_per_chunk R, and pads every chunk's stage-1 and stage-2 entries
+ * same rows_per_chunk R (at most min(2^(16 - ceil(log2 ng)) - 1, 255): pools
+ * keep 16-bit positions), and pads every chunk's stage-1 and stage-2 entries
  * (dummy-row entries) to the pool's largest counts, so chunk c of expert e
  * holds iterations [(e * C + c) * ipc, (e * C + c + 1) * ipc), C =
  * ceil(rows / R), its stage-2 ones from *stage1_iters on.  *n_iters =

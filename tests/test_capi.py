@@ -74,7 +74,7 @@ def test_moe_and_rht_reject_bad_arguments_on_host():
 
 def test_sorted_batch_rejects_bad_arguments_on_host():
     """vq2_sorted_gemm_batch / _argmax: batch outside 1..4, a short or
-    unaligned activation row, LDS beyond 80 KiB and a bad chunk height are
+    unaligned activation row, LDS beyond 150 KiB and a bad chunk height are
     refused before any HIP call (the pointers are never dereferenced)."""
     L = _lib.load()
 
@@ -89,11 +89,11 @@ def test_sorted_batch_rejects_bad_arguments_on_host():
     assert "batch=0" in _err(L.vq2_sorted_gemm_batch(*args(0, 2048, m, 2048)))
     assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2040, m, 2048)))
     assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2052, m, 2048)))
-    # n = 16384 (ng 2048, chunks of at most 31 rows): 4 fp16 rows are 128 KiB of LDS
-    big = mat(rows=64, ng=2048, R=31)
-    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(4, 16384, big, 16384)))
-    # rows_per_chunk beyond what 16-bit positions hold for ng = 256
-    assert "rows_per_chunk" in _err(L.vq2_sorted_gemm_batch(*args(2, 2048, mat(R=300), 2048)))
+    # n = 32768 (ng 4096, chunks of at most 31 rows): 4 fp16 rows are 256 KiB of LDS
+    big = mat(rows=64, ng=4096, R=31)
+    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(4, 32768, big, 32768)))
+    # rows_per_chunk beyond 511 (what 17-bit positions hold for ng = 256)
+    assert "rows_per_chunk" in _err(L.vq2_sorted_gemm_batch(*args(2, 2048, mat(R=600), 2048)))
     msg = _err(L.vq2_sorted_gemm_batch_argmax(4096, 0, 3, 2048, ctypes.byref(m), 4096, None, 1, 1, 2048, 1.0,
                                               4096, 1 << 20, None, None, None))
     assert "out_idx" in msg

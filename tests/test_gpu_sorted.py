@@ -56,6 +56,48 @@ def test_sorted_gemv_vs_oracle(dev, rows, n, bpw, fused, slices):
     assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
 
 
+@pytest.mark.parametrize("rows,n,bpw,R,slices", [
+    (700, 2048, 2, 350, None),    # 17-bit positions: bit 16 in each field's high byte
+    (1200, 2048, 4, 300, 3),
+    (300, 6144, 4, 120, 2),       # 6144 wide: 10 group bits + 7 row bits
+    (600, 2048, 3, 511, None),    # (16,8), the tallest chunk
+])
+def test_sorted_taller_chunks_vs_oracle(dev, rows, n, bpw, R, slices):
+    """Chunks of up to 511 rows (the LM head's default, 297 rows, is one of
+    them): the batch-1 kernel with the RHT prologue (row sums of 256 rows
+    or more in two halves), the batch kernel at B = 2 and 4 and, at 2 bpw,
+    the fused top-1 of both, against the oracle."""
+    from act_rounding import fp16_row_scaled
+
+    m = synth.vq_matrix(9560 + R, rows, n, bpw=bpw)
+    cb0 = synth.codebook(9561)
+    cb1 = synth.codebook(9562, 256 if bpw == 3 else 65536) if bpw > 2 else None
+    sp = K.SortedPlanes(m["idx0"], m["idx1"], rows, n, device=dev, rows_per_chunk=R)
+    assert sp.rows_per_chunk == R
+    c0, c1, sc = cb0.to(dev), None if cb1 is None else cb1.to(dev), m["scale"].to(dev)
+    x = synth.activations(9563, n, dtype=torch.float16)
+    perm, sign = synth.permutation(9564, n), synth.signs(9565, n)
+    (y,) = K.vq_sorted_gemv(x.to(dev), [(sp, sc)], c0, c1, n, perm.to(dev), sign.to(dev), 2048, slices=slices)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+    assert O.max_rel_err(y.cpu().numpy(), y64[0]) < TOL
+    for B in (2, 4):
+        xb = synth.activations(9566 + B, (B, n), dtype=torch.float32) * 0.5
+        (yb,) = K.vq_sorted_gemm_batch(xb.to(dev), [(sp, sc)], c0, c1, n, slices=slices)
+        # the batch kernel's fp16 activation with a power-of-two scale per row
+        _, yb64 = O.vq_gemv(fp16_row_scaled(xb.numpy()), m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+        for b in range(B):
+            assert O.max_rel_err(yb.cpu().numpy()[b], yb64[b]) < 1e-5, (B, b)
+        if bpw == 2:
+            idx, val = K.vq_sorted_gemm_batch_argmax(xb.to(dev), sp, sc, c0, None, n)
+            for b in range(B):
+                assert int(idx[b]) == int(np.argmax(yb64[b])), (B, b)
+    if bpw == 2:
+        idx, val = K.vq_sorted_gemv_argmax(x.to(dev), sp, sc, c0, None, n, perm.to(dev), sign.to(dev), 2048)
+        assert int(idx[0]) == int(np.argmax(y64[0]))
+        assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
+
+
 def test_sorted_gemv_bf16_codebook_and_outputs(dev):
     rows, n = 1536, 2048
     m, cb0, cb1, sp = _mk(9520, rows, n, 4, dev, cb_dtype=torch.bfloat16)
@@ -179,6 +221,8 @@ def test_sorted_lm_head_top1_full_size(dev, fused):
     equals the argmax of the oracle's logits."""
     rows, n = 151936, 2048
     m, cb0, _, sp = _mk(9550, rows, n, 2, dev)
+    if 2 * 255 * K._cu_count(dev) < rows:  # the tall-matrix chunking: 17-bit positions
+        assert sp.rows_per_chunk > 255 and sp.n_chunks % (2 * K._cu_count(dev)) == 0
     perm, sign = synth.permutation(9552, n), synth.signs(9553, n)
     if fused:
         x = synth.activations(9551, n, dtype=torch.float16)

@@ -160,12 +160,12 @@ def test_batch_gemm_errors(dev):
     s = m["scale"].to(dev)
     with pytest.raises(Vq2Error, match="1..4 activation rows"):
         K.vq_sorted_gemm_batch(torch.zeros(5, 2048, device=dev), [(sp, s)], cb0.to(dev), None, 2048)
-    # n = 16384: the fp16 activation of 4 rows alone is 128 KiB of LDS
-    big = synth.vq_matrix(9771, 64, 16384, bpw=2)
-    spb = K.SortedPlanes(big["idx0"], None, 64, 16384, device=dev)
+    # n = 32768: the fp16 activation of 4 rows alone is 256 KiB of LDS
+    big = synth.vq_matrix(9771, 64, 32768, bpw=2)
+    spb = K.SortedPlanes(big["idx0"], None, 64, 32768, device=dev)
     with pytest.raises(Vq2Error, match="LDS"):
-        K.vq_sorted_gemm_batch(torch.zeros(4, 16384, device=dev), [(spb, big["scale"].to(dev))], cb0.to(dev), None,
-                               16384)
+        K.vq_sorted_gemm_batch(torch.zeros(4, 32768, device=dev), [(spb, big["scale"].to(dev))], cb0.to(dev), None,
+                               32768)
 
 
 def test_batch_paths_graph_replays_match_eager(dev):

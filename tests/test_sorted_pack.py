@@ -69,18 +69,26 @@ def _decode(sp: SortedPlanes):
     return out
 
 
-@pytest.mark.parametrize("rows,n,bpw", [(300, 2048, 2), (256, 2048, 4), (100, 6144, 4), (1000, 512, 2),
-                                        (97, 800, 2), (5, 64, 4), (1, 2048, 2), (3, 16, 2), (200, 2048, 3),
-                                        (7, 16, 3)])
-def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw):
+@pytest.mark.parametrize("rows,n,bpw,R", [(300, 2048, 2, None), (256, 2048, 4, None), (100, 6144, 4, None),
+                                          (1000, 512, 2, None), (97, 800, 2, None), (5, 64, 4, None),
+                                          (1, 2048, 2, None), (3, 16, 2, None), (200, 2048, 3, None),
+                                          (7, 16, 3, None),
+                                          # taller chunks, 17-bit positions (bit 16 in the high byte)
+                                          (700, 2048, 2, 350), (600, 2048, 4, 300), (300, 6144, 4, 120),
+                                          (520, 512, 3, 511), (300, 2048, 3, 300)])
+def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw, R):
     ng = n // 8
     m = synth.vq_matrix(9800 + rows + bpw, rows, n, bpw=bpw)
-    sp = SortedPlanes(m["idx0"], m["idx1"], rows, n, device="cpu", threads=3)
-    R = int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1))
+    sp = SortedPlanes(m["idx0"], m["idx1"], rows, n, device="cpu", threads=3, rows_per_chunk=R)
     gb = _gb(ng)
-    assert sp.rows_per_chunk == R and (R + 1) * (1 << gb) <= 1 << 16 and _pb(ng, R) <= 16
-    assert sp.n_chunks == -(-rows // R) and R <= 255
-    assert R * sp.n_chunks - rows < sp.n_chunks      # the rows split evenly over the chunks
+    if R is None:  # the default chunking: 16-bit positions, at most 255 rows
+        R = int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1))
+        assert (R + 1) * (1 << gb) <= 1 << 16 and _pb(ng, R) <= 16 and R <= 255
+    else:
+        assert _pb(ng, R) == 17 or R == 511
+    assert sp.rows_per_chunk == R and sp.n_chunks == -(-rows // R)
+    if sp.rows_per_chunk == int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1)):
+        assert R * sp.n_chunks - rows < sp.n_chunks  # the default: the rows split evenly over the chunks
     assert rows // sp.n_chunks + (1 if rows % sp.n_chunks else 0) <= R
     assert sp.n_iters == sp.n_chunks * sp.iters_per_chunk                 # chunks padded to one size
     assert sp.entries.numel() == sp.n_iters * ITER_WORDS
@@ -156,15 +164,21 @@ def test_sorted_pack_rejects_bad_input():
                            ctypes.byref(ipc1), ctypes.byref(n_it), 1)
     assert st == _lib.ERR_ARG and n_it.value > 1   # capacity too small: the needed size is reported
     assert n_it.value == ipc.value and ipc1.value == ipc.value
-    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 256, buf.data_ptr(), 1000, ctypes.byref(ipc),
+    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 64, 512, buf.data_ptr(), 1000, ctypes.byref(ipc),
                            ctypes.byref(ipc1), ctypes.byref(n_it), 1)
-    assert st == _lib.ERR_ARG                     # rows_per_chunk beyond the 16-bit position field
+    assert st == _lib.ERR_ARG                     # rows_per_chunk beyond 511
+    st = L.vq2_sorted_pack(m["idx0"].data_ptr(), None, 16, 2048, 64, buf.data_ptr(), 1000, ctypes.byref(ipc),
+                           ctypes.byref(ipc1), ctypes.byref(n_it), 1)
+    assert st == _lib.ERR_ARG                     # ng 2048: 64 rows need an 18-bit position
 
 
 def test_sorted_rows_per_chunk_alignment():
     L = _lib.load()
-    assert L.vq2_sorted_rows_per_chunk(151936, 256, 256) == 198   # 768 chunks: 3 rounds of 256 CUs
-    assert L.vq2_sorted_rows_per_chunk(151936, 256, 1) == 255     # 596 chunks
+    # the LM head: 512 chunks of <= 297 rows (17-bit positions), one round
+    # of two workgroups per CU, instead of 768 of 198 with 16-bit positions
+    assert L.vq2_sorted_rows_per_chunk(151936, 256, 256) == 297
+    assert L.vq2_sorted_rows_per_chunk(151936, 256, 1) == 255     # 596 chunks (no alignment asked)
+    assert L.vq2_sorted_rows_per_chunk(100000, 256, 256) == 196   # 512 chunks, 16-bit positions suffice
     assert L.vq2_sorted_rows_per_chunk(6144, 256, 256) == 246     # 25 chunks (aligned ones would be too short)
     assert L.vq2_sorted_rows_per_chunk(2048, 768, 1) == 63        # 6144-wide: 63 rows at most (33 chunks)
     assert L.vq2_sorted_rows_per_chunk(100, 1 << 16, 1) == 0      # n beyond the 16-bit position field
