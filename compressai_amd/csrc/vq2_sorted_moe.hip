@@ -270,9 +270,11 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
 
     // chunk `chunk` of expert ex: iterations [(ex * C + chunk) * ipc, + ipc)
     // (in the pool: ex < n_experts, chunk < C), this slice's share of them
-    // gathers two iterations ahead in gate_up, one in down (measured: T = 1
-    // layer 22.7 / 21.4 / 23.2 / 21.0 us for 1-1, 2-2, 1-2, 2-1)
-    SortedPipe<CBT, MODE == 2 ? 1 : 2> pipe;
+    // gathers two iterations ahead in gate_up, one in down (measured, one
+    // workgroup per CU: T = 1 layer 22.7 / 21.4 / 23.2 / 21.0 us for 1-1,
+    // 2-2, 1-2, 2-1); one ahead in both parts of the one launch with fp16
+    // codebooks, which runs two workgroups per CU (vq_sorted_moe_fused_kernel)
+    SortedPipe<CBT, (MODE == 2 || (FUSED && CBT == VQ2_DT_F16)) ? 1 : 2> pipe;
     auto entries = [&](int64_t ex) {
         const int c_beg = (int)((ex * pl.C + chunk) * pl.ipc);
         const int s0 = c_beg + slice * a.sq + min(slice, a.sr);
@@ -503,8 +505,18 @@ __global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_kernel(const SortedM
 // workgroup's XCD is its own index mod 8), the rest down.  Workgroups are
 // dispatched in index order and a gate_up workgroup waits for nothing, so
 // every gate_up workgroup a down workgroup waits for is running or done.
+// Two workgroups per CU (64 VGPRs, ~76 KiB of LDS each): down workgroups
+// then start beside running gate_up ones, issue their loads and wait there,
+// instead of starting only when a gate_up workgroup leaves its CU (stamps:
+// at T = 1 the down workgroups started ~11.5 us into the launch, when the
+// gate_up ones ended).  Measured with the one-ahead pipelines: T = 1
+// 20.1 -> 19.8-20.0 us, T = 8 70.7 -> 66.8 us (64.5 with two gate_up
+// slices); with the gate_up part's two-ahead pipeline the 64-VGPR bound
+// spilled and T = 1 took 20.7 us.  bf16 codebooks (whose centroid
+// conversion needs more registers: 9-12 spilled at 64) keep one workgroup
+// per CU and the two-ahead gate_up pipeline.
 template <int CBT, int GU, int XT>
-__global__ void __launch_bounds__(SG_THREADS) vq_sorted_moe_fused_kernel(const SortedMoeArgs a, const SortedMoeArgs d)
+__global__ void __launch_bounds__(SG_THREADS, CBT == VQ2_DT_F16 ? 8 : 1) vq_sorted_moe_fused_kernel(const SortedMoeArgs a, const SortedMoeArgs d)
 {
     extern __shared__ __align__(16) float smem[];
     const int gu_blocks = (a.wgs + 7) & ~7;

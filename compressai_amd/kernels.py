@@ -858,12 +858,15 @@ _MOE_FIXED_US = (2.5, 2.0)
 def moe_slices(units, codes_per_unit, cu, fixed_us, one_launch=False):
     """Slices per chunk for `units` (pair, chunk) units: the count that
     minimises rounds x (work per slice + fixed cost), with one 16-wave
-    workgroup per CU at a time.  one_launch (gate_up and down in one launch):
-    units that fill the device on their own take one slice, since the down
-    workgroups fill a last partial round (measured, T = 8: one gate_up slice
-    72.97 us per layer, two 80.2)."""
-    if one_launch and units >= cu:
+    workgroup per CU at a time.  one_launch (gate_up and down in one launch,
+    two workgroups per CU): units that fill twice the CUs on their own take
+    one slice, units that fill the CUs two (measured, T = 8, 360 gate_up and
+    648 down units: gate_up / down slices 1 / 1 66.8 us per layer, 2 / 1
+    64.5, 3 / 1 64.5, 2 / 2 65.9, 1 / 2 70.5)."""
+    if one_launch and units >= 2 * cu:
         return 1
+    if one_launch and units >= cu:
+        return 2
     best, best_t = 1, None
     for s in range(1, 33):
         t = -(-units * s // cu) * (codes_per_unit / _MOE_RATE / s + fixed_us)

@@ -220,13 +220,19 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
 
 def test_moe_slices_cost_model():
     """Slice counts of the sorted MoE launches on 256 CUs: T = 1 fills one
-    round (gate_up 45 units x 5, down 81 x 3); T = 8 takes 2 and 1."""
+    round (gate_up 45 units x 5, down 81 x 3); T = 8 takes 2 and 1.  In the
+    one launch (two workgroups per CU) units that fill the CUs take 2 slices
+    and units that fill them twice 1; fewer follow the model."""
     from compressai_amd.kernels import moe_slices
 
     assert moe_slices(45, 205 * 256, 256, 2.5) == 5
     assert moe_slices(81, 228 * 64, 256, 2.0) == 3
     assert moe_slices(360, 205 * 256, 256, 2.5) == 2
     assert moe_slices(648, 228 * 64, 256, 2.0) == 1
+    assert moe_slices(45, 205 * 256, 256, 2.5, one_launch=True) == 5
+    assert moe_slices(81, 228 * 64, 256, 2.0, one_launch=True) == 3
+    assert moe_slices(360, 205 * 256, 256, 2.5, one_launch=True) == 2
+    assert moe_slices(648, 228 * 64, 256, 2.0, one_launch=True) == 1
 
 
 @pytest.mark.parametrize("s2", ["u8", "i16"])
