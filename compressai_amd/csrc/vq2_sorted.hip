@@ -77,11 +77,18 @@ namespace vq2 {
 // put more codes on each code value, so a wave's 63 sorted codes span
 // fewer codebook lines.  (Taller chunks for the other shapes measured
 // slower: gate+up 16.3 -> 17.5 us at 473 rows, down 13.8 -> 16.8 at 228.)
+// With chunk_align > 1 a matrix of fewer than 2^20 codes takes chunks of at
+// most 64 rows: its launch is bound by latency, and more, smaller
+// workgroups finish sooner (q, k and v in one launch: 9.5 us at 15 chunks of
+// 171-228 rows, 8.3 at 48 of 64; the o projection alone 9.0 -> 7.8 us).
 constexpr int64_t SG_MIN_ALIGNED_R = 128;
+constexpr int64_t SG_SMALL_CODES = int64_t(1) << 20;
+constexpr int64_t SG_SMALL_R = 64;
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
 {
-    const int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
+    int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
     if (rmax == 0 || out_rows < 1) return 0;
+    if (chunk_align > 1 && out_rows * ng < SG_SMALL_CODES) rmax = std::min(rmax, SG_SMALL_R);
     if (chunk_align > 1) {
         const int64_t rmax17 = sorted_max_rows(ng, 17), two = 2 * chunk_align;
         const int64_t n17 = ((out_rows + rmax17 - 1) / rmax17 + two - 1) / two * two;
