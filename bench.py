@@ -86,6 +86,8 @@ class DenseLayers:
         self.layers = []
         t0 = time.perf_counter()
         qkv_codes = sum(out * (n // 8) * (2 if bpw == 4 else 1) for name, out, n, bpw in self.PROJ[:3])
+        # q, k and v share one chunk height over their rows, as PackedProjections packs them
+        qkv_R = K.sorted_launch_rows_per_chunk([out for _, out, _, _ in self.PROJ[:3]], HIDDEN // 8, dev)
         for _ in range(L):
             lay = {}
             for name, out, n, bpw in self.PROJ:
@@ -93,7 +95,9 @@ class DenseLayers:
                 i1 = rand_i16((out, n // 8), g, dev) if bpw == 4 else None
                 sp = None
                 codes = out * (n // 8) * (2 if bpw == 4 else 1)
-                if codes >= SORTED_MIN_CODES or (name in ("q", "k", "v") and qkv_codes >= SORTED_MIN_LAUNCH_CODES):
+                if name in ("q", "k", "v") and qkv_codes >= SORTED_MIN_LAUNCH_CODES:
+                    sp = K.SortedPlanes(i0, i1, out, n, device=dev, rows_per_chunk=qkv_R)
+                elif codes >= SORTED_MIN_CODES:
                     sp = K.SortedPlanes(i0, i1, out, n, device=dev)
                 lay[name] = (i0, i1, rand_scale(out, g, dev), out, n, sp)
             self.layers.append(lay)
@@ -138,12 +142,12 @@ class DenseLayers:
 
     def step(self, l):
         """One decoder layer's projections, as the runtime runs them at batch
-        1: q/k/v in one sorted-layout launch (PackedProjections), o on the
-        gather kernel, gate/up and down on the sorted layout (PackedLinear);
-        every launch rotates its activation in LDS."""
+        1: q/k/v in one sorted-layout launch (PackedProjections), o, gate/up
+        and down on the sorted layout (PackedLinear); every launch rotates its
+        activation in LDS."""
         lay = self.layers[l]
         self.sorted(lay, ("q", "k", "v"), self.x_attn, self.perm_h, self.sign_h)
-        self.fused(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
+        self.sorted(lay, ("o",), self.x_o, self.perm_h, self.sign_h)
         self.sorted(lay, ("gate", "up"), self.x_mlp, self.perm_h, self.sign_h)
         self.sorted(lay, ("down",), self.x_down, self.perm_i, self.sign_i)
 
@@ -264,7 +268,9 @@ def bench_dense(args, dev):
 
 def bench_config0(args, dev, copies=1024):
     """RHT(2048, permutation + signs) + 2 bpw GEMV 2048 x 2048 at
-    batch 1, one fused launch per call, over 1024 distinct matrices (1 GiB)."""
+    batch 1, one fused launch per call, over 1024 distinct matrices (1 GiB):
+    as PackedLinear runs it (code-sorted layout, about 0.75 x CUs chunks of
+    one workgroup each), and on the gather kernel (vq_gemv_rht) beside it."""
     import torch
 
     from compressai_amd import kernels as K, synth
@@ -273,24 +279,34 @@ def bench_config0(args, dev, copies=1024):
     g = torch.Generator(device=dev).manual_seed(1000)
     cb = synth.codebook(1000).to(dev)
     mats = [(rand_i16((out, n // 8), g, dev), rand_scale(out, g, dev)) for _ in range(copies)]
+    sps = [K.SortedPlanes(i0, None, out, n, device=dev) for i0, _ in mats]
     x = synth.activations(1004, n, dtype=torch.float16).to(dev)
     sign = synth.signs(1005, n).to(dev)
     perm = synth.permutation(1006, n).to(dev)
     y = torch.empty(out, dtype=torch.float32, device=dev)
 
     def fwd(l):
+        K.vq_sorted_gemv(x, [(sps[l], mats[l][1])], cb, None, n, perm, sign, 2048, ys=[y])
+
+    def fwd_gather(l):
         i0, s = mats[l]
         K.vq_gemv_rht(x, [(i0, None, s, out)], cb, None, n, perm, sign, 2048, ys=[y])
 
-    gr = capture(fwd, copies, dev)
-    time_graph(gr, 1, dev)
-    us = statistics.median(time_graph(gr, 1, dev)[0] * 1e3 / copies for _ in range(REPEATS))
+    res = {}
+    for name, f in (("sorted", fwd), ("gather", fwd_gather)):
+        gr = capture(f, copies, dev)
+        time_graph(gr, 1, dev)
+        res[name] = statistics.median(time_graph(gr, 1, dev)[0] * 1e3 / copies for _ in range(REPEATS))
+        del gr
+    us = res["sorted"]
     nbytes = out * (n // 8) * 2 + out * 2
     gbps = nbytes / (us * 1e-6) / 1e9
-    log(f"config 0 (RHT 2048 + 2 bpw 2048x2048, {copies} copies): {us:.2f} us/call, {gbps:.1f} GB/s")
-    del gr, mats
+    log(f"config 0 (RHT 2048 + 2 bpw 2048x2048, {copies} copies): {us:.2f} us/call, {gbps:.1f} GB/s "
+        f"({sps[0].n_chunks} chunks of {sps[0].rows_per_chunk} rows; gather kernel {res['gather']:.2f} us)")
+    del mats, sps
     torch.cuda.empty_cache()
-    return {"us": round(us, 3), "gbps": round(gbps, 2), "bytes": nbytes, "copies": copies}
+    return {"us": round(us, 3), "gbps": round(gbps, 2), "bytes": nbytes, "copies": copies,
+            "us_gather_kernel": round(res["gather"], 3)}
 
 
 def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
@@ -776,8 +792,8 @@ def main():
         "config": {
             "workload": "configs[1]: dense decoder-layer projection set, batch 1, hidden 2048 (q,k,v,o 2 bpw; "
                         "gate,up,down 4 bpw; RHT 2048 x3 + 6144, each with permutation + signs); fp16 codebooks/"
-                        "scales/activations, fp32 out; q/k/v in one code-sorted launch (PackedProjections), o "
-                        "on the gather kernel, gate/up, down on the code-sorted layout (PackedLinear), batch 1",
+                        "scales/activations, fp32 out; q/k/v in one code-sorted launch (PackedProjections), o, "
+                        "gate/up, down on the code-sorted layout (PackedLinear), batch 1",
             "layers_cycled": min(d["layers"], d["steps"]),
             "layer_sets_resident": d["layers"],
             "bytes_per_step": d["bytes_per_step"],

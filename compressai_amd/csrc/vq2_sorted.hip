@@ -77,18 +77,24 @@ namespace vq2 {
 // put more codes on each code value, so a wave's 63 sorted codes span
 // fewer codebook lines.  (Taller chunks for the other shapes measured
 // slower: gate+up 16.3 -> 17.5 us at 473 rows, down 13.8 -> 16.8 at 228.)
-// With chunk_align > 1 a matrix of fewer than 2^20 codes takes chunks of at
-// most 64 rows: its launch is bound by latency, and more, smaller
-// workgroups finish sooner (q, k and v in one launch: 9.5 us at 15 chunks of
-// 171-228 rows, 8.3 at 48 of 64; the o projection alone 9.0 -> 7.8 us).
+// With chunk_align > 1 a matrix of fewer than 2^20 codes takes about
+// 0.75 x chunk_align chunks (at most 64 rows each), one workgroup each: its
+// launch is bound by latency, and one slice per chunk saves the slice sum
+// (the o projection: 8.5 us on the gather kernel, 7.3 at 187 chunks of 11
+// rows; 9.0 at 9 chunks of 228 rows x 8 slices; q, k and v in one launch,
+// chunks from their total rows: 7.7 us at 192 chunks of 16 rows, 9.5 at 15
+// of 171-228 x 8 slices).
 constexpr int64_t SG_MIN_ALIGNED_R = 128;
 constexpr int64_t SG_SMALL_CODES = int64_t(1) << 20;
 constexpr int64_t SG_SMALL_R = 64;
 int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
 {
-    int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
+    const int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
     if (rmax == 0 || out_rows < 1) return 0;
-    if (chunk_align > 1 && out_rows * ng < SG_SMALL_CODES) rmax = std::min(rmax, SG_SMALL_R);
+    if (chunk_align > 1 && out_rows * ng < SG_SMALL_CODES) {
+        const int64_t r = (4 * out_rows + 3 * chunk_align - 1) / (3 * chunk_align);
+        return std::max<int64_t>(1, std::min(r, std::min(rmax, SG_SMALL_R)));
+    }
     if (chunk_align > 1) {
         const int64_t rmax17 = sorted_max_rows(ng, 17), two = 2 * chunk_align;
         const int64_t n17 = ((out_rows + rmax17 - 1) / rmax17 + two - 1) / two * two;

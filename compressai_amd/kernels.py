@@ -568,6 +568,22 @@ def _cu_count(dev: torch.device) -> int:
     return _CU_COUNT[dev.index]
 
 
+def sorted_launch_rows_per_chunk(rows, ng, dev):
+    """Chunk height for matrices of `ng` groups sharing one launch (q, k and
+    v): launches of fewer than 2^20 codes (stage 1) take about 0.75 x CUs
+    chunks over their total rows, at most 64 rows each, one workgroup per
+    chunk (the library's rule for one small matrix, applied to the launch);
+    None for larger launches (each matrix its own default)."""
+    total = sum(int(r) for r in rows)
+    if total * int(ng) >= 1 << 20:
+        return None
+    cu = _cu_count(dev)
+    gb = max(0, (int(ng) - 1).bit_length())
+    rmax = min((1 << (16 - gb)) - 1, 255) if gb <= 15 else 0  # 16-bit positions
+    r = -(-4 * total // (3 * cu))
+    return max(1, min(r, 64, rmax))
+
+
 def sorted_slices(planes, dev) -> int:
     """Workgroups per chunk: as many as keep the launch within one workgroup
     per CU (the per-CU gather rate bounds this kernel, so a CU holding two

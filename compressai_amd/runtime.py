@@ -36,15 +36,19 @@ SMALL_M_MAX = 64
 
 # matrices with at least this many codes (all stages) use the code-sorted
 # layout at batch 1.  Measured on MI355X: gate + up (2 x 6144 x 2048, 4 bpw)
-# 20.0 us against 29.4 us, down (2048 x 6144, 4 bpw) 18.8 against 19.8, the
-# 151936 x 2048 LM head 70 against 171; the 2048 x 2048 q / o projections
-# (0.5 M codes) are faster on the gather kernel (14 against 8 us).
-SORTED_MIN_CODES = 1 << 21
+# 15.0 us against 29.6 us, down (2048 x 6144, 4 bpw) 12.3 against 20.1, the
+# 151936 x 2048 LM head 55 against 171; the 2048 x 2048 o projection
+# (0.5 M codes) 7.3 against 8.5 us, with the small-matrix chunking (about
+# 0.75 x CUs chunks of 11 rows, one workgroup each; 9.0 us at 9 chunks of
+# 228 rows x 8 slices).
+SORTED_MIN_CODES = 1 << 19
 # a launch of several projections of one activation (PackedProjections) uses
-# the code-sorted layout at batch 1 from this many codes on.  Measured on
-# MI355X: q, k and v of the 2048-wide attention (0.79 M codes) 9.3 us
-# against 11.4 us on the gather kernel; o alone (0.52 M codes) 8.9 against 7.9.
-SORTED_MIN_LAUNCH_CODES = 640 * 1024
+# the code-sorted layout at batch 1 from this many codes on, its members
+# repacked to one chunk height over the launch's rows (about 0.75 x CUs
+# chunks).  Measured on MI355X: q, k and v of the 2048-wide attention
+# (0.79 M codes, chunks of 16 rows) 7.7-7.9 us against 11.4 us on the gather
+# kernel; o alone (0.52 M codes, above) 7.3 against 8.5.
+SORTED_MIN_LAUNCH_CODES = SORTED_MIN_CODES
 # Batch 2-4 on the sorted layout (vq_sorted_gemm_batch: one centroid gather
 # for every activation row, the activation rotated by its own launch first)
 # where it was measured faster (HIP graphs, MI355X, us per call):
@@ -55,14 +59,18 @@ SORTED_MIN_LAUNCH_CODES = 640 * 1024
 #    28.9 on the gather kernel with the 6144-point RHT in its prologue);
 #  * PackedProjections at batch 3-4 (q, k, v in one launch: 22.0-24.4 against
 #    35.9-36.1 for the three projections on the matrix cores; gate + up:
-#    40.1-42.0 against 47.0-47.4), and at batch 2 with SORTED_MIN_CODES codes
-#    or more (gate + up: 24.6 against 37.6 in one gather-kernel launch).
+#    40.1-42.0 against 47.0-47.4), and at batch 2 with
+#    SORTED_BATCH2_LAUNCH_MIN_CODES codes or more (gate + up: 24.6 against
+#    37.6 in one gather-kernel launch).
 # Not used where it was slower: one 6144 x 2048 4 bpw matrix at batch 2
 # (23.2 against 20.9) and 3-4 (32-35 against 24 on the matrix cores), the
 # down matrix at batch 3-4 (35-39 against 25), q / k / v at batch 2 (17.6
 # against 12.9; 0.79 M codes).
 SORTED_BATCH = True
 SORTED_BATCH_MIN_CODES = 8 << 20
+# PackedProjections at batch 2 on the sorted layout from this many codes on
+# (gate + up, 6.3 M codes: faster; q, k, v, 0.79 M codes: slower)
+SORTED_BATCH2_LAUNCH_MIN_CODES = 2 << 20
 # the sorted kernel builds the RHT in LDS up to this width, else x is rotated first
 SORTED_FUSED_RHT_MAX_N = 8192
 
@@ -173,7 +181,8 @@ class PackedProjections(nn.Module):
     there): with the sorted layout (the matrices hold
     ``SORTED_MIN_LAUNCH_CODES`` codes or more together) one sorted launch at
     batch 1 and one sorted batch launch after the RHT at batch 3-4, and at
-    batch 2 with ``SORTED_MIN_CODES`` codes or more (gate + up); else one
+    batch 2 with ``SORTED_BATCH2_LAUNCH_MIN_CODES`` codes or more (gate +
+    up); else one
     gather-kernel launch with the RHT built in for batch <= 2; other batches
     run each projection.  Up to 4 projections."""
 
@@ -196,8 +205,17 @@ class PackedProjections(nn.Module):
             codes >= SORTED_MIN_LAUNCH_CODES and dev.type == "cuda" and a.cfg in ((16,), (16, 8), (16, 16)))
         self.sorted = None
         if use:
-            self.sorted = [m.sorted if m.sorted is not None else
-                           K.SortedPlanes(m.idx0, getattr(m, "idx1", None), m.out, m.n, device=dev) for m in lins]
+            # a launch of fewer than 2^20 codes (q, k, v): one chunk height
+            # over the launch's rows (about 0.75 x CUs chunks); the members
+            # then hold these planes (one sorted copy per matrix)
+            R = K.sorted_launch_rows_per_chunk([m.out for m in lins], a.n // 8, dev) if dev.type == "cuda" else None
+            self.sorted = []
+            for m in lins:
+                sp = m.sorted
+                if sp is None or (R is not None and sp.rows_per_chunk != R):
+                    sp = K.SortedPlanes(m.idx0, getattr(m, "idx1", None), m.out, m.n, device=dev, rows_per_chunk=R)
+                    m.sorted = sp
+                self.sorted.append(sp)
 
     def forward(self, x, out_dtype=None):
         lins = self.lins
@@ -211,7 +229,7 @@ class PackedProjections(nn.Module):
             ys = K.vq_sorted_gemv(xs, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n, perm,
                                   sign, hb, sc, out_dtype=od)
         elif (SORTED_BATCH and self.sorted is not None and 2 <= B <= K.SORTED_BATCH_MAX
-              and (B >= 3 or self.codes >= SORTED_MIN_CODES)
+              and (B >= 3 or self.codes >= SORTED_BATCH2_LAUNCH_MIN_CODES)
               and cb0.dtype in (torch.float16, torch.bfloat16) and K.sorted_batch_fits(self.sorted, B)):
             xr = a.rot.fwd(x2, out_dtype=torch.float32)
             ys = K.vq_sorted_gemm_batch(xr, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n,

@@ -331,7 +331,8 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  *   min(2^(16 - ceil(log2 ng)) - 1, 255) rows, over a multiple of
  *   chunk_align chunks when the chunks keep >= 128 rows, e.g. chunk_align =
  *   the CU count; with chunk_align > 1 a matrix of fewer than 2^20 codes
- *   takes chunks of at most 64 rows; a matrix tall enough that a multiple of 2 x chunk_align
+ *   takes ceil(4 out_rows / (3 chunk_align)) rows per chunk (about 0.75 x
+ *   chunk_align chunks), at most 64; a matrix tall enough that a multiple of 2 x chunk_align
  *   chunks of more rows (up to the first limit) covers it takes those, e.g.
  *   a 151,936-row LM head: 512 chunks of 297 rows) of near-equal height:
  *   chunk c holds rows

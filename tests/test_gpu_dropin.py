@@ -265,9 +265,13 @@ def test_packed_projections_qkv(dev, act):
         m = synth.vq_matrix(9391 + k, out, n, bpw=2)
         mats.append(m)
         lins.append(PackedLinear((out, n), (16,), "attn", [m["idx0"]], m["scale"], cbs, dev))
-    assert all(lin.sorted is None for lin in lins)
+    # q (2^19 codes) holds sorted planes of its own, k and v (2^17) do not
+    assert lins[0].sorted is not None and all(lin.sorted is None for lin in lins[1:])
     proj = PackedProjections(lins)
     assert proj.sorted is not None and len(proj.sorted) == 3
+    # one launch of 0.79 M codes: chunks of the launch's height for all three
+    R = K.sorted_launch_rows_per_chunk([2048, 512, 512], n // 8, dev)
+    assert R is not None and all(sp.rows_per_chunk == R for sp in proj.sorted)
     perm, sign = _rot_np(lins[0].rot)
     for B in (1, 2, 3):
         x = synth.activations(9395 + B, (B, n), dtype=act)

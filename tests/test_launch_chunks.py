@@ -1,0 +1,20 @@
+"""Chunk heights of small launches on the code-sorted layout: the launch-level rule that
+PackedProjections applies to q, k and v (about 0.75 x CUs chunks over their total rows, at
+most 64 rows, one workgroup per chunk), checked on the host with a stand-in CU count."""
+import torch
+
+from compressai_amd import kernels as K
+
+
+def test_launch_rows_per_chunk(monkeypatch):
+    monkeypatch.setitem(K._CU_COUNT, 0, 256)
+    dev = torch.device("cuda", 0)
+    assert K.sorted_launch_rows_per_chunk([2048, 512, 512], 256, dev) == 16    # q, k, v: 192 chunks
+    assert K.sorted_launch_rows_per_chunk([2048], 256, dev) == 11              # o: 187 chunks
+    assert K.sorted_launch_rows_per_chunk([6144, 6144], 256, dev) is None      # gate + up: the defaults
+    assert K.sorted_launch_rows_per_chunk([2048], 768, dev) is None            # 1.5 M codes
+    assert K.sorted_launch_rows_per_chunk([100], 256, dev) == 1
+    assert K.sorted_launch_rows_per_chunk([1024], 2048, dev) is None           # 2 M codes
+    assert K.sorted_launch_rows_per_chunk([64], 4096, dev) == 1                # 16-bit positions: 15 rows at most
+    monkeypatch.setitem(K._CU_COUNT, 0, 32)
+    assert K.sorted_launch_rows_per_chunk([2048, 512, 512], 256, dev) == 64    # few CUs: the 64-row cap

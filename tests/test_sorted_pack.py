@@ -179,9 +179,11 @@ def test_sorted_rows_per_chunk_alignment():
     assert L.vq2_sorted_rows_per_chunk(151936, 256, 256) == 297
     assert L.vq2_sorted_rows_per_chunk(151936, 256, 1) == 255     # 596 chunks (no alignment asked)
     assert L.vq2_sorted_rows_per_chunk(100000, 256, 256) == 196   # 512 chunks, 16-bit positions suffice
-    # fewer than 2^20 codes, packed for a launch of its own: chunks of <= 64 rows
-    assert L.vq2_sorted_rows_per_chunk(2048, 256, 256) == 64      # q, o: 32 chunks
-    assert L.vq2_sorted_rows_per_chunk(512, 256, 256) == 64       # k, v: 8 chunks
+    # fewer than 2^20 codes, packed for a launch of its own: about 0.75 x 256
+    # chunks (ceil(4 rows / 768) rows each, at most 64)
+    assert L.vq2_sorted_rows_per_chunk(2048, 256, 256) == 11      # o: 187 chunks
+    assert L.vq2_sorted_rows_per_chunk(512, 256, 256) == 3        # k or v alone: 171 chunks
+    assert L.vq2_sorted_rows_per_chunk(65536, 8, 256) == 64       # 0.5 M codes, capped at 64 rows
     assert L.vq2_sorted_rows_per_chunk(2048, 256, 1) == 228       # no alignment asked (expert pools): 9 chunks
     assert L.vq2_sorted_rows_per_chunk(6144, 256, 256) == 246     # 25 chunks (aligned ones would be too short)
     assert L.vq2_sorted_rows_per_chunk(2048, 768, 1) == 63        # 6144-wide: 63 rows at most (33 chunks)
