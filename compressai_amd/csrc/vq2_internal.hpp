@@ -166,6 +166,9 @@ int64_t sorted_rows_per_chunk(int64_t out_rows, int64_t ng, int64_t chunk_align)
 // iterations = chunks x iterations per chunk (*ks: its chunks).
 struct ChunkSplit;
 int sorted_check_call(const SortedCall& c, bool top1, const char* who, int64_t* rmax);
+// floats of one wave's accumulator arrays for the launch's tallest need:
+// max over its matrices of sorted_parts(R) x (R + 1)
+int64_t sorted_acc_arrays(const SortedCall& c);
 int sorted_check_seg(const SortedCall& c, int s, const char* who, ChunkSplit* ks);
 size_t sorted_batch_workspace_bytes(const SortedCall& c);
 size_t sorted_batch_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk, int64_t batch);

@@ -17,11 +17,13 @@
 //    pack time: the rows split evenly over the chunks; by default at most
 //    min(2^(16 - gbits) - 1, 255), more for very tall matrices), so row R is
 //    a dummy row that padding entries add to;
-//  * every wave keeps two accumulator arrays, one per 32-lane half; a
-//    chunk's codes are sorted by value (then position) and dealt into
-//    instructions of 64 lanes with no row twice in a half (an entry whose row
-//    both open halves already hold waits for the next instruction), so the
-//    lanes' read-add-write of their row's accumulator never collide;
+//  * every wave keeps two accumulator arrays, one per 32-lane half (four,
+//    one per 16 lanes, for chunks of at most 32 rows of a dense matrix,
+//    whose halves would otherwise run partly empty); a chunk's codes are
+//    sorted by value (then position) and dealt into instructions of 64
+//    lanes with no row twice in a lane group (an entry whose row every open
+//    group already holds waits for the next instruction), so the lanes'
+//    read-add-write of their row's accumulator never collide;
 //  * lane 63 of an instruction carries its base code (the smallest), the
 //    other 63 lanes one code each as a 24-bit field (code - base) << P | row
 //    << gbits | group (P = gbits + bitlen(R) <= 17); an instruction whose next
@@ -39,12 +41,12 @@
 //
 // Kernel: one workgroup of 16 waves per (chunk, slice).  The workgroup first
 // builds the rotated activation in LDS (the fused RHT prologue of the GEMV
-// kernel, or a copy of a pre-rotated x), fp32; every wave owns two LDS
-// accumulators per row of the chunk (2 x (R + 1) floats).  A wave takes iterations
-// of its slice round-robin: one 12-byte entry load, four centroid gathers,
-// then per entry the group's 8 activation values from LDS, the 8-term dot
-// product in fp32 and acc[half][row] += dot.  At the end the waves'
-// accumulators are summed in (wave, half) order: with one slice the rows are complete
+// kernel, or a copy of a pre-rotated x), fp32; every wave owns two (or
+// four) LDS accumulators per row of the chunk (parts x (R + 1) floats).  A
+// wave takes iterations of its slice round-robin: one 12-byte entry load,
+// four centroid gathers, then per entry the group's 8 activation values
+// from LDS, the 8-term dot product in fp32 and acc[part][row] += dot.  At
+// the end the waves' accumulators are summed in (wave, part) order: with one slice the rows are complete
 // (y = (acc * s) * rs, or the fused top-1 key per workgroup); with several
 // slices the raw partials go to a workspace and the last workgroup of the
 // chunk to arrive sums them in slice order.  Every order is fixed, so results
@@ -79,11 +81,14 @@ namespace vq2 {
 // slower: gate+up 16.3 -> 17.5 us at 473 rows, down 13.8 -> 16.8 at 228.)
 // With chunk_align > 1 a matrix of fewer than 2^20 codes takes about
 // 0.75 x chunk_align chunks (at most 64 rows each), one workgroup each: its
-// launch is bound by latency, and one slice per chunk saves the slice sum
-// (the o projection: 8.5 us on the gather kernel, 7.3 at 187 chunks of 11
-// rows; 9.0 at 9 chunks of 228 rows x 8 slices; q, k and v in one launch,
-// chunks from their total rows: 7.7 us at 192 chunks of 16 rows, 9.5 at 15
-// of 171-228 x 8 slices).
+// launch is bound by latency, and one slice per chunk saves the slice sum.
+// Measured with 1024 HBM-resident copies, one slice: the o projection
+// 2048 x 2048 at 11 / 16 / 20 / 24 / 32 rows 7.07 / 7.15 / 7.28 / 7.35 /
+// 8.15 us (8.5 on the gather kernel, 9.0 at 9 chunks of 228 rows x 8
+// slices); q, k and v in one launch, chunks from their total rows, at 16 /
+// 24 / 32 rows 7.57 / 7.67 / 8.51 us (9.5 at 15 chunks of 171-228 rows x 8
+// slices); fewer rows put the grid past one workgroup per CU (q, k, v at 12
+// rows, 257 chunks: 10.1 us).
 constexpr int64_t SG_MIN_ALIGNED_R = 128;
 constexpr int64_t SG_SMALL_CODES = int64_t(1) << 20;
 constexpr int64_t SG_SMALL_R = 64;
@@ -127,11 +132,12 @@ static void fill_pad_iters(uint32_t* dst, int64_t iters, uint32_t pad)
 }
 
 // Entries of one (chunk, stage) in lane layout: sorted by code, dealt into
-// 64-lane instructions (lanes 0-31 and 32-62 in two halves with distinct rows
-// each, lane 63 the instruction's base code) whose codes lie within 2^(24 - P)
-// of the base, padded to whole iterations.
+// 64-lane instructions (`parts` groups of 64 / parts lanes with distinct
+// rows each: lanes 0-31 and 32-62, or 0-15, 16-31, 32-47 and 48-62; lane 63
+// the instruction's base code) whose codes lie within 2^(24 - P) of the
+// base, padded to whole iterations.
 static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int64_t ng, int gb, int64_t R,
-                             std::vector<uint32_t>& out)
+                             int parts, std::vector<uint32_t>& out)
 {
     const int pb = sorted_pbits(gb, (int)R);
     const uint32_t span = 1u << (24 - pb);  // code offsets below this
@@ -152,13 +158,15 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
     // while stamp[row] == id)
     std::vector<int64_t> stamp((size_t)R + 1, -1);
     std::vector<uint8_t> used((size_t)R + 1, 0);
-    static_assert(SG_PARTS == 2 && SG_BASE_LANE == 63, "two halves, the base in the last lane");
-    const int cap[SG_PARTS] = {SG_PART_LANES, SG_PART_LANES - 1};
+    static_assert(SG_BASE_LANE == 63 && SG_MAX_PARTS <= 8, "the base in the last lane; one bit per part in used[]");
+    const int pl = 64 / parts;  // lanes per part; the last part's last lane is the base
+    int cap[SG_MAX_PARTS];
+    for (int qd = 0; qd < parts; qd++) cap[qd] = qd + 1 < parts ? pl : pl - 1;
     size_t next = 0;
     int64_t id = 0;
     while (next < keys.size() || !pending.empty()) {
-        uint32_t slot[SG_PARTS][SG_PART_LANES];
-        int fill[SG_PARTS] = {};
+        uint32_t slot[SG_MAX_PARTS][64 / SG_PARTS];
+        int fill[SG_MAX_PARTS] = {};
         int n = 0;
         bool have_base = false;
         uint32_t base = 0;
@@ -170,7 +178,7 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
             if (have_base && code - base >= span) return 2;
             const uint32_t row = kp >> gb;
             const uint8_t u = stamp[row] == id ? used[row] : 0;
-            for (int qd = 0; qd < SG_PARTS; qd++)
+            for (int qd = 0; qd < parts; qd++)
                 if (fill[qd] < cap[qd] && !(u & (1u << qd))) {
                     if (!have_base) {
                         have_base = true;
@@ -184,7 +192,7 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
                 }
             return 1;
         };
-        const int full = cap[0] + cap[1];
+        const int full = 63;
         // entries waiting since an earlier instruction go first (their codes
         // are the smallest left, in ascending order, so the first one placed
         // is the instruction's smallest code)
@@ -204,9 +212,9 @@ static void pack_chunk_stage(const int16_t* plane, int64_t r0, int64_t rows, int
             if (r == 1) pending.push_back(keys[next]);
             next++;
         }
-        for (int qd = 0; qd < SG_PARTS; qd++) {
-            while (fill[qd] < SG_PART_LANES) slot[qd][fill[qd]++] = pad;
-            instr.insert(instr.end(), slot[qd], slot[qd] + SG_PART_LANES);
+        for (int qd = 0; qd < parts; qd++) {
+            while (fill[qd] < pl) slot[qd][fill[qd]++] = pad;
+            instr.insert(instr.end(), slot[qd], slot[qd] + pl);
         }
         instr.back() = base;  // lane 63: the base code
         id++;
@@ -248,8 +256,8 @@ int sorted_pack(const int16_t* idx0, const int16_t* idx1, int64_t out_rows, int6
     auto work = [&](int t) {
         for (int64_t c = t; c < n_chunks; c += nt) {
             const int64_t r0 = c * ks.rb + std::min(c, ks.nbig), rows = ks.rb + (c < ks.nbig ? 1 : 0);
-            pack_chunk_stage(idx0, r0, rows, ng, gb, R, p1[c]);
-            if (idx1) pack_chunk_stage(idx1, r0, rows, ng, gb, R, p2[c]);
+            pack_chunk_stage(idx0, r0, rows, ng, gb, R, sorted_parts(R), p1[c]);
+            if (idx1) pack_chunk_stage(idx1, r0, rows, ng, gb, R, sorted_parts(R), p2[c]);
         }
     };
     if (nt == 1) {
@@ -317,8 +325,8 @@ int sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts,
         for (int64_t u = t; u < units; u += nt) {
             const int64_t e = u / C, c = u - e * C;
             const int64_t r0 = c * ks.rb + std::min(c, ks.nbig), nr = ks.rb + (c < ks.nbig ? 1 : 0);
-            pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, p1[u]);
-            if (idx1) pack_chunk_stage(idx1 + e * rows * ng, r0, nr, ng, gb, R, p2[u]);
+            pack_chunk_stage(idx + e * rows * ng, r0, nr, ng, gb, R, SG_PARTS, p1[u]);
+            if (idx1) pack_chunk_stage(idx1 + e * rows * ng, r0, nr, ng, gb, R, SG_PARTS, p2[u]);
         }
     };
     if (nt == 1) {
@@ -433,7 +441,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     float* s_nat = smem;
     const int xb = TALL ? (int)(n / 2) : SG_XB;
     float* s_x = smem + (XM != 0 ? n : 0);              // split activation
-    float* s_acc = s_x + (TALL ? n : SG_X_SPLIT);       // SG_WAVES x SG_PARTS x (R + 1)
+    float* s_acc = s_x + (TALL ? n : SG_X_SPLIT);       // SG_WAVES x sorted_parts(R) x (R + 1)
     // prologue loads first (they need only the activation fields, and
     // return before the entries and gathers)
     XProLoad first;
@@ -495,8 +503,9 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     pipe.set_fields(c_beg + sg.ipc1, a.gbits, R);
     if constexpr (XM == 0) pipe.gathers();
 
-    float* acc = sorted_acc(s_acc, wave, lane, R);
-    sorted_acc_zero(acc, lane, R);
+    const int parts = sorted_parts(R);
+    float* acc = sorted_acc(s_acc, wave, lane, R, parts);
+    sorted_acc_zero(acc, lane, R, parts);
     if constexpr (XM == 1) {
         void* s_stage = smem + n;  // dead once build_x is done: the split activation takes its place
         stage_x<1, XT>(a.g, s_stage, 1, n, 0, 0, first);
@@ -522,7 +531,7 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     __syncthreads();
 
     __shared__ float s_red[4][256];
-    const float sum = sorted_row_sums<TALL>(s_acc, R, s_red);
+    const float sum = sorted_row_sums<TALL>(s_acc, R, s_red, parts);
     // thread rr < R holds row rr's sum
     const int rr = TALL ? (int)threadIdx.x : (int)(threadIdx.x & 255);
     const bool lead = TALL || threadIdx.x < 256;
@@ -647,6 +656,16 @@ size_t sorted_top1_workspace_bytes(int64_t out_rows, int64_t rows_per_chunk)
     return (size_t)((out_rows + rows_per_chunk - 1) / rows_per_chunk) * sizeof(uint64_t);
 }
 
+int64_t sorted_acc_arrays(const SortedCall& c)
+{
+    int64_t f = 0;
+    for (int s = 0; s < c.nseg; s++) {
+        const int64_t R = c.seg[s].rows_per_chunk;
+        f = std::max<int64_t>(f, sorted_parts(R) * (R + 1));
+    }
+    return f;
+}
+
 int sorted_check_call(const SortedCall& c, bool top1, const char* who, int64_t* rmax)
 {
     if (c.nseg < 1 || c.nseg > SG_MAX_SEG) return set_error(VQ2_ERR_ARG, "%s: 1..%d matrices", who, SG_MAX_SEG);
@@ -694,7 +713,7 @@ int sorted_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     // chunks of 256 rows or more, or 17-bit positions: the TALL kernels
     const bool tall = rmax >= 256 || sorted_pbits(sorted_gbits(c.ng), (int)rmax) > 16;
     const size_t shm =
-        (size_t)((c.xm != 0 ? n : 0) + (tall ? n : SG_X_SPLIT) + SG_WAVES * SG_PARTS * (rmax + 1)) * sizeof(float);
+        (size_t)((c.xm != 0 ? n : 0) + (tall ? n : SG_X_SPLIT) + SG_WAVES * sorted_acc_arrays(c)) * sizeof(float);
     if (n > 2 * SG_XB || shm > SG_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMV: n=%lld too large (at most %d)", (long long)n, 2 * SG_XB);
     if (c.xm == 1) {

@@ -33,6 +33,15 @@ constexpr int SG_BASE_LANE = 63;    // the lane that carries the instructions' b
 constexpr int SG_MAX_R = 511;
 constexpr int SG_PARTS = 2;                   // accumulator arrays per wave
 constexpr int SG_PART_LANES = 64 / SG_PARTS;  // lanes sharing one array
+// Dense matrices packed in chunks of at most SG_QUAD_R rows take four
+// arrays per wave (16 lanes each): a 32-lane half can hold only R distinct
+// rows, so their instructions would run partly empty (2048 x 2048 in
+// 16-row chunks: 41 iterations per chunk with two arrays, 22 with four; 32
+// rows: 51 and 33).  Taller chunks keep two (their halves fill; four would
+// double the accumulators' LDS), and so do expert pools.
+constexpr int SG_QUAD_R = 32;
+constexpr int SG_MAX_PARTS = 4;
+__host__ __device__ constexpr int sorted_parts(int64_t R) { return R <= SG_QUAD_R ? SG_MAX_PARTS : SG_PARTS; }
 constexpr int SG_MAX_SHM = 150 * 1024;        // dynamic LDS: activation (+ stage) + accumulators
 constexpr int SG_MAX_SEG = 4;                 // matrices per launch
 
@@ -621,18 +630,20 @@ struct SortedPipe {
     }
 };
 
-// This lane's accumulator array: 2 per wave, one per 32-lane half.
-__device__ __forceinline__ float* sorted_acc(float* s_acc, int wave, int lane, int R)
+// This lane's accumulator array: `parts` per wave (2 or 4), one per
+// 64 / parts consecutive lanes.
+__device__ __forceinline__ float* sorted_acc(float* s_acc, int wave, int lane, int R, int parts = SG_PARTS)
 {
-    return s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
+    return s_acc + (wave * parts + (lane >> (parts == SG_MAX_PARTS ? 4 : 5))) * (R + 1);
 }
 
-__device__ __forceinline__ void sorted_acc_zero(float* acc, int lane, int R)
+__device__ __forceinline__ void sorted_acc_zero(float* acc, int lane, int R, int parts = SG_PARTS)
 {
-    for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = 0.0f;
+    const int pl = 64 / parts;
+    for (int i = lane & (pl - 1); i <= R; i += pl) acc[i] = 0.0f;
 }
 
-// Row sums of the SG_WAVES x SG_PARTS accumulator arrays (after a barrier):
+// Row sums of the SG_WAVES x parts accumulator arrays (after a barrier):
 // thread (p, r) adds a quarter of the arrays of row r, then the four
 // partials are added in p order (a fixed order: deterministic); chunks of
 // 256 rows or more (TALL instantiations), half of them and then the two
@@ -640,14 +651,14 @@ __device__ __forceinline__ void sorted_acc_zero(float* acc, int lane, int R)
 // threadIdx.x); ends with a barrier-free read, after the barrier between
 // the two halves.
 template <bool TALL = false>
-__device__ __forceinline__ float sorted_row_sums(const float* s_acc, int R, float (*s_red)[256])
+__device__ __forceinline__ float sorted_row_sums(const float* s_acc, int R, float (*s_red)[256], int parts = SG_PARTS)
 {
     if (TALL && R >= 256) {
         float* sr = &s_red[0][0];  // [2][512]
         const int rr = threadIdx.x & 511, pp = threadIdx.x >> 9;
         if (rr < R) {
             float part = 0.0f;
-            constexpr int NA = SG_WAVES * SG_PARTS / 2;
+            const int NA = SG_WAVES * parts / 2;
 #pragma unroll 4
             for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
             sr[pp * 512 + rr] = part;
@@ -658,7 +669,7 @@ __device__ __forceinline__ float sorted_row_sums(const float* s_acc, int R, floa
     const int rr = threadIdx.x & 255, pp = threadIdx.x >> 8;
     if (rr < R) {
         float part = 0.0f;
-        constexpr int NA = SG_WAVES * SG_PARTS / 4;
+        const int NA = SG_WAVES * parts / 4;
 #pragma unroll 4
         for (int w = NA * pp; w < NA * pp + NA; w++) part += s_acc[w * (R + 1) + rr];
         s_red[pp][rr] = part;

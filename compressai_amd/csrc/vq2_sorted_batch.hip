@@ -15,7 +15,8 @@
 // holds the activation as fp16, group-major with the NB (2 or 4) rows of a
 // group side by side (16 * NB bytes per group), and every wave owns two
 // accumulator arrays of NB floats per row of the chunk (one per 32-lane
-// half, as the packing guarantees distinct rows per half).  Per entry a lane
+// half, as the packing guarantees distinct rows per half; four, one per 16
+// lanes, for chunks of at most 32 rows).  Per entry a lane
 // reads its group's NB activation vectors, forms NB 8-term dot products in
 // fp32 (v_dot2_f32_f16 for fp16 codebooks) and adds them to its row with one
 // 8- or 16-byte read-add-write.
@@ -40,7 +41,6 @@ namespace vq2 {
 
 constexpr int SB_THREADS = 512;
 constexpr int SB_WAVES = SB_THREADS / 64;
-constexpr int SB_ARRAYS = SB_WAVES * SG_PARTS;  // accumulator arrays per workgroup
 constexpr int SB_MAX_SHM = 150 * 1024;          // two workgroups per CU up to 80 KiB (chunks of <= 255 rows)
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     _Float16* s_xh = (_Float16*)smem;             // [ng][NB][8]
-    accv* s_acc = (accv*)(smem + a.x_floats);     // SB_ARRAYS x (R + 1)
+    accv* s_acc = (accv*)(smem + a.x_floats);     // SB_WAVES x sorted_parts(R) x (R + 1)
 
     const int pos = (int)blockIdx.x;
     const int slice = pos / a.nc, gchunk = pos - slice * a.nc;
@@ -196,8 +196,9 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     SortedPipe<CBT, 1, SB_WAVES, TALL> pipe;
     pipe.start(sg.ent, a.cb0, a.cb1, c_beg, c_mid, s0, s1, wave, lane, a.gbits, R, a.c1mask);
 
-    accv* acc = s_acc + (wave * SG_PARTS + lane / SG_PART_LANES) * (R + 1);
-    for (int i = lane % SG_PART_LANES; i <= R; i += SG_PART_LANES) acc[i] = (accv)0.0f;
+    const int parts = sorted_parts(R), pl = 64 / parts;
+    accv* acc = s_acc + (wave * parts + (lane >> (parts == SG_MAX_PARTS ? 4 : 5))) * (R + 1);
+    for (int i = lane & (pl - 1); i <= R; i += pl) acc[i] = (accv)0.0f;
 
     // the activation: group-major fp16, rows >= batch zero
     const int64_t groups = a.ng * NB;
@@ -270,7 +271,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     // row sums: thread (pp, rr) adds half the arrays of row rr, then the two
     // halves in order (the activation's LDS is free by now); chunks of 256
     // rows or more: thread rr adds both halves itself (the same order)
-    constexpr int NA = SB_ARRAYS / 2;
+    const int NA = SB_WAVES * parts / 2;
     const bool tall = TALL && R >= 256;
     const int rr = tall ? (int)threadIdx.x : (int)(threadIdx.x & 255), pp = tall ? 0 : (int)(threadIdx.x >> 8);
     accv tsum = (accv)0.0f;
@@ -437,7 +438,7 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     const bool tall = rmax >= 256 || sorted_pbits(sorted_gbits(c.ng), (int)rmax) > 16;
     // activation (fp16, nb rows) or the row-sum stage, whichever is larger, then the accumulators
     const int64_t x_floats = std::max<int64_t>(n * nb / 2, 2 * 256 * nb);
-    const size_t shm = (size_t)(x_floats + (int64_t)SB_ARRAYS * (rmax + 1) * nb) * sizeof(float);
+    const size_t shm = (size_t)(x_floats + (int64_t)SB_WAVES * sorted_acc_arrays(c) * nb) * sizeof(float);
     if (shm > SB_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: n=%lld with %lld-row chunks needs %zu bytes of LDS "
                          "(at most %d)", (long long)n, (long long)rmax, shm, SB_MAX_SHM);

@@ -591,10 +591,14 @@ def sorted_slices(planes, dev) -> int:
     50 chunks x 5 slices 20.0 us, x 6 slices 31 us), and few enough that
     each of a workgroup's 16 waves has at least one iteration (measured on
     q, k, v of 2048-wide attention, 15 chunks of 171-228 iterations: 17
-    slices 10.6 us, 6-12 slices 9.3 us)."""
+    slices 10.6 us, 6-12 slices 9.3 us).  One slice where fewer than three
+    fit: the slice sum costs more than the shorter chunk saves (the o
+    projection 2048 x 2048: 128 chunks of 16 rows 6.97 us at one slice, 8.1
+    at two; 86 chunks of 24 rows 7.28 against 8.06)."""
     chunks = sum(p.n_chunks for p in planes)
     per_wave = min(p.iters_per_chunk for p in planes) // 20
-    return max(1, min(32, _cu_count(dev) // chunks, per_wave))
+    fit = _cu_count(dev) // chunks
+    return max(1, min(32, fit, per_wave)) if fit >= 3 else 1
 
 
 def _sorted_cbs(planes, cb0, cb1):
@@ -702,8 +706,9 @@ def sorted_batch_fits(planes, batch) -> bool:
     default 62-row chunks."""
     nb = 2 if batch <= 2 else 4
     n = planes[0].n
-    R = max(p.rows_per_chunk for p in planes)
-    return (max(n * nb // 2, 512 * nb) + 16 * (R + 1) * nb) * 4 <= 150 * 1024
+    # 8 waves x 2 accumulator arrays per row (4 for chunks of at most 32 rows)
+    acc = max((32 if p.rows_per_chunk <= 32 else 16) * (p.rows_per_chunk + 1) for p in planes)
+    return (max(n * nb // 2, 512 * nb) + acc * nb) * 4 <= 150 * 1024
 
 
 def _batch_x(x, n):

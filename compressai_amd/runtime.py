@@ -38,7 +38,7 @@ SMALL_M_MAX = 64
 # layout at batch 1.  Measured on MI355X: gate + up (2 x 6144 x 2048, 4 bpw)
 # 15.0 us against 29.6 us, down (2048 x 6144, 4 bpw) 12.3 against 20.1, the
 # 151936 x 2048 LM head 55 against 171; the 2048 x 2048 o projection
-# (0.5 M codes) 7.3 against 8.5 us, with the small-matrix chunking (about
+# (0.5 M codes) 7.1 against 8.5 us, with the small-matrix chunking (about
 # 0.75 x CUs chunks of 11 rows, one workgroup each; 9.0 us at 9 chunks of
 # 228 rows x 8 slices).
 SORTED_MIN_CODES = 1 << 19
@@ -46,8 +46,8 @@ SORTED_MIN_CODES = 1 << 19
 # the code-sorted layout at batch 1 from this many codes on, its members
 # repacked to one chunk height over the launch's rows (about 0.75 x CUs
 # chunks).  Measured on MI355X: q, k and v of the 2048-wide attention
-# (0.79 M codes, chunks of 16 rows) 7.7-7.9 us against 11.4 us on the gather
-# kernel; o alone (0.52 M codes, above) 7.3 against 8.5.
+# (0.79 M codes, 192 chunks of 16 rows) 7.6 us against 11.4 us on the gather
+# kernel; o alone (0.52 M codes, above) 7.1 against 8.5.
 SORTED_MIN_LAUNCH_CODES = SORTED_MIN_CODES
 # Batch 2-4 on the sorted layout (vq_sorted_gemm_batch: one centroid gather
 # for every activation row, the activation rotated by its own launch first)

@@ -339,7 +339,9 @@ int vq2_gemv_argmax(const void* x, int x_dt, int64_t batch, int64_t x_stride,
  *   [c * rb + min(c, nbig), + rb + (c < nbig)), rb = out_rows / n_chunks,
  *   nbig = out_rows % n_chunks; a chunk's codes are sorted by value and
  *   dealt into 64-lane instructions in which no row repeats within a
- *   32-lane half (lanes 0-31, 32-62); lane 63 carries the instruction's
+ *   32-lane half (lanes 0-31, 32-62), or within a 16-lane quarter (lanes
+ *   0-15, 16-31, 32-47, 48-62) for chunks of at most 32 rows (expert pools,
+ *   vq2_sorted_pack_pool: halves at any height); lane 63 carries the instruction's
  *   base code (its smallest), every other lane one code as the 24-bit field
  *   (code - base) << P | row_in_chunk << ceil(log2 ng) | group, P =
  *   ceil(log2 ng) + bitlen(rows_per_chunk) <= 17 (an instruction is closed
@@ -460,7 +462,8 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
  * plane as int16 -- a (16,8) uint8 plane widened to values 0..255 -- or
  * NULL) expert by expert, each as vq2_sorted_pack packs a matrix with the
  * same rows_per_chunk R (at most min(2^(16 - ceil(log2 ng)) - 1, 255): pools
- * keep 16-bit positions), and pads every chunk's stage-1 and stage-2 entries
+ * keep 16-bit positions; and 32-lane halves at every R, where
+ * vq2_sorted_pack takes quarters for R <= 32), and pads every chunk's stage-1 and stage-2 entries
  * (dummy-row entries) to the pool's largest counts, so chunk c of expert e
  * holds iterations [(e * C + c) * ipc, (e * C + c + 1) * ipc), C =
  * ceil(rows / R), its stage-2 ones from *stage1_iters on.  *n_iters =

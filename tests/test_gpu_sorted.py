@@ -98,6 +98,41 @@ def test_sorted_taller_chunks_vs_oracle(dev, rows, n, bpw, R, slices):
         assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
 
 
+@pytest.mark.parametrize("bpw", [2, 4])
+def test_sorted_mixed_lane_groups_in_one_launch(dev, bpw):
+    """One launch over matrices whose chunks take four 16-lane accumulator
+    groups (11 and 32 rows), two 32-lane groups (40 rows) and the
+    taller-chunk path (300 rows): the batch-1 kernel with the RHT prologue at
+    one slice and three, and the batch kernel at B = 4, against the oracle."""
+    from act_rounding import fp16_row_scaled
+
+    n = 2048
+    shapes = ((500, 11), (300, 32), (260, 40), (700, 300))
+    ms = [synth.vq_matrix(9580 + k, rows, n, bpw=bpw) for k, (rows, _) in enumerate(shapes)]
+    cb0 = synth.codebook(9585)
+    cb1 = synth.codebook(9586) if bpw == 4 else None
+    sps = [K.SortedPlanes(m["idx0"], m["idx1"], rows, n, device=dev, rows_per_chunk=R)
+           for m, (rows, R) in zip(ms, shapes)]
+    assert [sp.rows_per_chunk for sp in sps] == [R for _, R in shapes]
+    c0, c1 = cb0.to(dev), None if cb1 is None else cb1.to(dev)
+    mats = [(sp, m["scale"].to(dev)) for sp, m in zip(sps, ms)]
+    x = synth.activations(9587, n, dtype=torch.float16)
+    perm, sign = synth.permutation(9588, n), synth.signs(9589, n)
+    xr = O.rht(x, perm, sign, 2048).astype(np.float32)
+    for slices in (1, 3):
+        ys = K.vq_sorted_gemv(x.to(dev), mats, c0, c1, n, perm.to(dev), sign.to(dev), 2048, slices=slices)
+        for k, m in enumerate(ms):
+            _, y64 = O.vq_gemv(xr, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+            assert O.max_rel_err(ys[k].cpu().numpy(), y64[0]) < TOL, (slices, k)
+    xb = synth.activations(9590, (4, n), dtype=torch.float32) * 0.5
+    ybs = K.vq_sorted_gemm_batch(xb.to(dev), mats, c0, c1, n)
+    xk = fp16_row_scaled(xb.numpy())
+    for k, m in enumerate(ms):
+        _, yb64 = O.vq_gemv(xk, m["idx0"], m["idx1"], cb0, cb1, m["scale"])
+        for b in range(4):
+            assert O.max_rel_err(ybs[k].cpu().numpy()[b], yb64[b]) < 1e-5, (k, b)
+
+
 def test_sorted_gemv_bf16_codebook_and_outputs(dev):
     rows, n = 1536, 2048
     m, cb0, cb1, sp = _mk(9520, rows, n, 4, dev, cb_dtype=torch.bfloat16)

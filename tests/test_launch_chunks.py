@@ -1,6 +1,7 @@
 """Chunk heights of small launches on the code-sorted layout: the launch-level rule that
 PackedProjections applies to q, k and v (about 0.75 x CUs chunks over their total rows, at
-most 64 rows, one workgroup per chunk), checked on the host with a stand-in CU count."""
+most 64 rows, one workgroup per chunk), and the slice rule of batch-1 launches, checked on the
+host with a stand-in CU count."""
 import torch
 
 from compressai_amd import kernels as K
@@ -18,3 +19,19 @@ def test_launch_rows_per_chunk(monkeypatch):
     assert K.sorted_launch_rows_per_chunk([64], 4096, dev) == 1                # 16-bit positions: 15 rows at most
     monkeypatch.setitem(K._CU_COUNT, 0, 32)
     assert K.sorted_launch_rows_per_chunk([2048, 512, 512], 256, dev) == 64    # few CUs: the 64-row cap
+
+
+def test_sorted_slices_rule(monkeypatch):
+    """Workgroups per chunk of a batch-1 sorted launch: one where fewer than three fit on the
+    CUs (the small launches above), else as many as fit, each wave keeping an iteration."""
+    from types import SimpleNamespace as P
+
+    monkeypatch.setitem(K._CU_COUNT, 0, 256)
+    dev = torch.device("cuda", 0)
+    assert K.sorted_slices([P(n_chunks=187, iters_per_chunk=19)], dev) == 1       # o: 11-row chunks
+    assert K.sorted_slices([P(n_chunks=128, iters_per_chunk=41)], dev) == 1       # 2 would fit
+    assert K.sorted_slices([P(n_chunks=86, iters_per_chunk=42)], dev) == 1
+    assert K.sorted_slices([P(n_chunks=25, iters_per_chunk=494)] * 2, dev) == 5   # gate + up
+    assert K.sorted_slices([P(n_chunks=33, iters_per_chunk=200)], dev) == 7       # down
+    assert K.sorted_slices([P(n_chunks=32, iters_per_chunk=50)], dev) == 2        # few iterations per wave
+    assert K.sorted_slices([P(n_chunks=512, iters_per_chunk=300)], dev) == 1      # LM head

@@ -1,8 +1,9 @@
 """The code-sorted repack (vq2_sorted_pack, host code of libvq2_amd.so) on the
 CPU: every code of the planes appears exactly once in its chunk, with its row
-and group; no row repeats inside a 32-lane half of an instruction (each
-half read-add-writes its own accumulator array, so the kernel relies on
-it); lane 63 carries the instruction's smallest code and every offset fits
+and group; no row repeats inside a 32-lane half of an instruction, or a
+16-lane quarter for chunks of at most 32 rows (each lane group
+read-add-writes its own accumulator array, so the kernel relies on it);
+lane 63 carries the instruction's smallest code and every offset fits
 its field; padding is the dummy row at offset 0; and the instructions are
 sorted enough that a wave's 64 gathers touch few codebook lines.
 
@@ -75,7 +76,10 @@ def _decode(sp: SortedPlanes):
                                           (7, 16, 3, None),
                                           # taller chunks, 17-bit positions (bit 16 in the high byte)
                                           (700, 2048, 2, 350), (600, 2048, 4, 300), (300, 6144, 4, 120),
-                                          (520, 512, 3, 511), (300, 2048, 3, 300)])
+                                          (520, 512, 3, 511), (300, 2048, 3, 300),
+                                          # short chunks: four 16-lane groups per instruction
+                                          (300, 2048, 2, 16), (200, 2048, 4, 31), (97, 800, 3, 32),
+                                          (64, 1024, 2, 5)])
 def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw, R):
     ng = n // 8
     m = synth.vq_matrix(9800 + rows + bpw, rows, n, bpw=bpw)
@@ -85,7 +89,7 @@ def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw, R):
         R = int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1))
         assert (R + 1) * (1 << gb) <= 1 << 16 and _pb(ng, R) <= 16 and R <= 255
     else:
-        assert _pb(ng, R) == 17 or R == 511
+        assert _pb(ng, R) == 17 or R == 511 or R <= 32
     assert sp.rows_per_chunk == R and sp.n_chunks == -(-rows // R)
     if sp.rows_per_chunk == int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1)):
         assert R * sp.n_chunks - rows < sp.n_chunks  # the default: the rows split evenly over the chunks
@@ -125,7 +129,11 @@ def test_sorted_pack_is_a_permutation_with_distinct_rows(rows, n, bpw, R):
                 rl = ps != dummy
                 if rl.any():
                     assert base == cd[rl].min()           # the base is the instruction's smallest code
-                for lo, hi in ((0, 32), (32, 63)):        # no row twice in a 32-lane half (lane 63: the base)
+                # no row twice in a lane group (lane 63: the base): 32-lane
+                # halves, or 16-lane quarters for chunks of at most 32 rows
+                pl = 16 if R <= 32 else 32
+                for lo in range(0, 64, pl):
+                    hi = min(lo + pl, 63)
                     rr = ps[lo:hi][ps[lo:hi] != dummy] >> gb
                     assert len(np.unique(rr)) == len(rr)
 
@@ -193,9 +201,10 @@ def test_sorted_rows_per_chunk_alignment():
 @pytest.mark.parametrize("E,rows,n", [(3, 1024, 2048), (5, 2048, 512), (2, 100, 800)])
 def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
     """vq2_sorted_pack_pool lays the experts out one after another, each
-    chunk exactly as vq2_sorted_pack packs it alone, then padded with
-    dummy-row iterations (offset 0, base code 0) to the pool's common
-    iteration count."""
+    chunk exactly as vq2_sorted_pack packs it alone (chunks of more than 32
+    rows, where both deal into 32-lane halves), then padded with dummy-row
+    iterations (offset 0, base code 0) to the pool's common iteration
+    count."""
     from compressai_amd.kernels import SortedPool
 
     ng = n // 8
