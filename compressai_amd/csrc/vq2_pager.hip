@@ -42,13 +42,14 @@ struct PagerArgs {
 
 __global__ void __launch_bounds__(PG_THREADS) pager_kernel(const PagerArgs a)
 {
-    extern __shared__ int lds[];
+    extern __shared__ __align__(16) int lds[];
     const int E = a.n_experts, C = a.capacity, NP = a.n_pairs;
-    int* s_slot = lds;             // [E]
+    const int C4 = (C + 3) & ~3;
+    int* s_stamp = lds;            // [C4] (16-byte aligned; entries C.. hold the clock)
+    int* s_slot = s_stamp + C4;    // [E]
     int* s_first = s_slot + E;     // [E]: lowest pair index of a missing expert
     int* s_exp = s_first + E;      // [C]
-    int* s_stamp = s_exp + C;      // [C]
-    int* s_pe = s_stamp + C;       // [NP]: the pair's expert, -1 if invalid
+    int* s_pe = s_exp + C;         // [NP]: the pair's expert, -1 if invalid
     int* s_miss = s_pe + NP;       // [NP]: distinct missing experts in pair order
     int* s_vict = s_miss + NP;     // [NP]: victim slot of miss r
     __shared__ int s_nmiss, s_nelig, s_err, s_hits;
@@ -58,9 +59,9 @@ __global__ void __launch_bounds__(PG_THREADS) pager_kernel(const PagerArgs a)
         s_slot[i] = a.slot_of[i];
         s_first[i] = 0x7FFFFFFF;
     }
-    for (int i = tid; i < C; i += PG_THREADS) {
-        s_exp[i] = a.expert_of[i];
-        s_stamp[i] = a.stamp[i];
+    for (int i = tid; i < C4; i += PG_THREADS) {
+        if (i < C) s_exp[i] = a.expert_of[i];
+        s_stamp[i] = i < C ? a.stamp[i] : clock;  // padding: "used this step", never a victim
     }
     int err = 0;
     for (int i = tid; i < NP; i += PG_THREADS) {
@@ -106,19 +107,27 @@ __global__ void __launch_bounds__(PG_THREADS) pager_kernel(const PagerArgs a)
     __syncthreads();
     const int nmiss = s_nmiss;
     // victims: slots not used by this step, oldest stamp first (ties: lower
-    // slot); the slot of rank r serves miss r
-    for (int s = tid; s < C; s += PG_THREADS) {
-        const int st = s_stamp[s];
-        if (st == clock) continue;
-        int rank = 0;
-        for (int o = 0; o < C; o++) {
-            const int so = s_stamp[o];
-            rank += (so != clock && (so < st || (so == st && o < s))) ? 1 : 0;
+    // slot); the slot of rank r serves miss r.  A step with no misses skips
+    // the ranking (uniform: nmiss is in LDS); the stamps are read four at a
+    // time (all threads read the same words: LDS broadcasts)
+    if (nmiss > 0) {
+        for (int s = tid; s < C; s += PG_THREADS) {
+            const int st = s_stamp[s];
+            if (st == clock) continue;
+            int rank = 0;
+#pragma unroll 4
+            for (int o = 0; o < C4; o += 4) {
+                const int4 so = *(const int4*)(s_stamp + o);
+                rank += (so.x != clock && (so.x < st || (so.x == st && o < s))) ? 1 : 0;
+                rank += (so.y != clock && (so.y < st || (so.y == st && o + 1 < s))) ? 1 : 0;
+                rank += (so.z != clock && (so.z < st || (so.z == st && o + 2 < s))) ? 1 : 0;
+                rank += (so.w != clock && (so.w < st || (so.w == st && o + 3 < s))) ? 1 : 0;
+            }
+            if (rank < nmiss) s_vict[rank] = s;
+            atomicAdd(&s_nelig, 1);
         }
-        if (rank < nmiss) s_vict[rank] = s;
-        atomicAdd(&s_nelig, 1);
+        __syncthreads();
     }
-    __syncthreads();
     const int served = min(nmiss, s_nelig);
     if (tid == 0 && served < nmiss) atomicOr(&s_err, 2);
     for (int r = tid; r < served; r += PG_THREADS) {
@@ -153,7 +162,8 @@ __global__ void __launch_bounds__(PG_THREADS) pager_kernel(const PagerArgs a)
     }
 }
 
-constexpr int PG_CHUNK = 8192;  // bytes of a record per copy workgroup
+constexpr int PG_CHUNK = 8192;  // bytes of a record per work item
+constexpr int PG_COPY_WGS = 512;  // copy workgroups at most (each loops over work items)
 
 struct PagerCopyArgs {
     const uint8_t* mirror;  // device address of the pinned host mirror [n_experts][record_bytes]
@@ -166,33 +176,41 @@ struct PagerCopyArgs {
     int64_t dst_stride[4];  // bytes between slots
     int chunk0[5];          // first chunk of each segment (chunk0[4] = total)
     int scale_dt;
+    int max_copies;         // entries of copy_list
 };
 
+// Work item i = (copy r, chunk c) = (i / chunks, i % chunks) of the
+// state[1] copies this step; workgroup b takes items b, b + grid, ...  (a
+// fixed grid of at most PG_COPY_WGS: a step with nothing to copy dispatches
+// that many workgroups, not one per (copy slot, chunk) -- 1,192 for the
+// sorted records of the 35B expert shape)
 __global__ void __launch_bounds__(256) pager_copy_kernel(const PagerCopyArgs a)
 {
-    const int r = blockIdx.x;
-    if (r >= a.state[1]) return;  // uniform: nothing to copy for this entry
-    const int e = a.copy_list[2 * r], v = a.copy_list[2 * r + 1];
-    const int c = blockIdx.y;
-    int s = 0;
+    const int chunks = a.chunk0[4];
+    const int items = min(max(a.state[1], 0), a.max_copies) * chunks;  // uniform
+    for (int i = blockIdx.x; i < items; i += gridDim.x) {
+        const int r = i / chunks, c = i - r * chunks;
+        const int e = a.copy_list[2 * r], v = a.copy_list[2 * r + 1];
+        int s = 0;
 #pragma unroll
-    for (int k = 1; k < 4; k++) s += c >= a.chunk0[k] ? 1 : 0;
-    const int64_t b0 = (int64_t)(c - a.chunk0[s]) * PG_CHUNK;
-    const int64_t b1 = min(b0 + PG_CHUNK, a.seg_bytes[s]);
-    const uint8_t* src = a.mirror + (int64_t)e * a.record_bytes + a.seg_off[s];
-    uint8_t* dst = (uint8_t*)a.dst[s] + (int64_t)v * a.dst_stride[s];
-    if (s == 0 || s == 2) {
-        for (int64_t b = b0 + (int64_t)threadIdx.x * 16; b < b1; b += 256 * 16)
-            *(u32x4*)(dst + b) = *(const u32x4*)(src + b);
-    } else {
-        // 8 fp16 scales per thread and pass -> the pool's dtype
-        for (int64_t b = b0 + (int64_t)threadIdx.x * 16; b < b1; b += 256 * 16) {
-            const u32x4 w = *(const u32x4*)(src + b);
-            const int64_t i0 = b / 2;
+        for (int k = 1; k < 4; k++) s += c >= a.chunk0[k] ? 1 : 0;
+        const int64_t b0 = (int64_t)(c - a.chunk0[s]) * PG_CHUNK;
+        const int64_t b1 = min(b0 + PG_CHUNK, a.seg_bytes[s]);
+        const uint8_t* src = a.mirror + (int64_t)e * a.record_bytes + a.seg_off[s];
+        uint8_t* dst = (uint8_t*)a.dst[s] + (int64_t)v * a.dst_stride[s];
+        if (s == 0 || s == 2) {
+            for (int64_t b = b0 + (int64_t)threadIdx.x * 16; b < b1; b += 256 * 16)
+                *(u32x4*)(dst + b) = *(const u32x4*)(src + b);
+        } else {
+            // 8 fp16 scales per thread and pass -> the pool's dtype
+            for (int64_t b = b0 + (int64_t)threadIdx.x * 16; b < b1; b += 256 * 16) {
+                const u32x4 w = *(const u32x4*)(src + b);
+                const int64_t i0 = b / 2;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint16_t h = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
-                store_from_f32(dst, a.scale_dt, i0 + k, f16_bits_to_f32(h));
+                for (int k = 0; k < 8; k++) {
+                    const uint16_t h = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+                    store_from_f32(dst, a.scale_dt, i0 + k, f16_bits_to_f32(h));
+                }
             }
         }
     }
@@ -200,7 +218,7 @@ __global__ void __launch_bounds__(256) pager_copy_kernel(const PagerCopyArgs a)
 
 size_t pager_lds_bytes(int64_t n_experts, int64_t capacity, int64_t n_pairs)
 {
-    return (size_t)(2 * n_experts + 2 * capacity + 3 * n_pairs) * sizeof(int);
+    return (size_t)(2 * n_experts + ((capacity + 3) & ~int64_t(3)) + capacity + 3 * n_pairs) * sizeof(int);
 }
 
 int pager_step_launch(const void* ids, int ids_i64, int64_t n_pairs, int64_t n_experts, int64_t capacity,
@@ -235,6 +253,7 @@ int pager_copy_launch(const void* mirror_host, int64_t record_bytes, const int64
     a.copy_list = copy_list;
     a.state = state;
     a.scale_dt = scale_dt;
+    a.max_copies = (int)std::min<int64_t>(max_copies, 65535);
     int64_t off = 0, chunks = 0;
     for (int s = 0; s < 4; s++) {
         if (seg_bytes[s] < 16 || seg_bytes[s] % 16 || !dst[s] || (uintptr_t)dst[s] % 16 ||
@@ -251,10 +270,10 @@ int pager_copy_launch(const void* mirror_host, int64_t record_bytes, const int64
     }
     a.chunk0[4] = (int)chunks;
     if (off != record_bytes) return set_error(VQ2_ERR_ARG, "vq2_pager_copy: segments do not add up to the record");
-    if (max_copies < 1 || max_copies > 65535 || chunks > 65535)
+    if (max_copies < 1 || max_copies > 65535 || chunks > 65535 || max_copies * chunks > 0x7FFFFFFF)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2_pager_copy: grid too large");
-    hipLaunchKernelGGL(pager_copy_kernel, dim3((unsigned)max_copies, (unsigned)chunks), dim3(256), 0,
-                       (hipStream_t)stream, a);
+    const unsigned grid = (unsigned)std::min<int64_t>(max_copies * chunks, PG_COPY_WGS);
+    hipLaunchKernelGGL(pager_copy_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
     err = hipGetLastError();
     return err == hipSuccess ? VQ2_OK : set_hip_error(err, "vq2_pager_copy launch");
 }
