@@ -405,6 +405,9 @@ static hipError_t launch_batch_nb(int cb_dt, int x_dt, bool tall, const SortedBa
 
 static int batch_slots(int64_t batch) { return batch <= 2 ? 2 : 4; }
 
+// LDS of a workgroup that still lets two share a CU (160 KiB per CU)
+constexpr size_t SB_PAIR_SHM = 80 * 1024;
+
 // Workspace with several slices: VQ2_SORTED_WS_HEADER bytes of arrival
 // counters (zero between launches), then per matrix [slices][slots][rows]
 // row sums.
@@ -439,6 +442,23 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     // activation (fp16, nb rows) or the row-sum stage, whichever is larger, then the accumulators
     const int64_t x_floats = std::max<int64_t>(n * nb / 2, 2 * 256 * nb);
     const size_t shm = (size_t)(x_floats + (int64_t)SB_WAVES * sorted_acc_arrays(c) * nb) * sizeof(float);
+    if (nb == 4 && shm > SB_PAIR_SHM) {
+        // 4-row workgroups this large run one per CU (8 waves): rows 0-1,
+        // then the rest, as launches of 2-row workgroups, several per CU
+        // (the LM head 151936 x 2048 in 297-row chunks: top-1 at batch 4
+        // 148.9 -> 129.8 us, logits 145.3 -> 124.2, batch 3 147.7 -> 129.6;
+        // gate + up, 79.6 KiB at batch 4, stays one launch: 37.2 against
+        // 38.4 split).  Stream order lets the second call reuse the
+        // workspace (top-1 keys, slice counters back at zero).
+        SortedCall lo = c, hi = c;
+        lo.batch = 2;
+        hi.batch = c.batch - 2;
+        hi.x = (const char*)c.x + 2 * c.x_stride * dt_size(c.x_dt);
+        for (int s = 0; s < c.nseg; s++)
+            hi.seg[s].y = c.seg[s].y ? (char*)c.seg[s].y + 2 * c.seg[s].out_rows * dt_size(c.y_dt) : nullptr;
+        if (int r = sorted_batch_launch(lo, top1_idx, top1_val)) return r;
+        return sorted_batch_launch(hi, top1 ? top1_idx + 2 : nullptr, top1 ? top1_val + 2 : nullptr);
+    }
     if (shm > SB_MAX_SHM)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: n=%lld with %lld-row chunks needs %zu bytes of LDS "
                          "(at most %d)", (long long)n, (long long)rmax, shm, SB_MAX_SHM);

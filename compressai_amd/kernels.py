@@ -703,12 +703,15 @@ def sorted_batch_fits(planes, batch) -> bool:
     """Whether the batch kernel's LDS (fp16 activation of 2 or 4 rows, and
     the accumulators of the tallest chunk) fits its 150 KiB (two workgroups
     per CU up to 80 KiB): n = 2048 with any chunk height, n = 6144 with the
-    default 62-row chunks."""
-    nb = 2 if batch <= 2 else 4
+    default 62-row chunks.  Batch 3-4 whose 4-row workgroups would exceed
+    80 KiB runs as launches of at most 2 rows, so those must fit."""
     n = planes[0].n
     # 8 waves x 2 accumulator arrays per row (4 for chunks of at most 32 rows)
     acc = max((32 if p.rows_per_chunk <= 32 else 16) * (p.rows_per_chunk + 1) for p in planes)
-    return (max(n * nb // 2, 512 * nb) + acc * nb) * 4 <= 150 * 1024
+    shm = lambda nb: (max(n * nb // 2, 512 * nb) + acc * nb) * 4
+    if batch > 2 and shm(4) <= 80 * 1024:
+        return True
+    return shm(2) <= 150 * 1024
 
 
 def _batch_x(x, n):

@@ -432,11 +432,16 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
  * in fp32.  `slices` workgroups share each chunk; with more than one,
  * `workspace` (vq2_sorted_gemm_batch_workspace bytes, header zero as for
  * vq2_sorted_gemv, which it may share) holds the partials and the chunk's
- * last workgroup sums them in slice order (deterministic).  Needs
- * n * (2 or 4) * 2 + 64 * (rows_per_chunk + 1) * (2 or 4) bytes of LDS at
- * most 150 KiB (two workgroups per CU up to 80 KiB, e.g. n = 2048 with
- * 255-row chunks, n = 6144 with 62-row chunks; one above), else
- * VQ2_ERR_UNSUPPORTED.  Replaces the PackedLinear batch > 1
+ * last workgroup sums them in slice order (deterministic).  A workgroup
+ * holds 2 activation rows (batch <= 2) or 4 in
+ * max(n * rows / 2, 512 * rows) * 4 + 32 * parts * (rows_per_chunk + 1) *
+ * rows bytes of LDS (parts = 4 for chunks of at most 32 rows, else 2);
+ * at batch 3-4 a call whose 4-row workgroups would exceed 80 KiB (one per
+ * CU) runs as two launches of at most 2 rows each (the LM head's 297-row
+ * chunks: 15 % faster), sharing the workspace in stream order.  More than
+ * 150 KiB for the rows of a launch gives VQ2_ERR_UNSUPPORTED (n = 2048 fits
+ * with any chunk height, n = 6144 with 62-row chunks, n = 32768 at 2 rows).
+ * Replaces the PackedLinear batch > 1
  * fallback, dequant + F.linear (vq2/runtime.py:82-89, 105-110). */
 size_t vq2_sorted_gemm_batch_workspace(const vq2_sorted_mat* mats, int n_mat, int64_t batch, int slices);
 int vq2_sorted_gemm_batch(const void* x, int x_dt, int64_t batch, int64_t x_stride, int n_mat,

@@ -89,9 +89,11 @@ def test_sorted_batch_rejects_bad_arguments_on_host():
     assert "batch=0" in _err(L.vq2_sorted_gemm_batch(*args(0, 2048, m, 2048)))
     assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2040, m, 2048)))
     assert "row stride" in _err(L.vq2_sorted_gemm_batch(*args(2, 2052, m, 2048)))
-    # n = 32768 (ng 4096, chunks of at most 31 rows): 4 fp16 rows are 256 KiB of LDS
-    big = mat(rows=64, ng=4096, R=31)
-    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(4, 32768, big, 32768)))
+    # n = 65536 (ng 8192, chunks of at most 15 rows): 2 fp16 rows are 256 KiB of LDS (at
+    # batch 3-4 the call runs as 2-row launches, which do not fit either)
+    big = mat(rows=64, ng=8192, R=15)
+    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(4, 65536, big, 65536)))
+    assert "LDS" in _err(L.vq2_sorted_gemm_batch(*args(2, 65536, big, 65536)))
     # rows_per_chunk beyond 511 (what 17-bit positions hold for ng = 256)
     assert "rows_per_chunk" in _err(L.vq2_sorted_gemm_batch(*args(2, 2048, mat(R=600), 2048)))
     msg = _err(L.vq2_sorted_gemm_batch_argmax(4096, 0, 3, 2048, ctypes.byref(m), 4096, None, 1, 1, 2048, 1.0,

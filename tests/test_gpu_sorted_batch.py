@@ -160,12 +160,34 @@ def test_batch_gemm_errors(dev):
     s = m["scale"].to(dev)
     with pytest.raises(Vq2Error, match="1..4 activation rows"):
         K.vq_sorted_gemm_batch(torch.zeros(5, 2048, device=dev), [(sp, s)], cb0.to(dev), None, 2048)
-    # n = 32768: the fp16 activation of 4 rows alone is 256 KiB of LDS
-    big = synth.vq_matrix(9771, 64, 32768, bpw=2)
-    spb = K.SortedPlanes(big["idx0"], None, 64, 32768, device=dev)
-    with pytest.raises(Vq2Error, match="LDS"):
-        K.vq_sorted_gemm_batch(torch.zeros(4, 32768, device=dev), [(spb, big["scale"].to(dev))], cb0.to(dev), None,
-                               32768)
+    # n = 65536: the fp16 activation of 2 rows alone is 256 KiB of LDS
+    big = synth.vq_matrix(9771, 16, 65536, bpw=2)
+    spb = K.SortedPlanes(big["idx0"], None, 16, 65536, device=dev)
+    for B in (2, 4):
+        with pytest.raises(Vq2Error, match="LDS"):
+            K.vq_sorted_gemm_batch(torch.zeros(B, 65536, device=dev), [(spb, big["scale"].to(dev))], cb0.to(dev),
+                                   None, 65536)
+
+
+@pytest.mark.parametrize("B", [3, 4])
+def test_batch_gemm_split_into_two_row_launches(dev, B):
+    """4-row workgroups that would take more than half a CU's LDS run as
+    launches of at most 2 rows: n = 32768 (4 rows: 256 KiB, 2 rows: 132
+    KiB) and the LM head's 297-row chunks; logits and top-1 against the
+    oracle on the activation as the kernel holds it."""
+    from act_rounding import fp16_row_scaled
+
+    cb = synth.codebook(9772)
+    for rows, n, R in ((64, 32768, None), (700, 2048, 297)):
+        m = synth.vq_matrix(9773 + n, rows, n, bpw=2)
+        sp = K.SortedPlanes(m["idx0"], None, rows, n, device=dev, rows_per_chunk=R)
+        x = synth.activations(9774 + B, (B, n), dtype=torch.float32) * 0.5
+        (y,) = K.vq_sorted_gemm_batch(x.to(dev), [(sp, m["scale"].to(dev))], cb.to(dev), None, n)
+        _, y64 = O.vq_gemv(fp16_row_scaled(x.numpy()), m["idx0"], None, cb, None, m["scale"])
+        for b in range(B):
+            assert O.max_rel_err(y.cpu().numpy()[b], y64[b]) < 1e-5, (n, b)
+        idx, val = K.vq_sorted_gemm_batch_argmax(x.to(dev), sp, m["scale"].to(dev), cb.to(dev), None, n)
+        assert idx.cpu().tolist() == [int(np.argmax(y64[b])) for b in range(B)], n
 
 
 def test_batch_paths_graph_replays_match_eager(dev):

@@ -35,3 +35,16 @@ def test_sorted_slices_rule(monkeypatch):
     assert K.sorted_slices([P(n_chunks=33, iters_per_chunk=200)], dev) == 7       # down
     assert K.sorted_slices([P(n_chunks=32, iters_per_chunk=50)], dev) == 2        # few iterations per wave
     assert K.sorted_slices([P(n_chunks=512, iters_per_chunk=300)], dev) == 1      # LM head
+
+
+def test_sorted_batch_fits_rule():
+    """The batch kernel's LDS rule as the runtime reads it: 4-row workgroups above 80 KiB run as
+    2-row launches, which must fit in 150 KiB."""
+    from types import SimpleNamespace as P
+
+    assert K.sorted_batch_fits([P(n=2048, rows_per_chunk=246)] * 2, 4)        # gate + up: 79.6 KiB at 4 rows
+    assert K.sorted_batch_fits([P(n=2048, rows_per_chunk=297)], 4)            # LM head: split, 46 KiB at 2 rows
+    assert K.sorted_batch_fits([P(n=6144, rows_per_chunk=63)], 4)             # down
+    assert K.sorted_batch_fits([P(n=32768, rows_per_chunk=31)], 4)            # split: 139 KiB at 2 rows
+    assert not K.sorted_batch_fits([P(n=65536, rows_per_chunk=7)], 4)         # 2 rows: 256 KiB
+    assert not K.sorted_batch_fits([P(n=65536, rows_per_chunk=7)], 2)
