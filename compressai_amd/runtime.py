@@ -126,6 +126,43 @@ class PackedLinear(nn.Module):
         cb1 = self._cbs[0][self.keys[1]] if len(self.keys) > 1 else None
         return self.idx0, i1, cb0, cb1
 
+    @property
+    def planes_released(self):
+        return self.idx0 is None
+
+    def release_planes(self):
+        """Frees the reference index planes and keeps only the code-sorted
+        copy (~3.06 bytes per code resident instead of ~5.06 with both):
+        batch 1 runs on it as before, every other batch on the sorted batch
+        kernel in launches of up to 4 rows after the RHT (the activation held
+        in fp16 under a power-of-two scale per row, ~1e-4 of max |y|).  Needs
+        the sorted copy, fp16 / bf16 codebooks and a chunk height the batch
+        kernel fits; the planes cannot be restored.  A PackedProjections over
+        this module must be built before (it may repack the planes)."""
+        if self.planes_released:
+            return
+        cb0 = self._cbs[0][self.keys[0]]
+        if self.sorted is None:
+            raise K.Vq2Error("release_planes: no code-sorted copy to run on")
+        if cb0.dtype not in (torch.float16, torch.bfloat16):
+            raise K.Vq2Error("release_planes: the sorted kernels take fp16 / bf16 codebooks")
+        if not (K.sorted_batch_fits([self.sorted], 4) and K.sorted_batch_fits([self.sorted], 2)):
+            raise K.Vq2Error("release_planes: the sorted batch kernel does not fit these chunks")
+        for i in range(len(self.cfg)):
+            setattr(self, f"idx{i}", None)
+
+    def _sorted_rows(self, x2, od):
+        """Batch >= 2 without the planes: the sorted batch kernel over groups
+        of up to 4 rotated rows."""
+        _, _, cb0, cb1 = self._planes()
+        xr = self.rot.fwd(x2, out_dtype=torch.float32)
+        y = torch.empty((x2.shape[0], self.out), dtype=od, device=x2.device)
+        for b0 in range(0, x2.shape[0], K.SORTED_BATCH_MAX):
+            b1 = min(x2.shape[0], b0 + K.SORTED_BATCH_MAX)
+            K.vq_sorted_gemm_batch(xr[b0:b1], [(self.sorted, self.scale)], cb0, cb1, self.n, out_dtype=od,
+                                   ys=[y[b0:b1]])
+        return y
+
     def _sorted_ok(self, B, cb0):
         return self.sorted is not None and B == 1 and cb0.dtype in (torch.float16, torch.bfloat16)
 
@@ -158,6 +195,8 @@ class PackedLinear(nn.Module):
         elif self._sorted_batch_ok(B, cb0):
             xr = self.rot.fwd(x2, out_dtype=torch.float32)
             y = K.vq_sorted_gemm_batch(xr, [(self.sorted, self.scale)], cb0, cb1, self.n, out_dtype=od)[0]
+        elif self.planes_released:
+            y = self._sorted_rows(x2, od)
         elif B <= 2 and self.n % 64 == 0:
             # one launch: every workgroup rotates x in LDS, then multiplies
             y = K.vq_gemv_rht(x2, [(i0, i1, self.scale, self.out)], cb0, cb1, self.n, self.rot._perm32,
@@ -201,7 +240,7 @@ class PackedProjections(nn.Module):
         self.lins = nn.ModuleList(lins)
         codes = sum(m.out * (m.n // 8) * len(m.cfg) for m in lins)
         self.codes = codes
-        dev = a.idx0.device
+        dev = a.scale.device
         use = sorted_layout if sorted_layout is not None else (
             codes >= SORTED_MIN_LAUNCH_CODES and dev.type == "cuda" and a.cfg in ((16,), (16, 8), (16, 16)))
         self.sorted = None
@@ -214,6 +253,9 @@ class PackedProjections(nn.Module):
             for m in lins:
                 sp = m.sorted
                 if sp is None or (R is not None and sp.rows_per_chunk != R):
+                    if m.planes_released:
+                        raise K.Vq2Error("PackedProjections: a projection's planes were released before its "
+                                         "sorted copy could be packed for this launch")
                     sp = K.SortedPlanes(m.idx0, getattr(m, "idx1", None), m.out, m.n, device=dev, rows_per_chunk=R)
                     m.sorted = sp
                 self.sorted.append(sp)
@@ -235,6 +277,8 @@ class PackedProjections(nn.Module):
             xr = a.rot.fwd(x2, out_dtype=torch.float32)
             ys = K.vq_sorted_gemm_batch(xr, [(sp, m.scale) for sp, m in zip(self.sorted, lins)], cb0, cb1, a.n,
                                         out_dtype=od)
+        elif any(m.planes_released for m in lins):
+            return [m(x, out_dtype=out_dtype) for m in lins]
         elif B <= 2 and a.n % 64 == 0:
             mats = []
             for m in lins:
@@ -269,5 +313,10 @@ class PackedLMHead(nn.Module):
         if lin._sorted_batch_ok(x2.shape[0], cb0):
             xr = lin.rot.fwd(x2, out_dtype=torch.float32)
             return K.vq_sorted_gemm_batch_argmax(xr, lin.sorted, lin.scale, cb0, cb1, lin.n)
+        if lin.planes_released:
+            xr = lin.rot.fwd(x2, out_dtype=torch.float32)
+            parts = [K.vq_sorted_gemm_batch_argmax(xr[b0:b0 + K.SORTED_BATCH_MAX], lin.sorted, lin.scale, cb0, cb1,
+                                                   lin.n) for b0 in range(0, x2.shape[0], K.SORTED_BATCH_MAX)]
+            return torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
         xr = lin.rot.fwd(x2, out_dtype=lin.act_dtype)
         return K.vq_gemv_argmax(xr, i0, i1, cb0, cb1, lin.scale, lin.out, lin.n, 1.0)

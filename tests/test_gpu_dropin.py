@@ -197,6 +197,40 @@ def test_packed_linear_sorted_layout_batch1(dev, cfg, out, n):
         assert abs(float(val[0]) - y64[0].max()) <= 1e-5 * abs(y64[0].max())
 
 
+@pytest.mark.parametrize("cfg", [(16,), (16, 16)])
+def test_packed_linear_release_planes(dev, cfg):
+    """release_planes() frees the reference planes and keeps only the
+    code-sorted copy: batch 1 on the sorted GEMV, batch 2, 3 and 6 on the
+    sorted batch kernel in groups of up to 4 rows, and the top-1 of
+    PackedLMHead; outputs match the oracle on the activation as each kernel
+    holds it (to 1e-5), and the resident bytes drop by the planes."""
+    from compressai_amd.runtime import PackedLinear, PackedLMHead
+
+    out, n = 4096, 2048
+    bpw = 4 if cfg == (16, 16) else 2
+    cbs = {"16": synth.codebook(9400).to(dev), "16_16": synth.codebook(9401).to(dev)}
+    m = synth.vq_matrix(9402 + bpw, out, n, bpw=bpw)
+    lin = PackedLinear((out, n), cfg, f"t_release_{bpw}", [m["idx0"], m["idx1"]][:len(cfg)], m["scale"], cbs, dev)
+    assert lin.sorted is not None and not lin.planes_released
+    before = lin.nbytes()
+    lin.release_planes()
+    assert lin.planes_released and lin.idx0 is None
+    assert before - lin.nbytes() == out * (n // 8) * 2 * len(cfg)
+    cb1 = cbs["16_16"].cpu() if bpw == 4 else None
+    for B in (1, 2, 3, 6):
+        x = synth.activations(9405 + B, (B, n), dtype=torch.float32)
+        y = lin(x.to(dev), out_dtype=torch.float32)
+        assert y.shape == (B, out)
+        xr = lin.rot.fwd(x.to(dev), out_dtype=torch.float32).cpu().numpy()
+        xk = xr if B == 1 else fp16_row_scaled(xr)
+        _, y64 = O.vq_gemv(xk, m["idx0"], m["idx1"], cbs["16"].cpu(), cb1, lin.scale.cpu())
+        for b in range(B):
+            assert O.max_rel_err(y[b].cpu().numpy(), y64[b]) < 1e-5, (B, b)
+        if cfg == (16,):
+            idx, val = PackedLMHead(lin).argmax(x.to(dev))
+            assert idx.cpu().tolist() == [int(np.argmax(y64[b])) for b in range(B)], B
+
+
 def test_packed_linear_16_8_on_the_sorted_layout(dev):
     """A (16,8) 3 bpw PackedLinear of 2.1 M codes keeps a sorted copy whose
     stage 2 is the uint8 plane (packed as codes below 256 into the [256, 8]

@@ -174,6 +174,20 @@ def test_packed_linear_holds_bf16_scales():
     assert keep.scale.dtype == torch.float16 and torch.equal(keep.scale, m["scale"])
 
 
+def test_packed_linear_release_planes_needs_a_sorted_copy():
+    """release_planes() keeps the planes of a module without a code-sorted
+    copy (here: on the CPU, where none is built) and says why."""
+    from compressai_amd.kernels import Vq2Error
+    from compressai_amd.runtime import PackedLinear
+
+    m = synth.vq_matrix(8501, 64, 512, bpw=2)
+    lin = PackedLinear((64, 512), (16,), "t", [m["idx0"]], m["scale"], {"16": synth.codebook(8501)}, "cpu")
+    assert lin.sorted is None and not lin.planes_released
+    with pytest.raises(Vq2Error, match="no code-sorted copy"):
+        lin.release_planes()
+    assert torch.equal(lin.idx0, m["idx0"])
+
+
 def test_resident_experts_reference_constructor_on_cpu():
     """ResidentMoEExperts(q_gate_up, q_down, cb16, device): the quantized
     dicts are viewed as [E, 2I, H/8] / [E, H, I/8] pools with bf16 scales
