@@ -170,8 +170,10 @@ def test_sorted_moe_bad_expert_id_gives_nan_token(dev):
 @pytest.mark.parametrize("T", [1, 5])
 def test_sorted_moe_router_ids_and_weights(dev, T):
     """Router built into the sorted gate_up launch: the published ids and
-    weights equal the standalone router's bit for bit, and the layer output
-    equals the same experts run with those ids."""
+    weights equal the standalone router's bit for bit and the oracle's
+    router (softmax, top-k, renormalised, ties to the lower id; the shared
+    expert's sigmoid gate), and the layer output equals the same experts run
+    with those ids."""
     from compressai_amd.moe import MoELayer
 
     E, k = 64, 6
@@ -188,6 +190,12 @@ def test_sorted_moe_router_ids_and_weights(dev, T):
     rid, rw = layer.route(h, logits)
     assert torch.equal(ids.cpu(), rid.cpu().to(torch.int32))
     assert torch.equal(w.cpu(), rw.cpu())
+    oid, ow = O.router_topk(logits.float().cpu().numpy(), k)
+    assert ids.cpu()[:, :k].numpy().tolist() == oid.tolist()
+    assert np.allclose(w.cpu()[:, :k].numpy(), ow, rtol=1e-5, atol=1e-7)
+    assert (ids.cpu()[:, k] == E).all()
+    sg = 1 / (1 + np.exp(-(h.double().cpu().numpy() @ gate.double().numpy())))
+    assert np.allclose(w.cpu()[:, k].numpy(), sg, rtol=1e-5)
     again = m.experts(h, rid, rw)
     assert torch.equal(out, again)
     assert torch.equal(layer(h, logits), out)
