@@ -221,3 +221,37 @@ def test_batch_paths_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         for a, b in zip(out, ref):
             assert torch.equal(a, b), r
+
+
+def test_batch4_split_graph_replays_match_eager(dev):
+    """Logits and top-1 at batch 4 over 300-row chunks (4-row workgroups past
+    80 KiB of LDS, so each call runs as two 2-row launches sharing one
+    workspace) through a PackedLinear whose planes were released, captured
+    once; every replay, with eager work and synchronisations between the
+    replays, equals the eager step bit for bit."""
+    from compressai_amd.graph import DecodeStepGraph
+    from compressai_amd.runtime import PackedLinear, PackedLMHead
+
+    n, rows = 2048, 4800
+    cbs = {"16": synth.codebook(9790).to(dev)}
+    mh = synth.vq_matrix(9791, rows, n, bpw=2)
+    lin = PackedLinear((rows, n), (16,), "lm_head", [mh["idx0"]], mh["scale"], cbs, dev)
+    lin.sorted = K.SortedPlanes(mh["idx0"], None, rows, n, device=dev, rows_per_chunk=300)
+    lin.release_planes()
+    head = PackedLMHead(lin)
+
+    def step(x):
+        y = lin(x, out_dtype=torch.float32)
+        idx, val = head.argmax(x)
+        return y, idx, val
+
+    gstep = DecodeStepGraph(step, [synth.activations(9792, (4, n), dtype=torch.float16).to(dev)])
+    for r in range(4):
+        x = synth.activations(9793 + r, (4, n), dtype=torch.float16).to(dev)
+        ref = [t.clone() for t in step(x)]
+        torch.cuda.synchronize()
+        out = [t.clone() for t in gstep(x)]
+        torch.cuda.synchronize()
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), r
+        assert ref[1].cpu().tolist() == ref[0].argmax(dim=1).cpu().tolist()
