@@ -490,7 +490,8 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     // (a pre-rotated x is only copied: there the gathers go out at once)
     // gathers one iteration ahead (measured on the dense step: 49.1 us
     // against 49.3 at two; three, before the pipeline's tail stopped loading
-    // past the range, 51.3 against 50.2 at two); the 64-VGPR fused-RHT
+    // past the range, 51.3 against 50.2 at two; with 3-byte entries and the
+    // leading arguments 42.2 against 45.5 at two); the 64-VGPR fused-RHT
     // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
     // two
     SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2, SG_WAVES, TALL> pipe;
