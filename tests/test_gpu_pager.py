@@ -67,9 +67,10 @@ class LruModel:
         return [self.slot_of[e] if e >= 0 else -1 for e in pe], [(miss[r], elig[r]) for r in range(served)]
 
 
+@pytest.mark.parametrize("C,T", [(12, 2), (7, 1)])   # 7 slots: the stamps padded to 8 in LDS
 @pytest.mark.parametrize("sorted_layout", [False, True])
-def test_device_pager_tables_follow_the_model(dev, tmp_path, sorted_layout):
-    E, C, T, P = 40, 12, 2, 5
+def test_device_pager_tables_follow_the_model(dev, tmp_path, sorted_layout, C, T):
+    E, P = 40, 5
     store, (gui, gus, dni, dns) = _container(tmp_path, E)
     pager = paged.ExpertPager(store, 0, C, dev, device_tables=True, sorted_layout=sorted_layout)
     model = LruModel(E, C)
