@@ -86,6 +86,7 @@ struct SortedBatchArgs {
     int nseg;
     int nc;
     int x_floats;  // floats of LDS before the accumulators (activation, later the row-sum stage)
+    int rg_wgs;    // > 0: workgroups [g * rg_wgs, (g + 1) * rg_wgs) take rows NB g .. NB g + NB - 1
     SortedBatchSeg seg[SG_MAX_SEG];
     uint64_t* cand;  // EP 1: [workgroup][batch] best top-1 keys
 };
@@ -93,11 +94,11 @@ struct SortedBatchArgs {
 // Eight activation values of row b, group g (16-byte aligned: x and its row
 // stride are checked on the host).
 template <int XT>
-__device__ __forceinline__ void sb_load8(const SortedBatchArgs& a, int b, int64_t g, float (&v)[8])
+__device__ __forceinline__ void sb_load8(const SortedBatchArgs& a, const void* x, int b, int64_t g, float (&v)[8])
 {
     const int64_t off = (int64_t)b * a.x_stride + g * 8;
     if constexpr (XT == VQ2_DT_F32) {
-        const u32x4* q = (const u32x4*)((const float*)a.x + off);
+        const u32x4* q = (const u32x4*)((const float*)x + off);
         const u32x4 p0 = q[0], p1 = q[1];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -177,7 +178,11 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
     _Float16* s_xh = (_Float16*)smem;             // [ng][NB][8]
     accv* s_acc = (accv*)(smem + a.x_floats);     // SB_WAVES x sorted_parts(R) x (R + 1)
 
-    const int pos = (int)blockIdx.x;
+    // row group (rg_wgs > 0): this workgroup's rows are brow .. brow + nbat - 1
+    const int rg = a.rg_wgs ? (int)blockIdx.x / a.rg_wgs : 0;
+    const int pos = (int)blockIdx.x - rg * a.rg_wgs;
+    const int brow = NB * rg, nbat = min(NB, a.batch - brow);
+    const void* xg = (const char*)a.x + (int64_t)brow * a.x_stride * (XT == VQ2_DT_F32 ? 4 : 2);
     const int slice = pos / a.nc, gchunk = pos - slice * a.nc;
     int si = 0;
 #pragma unroll
@@ -208,7 +213,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
             const int64_t g = t / NB;
             const int b = (int)(t - g * NB);
             u32x4 v = {0u, 0u, 0u, 0u};
-            if (b < a.batch) v = *(const u32x4*)((const uint16_t*)a.x + (int64_t)b * a.x_stride + g * 8);
+            if (b < nbat) v = *(const u32x4*)((const uint16_t*)xg + (int64_t)b * a.x_stride + g * 8);
             *(u32x4*)(s_xh + t * 8) = v;
         }
     } else {
@@ -217,9 +222,9 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
         for (int64_t t = threadIdx.x; t < groups; t += SB_THREADS) {
             const int64_t g = t / NB;
             const int b = (int)(t - g * NB);
-            if (b < a.batch) {
+            if (b < nbat) {
                 float v[8];
-                sb_load8<XT>(a, b, g, v);
+                sb_load8<XT>(a, xg, b, g, v);
                 float am = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(v[k]));
@@ -239,9 +244,9 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
             const int64_t g = t / NB;
             const int b = (int)(t - g * NB);
             half8_t h = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (b < a.batch) {
+            if (b < nbat) {
                 float v[8];
-                sb_load8<XT>(a, b, g, v);  // an L2 hit: loaded above
+                sb_load8<XT>(a, xg, b, g, v);  // an L2 hit: loaded above
                 const int e = s_e[b];
 #pragma unroll
                 for (int k = 0; k < 8; k++) h[k] = (_Float16)ldexpf(v[k], e);
@@ -319,18 +324,18 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
             if (lane == 0) s_key[wave][b] = best;  // 0 from waves with no row of their own
         }
         __syncthreads();
-        if (threadIdx.x < NB && (int)threadIdx.x < a.batch) {
+        if (threadIdx.x < NB && (int)threadIdx.x < nbat) {
             const int b = threadIdx.x;
             uint64_t best = s_key[0][b];
             for (int w = 1; w < SB_WAVES; w++) best = s_key[w][b] > best ? s_key[w][b] : best;
-            a.cand[(int64_t)blockIdx.x * a.batch + b] = best;
+            a.cand[(int64_t)pos * a.batch + brow + b] = best;
         }
     } else if (a.slices == 1) {
         if (own) {
             const float sc = load_as_f32(sg.scale, a.s_dt, row);
 #pragma unroll
             for (int b = 0; b < NB; b++)
-                if (b < a.batch) store_from_f32(sg.y, a.y_dt, (int64_t)b * sg.out_rows + row, (sum[b] * sc) * a.rs);
+                if (b < nbat) store_from_f32(sg.y, a.y_dt, (int64_t)(brow + b) * sg.out_rows + row, (sum[b] * sc) * a.rs);
         }
     } else {
         // several slices: the last of the chunk's workgroups to finish adds
@@ -338,12 +343,12 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
         if (own)
 #pragma unroll
             for (int b = 0; b < NB; b++)
-                if (b < a.batch) share_store(sg.part + ((int64_t)slice * NB + b) * sg.out_rows + row, sum[b]);
+                if (b < nbat) share_store(sg.part + ((int64_t)slice * NB + b) * sg.out_rows + row, sum[b]);
         if (arrive_last(sg.cnt + chunk, (uint32_t)a.slices) && own) {
             const float sc = load_as_f32(sg.scale, a.s_dt, row);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                if (b >= a.batch) break;
+                if (b >= nbat) break;
                 float tot = 0.0f;
                 for (int j0 = 0; j0 < a.slices; j0 += 8) {
                     float v[8];
@@ -356,7 +361,7 @@ __global__ void __launch_bounds__(SB_THREADS, 2) vq_sorted_batch_kernel(const So
                     for (int j = 0; j < 8; j++)
                         if (j0 + j < a.slices) tot += v[j];
                 }
-                store_from_f32(sg.y, a.y_dt, (int64_t)b * sg.out_rows + row, (tot * sc) * a.rs);
+                store_from_f32(sg.y, a.y_dt, (int64_t)(brow + b) * sg.out_rows + row, (tot * sc) * a.rs);
             }
         }
     }
@@ -436,20 +441,33 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
     if (c.x_stride < n || c.x_stride % 8 || (uintptr_t)c.x % 16)
         return set_error(VQ2_ERR_ARG, "vq2 sorted GEMM: x must be 16-byte aligned with a row stride >= n, a multiple "
                          "of 8 (got %lld)", (long long)c.x_stride);
-    const int nb = batch_slots(c.batch);
+    int nb = batch_slots(c.batch), groups = 1;
     // chunks of 256 rows or more, or 17-bit positions: the TALL kernels
     const bool tall = rmax >= 256 || sorted_pbits(sorted_gbits(c.ng), (int)rmax) > 16;
     // activation (fp16, nb rows) or the row-sum stage, whichever is larger, then the accumulators
+    const auto shm_of = [&](int rows) {
+        return (size_t)(std::max<int64_t>(n * rows / 2, 2 * 256 * rows) + (int64_t)SB_WAVES * sorted_acc_arrays(c) * rows) *
+               sizeof(float);
+    };
+    if (nb == 4 && shm_of(4) > SB_PAIR_SHM && c.slices == 1) {
+        // 4-row workgroups this large run one per CU (8 waves): 2-row
+        // workgroups instead, several per CU, one launch over both row
+        // pairs (rows 2 g, 2 g + 1 in workgroups [g * wg, (g + 1) * wg))
+        // and one final top-1; a row group's workgroups start as the other's
+        // finish (the LM head 151936 x 2048 in 297-row chunks: top-1 at
+        // batch 4 148.9 us as 4-row workgroups, 129.8 as two 2-row launches,
+        // 121.6 as one; batch 3 147.7 / 120.5; logits at batch 4 145.3 /
+        // 116.9)
+        nb = 2;
+        groups = (int)((c.batch + 1) / 2);
+    }
     const int64_t x_floats = std::max<int64_t>(n * nb / 2, 2 * 256 * nb);
-    const size_t shm = (size_t)(x_floats + (int64_t)SB_WAVES * sorted_acc_arrays(c) * nb) * sizeof(float);
+    const size_t shm = shm_of(nb);
     if (nb == 4 && shm > SB_PAIR_SHM) {
-        // 4-row workgroups this large run one per CU (8 waves): rows 0-1,
-        // then the rest, as launches of 2-row workgroups, several per CU
-        // (the LM head 151936 x 2048 in 297-row chunks: top-1 at batch 4
-        // 148.9 -> 129.8 us, logits 145.3 -> 124.2, batch 3 147.7 -> 129.6;
-        // gate + up, 79.6 KiB at batch 4, stays one launch: 37.2 against
-        // 38.4 split).  Stream order lets the second call reuse the
-        // workspace (top-1 keys, slice counters back at zero).
+        // the same with several slices (whose counters and partials are per
+        // chunk): rows 0-1, then the rest, as two launches that reuse the
+        // workspace in stream order (gate + up, 79.6 KiB at batch 4, stays one
+        // launch: 37.2 us against 38.4 split)
         SortedCall lo = c, hi = c;
         lo.batch = 2;
         hi.batch = c.batch - 2;
@@ -523,18 +541,21 @@ int sorted_batch_launch(const SortedCall& c, int64_t* top1_idx, float* top1_val)
         return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: %lld chunks with several slices (at most %d)",
                          (long long)n_cnt, VQ2_SORTED_MAX_COUNTERS);
     if (wg == 0) return VQ2_OK;
-    if (wg > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: grid too large");
+    if (wg * groups > 0x7FFFFFFF) return set_error(VQ2_ERR_UNSUPPORTED, "vq2 sorted GEMM: grid too large");
     a.nc = (int)nc;
+    a.rg_wgs = groups > 1 ? (int)wg : 0;
+    const unsigned grid = (unsigned)(wg * groups);
     hipStream_t st = (hipStream_t)c.stream;
     hipError_t err;
     if (top1) {
-        err = nb == 2 ? launch_batch_nb<2, 1>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st)
-                      : launch_batch_nb<4, 1>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st);
+        // keys [workgroup of a group][batch]: one final pass over wg keys per row
+        err = nb == 2 ? launch_batch_nb<2, 1>(c.cb_dt, c.x_dt, tall, a, grid, shm, st)
+                      : launch_batch_nb<4, 1>(c.cb_dt, c.x_dt, tall, a, grid, shm, st);
         if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMM launch");
         return argmax_final_launch(a.cand, wg, c.batch, top1_idx, top1_val, c.stream);
     }
-    err = nb == 2 ? launch_batch_nb<2, 0>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st)
-                  : launch_batch_nb<4, 0>(c.cb_dt, c.x_dt, tall, a, (unsigned)wg, shm, st);
+    err = nb == 2 ? launch_batch_nb<2, 0>(c.cb_dt, c.x_dt, tall, a, grid, shm, st)
+                  : launch_batch_nb<4, 0>(c.cb_dt, c.x_dt, tall, a, grid, shm, st);
     if (err != hipSuccess) return set_hip_error(err, "vq2 sorted GEMM launch");
     return VQ2_OK;
 }

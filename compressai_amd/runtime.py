@@ -53,9 +53,9 @@ SORTED_MIN_LAUNCH_CODES = SORTED_MIN_CODES
 # for every activation row, the activation rotated by its own launch first)
 # where it was measured faster (HIP graphs, MI355X, us per call):
 #  * matrices of SORTED_BATCH_MIN_CODES codes or more -- the LM head
-#    151936 x 2048: 68.5 against 195.6 (gather kernel) at batch 2, 130
-#    (two 2-row launches) against 181 (matrix cores) at batch 4, top-1 or
-#    logits;
+#    151936 x 2048: 68.5 against 195.6 (gather kernel) at batch 2, 122
+#    (2-row workgroups over both row pairs) against 181 (matrix cores) at
+#    batch 4, top-1 or logits;
 #  * batch 2 of inputs wider than 2048 (down 2048 x 6144, 4 bpw: 22.4 against
 #    28.9 on the gather kernel with the 6144-point RHT in its prologue);
 #  * PackedProjections at batch 3-4 (q, k, v in one launch: 22.0-24.4 against

@@ -437,8 +437,10 @@ int vq2_sorted_gemv_argmax(const void* x, int x_dt, const int32_t* perm, const i
  * max(n * rows / 2, 512 * rows) * 4 + 32 * parts * (rows_per_chunk + 1) *
  * rows bytes of LDS (parts = 4 for chunks of at most 32 rows, else 2);
  * at batch 3-4 a call whose 4-row workgroups would exceed 80 KiB (one per
- * CU) runs as two launches of at most 2 rows each (the LM head's 297-row
- * chunks: 15 % faster), sharing the workspace in stream order.  More than
+ * CU) runs 2-row workgroups instead: with one slice, one launch over both
+ * row pairs and one final top-1 (the LM head's 297-row chunks: 18 % faster
+ * at batch 4); with several, two launches sharing the workspace in stream
+ * order.  More than
  * 150 KiB for the rows of a launch gives VQ2_ERR_UNSUPPORTED (n = 2048 fits
  * with any chunk height, n = 6144 with 62-row chunks, n = 32768 at 2 rows).
  * Replaces the PackedLinear batch > 1
