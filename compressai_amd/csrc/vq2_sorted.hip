@@ -491,10 +491,9 @@ __global__ void __launch_bounds__(SG_THREADS, (XM != 0 && EP == 1) ? 8 : 1)
     // gathers one iteration ahead (measured on the dense step: 49.1 us
     // against 49.3 at two; three, before the pipeline's tail stopped loading
     // past the range, 51.3 against 50.2 at two; with 3-byte entries and the
-    // leading arguments 42.2 against 45.5 at two); the 64-VGPR fused-RHT
-    // top-1, two workgroups per CU, needs one; the pre-rotated top-1 keeps
-    // two
-    SortedPipe<CBT, (XM != 0 || EP == 0) ? 1 : 2, SG_WAVES, TALL> pipe;
+    // leading arguments 42.2 against 45.5 at two); the top-1 of the LM head
+    // too, two workgroups per CU (pre-rotated: 51.5 against 55.6 us at two)
+    SortedPipe<CBT, 1, SG_WAVES, TALL> pipe;
     pipe.load_entries(ent, a.cb0, a.cb1, c_beg, c_beg, s0, s1, wave, lane, 0, 1, a.c1mask);
     // the fields the loop needs, from the argument struct (its lines were
     // not needed before this point)
