@@ -249,7 +249,11 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
     const int xcd = bid & 7;
     const int pos = a.xmap ? xcd * a.xq + min(xcd, a.xr) + (bid >> 3) : bid;
     const int units = a.n_pairs * pl.C;
-    const int slice = pos / units, unit = pos - slice * units;
+    // xmap: slice-major (a slice's code range per XCD); else pair-major (a
+    // pair's chunks and slices consecutive, so the pairs of a later round
+    // are whole pairs and the earlier ones complete in the first)
+    const int slice = a.xmap ? pos / units : pos % a.slices;
+    const int unit = a.xmap ? pos - slice * units : pos / a.slices;
     const int p = unit / pl.C, chunk = unit - p * pl.C;
     const int t = p / a.P, kslot = p - t * a.P;
 
