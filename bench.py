@@ -360,7 +360,7 @@ def bench_moe(args, dev, n_layers=40, tokens=(1, 8)):
     m0 = layers[0].experts_mod
     res["resident"] = dict(
         planes=sum(t.numel() * t.element_size() for t in (m0.gate_up_idx, m0.down_idx)),
-        sorted=sum(p.nbytes() for p in (m0.sorted_gu, m0.sorted_dn) if p is not None))
+        sorted=sum(p.nbytes() for p in (m0.sorted_gu, m0.sorted_dn, m0.sorted_dn_tall) if p is not None))
     return res
 
 

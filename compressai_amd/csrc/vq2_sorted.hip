@@ -308,7 +308,7 @@ int sorted_pack_pool(const int16_t* idx, const int16_t* idx1, int64_t n_experts,
                      uint32_t* entries, int64_t cap_iters, int64_t* iters_per_chunk, int64_t* stage1_iters,
                      int64_t* n_iters, int n_threads)
 {
-    const int64_t rmax = std::min<int64_t>(sorted_max_rows(ng, 16), 255);  // pools: 16-bit positions
+    const int64_t rmax = sorted_max_rows(ng, 16);  // pools: 16-bit positions
     if (rmax == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_pack_pool: ng=%lld outside 1..32768", (long long)ng);
     if (R < 1 || R > rmax)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_pack_pool: rows_per_chunk=%lld outside 1..%lld for ng=%lld",

@@ -328,7 +328,7 @@ __device__ __forceinline__ void rht2k_build(int k, int64_t n, const Rht2kLoad& L
 // 2 t + j read through `val` (natural order, index < 512), bit 0 in
 // registers, bits 1-6 across lanes, bits 7-8 as one radix-4 pass through
 // LDS (s_nat: 512 floats that `val` does not read) that scales and stores
-// the split layout.  A barrier must follow.
+// the split layout (halves xb floats apart).  A barrier must follow.
 struct RhtPairLoad {
     u32x2 p;     // permutation entries 2 t, 2 t + 1
     uint32_t s;  // their two sign bytes (low 16 bits)
@@ -346,7 +346,8 @@ __device__ __forceinline__ void rht512_load(const GemvArgs& a, RhtPairLoad& L)
 }
 
 template <typename F>
-__device__ __forceinline__ void rht512_transform(const RhtPairLoad& L, F val, float* s_nat, float* s_split, float scale)
+__device__ __forceinline__ void rht512_transform(const RhtPairLoad& L, F val, float* s_nat, float* s_split, float scale,
+                                                 int xb)
 {
     const int t = threadIdx.x, lane = t & 63;
     if (t < RHT512 / 2) {
@@ -381,7 +382,7 @@ __device__ __forceinline__ void rht512_transform(const RhtPairLoad& L, F val, fl
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = t + 128 * i;
-            s_split[((e >> 2) & 1) * SG_XB + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
+            s_split[((e >> 2) & 1) * xb + 4 * (e >> 3) + (e & 3)] = v[i] * scale;
         }
     }
 }

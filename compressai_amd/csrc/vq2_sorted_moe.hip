@@ -94,6 +94,14 @@ struct SortedMoeArgs {
     int out_dt;
 };
 
+// LDS floats between the natural-order activation and the accumulators:
+// the stage, later the split activation (n), and after it the 512-point
+// rotation's scratch of the down part (MODE 2) in the all-threads form.
+__host__ __device__ constexpr int64_t moe_split_floats(int mode, int f2k, int64_t n)
+{
+    return mode == 2 && f2k != 0 ? n + RHT512 : n;
+}
+
 // The pair's expert id by a scalar load (p is wave-uniform): waiting for it
 // does not wait for the vector loads issued before it.  In the down launch
 // the ids come from the gate_up launch before it (the scalar cache starts
@@ -233,10 +241,14 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const SortedPoolArgs& pl = a.pool;
     const int64_t n = (int64_t)pl.ng * 8;
-    float* s_x = smem;                     // natural-order activation, n floats
-    float* s_stage = smem + n;             // n floats; once build_x is done, the split activation
-    float* s_split = smem + n;             // (SG_X_SPLIT floats) takes its place
-    float* s_acc = s_split + SG_X_SPLIT;   // SG_WAVES x SG_PARTS x (R + 1)
+    // [natural-order activation: n][stage (n), later the split activation
+    // (n floats, halves xb = n / 2 apart); the down part's 512-point
+    // rotation also has its scratch there, n floats on][accumulators]
+    const int xb = (int)(n / 2);
+    float* s_x = smem;
+    float* s_stage = smem + n;
+    float* s_split = smem + n;
+    float* s_acc = s_split + moe_split_floats(MODE, F2K, n);  // SG_WAVES x SG_PARTS x (R + 1)
     const int R = pl.R;
     // Workgroup b runs on XCD b % 8; with xmap each XCD takes a contiguous
     // run of the (slice, pair, chunk) units in slice-major order.  A slice is
@@ -297,7 +309,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         entries(e);
         sorted_acc_zero(acc, lane, R);
         if constexpr (FAST) {
-            rht2k_build<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, SG_XB);
+            rht2k_build<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, xb);
         } else {
             stage_x<1, XT>(a.g, s_stage, 1, n, t, 0, first);
             build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
@@ -346,7 +358,7 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
             e = s_top[kslot];
             entries(e);
         }
-        if constexpr (FAST) rht2k_transform<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, SG_XB);
+        if constexpr (FAST) rht2k_transform<XT>(k2k, n, first2k, s_stage, s_x, s_split, a.g.xscale, xb);
         else build_x<1, XT>(a.g, s_x, s_stage, 1, n, first);
     } else {
         // the pair's gate_up rows: slices added in order, row scale, then
@@ -456,19 +468,19 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
         __syncthreads();
         if constexpr (F2K != 0) {
             // silu(gate) * up taken as the transform reads it; its natural-
-            // order scratch lies in the split buffer's unused middle
-            rht512_transform(first512, [&](uint32_t i) { return silu_f32(s_x[i]) * s_stage[i]; }, s_split + 2 * RHT512,
-                             s_split, a.g.xscale);
+            // order scratch follows the split activation
+            rht512_transform(first512, [&](uint32_t i) { return silu_f32(s_x[i]) * s_stage[i]; }, s_split + n,
+                             s_split, a.g.xscale, xb);
         } else {
             for (int64_t j = threadIdx.x; j < n; j += SG_THREADS) s_stage[j] = silu_f32(s_x[j]) * s_stage[j];
             __syncthreads();
             build_x<2, VQ2_DT_F32>(a.g, s_x, s_stage, 1, n, first);
         }
     }
-    if constexpr (F2K == 0) x_finalize(s_x, s_split, n, a.g.xscale, SG_XB);
+    if constexpr (F2K == 0) x_finalize(s_x, s_split, n, a.g.xscale, xb);
     __syncthreads();
     pipe.gathers();
-    pipe.run(acc, s_split, pl.gbits, pl.ng, R, SG_XB);
+    pipe.run(acc, s_split, pl.gbits, pl.ng, R, xb);
     __syncthreads();
 
     const int rr = threadIdx.x;
@@ -477,7 +489,8 @@ __device__ __forceinline__ void moe_body(const SortedMoeArgs& a, int bid, float*
     // MODE 2: each slice's share of the combine, w[p] * (sum * s[e][row])
     float f = 1.0f;
     if constexpr (MODE == 2) f = own ? wp * raw_as_f32(dsc, pl.s_dt) : 0.0f;
-    const float sum = sorted_row_sums(s_acc, R, s_red);
+    // chunks of 256 rows or more (taller down pools) sum rows in 512-thread halves
+    const float sum = sorted_row_sums<true>(s_acc, R, s_red);
     if (own) {
         float v = sum;
         if constexpr (MODE == 2) v = f * sum;
@@ -644,8 +657,8 @@ static hipError_t launch_fused(int cb_dt, int x_dt, const SortedMoeArgs& a, cons
 static int pool_args(const SortedPoolCall& pc, const char* name, int64_t n_experts, int64_t rows, int64_t ng,
                      SortedPoolArgs& pa)
 {
-    // pools: chunks of at most 255 rows with 16-bit positions
-    const int64_t r_lim = std::min<int64_t>(sorted_max_rows(ng, 16), 255);
+    // pools: 16-bit positions (chunks of up to 511 rows where they fit)
+    const int64_t r_lim = sorted_max_rows(ng, 16);
     if (r_lim == 0) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: %s: ng=%lld unsupported", name, (long long)ng);
     if (pc.rows != rows || pc.ng != ng)
         return set_error(VQ2_ERR_ARG, "vq2_sorted_moe: %s pool holds [%lld rows, %lld groups], expected [%lld, %lld]",
@@ -817,11 +830,12 @@ int sorted_moe_launch(const SortedMoeCall& c)
     a.xmap = a.slices > 1 && grid_gu <= device_cu_count();
     a.xq = (int)(grid_gu / 8);
     a.xr = (int)(grid_gu % 8);
-    const size_t shm_gu = (size_t)(H + SG_X_SPLIT + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
-    if (shm_gu > SG_MAX_SHM)
-        return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm_gu);
     // 2048-point blocks: the all-threads prologue
     const bool f2k = c.rot_h.hb == RHT2K && H == RHT2K;
+    const size_t shm_gu =
+        (size_t)(H + moe_split_floats(1, f2k, H) + SG_WAVES * SG_PARTS * (a.pool.R + 1)) * sizeof(float);
+    if (shm_gu > SG_MAX_SHM)
+        return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: gate_up needs %zu bytes of LDS", shm_gu);
 
     // down: SwiGLU + RHT_I prologue from the gate_up slices
     d.g.ng = I / 8;
@@ -849,10 +863,11 @@ int sorted_moe_launch(const SortedMoeCall& c)
     d.gu_scale = c.gate_up.scale;
     d.gu_s_dt = c.gate_up.scale_dt;
     d.w = w;
-    const size_t shm_dn = (size_t)(I + SG_X_SPLIT + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
-    if (shm_dn > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm_dn);
     // one 512-point rotation block: the all-threads prologue
     const bool f512 = c.rot_i.hb == RHT512 && I == RHT512;
+    const size_t shm_dn =
+        (size_t)(I + moe_split_floats(2, f512, I) + SG_WAVES * SG_PARTS * (d.pool.R + 1)) * sizeof(float);
+    if (shm_dn > SG_MAX_SHM) return set_error(VQ2_ERR_UNSUPPORTED, "vq2_sorted_moe: down needs %zu bytes of LDS", shm_dn);
 
     hipError_t err;
     if (f2k && f512 && n_pairs <= VQ2_SORTED_MAX_COUNTERS / MOE_CNT_STRIDE) {

@@ -789,9 +789,13 @@ class SortedPool:
     the kernels compute a chunk's offset instead of reading it).  Built once
     at load time by the expert modules; the pool stays the public format.
     ``SortedPool.slots`` makes an empty (zeroed) pool of the same layout for
-    a paged slot pool whose records are copied in later."""
+    a paged slot pool whose records are copied in later.  rows_per_chunk:
+    the chunk height (default: vq2_sorted_rows_per_chunk, at most 255 rows);
+    up to 511 where 16-bit positions hold it (taller chunks put more codes
+    on each code value: fewer codebook lines per instruction, fewer
+    workgroups per expert)."""
 
-    def __init__(self, idx, device=None, threads=0, idx1=None):
+    def __init__(self, idx, device=None, threads=0, idx1=None, rows_per_chunk=None):
         lib = _lib.load()
         idx = _idx16(idx, "idx")
         if idx.dim() != 3:
@@ -809,6 +813,8 @@ class SortedPool:
         R = int(lib.vq2_sorted_rows_per_chunk(rows, ng, 1))
         if R == 0:
             raise Vq2Error(f"sorted layout: ng={ng} unsupported")
+        if rows_per_chunk is not None:
+            R = int(rows_per_chunk)  # vq2_sorted_pack_pool checks it against the position bits
         self.n_experts, self.rows, self.ng, self.rows_per_chunk = E, rows, ng, R
         self.chunks = -(-rows // R)
         dev = torch.device(device) if device is not None else idx.device

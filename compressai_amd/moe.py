@@ -37,7 +37,10 @@ The reference pools stay the public format and serve ``act_dtype`` bf16,
 more than 256 routed experts and the paged feed; a caller that needs none
 of these frees them with ``release_reference_pools()`` (resident index
 memory then ~3.06 instead of ~5.06 bytes per code; ``sorted_layout=False``
-keeps only the 2-byte pools, on the gather kernels).
+keeps only the 2-byte pools, on the gather kernels).  The down pool is
+sorted twice where taller chunks fit its 16-bit positions (the 35B shape:
+5 chunks of 410 rows besides 9 of 228), the taller copy for T >= 2
+(``release_tall_down()`` drops it, ~1.2 bytes per down code).
 """
 from __future__ import annotations
 
@@ -46,6 +49,21 @@ import torch.nn as nn
 
 from . import kernels as K
 from .rot import get_rot
+
+
+def _tall_rows(rows, ng, default_rows):
+    """Chunk height of the taller down pool: the fewest chunks of at most 511
+    rows that 16-bit positions hold (the down pool of the 35B shape, 2048
+    rows of 64 groups: 5 chunks of 410 rows); None unless that is at least
+    a quarter taller than default_rows (the pool's memory buys little
+    otherwise)."""
+    gb = max(0, (int(ng) - 1).bit_length())
+    if gb > 15:
+        return None
+    rmax = min((1 << (16 - gb)) - 1, 511)
+    n = -(-int(rows) // rmax)
+    r = -(-int(rows) // n)
+    return r if 4 * r >= 5 * int(default_rows) else None
 
 
 class ResidentMoEExperts(nn.Module):
@@ -110,6 +128,25 @@ class ResidentMoEExperts(nn.Module):
             and hidden % 64 == 0 and self.intermediate_dim % 64 == 0 and hidden <= 8192)
         self.sorted_gu = K.SortedPool(gate_up_idx, device=dev) if use else None
         self.sorted_dn = K.SortedPool(down_idx, device=dev) if use else None
+        # the down pool again in taller chunks, for T >= 2 (_down_pool)
+        tall = _tall_rows(hidden, ng_i, self.sorted_dn.rows_per_chunk) if use else None
+        self.sorted_dn_tall = K.SortedPool(down_idx, device=dev, rows_per_chunk=tall) if tall else None
+
+    def _down_pool(self, T):
+        """The down pool for T tokens: from T = 2 on the taller chunks, whose
+        fewer, longer workgroups gather fewer codebook lines per instruction
+        (20 layers of the 35B shape, down in 5 chunks of 410 rows against 9
+        of 228: T = 2 / 3 / 4 / 8 28.8 / 33.5 / 40.7 / 59.2 us per layer
+        against 29.2 / 35.5 / 41.6 / 64.3; T = 1 20.6 against 19.8, so T = 1
+        keeps the default chunks)."""
+        if T >= 2 and self.sorted_dn_tall is not None:
+            return self.sorted_dn_tall
+        return self.sorted_dn
+
+    def release_tall_down(self):
+        """Drop the taller down pool (~1.2 bytes per down code less resident);
+        every T then runs on the default chunks."""
+        self.sorted_dn_tall = None
 
     def release_reference_pools(self):
         """Drop the reference index pools once the sorted copies exist (the
@@ -138,7 +175,7 @@ class ResidentMoEExperts(nn.Module):
         """Resident bytes: index pools, scales and the sorted copies."""
         own = sum(t.numel() * t.element_size() for t in (self.gate_up_idx, self.gate_up_scale, self.down_idx,
                                                           self.down_scale) if t is not None)
-        return own + sum(p.nbytes() for p in (self.sorted_gu, self.sorted_dn) if p is not None)
+        return own + sum(p.nbytes() for p in (self.sorted_gu, self.sorted_dn, self.sorted_dn_tall) if p is not None)
 
     def experts(self, h, ids, w, out=None):
         """h [T, H] (unrotated hidden states), ids [T, P] int32/int64,
@@ -148,8 +185,8 @@ class ResidentMoEExperts(nn.Module):
         SwiGLU + I-point RHT + down + weighted combine."""
         if self.sorted_gu is not None:
             rh, ri = self._rots()
-            return K.vq_sorted_moe(h, self.sorted_gu, self.gate_up_scale, self.sorted_dn, self.down_scale, self.cb16,
-                                   rh, ri, ids=ids, w=w, out=out, out_dtype=self.out_dtype or torch.float32)
+            return K.vq_sorted_moe(h, self.sorted_gu, self.gate_up_scale, self._down_pool(h.shape[0]), self.down_scale,
+                                   self.cb16, rh, ri, ids=ids, w=w, out=out, out_dtype=self.out_dtype or torch.float32)
         self._reference_pools()
         T, P = ids.shape
         I = self.intermediate_dim
@@ -208,7 +245,7 @@ class MoELayer(nn.Module):
         T = h2.shape[0]
         if m.sorted_gu is not None and self.n_routed <= 256:
             rh, ri = m._rots()
-            out, _, _ = K.vq_sorted_moe(h2, m.sorted_gu, m.gate_up_scale, m.sorted_dn, m.down_scale, m.cb16, rh, ri,
+            out, _, _ = K.vq_sorted_moe(h2, m.sorted_gu, m.gate_up_scale, m._down_pool(T), m.down_scale, m.cb16, rh, ri,
                                         logits=router_logits.reshape(T, -1), top_k=self.top_k,
                                         shared_id=self.n_routed, shared_gate=self.shared_gate,
                                         out_dtype=m.out_dtype or torch.float32)

@@ -468,7 +468,7 @@ int vq2_sorted_gemm_batch_argmax(const void* x, int x_dt, int64_t batch, int64_t
  * idx [n_experts, rows, ng] (the int16 stage-1 plane; idx1, the stage-2
  * plane as int16 -- a (16,8) uint8 plane widened to values 0..255 -- or
  * NULL) expert by expert, each as vq2_sorted_pack packs a matrix with the
- * same rows_per_chunk R (at most min(2^(16 - ceil(log2 ng)) - 1, 255): pools
+ * same rows_per_chunk R (at most min(2^(16 - ceil(log2 ng)) - 1, 511): pools
  * keep 16-bit positions; and 32-lane halves at every R, where
  * vq2_sorted_pack takes quarters for R <= 32), and pads every chunk's stage-1 and stage-2 entries
  * (dummy-row entries) to the pool's largest counts, so chunk c of expert e

@@ -68,6 +68,35 @@ def test_sorted_moe_experts_vs_oracle(dev, T, P, ids_dtype, h_dtype):
     assert O.max_rel_err(out.cpu().numpy(), ref) < TOL
 
 
+@pytest.mark.parametrize("T,slices", [(3, None), (3, (2, 1)), (3, (3, 2)), (15, None)])
+def test_sorted_moe_tall_down_pool(dev, T, slices):
+    """The down pool in taller chunks (5 of 410 rows, 16-bit positions, rows
+    summed in 512-thread halves), which the module runs from T = 2 on: the
+    oracle's result, bit-identical on repeated calls, in one launch (T = 3)
+    and in three (T = 15: 135 pairs); T = 1 keeps the default chunks, and
+    release_tall_down() returns every T to them."""
+    E, P = 12, 9
+    mod, cb, gu, gus, dn, dns = _module(dev, 9750, E)
+    tall = mod.sorted_dn_tall
+    assert tall is not None and tall.rows_per_chunk == 410 and tall.chunks == 5
+    assert mod._down_pool(1) is mod.sorted_dn and mod._down_pool(2) is tall
+    h = synth.activations(9751 + T, (T, 2048), dtype=torch.float16).to(dev)
+    ids = torch.stack([torch.randperm(E, generator=synth.gen(9760 + t))[:P] for t in range(T)]).to(torch.int32).to(dev)
+    w = torch.softmax(synth.activations(9770 + T, (T, P)).float(), -1).to(dev)
+    rh, ri = mod._rots()
+    run = lambda: K.vq_sorted_moe(h, mod.sorted_gu, mod.gate_up_scale, tall, mod.down_scale, mod.cb16, rh, ri,
+                                  ids=ids, w=w, slices=slices)
+    a = run()
+    b = run()
+    assert torch.equal(a, b)
+    ref = _oracle(mod, h.cpu(), ids.cpu().numpy(), w.cpu().numpy(), cb, gu, gus, dn, dns)
+    assert O.max_rel_err(a.cpu().numpy(), ref) < TOL
+    if slices is None:
+        assert torch.equal(mod.experts(h, ids, w), a)
+    mod.release_tall_down()
+    assert mod.sorted_dn_tall is None and mod._down_pool(8) is mod.sorted_dn
+
+
 @pytest.mark.parametrize("slices", [(1, 1), (3, 2), (7, 4), (2, 5), (9, 9)])
 def test_sorted_moe_slices_and_determinism(dev, slices):
     """Every slice count gives the oracle's result (the combine adds up to
@@ -185,7 +214,8 @@ def test_sorted_moe_router_ids_and_weights(dev, T):
     h = synth.activations(9902, (T, 2048), dtype=torch.float16).to(dev)
     logits = synth.activations(9903, (T, E), dtype=torch.float16).to(dev)
     rh, ri = m._rots()
-    out, ids, w = K.vq_sorted_moe(h, m.sorted_gu, m.gate_up_scale, m.sorted_dn, m.down_scale, m.cb16, rh, ri,
+    # the down pool the layer runs for T tokens (the taller chunks from T = 2 on)
+    out, ids, w = K.vq_sorted_moe(h, m.sorted_gu, m.gate_up_scale, m._down_pool(T), m.down_scale, m.cb16, rh, ri,
                                   logits=logits, top_k=k, shared_id=E, shared_gate=layer.shared_gate)
     rid, rw = layer.route(h, logits)
     assert torch.equal(ids.cpu(), rid.cpu().to(torch.int32))

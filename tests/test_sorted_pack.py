@@ -198,20 +198,23 @@ def test_sorted_rows_per_chunk_alignment():
     assert L.vq2_sorted_rows_per_chunk(100, 1 << 16, 1) == 0      # n beyond the 16-bit position field
 
 
-@pytest.mark.parametrize("E,rows,n", [(3, 1024, 2048), (5, 2048, 512), (2, 100, 800)])
-def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
+@pytest.mark.parametrize("E,rows,n,R", [(3, 1024, 2048, None), (5, 2048, 512, None), (2, 100, 800, None),
+                                         (3, 2048, 512, 410)])
+def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n, R):
     """vq2_sorted_pack_pool lays the experts out one after another, each
     chunk exactly as vq2_sorted_pack packs it alone (chunks of more than 32
     rows, where both deal into 32-lane halves), then padded with dummy-row
     iterations (offset 0, base code 0) to the pool's common iteration
-    count."""
+    count.  Also for a taller pool (the MoE down pool in 5 chunks of 410
+    rows, 16-bit positions)."""
     from compressai_amd.kernels import SortedPool
 
     ng = n // 8
     idx = synth.indices16(9950 + rows, (E, rows, ng))
-    pool = SortedPool(idx, device="cpu", threads=3)
-    C, R = pool.chunks, pool.rows_per_chunk
-    assert R == int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1)) and C == -(-rows // R)
+    pool = SortedPool(idx, device="cpu", threads=3, rows_per_chunk=R)
+    C, want = pool.chunks, R
+    R = pool.rows_per_chunk
+    assert R == (want or int(_lib.load().vq2_sorted_rows_per_chunk(rows, ng, 1))) and C == -(-rows // R)
     ipc = pool.iters_per_chunk
     assert pool.n_iters == E * C * ipc
     ent = pool.entries.numpy().view(np.uint32)
@@ -220,7 +223,7 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
     longest = 0
     W = ITER_WORDS
     for e in range(E):
-        sp = SortedPlanes(idx[e], None, rows, n, device="cpu", chunk_align=1)
+        sp = SortedPlanes(idx[e], None, rows, n, device="cpu", chunk_align=1, rows_per_chunk=R)
         assert sp.rows_per_chunk == R and sp.n_chunks == C
         ipe = sp.iters_per_chunk   # this expert's chunks, padded to its own longest
         own = sp.entries.numpy().view(np.uint32)
@@ -231,6 +234,27 @@ def test_sorted_pool_pack_equals_per_expert_pack(E, rows, n):
             tail = got[ipe * W:].reshape(-1, 64, 3)
             assert np.all(tail[:, :63] == pad_lane) and np.all(tail[:, 63] == 0)
     assert ipc == longest
+
+
+def test_sorted_pool_chunk_height_limits():
+    """Pools keep 16-bit positions: up to 511 rows where ceil(log2 ng) leaves
+    room (ng 64: 1023 would fit, 511 is the kernels' limit), 255 at ng 256;
+    the taller down pool's height rule (moe._tall_rows) stays within it."""
+    from compressai_amd.kernels import SortedPool
+    from compressai_amd.moe import _tall_rows
+
+    idx = synth.indices16(9960, (1, 600, 64))
+    assert SortedPool(idx, device="cpu", rows_per_chunk=511).chunks == 2
+    with pytest.raises(Vq2Error, match="rows_per_chunk=512"):
+        SortedPool(idx, device="cpu", rows_per_chunk=512)
+    idx = synth.indices16(9961, (1, 300, 256))
+    assert SortedPool(idx, device="cpu", rows_per_chunk=255).chunks == 2
+    with pytest.raises(Vq2Error, match="rows_per_chunk=256"):
+        SortedPool(idx, device="cpu", rows_per_chunk=256)
+    assert _tall_rows(2048, 64, 228) == 410       # the 35B down pool: 5 chunks instead of 9
+    assert _tall_rows(1024, 256, 205) is None     # gate_up: 255 rows at most, 205 already
+    assert _tall_rows(7168, 256, 240) is None     # 248 rows: not a quarter taller
+    assert _tall_rows(4096, 128, 228) == 456      # ng 128: 511 rows at most, 9 chunks
 
 
 def test_moe_slices_cost_model():
