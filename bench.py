@@ -802,8 +802,9 @@ def main():
         "pct_of_peak": round(100.0 * d["gbps"] / PEAK_HBM_GBPS, 3),
         "resident_index_bytes": {
             "note": "index bytes held on the device per unit: the reference planes (2 bytes per code, the public "
-                    "format) and the code-sorted copies the batch-1 kernels read (~3.06 bytes per code); both "
-                    "are resident unless the owner releases the planes",
+                    "format) and the code-sorted copies the batch-1 kernels read (~3.06 bytes per code; the MoE "
+                    "layer's down pool twice, in 9 chunks for T = 1 and 5 taller ones for T >= 2); both are "
+                    "resident unless the owner releases the planes",
             "dense_layer": {"planes": d["plane_bytes"], "sorted": d["sorted_bytes"]},
             "moe_layer_257_experts": None if moe is None else moe["resident"],
             "lm_head": None if lm1 is None else {"planes": lm1["plane_bytes"], "sorted": lm1["sorted_bytes"]},
