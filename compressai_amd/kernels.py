@@ -892,7 +892,10 @@ def moe_slices(units, codes_per_unit, cu, fixed_us, one_launch=False):
     two workgroups per CU): units that fill twice the CUs on their own take
     one slice, units that fill the CUs two (measured, T = 8, 360 gate_up and
     648 down units: gate_up / down slices 1 / 1 66.8 us per layer, 2 / 1
-    64.5, 3 / 1 64.5, 2 / 2 65.9, 1 / 2 70.5)."""
+    64.5, 3 / 1 64.5, 2 / 2 65.9, 1 / 2 70.5; with the down pool in 5
+    taller chunks, 360 and 360 units: 2 / 2 59.0-59.8, 2 / 3 61.2, 3 / 1
+    63.2, 3 / 2 63.5, 1 / 1 63.9, 3 / 3 63.9, 1 / 2 64.1, 2 / 1 65.5, 1 / 3
+    67.0)."""
     if one_launch and units >= 2 * cu:
         return 1
     if one_launch and units >= cu:
