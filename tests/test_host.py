@@ -210,6 +210,28 @@ def test_resident_experts_reference_constructor_on_cpu():
         ResidentMoEExperts(q_gu, q_dn, cb, "cpu", num_experts=E + 1, hidden_dim=H, intermediate_dim=I)
 
 
+def test_resident_experts_tall_down_pool_on_cpu():
+    """The sorted layout keeps the down pool twice at the 35B shape: 9 chunks
+    of 228 rows for T = 1 and 5 of 410 for T >= 2; both count in nbytes(),
+    and release_tall_down() returns every T to the default chunks."""
+    from compressai_amd.moe import ResidentMoEExperts
+
+    E, H, I = 2, 2048, 512
+    gu = synth.indices16(8610, (E, 2 * I, H // 8))
+    dn = synth.indices16(8611, (E, H, I // 8))
+    mod = ResidentMoEExperts.from_pools(gu, synth.scales(8612, (E, 2 * I)), dn, synth.scales(8613, (E, H)),
+                                        synth.codebook(8614), sorted_layout=True)
+    d, t = mod.sorted_dn, mod.sorted_dn_tall
+    assert (d.rows_per_chunk, d.chunks) == (228, 9) and (t.rows_per_chunk, t.chunks) == (410, 5)
+    assert mod._down_pool(1) is d and mod._down_pool(2) is t and mod._down_pool(64) is t
+    full = mod.nbytes()
+    mod.release_tall_down()
+    assert mod.sorted_dn_tall is None and mod._down_pool(8) is d and full - mod.nbytes() == t.nbytes()
+    plain = ResidentMoEExperts.from_pools(gu, synth.scales(8612, (E, 2 * I)), dn, synth.scales(8613, (E, H)),
+                                          synth.codebook(8614), sorted_layout=False)
+    assert plain.sorted_dn is None and plain.sorted_dn_tall is None
+
+
 # ---------------------------------- vq_sorted_moe argument checks (CPU)
 def _small_sorted_pools():
     from compressai_amd.kernels import SortedPool
